@@ -1,0 +1,199 @@
+/*
+ * glm53_moe.h -- C ABI of libglm53moe.so, the MI355X (gfx950) routed-MoE
+ * library for livglm's GLM-5.3-Flash MoE layer.
+ *
+ * Conventions (every entry point):
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream).
+ *     All work is enqueued on it; no entry point synchronises, allocates device
+ *     memory or frees it.  The caller owns every buffer.
+ *   - Pointers are device pointers to row-major arrays.  bf16 values travel as
+ *     uint16_t bit patterns.  Expert banks use the reference checkpoint layout
+ *     (weight_packed / weight_scale, expert_source.py:189-229), stacked over
+ *     experts: gate/up packed [E][I][d/2] u8, gate/up scales [E][I][d/32] u8,
+ *     down packed [E][d][I/2] u8, down scales [E][d][I/32] u8.
+ *   - Return value: GLM_OK (0) or a negative GLM_ERR_* code; the message is
+ *     available from glm_last_error() on the calling thread.  No C++ exception
+ *     crosses the ABI.
+ *   - Calls are re-entrant; concurrent calls on different streams must use
+ *     different output and workspace buffers.
+ */
+#ifndef GLM53_MOE_H
+#define GLM53_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GLM_ABI_VERSION 1
+
+#define GLM_OK 0
+#define GLM_ERR_INVALID_ARGUMENT (-1) /* null pointer, negative size, bad enum */
+#define GLM_ERR_UNSUPPORTED_SHAPE (-2) /* shape outside what the kernels accept */
+#define GLM_ERR_HIP (-3)               /* a HIP runtime call failed */
+#define GLM_ERR_WORKSPACE (-4)         /* workspace too small */
+
+/* Weight storage formats (layers.py:38-70 quantization_mode). */
+#define GLM_FMT_BF16 0  /* bf16 [out][in] */
+#define GLM_FMT_MXFP8 1 /* E4M3FN codes [out][in] u8 + E8M0 scales [out][in/32] */
+#define GLM_FMT_MXFP4 2 /* packed E2M1 [out][in/2] u8 + E8M0 scales [out][in/32] */
+
+/* Shared-exponent rules for glm_mx_quantize (the rule of mx.quantize is not
+ * published; see layers.py:89-94). */
+#define GLM_MX_RULE_NEAREST 0 /* e = round(log2(amax / elem_max)), saturating elements */
+#define GLM_MX_RULE_OCP 1     /* e = floor(log2(amax)) - emax_elem (OCP MX v1.0) */
+
+/* Version of this header's ABI; bump on any signature change. */
+int glm_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *glm_last_error(void);
+
+/*
+ * Router.  Replaces TopKRouter.__call__ (src/glm53flash/moe.py:36-63).
+ * x bf16 [T][d]; weight f32 [E][d]; bias f32 [E].
+ * logits f32 [T][E] = f32(x) @ weight^T; scores = sigmoid(logits);
+ * choice = scores + bias; group top-2-sum mask keeps `topk_group` of
+ * `n_group` groups; indices u32 [T][k] = the k best choices in ASCENDING order
+ * (best expert last, moe.py:33-34,58; ties rank the larger index higher);
+ * weights f32 [T][k] = scores[indices], normalised by (sum + 1e-20) when
+ * norm_topk_prob, times routed_scaling_factor.  logits is a required output.
+ * Limits: E <= 1024, E % n_group == 0, E / n_group >= 2, 1 <= k <= min(E, 64),
+ * d % 4 == 0; every buffer 16-byte aligned (all entry points require this).
+ */
+int glm_router_topk(void *stream, const uint16_t *x, int T, int d, const float *weight,
+                    const float *bias, int E, int top_k, int n_group, int topk_group,
+                    int norm_topk_prob, float routed_scaling_factor, float *logits,
+                    float *weights, uint32_t *indices);
+
+/*
+ * Token-to-expert dispatch: histogram, exclusive prefix sum, stable permute.
+ * Replaces the host-side route materialisation of
+ * _expert_ssd_route_cache_plan / ExpertSSD.__call__ dedupe+remap
+ * (native_expert_ssd.py:475-525, expert_ssd.py:159-169).
+ * indices u32 [T*k] (row-major (t, j) pairs, P = T*k).
+ * counts [E]; offsets [E+1] (exclusive scan of counts); perm [P] (sorted
+ * position -> pair t*k+j, each expert's pairs ascending); inv [P] (pair ->
+ * sorted position); pair_token [P] (sorted position -> token t); active [E]
+ * (ids of experts with count > 0, ascending); num_active [1]; status [1]
+ * (0, or 1 if an index >= E was seen -- such pairs are dropped, inv = -1).
+ * Limits: E <= 448 (one workgroup's LDS holds the per-expert bitmaps).
+ */
+int glm_moe_dispatch(void *stream, const uint32_t *indices, int T, int top_k, int E,
+                     int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
+                     int32_t *pair_token, int32_t *active, int32_t *num_active,
+                     int32_t *status);
+
+/*
+ * Routed gate/up projections + limited SwiGLU.  Replaces
+ * mx._expert_ssd_mxfp4_pair_qmv + limited_swiglu (native_expert_ssd.py:696-706,
+ * expert_ssd.py:103-107), and gather_qmm for T > 1 (native_expert_ssd.py:726-741).
+ * x bf16 [T][d]; h bf16 [T*k][I] in SORTED (dispatch) order:
+ * h[pos] = swiglu(bf16(x[pair_token[pos]] . Wg[e]^T), bf16(x . Wu[e]^T)).
+ * Limits: d % 32 == 0, I % 16 == 0.
+ */
+int glm_expert_gate_up(void *stream, const uint16_t *x, int T, int d, int I, int E, int top_k,
+                       const uint8_t *gate_packed, const uint8_t *gate_scales,
+                       const uint8_t *up_packed, const uint8_t *up_scales,
+                       const int32_t *offsets, const int32_t *pair_token,
+                       const int32_t *active, const int32_t *num_active, float swiglu_limit,
+                       uint16_t *h);
+
+/*
+ * Routed down projection.  Replaces mx._expert_ssd_mxfp4_masked_qmv
+ * (native_expert_ssd.py:707-717) and gather_qmm(down) (native_expert_ssd.py:743).
+ * h bf16 [T*k][I] (sorted order); y bf16 [T*k][d] (sorted order).
+ * Limits: I % 32 == 0, d % 16 == 0.
+ */
+int glm_expert_down(void *stream, const uint16_t *h, int T, int top_k, int I, int d, int E,
+                    const uint8_t *down_packed, const uint8_t *down_scales,
+                    const int32_t *offsets, const int32_t *active, const int32_t *num_active,
+                    uint16_t *y);
+
+/*
+ * Weighted combine + shared add (moe.py:198-201):
+ * out[t] = sum_{j=0..k-1} f32(y[inv[t*k+j]]) * weights[t*k+j]  (sequential j)
+ *          + f32(shared[t])    (shared may be NULL).
+ * out is f32 [T][d].
+ */
+int glm_moe_combine(void *stream, const uint16_t *y, const int32_t *inv, const float *weights,
+                    const uint16_t *shared, int T, int top_k, int d, float *out);
+
+/*
+ * Dense linear y = bf16(x @ deq(W)^T), f32 accumulate.  Replaces
+ * DeferredLinear.__call__ (layers.py:38-70): bf16 (`x @ weight.T`),
+ * mx.quantized_matmul(mode="mxfp8"/"mxfp4", group_size=32).
+ * x bf16 [T][in]; weight per `fmt`; scales NULL for bf16; y bf16 [T][out].
+ * Limits: in % 32 == 0, out % 16 == 0.
+ */
+int glm_linear(void *stream, const uint16_t *x, int T, int in_dims, const void *weight,
+               const uint8_t *scales, int fmt, int out_dims, uint16_t *y);
+
+/*
+ * Dense SwiGLU MLP (the shared expert).  Replaces DenseMLP.__call__
+ * (layers.py:160-171): out = down(limited_swiglu(gate(x), up(x))).
+ * All three weights share `fmt`.  h is caller scratch bf16 [T][I].
+ */
+int glm_dense_mlp(void *stream, const uint16_t *x, int T, int d, int I, int fmt,
+                  const void *gate_w, const uint8_t *gate_s, const void *up_w,
+                  const uint8_t *up_s, const void *down_w, const uint8_t *down_s,
+                  float swiglu_limit, uint16_t *h, uint16_t *out);
+
+/*
+ * Group-32 MX quantisation of a bf16 matrix.  Replaces
+ * mx.quantize(group_size=32, bits=8|4, mode="mxfp8"|"mxfp4") in
+ * DeferredLinear.quantize_to_mxfp (layers.py:72-99).
+ * w bf16 [rows][cols]; fmt GLM_FMT_MXFP8 (codes [rows][cols]) or
+ * GLM_FMT_MXFP4 (codes [rows][cols/2]); scales [rows][cols/32].
+ * Elements round to nearest-even and saturate at the format maximum.
+ */
+int glm_mx_quantize(void *stream, const uint16_t *w, int rows, int cols, int fmt, int rule,
+                    uint8_t *codes, uint8_t *scales);
+
+/*
+ * Group-32 MX dequantisation to f32 (the exact decode every MX kernel applies
+ * in registers; gather_qmm / quantized_matmul read the same values).
+ */
+int glm_mx_dequantize(void *stream, const uint8_t *codes, const uint8_t *scales, int rows,
+                      int cols, int fmt, float *out);
+
+/* limited_swiglu on bf16 arrays (expert_ssd.py:103-107), bf16 intermediates. */
+int glm_limited_swiglu(void *stream, const uint16_t *gate, const uint16_t *up, int64_t n,
+                       float limit, uint16_t *out);
+
+/*
+ * Workspace needed by glm_moe_forward for these sizes (bytes).
+ */
+size_t glm_moe_workspace_bytes(int T, int d, int E, int top_k, int I, int I_shared);
+
+/*
+ * One whole routed-MoE layer on a bf16 [T][d] input.  Replaces
+ * ExpertSSDMoE.__call__ / _call_impl (moe.py:96-201) with an HBM-resident
+ * expert bank: router -> dispatch -> gate/up+SwiGLU -> down -> shared expert
+ * -> weighted combine, all on `stream` with no host synchronisation.
+ * out f32 [T][d].  Optional outputs (may be NULL): weights f32 [T][k],
+ * indices u32 [T][k].  The shared expert is skipped when shared_gate is NULL.
+ * Shared-expert weights use `shared_fmt` (GLM_FMT_BF16: scale pointers NULL;
+ * GLM_FMT_MXFP8/MXFP4: the resident MX layout): gate/up [I_shared][d],
+ * down [d][I_shared].
+ * Limits: E <= 448, d % 32 == 0, I % 32 == 0.
+ */
+int glm_moe_forward(void *stream, const uint16_t *x, int T, int d, const float *router_weight,
+                    const float *router_bias, int E, int top_k, int n_group, int topk_group,
+                    int norm_topk_prob, float routed_scaling_factor, int I,
+                    const uint8_t *gate_packed, const uint8_t *gate_scales,
+                    const uint8_t *up_packed, const uint8_t *up_scales,
+                    const uint8_t *down_packed, const uint8_t *down_scales, int I_shared,
+                    int shared_fmt, const void *shared_gate, const uint8_t *shared_gate_scales,
+                    const void *shared_up, const uint8_t *shared_up_scales,
+                    const void *shared_down, const uint8_t *shared_down_scales,
+                    float swiglu_limit, void *workspace, size_t workspace_bytes, float *out,
+                    float *weights_out, uint32_t *indices_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GLM53_MOE_H */

@@ -1,0 +1,164 @@
+// Shared device helpers and host-side error plumbing for libglm53moe.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <initializer_list>
+
+#include "glm53_moe.h"
+
+// ---------------------------------------------------------------- host errors
+
+namespace glm {
+
+void set_error(const char *fmt, ...);
+void clear_error();
+
+}  // namespace glm
+
+#define GLM_REQUIRE(cond, code, ...)  \
+  do {                                \
+    if (!(cond)) {                    \
+      glm::set_error(__VA_ARGS__);    \
+      return (code);                  \
+    }                                 \
+  } while (0)
+
+#define GLM_HIP_CHECK(expr)                                                              \
+  do {                                                                                   \
+    hipError_t glm_err_ = (expr);                                                        \
+    if (glm_err_ != hipSuccess) {                                                        \
+      glm::set_error("%s failed: %s", #expr, hipGetErrorString(glm_err_));              \
+      return GLM_ERR_HIP;                                                                \
+    }                                                                                    \
+  } while (0)
+
+// Check the launch that was just enqueued.
+#define GLM_LAUNCH_CHECK(name)                                                           \
+  do {                                                                                   \
+    hipError_t glm_err_ = hipGetLastError();                                             \
+    if (glm_err_ != hipSuccess) {                                                        \
+      glm::set_error("launch of %s failed: %s", name, hipGetErrorString(glm_err_));     \
+      return GLM_ERR_HIP;                                                                \
+    }                                                                                    \
+  } while (0)
+
+// True when every non-null pointer is 16-byte aligned (the kernels use
+// 128-bit loads and stores).
+static inline bool glm_aligned16(std::initializer_list<const void *> ptrs) {
+  for (const void *p : ptrs)
+    if (p != nullptr && (reinterpret_cast<uintptr_t>(p) & 15u) != 0) return false;
+  return true;
+}
+
+// ---------------------------------------------------------------- device types
+
+typedef __attribute__((ext_vector_type(8))) __bf16 glm_bf16x8;
+typedef __attribute__((ext_vector_type(2))) __bf16 glm_bf16x2;
+typedef __attribute__((ext_vector_type(4))) float glm_f32x4;
+typedef __attribute__((ext_vector_type(4))) uint32_t glm_u32x4;
+
+namespace glm {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// f32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// E8M0 byte -> f32 scale 2^(e-127) (byte 255 = NaN).
+__device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
+  if (e == 0) return __uint_as_float(0x00400000u);  // 2^-127, subnormal
+  if (e == 255) return __uint_as_float(0x7fc00000u);
+  return __uint_as_float(e << 23);
+}
+
+// sigmoid in f32: y = 1/(1+exp(|x|)); x<0 ? y : 1-y.
+__device__ __forceinline__ float sigmoid_f32(float x) {
+  float y = 1.0f / (1.0f + expf(fabsf(x)));
+  return x < 0.0f ? y : 1.0f - y;
+}
+
+// limited_swiglu on one element with bf16 intermediates (expert_ssd.py:103-107):
+// g = min(g, L); u = clip(u, -L, L); h = bf16(bf16(g * bf16(sigmoid(g))) * u).
+__device__ __forceinline__ float limited_swiglu(float g, float u, float limit_bf16) {
+  if (limit_bf16 > 0.0f) {
+    g = fminf(g, limit_bf16);
+    u = fminf(fmaxf(u, -limit_bf16), limit_bf16);
+  }
+  float s = bf16_round(sigmoid_f32(g));
+  float a = bf16_round(g * s);
+  return bf16_round(a * u);
+}
+
+// 8 packed E2M1 codes (one u32, low nibble first) -> 8 bf16 times `scale`,
+// through the gfx950 scaled converts (exact: every value fits bf16).
+__device__ __forceinline__ glm_bf16x8 mxfp4_word_to_bf16x8(uint32_t w, float scale) {
+  const glm_bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0);
+  const glm_bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1);
+  const glm_bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2);
+  const glm_bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3);
+  glm_bf16x8 o;
+  o[0] = p0[0];
+  o[1] = p0[1];
+  o[2] = p1[0];
+  o[3] = p1[1];
+  o[4] = p2[0];
+  o[5] = p2[1];
+  o[6] = p3[0];
+  o[7] = p3[1];
+  return o;
+}
+
+// 8 E4M3FN codes (two u32, byte 0 first) -> 8 bf16 times `scale`.
+__device__ __forceinline__ glm_bf16x8 mxfp8_words_to_bf16x8(uint32_t w0, uint32_t w1,
+                                                            float scale) {
+  const glm_bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, scale, false);
+  const glm_bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, scale, true);
+  const glm_bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, scale, false);
+  const glm_bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, scale, true);
+  glm_bf16x8 o;
+  o[0] = p0[0];
+  o[1] = p0[1];
+  o[2] = p1[0];
+  o[3] = p1[1];
+  o[4] = p2[0];
+  o[5] = p2[1];
+  o[6] = p3[0];
+  o[7] = p3[1];
+  return o;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+}  // namespace glm
+
+// Host helper: the swiglu limit as the bf16 value MLX compares against.
+static inline float glm_limit_bf16(float limit) {
+  union {
+    float f;
+    uint32_t u;
+  } v;
+  v.f = limit;
+  uint32_t u = v.u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  v.u = (u >> 16) << 16;
+  return v.f;
+}

@@ -1,0 +1,187 @@
+// Whole routed-MoE layer (ExpertSSDMoE._call_impl, moe.py:123-201) on one
+// stream, plus the library's error plumbing and version query.
+#include <string>
+
+#include "glm_common.h"
+
+// ---------------------------------------------------------------- errors
+
+namespace glm {
+
+static thread_local std::string g_last_error;
+
+void set_error(const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+}  // namespace glm
+
+extern "C" int glm_abi_version(void) { return GLM_ABI_VERSION; }
+
+extern "C" const char *glm_last_error(void) { return glm::g_last_error.c_str(); }
+
+// ---------------------------------------------------------------- launchers from other units
+
+int glm_router_validate(const void *x, int T, int d, const void *weight, const void *bias, int E,
+                        int k, int n_group, int topk_group, const void *weights,
+                        const void *indices);
+int glm_router_launch(hipStream_t stream, const uint16_t *x, int T, int d, const float *weight,
+                      const float *bias, int E, int k, int n_group, int topk_group, int norm,
+                      float scale, float *logits, float *weights, uint32_t *indices);
+int glm_dispatch_launch(hipStream_t stream, const uint32_t *indices, int T, int k, int E,
+                        int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
+                        int32_t *pair_token, int32_t *active, int32_t *num_active,
+                        int32_t *status);
+int glm_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int E, int k,
+                       const uint8_t *gw, const uint8_t *gs, const uint8_t *uw, const uint8_t *us,
+                       const int32_t *offsets, const int32_t *pair_token, const int32_t *active,
+                       const int32_t *num_active, float limit, uint16_t *h);
+int glm_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, int d, int E,
+                    const uint8_t *dw, const uint8_t *ds, const int32_t *offsets,
+                    const int32_t *active, const int32_t *num_active, uint16_t *y);
+int glm_mlp_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int fmt,
+                   const void *gw, const uint8_t *gs, const void *uw, const uint8_t *us,
+                   const void *dw, const uint8_t *ds, float limit, uint16_t *h, uint16_t *out);
+int glm_combine_launch(hipStream_t stream, const uint16_t *y, const int32_t *inv, const float *w,
+                       const uint16_t *shared, int T, int k, int d, float *out);
+
+// ---------------------------------------------------------------- workspace
+
+namespace {
+
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+struct Workspace {
+  float *logits;
+  float *weights;
+  uint32_t *indices;
+  int32_t *counts;
+  int32_t *offsets;
+  int32_t *active;
+  int32_t *num_active;
+  int32_t *status;
+  int32_t *perm;
+  int32_t *inv;
+  int32_t *pair_token;
+  uint16_t *h;
+  uint16_t *y;
+  uint16_t *shared_h;
+  uint16_t *shared_out;
+  size_t bytes;
+};
+
+// Carves the workspace; with base == nullptr only computes the size.
+Workspace carve(char *base, int T, int d, int E, int k, int I, int Is) {
+  Workspace w{};
+  size_t off = 0;
+  const size_t P = (size_t)T * k;
+  auto take = [&](size_t bytes) -> char * {
+    char *p = base ? base + off : nullptr;
+    off += align_up(bytes);
+    return p;
+  };
+  w.logits = (float *)take((size_t)T * E * 4);
+  w.weights = (float *)take(P * 4);
+  w.indices = (uint32_t *)take(P * 4);
+  w.counts = (int32_t *)take((size_t)E * 4);
+  w.offsets = (int32_t *)take((size_t)(E + 1) * 4);
+  w.active = (int32_t *)take((size_t)E * 4);
+  w.num_active = (int32_t *)take(4);
+  w.status = (int32_t *)take(4);
+  w.perm = (int32_t *)take(P * 4);
+  w.inv = (int32_t *)take(P * 4);
+  w.pair_token = (int32_t *)take(P * 4);
+  w.h = (uint16_t *)take(P * I * 2);
+  w.y = (uint16_t *)take(P * d * 2);
+  w.shared_h = (uint16_t *)take((size_t)T * (Is > 0 ? Is : 0) * 2);
+  w.shared_out = (uint16_t *)take((size_t)T * (Is > 0 ? d : 0) * 2);
+  w.bytes = off;
+  return w;
+}
+
+}  // namespace
+
+extern "C" size_t glm_moe_workspace_bytes(int T, int d, int E, int top_k, int I, int I_shared) {
+  if (T < 0 || d <= 0 || E <= 0 || top_k <= 0 || I <= 0) return 0;
+  return carve(nullptr, T, d, E, top_k, I, I_shared).bytes;
+}
+
+extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
+                               const float *router_weight, const float *router_bias, int E,
+                               int top_k, int n_group, int topk_group, int norm_topk_prob,
+                               float routed_scaling_factor, int I, const uint8_t *gate_packed,
+                               const uint8_t *gate_scales, const uint8_t *up_packed,
+                               const uint8_t *up_scales, const uint8_t *down_packed,
+                               const uint8_t *down_scales, int I_shared, int shared_fmt,
+                               const void *shared_gate, const uint8_t *shared_gate_scales,
+                               const void *shared_up, const uint8_t *shared_up_scales,
+                               const void *shared_down, const uint8_t *shared_down_scales,
+                               float swiglu_limit, void *workspace, size_t workspace_bytes,
+                               float *out, float *weights_out, uint32_t *indices_out) {
+  glm::clear_error();
+  hipStream_t stream = (hipStream_t)stream_v;
+  GLM_REQUIRE(x && router_weight && router_bias && gate_packed && gate_scales && up_packed &&
+                  up_scales && down_packed && down_scales && workspace && out,
+              GLM_ERR_INVALID_ARGUMENT, "moe_forward: null pointer argument");
+  GLM_REQUIRE(T >= 0 && d > 0 && E > 0 && top_k > 0 && I > 0, GLM_ERR_INVALID_ARGUMENT,
+              "moe_forward: invalid sizes T=%d d=%d E=%d k=%d I=%d", T, d, E, top_k, I);
+  GLM_REQUIRE(d % 32 == 0 && I % 32 == 0, GLM_ERR_UNSUPPORTED_SHAPE,
+              "moe_forward: d=%d and I=%d must be multiples of 32", d, I);
+  GLM_REQUIRE(E <= 448, GLM_ERR_UNSUPPORTED_SHAPE, "moe_forward: E=%d exceeds 448", E);
+  const bool has_shared = shared_gate != nullptr;
+  GLM_REQUIRE(!has_shared || (shared_up && shared_down && I_shared > 0 && I_shared % 32 == 0),
+              GLM_ERR_INVALID_ARGUMENT, "moe_forward: incomplete shared expert (I_shared=%d)",
+              I_shared);
+  GLM_REQUIRE(shared_fmt == GLM_FMT_BF16 || shared_fmt == GLM_FMT_MXFP8 ||
+                  shared_fmt == GLM_FMT_MXFP4,
+              GLM_ERR_INVALID_ARGUMENT, "moe_forward: unknown shared format %d", shared_fmt);
+  GLM_REQUIRE(!has_shared || shared_fmt == GLM_FMT_BF16 ||
+                  (shared_gate_scales && shared_up_scales && shared_down_scales),
+              GLM_ERR_INVALID_ARGUMENT, "moe_forward: MX shared expert needs scales");
+  int rc = glm_router_validate(x, T, d, router_weight, router_bias, E, top_k, n_group,
+                               topk_group, out, out);
+  if (rc != GLM_OK) return rc;
+  GLM_REQUIRE(glm_aligned16({x, router_weight, router_bias, gate_packed, up_packed, down_packed,
+                              shared_gate, shared_up, shared_down, workspace, out, weights_out,
+                              indices_out}),
+              GLM_ERR_INVALID_ARGUMENT, "moe_forward: buffers must be 16-byte aligned");
+  const Workspace need = carve(nullptr, T, d, E, top_k, I, has_shared ? I_shared : 0);
+  GLM_REQUIRE(workspace_bytes >= need.bytes, GLM_ERR_WORKSPACE,
+              "moe_forward: workspace of %zu bytes is below the %zu required", workspace_bytes,
+              need.bytes);
+  if (T == 0) return GLM_OK;
+  Workspace w = carve((char *)workspace, T, d, E, top_k, I, has_shared ? I_shared : 0);
+  float *wts = weights_out ? weights_out : w.weights;
+  uint32_t *idx = indices_out ? indices_out : w.indices;
+
+  rc = glm_router_launch(stream, x, T, d, router_weight, router_bias, E, top_k, n_group,
+                         topk_group, norm_topk_prob, routed_scaling_factor, w.logits, wts, idx);
+  if (rc) return rc;
+  rc = glm_dispatch_launch(stream, idx, T, top_k, E, w.counts, w.offsets, w.perm, w.inv,
+                           w.pair_token, w.active, w.num_active, w.status);
+  if (rc) return rc;
+  rc = glm_gate_up_launch(stream, x, T, d, I, E, top_k, gate_packed, gate_scales, up_packed,
+                          up_scales, w.offsets, w.pair_token, w.active, w.num_active,
+                          swiglu_limit, w.h);
+  if (rc) return rc;
+  rc = glm_down_launch(stream, w.h, T, top_k, I, d, E, down_packed, down_scales, w.offsets,
+                       w.active, w.num_active, w.y);
+  if (rc) return rc;
+  if (has_shared) {
+    rc = glm_mlp_launch(stream, x, T, d, I_shared, shared_fmt, shared_gate, shared_gate_scales,
+                        shared_up, shared_up_scales, shared_down, shared_down_scales,
+                        swiglu_limit, w.shared_h, w.shared_out);
+    if (rc) return rc;
+  }
+  return glm_combine_launch(stream, w.y, w.inv, wts, has_shared ? w.shared_out : nullptr, T,
+                            top_k, d, out);
+}

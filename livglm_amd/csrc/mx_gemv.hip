@@ -1,0 +1,570 @@
+// Skinny GEMM ("GEMV" for decode) on MX-quantised or bf16 weights, for gfx950.
+//
+// out[pos][row] = bf16( sum_k act[arow(pos)][k] * W_e[row][k] )      (NPROJ = 1)
+// out[pos][row] = limited_swiglu(bf16(x.Wg_e[row]), bf16(x.Wu_e[row]))  (NPROJ = 2)
+//
+// Used for the routed expert projections (W_e = expert e of a stacked bank,
+// rows grouped by the dispatch offsets), for the shared expert and for the
+// resident linears (one "expert", identity activation rows).
+//
+// Mapping onto CDNA4: a wave owns a 16-row tile of W and a slice of K.  For
+// each 128-wide K chunk, lane (r = l & 15, q = l >> 4) reads the 16 bytes of
+// packed MXFP4 codes that form ONE complete E8M0 group of row r (group
+// 4c + q; a wave's load touches 16 rows x 64 contiguous bytes), converts them
+// with v_cvt_scalef32_pk_bf16_fp4 (scale applied in the convert -- the values
+// are exact in bf16) and feeds four v_mfma_f32_16x16x32_bf16 whose B operand
+// is the activation columns of up to 16 tokens.  The MFMA performs the K
+// reduction, so no cross-lane shuffles are needed; the K-split partials of a
+// workgroup are reduced through LDS in a fixed wave order, so results are
+// deterministic.  K index of MFMA i, slot s of lane (r, q) = c*128 + 32q + 8i + s.
+#include "glm_common.h"
+
+#include <algorithm>
+
+namespace glm {
+
+enum { FMT_BF16 = GLM_FMT_BF16, FMT_MXFP8 = GLM_FMT_MXFP8, FMT_MXFP4 = GLM_FMT_MXFP4 };
+
+struct GemvArgs {
+  const uint16_t *act;       // activation rows, bf16 [*][K]
+  const int32_t *act_index;  // sorted position -> activation row; nullptr = identity
+  const uint8_t *w[2];       // weights of expert 0, per projection
+  const uint8_t *s[2];       // scales of expert 0, per projection (unused for bf16)
+  long long w_stride;        // bytes between consecutive experts' weights
+  long long s_stride;        // bytes between consecutive experts' scales
+  int N;                     // rows per expert (output features)
+  int K;                     // reduction length
+  const int32_t *offsets;    // [E+1] routed mode; nullptr = dense mode
+  const int32_t *active;     // [E] active expert ids (routed mode)
+  const int32_t *num_active; // [1] (routed mode)
+  int dense_rows;            // dense mode: number of activation rows
+  uint16_t *out;             // bf16 [pos][N]
+  float limit;               // bf16-rounded swiglu limit (NPROJ == 2)
+};
+
+__host__ __device__ constexpr int row_bytes(int fmt, int K) {
+  return fmt == FMT_MXFP4 ? K / 2 : (fmt == FMT_MXFP8 ? K : 2 * K);
+}
+
+// Raw bytes of one (16-row x 128-K) chunk for one lane.
+template <int FMT>
+struct Raw;
+template <>
+struct Raw<FMT_MXFP4> {
+  glm_u32x4 c;
+  uint32_t s;
+};
+template <>
+struct Raw<FMT_MXFP8> {
+  glm_u32x4 c0, c1;
+  uint32_t s;
+};
+template <>
+struct Raw<FMT_BF16> {
+  glm_u32x4 v[4];
+};
+
+template <int FMT>
+__device__ __forceinline__ Raw<FMT> load_raw(const uint8_t *wrow, const uint8_t *srow, int k0,
+                                             int q);
+
+template <>
+__device__ __forceinline__ Raw<FMT_MXFP4> load_raw<FMT_MXFP4>(const uint8_t *wrow,
+                                                              const uint8_t *srow, int k0,
+                                                              int q) {
+  Raw<FMT_MXFP4> r;
+  r.c = *reinterpret_cast<const glm_u32x4 *>(wrow + (k0 >> 1) + 16 * q);
+  r.s = srow[(k0 >> 5) + q];
+  return r;
+}
+
+template <>
+__device__ __forceinline__ Raw<FMT_MXFP8> load_raw<FMT_MXFP8>(const uint8_t *wrow,
+                                                              const uint8_t *srow, int k0,
+                                                              int q) {
+  Raw<FMT_MXFP8> r;
+  const glm_u32x4 *p = reinterpret_cast<const glm_u32x4 *>(wrow + k0 + 32 * q);
+  r.c0 = p[0];
+  r.c1 = p[1];
+  r.s = srow[(k0 >> 5) + q];
+  return r;
+}
+
+template <>
+__device__ __forceinline__ Raw<FMT_BF16> load_raw<FMT_BF16>(const uint8_t *wrow,
+                                                            const uint8_t *srow, int k0, int q) {
+  Raw<FMT_BF16> r;
+  const glm_u32x4 *p = reinterpret_cast<const glm_u32x4 *>(wrow + 2 * (k0 + 32 * q));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r.v[i] = p[i];
+  return r;
+}
+
+// Dequantise one raw chunk into the four MFMA A fragments.
+template <int FMT>
+__device__ __forceinline__ void to_frags(const Raw<FMT> &r, glm_bf16x8 a[4]);
+
+template <>
+__device__ __forceinline__ void to_frags<FMT_MXFP4>(const Raw<FMT_MXFP4> &r, glm_bf16x8 a[4]) {
+  const float sc = e8m0_to_f32(r.s);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = mxfp4_word_to_bf16x8(r.c[i], sc);
+}
+
+template <>
+__device__ __forceinline__ void to_frags<FMT_MXFP8>(const Raw<FMT_MXFP8> &r, glm_bf16x8 a[4]) {
+  const float sc = e8m0_to_f32(r.s);
+  a[0] = mxfp8_words_to_bf16x8(r.c0[0], r.c0[1], sc);
+  a[1] = mxfp8_words_to_bf16x8(r.c0[2], r.c0[3], sc);
+  a[2] = mxfp8_words_to_bf16x8(r.c1[0], r.c1[1], sc);
+  a[3] = mxfp8_words_to_bf16x8(r.c1[2], r.c1[3], sc);
+}
+
+template <>
+__device__ __forceinline__ void to_frags<FMT_BF16>(const Raw<FMT_BF16> &r, glm_bf16x8 a[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = __builtin_bit_cast(glm_bf16x8, r.v[i]);
+}
+
+constexpr int kMaxTiles = 4;  // token tiles of 16 held in registers per pass
+
+template <int FMT, int NPROJ, int CPW>
+__global__ __launch_bounds__(512) void mx_gemv_kernel(const GemvArgs args) {
+  extern __shared__ glm_f32x4 red[];  // [ksplit][kMaxTiles][NPROJ][64]
+  const int ksplit = blockDim.x >> 6;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int q = lane >> 4;
+
+  int e = 0, base = 0, n = args.dense_rows;
+  if (args.offsets != nullptr) {
+    const int u = blockIdx.y;
+    if (u >= args.num_active[0]) return;
+    e = args.active[u];
+    base = args.offsets[e];
+    n = args.offsets[e + 1] - base;
+  }
+  if (n <= 0) return;
+  const int K = args.K;
+  const int N = args.N;
+  const int row0 = blockIdx.x * 16;
+  const int rb = row_bytes(FMT, K);
+  const uint8_t *wrow[NPROJ];
+  const uint8_t *srow[NPROJ];
+#pragma unroll
+  for (int p = 0; p < NPROJ; ++p) {
+    wrow[p] = args.w[p] + (long long)e * args.w_stride + (long long)(row0 + r) * rb;
+    srow[p] = FMT == FMT_BF16 ? nullptr
+                              : args.s[p] + (long long)e * args.s_stride +
+                                    (long long)(row0 + r) * (K >> 5);
+  }
+  const int kbase = wave * CPW * 128;
+
+  for (int p0 = 0; p0 < n; p0 += 16 * kMaxTiles) {
+    const int ntiles = min(kMaxTiles, (n - p0 + 15) >> 4);
+    // Issue every weight load of this wave first.
+    Raw<FMT> raw[NPROJ][CPW];
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+      for (int p = 0; p < NPROJ; ++p) raw[p][c] = load_raw<FMT>(wrow[p], srow[p], kbase + c * 128, q);
+
+    // Activation row of this lane's token column, per tile (-1 = padding).
+    int arow[kMaxTiles];
+#pragma unroll
+    for (int tt = 0; tt < kMaxTiles; ++tt) {
+      const int pair = p0 + tt * 16 + r;
+      arow[tt] = -1;
+      if (tt < ntiles && pair < n)
+        arow[tt] = args.act_index ? args.act_index[base + pair] : base + pair;
+    }
+
+    glm_f32x4 acc[kMaxTiles][NPROJ];
+#pragma unroll
+    for (int tt = 0; tt < kMaxTiles; ++tt)
+#pragma unroll
+      for (int p = 0; p < NPROJ; ++p) acc[tt][p] = glm_f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      glm_bf16x8 a[NPROJ][4];
+#pragma unroll
+      for (int p = 0; p < NPROJ; ++p) to_frags<FMT>(raw[p][c], a[p]);
+      const int k0 = kbase + c * 128 + 32 * q;
+#pragma unroll
+      for (int tt = 0; tt < kMaxTiles; ++tt) {
+        if (tt < ntiles) {
+          glm_bf16x8 b[4];
+          if (arow[tt] >= 0) {
+            const glm_bf16x8 *src =
+                reinterpret_cast<const glm_bf16x8 *>(args.act + (long long)arow[tt] * K + k0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) b[i] = src[i];
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) b[i] = glm_bf16x8{};
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int p = 0; p < NPROJ; ++p)
+              acc[tt][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[p][i], b[i], acc[tt][p], 0, 0, 0);
+        }
+      }
+    }
+
+    // Fixed-order reduction of the K-split partials.
+    if (ksplit > 1) {
+#pragma unroll
+      for (int tt = 0; tt < kMaxTiles; ++tt)
+        if (tt < ntiles)
+#pragma unroll
+          for (int p = 0; p < NPROJ; ++p)
+            red[((wave * kMaxTiles + tt) * NPROJ + p) * 64 + lane] = acc[tt][p];
+      __syncthreads();
+    }
+    // Wave w finishes tiles tt = w, w + ksplit, ...
+    for (int tt = (ksplit > 1 ? wave : 0); tt < ntiles; tt += ksplit) {
+      glm_f32x4 sum[NPROJ];
+      if (ksplit > 1) {
+#pragma unroll
+        for (int p = 0; p < NPROJ; ++p) {
+          sum[p] = red[((0 * kMaxTiles + tt) * NPROJ + p) * 64 + lane];
+          for (int w = 1; w < ksplit; ++w) sum[p] += red[((w * kMaxTiles + tt) * NPROJ + p) * 64 + lane];
+        }
+      } else {
+        // ksplit == 1: the loop visits every tile; select it from registers.
+#pragma unroll
+        for (int t2 = 0; t2 < kMaxTiles; ++t2)
+          if (t2 == tt)
+#pragma unroll
+            for (int p = 0; p < NPROJ; ++p) sum[p] = acc[t2][p];
+      }
+      // Lane (r, q) holds rows 4q..4q+3 of the tile for token column r.
+      const int pair = p0 + tt * 16 + r;
+      if (pair < n) {
+        uint32_t o[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          if (NPROJ == 2) {
+            const float g = bf16_round(sum[0][m]);
+            const float u = bf16_round(sum[NPROJ - 1][m]);
+            o[m] = f32_to_bf16(limited_swiglu(g, u, args.limit));
+          } else {
+            o[m] = f32_to_bf16(sum[0][m]);
+          }
+        }
+        uint2 packed;
+        packed.x = o[0] | (o[1] << 16);
+        packed.y = o[2] | (o[3] << 16);
+        *reinterpret_cast<uint2 *>(args.out + (long long)(base + pair) * N + row0 + 4 * q) = packed;
+      }
+    }
+    if (ksplit > 1) __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Generic fallback for shapes the MFMA tiling does not cover (K % 128 or
+// N % 16 non-zero; e.g. the tiny test geometries).  One thread per output.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float e2m1_value(uint32_t code) {
+  const float mags[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+  const float m = mags[code & 7];
+  return (code & 8) ? -m : m;
+}
+
+__device__ __forceinline__ float e4m3fn_value(uint32_t byte) {
+  const uint32_t e = (byte >> 3) & 15, m = byte & 7;
+  float v;
+  if (e == 0) v = ldexpf((float)m / 8.0f, -6);
+  else if (e == 15 && m == 7) v = __uint_as_float(0x7fc00000u);
+  else v = ldexpf(1.0f + (float)m / 8.0f, (int)e - 7);
+  return (byte & 0x80) ? -v : v;
+}
+
+template <int FMT>
+__device__ __forceinline__ float weight_at(const uint8_t *wrow, const uint8_t *srow, int k) {
+  if (FMT == FMT_BF16) return bf16_to_f32(reinterpret_cast<const uint16_t *>(wrow)[k]);
+  const float sc = e8m0_to_f32(srow[k >> 5]);
+  if (FMT == FMT_MXFP4) {
+    const uint32_t byte = wrow[k >> 1];
+    return e2m1_value((k & 1) ? (byte >> 4) : (byte & 15)) * sc;
+  }
+  return e4m3fn_value(wrow[k]) * sc;
+}
+
+template <int FMT, int NPROJ>
+__global__ __launch_bounds__(256) void gemv_generic_kernel(const GemvArgs args) {
+  const int row = blockIdx.x * blockDim.x + threadIdx.x;
+  int e = 0, base = 0, n = args.dense_rows;
+  if (args.offsets != nullptr) {
+    const int u = blockIdx.y;
+    if (u >= args.num_active[0]) return;
+    e = args.active[u];
+    base = args.offsets[e];
+    n = args.offsets[e + 1] - base;
+  }
+  if (row >= args.N) return;
+  const int K = args.K;
+  const int rb = row_bytes(FMT, K);
+  const uint8_t *wrow[NPROJ];
+  const uint8_t *srow[NPROJ];
+  for (int p = 0; p < NPROJ; ++p) {
+    wrow[p] = args.w[p] + (long long)e * args.w_stride + (long long)row * rb;
+    srow[p] = FMT == FMT_BF16 ? nullptr
+                              : args.s[p] + (long long)e * args.s_stride + (long long)row * (K >> 5);
+  }
+  for (int pair = 0; pair < n; ++pair) {
+    const int arow = args.act_index ? args.act_index[base + pair] : base + pair;
+    const uint16_t *xr = args.act + (long long)arow * K;
+    float acc[NPROJ];
+    for (int p = 0; p < NPROJ; ++p) {
+      float a = 0.0f;
+      for (int k = 0; k < K; ++k) a = fmaf(bf16_to_f32(xr[k]), weight_at<FMT>(wrow[p], srow[p], k), a);
+      acc[p] = a;
+    }
+    float v;
+    if (NPROJ == 2) v = limited_swiglu(bf16_round(acc[0]), bf16_round(acc[NPROJ - 1]), args.limit);
+    else v = acc[0];
+    args.out[(long long)(base + pair) * args.N + row] = (uint16_t)f32_to_bf16(v);
+  }
+}
+
+}  // namespace glm
+
+using glm::GemvArgs;
+
+// Picks the K split for the MFMA path: total chunks KC = K/128 = ksplit*cpw.
+static bool choose_split(int fmt, int nproj, int K, int *ksplit, int *cpw) {
+  if (K % 128 != 0) return false;
+  const int kc = K / 128;
+  const int max_cpw = (fmt == GLM_FMT_BF16 && nproj == 2) ? 2 : 4;
+  // Prefer a 4-wave split, then 2, 8, 1; within that the largest cpw that fits.
+  const int splits[] = {4, 2, 8, 1, 3, 6};
+  for (int s : splits) {
+    if (kc % s) continue;
+    const int c = kc / s;
+    if (c >= 1 && c <= max_cpw) {
+      *ksplit = s;
+      *cpw = c;
+      return true;
+    }
+  }
+  return false;
+}
+
+template <int FMT, int NPROJ>
+static int launch_fmt(hipStream_t stream, const GemvArgs &a, int grid_y) {
+  int ksplit = 0, cpw = 0;
+  if (a.N % 16 == 0 && choose_split(FMT, NPROJ, a.K, &ksplit, &cpw)) {
+    dim3 grid(a.N / 16, grid_y);
+    dim3 block(64 * ksplit);
+    const size_t lds = ksplit > 1 ? (size_t)ksplit * glm::kMaxTiles * NPROJ * 64 * 16 : 0;
+    switch (cpw) {
+      case 1:
+        hipLaunchKernelGGL((glm::mx_gemv_kernel<FMT, NPROJ, 1>), grid, block, lds, stream, a);
+        break;
+      case 2:
+        hipLaunchKernelGGL((glm::mx_gemv_kernel<FMT, NPROJ, 2>), grid, block, lds, stream, a);
+        break;
+      case 3:
+        hipLaunchKernelGGL((glm::mx_gemv_kernel<FMT, NPROJ, 3>), grid, block, lds, stream, a);
+        break;
+      default:
+        hipLaunchKernelGGL((glm::mx_gemv_kernel<FMT, NPROJ, 4>), grid, block, lds, stream, a);
+        break;
+    }
+    GLM_LAUNCH_CHECK("mx_gemv_kernel");
+    return GLM_OK;
+  }
+  dim3 grid((a.N + 255) / 256, grid_y);
+  hipLaunchKernelGGL((glm::gemv_generic_kernel<FMT, NPROJ>), grid, dim3(256), 0, stream, a);
+  GLM_LAUNCH_CHECK("gemv_generic_kernel");
+  return GLM_OK;
+}
+
+// grid_y = number of expert slots to cover (routed) or 1 (dense).
+int glm_gemv_launch(hipStream_t stream, int fmt, int nproj, const GemvArgs &a, int grid_y) {
+  if (grid_y <= 0) return GLM_OK;
+  if (nproj == 2) {
+    switch (fmt) {
+      case GLM_FMT_MXFP4: return launch_fmt<GLM_FMT_MXFP4, 2>(stream, a, grid_y);
+      case GLM_FMT_MXFP8: return launch_fmt<GLM_FMT_MXFP8, 2>(stream, a, grid_y);
+      default: return launch_fmt<GLM_FMT_BF16, 2>(stream, a, grid_y);
+    }
+  }
+  switch (fmt) {
+    case GLM_FMT_MXFP4: return launch_fmt<GLM_FMT_MXFP4, 1>(stream, a, grid_y);
+    case GLM_FMT_MXFP8: return launch_fmt<GLM_FMT_MXFP8, 1>(stream, a, grid_y);
+    default: return launch_fmt<GLM_FMT_BF16, 1>(stream, a, grid_y);
+  }
+}
+
+static int check_fmt(int fmt) {
+  GLM_REQUIRE(fmt == GLM_FMT_BF16 || fmt == GLM_FMT_MXFP8 || fmt == GLM_FMT_MXFP4,
+              GLM_ERR_INVALID_ARGUMENT, "unknown weight format %d", fmt);
+  return GLM_OK;
+}
+
+int glm_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int E, int k,
+                       const uint8_t *gw, const uint8_t *gs, const uint8_t *uw, const uint8_t *us,
+                       const int32_t *offsets, const int32_t *pair_token, const int32_t *active,
+                       const int32_t *num_active, float limit, uint16_t *h) {
+  GemvArgs a{};
+  a.act = x;
+  a.act_index = pair_token;
+  a.w[0] = gw;
+  a.w[1] = uw;
+  a.s[0] = gs;
+  a.s[1] = us;
+  a.w_stride = (long long)I * (d / 2);
+  a.s_stride = (long long)I * (d / 32);
+  a.N = I;
+  a.K = d;
+  a.offsets = offsets;
+  a.active = active;
+  a.num_active = num_active;
+  a.out = h;
+  a.limit = glm_limit_bf16(limit);
+  const int slots = std::min(E, T * k);
+  return glm_gemv_launch(stream, GLM_FMT_MXFP4, 2, a, slots);
+}
+
+int glm_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, int d, int E,
+                    const uint8_t *dw, const uint8_t *ds, const int32_t *offsets,
+                    const int32_t *active, const int32_t *num_active, uint16_t *y) {
+  GemvArgs a{};
+  a.act = h;
+  a.act_index = nullptr;
+  a.w[0] = a.w[1] = dw;
+  a.s[0] = a.s[1] = ds;
+  a.w_stride = (long long)d * (I / 2);
+  a.s_stride = (long long)d * (I / 32);
+  a.N = d;
+  a.K = I;
+  a.offsets = offsets;
+  a.active = active;
+  a.num_active = num_active;
+  a.out = y;
+  const int slots = std::min(E, T * k);
+  return glm_gemv_launch(stream, GLM_FMT_MXFP4, 1, a, slots);
+}
+
+int glm_linear_launch(hipStream_t stream, const uint16_t *x, int T, int in_dims,
+                      const void *weight, const uint8_t *scales, int fmt, int out_dims,
+                      uint16_t *y) {
+  GemvArgs a{};
+  a.act = x;
+  a.w[0] = a.w[1] = static_cast<const uint8_t *>(weight);
+  a.s[0] = a.s[1] = scales;
+  a.N = out_dims;
+  a.K = in_dims;
+  a.dense_rows = T;
+  a.out = y;
+  return glm_gemv_launch(stream, fmt, 1, a, T > 0 ? 1 : 0);
+}
+
+int glm_mlp_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int fmt,
+                   const void *gw, const uint8_t *gs, const void *uw, const uint8_t *us,
+                   const void *dw, const uint8_t *ds, float limit, uint16_t *h, uint16_t *out) {
+  GemvArgs a{};
+  a.act = x;
+  a.w[0] = static_cast<const uint8_t *>(gw);
+  a.w[1] = static_cast<const uint8_t *>(uw);
+  a.s[0] = gs;
+  a.s[1] = us;
+  a.N = I;
+  a.K = d;
+  a.dense_rows = T;
+  a.out = h;
+  a.limit = glm_limit_bf16(limit);
+  int rc = glm_gemv_launch(stream, fmt, 2, a, T > 0 ? 1 : 0);
+  if (rc != GLM_OK) return rc;
+  return glm_linear_launch(stream, h, T, I, dw, ds, fmt, d, out);
+}
+
+static int check_mx_geometry(const char *who, int fmt, int in_dims, int out_dims) {
+  GLM_REQUIRE(in_dims > 0 && out_dims > 0, GLM_ERR_INVALID_ARGUMENT, "%s: invalid dims %d x %d",
+              who, out_dims, in_dims);
+  GLM_REQUIRE(in_dims % 32 == 0, GLM_ERR_UNSUPPORTED_SHAPE,
+              "%s: input width %d is not a multiple of 32", who, in_dims);
+  (void)fmt;
+  return GLM_OK;
+}
+
+extern "C" int glm_expert_gate_up(void *stream, const uint16_t *x, int T, int d, int I, int E,
+                                  int top_k, const uint8_t *gate_packed,
+                                  const uint8_t *gate_scales, const uint8_t *up_packed,
+                                  const uint8_t *up_scales, const int32_t *offsets,
+                                  const int32_t *pair_token, const int32_t *active,
+                                  const int32_t *num_active, float swiglu_limit, uint16_t *h) {
+  glm::clear_error();
+  GLM_REQUIRE(x && gate_packed && gate_scales && up_packed && up_scales && offsets &&
+                  pair_token && active && num_active && h,
+              GLM_ERR_INVALID_ARGUMENT, "expert_gate_up: null pointer argument");
+  GLM_REQUIRE(T >= 0 && E >= 1 && top_k >= 1, GLM_ERR_INVALID_ARGUMENT,
+              "expert_gate_up: invalid sizes");
+  int rc = check_mx_geometry("expert_gate_up", GLM_FMT_MXFP4, d, I);
+  if (rc) return rc;
+  GLM_REQUIRE(glm_aligned16({x, gate_packed, up_packed, h}), GLM_ERR_INVALID_ARGUMENT,
+              "expert_gate_up: buffers must be 16-byte aligned");
+  return glm_gate_up_launch((hipStream_t)stream, x, T, d, I, E, top_k, gate_packed, gate_scales,
+                            up_packed, up_scales, offsets, pair_token, active, num_active,
+                            swiglu_limit, h);
+}
+
+extern "C" int glm_expert_down(void *stream, const uint16_t *h, int T, int top_k, int I, int d,
+                               int E, const uint8_t *down_packed, const uint8_t *down_scales,
+                               const int32_t *offsets, const int32_t *active,
+                               const int32_t *num_active, uint16_t *y) {
+  glm::clear_error();
+  GLM_REQUIRE(h && down_packed && down_scales && offsets && active && num_active && y,
+              GLM_ERR_INVALID_ARGUMENT, "expert_down: null pointer argument");
+  GLM_REQUIRE(T >= 0 && E >= 1 && top_k >= 1, GLM_ERR_INVALID_ARGUMENT,
+              "expert_down: invalid sizes");
+  int rc = check_mx_geometry("expert_down", GLM_FMT_MXFP4, I, d);
+  if (rc) return rc;
+  GLM_REQUIRE(glm_aligned16({h, down_packed, y}), GLM_ERR_INVALID_ARGUMENT,
+              "expert_down: buffers must be 16-byte aligned");
+  return glm_down_launch((hipStream_t)stream, h, T, top_k, I, d, E, down_packed, down_scales,
+                         offsets, active, num_active, y);
+}
+
+extern "C" int glm_linear(void *stream, const uint16_t *x, int T, int in_dims, const void *weight,
+                          const uint8_t *scales, int fmt, int out_dims, uint16_t *y) {
+  glm::clear_error();
+  int rc = check_fmt(fmt);
+  if (rc) return rc;
+  GLM_REQUIRE(x && weight && y && (fmt == GLM_FMT_BF16 || scales), GLM_ERR_INVALID_ARGUMENT,
+              "linear: null pointer argument");
+  GLM_REQUIRE(T >= 0, GLM_ERR_INVALID_ARGUMENT, "linear: negative T");
+  rc = check_mx_geometry("linear", fmt, in_dims, out_dims);
+  if (rc) return rc;
+  GLM_REQUIRE(glm_aligned16({x, weight, y}), GLM_ERR_INVALID_ARGUMENT,
+              "linear: buffers must be 16-byte aligned");
+  return glm_linear_launch((hipStream_t)stream, x, T, in_dims, weight, scales, fmt, out_dims, y);
+}
+
+extern "C" int glm_dense_mlp(void *stream, const uint16_t *x, int T, int d, int I, int fmt,
+                             const void *gate_w, const uint8_t *gate_s, const void *up_w,
+                             const uint8_t *up_s, const void *down_w, const uint8_t *down_s,
+                             float swiglu_limit, uint16_t *h, uint16_t *out) {
+  glm::clear_error();
+  int rc = check_fmt(fmt);
+  if (rc) return rc;
+  GLM_REQUIRE(x && gate_w && up_w && down_w && h && out, GLM_ERR_INVALID_ARGUMENT,
+              "dense_mlp: null pointer argument");
+  GLM_REQUIRE(fmt == GLM_FMT_BF16 || (gate_s && up_s && down_s), GLM_ERR_INVALID_ARGUMENT,
+              "dense_mlp: MX weights need scales");
+  GLM_REQUIRE(T >= 0, GLM_ERR_INVALID_ARGUMENT, "dense_mlp: negative T");
+  rc = check_mx_geometry("dense_mlp", fmt, d, I);
+  if (rc) return rc;
+  rc = check_mx_geometry("dense_mlp", fmt, I, d);
+  if (rc) return rc;
+  GLM_REQUIRE(glm_aligned16({x, gate_w, up_w, down_w, h, out}), GLM_ERR_INVALID_ARGUMENT,
+              "dense_mlp: buffers must be 16-byte aligned");
+  return glm_mlp_launch((hipStream_t)stream, x, T, d, I, fmt, gate_w, gate_s, up_w, up_s, down_w,
+                        down_s, swiglu_limit, h, out);
+}

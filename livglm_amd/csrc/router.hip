@@ -1,0 +1,235 @@
+// Router: logits GEMV + sigmoid/bias/group-mask/top-k/normalise.
+// Restates TopKRouter.__call__ (moe.py:36-63) for gfx950.
+#include "glm_common.h"
+
+namespace glm {
+
+// ---------------------------------------------------------------------------
+// logits[t][e] = sum_i f32(x[t][i]) * w[e][i]
+//
+// One wave owns one expert row of W (read once per TT-token pass, 16 B per
+// lane per step, fully coalesced) and TT tokens; lane l accumulates the K
+// positions 4l + 256s.  The final f32 value is a butterfly wave sum.
+// ---------------------------------------------------------------------------
+template <int TT>
+__global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t *__restrict__ x,
+                                                            const float *__restrict__ w, int T,
+                                                            int d, int E,
+                                                            float *__restrict__ logits) {
+  const int lane = threadIdx.x & 63;
+  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int t0 = blockIdx.y * TT;
+  if (e >= E) return;
+  const float *wrow = w + (size_t)e * d;
+  float acc[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) acc[t] = 0.0f;
+  const int nt = min(TT, T - t0);
+  for (int k = lane * 4; k < d; k += 256) {
+    const float4 wv = *reinterpret_cast<const float4 *>(wrow + k);
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      if (t < nt) {
+        const uint2 xv = *reinterpret_cast<const uint2 *>(x + (size_t)(t0 + t) * d + k);
+        float a = acc[t];
+        a = fmaf(bf16_to_f32(xv.x & 0xffffu), wv.x, a);
+        a = fmaf(bf16_to_f32(xv.x >> 16), wv.y, a);
+        a = fmaf(bf16_to_f32(xv.y & 0xffffu), wv.z, a);
+        a = fmaf(bf16_to_f32(xv.y >> 16), wv.w, a);
+        acc[t] = a;
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    if (t < nt) {
+      const float v = wave_sum(acc[t]);
+      if (lane == 0) logits[(size_t)(t0 + t) * E + e] = v;
+    }
+  }
+}
+
+// Lexicographic "better" for (value, index): larger value; on a tie the
+// larger index (a stable ascending argsort puts it last, moe.py:33-34).
+__device__ __forceinline__ bool better(float v1, int i1, float v2, int i2) {
+  return v1 > v2 || (v1 == v2 && i1 > i2);
+}
+
+// ---------------------------------------------------------------------------
+// Selection: one wave per token.  Lane l holds experts l + 64 i.
+// ---------------------------------------------------------------------------
+template <int EPL>
+__global__ __launch_bounds__(64) void router_select_kernel(
+    const float *__restrict__ logits, const float *__restrict__ bias, int T, int E, int k,
+    int n_group, int topk_group, int norm, float scale, float *__restrict__ weights,
+    uint32_t *__restrict__ indices) {
+  __shared__ float s_choice[64 * EPL];
+  __shared__ float s_gscore[64];
+  __shared__ int s_gkeep[64];
+  __shared__ float s_wsel[64];
+  __shared__ int s_isel[64];
+  const int t = blockIdx.x;
+  const int lane = threadIdx.x;
+  if (t >= T) return;
+  float score[EPL], choice[EPL];
+  bool taken[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    taken[i] = false;
+    if (e < E) {
+      const float l = logits[(size_t)t * E + e];
+      score[i] = sigmoid_f32(l);
+      choice[i] = score[i] + bias[e];
+    } else {
+      score[i] = 0.0f;
+      choice[i] = -INFINITY;
+      taken[i] = true;  // never selectable
+    }
+  }
+  if (n_group > 1) {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) s_choice[lane + 64 * i] = choice[i];
+    __syncthreads();
+    const int per = E / n_group;
+    if (lane < n_group) {
+      float top1 = -INFINITY, top2 = -INFINITY;
+      for (int q = 0; q < per; ++q) {
+        const float v = s_choice[lane * per + q];
+        if (v > top1) {
+          top2 = top1;
+          top1 = v;
+        } else if (v > top2) {
+          top2 = v;
+        }
+      }
+      s_gscore[lane] = top2 + top1;
+    }
+    __syncthreads();
+    if (lane < n_group) {
+      const float mine = s_gscore[lane];
+      int rank = 0;
+      for (int g = 0; g < n_group; ++g)
+        if (better(s_gscore[g], g, mine, lane)) ++rank;
+      s_gkeep[lane] = rank < topk_group;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E && !s_gkeep[e / per]) choice[i] = -INFINITY;
+    }
+  }
+  // k rounds of wave-wide argmax; round r fills ascending position k-1-r.
+  for (int r = 0; r < k; ++r) {
+    float bv = -INFINITY, bs = 0.0f;
+    int bi = -1;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      if (!taken[i] && (bi < 0 || better(choice[i], e, bv, bi))) {
+        bv = choice[i];
+        bi = e;
+        bs = score[i];
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      const float os = __shfl_xor(bs, off, 64);
+      if (oi >= 0 && (bi < 0 || better(ov, oi, bv, bi))) {
+        bv = ov;
+        bi = oi;
+        bs = os;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < EPL; ++i)
+      if (lane + 64 * i == bi) taken[i] = true;
+    if (lane == 0) {
+      s_isel[k - 1 - r] = bi;
+      s_wsel[k - 1 - r] = bs;
+    }
+  }
+  __syncthreads();
+  if (lane == 0) {
+    float total = 0.0f;
+    if (norm)
+      for (int j = 0; j < k; ++j) total += s_wsel[j];
+    for (int j = 0; j < k; ++j) {
+      float wj = s_wsel[j];
+      if (norm) wj = wj / (total + 1e-20f);
+      weights[(size_t)t * k + j] = wj * scale;
+      indices[(size_t)t * k + j] = (uint32_t)s_isel[j];
+    }
+  }
+}
+
+}  // namespace glm
+
+// Launches the router; `logits` must be a valid [T][E] buffer here.
+int glm_router_launch(hipStream_t stream, const uint16_t *x, int T, int d, const float *weight,
+                      const float *bias, int E, int k, int n_group, int topk_group, int norm,
+                      float scale, float *logits, float *weights, uint32_t *indices) {
+  using namespace glm;
+  if (T == 0) return GLM_OK;
+  if (T <= 2) {
+    dim3 grid((E + 3) / 4, (T + 1) / 2);
+    hipLaunchKernelGGL(router_logits_kernel<2>, grid, dim3(256), 0, stream, x, weight, T, d, E,
+                       logits);
+  } else {
+    dim3 grid((E + 3) / 4, (T + 7) / 8);
+    hipLaunchKernelGGL(router_logits_kernel<8>, grid, dim3(256), 0, stream, x, weight, T, d, E,
+                       logits);
+  }
+  GLM_LAUNCH_CHECK("router_logits_kernel");
+  const int epl = (E + 63) / 64;
+#define GLM_SELECT(N)                                                                         \
+  hipLaunchKernelGGL(router_select_kernel<N>, dim3(T), dim3(64), 0, stream, logits, bias, T, \
+                     E, k, n_group, topk_group, norm, scale, weights, indices)
+  if (epl <= 1) GLM_SELECT(1);
+  else if (epl <= 2) GLM_SELECT(2);
+  else if (epl <= 4) GLM_SELECT(4);
+  else if (epl <= 8) GLM_SELECT(8);
+  else GLM_SELECT(16);
+#undef GLM_SELECT
+  GLM_LAUNCH_CHECK("router_select_kernel");
+  return GLM_OK;
+}
+
+int glm_router_validate(const void *x, int T, int d, const void *weight, const void *bias, int E,
+                        int k, int n_group, int topk_group, const void *weights,
+                        const void *indices) {
+  GLM_REQUIRE(x && weight && bias && weights && indices, GLM_ERR_INVALID_ARGUMENT,
+              "router: null pointer argument");
+  GLM_REQUIRE(T >= 0 && d > 0 && E > 0, GLM_ERR_INVALID_ARGUMENT,
+              "router: invalid sizes T=%d d=%d E=%d", T, d, E);
+  GLM_REQUIRE(d % 4 == 0, GLM_ERR_UNSUPPORTED_SHAPE, "router: d=%d must be a multiple of 4", d);
+  GLM_REQUIRE(E <= 1024, GLM_ERR_UNSUPPORTED_SHAPE, "router: E=%d exceeds 1024", E);
+  GLM_REQUIRE(k >= 1 && k <= E, GLM_ERR_INVALID_ARGUMENT, "router: invalid top-k %d for E=%d",
+              k, E);
+  GLM_REQUIRE(k <= 64, GLM_ERR_UNSUPPORTED_SHAPE, "router: top-k %d exceeds 64", k);
+  GLM_REQUIRE(glm_aligned16({x, weight, bias, weights, indices}), GLM_ERR_INVALID_ARGUMENT,
+              "router: buffers must be 16-byte aligned");
+  GLM_REQUIRE(n_group >= 1 && n_group <= 64 && E % n_group == 0 && E / n_group >= 2,
+              GLM_ERR_INVALID_ARGUMENT, "router: invalid n_group=%d for E=%d", n_group, E);
+  GLM_REQUIRE(topk_group >= 1 && topk_group <= n_group, GLM_ERR_INVALID_ARGUMENT,
+              "router: invalid topk_group=%d", topk_group);
+  return GLM_OK;
+}
+
+extern "C" int glm_router_topk(void *stream, const uint16_t *x, int T, int d, const float *weight,
+                               const float *bias, int E, int top_k, int n_group, int topk_group,
+                               int norm_topk_prob, float routed_scaling_factor, float *logits,
+                               float *weights, uint32_t *indices) {
+  glm::clear_error();
+  int rc = glm_router_validate(x, T, d, weight, bias, E, top_k, n_group, topk_group, weights,
+                               indices);
+  if (rc != GLM_OK) return rc;
+  GLM_REQUIRE(logits != nullptr, GLM_ERR_INVALID_ARGUMENT,
+              "router: logits buffer is required by this entry point");
+  return glm_router_launch((hipStream_t)stream, x, T, d, weight, bias, E, top_k, n_group,
+                           topk_group, norm_topk_prob, routed_scaling_factor, logits, weights,
+                           indices);
+}

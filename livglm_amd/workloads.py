@@ -1,0 +1,133 @@
+"""Synthetic MoE-layer workloads (seeded) for tests and the benchmark.
+
+Shapes follow the routed-MoE layer of GLM-5.3-Flash at benchmark geometry:
+
+* ``decode_t1``    T=1,    d=1024, E=16,  k=2, I=512  (+ bf16 shared expert)
+* ``verify_t2``    T=2,    d=2048, E=128, k=8, I=768  (MTP width-two verify)
+* ``batch_t64``    T=64,   as verify_t2, Zipf(s=1.1)-skewed routing bias
+* ``prefill_t4096`` T=4096, as verify_t2, near-uniform routing
+* ``stack42_t1``   T=1, 42 layers of (2048x2048 MXFP8 resident linear + MoE
+  as verify_t2), 256 decode steps, Markov routing with 70% expert reuse
+
+Expert weights: uniform random E2M1 codes (uniform bytes) and E8M0 scale
+bytes uniform in [119, 127].  Activations bf16 N(0, 1).  Router weight f32
+N(0, 0.02), bias 0 unless stated.  Shared expert bf16 N(0, 0.02).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+
+@dataclass(frozen=True)
+class MoEShape:
+    name: str
+    T: int
+    d: int
+    E: int
+    k: int
+    I: int
+    I_shared: int
+    routing: str = "uniform"  # "uniform" | "zipf" | "markov"
+    n_group: int = 1
+    topk_group: int = 1
+    routed_scaling_factor: float = 2.5
+    swiglu_limit: float = 10.0
+    norm_topk_prob: bool = True
+    layers: int = 1
+    steps: int = 1
+
+    @property
+    def expert_bytes(self) -> int:
+        """MXFP4 bytes of one expert: 3 projections x (I*d/2 codes + I*d/32 scales)."""
+        return 3 * (self.I * self.d // 2 + self.I * self.d // 32)
+
+    @property
+    def bank_bytes(self) -> int:
+        return self.E * self.expert_bytes
+
+
+SHAPES = {
+    "decode_t1": MoEShape("decode_t1", T=1, d=1024, E=16, k=2, I=512, I_shared=512),
+    "verify_t2": MoEShape("verify_t2", T=2, d=2048, E=128, k=8, I=768, I_shared=768),
+    "batch_t64": MoEShape("batch_t64", T=64, d=2048, E=128, k=8, I=768, I_shared=768,
+                          routing="zipf"),
+    "prefill_t4096": MoEShape("prefill_t4096", T=4096, d=2048, E=128, k=8, I=768, I_shared=768),
+    "stack42_t1": MoEShape("stack42_t1", T=1, d=2048, E=128, k=8, I=768, I_shared=768,
+                           routing="markov", layers=42, steps=256),
+}
+
+SCALE_LO, SCALE_HI = 119, 127  # inclusive E8M0 range of the synthetic scales
+
+
+def f32_to_bf16_bits(a: np.ndarray) -> np.ndarray:
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def zipf_bias(E: int, rng: np.random.Generator, s: float = 1.1, scale: float = 1.0) -> np.ndarray:
+    """Per-expert bias from a Zipf(s) rank profile over a random expert order:
+    ``bias[pi[r]] = scale * (r + 1) ** -s``."""
+    order = rng.permutation(E)
+    bias = np.zeros(E, dtype=np.float32)
+    bias[order] = (scale * np.arange(1, E + 1, dtype=np.float64) ** (-s)).astype(np.float32)
+    return bias
+
+
+def markov_bias_trace(E: int, k: int, layers: int, steps: int, rng: np.random.Generator,
+                      keep: float = 0.7, boost: float = 10.0) -> np.ndarray:
+    """Bias vectors [steps, layers, E] that force each layer's top-k to keep
+    each of the previous step's experts with probability ``keep`` and draw the
+    rest uniformly from the unused experts (a boost of ``boost`` on the chosen
+    set dominates every sigmoid score)."""
+    out = np.zeros((steps, layers, E), dtype=np.float32)
+    prev = [rng.choice(E, k, replace=False) for _ in range(layers)]
+    for s in range(steps):
+        for layer in range(layers):
+            if s == 0:
+                chosen = prev[layer]
+            else:
+                kept = [e for e in prev[layer] if rng.random() < keep]
+                pool = np.setdiff1d(np.arange(E), kept)
+                fresh = rng.choice(pool, k - len(kept), replace=False)
+                chosen = np.concatenate([np.array(kept, dtype=np.int64), fresh])
+            out[s, layer, chosen] = boost
+            prev[layer] = chosen
+    return out
+
+
+def make_layer(shape: MoEShape, seed: int, *, T: int | None = None) -> dict[str, np.ndarray]:
+    """One layer's inputs and weights as numpy arrays (bf16 as uint16 bits)."""
+    rng = np.random.default_rng(seed)
+    T = shape.T if T is None else T
+    d, E, I, Is = shape.d, shape.E, shape.I, shape.I_shared
+
+    def codes(*s):
+        return rng.integers(0, 256, s, dtype=np.uint8)
+
+    def scales(*s):
+        return rng.integers(SCALE_LO, SCALE_HI + 1, s, dtype=np.uint8)
+
+    layer = {
+        "x": f32_to_bf16_bits(rng.standard_normal((T, d), dtype=np.float32)),
+        "router_weight": rng.normal(0.0, 0.02, (E, d)).astype(np.float32),
+        "router_bias": np.zeros(E, dtype=np.float32),
+        "gate_proj.weight_packed": codes(E, I, d // 2),
+        "gate_proj.weight_scale": scales(E, I, d // 32),
+        "up_proj.weight_packed": codes(E, I, d // 2),
+        "up_proj.weight_scale": scales(E, I, d // 32),
+        "down_proj.weight_packed": codes(E, d, I // 2),
+        "down_proj.weight_scale": scales(E, d, I // 32),
+        "shared.gate": f32_to_bf16_bits(rng.normal(0.0, 0.02, (Is, d)).astype(np.float32)),
+        "shared.up": f32_to_bf16_bits(rng.normal(0.0, 0.02, (Is, d)).astype(np.float32)),
+        "shared.down": f32_to_bf16_bits(rng.normal(0.0, 0.02, (d, Is)).astype(np.float32)),
+    }
+    if shape.routing == "zipf":
+        layer["router_bias"] = zipf_bias(E, rng)
+    return layer
+
+
+BANK_KEYS = ("gate_proj.weight_packed", "gate_proj.weight_scale", "up_proj.weight_packed",
+             "up_proj.weight_scale", "down_proj.weight_packed", "down_proj.weight_scale")

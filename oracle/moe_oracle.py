@@ -1,0 +1,486 @@
+"""CPU oracle for livglm's routed-MoE layer -- TEST INFRASTRUCTURE ONLY.
+
+This module restates, in numpy, the arithmetic of the reference's routed-MoE
+hot path so that the HIP kernels can be checked against it.  It is imported
+only by ``tests/``, by ``__graft_entry__.smoke()`` and by the ``cpu_baseline``
+leg of ``bench.py``, and only as the checker.  The product path
+(``src/glm53flash`` + ``livglm_amd``) never calls it and fails loudly when its
+HIP library is missing.
+
+Each function names the reference file:line it follows.  The reference runs on
+MLX (``mx.gather_qmm``, ``mx.quantized_matmul``, ``mx.quantize``), which is not
+available here, so the MLX-internal choices are stated explicitly:
+
+* f32 accumulation is modelled as an exact (float64) dot product rounded once
+  to f32 -- the kernels' own f32 summation order differs by a few f32 ulps;
+* every bf16 result is rounded to nearest-even from f32;
+* ``argsort`` is taken as stable ascending (ties rank the larger index last,
+  i.e. "better");
+* sigmoid is ``y = 1 / (1 + exp(|x|)); s = x < 0 ? y : 1 - y`` in f32;
+* the MX scale rule of ``mx.quantize`` is selectable (``MX_RULE_NEAREST`` /
+  ``MX_RULE_OCP``).
+
+Pinning status of each function (how a plausible mistake would be caught) is
+listed in ``PINNING`` at the bottom of this file and checked by
+``tests/test_oracle.py``.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+# ---------------------------------------------------------------------------
+# bf16 helpers
+# ---------------------------------------------------------------------------
+
+
+def f32_to_bf16_bits(values) -> np.ndarray:
+    """Round f32 to bf16 (nearest-even) and return the 16-bit patterns."""
+    a = np.ascontiguousarray(values, dtype=np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    quiet = (u >> 16) | 0x40
+    return np.where(nan, quiet, rounded).astype(np.uint16)
+
+
+def bf16_bits_to_f32(bits) -> np.ndarray:
+    b = np.ascontiguousarray(bits, dtype=np.uint16)
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_round(values) -> np.ndarray:
+    """f32 -> nearest-even bf16 -> f32."""
+    return bf16_bits_to_f32(f32_to_bf16_bits(values))
+
+
+# ---------------------------------------------------------------------------
+# Element and scale codecs
+# ---------------------------------------------------------------------------
+
+# OCP MX v1.0 E2M1 magnitudes for codes 0..7; bit 3 is the sign.
+E2M1_MAGNITUDES = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0)
+
+
+def e2m1_table() -> np.ndarray:
+    """All 16 E2M1 values, indexed by the 4-bit code."""
+    mags = np.array(E2M1_MAGNITUDES, dtype=np.float32)
+    return np.concatenate([mags, -mags]).astype(np.float32)
+
+
+def e4m3fn_table() -> np.ndarray:
+    """All 256 E4M3FN values, as ``fp8.py:13-30`` builds them (0x7F/0xFF NaN)."""
+    out = np.empty(256, dtype=np.float32)
+    for byte in range(256):
+        sign = -1.0 if byte & 0x80 else 1.0
+        exponent = (byte >> 3) & 0x0F
+        mantissa = byte & 0x07
+        if exponent == 0:
+            value = math.ldexp(mantissa / 8.0, -6)
+        elif exponent == 0x0F and mantissa == 0x07:
+            value = math.nan
+        else:
+            value = math.ldexp(1.0 + mantissa / 8.0, exponent - 7)
+        out[byte] = sign * value
+    return out
+
+
+def e8m0_to_f32(exponents) -> np.ndarray:
+    """E8M0 scale ``2**(e-127)``; 0xFF is NaN (OCP MX v1.0)."""
+    e = np.asarray(exponents, dtype=np.int64)
+    vals = np.ldexp(np.ones(e.shape, dtype=np.float64), e - 127)
+    vals = np.where(e == 255, np.nan, vals)
+    return vals.astype(np.float32)
+
+
+def unpack_e2m1_codes(packed) -> np.ndarray:
+    """Split packed bytes into 4-bit codes.
+
+    Byte ``b`` holds element ``2b`` in its low nibble and ``2b+1`` in its high
+    nibble; the reference views the bytes as little-endian u32 words, so eight
+    codes per word run low nibble first (``expert_source.py:210-214``).
+    """
+    p = np.asarray(packed, dtype=np.uint8)
+    codes = np.empty(p.shape[:-1] + (p.shape[-1] * 2,), dtype=np.uint8)
+    codes[..., 0::2] = p & 0x0F
+    codes[..., 1::2] = p >> 4
+    return codes
+
+
+def dequant_mxfp4(packed, scales) -> np.ndarray:
+    """MXFP4 group-32 dequantisation as ``gather_qmm(mode="mxfp4")`` reads it
+    (``expert_ssd.py:174-183``): ``E2M1[code] * 2**(scale-127)``, f32."""
+    codes = unpack_e2m1_codes(packed)
+    s = e8m0_to_f32(scales)
+    if codes.shape[-1] != s.shape[-1] * 32:
+        raise ValueError("MXFP4 codes and scales disagree on the group count")
+    vals = e2m1_table()[codes]
+    with np.errstate(over="ignore", invalid="ignore"):
+        return (vals * np.repeat(s, 32, axis=-1)).astype(np.float32)
+
+
+def dequant_mxfp8(codes, scales) -> np.ndarray:
+    """MXFP8 (E4M3FN elements, E8M0 group-32 scales) dequantisation as
+    ``quantized_matmul(mode="mxfp8")`` reads it (``layers.py:56-65``)."""
+    c = np.asarray(codes, dtype=np.uint8)
+    s = e8m0_to_f32(scales)
+    if c.shape[-1] != s.shape[-1] * 32:
+        raise ValueError("MXFP8 codes and scales disagree on the group count")
+    with np.errstate(over="ignore", invalid="ignore"):
+        return (e4m3fn_table()[c] * np.repeat(s, 32, axis=-1)).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# MX quantisation (the startup conversion of layers.py:72-99)
+# ---------------------------------------------------------------------------
+
+MX_RULE_NEAREST = 0  # e = round-to-nearest(log2(amax / elem_max))
+MX_RULE_OCP = 1  # e = floor(log2(amax)) - emax_elem (OCP MX v1.0 sec. 6.3)
+
+_SQRT2_F32_BITS = 0x3FB504F3  # largest f32 below sqrt(2)
+
+
+def mx_scale_exponent(amax: float, elem_max: float, emax_elem: int, rule: int) -> int:
+    """Unbiased shared exponent for one group, clamped to [-127, 127].
+
+    ``amax`` is an f32 group maximum.  For ``MX_RULE_NEAREST`` the f32 quotient
+    ``amax / elem_max`` is formed (correctly rounded) and its log2 rounded to
+    the nearest integer exactly (mantissa compared with sqrt(2)).  A zero group
+    gets exponent -127 (byte 0)."""
+    a = np.float32(amax)
+    if not np.isfinite(a):
+        return 128  # byte 255: NaN scale
+    if a == 0:
+        return -127
+    if rule == MX_RULE_NEAREST:
+        s = np.float32(a / np.float32(elem_max))
+        bits = int(np.array(s, dtype=np.float32).view(np.uint32))
+        biased = (bits >> 23) & 0xFF
+        mant = bits & 0x7FFFFF
+        if biased == 0:  # subnormal quotient: normalise
+            m, ex = math.frexp(float(s))  # s = m * 2**ex, m in [0.5, 1)
+            n = ex - 1
+            n += 1 if (2.0 * m) > math.sqrt(2.0) else 0
+        else:
+            n = biased - 127
+            n += 1 if (0x3F800000 | mant) > _SQRT2_F32_BITS else 0
+    elif rule == MX_RULE_OCP:
+        m, ex = math.frexp(float(a))
+        n = (ex - 1) - emax_elem
+    else:
+        raise ValueError(f"unknown MX scale rule {rule}")
+    return max(-127, min(127, n))
+
+
+def e4m3fn_encode(values) -> np.ndarray:
+    """f32 -> E4M3FN code, round-to-nearest-even, saturating at +-448."""
+    v = np.asarray(values, dtype=np.float32).astype(np.float64)
+    sign = np.signbit(v)
+    a = np.minimum(np.abs(v), 448.0)
+    out = np.zeros(v.shape, dtype=np.uint8)
+    # quantum: 2**-9 below 2**-6 (subnormal), else 2**(floor(log2 a) - 3)
+    with np.errstate(divide="ignore"):
+        ex = np.floor(np.log2(np.where(a > 0, a, 1.0)))
+    ex = np.maximum(ex, -6)
+    q = np.ldexp(1.0, (ex - 3).astype(np.int64))
+    r = a / q
+    n = np.floor(r)
+    frac = r - n
+    up = (frac > 0.5) | ((frac == 0.5) & (np.mod(n, 2) == 1))
+    n = n + up
+    mag = n * q  # exact representable magnitude (may carry into next binade)
+    table = e4m3fn_table()
+    finite_pos = table[:0x7F]  # codes 0x00..0x7E, ascending magnitudes
+    idx = np.searchsorted(finite_pos, mag)
+    idx = np.minimum(idx, 0x7E)
+    out = idx.astype(np.uint8)
+    out = np.where(sign & (mag > 0), out | 0x80, out)
+    out = np.where(sign & (mag == 0), np.uint8(0x80), out)
+    return out.astype(np.uint8)
+
+
+def e2m1_encode(values) -> np.ndarray:
+    """f32 -> E2M1 code, round-to-nearest-even, saturating at +-6."""
+    v = np.asarray(values, dtype=np.float32).astype(np.float64)
+    a = np.minimum(np.abs(v), 6.0)
+    mags = np.array(E2M1_MAGNITUDES)
+    # nearest magnitude with ties to the even code (codes 0,2,4,6 are even)
+    diff = np.abs(a[..., None] - mags)
+    best = np.argmin(diff, axis=-1)
+    dmin = np.take_along_axis(diff, best[..., None], axis=-1)[..., 0]
+    tie = np.sum(diff == dmin[..., None], axis=-1) > 1
+    # on a tie the two candidates are best and best+1; pick the even one
+    best = np.where(tie & (best % 2 == 1), best + 1, best)
+    code = best.astype(np.uint8)
+    return np.where(np.signbit(v) & (code > 0), code | 0x8, np.where(np.signbit(v), 0x8, code)).astype(np.uint8)
+
+
+def quantize_mx(w_bf16_bits, bits: int, rule: int = MX_RULE_NEAREST):
+    """Group-32 MX quantisation of a bf16 matrix (``layers.py:89-94``).
+
+    Returns ``(codes, scales)``: for bits=8 codes are E4M3FN bytes
+    ``[rows, K]``; for bits=4 codes are packed E2M1 bytes ``[rows, K/2]``.
+    Scales are E8M0 bytes ``[rows, K/32]``."""
+    w = bf16_bits_to_f32(w_bf16_bits)
+    if w.ndim != 2 or w.shape[1] % 32:
+        raise ValueError(f"group-32 quantisation needs [rows, K%32==0], got {w.shape}")
+    rows, K = w.shape
+    groups = w.reshape(rows, K // 32, 32)
+    amax = np.max(np.abs(groups), axis=-1)
+    elem_max, emax_elem = (448.0, 8) if bits == 8 else (6.0, 2)
+    exps = np.vectorize(lambda a: mx_scale_exponent(a, elem_max, emax_elem, rule), otypes=[np.int64])(amax)
+    scales = (exps + 127).astype(np.uint8)
+    inv = np.ldexp(np.ones_like(exps, dtype=np.float64), -exps)
+    scaled = (groups.astype(np.float64) * inv[..., None]).astype(np.float32)
+    if bits == 8:
+        codes = e4m3fn_encode(scaled).reshape(rows, K)
+    elif bits == 4:
+        c = e2m1_encode(scaled).reshape(rows, K)
+        codes = (c[:, 0::2] | (c[:, 1::2] << 4)).astype(np.uint8)
+    else:
+        raise ValueError(f"unsupported MX width {bits}")
+    return codes, scales
+
+
+# ---------------------------------------------------------------------------
+# Elementwise pieces
+# ---------------------------------------------------------------------------
+
+
+def sigmoid_f32(x) -> np.ndarray:
+    """f32 sigmoid, ``y = 1/(1+exp(|x|)); x<0 ? y : 1-y`` evaluated in f32
+    (the small tail is formed directly, so large negative inputs keep their
+    relative precision)."""
+    x = np.asarray(x, dtype=np.float32)
+    with np.errstate(over="ignore"):
+        y = (np.float32(1.0) / (np.float32(1.0) + np.exp(np.abs(x)))).astype(np.float32)
+    return np.where(x < 0, y, (np.float32(1.0) - y).astype(np.float32)).astype(np.float32)
+
+
+def limited_swiglu_bf16(gate, up, limit: float) -> np.ndarray:
+    """``limited_swiglu`` (``expert_ssd.py:103-107``) with bf16 intermediates.
+
+    ``gate = min(gate, L)``; ``up = clip(up, -L, L)``; ``silu(g) = g *
+    sigmoid(g)``; every op's result is rounded to bf16 (MLX evaluates each
+    elementwise op in its output dtype)."""
+    g = np.asarray(gate, dtype=np.float32)
+    u = np.asarray(up, dtype=np.float32)
+    if limit > 0:
+        L = bf16_round(np.float32(limit))
+        g = np.minimum(g, L)
+        u = np.clip(u, -L, L)
+    s = bf16_round(sigmoid_f32(g))
+    a = bf16_round(g * s)
+    return bf16_round(a * u)
+
+
+def _dot_f32(a, b) -> np.ndarray:
+    """Model of an f32-accumulated product: exact (f64) then one f32 rounding."""
+    return (np.asarray(a, dtype=np.float64) @ np.asarray(b, dtype=np.float64)).astype(np.float32)
+
+
+def linear_bf16(x, weight_f32) -> np.ndarray:
+    """``x @ W.T`` with bf16 output (``layers.py:67``, and the MX paths of
+    ``layers.py:56-65`` once W is dequantised)."""
+    return bf16_round(_dot_f32(x, np.asarray(weight_f32).T))
+
+
+# ---------------------------------------------------------------------------
+# Router (moe.py:36-63)
+# ---------------------------------------------------------------------------
+
+
+def router(x, weight, bias, *, top_k: int, n_group: int, topk_group: int,
+           norm_topk_prob: bool, routed_scaling_factor: float):
+    """``TopKRouter.__call__`` (``moe.py:36-63``).
+
+    Returns ``(logits f32 [T,E], weights f32 [T,k], indices u32 [T,k], choice
+    f32 [T,E])``.  Indices are ascending by choice score: the best expert is
+    the LAST column (``moe.py:33-34,58``)."""
+    rows = np.asarray(x, dtype=np.float32).reshape(-1, np.asarray(weight).shape[1])
+    W = np.asarray(weight, dtype=np.float32)
+    E = W.shape[0]
+    logits = _dot_f32(rows, W.T)
+    scores = sigmoid_f32(logits)
+    choice = (scores + np.asarray(bias, dtype=np.float32)).astype(np.float32)
+    T = rows.shape[0]
+    per_group = E // n_group
+    grouped = choice.reshape(T, n_group, per_group)
+    top2 = np.sort(grouped, axis=-1)[..., -2:]
+    group_scores = (top2[..., 0] + top2[..., 1]).astype(np.float32)
+    group_idx = np.argsort(group_scores, axis=-1, kind="stable")[..., -topk_group:]
+    group_mask = np.zeros(group_scores.shape, dtype=bool)
+    np.put_along_axis(group_mask, group_idx, True, axis=-1)
+    score_mask = np.broadcast_to(group_mask[..., None], grouped.shape).reshape(T, E)
+    masked = np.where(score_mask, choice, np.float32(-np.inf)).astype(np.float32)
+    indices = np.argsort(masked, axis=-1, kind="stable")[..., -top_k:]
+    weights = np.take_along_axis(scores, indices, axis=-1).astype(np.float32)
+    if norm_topk_prob:
+        total = np.zeros((T,), dtype=np.float32)
+        for j in range(top_k):
+            total = (total + weights[:, j]).astype(np.float32)
+        weights = (weights / (total + np.float32(1e-20))[:, None]).astype(np.float32)
+    weights = (weights * np.float32(routed_scaling_factor)).astype(np.float32)
+    return logits, weights, indices.astype(np.uint32), masked
+
+
+def topk_margin(choice_masked, k: int) -> np.ndarray:
+    """Smallest gap between adjacent values among the top k+1 choice scores of
+    each row (f64).  A tiny margin means the k-th/(k+1)-th selection or the
+    order inside the top-k can legitimately flip under a different f32
+    summation order; parity tests treat such rows as ambiguous."""
+    c = np.sort(np.asarray(choice_masked, dtype=np.float64), axis=-1)[..., ::-1]
+    c = c[..., : min(k + 1, c.shape[-1])]
+    gaps = c[..., :-1] - c[..., 1:]
+    gaps = np.where(np.isnan(gaps), np.inf, gaps)
+    return np.min(gaps, axis=-1)
+
+
+# ---------------------------------------------------------------------------
+# Dispatch (the build's histogram / prefix-sum / stable permute)
+# ---------------------------------------------------------------------------
+
+
+def dispatch(indices, num_experts: int):
+    """Counting sort of the row-major (t, j) pairs by expert id.
+
+    The reference materialises the same grouping on the host (first-occurrence
+    unique + compact remap, ``expert_ssd.py:159-169``;
+    ``native_expert_ssd.py:500-525``).  Returns ``counts[E]``,
+    ``offsets[E+1]``, ``perm[P]`` (sorted position -> pair ``t*k+j``, each
+    expert's pairs ascending) and ``inv[P]`` (pair -> sorted position)."""
+    flat = np.asarray(indices, dtype=np.int64).reshape(-1)
+    if flat.size and (flat.min() < 0 or flat.max() >= num_experts):
+        raise ValueError("routed expert ids are out of range")
+    counts = np.bincount(flat, minlength=num_experts).astype(np.int32)
+    offsets = np.zeros(num_experts + 1, dtype=np.int32)
+    offsets[1:] = np.cumsum(counts)
+    perm = np.argsort(flat, kind="stable").astype(np.int32)
+    inv = np.empty_like(perm)
+    inv[perm] = np.arange(perm.size, dtype=np.int32)
+    active = np.nonzero(counts)[0].astype(np.int32)
+    return counts, offsets, perm, inv, active
+
+
+# ---------------------------------------------------------------------------
+# Routed experts, shared expert, combine (expert_ssd.py:159-188, moe.py:123-201)
+# ---------------------------------------------------------------------------
+
+
+class Bank:
+    """Row-major MXFP4 expert bank in the reference's tensor layout
+    (``expert_source.py:189-229``): per expert ``gate/up.weight_packed``
+    ``[I, d/2]`` u8, ``gate/up.weight_scale`` ``[I, d/32]`` u8,
+    ``down.weight_packed`` ``[d, I/2]`` u8, ``down.weight_scale`` ``[d, I/32]``."""
+
+    def __init__(self, gate_w, gate_s, up_w, up_s, down_w, down_s):
+        self.gate_w, self.gate_s = np.asarray(gate_w), np.asarray(gate_s)
+        self.up_w, self.up_s = np.asarray(up_w), np.asarray(up_s)
+        self.down_w, self.down_s = np.asarray(down_w), np.asarray(down_s)
+
+    def projection(self, name: str, expert: int) -> np.ndarray:
+        w, s = {
+            "gate_proj": (self.gate_w, self.gate_s),
+            "up_proj": (self.up_w, self.up_s),
+            "down_proj": (self.down_w, self.down_s),
+        }[name]
+        return dequant_mxfp4(w[expert], s[expert])
+
+
+def routed_experts(x, indices, bank: Bank, swiglu_limit: float, *, return_intermediates=False):
+    """``ExpertSSD.__call__`` (``expert_ssd.py:159-188``): for every (t, j)
+    pair, ``down(limited_swiglu(gate(x_t), up(x_t)))`` with expert
+    ``indices[t, j]``; output ``[T, k, d]`` bf16 in route order."""
+    x = np.asarray(x, dtype=np.float32)
+    idx = np.asarray(indices, dtype=np.int64)
+    T, k = idx.shape
+    d = x.shape[1]
+    I = bank.gate_w.shape[1]
+    g = np.zeros((T, k, I), dtype=np.float32)
+    u = np.zeros((T, k, I), dtype=np.float32)
+    y = np.zeros((T, k, d), dtype=np.float32)
+    for e in np.unique(idx):
+        t_sel, j_sel = np.nonzero(idx == e)
+        xs = x[t_sel]
+        ge = linear_bf16(xs, bank.projection("gate_proj", e))
+        ue = linear_bf16(xs, bank.projection("up_proj", e))
+        g[t_sel, j_sel] = ge
+        u[t_sel, j_sel] = ue
+    h = limited_swiglu_bf16(g, u, swiglu_limit)
+    for e in np.unique(idx):
+        t_sel, j_sel = np.nonzero(idx == e)
+        y[t_sel, j_sel] = linear_bf16(h[t_sel, j_sel], bank.projection("down_proj", e))
+    if return_intermediates:
+        return y, {"gate": g, "up": u, "h": h}
+    return y
+
+
+def dense_mlp(x, gate_w, up_w, down_w, swiglu_limit: float) -> np.ndarray:
+    """``DenseMLP.__call__`` with bf16 weights (``layers.py:160-171``)."""
+    g = linear_bf16(x, gate_w)
+    u = linear_bf16(x, up_w)
+    return linear_bf16(limited_swiglu_bf16(g, u, swiglu_limit), down_w)
+
+
+def combine(route_outputs, weights, shared) -> np.ndarray:
+    """``sum(route_outputs * weights[..., None], axis=-2) + shared``
+    (``moe.py:198-201``): bf16 x f32 promotes to f32; sequential j order."""
+    y = np.asarray(route_outputs, dtype=np.float32)
+    w = np.asarray(weights, dtype=np.float32)
+    T, k, d = y.shape
+    out = np.zeros((T, d), dtype=np.float32)
+    for j in range(k):
+        out = (out + (y[:, j, :] * w[:, j, None]).astype(np.float32)).astype(np.float32)
+    if shared is not None:
+        out = (out + np.asarray(shared, dtype=np.float32)).astype(np.float32)
+    return out
+
+
+def moe_layer(x, router_weight, router_bias, bank: Bank, shared_weights, *, top_k, n_group,
+              topk_group, norm_topk_prob, routed_scaling_factor, swiglu_limit,
+              return_intermediates=False):
+    """``ExpertSSDMoE._call_impl`` (``moe.py:123-201``) on a bf16 ``[T, d]``
+    input: router -> routed experts -> shared expert -> weighted merge."""
+    logits, w, idx, masked = router(
+        x, router_weight, router_bias, top_k=top_k, n_group=n_group, topk_group=topk_group,
+        norm_topk_prob=norm_topk_prob, routed_scaling_factor=routed_scaling_factor)
+    y, inter = routed_experts(x, idx, bank, swiglu_limit, return_intermediates=True)
+    shared = None
+    if shared_weights is not None:
+        shared = dense_mlp(x, *shared_weights, swiglu_limit)
+    out = combine(y, w, shared)
+    if return_intermediates:
+        return out, {"logits": logits, "weights": w, "indices": idx, "choice": masked,
+                     "route_outputs": y, "shared": shared, **inter}
+    return out
+
+
+def rel_l2(actual, expected) -> float:
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected, dtype=np.float64)
+    return float(np.linalg.norm(a - e) / max(np.linalg.norm(e), 1e-30))
+
+
+# How each function is pinned (checked in tests/test_oracle.py).
+PINNING = {
+    "e2m1_table": "OCP MX v1.0 closed form; every code checked",
+    "unpack_e2m1_codes": "nibble order: MXFP4 round trip of N(0,s) weights gives cosine > 0.99 only "
+                         "with low-nibble-first (reports/preflight.json:22-155 scale)",
+    "e4m3fn_table": "reference KAT tests/test_fp8.py:31-35 + NaN codes test_fp8.py:55-59",
+    "e8m0_to_f32": "closed form 2**(e-127), all 256 bytes",
+    "dequant_mxfp4/8": "closed forms above; group broadcast checked on one-hot scales",
+    "mx_scale_exponent": "brute force against math.log2 on random and boundary values",
+    "e4m3fn_encode / e2m1_encode": "brute force nearest-even search over all codes",
+    "quantize_mx": "byte counts of tests/test_resident_mxfp8.py:19-20,43-44; error bounds "
+                   "rtol .03/.20 of the same tests",
+    "sigmoid_f32": "against exp in f64 (|err| <= 4 f32 ulp)",
+    "limited_swiglu_bf16": "closed form on hand-picked values incl. the clamp edges",
+    "router": "reference KAT tests/test_moe.py:10-23; brute-force sorted() on small cases",
+    "dispatch": "brute force (python sort) + invariants inv[perm]=id, per-expert ascending",
+    "routed_experts": "per-pair brute-force f64 products on dequantised weights; the [T,k,d] "
+                      "route order of tests/test_expert_ssd.py:49-63",
+    "combine": "closed form; sequential f32 order",
+    "dense_mlp / linear_bf16": "brute-force f64 products",
+}

@@ -1,0 +1,82 @@
+"""Helpers for the GPU parity tests: numpy <-> device tensors, C-ABI calls."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from livglm_amd import native
+from livglm_amd.workloads import BANK_KEYS
+
+
+def to_dev(a: np.ndarray) -> torch.Tensor:
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        t = torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)
+    elif a.dtype == np.uint32:
+        t = torch.from_numpy(a.view(np.int32))
+    else:
+        t = torch.from_numpy(a)
+    return t.to("cuda")
+
+
+def bf16_bits(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().numpy()
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+# Tensors whose pointers were handed out by p(): kept alive until the next
+# call() has synchronised, so temporaries such as p(to_dev(a)) cannot be
+# freed (and their memory reused) before the kernel reads them.
+_live: list[torch.Tensor] = []
+
+
+def call(name: str, *args) -> None:
+    try:
+        native.call(name, *args)
+        torch.cuda.synchronize()
+    finally:
+        _live.clear()
+
+
+def p(t: torch.Tensor | None):
+    if t is None:
+        return None
+    _live.append(t)
+    return t.data_ptr()
+
+
+def upload_layer(layer: dict[str, np.ndarray]) -> dict[str, torch.Tensor]:
+    return {k: to_dev(v) for k, v in layer.items()}
+
+
+def run_layer(dl: dict[str, torch.Tensor], shape, T: int | None = None, shared: bool = True,
+              bias: torch.Tensor | None = None):
+    """glm_moe_forward on uploaded layer tensors; returns (out, weights, indices)."""
+    T = dl["x"].shape[0] if T is None else T
+    d, E, k, I, Is = shape.d, shape.E, shape.k, shape.I, shape.I_shared
+    lib = native.load()
+    ws_bytes = lib.glm_moe_workspace_bytes(T, d, E, k, I, Is if shared else 0)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    out = torch.empty((T, d), dtype=torch.float32, device="cuda")
+    w = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    idx = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    b = dl["router_bias"] if bias is None else bias
+    args = [stream(), p(dl["x"]), T, d, p(dl["router_weight"]), p(b), E, k, shape.n_group,
+            shape.topk_group, int(shape.norm_topk_prob), shape.routed_scaling_factor, I]
+    args += [p(dl[key]) for key in BANK_KEYS]
+    if shared:
+        args += [Is, native.GLM_FMT_BF16, p(dl["shared.gate"]), None, p(dl["shared.up"]), None,
+                 p(dl["shared.down"]), None]
+    else:
+        args += [0, native.GLM_FMT_BF16, None, None, None, None, None, None]
+    args += [shape.swiglu_limit, p(ws), ws_bytes, p(out), p(w), p(idx)]
+    call("glm_moe_forward", *args)
+    return out, w, idx

@@ -1,0 +1,377 @@
+"""GPU parity of the HIP kernels (through the C ABI) against the CPU oracle.
+
+Integer and byte work (dequantised values, quantised codes, routing indices,
+permutation) must be bit-exact; bf16 layer outputs must be within rel-L2 2e-3
+of the oracle.  Router indices are compared exactly on every row whose top-k
+margin (f64, over the top k+1 choice scores) exceeds MARGIN; rows under it may
+legitimately flip under a different f32 summation order and are counted.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import moe_oracle as O
+from livglm_amd import native
+from livglm_amd.workloads import SHAPES, BANK_KEYS, MoEShape, make_layer
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 2e-3  # bf16 layer-output tolerance (north-star parity bar)
+MARGIN = 1e-5  # choice-score gap below which top-k order may flip
+
+
+def _torch():
+    import torch
+    return torch
+
+
+@pytest.fixture(scope="module")
+def gu():
+    import gpu_util
+    native.load()
+    return gpu_util
+
+
+def _bank(layer):
+    return O.Bank(*(layer[k] for k in BANK_KEYS))
+
+
+def _oracle_layer(layer, shape, shared=True):
+    x = O.bf16_bits_to_f32(layer["x"])
+    sw = None
+    if shared:
+        sw = tuple(O.bf16_bits_to_f32(layer[k]) for k in ("shared.gate", "shared.up", "shared.down"))
+    return O.moe_layer(x, layer["router_weight"], layer["router_bias"], _bank(layer), sw,
+                       top_k=shape.k, n_group=shape.n_group, topk_group=shape.topk_group,
+                       norm_topk_prob=shape.norm_topk_prob,
+                       routed_scaling_factor=shape.routed_scaling_factor,
+                       swiglu_limit=shape.swiglu_limit, return_intermediates=True)
+
+
+def _check_indices(got, want, choice, k):
+    margin = O.topk_margin(choice, k)
+    sure = margin > MARGIN
+    mism = np.any(got != want, axis=1)
+    assert not np.any(mism & sure), f"index mismatch on unambiguous rows {np.nonzero(mism & sure)[0][:10]}"
+    return int(np.sum(~sure))
+
+
+# --------------------------------------------------------------------------- codecs
+
+
+# Scale bytes whose decoded values stay inside bf16's range: the kernels
+# dequantise to bf16 in registers, which is exact for E2M1 when e >= 1 and for
+# E4M3FN when e >= 3.  Smaller scales (group scales of 2^-127..2^-125) flush
+# their subnormal tail and are outside the supported domain; real checkpoints
+# and the synthetic banks use e in [119, 127].
+MXFP4_SCALES = np.array([1, 2, 3, 64, 100, 119, 120, 123, 125, 126, 127, 130, 200, 253, 254, 255],
+                        np.uint8)
+MXFP8_SCALES = np.array([3, 4, 64, 100, 119, 121, 124, 127, 128, 140, 200, 253, 254, 255], np.uint8)
+
+
+def _dequant_case(gu, codes, scl, K, fmt):
+    torch = _torch()
+    R = len(scl)
+    scales = np.repeat(scl[:, None], K // 32, axis=1)
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = O.dequant_mxfp4(codes, scales) if fmt == native.GLM_FMT_MXFP4 \
+            else O.dequant_mxfp8(codes, scales)
+    out = torch.empty((R, K), dtype=torch.float32, device="cuda")
+    gu.call("glm_mx_dequantize", gu.stream(), gu.p(gu.to_dev(codes)), gu.p(gu.to_dev(scales)), R,
+            K, fmt, gu.p(out))
+    got = gu.host(out)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    np.testing.assert_array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_mxfp4_dequant_bit_exact(gu):
+    # every packed byte (all 16x16 code pairs) under every scale class
+    codes = np.tile(np.arange(256, dtype=np.uint8), (len(MXFP4_SCALES), 1))
+    _dequant_case(gu, codes, MXFP4_SCALES, 512, native.GLM_FMT_MXFP4)
+
+
+def test_mxfp8_dequant_bit_exact(gu):
+    codes = np.tile(np.arange(256, dtype=np.uint8), (len(MXFP8_SCALES), 1))
+    _dequant_case(gu, codes, MXFP8_SCALES, 256, native.GLM_FMT_MXFP8)
+
+
+def test_mxfp4_dequant_random_bank_bit_exact(gu):
+    rng = np.random.default_rng(5)
+    codes = rng.integers(0, 256, (64, 1024), dtype=np.uint8)
+    scl = rng.integers(119, 128, 64).astype(np.uint8)
+    _dequant_case(gu, codes, scl, 2048, native.GLM_FMT_MXFP4)
+
+
+def _quant_inputs():
+    rng = np.random.default_rng(77)
+    a = rng.normal(0, 0.02, (64, 256)).astype(np.float32)
+    a[0, :32] = 0.0  # all-zero group
+    a[1, :32] = rng.normal(0, 1e-30, 32)  # tiny
+    a[2, :32] = rng.normal(0, 1e4, 32)  # large
+    a[3] = np.linspace(-3, 3, 256)  # ties and boundaries
+    a[4, :32] = -0.0
+    return O.f32_to_bf16_bits(a)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("rule", [O.MX_RULE_NEAREST, O.MX_RULE_OCP])
+def test_mx_quantize_bit_exact(gu, bits, rule):
+    torch = _torch()
+    w = _quant_inputs()
+    rows, cols = w.shape
+    want_codes, want_scales = O.quantize_mx(w, bits, rule)
+    codes = torch.empty(want_codes.shape, dtype=torch.uint8, device="cuda")
+    scales = torch.empty(want_scales.shape, dtype=torch.uint8, device="cuda")
+    fmt = native.GLM_FMT_MXFP8 if bits == 8 else native.GLM_FMT_MXFP4
+    gu.call("glm_mx_quantize", gu.stream(), gu.p(gu.to_dev(w)), rows, cols, fmt, rule, gu.p(codes),
+            gu.p(scales))
+    np.testing.assert_array_equal(gu.host(scales), want_scales)
+    np.testing.assert_array_equal(gu.host(codes), want_codes)
+
+
+# --------------------------------------------------------------------------- router / dispatch
+
+
+def _router_case(shape, seed, T=None, n_group=1, topk_group=1):
+    layer = make_layer(shape, seed, T=T)
+    return layer, MoEShape(shape.name, layer["x"].shape[0], shape.d, shape.E, shape.k, shape.I,
+                           shape.I_shared, shape.routing, n_group, topk_group)
+
+
+@pytest.mark.parametrize("name,T,groups", [
+    ("decode_t1", None, (1, 1)),
+    ("verify_t2", None, (1, 1)),
+    ("batch_t64", None, (1, 1)),
+    ("verify_t2", 300, (8, 4)),
+    ("prefill_t4096", 1024, (1, 1)),
+])
+def test_router_parity(gu, name, T, groups):
+    torch = _torch()
+    shape, seed = SHAPES[name], 5300 + list(SHAPES).index(name)
+    layer, sh = _router_case(shape, seed, T, *groups)
+    T = sh.T
+    x = O.bf16_bits_to_f32(layer["x"])
+    logits, w, idx, choice = O.router(x, layer["router_weight"], layer["router_bias"], top_k=sh.k,
+                                      n_group=sh.n_group, topk_group=sh.topk_group,
+                                      norm_topk_prob=True, routed_scaling_factor=2.5)
+    dl = gu.upload_layer({k: layer[k] for k in ("x", "router_weight", "router_bias")})
+    g_logits = torch.empty((T, sh.E), dtype=torch.float32, device="cuda")
+    g_w = torch.empty((T, sh.k), dtype=torch.float32, device="cuda")
+    g_idx = torch.empty((T, sh.k), dtype=torch.int32, device="cuda")
+    gu.call("glm_router_topk", gu.stream(), gu.p(dl["x"]), T, sh.d, gu.p(dl["router_weight"]),
+            gu.p(dl["router_bias"]), sh.E, sh.k, sh.n_group, sh.topk_group, 1, 2.5, gu.p(g_logits),
+            gu.p(g_w), gu.p(g_idx))
+    np.testing.assert_allclose(gu.host(g_logits), logits, rtol=1e-4, atol=1e-5)
+    got_idx = gu.host(g_idx).astype(np.uint32)
+    ambiguous = _check_indices(got_idx, idx, choice, sh.k)
+    assert ambiguous <= max(1, T // 100)
+    same = np.all(got_idx == idx, axis=1)
+    np.testing.assert_allclose(gu.host(g_w)[same], w[same], rtol=2e-6, atol=1e-7)
+
+
+def test_router_reference_known_answer(gu):
+    # reference tests/test_moe.py:10-23 through the kernel
+    torch = _torch()
+    x = np.zeros((1, 32), np.uint16)
+    W = np.zeros((4, 32), np.float32)
+    bias = np.array([10.0, 9.0, 1.0, 0.0], np.float32)
+    lg = torch.empty((1, 4), dtype=torch.float32, device="cuda")
+    w = torch.empty((1, 2), dtype=torch.float32, device="cuda")
+    idx = torch.empty((1, 2), dtype=torch.int32, device="cuda")
+    gu.call("glm_router_topk", gu.stream(), gu.p(gu.to_dev(x)), 1, 32, gu.p(gu.to_dev(W)),
+            gu.p(gu.to_dev(bias)), 4, 2, 2, 1, 1, 2.5, gu.p(lg), gu.p(w), gu.p(idx))
+    assert gu.host(idx).tolist() == [[1, 0]]
+    np.testing.assert_allclose(gu.host(w), [[1.25, 1.25]], atol=1e-6)
+
+
+def _dispatch(gu, idx, E):
+    torch = _torch()
+    T, k = idx.shape
+    P = T * k
+    i32 = dict(dtype=torch.int32, device="cuda")
+    bufs = {n: torch.full((s,), -7, **i32) for n, s in
+            [("counts", E), ("offsets", E + 1), ("perm", P), ("inv", P), ("pair_token", P),
+             ("active", E), ("num_active", 1), ("status", 1)]}
+    gu.call("glm_moe_dispatch", gu.stream(), gu.p(gu.to_dev(idx.astype(np.uint32))), T, k, E,
+            *(gu.p(bufs[n]) for n in ("counts", "offsets", "perm", "inv", "pair_token", "active",
+                                      "num_active", "status")))
+    return {n: gu.host(t) for n, t in bufs.items()}
+
+
+@pytest.mark.parametrize("T,k,E,kind", [
+    (1, 2, 16, "distinct"), (2, 8, 128, "distinct"), (64, 8, 128, "skew"),
+    (4096, 8, 128, "distinct"), (3000, 8, 288, "skew"), (5, 4, 8, "dups"), (1, 1, 1, "distinct"),
+])
+def test_dispatch_bit_exact(gu, T, k, E, kind):
+    rng = np.random.default_rng(T * 31 + k + E)
+    if kind == "distinct":
+        idx = np.stack([rng.choice(E, k, replace=False) for _ in range(T)])
+    elif kind == "skew":
+        p = 1.0 / np.arange(1, E + 1) ** 1.1
+        idx = np.stack([rng.choice(E, k, replace=False, p=p / p.sum()) for _ in range(T)])
+    else:
+        idx = rng.integers(0, E, (T, k))
+    got = _dispatch(gu, idx, E)
+    counts, offsets, perm, inv, active = O.dispatch(idx, E)
+    np.testing.assert_array_equal(got["counts"], counts)
+    np.testing.assert_array_equal(got["offsets"], offsets)
+    np.testing.assert_array_equal(got["perm"], perm)
+    np.testing.assert_array_equal(got["inv"], inv)
+    np.testing.assert_array_equal(got["pair_token"], perm // k)
+    assert got["num_active"][0] == len(active)
+    np.testing.assert_array_equal(got["active"][: len(active)], active)
+    assert np.all(got["active"][len(active):] == -1)
+    assert got["status"][0] == 0
+
+
+def test_dispatch_flags_out_of_range(gu):
+    idx = np.array([[0, 5], [3, 1]])
+    got = _dispatch(gu, idx, 4)
+    assert got["status"][0] == 1
+    assert got["inv"][1] == -1
+    assert got["offsets"][-1] == 3
+
+
+# --------------------------------------------------------------------------- experts
+
+
+def _expert_parity(gu, shape, seed, T=None):
+    torch = _torch()
+    layer = make_layer(shape, seed, T=T)
+    T = layer["x"].shape[0]
+    k, E, d, I = shape.k, shape.E, shape.d, shape.I
+    x = O.bf16_bits_to_f32(layer["x"])
+    _, _, idx, _ = O.router(x, layer["router_weight"], layer["router_bias"], top_k=k, n_group=1,
+                            topk_group=1, norm_topk_prob=True, routed_scaling_factor=2.5)
+    y_want, inter = O.routed_experts(x, idx, _bank(layer), shape.swiglu_limit,
+                                     return_intermediates=True)
+    counts, offsets, perm, inv, active = O.dispatch(idx, E)
+    dl = gu.upload_layer({key: layer[key] for key in ("x",) + BANK_KEYS})
+    P = T * k
+    i32 = dict(dtype=torch.int32, device="cuda")
+    d_off = gu.to_dev(offsets)
+    d_tok = gu.to_dev((perm // k).astype(np.int32))
+    d_act = gu.to_dev(np.concatenate([active, -np.ones(E - len(active), np.int32)]).astype(np.int32))
+    d_na = gu.to_dev(np.array([len(active)], np.int32))
+    h = torch.empty((P, I), dtype=torch.bfloat16, device="cuda")
+    y = torch.empty((P, d), dtype=torch.bfloat16, device="cuda")
+    gu.call("glm_expert_gate_up", gu.stream(), gu.p(dl["x"]), T, d, I, E, k,
+            *(gu.p(dl[key]) for key in BANK_KEYS[:4]), gu.p(d_off), gu.p(d_tok), gu.p(d_act),
+            gu.p(d_na), shape.swiglu_limit, gu.p(h))
+    gu.call("glm_expert_down", gu.stream(), gu.p(h), T, k, I, d, E, gu.p(dl[BANK_KEYS[4]]),
+            gu.p(dl[BANK_KEYS[5]]), gu.p(d_off), gu.p(d_act), gu.p(d_na), gu.p(y))
+    h_got = O.bf16_bits_to_f32(gu.bf16_bits(h))[inv].reshape(T, k, I)
+    y_got = O.bf16_bits_to_f32(gu.bf16_bits(y))[inv].reshape(T, k, d)
+    return h_got, inter["h"], y_got, y_want
+
+
+@pytest.mark.parametrize("name,T", [("decode_t1", None), ("verify_t2", None), ("batch_t64", None),
+                                    ("verify_t2", 40)])
+def test_routed_experts_parity(gu, name, T):
+    shape = SHAPES[name]
+    h_got, h_want, y_got, y_want = _expert_parity(gu, shape, 900 + len(name), T)
+    assert O.rel_l2(h_got, h_want) < REL_L2
+    assert O.rel_l2(y_got, y_want) < REL_L2
+    # bf16 results differ from the oracle only by summation order: nearly all bit-exact
+    assert np.mean(h_got == h_want) > 0.97
+    assert np.mean(y_got == y_want) > 0.97
+
+
+def test_routed_experts_generic_shapes(gu):
+    # tiny geometry of the reference's tests (tests/helpers.py: d=32, I=32) and
+    # one more that is not a multiple of the 128-wide MFMA chunk
+    for d, I, E, k, T in [(32, 32, 4, 2, 3), (96, 64, 5, 3, 7)]:
+        shape = MoEShape("tiny", T=T, d=d, E=E, k=k, I=I, I_shared=32)
+        h_got, h_want, y_got, y_want = _expert_parity(gu, shape, 11 + d, T)
+        assert O.rel_l2(y_got, y_want) < REL_L2
+        assert np.mean(y_got == y_want) > 0.95
+
+
+def test_combine_bit_exact(gu):
+    torch = _torch()
+    rng = np.random.default_rng(3)
+    T, k, d = 5, 4, 256
+    y = O.f32_to_bf16_bits(rng.normal(0, 1, (T * k, d)).astype(np.float32))
+    w = rng.uniform(0, 1, (T, k)).astype(np.float32)
+    shared = O.f32_to_bf16_bits(rng.normal(0, 1, (T, d)).astype(np.float32))
+    inv = rng.permutation(T * k).astype(np.int32)
+    want = O.combine(O.bf16_bits_to_f32(y)[inv].reshape(T, k, d), w, O.bf16_bits_to_f32(shared))
+    out = torch.empty((T, d), dtype=torch.float32, device="cuda")
+    gu.call("glm_moe_combine", gu.stream(), gu.p(gu.to_dev(y)), gu.p(gu.to_dev(inv)),
+            gu.p(gu.to_dev(w)), gu.p(gu.to_dev(shared)), T, k, d, gu.p(out))
+    np.testing.assert_array_equal(gu.host(out).view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", [native.GLM_FMT_BF16, native.GLM_FMT_MXFP8])
+def test_dense_mlp_parity(gu, fmt):
+    torch = _torch()
+    rng = np.random.default_rng(21)
+    T, d, I = 3, 2048, 768
+    ws = [O.f32_to_bf16_bits(rng.normal(0, 0.02, s).astype(np.float32)) for s in [(I, d), (I, d), (d, I)]]
+    x = O.f32_to_bf16_bits(rng.normal(0, 1, (T, d)).astype(np.float32))
+    if fmt == native.GLM_FMT_BF16:
+        mats = [O.bf16_bits_to_f32(w) for w in ws]
+        dev = [(gu.to_dev(w), None) for w in ws]
+    else:
+        q = [O.quantize_mx(w, 8, O.MX_RULE_NEAREST) for w in ws]
+        mats = [O.dequant_mxfp8(c, s) for c, s in q]
+        dev = [(gu.to_dev(c), gu.to_dev(s)) for c, s in q]
+    want = O.dense_mlp(O.bf16_bits_to_f32(x), *mats, 10.0)
+    h = torch.empty((T, I), dtype=torch.bfloat16, device="cuda")
+    out = torch.empty((T, d), dtype=torch.bfloat16, device="cuda")
+    gu.call("glm_dense_mlp", gu.stream(), gu.p(gu.to_dev(x)), T, d, I, fmt,
+            gu.p(dev[0][0]), gu.p(dev[0][1]), gu.p(dev[1][0]), gu.p(dev[1][1]), gu.p(dev[2][0]),
+            gu.p(dev[2][1]), 10.0, gu.p(h), gu.p(out))
+    got = O.bf16_bits_to_f32(gu.bf16_bits(out))
+    assert O.rel_l2(got, want) < REL_L2
+    assert np.mean(got == want) > 0.97
+
+
+# --------------------------------------------------------------------------- whole layer
+
+
+@pytest.mark.parametrize("name", ["decode_t1", "verify_t2", "batch_t64"])
+def test_moe_layer_parity(gu, name):
+    shape = SHAPES[name]
+    layer = make_layer(shape, 5300 + list(SHAPES).index(name))
+    want, inter = _oracle_layer(layer, shape)
+    out, w, idx = gu.run_layer(gu.upload_layer(layer), shape)
+    got_idx = gu.host(idx).astype(np.uint32)
+    _check_indices(got_idx, inter["indices"], inter["choice"], shape.k)
+    assert np.array_equal(got_idx, inter["indices"]), "standard seeds have no near-ties"
+    np.testing.assert_allclose(gu.host(w), inter["weights"], rtol=2e-6, atol=1e-7)
+    assert O.rel_l2(gu.host(out), want) < REL_L2
+
+
+def test_moe_layer_prefill_sampled(gu):
+    shape = SHAPES["prefill_t4096"]
+    layer = make_layer(shape, 5303)
+    out, w, idx = gu.run_layer(gu.upload_layer(layer), shape)
+    x = O.bf16_bits_to_f32(layer["x"])
+    _, w_want, idx_want, choice = O.router(x, layer["router_weight"], layer["router_bias"],
+                                           top_k=shape.k, n_group=1, topk_group=1,
+                                           norm_topk_prob=True, routed_scaling_factor=2.5)
+    got_idx = gu.host(idx).astype(np.uint32)
+    amb = _check_indices(got_idx, idx_want, choice, shape.k)
+    assert amb <= 41
+    # every token routed once per slot: counts sum to T*k (size-independent check)
+    assert np.bincount(got_idx.reshape(-1), minlength=shape.E).sum() == shape.T * shape.k
+    rng = np.random.default_rng(0)
+    sample = rng.choice(shape.T, 24, replace=False)
+    sub = dict(layer)
+    sub["x"] = layer["x"][sample]
+    want, _ = _oracle_layer(sub, MoEShape("s", 24, shape.d, shape.E, shape.k, shape.I,
+                                          shape.I_shared))
+    same = np.all(got_idx[sample] == idx_want[sample], axis=1)
+    assert O.rel_l2(gu.host(out)[sample][same], want[same]) < REL_L2
+
+
+def test_moe_layer_deterministic(gu):
+    shape = SHAPES["batch_t64"]
+    dl = gu.upload_layer(make_layer(shape, 42))
+    a, _, _ = gu.run_layer(dl, shape)
+    b, _, _ = gu.run_layer(dl, shape)
+    assert np.array_equal(gu.host(a).view(np.uint32), gu.host(b).view(np.uint32))

@@ -1,0 +1,98 @@
+"""CPU-side checks of the C ABI: the library loads, exports every symbol the
+header declares with the expected version, and rejects bad arguments on the
+host before touching a GPU (no compute calls here)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from livglm_amd import native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "glm53_moe.h")
+
+
+def declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(glm_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(native.LIB_PATH):
+        pytest.fail("libglm53moe.so is not built; run `python -m livglm_amd.build`")
+    return native.load()
+
+
+def test_header_and_binding_agree():
+    assert set(declared_functions()) == set(native.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", native.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\b(glm_[a-z0-9_]+)\b", out))
+    missing = set(declared_functions()) - exported
+    assert not missing, missing
+
+
+def test_abi_version(lib):
+    assert lib.glm_abi_version() == native.ABI_VERSION == 1
+
+
+def test_workspace_size_is_host_only_and_monotone(lib):
+    small = lib.glm_moe_workspace_bytes(2, 2048, 128, 8, 768, 768)
+    big = lib.glm_moe_workspace_bytes(4096, 2048, 128, 8, 768, 768)
+    assert 0 < small < big
+    assert small % 256 == 0
+    assert lib.glm_moe_workspace_bytes(-1, 2048, 128, 8, 768, 768) == 0
+
+
+def _expect(code, name, *args):
+    rc = getattr(native.load(), name)(*args)
+    assert rc == code, (name, rc, native.load().glm_last_error())
+    return native.load().glm_last_error().decode()
+
+
+def test_null_pointers_are_rejected_on_host(lib):
+    msg = _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_router_topk", None, None, 1, 32, None,
+                  None, 4, 2, 1, 1, 1, 2.5, None, None, None)
+    assert "null" in msg
+    _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_moe_dispatch", None, None, 1, 2, 4, None, None,
+            None, None, None, None, None, None)
+    _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_moe_combine", None, None, None, None, None, 1,
+            2, 32, None)
+    _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_limited_swiglu", None, None, None, 4, 10.0,
+            None)
+
+
+def test_unsupported_shapes_are_rejected_on_host(lib):
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_mx_quantize", None, fake, 4, 48,
+            native.GLM_FMT_MXFP8, 0, fake, fake)
+    _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_mx_quantize", None, fake, 4, 64, 7, 0, fake,
+            fake)
+    _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_mx_quantize", None, fake, 4, 64,
+            native.GLM_FMT_MXFP8, 9, fake, fake)
+    _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_moe_dispatch", None, fake, 1, 2, 4096, fake,
+            fake, fake, fake, fake, fake, fake, fake)
+    msg = _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_router_topk", None, fake, 1, 32, fake,
+                  fake, 6, 2, 4, 1, 1, 2.5, fake, fake, fake)
+    assert "n_group" in msg
+    _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_linear", None, fake, 1, 40, fake, None,
+            native.GLM_FMT_BF16, 16, fake)
+
+
+def test_moe_forward_rejects_small_workspace(lib):
+    fake = ctypes.c_void_p(0x1000)
+    args = [None, fake, 2, 2048, fake, fake, 128, 8, 1, 1, 1, 2.5, 768] + [fake] * 6
+    args += [768, native.GLM_FMT_BF16, fake, None, fake, None, fake, None, 10.0, fake, 1024,
+             fake, None, None]
+    msg = _expect(native.GLM_ERR_WORKSPACE, "glm_moe_forward", *args)
+    assert "workspace" in msg
