@@ -77,13 +77,15 @@ int glm_router_topk(void *stream, const uint16_t *x, int T, int d, const float *
  * counts [E]; offsets [E+1] (exclusive scan of counts); perm [P] (sorted
  * position -> pair t*k+j, each expert's pairs ascending); inv [P] (pair ->
  * sorted position); pair_token [P] (sorted position -> token t); active [E]
- * (ids of experts with count > 0, ascending); num_active [1]; status [1]
- * (0, or 1 if an index >= E was seen -- such pairs are dropped, inv = -1).
+ * (ids of experts with count > 0, ascending, then -1); num_active [1];
+ * work [E][4] (per active slot u: {expert, offsets[expert], count, 0}; slots
+ * u >= num_active hold {-1, 0, 0, 0}); status [1] (0, or 1 if an index >= E
+ * was seen -- such pairs are dropped, inv = -1).
  * Limits: E <= 448 (one workgroup's LDS holds the per-expert bitmaps).
  */
 int glm_moe_dispatch(void *stream, const uint32_t *indices, int T, int top_k, int E,
                      int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
-                     int32_t *pair_token, int32_t *active, int32_t *num_active,
+                     int32_t *pair_token, int32_t *active, int32_t *num_active, int32_t *work,
                      int32_t *status);
 
 /*
@@ -91,14 +93,14 @@ int glm_moe_dispatch(void *stream, const uint32_t *indices, int T, int top_k, in
  * mx._expert_ssd_mxfp4_pair_qmv + limited_swiglu (native_expert_ssd.py:696-706,
  * expert_ssd.py:103-107), and gather_qmm for T > 1 (native_expert_ssd.py:726-741).
  * x bf16 [T][d]; h bf16 [T*k][I] in SORTED (dispatch) order:
- * h[pos] = swiglu(bf16(x[pair_token[pos]] . Wg[e]^T), bf16(x . Wu[e]^T)).
+ * h[pos] = swiglu(bf16(x[pair_token[pos]] . Wg[e]^T), bf16(x . Wu[e]^T)) for
+ * the rows pos of each work slot (glm_moe_dispatch).
  * Limits: d % 32 == 0, I % 16 == 0.
  */
 int glm_expert_gate_up(void *stream, const uint16_t *x, int T, int d, int I, int E, int top_k,
                        const uint8_t *gate_packed, const uint8_t *gate_scales,
                        const uint8_t *up_packed, const uint8_t *up_scales,
-                       const int32_t *offsets, const int32_t *pair_token,
-                       const int32_t *active, const int32_t *num_active, float swiglu_limit,
+                       const int32_t *pair_token, const int32_t *work, float swiglu_limit,
                        uint16_t *h);
 
 /*
@@ -108,8 +110,7 @@ int glm_expert_gate_up(void *stream, const uint16_t *x, int T, int d, int I, int
  * Limits: I % 32 == 0, d % 16 == 0.
  */
 int glm_expert_down(void *stream, const uint16_t *h, int T, int top_k, int I, int d, int E,
-                    const uint8_t *down_packed, const uint8_t *down_scales,
-                    const int32_t *offsets, const int32_t *active, const int32_t *num_active,
+                    const uint8_t *down_packed, const uint8_t *down_scales, const int32_t *work,
                     uint16_t *y);
 
 /*
@@ -169,10 +170,23 @@ int glm_limited_swiglu(void *stream, const uint16_t *gate, const uint16_t *up, i
 size_t glm_moe_workspace_bytes(int T, int d, int E, int top_k, int I, int I_shared);
 
 /*
+ * Zero-fills a workspace with a plain kernel (no memset node, so it may be
+ * captured in a graph).  glm_moe_forward does not need it; it is provided so
+ * callers can give a workspace a defined initial state.  Calls that overlap
+ * on one workspace race.
+ */
+int glm_moe_workspace_init(void *stream, void *workspace, size_t workspace_bytes);
+
+/*
  * One whole routed-MoE layer on a bf16 [T][d] input.  Replaces
  * ExpertSSDMoE.__call__ / _call_impl (moe.py:96-201) with an HBM-resident
  * expert bank: router -> dispatch -> gate/up+SwiGLU -> down -> shared expert
- * -> weighted combine, all on `stream` with no host synchronisation.
+ * -> weighted combine, all on `stream` with no host synchronisation.  For
+ * decode sizes (T*k <= 512) it is five kernels: router logits, selection +
+ * dispatch, routed (+ bf16 shared) gate/up, routed (+ shared) down, combine.
+ * shared_in (may be NULL): the shared expert's bf16 output [T][d] computed by
+ * the caller -- e.g. with glm_dense_mlp on a second stream, overlapping the
+ * routing -- in which case the shared weights are not read.
  * out f32 [T][d].  Optional outputs (may be NULL): weights f32 [T][k],
  * indices u32 [T][k].  The shared expert is skipped when shared_gate is NULL.
  * Shared-expert weights use `shared_fmt` (GLM_FMT_BF16: scale pointers NULL;
@@ -189,8 +203,9 @@ int glm_moe_forward(void *stream, const uint16_t *x, int T, int d, const float *
                     int shared_fmt, const void *shared_gate, const uint8_t *shared_gate_scales,
                     const void *shared_up, const uint8_t *shared_up_scales,
                     const void *shared_down, const uint8_t *shared_down_scales,
-                    float swiglu_limit, void *workspace, size_t workspace_bytes, float *out,
-                    float *weights_out, uint32_t *indices_out);
+                    const uint16_t *shared_in, float swiglu_limit, void *workspace,
+                    size_t workspace_bytes, float *out, float *weights_out,
+                    uint32_t *indices_out);
 
 #ifdef __cplusplus
 }

@@ -47,7 +47,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     const uint32_t *__restrict__ idx, int P, int k, int E, int32_t *__restrict__ counts,
     int32_t *__restrict__ offsets, int32_t *__restrict__ perm, int32_t *__restrict__ inv,
     int32_t *__restrict__ pair_token, int32_t *__restrict__ active,
-    int32_t *__restrict__ num_active, int32_t *__restrict__ status) {
+    int32_t *__restrict__ num_active, int4 *__restrict__ work, int32_t *__restrict__ status) {
   extern __shared__ uint32_t smem[];
   uint32_t *cnt = smem;
   uint32_t *off = cnt + E;
@@ -83,7 +83,10 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
       off[e] = carry + ex;
       offsets[e] = carry + ex;
       counts[e] = c;
-      if (c > 0) active[carry_active + ex_a] = e;
+      if (c > 0) {
+        active[carry_active + ex_a] = e;
+        work[carry_active + ex_a] = make_int4(e, carry + ex, c, 0);
+      }
     }
     carry += tot;
     carry_active += tot_a;
@@ -93,7 +96,10 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     num_active[0] = carry_active;
     status[0] = s_bad;
   }
-  for (int e = carry_active + tid; e < E; e += kDispatchThreads) active[e] = -1;
+  for (int e = carry_active + tid; e < E; e += kDispatchThreads) {
+    active[e] = -1;
+    work[e] = make_int4(-1, 0, 0, 0);
+  }
   __syncthreads();
 
   // Stable ranks, one 1024-pair chunk at a time: rank(p) = run[e] + number
@@ -139,12 +145,12 @@ size_t glm_dispatch_lds_bytes(int E) { return (size_t)E * (3 + 32) * sizeof(uint
 
 int glm_dispatch_launch(hipStream_t stream, const uint32_t *indices, int T, int k, int E,
                         int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
-                        int32_t *pair_token, int32_t *active, int32_t *num_active,
+                        int32_t *pair_token, int32_t *active, int32_t *num_active, int4 *work,
                         int32_t *status) {
   const int P = T * k;
   hipLaunchKernelGGL(glm::dispatch_kernel, dim3(1), dim3(glm::kDispatchThreads),
                      glm_dispatch_lds_bytes(E), stream, indices, P, k, E, counts, offsets, perm,
-                     inv, pair_token, active, num_active, status);
+                     inv, pair_token, active, num_active, work, status);
   GLM_LAUNCH_CHECK("dispatch_kernel");
   return GLM_OK;
 }
@@ -152,16 +158,18 @@ int glm_dispatch_launch(hipStream_t stream, const uint32_t *indices, int T, int 
 extern "C" int glm_moe_dispatch(void *stream, const uint32_t *indices, int T, int top_k, int E,
                                 int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
                                 int32_t *pair_token, int32_t *active, int32_t *num_active,
-                                int32_t *status) {
+                                int32_t *work, int32_t *status) {
   glm::clear_error();
   GLM_REQUIRE(indices && counts && offsets && perm && inv && pair_token && active &&
-                  num_active && status,
+                  num_active && work && status,
               GLM_ERR_INVALID_ARGUMENT, "dispatch: null pointer argument");
   GLM_REQUIRE(T >= 0 && top_k >= 1 && E >= 1, GLM_ERR_INVALID_ARGUMENT,
               "dispatch: invalid sizes T=%d k=%d E=%d", T, top_k, E);
   GLM_REQUIRE(E <= 448, GLM_ERR_UNSUPPORTED_SHAPE, "dispatch: E=%d exceeds 448", E);
   GLM_REQUIRE((long long)T * top_k < (1LL << 30), GLM_ERR_UNSUPPORTED_SHAPE,
               "dispatch: too many pairs");
+  GLM_REQUIRE(glm_aligned16({work}), GLM_ERR_INVALID_ARGUMENT,
+              "dispatch: work must be 16-byte aligned");
   return glm_dispatch_launch((hipStream_t)stream, indices, T, top_k, E, counts, offsets, perm,
-                             inv, pair_token, active, num_active, status);
+                             inv, pair_token, active, num_active, (int4 *)work, status);
 }

@@ -5,7 +5,10 @@ namespace glm {
 
 // out[t][c] = sum_j f32(y[inv[t*k+j]][c]) * w[t*k+j] + f32(shared[t][c])
 // in the order of moe.py:198-201 (sequential j, then the shared add).
-// Each thread owns 4 consecutive columns (8-byte loads of bf16).
+// Each thread owns 4 consecutive columns (8-byte loads of bf16).  For k <= KMAX
+// the row positions and weights are loaded first, then every y row at once, so
+// the kernel pays two memory latencies instead of 2k.
+template <int KMAX>
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict__ y,
                                                       const int32_t *__restrict__ inv,
                                                       const float *__restrict__ w,
@@ -17,15 +20,37 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict
   const int c = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (c >= d) return;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < k; ++j) {
-    const int pos = inv[(long long)t * k + j];
-    if (pos < 0) continue;
-    const float wj = w[(long long)t * k + j];
-    const uint2 v = *reinterpret_cast<const uint2 *>(y + (long long)pos * d + c);
-    acc[0] = acc[0] + bf16_to_f32(v.x & 0xffffu) * wj;
-    acc[1] = acc[1] + bf16_to_f32(v.x >> 16) * wj;
-    acc[2] = acc[2] + bf16_to_f32(v.y & 0xffffu) * wj;
-    acc[3] = acc[3] + bf16_to_f32(v.y >> 16) * wj;
+  if (KMAX > 0 && k <= KMAX) {
+    int pos[KMAX > 0 ? KMAX : 1];
+    float wj[KMAX > 0 ? KMAX : 1];
+    uint2 v[KMAX > 0 ? KMAX : 1];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      pos[j] = j < k ? inv[(long long)t * k + j] : -1;
+      wj[j] = j < k ? w[(long long)t * k + j] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j)
+      if (pos[j] >= 0) v[j] = *reinterpret_cast<const uint2 *>(y + (long long)pos[j] * d + c);
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      if (pos[j] < 0) continue;
+      acc[0] = acc[0] + bf16_to_f32(v[j].x & 0xffffu) * wj[j];
+      acc[1] = acc[1] + bf16_to_f32(v[j].x >> 16) * wj[j];
+      acc[2] = acc[2] + bf16_to_f32(v[j].y & 0xffffu) * wj[j];
+      acc[3] = acc[3] + bf16_to_f32(v[j].y >> 16) * wj[j];
+    }
+  } else {
+    for (int j = 0; j < k; ++j) {
+      const int p = inv[(long long)t * k + j];
+      if (p < 0) continue;
+      const float wjj = w[(long long)t * k + j];
+      const uint2 vv = *reinterpret_cast<const uint2 *>(y + (long long)p * d + c);
+      acc[0] = acc[0] + bf16_to_f32(vv.x & 0xffffu) * wjj;
+      acc[1] = acc[1] + bf16_to_f32(vv.x >> 16) * wjj;
+      acc[2] = acc[2] + bf16_to_f32(vv.y & 0xffffu) * wjj;
+      acc[3] = acc[3] + bf16_to_f32(vv.y >> 16) * wjj;
+    }
   }
   if (shared != nullptr) {
     const uint2 v = *reinterpret_cast<const uint2 *>(shared + (long long)t * d + c);
@@ -203,8 +228,15 @@ int glm_combine_launch(hipStream_t stream, const uint16_t *y, const int32_t *inv
                        const uint16_t *shared, int T, int k, int d, float *out) {
   if (T == 0) return GLM_OK;
   dim3 grid((d / 4 + 255) / 256, T);
-  hipLaunchKernelGGL(glm::combine_kernel, grid, dim3(256), 0, stream, y, inv, w, shared, T, k, d,
-                     out);
+  if (k <= 8)
+    hipLaunchKernelGGL(glm::combine_kernel<8>, grid, dim3(256), 0, stream, y, inv, w, shared, T,
+                       k, d, out);
+  else if (k <= 16)
+    hipLaunchKernelGGL(glm::combine_kernel<16>, grid, dim3(256), 0, stream, y, inv, w, shared, T,
+                       k, d, out);
+  else
+    hipLaunchKernelGGL(glm::combine_kernel<0>, grid, dim3(256), 0, stream, y, inv, w, shared, T,
+                       k, d, out);
   GLM_LAUNCH_CHECK("combine_kernel");
   return GLM_OK;
 }

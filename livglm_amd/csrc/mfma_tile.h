@@ -1,0 +1,214 @@
+// Building blocks of the weight-streaming MFMA tiles (decode GEMV / skinny GEMM).
+//
+// A wave owns a 16-row tile of W and a K range of CPW chunks of 128.  For
+// chunk c, lane (r = l & 15, q = l >> 4) holds the weights of row r at
+// K = c*128 + 32q .. +31 -- exactly one E8M0 group -- which the gfx950
+// scaled converts turn into four bf16x8 MFMA A-fragments (values exact in
+// bf16).  The B operand is one activation row per token column r (the same
+// K positions), so v_mfma_f32_16x16x32_bf16 does the whole K reduction:
+//   MFMA i, slot s of lane (r, q)  <->  K = c*128 + 32q + 8i + s.
+// Output lane (r, q) holds rows 4q..4q+3 of the tile for token column r.
+#pragma once
+
+#include "glm_common.h"
+
+namespace glm {
+
+enum { FMT_BF16 = GLM_FMT_BF16, FMT_MXFP8 = GLM_FMT_MXFP8, FMT_MXFP4 = GLM_FMT_MXFP4 };
+
+__host__ __device__ constexpr int row_bytes(int fmt, int K) {
+  return fmt == FMT_MXFP4 ? K / 2 : (fmt == FMT_MXFP8 ? K : 2 * K);
+}
+
+// Weights are streamed once: non-temporal loads keep them from evicting the
+// small, reused activations and plans from the caches.
+__device__ __forceinline__ glm_u32x4 load_stream(const uint8_t *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const glm_u32x4 *>(p));
+}
+
+template <int FMT>
+struct WChunk;
+template <>
+struct WChunk<FMT_MXFP4> {
+  glm_u32x4 c;
+};
+template <>
+struct WChunk<FMT_MXFP8> {
+  glm_u32x4 c0, c1;
+};
+template <>
+struct WChunk<FMT_BF16> {
+  glm_u32x4 v[4];
+};
+
+template <int FMT>
+__device__ __forceinline__ WChunk<FMT> load_chunk(const uint8_t *wrow, int k0, int q) {
+  WChunk<FMT> w;
+  if constexpr (FMT == FMT_MXFP4) {
+    w.c = load_stream(wrow + (k0 >> 1) + 16 * q);
+  } else if constexpr (FMT == FMT_MXFP8) {
+    w.c0 = load_stream(wrow + k0 + 32 * q);
+    w.c1 = load_stream(wrow + k0 + 32 * q + 16);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w.v[i] = load_stream(wrow + 2 * (k0 + 32 * q) + 16 * i);
+  }
+  return w;
+}
+
+template <int FMT>
+__device__ __forceinline__ void chunk_frags(const WChunk<FMT> &w, uint32_t scale_byte,
+                                            glm_bf16x8 a[4]) {
+  if constexpr (FMT == FMT_MXFP4) {
+    const float sc = e8m0_to_f32(scale_byte);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = mxfp4_word_to_bf16x8(w.c[i], sc);
+  } else if constexpr (FMT == FMT_MXFP8) {
+    const float sc = e8m0_to_f32(scale_byte);
+    a[0] = mxfp8_words_to_bf16x8(w.c0[0], w.c0[1], sc);
+    a[1] = mxfp8_words_to_bf16x8(w.c0[2], w.c0[3], sc);
+    a[2] = mxfp8_words_to_bf16x8(w.c1[0], w.c1[1], sc);
+    a[3] = mxfp8_words_to_bf16x8(w.c1[2], w.c1[3], sc);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = __builtin_bit_cast(glm_bf16x8, w.v[i]);
+  }
+}
+
+__host__ __device__ constexpr int bf16_batch(int cpw, int max_batch) {
+  for (int b = max_batch; b > 1; --b)
+    if (cpw % b == 0) return b;
+  return 1;
+}
+
+// The MX weights of one wave (CPW chunks x NPROJ matrices): issued as one
+// batch of 128-bit loads before anything that depends on the activations.
+template <int FMT, int NPROJ, int CPW>
+struct WaveWeights {
+  WChunk<FMT> w[NPROJ][CPW];
+  uint32_t sd[NPROJ][CPW];  // scale dwords: byte q of dword c is lane q's group of chunk c
+};
+
+template <int FMT, int NPROJ, int CPW>
+__device__ __forceinline__ void load_wave_weights(WaveWeights<FMT, NPROJ, CPW> &ww,
+                                                  const uint8_t *const wrow[NPROJ],
+                                                  const uint8_t *const srow[NPROJ], int kbase,
+                                                  int q) {
+  static_assert(FMT != FMT_BF16, "bf16 weights are streamed in batches by wave_mma");
+#pragma unroll
+  for (int c = 0; c < CPW; ++c)
+#pragma unroll
+    for (int p = 0; p < NPROJ; ++p) ww.w[p][c] = load_chunk<FMT>(wrow[p], kbase + c * 128, q);
+#pragma unroll
+  for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+      ww.sd[p][c] = reinterpret_cast<const uint32_t *>(srow[p] + (kbase >> 5))[c];
+}
+
+__device__ __forceinline__ void load_act_frags(const uint16_t *act, int k0, int q,
+                                               glm_bf16x8 xb[4]) {
+  if (act != nullptr) {
+    const glm_bf16x8 *src = reinterpret_cast<const glm_bf16x8 *>(act + k0 + 32 * q);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xb[i] = src[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xb[i] = glm_bf16x8{};
+  }
+}
+
+// MFMAs of preloaded MX weights against one activation row per lane column.
+template <int FMT, int NPROJ, int CPW>
+__device__ __forceinline__ void mma_wave_weights(const WaveWeights<FMT, NPROJ, CPW> &ww,
+                                                 int kbase, int q, const uint16_t *act,
+                                                 glm_f32x4 acc[NPROJ]) {
+  glm_bf16x8 xb[CPW][4];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) load_act_frags(act, kbase + c * 128, q, xb[c]);
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+#pragma unroll
+    for (int p = 0; p < NPROJ; ++p) {
+      glm_bf16x8 a[4];
+      chunk_frags<FMT>(ww.w[p][c], (ww.sd[p][c] >> (8 * q)) & 0xffu, a);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], xb[c][i], acc[p], 0, 0, 0);
+    }
+  }
+}
+
+// Accumulates, over chunks [kbase/128, kbase/128 + CPW), the 16-row tile of
+// NPROJ weight matrices against one activation row per lane column.
+// wrow/srow: this lane's weight/scale row; act: this lane's activation row
+// (nullptr for a padding column).  Scales of the CPW chunks are CPW aligned
+// dwords at srow + kbase/32 (byte q of dword c is this lane's group).
+template <int FMT, int NPROJ, int CPW>
+__device__ __forceinline__ void wave_mma(const uint8_t *const wrow[NPROJ],
+                                         const uint8_t *const srow[NPROJ], int kbase, int q,
+                                         const uint16_t *act, glm_f32x4 acc[NPROJ]) {
+  if constexpr (FMT != FMT_BF16) {
+    WaveWeights<FMT, NPROJ, CPW> ww;
+    load_wave_weights<FMT, NPROJ, CPW>(ww, wrow, srow, kbase, q);
+    mma_wave_weights<FMT, NPROJ, CPW>(ww, kbase, q, act, acc);
+  } else {
+    // bf16 chunks are 64 B per lane: stream them in batches that divide CPW.
+    constexpr int NB = bf16_batch(CPW, NPROJ == 2 ? 2 : 4);
+    static_assert(CPW % NB == 0, "chunk batch must divide the chunks per wave");
+#pragma unroll
+    for (int b0 = 0; b0 < CPW; b0 += NB) {
+      WChunk<FMT> w[NPROJ][NB];
+#pragma unroll
+      for (int c = 0; c < NB; ++c)
+#pragma unroll
+        for (int p = 0; p < NPROJ; ++p) w[p][c] = load_chunk<FMT>(wrow[p], kbase + (b0 + c) * 128, q);
+      glm_bf16x8 xb[NB][4];
+#pragma unroll
+      for (int c = 0; c < NB; ++c) load_act_frags(act, kbase + (b0 + c) * 128, q, xb[c]);
+#pragma unroll
+      for (int c = 0; c < NB; ++c) {
+#pragma unroll
+        for (int p = 0; p < NPROJ; ++p) {
+          glm_bf16x8 a[4];
+          chunk_frags<FMT>(w[p][c], 0u, a);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], xb[c][i], acc[p], 0, 0, 0);
+        }
+      }
+    }
+  }
+}
+
+// Sums the K-split partials of `nwaves` waves in fixed wave order through LDS
+// (red: nwaves * NPROJ * 64 float4).  Returns true on the wave that holds the
+// total (wave 0); the block must call it uniformly.
+template <int NPROJ>
+__device__ __forceinline__ bool ksplit_reduce(glm_f32x4 acc[NPROJ], glm_f32x4 *red, int wave,
+                                              int nwaves, int lane) {
+  if (nwaves == 1) return true;
+#pragma unroll
+  for (int p = 0; p < NPROJ; ++p) red[(wave * NPROJ + p) * 64 + lane] = acc[p];
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int p = 0; p < NPROJ; ++p) {
+      glm_f32x4 s = red[p * 64 + lane];
+      for (int w = 1; w < nwaves; ++w) s += red[(w * NPROJ + p) * 64 + lane];
+      acc[p] = s;
+    }
+  }
+  __syncthreads();
+  return wave == 0;
+}
+
+// Stores lane (r, q)'s four rows 4q..4q+3 (bf16) of token column r.
+__device__ __forceinline__ void store_rows4(uint16_t *dst, const uint32_t o[4]) {
+  uint2 packed;
+  packed.x = o[0] | (o[1] << 16);
+  packed.y = o[2] | (o[3] << 16);
+  *reinterpret_cast<uint2 *>(dst) = packed;
+}
+
+}  // namespace glm

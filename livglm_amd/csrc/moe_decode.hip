@@ -1,0 +1,629 @@
+// Decode-size routed-MoE layer (T*k <= 512 pairs) in five short kernels:
+//
+//   1. route_logits_kernel    router logits, one block per expert (4 waves
+//                             split d), all tokens.
+//   2. select_dispatch_kernel one block: top-k selection of every token
+//                             (moe.py:39-62) and the dispatch -- histogram,
+//                             exclusive scan, stable permute, work list -- in
+//                             LDS.
+//   3. decode_gate_up_kernel  routed MXFP4 gate/up + SwiGLU, one grid row per
+//                             active expert slot (plus, optionally, one row of
+//                             bf16 shared-expert tiles).
+//   4. decode_down_kernel     routed MXFP4 down (plus optional shared down).
+//   5. combine_kernel         weighted top-k merge + shared add.
+//
+// Every kernel boundary is a stream-ordered dependency; nothing synchronises
+// across blocks inside a kernel, and every reduction runs in one fixed order.
+#include "mfma_tile.h"
+
+namespace glm {
+
+constexpr int kRouteThreads = 256;
+constexpr int kMaxFusedPairs = 512;  // T*k handled by the fused route kernel
+constexpr int kFusedMaxE = 448;
+
+struct RouteArgs {
+  const uint16_t *x;
+  const float *w;
+  const float *bias;
+  int T, d, E, k, n_group, topk_group, norm;
+  float scale;
+  float *logits;
+  float *weights;
+  uint32_t *indices;
+  int32_t *counts, *offsets, *perm, *inv, *pair_token, *active, *num_active, *status;
+  int4 *work;
+};
+
+__device__ __forceinline__ bool better(float v1, int i1, float v2, int i2) {
+  return v1 > v2 || (v1 == v2 && i1 > i2);
+}
+
+// Orders LDS traffic between the lanes of one wave.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Sortable key of a (choice, expert) pair: larger key = better candidate
+// (larger value; on equal values the larger index, as a stable ascending
+// argsort ranks it, moe.py:33-34).  -inf sorts below every finite value.
+__device__ __forceinline__ uint64_t choice_key(float v, int e) {
+  const uint32_t b = __float_as_uint(v);
+  const uint32_t u = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((uint64_t)u << 32) | (uint32_t)e;
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xf, 0xf, false);
+  const uint32_t hi =
+      (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, false);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l) << 32) |
+         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// Maximum of a u64 over the wave: DPP within each row of 16 lanes (quad
+// swaps, then row rotations by 4 and 8), then the four row maxima.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  v = max_u64(v, dpp_u64<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = max_u64(v, dpp_u64<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = max_u64(v, dpp_u64<0x124>(v));  // row_ror:4
+  v = max_u64(v, dpp_u64<0x128>(v));  // row_ror:8
+  return max_u64(max_u64(readlane_u64(v, 0), readlane_u64(v, 16)),
+                 max_u64(readlane_u64(v, 32), readlane_u64(v, 48)));
+}
+
+// Top-k selection of one token by one wave (moe.py:39-62).  Lane l holds
+// experts l + 64i; k rounds of a DPP wave maximum over sortable keys pick the
+// experts best first.
+// `scratch` is this wave's LDS area (>= 64*EPL + 256 words).
+template <int EPL>
+__device__ void select_token(const float *logits_row, const float *bias, int E, int k,
+                             int n_group, int topk_group, int norm, float scale, float *w_out,
+                             uint32_t *i_out, int *pair_idx, float *scratch, int lane) {
+  float score[EPL], choice[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    score[i] = 0.0f;
+    choice[i] = -INFINITY;
+    if (e < E) {
+      score[i] = sigmoid_f32(logits_row[e]);
+      choice[i] = score[i] + bias[e];
+    }
+  }
+  float *s_choice = scratch;            // [64*EPL]
+  float *s_g = scratch + 64 * EPL;      // [64] group scores
+  int *s_keep = (int *)(s_g + 64);      // [64]
+  int *s_isel = s_keep + 64;            // [64]
+  float *s_wsel = (float *)(s_isel + 64);  // [64]
+  if (n_group > 1) {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) s_choice[lane + 64 * i] = choice[i];
+    wave_lds_sync();
+    const int per = E / n_group;
+    if (lane < n_group) {
+      float t1 = -INFINITY, t2 = -INFINITY;
+      for (int qq = 0; qq < per; ++qq) {
+        const float v = s_choice[lane * per + qq];
+        if (v > t1) {
+          t2 = t1;
+          t1 = v;
+        } else if (v > t2) {
+          t2 = v;
+        }
+      }
+      s_g[lane] = t2 + t1;
+    }
+    wave_lds_sync();
+    if (lane < n_group) {
+      const float mine = s_g[lane];
+      int rank = 0;
+      for (int g = 0; g < n_group; ++g) rank += better(s_g[g], g, mine, lane) ? 1 : 0;
+      s_keep[lane] = rank < topk_group;
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E && !s_keep[e / per]) choice[i] = -INFINITY;
+    }
+  }
+  // k rounds of a wave-wide max over the candidates' keys; the winner of
+  // round r lands in ascending column k-1-r and drops out (key 0).
+  uint64_t key[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) key[i] = lane + 64 * i < E ? choice_key(choice[i], lane + 64 * i) : 0;
+  for (int r = 0; r < k; ++r) {
+    uint64_t best = key[0];
+#pragma unroll
+    for (int i = 1; i < EPL; ++i) best = key[i] > best ? key[i] : best;
+    const uint64_t win = wave_max_u64(best);
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      if (key[i] == win) {
+        s_isel[k - 1 - r] = lane + 64 * i;
+        s_wsel[k - 1 - r] = score[i];
+        key[i] = 0;
+      }
+    }
+  }
+  wave_lds_sync();
+  // every lane forms the same sequential sum; lane j < k writes column j
+  float total = 0.0f;
+  if (norm)
+    for (int j = 0; j < k; ++j) total += s_wsel[j];
+  if (lane < k) {
+    float wj = s_wsel[lane];
+    if (norm) wj = wj / (total + 1e-20f);
+    w_out[lane] = wj * scale;
+    i_out[lane] = (uint32_t)s_isel[lane];
+    pair_idx[lane] = s_isel[lane];
+  }
+  wave_lds_sync();
+}
+
+// Exclusive scan over a 256-thread block (4 waves); *total gets the sum.
+__device__ __forceinline__ int scan256(int v, int *s_tmp, int *total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) s_tmp[wave] = incl;
+  __syncthreads();
+  int base = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int s = s_tmp[w];
+    if (w < wave) base += s;
+    tot += s;
+  }
+  __syncthreads();
+  *total = tot;
+  return base + incl - v;
+}
+
+// logits[t][e] = f32(x[t]) . w[e] for all tokens; block = expert e, wave w
+// sums the K range [w*d/4, (w+1)*d/4), partials added in wave order.
+template <int TT>
+__global__ __launch_bounds__(kRouteThreads) void route_logits_kernel(RouteArgs a) {
+  __shared__ float s_part[4][TT];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e = blockIdx.x;
+  const int T = a.T, d = a.d, E = a.E;
+  const int kq = d >> 2;
+  const float *wrow = a.w + (size_t)e * d + wave * kq;
+  for (int t0 = 0; t0 < T; t0 += TT) {
+    float acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) acc[t] = 0.0f;
+    for (int kk = lane * 4; kk < kq; kk += 256) {
+      const float4 wv = *reinterpret_cast<const float4 *>(wrow + kk);
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        if (t0 + t < T) {
+          const uint2 xv =
+              *reinterpret_cast<const uint2 *>(a.x + (size_t)(t0 + t) * d + wave * kq + kk);
+          float s = acc[t];
+          s = fmaf(bf16_to_f32(xv.x & 0xffffu), wv.x, s);
+          s = fmaf(bf16_to_f32(xv.x >> 16), wv.y, s);
+          s = fmaf(bf16_to_f32(xv.y & 0xffffu), wv.z, s);
+          s = fmaf(bf16_to_f32(xv.y >> 16), wv.w, s);
+          acc[t] = s;
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      const float v = wave_sum(acc[t]);
+      if (lane == 0) s_part[wave][t] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < TT && t0 + (int)threadIdx.x < T) {
+      const int t = threadIdx.x;
+      a.logits[(size_t)(t0 + t) * E + e] = ((s_part[0][t] + s_part[1][t]) + s_part[2][t]) + s_part[3][t];
+    }
+    __syncthreads();
+  }
+}
+
+// One block: selection for every token, then the dispatch of its P pairs.
+template <int EPL>
+__global__ __launch_bounds__(kRouteThreads) void select_dispatch_kernel(RouteArgs a) {
+  extern __shared__ int lds[];
+  __shared__ int s_tmp[4];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int T = a.T, E = a.E, k = a.k;
+  const int P = T * k;
+  int *s_idx = lds;                       // [P]
+  int *cnt = s_idx + kMaxFusedPairs;      // [E]
+  int *off = cnt + kFusedMaxE;            // [E]
+  int *s_active = off + kFusedMaxE;       // [E]
+  uint32_t *bits = (uint32_t *)(s_active + kFusedMaxE);  // [E][16]
+  float *wave_scratch = (float *)(bits + kFusedMaxE * 16) + wave * (64 * EPL + 256);
+
+  for (int i = threadIdx.x; i < E; i += kRouteThreads) cnt[i] = 0;
+  for (int i = threadIdx.x; i < E * 16; i += kRouteThreads) bits[i] = 0;
+  // top-k per token (wave w: tokens w, w+4, ...)
+  for (int t = wave; t < T; t += 4)
+    select_token<EPL>(a.logits + (size_t)t * E, a.bias, E, k, a.n_group, a.topk_group, a.norm,
+                      a.scale, a.weights + (size_t)t * k, a.indices + (size_t)t * k,
+                      s_idx + t * k, wave_scratch, lane);
+  __syncthreads();
+
+  for (int p = threadIdx.x; p < P; p += kRouteThreads) {
+    const int ee = s_idx[p];
+    atomicAdd(&cnt[ee], 1);
+    atomicOr(&bits[ee * 16 + (p >> 5)], 1u << (p & 31));
+  }
+  __syncthreads();
+  const int per = (E + kRouteThreads - 1) / kRouteThreads;  // experts per thread (<= 2)
+  int local = 0, local_act = 0;
+  for (int i = 0; i < per; ++i) {
+    const int ee = threadIdx.x * per + i;
+    if (ee < E) {
+      local += cnt[ee];
+      local_act += cnt[ee] > 0;
+    }
+  }
+  int tot = 0, tot_act = 0;
+  const int base = scan256(local, s_tmp, &tot);
+  const int base_act = scan256(local_act, s_tmp, &tot_act);
+  {
+    int run = base, run_act = base_act;
+    for (int i = 0; i < per; ++i) {
+      const int ee = threadIdx.x * per + i;
+      if (ee < E) {
+        off[ee] = run;
+        a.offsets[ee] = run;
+        a.counts[ee] = cnt[ee];
+        if (cnt[ee] > 0) {
+          s_active[run_act] = ee;
+          ++run_act;
+        }
+        run += cnt[ee];
+      }
+    }
+  }
+  if (threadIdx.x == 0) {
+    a.offsets[E] = tot;
+    a.num_active[0] = tot_act;
+    a.status[0] = 0;
+  }
+  __syncthreads();
+  for (int u = threadIdx.x; u < E; u += kRouteThreads) {
+    if (u < tot_act) {
+      const int ee = s_active[u];
+      a.active[u] = ee;
+      a.work[u] = make_int4(ee, off[ee], cnt[ee], 0);
+    } else {
+      a.active[u] = -1;
+      a.work[u] = make_int4(-1, 0, 0, 0);
+    }
+  }
+  for (int p = threadIdx.x; p < P; p += kRouteThreads) {
+    const int ee = s_idx[p];
+    const uint32_t *row = bits + ee * 16;
+    int r = 0;
+    const int word = p >> 5;
+    for (int w = 0; w < word; ++w) r += __popc(row[w]);
+    r += __popc(row[word] & ((1u << (p & 31)) - 1u));
+    const int pos = off[ee] + r;
+    a.perm[pos] = p;
+    a.inv[p] = pos;
+    a.pair_token[pos] = p / k;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Gate/up: grid (row tiles, [1 +] slots).  With a shared expert, grid row 0
+// holds its bf16 tiles (all T tokens) and row 1 + u the routed expert of work
+// slot u (MXFP4); otherwise row u is work slot u.
+// Four waves split K; wave 0 reduces and applies SwiGLU.
+// ---------------------------------------------------------------------------
+struct GateUpArgs {
+  const uint16_t *x;
+  const int32_t *pair_token;
+  const int4 *work;
+  int slots;
+  const uint8_t *gw, *gs, *uw, *us;
+  long long w_stride, s_stride;
+  int I, d;
+  uint16_t *h;  // [P][I]
+  const uint8_t *sg, *su;  // shared bf16 gate/up [Is][d] (nullptr: none)
+  int Is, T;
+  uint16_t *hs;  // [T][Is]
+  float limit;
+};
+
+template <int CPW, bool SHARED>
+__global__ __launch_bounds__(256) void decode_gate_up_kernel(GateUpArgs a) {
+  __shared__ glm_f32x4 red[4 * 2 * 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int row0 = blockIdx.x * 16;
+  const int kbase = wave * CPW * 128;
+  const int d = a.d;
+  // the shared expert is grid row 0, so its tiles start with the first wave of
+  // blocks instead of trailing after every routed tile
+  const bool shared = SHARED && blockIdx.y == 0;
+  int e = 0, base = 0, n = a.T, N = a.Is;
+  if (!shared) {
+    const int4 wk = a.work[blockIdx.y - (SHARED ? 1 : 0)];
+    e = wk.x;
+    base = wk.y;
+    n = wk.z;
+    N = a.I;
+  }
+  if (e < 0 || n <= 0 || row0 >= N) return;
+
+  for (int p0 = 0; p0 < n; p0 += 16) {
+    const int pair = p0 + r;
+    glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
+    if (!shared) {
+      const uint8_t *wrow[2] = {a.gw + e * a.w_stride + (size_t)(row0 + r) * (d / 2),
+                                a.uw + e * a.w_stride + (size_t)(row0 + r) * (d / 2)};
+      const uint8_t *srow[2] = {a.gs + e * a.s_stride + (size_t)(row0 + r) * (d / 32),
+                                a.us + e * a.s_stride + (size_t)(row0 + r) * (d / 32)};
+      // weight stream first; the token lookup overlaps with it
+      WaveWeights<FMT_MXFP4, 2, CPW> ww;
+      load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
+      const uint16_t *act = pair < n ? a.x + (size_t)a.pair_token[base + pair] * d : nullptr;
+      mma_wave_weights<FMT_MXFP4, 2, CPW>(ww, kbase, q, act, acc);
+    } else if constexpr (SHARED) {
+      const uint16_t *act = pair < n ? a.x + (size_t)pair * d : nullptr;
+      const uint8_t *wrow[2] = {a.sg + (size_t)(row0 + r) * d * 2, a.su + (size_t)(row0 + r) * d * 2};
+      const uint8_t *srow[2] = {nullptr, nullptr};
+      wave_mma<FMT_BF16, 2, CPW>(wrow, srow, kbase, q, act, acc);
+    }
+    if (ksplit_reduce<2>(acc, red, wave, 4, lane) && pair < n) {
+      uint32_t o[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        o[m] = f32_to_bf16(limited_swiglu(bf16_round(acc[0][m]), bf16_round(acc[1][m]), a.limit));
+      uint16_t *dst = shared ? a.hs + (size_t)pair * N : a.h + (size_t)(base + pair) * N;
+      store_rows4(dst + row0 + 4 * q, o);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Down: grid (d/64 row tiles, slots [+ 1 shared]).  Each wave owns 16 output
+// rows over the full K = I.
+// ---------------------------------------------------------------------------
+struct DownArgs {
+  const uint16_t *h;
+  const int4 *work;
+  int slots;
+  const uint8_t *dw, *ds;
+  long long w_stride, s_stride;
+  int I, d;
+  uint16_t *y;  // [P][d]
+  const uint16_t *hs;  // [T][Is]
+  const uint8_t *sd;   // shared bf16 down [d][Is] (nullptr: none)
+  int Is, T;
+  uint16_t *ys;  // [T][d]
+};
+
+template <int CPW_R, int CPW_S>
+__global__ __launch_bounds__(256) void decode_down_kernel(DownArgs a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int tile = blockIdx.x;
+  const int row0 = tile * 64 + wave * 16;
+  const int d = a.d;
+  const bool shared = a.sd != nullptr && blockIdx.y == 0;  // shared expert: grid row 0
+  int e = 0, base = 0, n = a.T;
+  if (!shared) {
+    const int4 wk = a.work[blockIdx.y - (a.sd != nullptr ? 1 : 0)];
+    e = wk.x;
+    base = wk.y;
+    n = wk.z;
+    if (e < 0 || n <= 0) return;
+  }
+  for (int p0 = 0; p0 < n; p0 += 16) {
+    const int pair = p0 + r;
+    glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
+    if (!shared) {
+      const uint16_t *act = pair < n ? a.h + (size_t)(base + pair) * a.I : nullptr;
+      const uint8_t *wrow[1] = {a.dw + e * a.w_stride + (size_t)(row0 + r) * (a.I / 2)};
+      const uint8_t *srow[1] = {a.ds + e * a.s_stride + (size_t)(row0 + r) * (a.I / 32)};
+      wave_mma<FMT_MXFP4, 1, CPW_R>(wrow, srow, 0, q, act, acc);
+    } else {
+      const uint16_t *act = pair < n ? a.hs + (size_t)pair * a.Is : nullptr;
+      const uint8_t *wrow[1] = {reinterpret_cast<const uint8_t *>(a.sd) + (size_t)(row0 + r) * a.Is * 2};
+      const uint8_t *srow[1] = {nullptr};
+      wave_mma<FMT_BF16, 1, CPW_S>(wrow, srow, 0, q, act, acc);
+    }
+    if (pair < n) {
+      uint32_t o[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) o[m] = f32_to_bf16(acc[0][m]);
+      uint16_t *dst = shared ? a.ys + (size_t)pair * d : a.y + (size_t)(base + pair) * d;
+      store_rows4(dst + row0 + 4 * q, o);
+    }
+  }
+
+}
+
+// zero-fill (workspace initialisation)
+__global__ void fill_zero_kernel(uint32_t *p, long long n) {
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n;
+       i += (long long)gridDim.x * blockDim.x)
+    p[i] = 0;
+}
+
+}  // namespace glm
+
+using namespace glm;
+
+size_t glm_select_dispatch_lds_bytes(int EPL) {
+  return (size_t)(kMaxFusedPairs + 3 * kFusedMaxE + 16 * kFusedMaxE) * 4 +
+         (size_t)4 * (64 * EPL + 256) * 4;
+}
+
+// Whether the decode kernels cover this layer shape.
+static bool chunk_count_ok(int c) { return c == 1 || c == 2 || c == 4 || c == 6 || c == 8; }
+
+bool glm_decode_gate_up_supported(int d, int I) {
+  return d % 512 == 0 && d / 512 >= 2 && chunk_count_ok(d / 512) && I % 16 == 0;
+}
+
+bool glm_decode_down_supported(int I, int d) {
+  return I % 128 == 0 && chunk_count_ok(I / 128) && d % 64 == 0;
+}
+
+bool glm_decode_path_supported(int T, int d, int E, int k, int I, int Is) {
+  if (T < 1 || (long long)T * k > kMaxFusedPairs || E > kFusedMaxE) return false;
+  // gate/up: 4 waves x CPW chunks of 128 over d; down: 64-row tiles of d
+  if (d % 512 != 0 || !chunk_count_ok(d / 512) || d / 512 < 2) return false;
+  if (I % 128 != 0 || !chunk_count_ok(I / 128)) return false;
+  if (Is > 0 && (Is % 128 != 0 || !chunk_count_ok(Is / 128))) return false;
+  return true;
+}
+
+int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d, const float *w,
+                            const float *bias, int E, int k, int n_group, int topk_group,
+                            int norm, float scale, float *logits, float *weights,
+                            uint32_t *indices, int32_t *counts, int32_t *offsets, int32_t *perm,
+                            int32_t *inv, int32_t *pair_token, int32_t *active,
+                            int32_t *num_active, int32_t *status, int4 *work) {
+  RouteArgs a{x,      w,      bias,   T,   d,          E,      k,          n_group,
+              topk_group, norm, scale, logits, weights, indices, counts, offsets,
+              perm,   inv,    pair_token, active, num_active, status, work};
+  if (T <= 2)
+    hipLaunchKernelGGL((route_logits_kernel<2>), dim3(E), dim3(kRouteThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((route_logits_kernel<8>), dim3(E), dim3(kRouteThreads), 0, stream, a);
+  GLM_LAUNCH_CHECK("route_logits_kernel");
+  const int epl = (E + 63) / 64;
+  const int e8 = epl <= 1 ? 1 : (epl <= 2 ? 2 : (epl <= 4 ? 4 : 8));
+  const size_t lds = glm_select_dispatch_lds_bytes(e8);
+#define GLM_SEL(EP) \
+  hipLaunchKernelGGL((select_dispatch_kernel<EP>), dim3(1), dim3(kRouteThreads), lds, stream, a)
+  if (e8 == 1) GLM_SEL(1);
+  else if (e8 == 2) GLM_SEL(2);
+  else if (e8 == 4) GLM_SEL(4);
+  else GLM_SEL(8);
+#undef GLM_SEL
+  GLM_LAUNCH_CHECK("select_dispatch_kernel");
+  return GLM_OK;
+}
+
+int glm_decode_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int E,
+                              int k, const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
+                              const uint8_t *us, const int32_t *pair_token, const int4 *work,
+                              const uint16_t *sg, const uint16_t *su, int Is, uint16_t *h,
+                              uint16_t *hs, float limit) {
+  GateUpArgs a{};
+  a.x = x;
+  a.pair_token = pair_token;
+  a.work = work;
+  a.slots = std::min(E, T * k);
+  a.gw = gw;
+  a.gs = gs;
+  a.uw = uw;
+  a.us = us;
+  a.w_stride = (long long)I * (d / 2);
+  a.s_stride = (long long)I * (d / 32);
+  a.I = I;
+  a.d = d;
+  a.h = h;
+  a.sg = reinterpret_cast<const uint8_t *>(sg);
+  a.su = reinterpret_cast<const uint8_t *>(su);
+  a.Is = sg ? Is : 0;
+  a.T = T;
+  a.hs = hs;
+  a.limit = glm_limit_bf16(limit);
+  const int rows = std::max(I, a.Is);
+  const bool with_shared = a.Is > 0;
+  dim3 grid(rows / 16, a.slots + (with_shared ? 1 : 0));
+  const int cpw = d / 512;
+#define GLM_GU(C)                                                                          \
+  if (with_shared)                                                                          \
+    hipLaunchKernelGGL((decode_gate_up_kernel<C, true>), grid, dim3(256), 0, stream, a);   \
+  else                                                                                      \
+    hipLaunchKernelGGL((decode_gate_up_kernel<C, false>), grid, dim3(256), 0, stream, a)
+  switch (cpw) {
+    case 2: GLM_GU(2); break;
+    case 4: GLM_GU(4); break;
+    case 6: GLM_GU(6); break;
+    case 8: GLM_GU(8); break;
+    default: glm::set_error("decode gate/up: unsupported d=%d", d); return GLM_ERR_UNSUPPORTED_SHAPE;
+  }
+#undef GLM_GU
+  GLM_LAUNCH_CHECK("decode_gate_up_kernel");
+  return GLM_OK;
+}
+
+template <int CR>
+static void launch_down_cs(hipStream_t stream, dim3 grid, const DownArgs &a, int cs) {
+  switch (cs) {
+    case 1: hipLaunchKernelGGL((decode_down_kernel<CR, 1>), grid, dim3(256), 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((decode_down_kernel<CR, 2>), grid, dim3(256), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL((decode_down_kernel<CR, 4>), grid, dim3(256), 0, stream, a); break;
+    case 6: hipLaunchKernelGGL((decode_down_kernel<CR, 6>), grid, dim3(256), 0, stream, a); break;
+    default: hipLaunchKernelGGL((decode_down_kernel<CR, 8>), grid, dim3(256), 0, stream, a); break;
+  }
+}
+
+int glm_decode_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, int d,
+                           int E, const uint8_t *dw, const uint8_t *ds, const int4 *work,
+                           const uint16_t *hs, const uint16_t *sd, int Is, uint16_t *y,
+                           uint16_t *ys) {
+  DownArgs a{};
+  a.h = h;
+  a.work = work;
+  a.slots = std::min(E, T * k);
+  a.dw = dw;
+  a.ds = ds;
+  a.w_stride = (long long)d * (I / 2);
+  a.s_stride = (long long)d * (I / 32);
+  a.I = I;
+  a.d = d;
+  a.y = y;
+  a.hs = hs;
+  a.sd = reinterpret_cast<const uint8_t *>(sd);
+  a.Is = sd ? Is : 0;
+  a.T = T;
+  a.ys = ys;
+  dim3 grid(d / 64, a.slots + (sd ? 1 : 0));
+  const int cr = I / 128;
+  const int cs = sd ? Is / 128 : 1;
+  if (cs != 1 && cs != 2 && cs != 4 && cs != 6 && cs != 8) {
+    glm::set_error("decode down: unsupported I_shared=%d", Is);
+    return GLM_ERR_UNSUPPORTED_SHAPE;
+  }
+  switch (cr) {
+    case 1: launch_down_cs<1>(stream, grid, a, cs); break;
+    case 2: launch_down_cs<2>(stream, grid, a, cs); break;
+    case 4: launch_down_cs<4>(stream, grid, a, cs); break;
+    case 6: launch_down_cs<6>(stream, grid, a, cs); break;
+    case 8: launch_down_cs<8>(stream, grid, a, cs); break;
+    default: glm::set_error("decode down: unsupported I=%d", I); return GLM_ERR_UNSUPPORTED_SHAPE;
+  }
+  GLM_LAUNCH_CHECK("decode_down_kernel");
+  return GLM_OK;
+}
+
+int glm_fill_zero_launch(hipStream_t stream, void *p, size_t bytes) {
+  const long long n = (long long)(bytes / 4);
+  if (n == 0) return GLM_OK;
+  long long blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     (uint32_t *)p, n);
+  GLM_LAUNCH_CHECK("fill_zero_kernel");
+  return GLM_OK;
+}

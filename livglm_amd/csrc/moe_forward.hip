@@ -37,20 +37,35 @@ int glm_router_launch(hipStream_t stream, const uint16_t *x, int T, int d, const
                       float scale, float *logits, float *weights, uint32_t *indices);
 int glm_dispatch_launch(hipStream_t stream, const uint32_t *indices, int T, int k, int E,
                         int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
-                        int32_t *pair_token, int32_t *active, int32_t *num_active,
+                        int32_t *pair_token, int32_t *active, int32_t *num_active, int4 *work,
                         int32_t *status);
 int glm_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int E, int k,
                        const uint8_t *gw, const uint8_t *gs, const uint8_t *uw, const uint8_t *us,
-                       const int32_t *offsets, const int32_t *pair_token, const int32_t *active,
-                       const int32_t *num_active, float limit, uint16_t *h);
+                       const int32_t *pair_token, const int4 *work, float limit, uint16_t *h);
 int glm_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, int d, int E,
-                    const uint8_t *dw, const uint8_t *ds, const int32_t *offsets,
-                    const int32_t *active, const int32_t *num_active, uint16_t *y);
+                    const uint8_t *dw, const uint8_t *ds, const int4 *work, uint16_t *y);
 int glm_mlp_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int fmt,
                    const void *gw, const uint8_t *gs, const void *uw, const uint8_t *us,
                    const void *dw, const uint8_t *ds, float limit, uint16_t *h, uint16_t *out);
 int glm_combine_launch(hipStream_t stream, const uint16_t *y, const int32_t *inv, const float *w,
                        const uint16_t *shared, int T, int k, int d, float *out);
+bool glm_decode_path_supported(int T, int d, int E, int k, int I, int Is);
+int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d, const float *w,
+                            const float *bias, int E, int k, int n_group, int topk_group,
+                            int norm, float scale, float *logits, float *weights,
+                            uint32_t *indices, int32_t *counts, int32_t *offsets, int32_t *perm,
+                            int32_t *inv, int32_t *pair_token, int32_t *active,
+                            int32_t *num_active, int32_t *status, int4 *work);
+int glm_decode_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int E,
+                              int k, const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
+                              const uint8_t *us, const int32_t *pair_token, const int4 *work,
+                              const uint16_t *sg, const uint16_t *su, int Is, uint16_t *h,
+                              uint16_t *hs, float limit);
+int glm_decode_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, int d,
+                           int E, const uint8_t *dw, const uint8_t *ds, const int4 *work,
+                           const uint16_t *hs, const uint16_t *sd, int Is, uint16_t *y,
+                           uint16_t *ys);
+int glm_fill_zero_launch(hipStream_t stream, void *p, size_t bytes);
 
 // ---------------------------------------------------------------- workspace
 
@@ -76,6 +91,7 @@ struct Workspace {
   uint16_t *y;
   uint16_t *shared_h;
   uint16_t *shared_out;
+  int4 *work;
   size_t bytes;
 };
 
@@ -104,6 +120,7 @@ Workspace carve(char *base, int T, int d, int E, int k, int I, int Is) {
   w.y = (uint16_t *)take(P * d * 2);
   w.shared_h = (uint16_t *)take((size_t)T * (Is > 0 ? Is : 0) * 2);
   w.shared_out = (uint16_t *)take((size_t)T * (Is > 0 ? d : 0) * 2);
+  w.work = (int4 *)take((size_t)E * sizeof(int4));
   w.bytes = off;
   return w;
 }
@@ -113,6 +130,14 @@ Workspace carve(char *base, int T, int d, int E, int k, int I, int Is) {
 extern "C" size_t glm_moe_workspace_bytes(int T, int d, int E, int top_k, int I, int I_shared) {
   if (T < 0 || d <= 0 || E <= 0 || top_k <= 0 || I <= 0) return 0;
   return carve(nullptr, T, d, E, top_k, I, I_shared).bytes;
+}
+
+extern "C" int glm_moe_workspace_init(void *stream, void *workspace, size_t workspace_bytes) {
+  glm::clear_error();
+  GLM_REQUIRE(workspace != nullptr, GLM_ERR_INVALID_ARGUMENT, "workspace_init: null workspace");
+  GLM_REQUIRE(glm_aligned16({workspace}) && workspace_bytes % 4 == 0, GLM_ERR_INVALID_ARGUMENT,
+              "workspace_init: workspace must be 16-byte aligned and a multiple of 4 bytes");
+  return glm_fill_zero_launch((hipStream_t)stream, workspace, workspace_bytes);
 }
 
 extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
@@ -125,8 +150,9 @@ extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
                                const void *shared_gate, const uint8_t *shared_gate_scales,
                                const void *shared_up, const uint8_t *shared_up_scales,
                                const void *shared_down, const uint8_t *shared_down_scales,
-                               float swiglu_limit, void *workspace, size_t workspace_bytes,
-                               float *out, float *weights_out, uint32_t *indices_out) {
+                               const uint16_t *shared_in, float swiglu_limit, void *workspace,
+                               size_t workspace_bytes, float *out, float *weights_out,
+                               uint32_t *indices_out) {
   glm::clear_error();
   hipStream_t stream = (hipStream_t)stream_v;
   GLM_REQUIRE(x && router_weight && router_bias && gate_packed && gate_scales && up_packed &&
@@ -151,8 +177,8 @@ extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
                                topk_group, out, out);
   if (rc != GLM_OK) return rc;
   GLM_REQUIRE(glm_aligned16({x, router_weight, router_bias, gate_packed, up_packed, down_packed,
-                              shared_gate, shared_up, shared_down, workspace, out, weights_out,
-                              indices_out}),
+                              shared_gate, shared_up, shared_down, shared_in, workspace, out,
+                              weights_out, indices_out}),
               GLM_ERR_INVALID_ARGUMENT, "moe_forward: buffers must be 16-byte aligned");
   const Workspace need = carve(nullptr, T, d, E, top_k, I, has_shared ? I_shared : 0);
   GLM_REQUIRE(workspace_bytes >= need.bytes, GLM_ERR_WORKSPACE,
@@ -163,25 +189,55 @@ extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
   float *wts = weights_out ? weights_out : w.weights;
   uint32_t *idx = indices_out ? indices_out : w.indices;
 
+  const int Is = has_shared ? I_shared : 0;
+  const bool shared_bf16 = has_shared && shared_fmt == GLM_FMT_BF16;
+  const uint16_t *shared_ready = shared_in;  // caller-computed shared output, if any
+  if (glm_decode_path_supported(T, d, E, top_k, I, shared_bf16 && !shared_in ? Is : 0)) {
+    // decode: five short kernels, no host synchronisation
+    rc = glm_route_decode_launch(stream, x, T, d, router_weight, router_bias, E, top_k, n_group,
+                                 topk_group, norm_topk_prob, routed_scaling_factor, w.logits,
+                                 wts, idx, w.counts, w.offsets, w.perm, w.inv, w.pair_token,
+                                 w.active, w.num_active, w.status, w.work);
+    if (rc) return rc;
+    const bool fuse_shared = shared_bf16 && !shared_in;
+    rc = glm_decode_gate_up_launch(stream, x, T, d, I, E, top_k, gate_packed, gate_scales,
+                                   up_packed, up_scales, w.pair_token, w.work,
+                                   fuse_shared ? (const uint16_t *)shared_gate : nullptr,
+                                   fuse_shared ? (const uint16_t *)shared_up : nullptr, Is, w.h,
+                                   w.shared_h, swiglu_limit);
+    if (rc) return rc;
+    rc = glm_decode_down_launch(stream, w.h, T, top_k, I, d, E, down_packed, down_scales, w.work,
+                                w.shared_h,
+                                fuse_shared ? (const uint16_t *)shared_down : nullptr, Is, w.y,
+                                w.shared_out);
+    if (rc) return rc;
+    if (fuse_shared) shared_ready = w.shared_out;
+    else if (has_shared && !shared_in) {
+      rc = glm_mlp_launch(stream, x, T, d, I_shared, shared_fmt, shared_gate, shared_gate_scales,
+                          shared_up, shared_up_scales, shared_down, shared_down_scales,
+                          swiglu_limit, w.shared_h, w.shared_out);
+      if (rc) return rc;
+      shared_ready = w.shared_out;
+    }
+    return glm_combine_launch(stream, w.y, w.inv, wts, shared_ready, T, top_k, d, out);
+  }
   rc = glm_router_launch(stream, x, T, d, router_weight, router_bias, E, top_k, n_group,
                          topk_group, norm_topk_prob, routed_scaling_factor, w.logits, wts, idx);
   if (rc) return rc;
   rc = glm_dispatch_launch(stream, idx, T, top_k, E, w.counts, w.offsets, w.perm, w.inv,
-                           w.pair_token, w.active, w.num_active, w.status);
+                           w.pair_token, w.active, w.num_active, w.work, w.status);
   if (rc) return rc;
   rc = glm_gate_up_launch(stream, x, T, d, I, E, top_k, gate_packed, gate_scales, up_packed,
-                          up_scales, w.offsets, w.pair_token, w.active, w.num_active,
-                          swiglu_limit, w.h);
+                          up_scales, w.pair_token, w.work, swiglu_limit, w.h);
   if (rc) return rc;
-  rc = glm_down_launch(stream, w.h, T, top_k, I, d, E, down_packed, down_scales, w.offsets,
-                       w.active, w.num_active, w.y);
+  rc = glm_down_launch(stream, w.h, T, top_k, I, d, E, down_packed, down_scales, w.work, w.y);
   if (rc) return rc;
-  if (has_shared) {
+  if (has_shared && !shared_in) {
     rc = glm_mlp_launch(stream, x, T, d, I_shared, shared_fmt, shared_gate, shared_gate_scales,
                         shared_up, shared_up_scales, shared_down, shared_down_scales,
                         swiglu_limit, w.shared_h, w.shared_out);
     if (rc) return rc;
+    shared_ready = w.shared_out;
   }
-  return glm_combine_launch(stream, w.y, w.inv, wts, has_shared ? w.shared_out : nullptr, T,
-                            top_k, d, out);
+  return glm_combine_launch(stream, w.y, w.inv, wts, shared_ready, T, top_k, d, out);
 }

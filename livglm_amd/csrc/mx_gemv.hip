@@ -34,9 +34,7 @@ struct GemvArgs {
   long long s_stride;        // bytes between consecutive experts' scales
   int N;                     // rows per expert (output features)
   int K;                     // reduction length
-  const int32_t *offsets;    // [E+1] routed mode; nullptr = dense mode
-  const int32_t *active;     // [E] active expert ids (routed mode)
-  const int32_t *num_active; // [1] (routed mode)
+  const int4 *work;          // routed mode: {expert, first row, rows, 0} per slot; nullptr = dense
   int dense_rows;            // dense mode: number of activation rows
   uint16_t *out;             // bf16 [pos][N]
   float limit;               // bf16-rounded swiglu limit (NPROJ == 2)
@@ -138,12 +136,12 @@ __global__ __launch_bounds__(512) void mx_gemv_kernel(const GemvArgs args) {
   const int q = lane >> 4;
 
   int e = 0, base = 0, n = args.dense_rows;
-  if (args.offsets != nullptr) {
-    const int u = blockIdx.y;
-    if (u >= args.num_active[0]) return;
-    e = args.active[u];
-    base = args.offsets[e];
-    n = args.offsets[e + 1] - base;
+  if (args.work != nullptr) {
+    const int4 wk = args.work[blockIdx.y];
+    if (wk.x < 0) return;
+    e = wk.x;
+    base = wk.y;
+    n = wk.z;
   }
   if (n <= 0) return;
   const int K = args.K;
@@ -299,12 +297,12 @@ template <int FMT, int NPROJ>
 __global__ __launch_bounds__(256) void gemv_generic_kernel(const GemvArgs args) {
   const int row = blockIdx.x * blockDim.x + threadIdx.x;
   int e = 0, base = 0, n = args.dense_rows;
-  if (args.offsets != nullptr) {
-    const int u = blockIdx.y;
-    if (u >= args.num_active[0]) return;
-    e = args.active[u];
-    base = args.offsets[e];
-    n = args.offsets[e + 1] - base;
+  if (args.work != nullptr) {
+    const int4 wk = args.work[blockIdx.y];
+    if (wk.x < 0) return;
+    e = wk.x;
+    base = wk.y;
+    n = wk.z;
   }
   if (row >= args.N) return;
   const int K = args.K;
@@ -408,10 +406,24 @@ static int check_fmt(int fmt) {
   return GLM_OK;
 }
 
+int glm_decode_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int E,
+                              int k, const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
+                              const uint8_t *us, const int32_t *pair_token, const int4 *work,
+                              const uint16_t *sg, const uint16_t *su, int Is, uint16_t *h,
+                              uint16_t *hs, float limit);
+int glm_decode_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, int d,
+                           int E, const uint8_t *dw, const uint8_t *ds, const int4 *work,
+                           const uint16_t *hs, const uint16_t *sd, int Is, uint16_t *y,
+                           uint16_t *ys);
+bool glm_decode_gate_up_supported(int d, int I);
+bool glm_decode_down_supported(int I, int d);
+
 int glm_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int E, int k,
                        const uint8_t *gw, const uint8_t *gs, const uint8_t *uw, const uint8_t *us,
-                       const int32_t *offsets, const int32_t *pair_token, const int32_t *active,
-                       const int32_t *num_active, float limit, uint16_t *h) {
+                       const int32_t *pair_token, const int4 *work, float limit, uint16_t *h) {
+  if (glm_decode_gate_up_supported(d, I))
+    return glm_decode_gate_up_launch(stream, x, T, d, I, E, k, gw, gs, uw, us, pair_token, work,
+                                     nullptr, nullptr, 0, h, nullptr, limit);
   GemvArgs a{};
   a.act = x;
   a.act_index = pair_token;
@@ -423,9 +435,7 @@ int glm_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int 
   a.s_stride = (long long)I * (d / 32);
   a.N = I;
   a.K = d;
-  a.offsets = offsets;
-  a.active = active;
-  a.num_active = num_active;
+  a.work = work;
   a.out = h;
   a.limit = glm_limit_bf16(limit);
   const int slots = std::min(E, T * k);
@@ -433,8 +443,10 @@ int glm_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int 
 }
 
 int glm_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, int d, int E,
-                    const uint8_t *dw, const uint8_t *ds, const int32_t *offsets,
-                    const int32_t *active, const int32_t *num_active, uint16_t *y) {
+                    const uint8_t *dw, const uint8_t *ds, const int4 *work, uint16_t *y) {
+  if (glm_decode_down_supported(I, d))
+    return glm_decode_down_launch(stream, h, T, k, I, d, E, dw, ds, work, nullptr, nullptr, 0, y,
+                                  nullptr);
   GemvArgs a{};
   a.act = h;
   a.act_index = nullptr;
@@ -444,9 +456,7 @@ int glm_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, 
   a.s_stride = (long long)d * (I / 32);
   a.N = d;
   a.K = I;
-  a.offsets = offsets;
-  a.active = active;
-  a.num_active = num_active;
+  a.work = work;
   a.out = y;
   const int slots = std::min(E, T * k);
   return glm_gemv_launch(stream, GLM_FMT_MXFP4, 1, a, slots);
@@ -497,39 +507,38 @@ static int check_mx_geometry(const char *who, int fmt, int in_dims, int out_dims
 extern "C" int glm_expert_gate_up(void *stream, const uint16_t *x, int T, int d, int I, int E,
                                   int top_k, const uint8_t *gate_packed,
                                   const uint8_t *gate_scales, const uint8_t *up_packed,
-                                  const uint8_t *up_scales, const int32_t *offsets,
-                                  const int32_t *pair_token, const int32_t *active,
-                                  const int32_t *num_active, float swiglu_limit, uint16_t *h) {
+                                  const uint8_t *up_scales, const int32_t *pair_token,
+                                  const int32_t *work, float swiglu_limit, uint16_t *h) {
   glm::clear_error();
-  GLM_REQUIRE(x && gate_packed && gate_scales && up_packed && up_scales && offsets &&
-                  pair_token && active && num_active && h,
+  GLM_REQUIRE(x && gate_packed && gate_scales && up_packed && up_scales && pair_token && work &&
+                  h,
               GLM_ERR_INVALID_ARGUMENT, "expert_gate_up: null pointer argument");
   GLM_REQUIRE(T >= 0 && E >= 1 && top_k >= 1, GLM_ERR_INVALID_ARGUMENT,
               "expert_gate_up: invalid sizes");
   int rc = check_mx_geometry("expert_gate_up", GLM_FMT_MXFP4, d, I);
   if (rc) return rc;
-  GLM_REQUIRE(glm_aligned16({x, gate_packed, up_packed, h}), GLM_ERR_INVALID_ARGUMENT,
+  GLM_REQUIRE(glm_aligned16({x, gate_packed, up_packed, h, work}), GLM_ERR_INVALID_ARGUMENT,
               "expert_gate_up: buffers must be 16-byte aligned");
+  if (T == 0) return GLM_OK;
   return glm_gate_up_launch((hipStream_t)stream, x, T, d, I, E, top_k, gate_packed, gate_scales,
-                            up_packed, up_scales, offsets, pair_token, active, num_active,
-                            swiglu_limit, h);
+                            up_packed, up_scales, pair_token, (const int4 *)work, swiglu_limit, h);
 }
 
 extern "C" int glm_expert_down(void *stream, const uint16_t *h, int T, int top_k, int I, int d,
                                int E, const uint8_t *down_packed, const uint8_t *down_scales,
-                               const int32_t *offsets, const int32_t *active,
-                               const int32_t *num_active, uint16_t *y) {
+                               const int32_t *work, uint16_t *y) {
   glm::clear_error();
-  GLM_REQUIRE(h && down_packed && down_scales && offsets && active && num_active && y,
-              GLM_ERR_INVALID_ARGUMENT, "expert_down: null pointer argument");
+  GLM_REQUIRE(h && down_packed && down_scales && work && y, GLM_ERR_INVALID_ARGUMENT,
+              "expert_down: null pointer argument");
   GLM_REQUIRE(T >= 0 && E >= 1 && top_k >= 1, GLM_ERR_INVALID_ARGUMENT,
               "expert_down: invalid sizes");
   int rc = check_mx_geometry("expert_down", GLM_FMT_MXFP4, I, d);
   if (rc) return rc;
-  GLM_REQUIRE(glm_aligned16({h, down_packed, y}), GLM_ERR_INVALID_ARGUMENT,
+  GLM_REQUIRE(glm_aligned16({h, down_packed, y, work}), GLM_ERR_INVALID_ARGUMENT,
               "expert_down: buffers must be 16-byte aligned");
+  if (T == 0) return GLM_OK;
   return glm_down_launch((hipStream_t)stream, h, T, top_k, I, d, E, down_packed, down_scales,
-                         offsets, active, num_active, y);
+                         (const int4 *)work, y);
 }
 
 extern "C" int glm_linear(void *stream, const uint16_t *x, int T, int in_dims, const void *weight,

@@ -39,9 +39,9 @@ SIGNATURES = {
     "glm_abi_version": (_i, []),
     "glm_last_error": (ctypes.c_char_p, []),
     "glm_router_topk": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _i, _f, _p, _p, _p]),
-    "glm_moe_dispatch": (_i, [_p, _p, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p]),
-    "glm_expert_gate_up": (_i, [_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _f, _p]),
-    "glm_expert_down": (_i, [_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p]),
+    "glm_moe_dispatch": (_i, [_p, _p, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p]),
+    "glm_expert_gate_up": (_i, [_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _f, _p]),
+    "glm_expert_down": (_i, [_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _p]),
     "glm_moe_combine": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _p]),
     "glm_linear": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _p]),
     "glm_dense_mlp": (_i, [_p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _f, _p, _p]),
@@ -49,8 +49,9 @@ SIGNATURES = {
     "glm_mx_dequantize": (_i, [_p, _p, _p, _i, _i, _i, _p]),
     "glm_limited_swiglu": (_i, [_p, _p, _p, _i64, _f, _p]),
     "glm_moe_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
+    "glm_moe_workspace_init": (_i, [_p, _p, _sz]),
     "glm_moe_forward": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _i, _f, _i,
-                             _p, _p, _p, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p, _p,
+                             _p, _p, _p, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p, _p, _p,
                              _f, _p, _sz, _p, _p, _p]),
 }
 

@@ -65,6 +65,7 @@ class RoutePlan:
     pair_token: torch.Tensor   # [T*k] sorted position -> token
     active: torch.Tensor       # [E] active expert ids, ascending (-1 padded)
     num_active: torch.Tensor   # [1]
+    work: torch.Tensor         # [E, 4] per active slot: expert, first row, rows, 0
     status: torch.Tensor       # [1] 1 if an out-of-range id was seen
 
     def check(self, num_experts: int) -> None:
@@ -208,11 +209,12 @@ class HBMExpertBank:
         i32 = dict(dtype=torch.int32, device=dev)
         plan = RoutePlan(idx, torch.empty(E, **i32), torch.empty(E + 1, **i32),
                          torch.empty(P, **i32), torch.empty(P, **i32), torch.empty(P, **i32),
-                         torch.empty(E, **i32), torch.empty(1, **i32), torch.empty(1, **i32))
+                         torch.empty(E, **i32), torch.empty(1, **i32), torch.empty((E, 4), **i32),
+                         torch.empty(1, **i32))
         N.call("glm_moe_dispatch", N.stream_of(idx), idx.data_ptr(), T, k, E,
                plan.counts.data_ptr(), plan.offsets.data_ptr(), plan.perm.data_ptr(),
                plan.inv.data_ptr(), plan.pair_token.data_ptr(), plan.active.data_ptr(),
-               plan.num_active.data_ptr(), plan.status.data_ptr())
+               plan.num_active.data_ptr(), plan.work.data_ptr(), plan.status.data_ptr())
         self.last_plan = plan
         self._calls += 1
         return plan
@@ -234,12 +236,10 @@ class HBMExpertBank:
         uw, us = self.projection("up_proj")
         dw, ds = self.projection("down_proj")
         N.call("glm_expert_gate_up", stream, rows.data_ptr(), T, d, I, E, k, gw.data_ptr(),
-               gs.data_ptr(), uw.data_ptr(), us.data_ptr(), plan.offsets.data_ptr(),
-               plan.pair_token.data_ptr(), plan.active.data_ptr(), plan.num_active.data_ptr(),
-               float(self.swiglu_limit), h.data_ptr())
+               gs.data_ptr(), uw.data_ptr(), us.data_ptr(), plan.pair_token.data_ptr(),
+               plan.work.data_ptr(), float(self.swiglu_limit), h.data_ptr())
         N.call("glm_expert_down", stream, h.data_ptr(), T, k, I, d, E, dw.data_ptr(),
-               ds.data_ptr(), plan.offsets.data_ptr(), plan.active.data_ptr(),
-               plan.num_active.data_ptr(), y.data_ptr())
+               ds.data_ptr(), plan.work.data_ptr(), y.data_ptr())
         # un-permute: row of pair p lives at sorted position inv[p]
         return y.index_select(0, plan.inv.long()).reshape(T, k, d)
 

@@ -98,6 +98,7 @@ class ExpertSSDMoE:
         ws = self._workspace
         if ws is None or ws.numel() < need or ws.device != device:
             ws = torch.empty(max(need, 256), dtype=torch.uint8, device=device)
+            N.call("glm_moe_workspace_init", N.stream_of(ws), ws.data_ptr(), ws.numel())
             self._workspace = ws
         return ws
 
@@ -133,7 +134,7 @@ class ExpertSSDMoE:
                cfg.moe_intermediate_size, gw.data_ptr(), gs.data_ptr(), uw.data_ptr(),
                us.data_ptr(), dw.data_ptr(), ds.data_ptr(), shared.intermediate_size, fmt,
                sg.data_ptr(), N.ptr(shared.gate_proj.scales), su.data_ptr(),
-               N.ptr(shared.up_proj.scales), sd.data_ptr(), N.ptr(shared.down_proj.scales),
+               N.ptr(shared.up_proj.scales), sd.data_ptr(), N.ptr(shared.down_proj.scales), None,
                float(cfg.swiglu_limit), ws.data_ptr(), ws.numel(), out.data_ptr(),
                weights.data_ptr(), indices.data_ptr())
         self.last_weights = weights

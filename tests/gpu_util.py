@@ -57,14 +57,23 @@ def upload_layer(layer: dict[str, np.ndarray]) -> dict[str, torch.Tensor]:
     return {k: to_dev(v) for k, v in layer.items()}
 
 
+def workspace(nbytes: int) -> torch.Tensor:
+    """A layer workspace, initialised through the C ABI (hand-off counters at zero)."""
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    call("glm_moe_workspace_init", stream(), p(ws), nbytes)
+    return ws
+
+
 def run_layer(dl: dict[str, torch.Tensor], shape, T: int | None = None, shared: bool = True,
-              bias: torch.Tensor | None = None):
+              bias: torch.Tensor | None = None, ws: torch.Tensor | None = None,
+              shared_in: torch.Tensor | None = None):
     """glm_moe_forward on uploaded layer tensors; returns (out, weights, indices)."""
     T = dl["x"].shape[0] if T is None else T
     d, E, k, I, Is = shape.d, shape.E, shape.k, shape.I, shape.I_shared
     lib = native.load()
     ws_bytes = lib.glm_moe_workspace_bytes(T, d, E, k, I, Is if shared else 0)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    if ws is None:
+        ws = workspace(ws_bytes)
     out = torch.empty((T, d), dtype=torch.float32, device="cuda")
     w = torch.empty((T, k), dtype=torch.float32, device="cuda")
     idx = torch.empty((T, k), dtype=torch.int32, device="cuda")
@@ -74,9 +83,9 @@ def run_layer(dl: dict[str, torch.Tensor], shape, T: int | None = None, shared: 
     args += [p(dl[key]) for key in BANK_KEYS]
     if shared:
         args += [Is, native.GLM_FMT_BF16, p(dl["shared.gate"]), None, p(dl["shared.up"]), None,
-                 p(dl["shared.down"]), None]
+                 p(dl["shared.down"]), None, p(shared_in)]
     else:
-        args += [0, native.GLM_FMT_BF16, None, None, None, None, None, None]
+        args += [0, native.GLM_FMT_BF16, None, None, None, None, None, None, p(shared_in)]
     args += [shape.swiglu_limit, p(ws), ws_bytes, p(out), p(w), p(idx)]
     call("glm_moe_forward", *args)
     return out, w, idx

@@ -187,6 +187,13 @@ def test_router_reference_known_answer(gu):
     np.testing.assert_allclose(gu.host(w), [[1.25, 1.25]], atol=1e-6)
 
 
+def _work_list(counts, offsets, active, E):
+    work = np.tile(np.array([-1, 0, 0, 0], np.int32), (E, 1))
+    for u, e in enumerate(active):
+        work[u] = (e, offsets[e], counts[e], 0)
+    return work
+
+
 def _dispatch(gu, idx, E):
     torch = _torch()
     T, k = idx.shape
@@ -194,10 +201,10 @@ def _dispatch(gu, idx, E):
     i32 = dict(dtype=torch.int32, device="cuda")
     bufs = {n: torch.full((s,), -7, **i32) for n, s in
             [("counts", E), ("offsets", E + 1), ("perm", P), ("inv", P), ("pair_token", P),
-             ("active", E), ("num_active", 1), ("status", 1)]}
+             ("active", E), ("num_active", 1), ("work", 4 * E), ("status", 1)]}
     gu.call("glm_moe_dispatch", gu.stream(), gu.p(gu.to_dev(idx.astype(np.uint32))), T, k, E,
             *(gu.p(bufs[n]) for n in ("counts", "offsets", "perm", "inv", "pair_token", "active",
-                                      "num_active", "status")))
+                                      "num_active", "work", "status")))
     return {n: gu.host(t) for n, t in bufs.items()}
 
 
@@ -224,6 +231,7 @@ def test_dispatch_bit_exact(gu, T, k, E, kind):
     assert got["num_active"][0] == len(active)
     np.testing.assert_array_equal(got["active"][: len(active)], active)
     assert np.all(got["active"][len(active):] == -1)
+    np.testing.assert_array_equal(got["work"].reshape(E, 4), _work_list(counts, offsets, active, E))
     assert got["status"][0] == 0
 
 
@@ -252,17 +260,15 @@ def _expert_parity(gu, shape, seed, T=None):
     dl = gu.upload_layer({key: layer[key] for key in ("x",) + BANK_KEYS})
     P = T * k
     i32 = dict(dtype=torch.int32, device="cuda")
-    d_off = gu.to_dev(offsets)
     d_tok = gu.to_dev((perm // k).astype(np.int32))
-    d_act = gu.to_dev(np.concatenate([active, -np.ones(E - len(active), np.int32)]).astype(np.int32))
-    d_na = gu.to_dev(np.array([len(active)], np.int32))
+    d_work = gu.to_dev(_work_list(counts, offsets, active, E))
     h = torch.empty((P, I), dtype=torch.bfloat16, device="cuda")
     y = torch.empty((P, d), dtype=torch.bfloat16, device="cuda")
     gu.call("glm_expert_gate_up", gu.stream(), gu.p(dl["x"]), T, d, I, E, k,
-            *(gu.p(dl[key]) for key in BANK_KEYS[:4]), gu.p(d_off), gu.p(d_tok), gu.p(d_act),
-            gu.p(d_na), shape.swiglu_limit, gu.p(h))
+            *(gu.p(dl[key]) for key in BANK_KEYS[:4]), gu.p(d_tok), gu.p(d_work),
+            shape.swiglu_limit, gu.p(h))
     gu.call("glm_expert_down", gu.stream(), gu.p(h), T, k, I, d, E, gu.p(dl[BANK_KEYS[4]]),
-            gu.p(dl[BANK_KEYS[5]]), gu.p(d_off), gu.p(d_act), gu.p(d_na), gu.p(y))
+            gu.p(dl[BANK_KEYS[5]]), gu.p(d_work), gu.p(y))
     h_got = O.bf16_bits_to_f32(gu.bf16_bits(h))[inv].reshape(T, k, I)
     y_got = O.bf16_bits_to_f32(gu.bf16_bits(y))[inv].reshape(T, k, d)
     return h_got, inter["h"], y_got, y_want
@@ -375,3 +381,41 @@ def test_moe_layer_deterministic(gu):
     a, _, _ = gu.run_layer(dl, shape)
     b, _, _ = gu.run_layer(dl, shape)
     assert np.array_equal(gu.host(a).view(np.uint32), gu.host(b).view(np.uint32))
+
+
+def test_moe_layer_repeated_calls_share_workspace(gu):
+    # the device-side hand-off counters must return to zero after every call
+    shape = SHAPES["verify_t2"]
+    layer = make_layer(shape, 77)
+    dl = gu.upload_layer(layer)
+    lib = native.load()
+    ws = gu.workspace(lib.glm_moe_workspace_bytes(shape.T, shape.d, shape.E, shape.k, shape.I,
+                                                  shape.I_shared))
+    rng = np.random.default_rng(1)
+    for it in range(4):
+        x = O.f32_to_bf16_bits(rng.standard_normal((shape.T, shape.d)).astype(np.float32))
+        dl["x"] = gu.to_dev(x)
+        out, _, idx = gu.run_layer(dl, shape, ws=ws)
+        sub = dict(layer)
+        sub["x"] = x
+        want, inter = _oracle_layer(sub, shape)
+        assert np.array_equal(gu.host(idx).astype(np.uint32), inter["indices"]), it
+        assert O.rel_l2(gu.host(out), want) < REL_L2, it
+
+
+def test_moe_layer_with_caller_computed_shared(gu):
+    # shared expert computed separately (glm_dense_mlp, as a second stream
+    # would) and handed in: same result as the fused layer
+    torch = _torch()
+    shape = SHAPES["verify_t2"]
+    layer = make_layer(shape, 99)
+    dl = gu.upload_layer(layer)
+    T, d, Is = shape.T, shape.d, shape.I_shared
+    h = torch.empty((T, Is), dtype=torch.bfloat16, device="cuda")
+    shared = torch.empty((T, d), dtype=torch.bfloat16, device="cuda")
+    gu.call("glm_dense_mlp", gu.stream(), gu.p(dl["x"]), T, d, Is, native.GLM_FMT_BF16,
+            gu.p(dl["shared.gate"]), None, gu.p(dl["shared.up"]), None, gu.p(dl["shared.down"]),
+            None, shape.swiglu_limit, gu.p(h), gu.p(shared))
+    want, _ = _oracle_layer(layer, shape)
+    b, _, _ = gu.run_layer(dl, shape, shared=False, shared_in=shared)
+    assert O.rel_l2(gu.host(b), want) < REL_L2

@@ -65,7 +65,7 @@ def test_null_pointers_are_rejected_on_host(lib):
                   None, 4, 2, 1, 1, 1, 2.5, None, None, None)
     assert "null" in msg
     _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_moe_dispatch", None, None, 1, 2, 4, None, None,
-            None, None, None, None, None, None)
+            None, None, None, None, None, None, None)
     _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_moe_combine", None, None, None, None, None, 1,
             2, 32, None)
     _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_limited_swiglu", None, None, None, 4, 10.0,
@@ -81,7 +81,7 @@ def test_unsupported_shapes_are_rejected_on_host(lib):
     _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_mx_quantize", None, fake, 4, 64,
             native.GLM_FMT_MXFP8, 9, fake, fake)
     _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_moe_dispatch", None, fake, 1, 2, 4096, fake,
-            fake, fake, fake, fake, fake, fake, fake)
+            fake, fake, fake, fake, fake, fake, fake, fake)
     msg = _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_router_topk", None, fake, 1, 32, fake,
                   fake, 6, 2, 4, 1, 1, 2.5, fake, fake, fake)
     assert "n_group" in msg
@@ -92,7 +92,7 @@ def test_unsupported_shapes_are_rejected_on_host(lib):
 def test_moe_forward_rejects_small_workspace(lib):
     fake = ctypes.c_void_p(0x1000)
     args = [None, fake, 2, 2048, fake, fake, 128, 8, 1, 1, 1, 2.5, 768] + [fake] * 6
-    args += [768, native.GLM_FMT_BF16, fake, None, fake, None, fake, None, 10.0, fake, 1024,
-             fake, None, None]
+    args += [768, native.GLM_FMT_BF16, fake, None, fake, None, fake, None, None, 10.0, fake,
+             1024, fake, None, None]
     msg = _expect(native.GLM_ERR_WORKSPACE, "glm_moe_forward", *args)
     assert "workspace" in msg
