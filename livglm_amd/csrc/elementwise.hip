@@ -12,8 +12,10 @@ template <int KMAX>
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict__ y,
                                                       const int32_t *__restrict__ inv,
                                                       const float *__restrict__ w,
-                                                      const uint16_t *__restrict__ shared, int T,
-                                                      int k, int d, float *__restrict__ out) {
+                                                      const uint16_t *__restrict__ shared,
+                                                      const float *__restrict__ shared_parts,
+                                                      int nparts, int T, int k, int d,
+                                                      float *__restrict__ out) {
   // MLX forms the bf16*f32 products and their sum as separate f32 operations.
 #pragma clang fp contract(off)
   const int t = blockIdx.y;
@@ -52,7 +54,21 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict
       acc[3] = acc[3] + bf16_to_f32(vv.y >> 16) * wjj;
     }
   }
-  if (shared != nullptr) {
+  if (shared_parts != nullptr) {
+    // shared expert output = bf16 of its K-range partial sums added in order
+    float4 sp = *reinterpret_cast<const float4 *>(shared_parts + (long long)t * d + c);
+    for (int q = 1; q < nparts; ++q) {
+      const float4 v = *reinterpret_cast<const float4 *>(shared_parts + ((long long)q * T + t) * d + c);
+      sp.x = sp.x + v.x;
+      sp.y = sp.y + v.y;
+      sp.z = sp.z + v.z;
+      sp.w = sp.w + v.w;
+    }
+    acc[0] = acc[0] + bf16_round(sp.x);
+    acc[1] = acc[1] + bf16_round(sp.y);
+    acc[2] = acc[2] + bf16_round(sp.z);
+    acc[3] = acc[3] + bf16_round(sp.w);
+  } else if (shared != nullptr) {
     const uint2 v = *reinterpret_cast<const uint2 *>(shared + (long long)t * d + c);
     acc[0] = acc[0] + bf16_to_f32(v.x & 0xffffu);
     acc[1] = acc[1] + bf16_to_f32(v.x >> 16);
@@ -224,21 +240,27 @@ __global__ void mx_dequantize_kernel(const uint8_t *__restrict__ codes,
 
 }  // namespace glm
 
-int glm_combine_launch(hipStream_t stream, const uint16_t *y, const int32_t *inv, const float *w,
-                       const uint16_t *shared, int T, int k, int d, float *out) {
+int glm_combine_parts_launch(hipStream_t stream, const uint16_t *y, const int32_t *inv,
+                             const float *w, const uint16_t *shared, const float *shared_parts,
+                             int nparts, int T, int k, int d, float *out) {
   if (T == 0) return GLM_OK;
   dim3 grid((d / 4 + 255) / 256, T);
   if (k <= 8)
-    hipLaunchKernelGGL(glm::combine_kernel<8>, grid, dim3(256), 0, stream, y, inv, w, shared, T,
-                       k, d, out);
+    hipLaunchKernelGGL(glm::combine_kernel<8>, grid, dim3(256), 0, stream, y, inv, w, shared,
+                       shared_parts, nparts, T, k, d, out);
   else if (k <= 16)
-    hipLaunchKernelGGL(glm::combine_kernel<16>, grid, dim3(256), 0, stream, y, inv, w, shared, T,
-                       k, d, out);
+    hipLaunchKernelGGL(glm::combine_kernel<16>, grid, dim3(256), 0, stream, y, inv, w, shared,
+                       shared_parts, nparts, T, k, d, out);
   else
-    hipLaunchKernelGGL(glm::combine_kernel<0>, grid, dim3(256), 0, stream, y, inv, w, shared, T,
-                       k, d, out);
+    hipLaunchKernelGGL(glm::combine_kernel<0>, grid, dim3(256), 0, stream, y, inv, w, shared,
+                       shared_parts, nparts, T, k, d, out);
   GLM_LAUNCH_CHECK("combine_kernel");
   return GLM_OK;
+}
+
+int glm_combine_launch(hipStream_t stream, const uint16_t *y, const int32_t *inv, const float *w,
+                       const uint16_t *shared, int T, int k, int d, float *out) {
+  return glm_combine_parts_launch(stream, y, inv, w, shared, nullptr, 0, T, k, d, out);
 }
 
 static int grid_for(long long n, int block) {

@@ -341,66 +341,99 @@ struct GateUpArgs {
   long long w_stride, s_stride;
   int I, d;
   uint16_t *h;  // [P][I]
-  const uint8_t *sg, *su;  // shared bf16 gate/up [Is][d] (nullptr: none)
-  int Is, T;
-  uint16_t *hs;  // [T][Is]
+  // shared expert: bf16 gate/up [Is][d] split into skq K ranges of d/skq
+  const uint8_t *sg, *su;
+  int Is, T, skq, shared_blocks;
+  float *gp, *up;  // skq > 1: per-range partial sums [skq][T][Is]
+  uint16_t *hs;    // skq == 1: shared activations [T][Is]
   float limit;
 };
 
-template <int CPW, bool SHARED>
+// Linear grid: blocks [0, shared_blocks) are shared-expert tiles (16 rows x
+// d/skq, one 128-wide chunk per wave -- about the bytes of a routed tile, and
+// scheduled first); the rest are routed tiles (work slot, 16 rows, full d).
+template <int CPW>
 __global__ __launch_bounds__(256) void decode_gate_up_kernel(GateUpArgs a) {
   __shared__ glm_f32x4 red[4 * 2 * 64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int row0 = blockIdx.x * 16;
-  const int kbase = wave * CPW * 128;
   const int d = a.d;
-  // the shared expert is grid row 0, so its tiles start with the first wave of
-  // blocks instead of trailing after every routed tile
-  const bool shared = SHARED && blockIdx.y == 0;
-  int e = 0, base = 0, n = a.T, N = a.Is;
-  if (!shared) {
-    const int4 wk = a.work[blockIdx.y - (SHARED ? 1 : 0)];
-    e = wk.x;
-    base = wk.y;
-    n = wk.z;
-    N = a.I;
+  int b = blockIdx.x;
+  if (b < a.shared_blocks) {
+    const uint8_t *srow[2] = {nullptr, nullptr};
+    if (a.skq > 1) {
+      // few tokens: split K over skq blocks, write f32 partial sums
+      const int row0 = (b / a.skq) * 16;
+      const int kq = b % a.skq;
+      const int kbase = kq * (d / a.skq) + wave * 128;
+      const uint8_t *wrow[2] = {a.sg + (size_t)(row0 + r) * d * 2, a.su + (size_t)(row0 + r) * d * 2};
+      for (int p0 = 0; p0 < a.T; p0 += 16) {
+        const int t = p0 + r;
+        const uint16_t *act = t < a.T ? a.x + (size_t)t * d : nullptr;
+        glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
+        wave_mma<FMT_BF16, 2, 1>(wrow, srow, kbase, q, act, acc);
+        if (ksplit_reduce<2>(acc, red, wave, 4, lane) && t < a.T) {
+          const size_t o = ((size_t)kq * a.T + t) * a.Is + row0 + 4 * q;
+          *reinterpret_cast<glm_f32x4 *>(a.gp + o) = acc[0];
+          *reinterpret_cast<glm_f32x4 *>(a.up + o) = acc[1];
+        }
+      }
+    } else {
+      // more tokens: full-K tiles, SwiGLU applied here, bf16 activations out
+      const int row0 = b * 16;
+      const int kbase = wave * CPW * 128;
+      const uint8_t *wrow[2] = {a.sg + (size_t)(row0 + r) * d * 2, a.su + (size_t)(row0 + r) * d * 2};
+      for (int p0 = 0; p0 < a.T; p0 += 16) {
+        const int t = p0 + r;
+        const uint16_t *act = t < a.T ? a.x + (size_t)t * d : nullptr;
+        glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
+        wave_mma<FMT_BF16, 2, CPW>(wrow, srow, kbase, q, act, acc);
+        if (ksplit_reduce<2>(acc, red, wave, 4, lane) && t < a.T) {
+          uint32_t o[4];
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+            o[m] = f32_to_bf16(limited_swiglu(bf16_round(acc[0][m]), bf16_round(acc[1][m]), a.limit));
+          store_rows4(a.hs + (size_t)t * a.Is + row0 + 4 * q, o);
+        }
+      }
+    }
+    return;
   }
-  if (e < 0 || n <= 0 || row0 >= N) return;
-
+  b -= a.shared_blocks;
+  const int tiles = a.I / 16;
+  const int4 wk = a.work[b / tiles];
+  const int row0 = (b % tiles) * 16;
+  const int e = wk.x, base = wk.y, n = wk.z;
+  if (e < 0 || n <= 0) return;
+  const int kbase = wave * CPW * 128;
   for (int p0 = 0; p0 < n; p0 += 16) {
     const int pair = p0 + r;
     glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
-    if (!shared) {
-      const uint8_t *wrow[2] = {a.gw + e * a.w_stride + (size_t)(row0 + r) * (d / 2),
-                                a.uw + e * a.w_stride + (size_t)(row0 + r) * (d / 2)};
-      const uint8_t *srow[2] = {a.gs + e * a.s_stride + (size_t)(row0 + r) * (d / 32),
-                                a.us + e * a.s_stride + (size_t)(row0 + r) * (d / 32)};
-      // weight stream first; the token lookup overlaps with it
-      WaveWeights<FMT_MXFP4, 2, CPW> ww;
-      load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
-      const uint16_t *act = pair < n ? a.x + (size_t)a.pair_token[base + pair] * d : nullptr;
-      mma_wave_weights<FMT_MXFP4, 2, CPW>(ww, kbase, q, act, acc);
-    } else if constexpr (SHARED) {
-      const uint16_t *act = pair < n ? a.x + (size_t)pair * d : nullptr;
-      const uint8_t *wrow[2] = {a.sg + (size_t)(row0 + r) * d * 2, a.su + (size_t)(row0 + r) * d * 2};
-      const uint8_t *srow[2] = {nullptr, nullptr};
-      wave_mma<FMT_BF16, 2, CPW>(wrow, srow, kbase, q, act, acc);
-    }
+    const uint8_t *wrow[2] = {a.gw + e * a.w_stride + (size_t)(row0 + r) * (d / 2),
+                              a.uw + e * a.w_stride + (size_t)(row0 + r) * (d / 2)};
+    const uint8_t *srow[2] = {a.gs + e * a.s_stride + (size_t)(row0 + r) * (d / 32),
+                              a.us + e * a.s_stride + (size_t)(row0 + r) * (d / 32)};
+    // weight stream first; the token lookup overlaps with it
+    WaveWeights<FMT_MXFP4, 2, CPW> ww;
+    load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
+    const uint16_t *act = pair < n ? a.x + (size_t)a.pair_token[base + pair] * d : nullptr;
+    mma_wave_weights<FMT_MXFP4, 2, CPW>(ww, kbase, q, act, acc);
     if (ksplit_reduce<2>(acc, red, wave, 4, lane) && pair < n) {
       uint32_t o[4];
 #pragma unroll
       for (int m = 0; m < 4; ++m)
         o[m] = f32_to_bf16(limited_swiglu(bf16_round(acc[0][m]), bf16_round(acc[1][m]), a.limit));
-      uint16_t *dst = shared ? a.hs + (size_t)pair * N : a.h + (size_t)(base + pair) * N;
-      store_rows4(dst + row0 + 4 * q, o);
+      store_rows4(a.h + (size_t)(base + pair) * a.I + row0 + 4 * q, o);
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Down: grid (d/64 row tiles, slots [+ 1 shared]).  Each wave owns 16 output
-// rows over the full K = I.
+// Down.  Linear grid: blocks [0, shared_blocks) are shared-expert tiles (64
+// rows x Is/skd, CPW_S chunks per wave) whose activations are rebuilt in LDS
+// from the gate/up partials (fixed-order sum, bf16, SwiGLU); the rest are
+// routed tiles (work slot, 64 rows, full I).  Shared tiles write f32 partial
+// sums [skd][T][d] that the combine adds in order.
 // ---------------------------------------------------------------------------
 struct DownArgs {
   const uint16_t *h;
@@ -410,51 +443,74 @@ struct DownArgs {
   long long w_stride, s_stride;
   int I, d;
   uint16_t *y;  // [P][d]
-  const uint16_t *hs;  // [T][Is]
-  const uint8_t *sd;   // shared bf16 down [d][Is] (nullptr: none)
-  int Is, T;
-  uint16_t *ys;  // [T][d]
+  const uint8_t *sd;  // shared bf16 down [d][Is]
+  const float *gp, *up;  // skq > 1: gate/up partial sums
+  const uint16_t *hs;    // skq == 1: shared activations [T][Is]
+  int Is, T, skq, skd, shared_blocks;
+  float limit;
+  float *yp;  // [skd][T][d]
 };
 
 template <int CPW_R, int CPW_S>
 __global__ __launch_bounds__(256) void decode_down_kernel(DownArgs a) {
+  extern __shared__ uint16_t s_h[];  // [T][CPW_S * 128] shared-expert activations
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int tile = blockIdx.x;
-  const int row0 = tile * 64 + wave * 16;
   const int d = a.d;
-  const bool shared = a.sd != nullptr && blockIdx.y == 0;  // shared expert: grid row 0
-  int e = 0, base = 0, n = a.T;
-  if (!shared) {
-    const int4 wk = a.work[blockIdx.y - (a.sd != nullptr ? 1 : 0)];
-    e = wk.x;
-    base = wk.y;
-    n = wk.z;
-    if (e < 0 || n <= 0) return;
+  int b = blockIdx.x;
+  if (b < a.shared_blocks) {
+    constexpr int KS = CPW_S * 128;
+    const int tile = b / a.skd, kd = b % a.skd;
+    const int row0 = tile * 64 + wave * 16;
+    const int kbase = kd * KS;
+    if (a.skq > 1) {
+      // rebuild this K range of the shared activations from the gate/up partials
+      for (int i = threadIdx.x; i < a.T * KS; i += 256) {
+        const int t = i / KS, kk = kbase + i % KS;
+        float g = 0.0f, u = 0.0f;
+        for (int qq = 0; qq < a.skq; ++qq) {
+          g += a.gp[((size_t)qq * a.T + t) * a.Is + kk];
+          u += a.up[((size_t)qq * a.T + t) * a.Is + kk];
+        }
+        s_h[i] = (uint16_t)f32_to_bf16(limited_swiglu(bf16_round(g), bf16_round(u), a.limit));
+      }
+      __syncthreads();
+    }
+    const uint8_t *wrow[1] = {a.sd + ((size_t)(row0 + r) * a.Is + kbase) * 2};
+    const uint8_t *srow[1] = {nullptr};
+    for (int p0 = 0; p0 < a.T; p0 += 16) {
+      const int t = p0 + r;
+      glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
+      const uint16_t *act = t >= a.T ? nullptr
+                            : (a.skq > 1 ? s_h + (size_t)t * KS : a.hs + (size_t)t * a.Is + kbase);
+      wave_mma<FMT_BF16, 1, CPW_S>(wrow, srow, 0, q, act, acc);
+      if (t < a.T)
+        *reinterpret_cast<glm_f32x4 *>(a.yp + ((size_t)kd * a.T + t) * d + row0 + 4 * q) = acc[0];
+    }
+    return;
   }
+  b -= a.shared_blocks;
+  const int tiles = d / 64;
+  const int4 wk = a.work[b / tiles];
+  const int row0 = (b % tiles) * 64 + wave * 16;
+  const int e = wk.x, base = wk.y, n = wk.z;
+  if (e < 0 || n <= 0) return;
   for (int p0 = 0; p0 < n; p0 += 16) {
     const int pair = p0 + r;
     glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
-    if (!shared) {
-      const uint16_t *act = pair < n ? a.h + (size_t)(base + pair) * a.I : nullptr;
-      const uint8_t *wrow[1] = {a.dw + e * a.w_stride + (size_t)(row0 + r) * (a.I / 2)};
-      const uint8_t *srow[1] = {a.ds + e * a.s_stride + (size_t)(row0 + r) * (a.I / 32)};
-      wave_mma<FMT_MXFP4, 1, CPW_R>(wrow, srow, 0, q, act, acc);
-    } else {
-      const uint16_t *act = pair < n ? a.hs + (size_t)pair * a.Is : nullptr;
-      const uint8_t *wrow[1] = {reinterpret_cast<const uint8_t *>(a.sd) + (size_t)(row0 + r) * a.Is * 2};
-      const uint8_t *srow[1] = {nullptr};
-      wave_mma<FMT_BF16, 1, CPW_S>(wrow, srow, 0, q, act, acc);
-    }
+    const uint8_t *wrow[1] = {a.dw + e * a.w_stride + (size_t)(row0 + r) * (a.I / 2)};
+    const uint8_t *srow[1] = {a.ds + e * a.s_stride + (size_t)(row0 + r) * (a.I / 32)};
+    WaveWeights<FMT_MXFP4, 1, CPW_R> ww;
+    load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
+    const uint16_t *act = pair < n ? a.h + (size_t)(base + pair) * a.I : nullptr;
+    mma_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, 0, q, act, acc);
     if (pair < n) {
       uint32_t o[4];
 #pragma unroll
       for (int m = 0; m < 4; ++m) o[m] = f32_to_bf16(acc[0][m]);
-      uint16_t *dst = shared ? a.ys + (size_t)pair * d : a.y + (size_t)(base + pair) * d;
-      store_rows4(dst + row0 + 4 * q, o);
+      store_rows4(a.y + (size_t)(base + pair) * d + row0 + 4 * q, o);
     }
   }
-
 }
 
 // zero-fill (workspace initialisation)
@@ -485,7 +541,7 @@ bool glm_decode_down_supported(int I, int d) {
 }
 
 bool glm_decode_path_supported(int T, int d, int E, int k, int I, int Is) {
-  if (T < 1 || (long long)T * k > kMaxFusedPairs || E > kFusedMaxE) return false;
+  if (T < 1 || T > 64 || (long long)T * k > kMaxFusedPairs || E > kFusedMaxE) return false;
   // gate/up: 4 waves x CPW chunks of 128 over d; down: 64-row tiles of d
   if (d % 512 != 0 || !chunk_count_ok(d / 512) || d / 512 < 2) return false;
   if (I % 128 != 0 || !chunk_count_ok(I / 128)) return false;
@@ -521,11 +577,17 @@ int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d,
   return GLM_OK;
 }
 
+// Shared-expert K split of the decode kernels: gate/up uses d/512 ranges (one
+// 128-wide chunk per wave); down uses ranges of 2 chunks (1 if Is == 128).
+int glm_decode_shared_skq(int T, int d) { return T <= 8 ? d / 512 : 1; }
+int glm_decode_shared_cpws(int Is) { return Is / 128 == 1 ? 1 : 2; }
+int glm_decode_shared_skd(int Is) { return Is / 128 / glm_decode_shared_cpws(Is); }
+
 int glm_decode_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int E,
                               int k, const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
                               const uint8_t *us, const int32_t *pair_token, const int4 *work,
                               const uint16_t *sg, const uint16_t *su, int Is, uint16_t *h,
-                              uint16_t *hs, float limit) {
+                              float *gp, float *up, uint16_t *hs, float limit) {
   GateUpArgs a{};
   a.x = x;
   a.pair_token = pair_token;
@@ -544,44 +606,37 @@ int glm_decode_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int 
   a.su = reinterpret_cast<const uint8_t *>(su);
   a.Is = sg ? Is : 0;
   a.T = T;
+  a.skq = glm_decode_shared_skq(T, d);
+  a.shared_blocks = sg ? (Is / 16) * a.skq : 0;
+  a.gp = gp;
+  a.up = up;
   a.hs = hs;
   a.limit = glm_limit_bf16(limit);
-  const int rows = std::max(I, a.Is);
-  const bool with_shared = a.Is > 0;
-  dim3 grid(rows / 16, a.slots + (with_shared ? 1 : 0));
+  const int blocks = a.shared_blocks + a.slots * (I / 16);
   const int cpw = d / 512;
-#define GLM_GU(C)                                                                          \
-  if (with_shared)                                                                          \
-    hipLaunchKernelGGL((decode_gate_up_kernel<C, true>), grid, dim3(256), 0, stream, a);   \
-  else                                                                                      \
-    hipLaunchKernelGGL((decode_gate_up_kernel<C, false>), grid, dim3(256), 0, stream, a)
   switch (cpw) {
-    case 2: GLM_GU(2); break;
-    case 4: GLM_GU(4); break;
-    case 6: GLM_GU(6); break;
-    case 8: GLM_GU(8); break;
+    case 2: hipLaunchKernelGGL(decode_gate_up_kernel<2>, dim3(blocks), dim3(256), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL(decode_gate_up_kernel<4>, dim3(blocks), dim3(256), 0, stream, a); break;
+    case 6: hipLaunchKernelGGL(decode_gate_up_kernel<6>, dim3(blocks), dim3(256), 0, stream, a); break;
+    case 8: hipLaunchKernelGGL(decode_gate_up_kernel<8>, dim3(blocks), dim3(256), 0, stream, a); break;
     default: glm::set_error("decode gate/up: unsupported d=%d", d); return GLM_ERR_UNSUPPORTED_SHAPE;
   }
-#undef GLM_GU
   GLM_LAUNCH_CHECK("decode_gate_up_kernel");
   return GLM_OK;
 }
 
 template <int CR>
-static void launch_down_cs(hipStream_t stream, dim3 grid, const DownArgs &a, int cs) {
-  switch (cs) {
-    case 1: hipLaunchKernelGGL((decode_down_kernel<CR, 1>), grid, dim3(256), 0, stream, a); break;
-    case 2: hipLaunchKernelGGL((decode_down_kernel<CR, 2>), grid, dim3(256), 0, stream, a); break;
-    case 4: hipLaunchKernelGGL((decode_down_kernel<CR, 4>), grid, dim3(256), 0, stream, a); break;
-    case 6: hipLaunchKernelGGL((decode_down_kernel<CR, 6>), grid, dim3(256), 0, stream, a); break;
-    default: hipLaunchKernelGGL((decode_down_kernel<CR, 8>), grid, dim3(256), 0, stream, a); break;
-  }
+static void launch_down_cs(hipStream_t stream, int blocks, size_t lds, const DownArgs &a, int cs) {
+  if (cs == 1)
+    hipLaunchKernelGGL((decode_down_kernel<CR, 1>), dim3(blocks), dim3(256), lds, stream, a);
+  else
+    hipLaunchKernelGGL((decode_down_kernel<CR, 2>), dim3(blocks), dim3(256), lds, stream, a);
 }
 
 int glm_decode_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, int d,
                            int E, const uint8_t *dw, const uint8_t *ds, const int4 *work,
-                           const uint16_t *hs, const uint16_t *sd, int Is, uint16_t *y,
-                           uint16_t *ys) {
+                           const uint16_t *sd, const float *gp, const float *up,
+                           const uint16_t *hs, int Is, float limit, uint16_t *y, float *yp) {
   DownArgs a{};
   a.h = h;
   a.work = work;
@@ -593,24 +648,26 @@ int glm_decode_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, 
   a.I = I;
   a.d = d;
   a.y = y;
-  a.hs = hs;
   a.sd = reinterpret_cast<const uint8_t *>(sd);
+  a.gp = gp;
+  a.up = up;
+  a.hs = hs;
   a.Is = sd ? Is : 0;
   a.T = T;
-  a.ys = ys;
-  dim3 grid(d / 64, a.slots + (sd ? 1 : 0));
-  const int cr = I / 128;
-  const int cs = sd ? Is / 128 : 1;
-  if (cs != 1 && cs != 2 && cs != 4 && cs != 6 && cs != 8) {
-    glm::set_error("decode down: unsupported I_shared=%d", Is);
-    return GLM_ERR_UNSUPPORTED_SHAPE;
-  }
-  switch (cr) {
-    case 1: launch_down_cs<1>(stream, grid, a, cs); break;
-    case 2: launch_down_cs<2>(stream, grid, a, cs); break;
-    case 4: launch_down_cs<4>(stream, grid, a, cs); break;
-    case 6: launch_down_cs<6>(stream, grid, a, cs); break;
-    case 8: launch_down_cs<8>(stream, grid, a, cs); break;
+  a.skq = glm_decode_shared_skq(T, d);
+  const int cs = sd ? glm_decode_shared_cpws(Is) : 1;
+  a.skd = sd ? glm_decode_shared_skd(Is) : 1;
+  a.shared_blocks = sd ? (d / 64) * a.skd : 0;
+  a.limit = glm_limit_bf16(limit);
+  a.yp = yp;
+  const int blocks = a.shared_blocks + a.slots * (d / 64);
+  const size_t lds = sd && a.skq > 1 ? (size_t)T * cs * 128 * 2 : 0;
+  switch (I / 128) {
+    case 1: launch_down_cs<1>(stream, blocks, lds, a, cs); break;
+    case 2: launch_down_cs<2>(stream, blocks, lds, a, cs); break;
+    case 4: launch_down_cs<4>(stream, blocks, lds, a, cs); break;
+    case 6: launch_down_cs<6>(stream, blocks, lds, a, cs); break;
+    case 8: launch_down_cs<8>(stream, blocks, lds, a, cs); break;
     default: glm::set_error("decode down: unsupported I=%d", I); return GLM_ERR_UNSUPPORTED_SHAPE;
   }
   GLM_LAUNCH_CHECK("decode_down_kernel");

@@ -60,11 +60,16 @@ int glm_decode_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int 
                               int k, const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
                               const uint8_t *us, const int32_t *pair_token, const int4 *work,
                               const uint16_t *sg, const uint16_t *su, int Is, uint16_t *h,
-                              uint16_t *hs, float limit);
+                              float *gp, float *up, uint16_t *hs, float limit);
 int glm_decode_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, int d,
                            int E, const uint8_t *dw, const uint8_t *ds, const int4 *work,
-                           const uint16_t *hs, const uint16_t *sd, int Is, uint16_t *y,
-                           uint16_t *ys);
+                           const uint16_t *sd, const float *gp, const float *up,
+                           const uint16_t *hs, int Is, float limit, uint16_t *y, float *yp);
+int glm_combine_parts_launch(hipStream_t stream, const uint16_t *y, const int32_t *inv,
+                             const float *w, const uint16_t *shared, const float *shared_parts,
+                             int nparts, int T, int k, int d, float *out);
+int glm_decode_shared_skq(int T, int d);
+int glm_decode_shared_skd(int Is);
 int glm_fill_zero_launch(hipStream_t stream, void *p, size_t bytes);
 
 // ---------------------------------------------------------------- workspace
@@ -92,6 +97,8 @@ struct Workspace {
   uint16_t *shared_h;
   uint16_t *shared_out;
   int4 *work;
+  float *gp, *up;  // decode shared-expert gate/up partials [skq][T][Is]
+  float *yp;       // decode shared-expert down partials [skd][T][d]
   size_t bytes;
 };
 
@@ -121,6 +128,12 @@ Workspace carve(char *base, int T, int d, int E, int k, int I, int Is) {
   w.shared_h = (uint16_t *)take((size_t)T * (Is > 0 ? Is : 0) * 2);
   w.shared_out = (uint16_t *)take((size_t)T * (Is > 0 ? d : 0) * 2);
   w.work = (int4 *)take((size_t)E * sizeof(int4));
+  const size_t tis = (size_t)T * (Is > 0 ? Is : 0) * 4;
+  const int skq = d % 512 == 0 ? d / 512 : 1;
+  const int skd = Is >= 128 ? Is / 128 : 1;  // bound on the down K split
+  w.gp = (float *)take(tis * skq);
+  w.up = (float *)take(tis * skq);
+  w.yp = (float *)take((size_t)T * (Is > 0 ? d : 0) * 4 * skd);
   w.bytes = off;
   return w;
 }
@@ -204,15 +217,16 @@ extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
                                    up_packed, up_scales, w.pair_token, w.work,
                                    fuse_shared ? (const uint16_t *)shared_gate : nullptr,
                                    fuse_shared ? (const uint16_t *)shared_up : nullptr, Is, w.h,
-                                   w.shared_h, swiglu_limit);
+                                   w.gp, w.up, w.shared_h, swiglu_limit);
     if (rc) return rc;
     rc = glm_decode_down_launch(stream, w.h, T, top_k, I, d, E, down_packed, down_scales, w.work,
-                                w.shared_h,
-                                fuse_shared ? (const uint16_t *)shared_down : nullptr, Is, w.y,
-                                w.shared_out);
+                                fuse_shared ? (const uint16_t *)shared_down : nullptr, w.gp, w.up,
+                                w.shared_h, Is, swiglu_limit, w.y, w.yp);
     if (rc) return rc;
-    if (fuse_shared) shared_ready = w.shared_out;
-    else if (has_shared && !shared_in) {
+    if (fuse_shared)
+      return glm_combine_parts_launch(stream, w.y, w.inv, wts, nullptr, w.yp,
+                                      glm_decode_shared_skd(Is), T, top_k, d, out);
+    if (has_shared && !shared_in) {
       rc = glm_mlp_launch(stream, x, T, d, I_shared, shared_fmt, shared_gate, shared_gate_scales,
                           shared_up, shared_up_scales, shared_down, shared_down_scales,
                           swiglu_limit, w.shared_h, w.shared_out);
