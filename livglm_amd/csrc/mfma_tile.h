@@ -139,6 +139,54 @@ __device__ __forceinline__ void mma_wave_weights(const WaveWeights<FMT, NPROJ, C
   }
 }
 
+// As mma_wave_weights, with the activation rows staged in LDS: s_row is this
+// lane's token row there (nullptr: padding column).  B fragments are read per
+// chunk with ds_read_b128, so registers stay free for the weight stream.
+template <int FMT, int NPROJ, int CPW>
+__device__ __forceinline__ void mma_wave_weights_lds(const WaveWeights<FMT, NPROJ, CPW> &ww,
+                                                     int kbase, int q, const uint16_t *s_row,
+                                                     glm_f32x4 acc[NPROJ]) {
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    glm_bf16x8 xb[4];
+    if (s_row != nullptr) {
+      const glm_bf16x8 *src =
+          reinterpret_cast<const glm_bf16x8 *>(s_row + kbase + c * 128 + 32 * q);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xb[i] = src[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xb[i] = glm_bf16x8{};
+    }
+#pragma unroll
+    for (int p = 0; p < NPROJ; ++p) {
+      glm_bf16x8 a[4];
+      chunk_frags<FMT>(ww.w[p][c], (ww.sd[p][c] >> (8 * q)) & 0xffu, a);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], xb[i], acc[p], 0, 0, 0);
+    }
+  }
+}
+
+// LDS row stride (bf16 elements) for staged activation rows of length K: the
+// 16-byte pad spreads the rows of one MFMA B fragment over distinct banks.
+__host__ __device__ constexpr int lds_row_stride(int K) { return K + 8; }
+
+// Block-cooperative copy of `rows` activation rows of length K (bf16, K % 8
+// == 0) into LDS: row j comes from src + index(j) * K, where index(j) =
+// row_index[j] if row_index is given, else j.
+__device__ __forceinline__ void stage_rows(uint16_t *s_x, const uint16_t *src,
+                                           const int32_t *row_index, int rows, int K) {
+  const int per_row = K / 8;
+  for (int i = threadIdx.x; i < rows * per_row; i += blockDim.x) {
+    const int j = i / per_row, c8 = i % per_row;
+    const long long srow = row_index != nullptr ? row_index[j] : j;
+    *reinterpret_cast<glm_u32x4 *>(s_x + j * lds_row_stride(K) + c8 * 8) =
+        *reinterpret_cast<const glm_u32x4 *>(src + srow * K + c8 * 8);
+  }
+}
+
 // Accumulates, over chunks [kbase/128, kbase/128 + CPW), the 16-row tile of
 // NPROJ weight matrices against one activation row per lane column.
 // wrow/srow: this lane's weight/scale row; act: this lane's activation row
@@ -182,20 +230,22 @@ __device__ __forceinline__ void wave_mma(const uint8_t *const wrow[NPROJ],
 }
 
 // Sums the K-split partials of `nwaves` waves in fixed wave order through LDS
-// (red: nwaves * NPROJ * 64 float4).  Returns true on the wave that holds the
+// (red: (nwaves - 1) * NPROJ * 64 float4; wave 0 keeps its own in registers).  Returns true on the wave that holds the
 // total (wave 0); the block must call it uniformly.
 template <int NPROJ>
 __device__ __forceinline__ bool ksplit_reduce(glm_f32x4 acc[NPROJ], glm_f32x4 *red, int wave,
                                               int nwaves, int lane) {
   if (nwaves == 1) return true;
+  if (wave > 0) {
 #pragma unroll
-  for (int p = 0; p < NPROJ; ++p) red[(wave * NPROJ + p) * 64 + lane] = acc[p];
+    for (int p = 0; p < NPROJ; ++p) red[((wave - 1) * NPROJ + p) * 64 + lane] = acc[p];
+  }
   __syncthreads();
   if (wave == 0) {
 #pragma unroll
     for (int p = 0; p < NPROJ; ++p) {
-      glm_f32x4 s = red[p * 64 + lane];
-      for (int w = 1; w < nwaves; ++w) s += red[(w * NPROJ + p) * 64 + lane];
+      glm_f32x4 s = acc[p];
+      for (int w = 1; w < nwaves; ++w) s += red[((w - 1) * NPROJ + p) * 64 + lane];
       acc[p] = s;
     }
   }

@@ -1,15 +1,16 @@
-// Decode-size routed-MoE layer (T*k <= 512 pairs) in five short kernels:
+// Decode-size routed-MoE layer (T <= 64, T*k <= 512 pairs) in five kernels:
 //
-//   1. route_logits_kernel    router logits, one block per expert (4 waves
-//                             split d), all tokens.
-//   2. select_dispatch_kernel one block: top-k selection of every token
+//   1. route_logits_kernel    router logits (one block per expert, 4 waves
+//                             split d) -- and, in extra blocks, the bf16
+//                             shared expert's gate/up tiles, which do not
+//                             depend on routing and so overlap with it.
+//   2. select_dispatch_kernel block 0: top-k selection of every token
 //                             (moe.py:39-62) and the dispatch -- histogram,
 //                             exclusive scan, stable permute, work list -- in
-//                             LDS.
-//   3. decode_gate_up_kernel  routed MXFP4 gate/up + SwiGLU, one grid row per
-//                             active expert slot (plus, optionally, one row of
-//                             bf16 shared-expert tiles).
-//   4. decode_down_kernel     routed MXFP4 down (plus optional shared down).
+//                             LDS; extra blocks: the shared expert's down tiles.
+//   3. decode_gate_up_kernel  routed MXFP4 gate/up + SwiGLU, one group of
+//                             tiles per active expert slot.
+//   4. decode_down_kernel     routed MXFP4 down.
 //   5. combine_kernel         weighted top-k merge + shared add.
 //
 // Every kernel boundary is a stream-ordered dependency; nothing synchronises
@@ -21,6 +22,7 @@ namespace glm {
 constexpr int kRouteThreads = 256;
 constexpr int kMaxFusedPairs = 512;  // T*k handled by the fused route kernel
 constexpr int kFusedMaxE = 448;
+constexpr int kStageTokens = 8;  // activation rows per LDS staging batch
 
 struct RouteArgs {
   const uint16_t *x;
@@ -194,14 +196,113 @@ __device__ __forceinline__ int scan256(int v, int *s_tmp, int *total) {
   return base + incl - v;
 }
 
+// The bf16 shared expert (DenseMLP, layers.py:160-171) as tiles that ride in
+// the routing kernels.  Gate/up tiles are 16 rows; with few tokens (skq > 1)
+// their K range is split over skq tiles that write f32 partial sums, which the
+// down tiles add in order and turn into bf16 SwiGLU activations in LDS;
+// otherwise gate/up tiles cover all of d and write bf16 activations.  Down
+// tiles are 64 rows x Is/skd and write f32 partial sums [skd][T][d] that the
+// combine adds in order (all partial sums are exact f32 reductions of
+// disjoint K ranges, so the result is the f32 dot product rounded once).
+struct SharedArgs {
+  const uint16_t *x;
+  const uint8_t *sg, *su, *sd;  // bf16 gate/up [Is][d], down [d][Is] (sg == nullptr: none)
+  int T, d, Is, skq, skd, gu_blocks, dn_blocks;
+  float *gp, *up;  // skq > 1: gate/up partial sums [skq][T][Is]
+  uint16_t *hs;    // skq == 1: activations [T][Is]
+  float *yp;       // down partial sums [skd][T][d]
+  float limit;
+};
+
+template <int CPW>
+__device__ void shared_gate_up_tile(const SharedArgs &a, int b, glm_f32x4 *red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int d = a.d;
+  const uint8_t *srow[2] = {nullptr, nullptr};
+  if (a.skq > 1) {
+    const int row0 = (b / a.skq) * 16;
+    const int kq = b % a.skq;
+    const int kbase = kq * (d / a.skq) + wave * 128;
+    const uint8_t *wrow[2] = {a.sg + (size_t)(row0 + r) * d * 2, a.su + (size_t)(row0 + r) * d * 2};
+    for (int p0 = 0; p0 < a.T; p0 += 16) {
+      const int t = p0 + r;
+      const uint16_t *act = t < a.T ? a.x + (size_t)t * d : nullptr;
+      glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
+      wave_mma<FMT_BF16, 2, 1>(wrow, srow, kbase, q, act, acc);
+      if (ksplit_reduce<2>(acc, red, wave, 4, lane) && t < a.T) {
+        const size_t o = ((size_t)kq * a.T + t) * a.Is + row0 + 4 * q;
+        *reinterpret_cast<glm_f32x4 *>(a.gp + o) = acc[0];
+        *reinterpret_cast<glm_f32x4 *>(a.up + o) = acc[1];
+      }
+    }
+  } else {
+    const int row0 = b * 16;
+    const int kbase = wave * CPW * 128;
+    const uint8_t *wrow[2] = {a.sg + (size_t)(row0 + r) * d * 2, a.su + (size_t)(row0 + r) * d * 2};
+    for (int p0 = 0; p0 < a.T; p0 += 16) {
+      const int t = p0 + r;
+      const uint16_t *act = t < a.T ? a.x + (size_t)t * d : nullptr;
+      glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
+      wave_mma<FMT_BF16, 2, CPW>(wrow, srow, kbase, q, act, acc);
+      if (ksplit_reduce<2>(acc, red, wave, 4, lane) && t < a.T) {
+        uint32_t o[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          o[m] = f32_to_bf16(limited_swiglu(bf16_round(acc[0][m]), bf16_round(acc[1][m]), a.limit));
+        store_rows4(a.hs + (size_t)t * a.Is + row0 + 4 * q, o);
+      }
+    }
+  }
+}
+
+template <int CPW_S>
+__device__ void shared_down_tile(const SharedArgs &a, int b, uint16_t *s_h) {
+  constexpr int KS = CPW_S * 128;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int d = a.d;
+  const int tile = b / a.skd, kd = b % a.skd;
+  const int row0 = tile * 64 + wave * 16;
+  const int kbase = kd * KS;
+  if (a.skq > 1) {
+    for (int i = threadIdx.x; i < a.T * KS; i += 256) {
+      const int t = i / KS, kk = kbase + i % KS;
+      float g = 0.0f, u = 0.0f;
+      for (int qq = 0; qq < a.skq; ++qq) {
+        g += a.gp[((size_t)qq * a.T + t) * a.Is + kk];
+        u += a.up[((size_t)qq * a.T + t) * a.Is + kk];
+      }
+      s_h[i] = (uint16_t)f32_to_bf16(limited_swiglu(bf16_round(g), bf16_round(u), a.limit));
+    }
+    __syncthreads();
+  }
+  const uint8_t *wrow[1] = {a.sd + ((size_t)(row0 + r) * a.Is + kbase) * 2};
+  const uint8_t *srow[1] = {nullptr};
+  for (int p0 = 0; p0 < a.T; p0 += 16) {
+    const int t = p0 + r;
+    glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
+    const uint16_t *act = t >= a.T ? nullptr
+                          : (a.skq > 1 ? s_h + (size_t)t * KS : a.hs + (size_t)t * a.Is + kbase);
+    wave_mma<FMT_BF16, 1, CPW_S>(wrow, srow, 0, q, act, acc);
+    if (t < a.T)
+      *reinterpret_cast<glm_f32x4 *>(a.yp + ((size_t)kd * a.T + t) * d + row0 + 4 * q) = acc[0];
+  }
+}
+
 // logits[t][e] = f32(x[t]) . w[e] for all tokens; block = expert e, wave w
 // sums the K range [w*d/4, (w+1)*d/4), partials added in wave order.
-template <int TT>
-__global__ __launch_bounds__(kRouteThreads) void route_logits_kernel(RouteArgs a) {
+template <int TT, int CPW>
+__global__ __launch_bounds__(kRouteThreads) void route_logits_kernel(RouteArgs a, SharedArgs sh) {
   __shared__ float s_part[4][TT];
+  __shared__ glm_f32x4 red[3 * 2 * 64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int e = blockIdx.x;
   const int T = a.T, d = a.d, E = a.E;
+  if (e >= E) {
+    shared_gate_up_tile<CPW>(sh, e - E, red);
+    return;
+  }
   const int kq = d >> 2;
   const float *wrow = a.w + (size_t)e * d + wave * kq;
   for (int t0 = 0; t0 < T; t0 += TT) {
@@ -239,10 +340,15 @@ __global__ __launch_bounds__(kRouteThreads) void route_logits_kernel(RouteArgs a
 }
 
 // One block: selection for every token, then the dispatch of its P pairs.
-template <int EPL>
-__global__ __launch_bounds__(kRouteThreads) void select_dispatch_kernel(RouteArgs a) {
+template <int EPL, int CPW_S>
+__global__ __launch_bounds__(kRouteThreads) void select_dispatch_kernel(RouteArgs a,
+                                                                        SharedArgs sh) {
   extern __shared__ int lds[];
   __shared__ int s_tmp[4];
+  if (blockIdx.x > 0) {
+    shared_down_tile<CPW_S>(sh, blockIdx.x - 1, reinterpret_cast<uint16_t *>(lds));
+    return;
+  }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int T = a.T, E = a.E, k = a.k;
   const int P = T * k;
@@ -341,100 +447,51 @@ struct GateUpArgs {
   long long w_stride, s_stride;
   int I, d;
   uint16_t *h;  // [P][I]
-  // shared expert: bf16 gate/up [Is][d] split into skq K ranges of d/skq
-  const uint8_t *sg, *su;
-  int Is, T, skq, shared_blocks;
-  float *gp, *up;  // skq > 1: per-range partial sums [skq][T][Is]
-  uint16_t *hs;    // skq == 1: shared activations [T][Is]
   float limit;
+  int tp;  // token rows staged in LDS per batch
 };
 
-// Linear grid: blocks [0, shared_blocks) are shared-expert tiles (16 rows x
-// d/skq, one 128-wide chunk per wave -- about the bytes of a routed tile, and
-// scheduled first); the rest are routed tiles (work slot, 16 rows, full d).
+// Routed gate/up: block b = (work slot b / (I/16), 16-row tile); 4 waves split
+// d.  The expert's token rows are staged in LDS, `tp` at a time (weights are
+// re-read from L2 for each further batch of tp tokens).
 template <int CPW>
 __global__ __launch_bounds__(256) void decode_gate_up_kernel(GateUpArgs a) {
-  __shared__ glm_f32x4 red[4 * 2 * 64];
+  extern __shared__ __attribute__((aligned(16))) uint16_t s_x[];  // [tp][lds_row_stride(d)]
+  __shared__ glm_f32x4 red[3 * 2 * 64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int d = a.d;
-  int b = blockIdx.x;
-  if (b < a.shared_blocks) {
-    const uint8_t *srow[2] = {nullptr, nullptr};
-    if (a.skq > 1) {
-      // few tokens: split K over skq blocks, write f32 partial sums
-      const int row0 = (b / a.skq) * 16;
-      const int kq = b % a.skq;
-      const int kbase = kq * (d / a.skq) + wave * 128;
-      const uint8_t *wrow[2] = {a.sg + (size_t)(row0 + r) * d * 2, a.su + (size_t)(row0 + r) * d * 2};
-      for (int p0 = 0; p0 < a.T; p0 += 16) {
-        const int t = p0 + r;
-        const uint16_t *act = t < a.T ? a.x + (size_t)t * d : nullptr;
-        glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
-        wave_mma<FMT_BF16, 2, 1>(wrow, srow, kbase, q, act, acc);
-        if (ksplit_reduce<2>(acc, red, wave, 4, lane) && t < a.T) {
-          const size_t o = ((size_t)kq * a.T + t) * a.Is + row0 + 4 * q;
-          *reinterpret_cast<glm_f32x4 *>(a.gp + o) = acc[0];
-          *reinterpret_cast<glm_f32x4 *>(a.up + o) = acc[1];
-        }
-      }
-    } else {
-      // more tokens: full-K tiles, SwiGLU applied here, bf16 activations out
-      const int row0 = b * 16;
-      const int kbase = wave * CPW * 128;
-      const uint8_t *wrow[2] = {a.sg + (size_t)(row0 + r) * d * 2, a.su + (size_t)(row0 + r) * d * 2};
-      for (int p0 = 0; p0 < a.T; p0 += 16) {
-        const int t = p0 + r;
-        const uint16_t *act = t < a.T ? a.x + (size_t)t * d : nullptr;
-        glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
-        wave_mma<FMT_BF16, 2, CPW>(wrow, srow, kbase, q, act, acc);
-        if (ksplit_reduce<2>(acc, red, wave, 4, lane) && t < a.T) {
-          uint32_t o[4];
-#pragma unroll
-          for (int m = 0; m < 4; ++m)
-            o[m] = f32_to_bf16(limited_swiglu(bf16_round(acc[0][m]), bf16_round(acc[1][m]), a.limit));
-          store_rows4(a.hs + (size_t)t * a.Is + row0 + 4 * q, o);
-        }
-      }
-    }
-    return;
-  }
-  b -= a.shared_blocks;
   const int tiles = a.I / 16;
-  const int4 wk = a.work[b / tiles];
-  const int row0 = (b % tiles) * 16;
+  const int4 wk = a.work[blockIdx.x / tiles];
+  const int row0 = (blockIdx.x % tiles) * 16;
   const int e = wk.x, base = wk.y, n = wk.z;
   if (e < 0 || n <= 0) return;
   const int kbase = wave * CPW * 128;
-  for (int p0 = 0; p0 < n; p0 += 16) {
-    const int pair = p0 + r;
-    glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
-    const uint8_t *wrow[2] = {a.gw + e * a.w_stride + (size_t)(row0 + r) * (d / 2),
-                              a.uw + e * a.w_stride + (size_t)(row0 + r) * (d / 2)};
-    const uint8_t *srow[2] = {a.gs + e * a.s_stride + (size_t)(row0 + r) * (d / 32),
-                              a.us + e * a.s_stride + (size_t)(row0 + r) * (d / 32)};
-    // weight stream first; the token lookup overlaps with it
+  const uint8_t *wrow[2] = {a.gw + e * a.w_stride + (size_t)(row0 + r) * (d / 2),
+                            a.uw + e * a.w_stride + (size_t)(row0 + r) * (d / 2)};
+  const uint8_t *srow[2] = {a.gs + e * a.s_stride + (size_t)(row0 + r) * (d / 32),
+                            a.us + e * a.s_stride + (size_t)(row0 + r) * (d / 32)};
+  for (int p0 = 0; p0 < n; p0 += a.tp) {
+    const int rows = min(a.tp, n - p0);
+    // weight stream first; the token staging overlaps with it
     WaveWeights<FMT_MXFP4, 2, CPW> ww;
     load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
-    const uint16_t *act = pair < n ? a.x + (size_t)a.pair_token[base + pair] * d : nullptr;
-    mma_wave_weights<FMT_MXFP4, 2, CPW>(ww, kbase, q, act, acc);
-    if (ksplit_reduce<2>(acc, red, wave, 4, lane) && pair < n) {
+    if (p0 > 0) __syncthreads();
+    stage_rows(s_x, a.x, a.pair_token + base + p0, rows, d);
+    __syncthreads();
+    glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
+    mma_wave_weights_lds<FMT_MXFP4, 2, CPW>(ww, kbase, q,
+                                            r < rows ? s_x + r * lds_row_stride(d) : nullptr, acc);
+    if (ksplit_reduce<2>(acc, red, wave, 4, lane) && r < rows) {
       uint32_t o[4];
 #pragma unroll
       for (int m = 0; m < 4; ++m)
         o[m] = f32_to_bf16(limited_swiglu(bf16_round(acc[0][m]), bf16_round(acc[1][m]), a.limit));
-      store_rows4(a.h + (size_t)(base + pair) * a.I + row0 + 4 * q, o);
+      store_rows4(a.h + (size_t)(base + p0 + r) * a.I + row0 + 4 * q, o);
     }
   }
 }
 
-// ---------------------------------------------------------------------------
-// Down.  Linear grid: blocks [0, shared_blocks) are shared-expert tiles (64
-// rows x Is/skd, CPW_S chunks per wave) whose activations are rebuilt in LDS
-// from the gate/up partials (fixed-order sum, bf16, SwiGLU); the rest are
-// routed tiles (work slot, 64 rows, full I).  Shared tiles write f32 partial
-// sums [skd][T][d] that the combine adds in order.
-// ---------------------------------------------------------------------------
 struct DownArgs {
   const uint16_t *h;
   const int4 *work;
@@ -443,72 +500,40 @@ struct DownArgs {
   long long w_stride, s_stride;
   int I, d;
   uint16_t *y;  // [P][d]
-  const uint8_t *sd;  // shared bf16 down [d][Is]
-  const float *gp, *up;  // skq > 1: gate/up partial sums
-  const uint16_t *hs;    // skq == 1: shared activations [T][Is]
-  int Is, T, skq, skd, shared_blocks;
-  float limit;
-  float *yp;  // [skd][T][d]
+  int tp;  // h rows staged in LDS per batch
 };
 
-template <int CPW_R, int CPW_S>
+// Routed down: block b = (work slot b / (d/64), 64-row tile); each wave owns
+// 16 output rows over the full K = I.  The slot's h rows are staged in LDS,
+// `tp` at a time.
+template <int CPW_R>
 __global__ __launch_bounds__(256) void decode_down_kernel(DownArgs a) {
-  extern __shared__ uint16_t s_h[];  // [T][CPW_S * 128] shared-expert activations
+  extern __shared__ __attribute__((aligned(16))) uint16_t s_x[];  // [tp][lds_row_stride(I)]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int d = a.d;
-  int b = blockIdx.x;
-  if (b < a.shared_blocks) {
-    constexpr int KS = CPW_S * 128;
-    const int tile = b / a.skd, kd = b % a.skd;
-    const int row0 = tile * 64 + wave * 16;
-    const int kbase = kd * KS;
-    if (a.skq > 1) {
-      // rebuild this K range of the shared activations from the gate/up partials
-      for (int i = threadIdx.x; i < a.T * KS; i += 256) {
-        const int t = i / KS, kk = kbase + i % KS;
-        float g = 0.0f, u = 0.0f;
-        for (int qq = 0; qq < a.skq; ++qq) {
-          g += a.gp[((size_t)qq * a.T + t) * a.Is + kk];
-          u += a.up[((size_t)qq * a.T + t) * a.Is + kk];
-        }
-        s_h[i] = (uint16_t)f32_to_bf16(limited_swiglu(bf16_round(g), bf16_round(u), a.limit));
-      }
-      __syncthreads();
-    }
-    const uint8_t *wrow[1] = {a.sd + ((size_t)(row0 + r) * a.Is + kbase) * 2};
-    const uint8_t *srow[1] = {nullptr};
-    for (int p0 = 0; p0 < a.T; p0 += 16) {
-      const int t = p0 + r;
-      glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
-      const uint16_t *act = t >= a.T ? nullptr
-                            : (a.skq > 1 ? s_h + (size_t)t * KS : a.hs + (size_t)t * a.Is + kbase);
-      wave_mma<FMT_BF16, 1, CPW_S>(wrow, srow, 0, q, act, acc);
-      if (t < a.T)
-        *reinterpret_cast<glm_f32x4 *>(a.yp + ((size_t)kd * a.T + t) * d + row0 + 4 * q) = acc[0];
-    }
-    return;
-  }
-  b -= a.shared_blocks;
   const int tiles = d / 64;
-  const int4 wk = a.work[b / tiles];
-  const int row0 = (b % tiles) * 64 + wave * 16;
+  const int4 wk = a.work[blockIdx.x / tiles];
+  const int row0 = (blockIdx.x % tiles) * 64 + wave * 16;
   const int e = wk.x, base = wk.y, n = wk.z;
   if (e < 0 || n <= 0) return;
-  for (int p0 = 0; p0 < n; p0 += 16) {
-    const int pair = p0 + r;
-    glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
-    const uint8_t *wrow[1] = {a.dw + e * a.w_stride + (size_t)(row0 + r) * (a.I / 2)};
-    const uint8_t *srow[1] = {a.ds + e * a.s_stride + (size_t)(row0 + r) * (a.I / 32)};
+  const uint8_t *wrow[1] = {a.dw + e * a.w_stride + (size_t)(row0 + r) * (a.I / 2)};
+  const uint8_t *srow[1] = {a.ds + e * a.s_stride + (size_t)(row0 + r) * (a.I / 32)};
+  for (int p0 = 0; p0 < n; p0 += a.tp) {
+    const int rows = min(a.tp, n - p0);
     WaveWeights<FMT_MXFP4, 1, CPW_R> ww;
     load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
-    const uint16_t *act = pair < n ? a.h + (size_t)(base + pair) * a.I : nullptr;
-    mma_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, 0, q, act, acc);
-    if (pair < n) {
+    if (p0 > 0) __syncthreads();
+    stage_rows(s_x, a.h + (size_t)(base + p0) * a.I, nullptr, rows, a.I);
+    __syncthreads();
+    glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
+    mma_wave_weights_lds<FMT_MXFP4, 1, CPW_R>(ww, 0, q,
+                                              r < rows ? s_x + r * lds_row_stride(a.I) : nullptr, acc);
+    if (r < rows) {
       uint32_t o[4];
 #pragma unroll
       for (int m = 0; m < 4; ++m) o[m] = f32_to_bf16(acc[0][m]);
-      store_rows4(a.y + (size_t)(base + pair) * d + row0 + 4 * q, o);
+      store_rows4(a.y + (size_t)(base + p0 + r) * d + row0 + 4 * q, o);
     }
   }
 }
@@ -549,25 +574,66 @@ bool glm_decode_path_supported(int T, int d, int E, int k, int I, int Is) {
   return true;
 }
 
+// Shared-expert splits: gate/up K in d/512 ranges when T <= 8 (one 128-wide
+// chunk per wave), else full-K tiles; down K in ranges of 2 chunks (1 if Is == 128).
+int glm_decode_shared_skq(int T, int d) { return T <= 8 ? d / 512 : 1; }
+int glm_decode_shared_cpws(int Is) { return Is / 128 == 1 ? 1 : 2; }
+int glm_decode_shared_skd(int Is) { return Is / 128 / glm_decode_shared_cpws(Is); }
+
 int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d, const float *w,
                             const float *bias, int E, int k, int n_group, int topk_group,
                             int norm, float scale, float *logits, float *weights,
                             uint32_t *indices, int32_t *counts, int32_t *offsets, int32_t *perm,
                             int32_t *inv, int32_t *pair_token, int32_t *active,
-                            int32_t *num_active, int32_t *status, int4 *work) {
+                            int32_t *num_active, int32_t *status, int4 *work,
+                            const uint16_t *sg, const uint16_t *su, const uint16_t *sd, int Is,
+                            float *gp, float *up, uint16_t *hs, float *yp, float limit) {
   RouteArgs a{x,      w,      bias,   T,   d,          E,      k,          n_group,
               topk_group, norm, scale, logits, weights, indices, counts, offsets,
               perm,   inv,    pair_token, active, num_active, status, work};
-  if (T <= 2)
-    hipLaunchKernelGGL((route_logits_kernel<2>), dim3(E), dim3(kRouteThreads), 0, stream, a);
-  else
-    hipLaunchKernelGGL((route_logits_kernel<8>), dim3(E), dim3(kRouteThreads), 0, stream, a);
+  SharedArgs sh{};
+  sh.x = x;
+  sh.sg = reinterpret_cast<const uint8_t *>(sg);
+  sh.su = reinterpret_cast<const uint8_t *>(su);
+  sh.sd = reinterpret_cast<const uint8_t *>(sd);
+  sh.T = T;
+  sh.d = d;
+  sh.Is = sg ? Is : 0;
+  sh.skq = glm_decode_shared_skq(T, d);
+  sh.skd = sg ? glm_decode_shared_skd(Is) : 1;
+  sh.gu_blocks = sg ? (Is / 16) * sh.skq : 0;
+  sh.dn_blocks = sg ? (d / 64) * sh.skd : 0;
+  sh.gp = gp;
+  sh.up = up;
+  sh.hs = hs;
+  sh.yp = yp;
+  sh.limit = glm_limit_bf16(limit);
+  const int cpw = d / 512;
+  const dim3 g1(E + sh.gu_blocks);
+#define GLM_LOGITS(TT)                                                                          \
+  switch (cpw) {                                                                                \
+    case 2: hipLaunchKernelGGL((route_logits_kernel<TT, 2>), g1, dim3(kRouteThreads), 0, stream, a, sh); break; \
+    case 4: hipLaunchKernelGGL((route_logits_kernel<TT, 4>), g1, dim3(kRouteThreads), 0, stream, a, sh); break; \
+    case 6: hipLaunchKernelGGL((route_logits_kernel<TT, 6>), g1, dim3(kRouteThreads), 0, stream, a, sh); break; \
+    default: hipLaunchKernelGGL((route_logits_kernel<TT, 8>), g1, dim3(kRouteThreads), 0, stream, a, sh); break; \
+  }
+  if (T <= 2) {
+    GLM_LOGITS(2)
+  } else {
+    GLM_LOGITS(8)
+  }
+#undef GLM_LOGITS
   GLM_LAUNCH_CHECK("route_logits_kernel");
   const int epl = (E + 63) / 64;
   const int e8 = epl <= 1 ? 1 : (epl <= 2 ? 2 : (epl <= 4 ? 4 : 8));
-  const size_t lds = glm_select_dispatch_lds_bytes(e8);
-#define GLM_SEL(EP) \
-  hipLaunchKernelGGL((select_dispatch_kernel<EP>), dim3(1), dim3(kRouteThreads), lds, stream, a)
+  const int cs = sg ? glm_decode_shared_cpws(Is) : 1;
+  const size_t lds = std::max(glm_select_dispatch_lds_bytes(e8), (size_t)T * cs * 128 * 2);
+  const dim3 g2(1 + sh.dn_blocks);
+#define GLM_SEL(EP)                                                                           \
+  if (cs == 1)                                                                                \
+    hipLaunchKernelGGL((select_dispatch_kernel<EP, 1>), g2, dim3(kRouteThreads), lds, stream, a, sh); \
+  else                                                                                        \
+    hipLaunchKernelGGL((select_dispatch_kernel<EP, 2>), g2, dim3(kRouteThreads), lds, stream, a, sh)
   if (e8 == 1) GLM_SEL(1);
   else if (e8 == 2) GLM_SEL(2);
   else if (e8 == 4) GLM_SEL(4);
@@ -577,17 +643,10 @@ int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d,
   return GLM_OK;
 }
 
-// Shared-expert K split of the decode kernels: gate/up uses d/512 ranges (one
-// 128-wide chunk per wave); down uses ranges of 2 chunks (1 if Is == 128).
-int glm_decode_shared_skq(int T, int d) { return T <= 8 ? d / 512 : 1; }
-int glm_decode_shared_cpws(int Is) { return Is / 128 == 1 ? 1 : 2; }
-int glm_decode_shared_skd(int Is) { return Is / 128 / glm_decode_shared_cpws(Is); }
-
 int glm_decode_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int E,
                               int k, const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
                               const uint8_t *us, const int32_t *pair_token, const int4 *work,
-                              const uint16_t *sg, const uint16_t *su, int Is, uint16_t *h,
-                              float *gp, float *up, uint16_t *hs, float limit) {
+                              uint16_t *h, float limit) {
   GateUpArgs a{};
   a.x = x;
   a.pair_token = pair_token;
@@ -602,41 +661,24 @@ int glm_decode_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int 
   a.I = I;
   a.d = d;
   a.h = h;
-  a.sg = reinterpret_cast<const uint8_t *>(sg);
-  a.su = reinterpret_cast<const uint8_t *>(su);
-  a.Is = sg ? Is : 0;
-  a.T = T;
-  a.skq = glm_decode_shared_skq(T, d);
-  a.shared_blocks = sg ? (Is / 16) * a.skq : 0;
-  a.gp = gp;
-  a.up = up;
-  a.hs = hs;
   a.limit = glm_limit_bf16(limit);
-  const int blocks = a.shared_blocks + a.slots * (I / 16);
-  const int cpw = d / 512;
-  switch (cpw) {
-    case 2: hipLaunchKernelGGL(decode_gate_up_kernel<2>, dim3(blocks), dim3(256), 0, stream, a); break;
-    case 4: hipLaunchKernelGGL(decode_gate_up_kernel<4>, dim3(blocks), dim3(256), 0, stream, a); break;
-    case 6: hipLaunchKernelGGL(decode_gate_up_kernel<6>, dim3(blocks), dim3(256), 0, stream, a); break;
-    case 8: hipLaunchKernelGGL(decode_gate_up_kernel<8>, dim3(blocks), dim3(256), 0, stream, a); break;
+  a.tp = std::min(T, kStageTokens);
+  const size_t lds = (size_t)a.tp * lds_row_stride(d) * 2;
+  const int blocks = a.slots * (I / 16);
+  switch (d / 512) {
+    case 2: hipLaunchKernelGGL(decode_gate_up_kernel<2>, dim3(blocks), dim3(256), lds, stream, a); break;
+    case 4: hipLaunchKernelGGL(decode_gate_up_kernel<4>, dim3(blocks), dim3(256), lds, stream, a); break;
+    case 6: hipLaunchKernelGGL(decode_gate_up_kernel<6>, dim3(blocks), dim3(256), lds, stream, a); break;
+    case 8: hipLaunchKernelGGL(decode_gate_up_kernel<8>, dim3(blocks), dim3(256), lds, stream, a); break;
     default: glm::set_error("decode gate/up: unsupported d=%d", d); return GLM_ERR_UNSUPPORTED_SHAPE;
   }
   GLM_LAUNCH_CHECK("decode_gate_up_kernel");
   return GLM_OK;
 }
 
-template <int CR>
-static void launch_down_cs(hipStream_t stream, int blocks, size_t lds, const DownArgs &a, int cs) {
-  if (cs == 1)
-    hipLaunchKernelGGL((decode_down_kernel<CR, 1>), dim3(blocks), dim3(256), lds, stream, a);
-  else
-    hipLaunchKernelGGL((decode_down_kernel<CR, 2>), dim3(blocks), dim3(256), lds, stream, a);
-}
-
 int glm_decode_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, int d,
                            int E, const uint8_t *dw, const uint8_t *ds, const int4 *work,
-                           const uint16_t *sd, const float *gp, const float *up,
-                           const uint16_t *hs, int Is, float limit, uint16_t *y, float *yp) {
+                           uint16_t *y) {
   DownArgs a{};
   a.h = h;
   a.work = work;
@@ -648,26 +690,15 @@ int glm_decode_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, 
   a.I = I;
   a.d = d;
   a.y = y;
-  a.sd = reinterpret_cast<const uint8_t *>(sd);
-  a.gp = gp;
-  a.up = up;
-  a.hs = hs;
-  a.Is = sd ? Is : 0;
-  a.T = T;
-  a.skq = glm_decode_shared_skq(T, d);
-  const int cs = sd ? glm_decode_shared_cpws(Is) : 1;
-  a.skd = sd ? glm_decode_shared_skd(Is) : 1;
-  a.shared_blocks = sd ? (d / 64) * a.skd : 0;
-  a.limit = glm_limit_bf16(limit);
-  a.yp = yp;
-  const int blocks = a.shared_blocks + a.slots * (d / 64);
-  const size_t lds = sd && a.skq > 1 ? (size_t)T * cs * 128 * 2 : 0;
+  a.tp = std::min(T * k, kStageTokens);
+  const size_t lds = (size_t)a.tp * lds_row_stride(I) * 2;
+  const int blocks = a.slots * (d / 64);
   switch (I / 128) {
-    case 1: launch_down_cs<1>(stream, blocks, lds, a, cs); break;
-    case 2: launch_down_cs<2>(stream, blocks, lds, a, cs); break;
-    case 4: launch_down_cs<4>(stream, blocks, lds, a, cs); break;
-    case 6: launch_down_cs<6>(stream, blocks, lds, a, cs); break;
-    case 8: launch_down_cs<8>(stream, blocks, lds, a, cs); break;
+    case 1: hipLaunchKernelGGL(decode_down_kernel<1>, dim3(blocks), dim3(256), lds, stream, a); break;
+    case 2: hipLaunchKernelGGL(decode_down_kernel<2>, dim3(blocks), dim3(256), lds, stream, a); break;
+    case 4: hipLaunchKernelGGL(decode_down_kernel<4>, dim3(blocks), dim3(256), lds, stream, a); break;
+    case 6: hipLaunchKernelGGL(decode_down_kernel<6>, dim3(blocks), dim3(256), lds, stream, a); break;
+    case 8: hipLaunchKernelGGL(decode_down_kernel<8>, dim3(blocks), dim3(256), lds, stream, a); break;
     default: glm::set_error("decode down: unsupported I=%d", I); return GLM_ERR_UNSUPPORTED_SHAPE;
   }
   GLM_LAUNCH_CHECK("decode_down_kernel");

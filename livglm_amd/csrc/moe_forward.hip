@@ -55,16 +55,16 @@ int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d,
                             int norm, float scale, float *logits, float *weights,
                             uint32_t *indices, int32_t *counts, int32_t *offsets, int32_t *perm,
                             int32_t *inv, int32_t *pair_token, int32_t *active,
-                            int32_t *num_active, int32_t *status, int4 *work);
+                            int32_t *num_active, int32_t *status, int4 *work,
+                            const uint16_t *sg, const uint16_t *su, const uint16_t *sd, int Is,
+                            float *gp, float *up, uint16_t *hs, float *yp, float limit);
 int glm_decode_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int E,
                               int k, const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
                               const uint8_t *us, const int32_t *pair_token, const int4 *work,
-                              const uint16_t *sg, const uint16_t *su, int Is, uint16_t *h,
-                              float *gp, float *up, uint16_t *hs, float limit);
+                              uint16_t *h, float limit);
 int glm_decode_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, int d,
                            int E, const uint8_t *dw, const uint8_t *ds, const int4 *work,
-                           const uint16_t *sd, const float *gp, const float *up,
-                           const uint16_t *hs, int Is, float limit, uint16_t *y, float *yp);
+                           uint16_t *y);
 int glm_combine_parts_launch(hipStream_t stream, const uint16_t *y, const int32_t *inv,
                              const float *w, const uint16_t *shared, const float *shared_parts,
                              int nparts, int T, int k, int d, float *out);
@@ -206,22 +206,23 @@ extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
   const bool shared_bf16 = has_shared && shared_fmt == GLM_FMT_BF16;
   const uint16_t *shared_ready = shared_in;  // caller-computed shared output, if any
   if (glm_decode_path_supported(T, d, E, top_k, I, shared_bf16 && !shared_in ? Is : 0)) {
-    // decode: five short kernels, no host synchronisation
-    rc = glm_route_decode_launch(stream, x, T, d, router_weight, router_bias, E, top_k, n_group,
-                                 topk_group, norm_topk_prob, routed_scaling_factor, w.logits,
-                                 wts, idx, w.counts, w.offsets, w.perm, w.inv, w.pair_token,
-                                 w.active, w.num_active, w.status, w.work);
-    if (rc) return rc;
+    // decode: five short kernels, no host synchronisation; the bf16 shared
+    // expert rides in the two routing kernels
     const bool fuse_shared = shared_bf16 && !shared_in;
+    rc = glm_route_decode_launch(
+        stream, x, T, d, router_weight, router_bias, E, top_k, n_group, topk_group,
+        norm_topk_prob, routed_scaling_factor, w.logits, wts, idx, w.counts, w.offsets, w.perm,
+        w.inv, w.pair_token, w.active, w.num_active, w.status, w.work,
+        fuse_shared ? (const uint16_t *)shared_gate : nullptr,
+        fuse_shared ? (const uint16_t *)shared_up : nullptr,
+        fuse_shared ? (const uint16_t *)shared_down : nullptr, Is, w.gp, w.up, w.shared_h, w.yp,
+        swiglu_limit);
+    if (rc) return rc;
     rc = glm_decode_gate_up_launch(stream, x, T, d, I, E, top_k, gate_packed, gate_scales,
-                                   up_packed, up_scales, w.pair_token, w.work,
-                                   fuse_shared ? (const uint16_t *)shared_gate : nullptr,
-                                   fuse_shared ? (const uint16_t *)shared_up : nullptr, Is, w.h,
-                                   w.gp, w.up, w.shared_h, swiglu_limit);
+                                   up_packed, up_scales, w.pair_token, w.work, w.h, swiglu_limit);
     if (rc) return rc;
     rc = glm_decode_down_launch(stream, w.h, T, top_k, I, d, E, down_packed, down_scales, w.work,
-                                fuse_shared ? (const uint16_t *)shared_down : nullptr, w.gp, w.up,
-                                w.shared_h, Is, swiglu_limit, w.y, w.yp);
+                                w.y);
     if (rc) return rc;
     if (fuse_shared)
       return glm_combine_parts_launch(stream, w.y, w.inv, wts, nullptr, w.yp,
