@@ -13,6 +13,20 @@
 //   4. decode_down_kernel     routed MXFP4 down.
 //   5. combine_kernel         weighted top-k merge + shared add.
 //
+// With very few tokens (T <= 4, k <= 8) experts are rarely shared between
+// tokens, so the layer runs token-major in three kernels and skips the
+// dispatch altogether:
+//
+//   1. route_logits_kernel    as above.
+//   2. select_gate_up_kernel  block = (pair t*k + j, 16-row tile): wave 0
+//                             selects token t's experts from its logits, then
+//                             the block computes gate/up + SwiGLU of expert j
+//                             for that token; extra blocks: shared down tiles.
+//   3. down_combine_kernel    block = (token, 16 rows of d): each wave runs the
+//                             down projection of k/4 of the token's experts,
+//                             and the weighted merge + shared add happen in
+//                             LDS in the combine's order.
+//
 // Every kernel boundary is a stream-ordered dependency; nothing synchronises
 // across blocks inside a kernel, and every reduction runs in one fixed order.
 #include "mfma_tile.h"
@@ -85,7 +99,8 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 
 // Top-k selection of one token by one wave (moe.py:39-62).  Lane l holds
 // experts l + 64i; k rounds of a DPP wave maximum over sortable keys pick the
-// experts best first.
+// experts best first.  Lanes j < k write column j of the weights and indices
+// (skipped where w_out / i_out are null) and of pair_idx.
 // `scratch` is this wave's LDS area (>= 64*EPL + 256 words).
 template <int EPL>
 __device__ void select_token(const float *logits_row, const float *bias, int E, int k,
@@ -166,8 +181,8 @@ __device__ void select_token(const float *logits_row, const float *bias, int E, 
   if (lane < k) {
     float wj = s_wsel[lane];
     if (norm) wj = wj / (total + 1e-20f);
-    w_out[lane] = wj * scale;
-    i_out[lane] = (uint32_t)s_isel[lane];
+    if (w_out != nullptr) w_out[lane] = wj * scale;
+    if (i_out != nullptr) i_out[lane] = (uint32_t)s_isel[lane];
     pair_idx[lane] = s_isel[lane];
   }
   wave_lds_sync();
@@ -538,6 +553,156 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DownArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Few-token path: token-major selection + gate/up, then down + combine.
+// ---------------------------------------------------------------------------
+constexpr int kPairMaxT = 4;
+constexpr int kPairMaxK = 8;
+
+struct PairArgs {
+  const float *logits, *bias;
+  int T, E, k, n_group, topk_group, norm;
+  float scale;
+  float *weights;     // [T][k]
+  uint32_t *indices;  // [T][k]
+  const uint16_t *x;
+  const uint8_t *gw, *gs, *uw, *us;
+  long long w_stride, s_stride;
+  int d, I;
+  uint16_t *h;  // [T*k][I] in pair order
+  float limit;
+  int routed_blocks;
+};
+
+// LDS bytes of select_gate_up_kernel: the token row, then wave 0's
+// selection scratch; shared down tiles reuse the area for their activations.
+__host__ __device__ constexpr size_t pair_gate_up_lds_bytes(int d, int EPL) {
+  return (size_t)lds_row_stride(d) * 2 + (size_t)(64 * EPL + 256) * 4;
+}
+
+template <int EPL, int CPW, int CPW_S>
+__global__ __launch_bounds__(256) void select_gate_up_kernel(PairArgs a, SharedArgs sh) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t s_dyn[];
+  __shared__ glm_f32x4 red[3 * 2 * 64];
+  __shared__ int s_sel[kPairMaxK];
+  if ((int)blockIdx.x >= a.routed_blocks) {
+    shared_down_tile<CPW_S>(sh, blockIdx.x - a.routed_blocks, s_dyn);
+    return;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int d = a.d, k = a.k, E = a.E;
+  const int tiles = a.I / 16;
+  const int tile = blockIdx.x % tiles;
+  const int pr = blockIdx.x / tiles;  // pair t*k + j
+  const int t = pr / k, j = pr % k;
+  uint16_t *s_x = s_dyn;  // token t's row
+  stage_rows(s_x, a.x + (size_t)t * d, nullptr, 1, d);
+  if (wave == 0) {
+    const bool first = j == 0 && tile == 0;  // one block per token publishes the route
+    float *scratch = reinterpret_cast<float *>(s_dyn + lds_row_stride(d));
+    select_token<EPL>(a.logits + (size_t)t * E, a.bias, E, k, a.n_group, a.topk_group, a.norm,
+                      a.scale, first ? a.weights + (size_t)t * k : nullptr,
+                      first ? a.indices + (size_t)t * k : nullptr, s_sel, scratch, lane);
+  }
+  __syncthreads();
+  const long long e = s_sel[j];
+  const int row0 = tile * 16;
+  const int kbase = wave * CPW * 128;
+  const uint8_t *wrow[2] = {a.gw + e * a.w_stride + (size_t)(row0 + r) * (d / 2),
+                            a.uw + e * a.w_stride + (size_t)(row0 + r) * (d / 2)};
+  const uint8_t *srow[2] = {a.gs + e * a.s_stride + (size_t)(row0 + r) * (d / 32),
+                            a.us + e * a.s_stride + (size_t)(row0 + r) * (d / 32)};
+  WaveWeights<FMT_MXFP4, 2, CPW> ww;
+  load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
+  glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
+  mma_wave_weights_lds<FMT_MXFP4, 2, CPW>(ww, kbase, q, r == 0 ? s_x : nullptr, acc);
+  if (ksplit_reduce<2>(acc, red, wave, 4, lane) && r == 0) {
+    uint32_t o[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      o[m] = f32_to_bf16(limited_swiglu(bf16_round(acc[0][m]), bf16_round(acc[1][m]), a.limit));
+    store_rows4(a.h + (size_t)pr * a.I + row0 + 4 * q, o);
+  }
+}
+
+struct PairDownArgs {
+  const uint16_t *h;  // [T*k][I] in pair order
+  const float *weights;
+  const uint32_t *indices;
+  const uint8_t *dw, *ds;
+  long long w_stride, s_stride;
+  int T, k, I, d;
+  const uint16_t *shared;      // bf16 shared output [T][d], or
+  const float *shared_parts;   // its f32 K-range partial sums [nparts][T][d], or neither
+  int nparts;
+  float *out;  // [T][d] f32
+};
+
+// Down projection of all k experts of one token on 16 rows of d, merged in
+// the combine's order: out = sum_j f32(bf16(y_j)) * w_j (sequential j, no
+// contraction) + shared, where shared = bf16 of its partial sums added in order.
+template <int CPW_R, int JPW>
+__global__ __launch_bounds__(256) void down_combine_kernel(PairDownArgs a) {
+#pragma clang fp contract(off)
+  extern __shared__ __attribute__((aligned(16))) uint16_t s_h[];  // [k][lds_row_stride(I)]
+  __shared__ float s_p[kPairMaxK][16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int k = a.k, d = a.d, I = a.I;
+  const int tiles = d / 16;
+  const int t = blockIdx.x / tiles;
+  const int row0 = (blockIdx.x % tiles) * 16;
+  WaveWeights<FMT_MXFP4, 1, CPW_R> ww[JPW];
+  float wj[JPW];
+#pragma unroll
+  for (int s = 0; s < JPW; ++s) {
+    const int j = wave + 4 * s;
+    wj[s] = 0.0f;
+    if (j < k) {
+      const long long e = a.indices[(size_t)t * k + j];
+      wj[s] = a.weights[(size_t)t * k + j];
+      const uint8_t *wrow[1] = {a.dw + e * a.w_stride + (size_t)(row0 + r) * (I / 2)};
+      const uint8_t *srow[1] = {a.ds + e * a.s_stride + (size_t)(row0 + r) * (I / 32)};
+      load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww[s], wrow, srow, 0, q);
+    }
+  }
+  // the shared expert's contribution to these 16 outputs (thread c < 16)
+  float shared_v = 0.0f;
+  const int c = row0 + threadIdx.x;
+  if (threadIdx.x < 16) {
+    if (a.shared_parts != nullptr) {
+      float sp = a.shared_parts[(size_t)t * d + c];
+      for (int qq = 1; qq < a.nparts; ++qq) sp = sp + a.shared_parts[((size_t)qq * a.T + t) * d + c];
+      shared_v = bf16_round(sp);
+    } else if (a.shared != nullptr) {
+      shared_v = bf16_to_f32(a.shared[(size_t)t * d + c]);
+    }
+  }
+  stage_rows(s_h, a.h + (size_t)t * k * I, nullptr, k, I);
+  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < JPW; ++s) {
+    const int j = wave + 4 * s;
+    if (j < k) {
+      glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
+      mma_wave_weights_lds<FMT_MXFP4, 1, CPW_R>(
+          ww[s], 0, q, r == 0 ? s_h + j * lds_row_stride(I) : nullptr, acc);
+      if (r == 0) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) s_p[j][4 * q + m] = bf16_round(acc[0][m]) * wj[s];
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    float o = 0.0f;
+    for (int j = 0; j < k; ++j) o = o + s_p[j][threadIdx.x];
+    if (a.shared_parts != nullptr || a.shared != nullptr) o = o + shared_v;
+    a.out[(size_t)t * d + c] = o;
+  }
+}
+
 // zero-fill (workspace initialisation)
 __global__ void fill_zero_kernel(uint32_t *p, long long n) {
   for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n;
@@ -580,17 +745,9 @@ int glm_decode_shared_skq(int T, int d) { return T <= 8 ? d / 512 : 1; }
 int glm_decode_shared_cpws(int Is) { return Is / 128 == 1 ? 1 : 2; }
 int glm_decode_shared_skd(int Is) { return Is / 128 / glm_decode_shared_cpws(Is); }
 
-int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d, const float *w,
-                            const float *bias, int E, int k, int n_group, int topk_group,
-                            int norm, float scale, float *logits, float *weights,
-                            uint32_t *indices, int32_t *counts, int32_t *offsets, int32_t *perm,
-                            int32_t *inv, int32_t *pair_token, int32_t *active,
-                            int32_t *num_active, int32_t *status, int4 *work,
-                            const uint16_t *sg, const uint16_t *su, const uint16_t *sd, int Is,
-                            float *gp, float *up, uint16_t *hs, float *yp, float limit) {
-  RouteArgs a{x,      w,      bias,   T,   d,          E,      k,          n_group,
-              topk_group, norm, scale, logits, weights, indices, counts, offsets,
-              perm,   inv,    pair_token, active, num_active, status, work};
+static SharedArgs make_shared_args(const uint16_t *x, int T, int d, const uint16_t *sg,
+                                   const uint16_t *su, const uint16_t *sd, int Is, float *gp,
+                                   float *up, uint16_t *hs, float *yp, float limit) {
   SharedArgs sh{};
   sh.x = x;
   sh.sg = reinterpret_cast<const uint8_t *>(sg);
@@ -608,8 +765,13 @@ int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d,
   sh.hs = hs;
   sh.yp = yp;
   sh.limit = glm_limit_bf16(limit);
-  const int cpw = d / 512;
-  const dim3 g1(E + sh.gu_blocks);
+  return sh;
+}
+
+// Router logits for every token, plus the shared expert's gate/up tiles.
+static int launch_route_logits(hipStream_t stream, const RouteArgs &a, const SharedArgs &sh) {
+  const int cpw = a.d / 512;
+  const dim3 g1(a.E + sh.gu_blocks);
 #define GLM_LOGITS(TT)                                                                          \
   switch (cpw) {                                                                                \
     case 2: hipLaunchKernelGGL((route_logits_kernel<TT, 2>), g1, dim3(kRouteThreads), 0, stream, a, sh); break; \
@@ -617,13 +779,30 @@ int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d,
     case 6: hipLaunchKernelGGL((route_logits_kernel<TT, 6>), g1, dim3(kRouteThreads), 0, stream, a, sh); break; \
     default: hipLaunchKernelGGL((route_logits_kernel<TT, 8>), g1, dim3(kRouteThreads), 0, stream, a, sh); break; \
   }
-  if (T <= 2) {
+  if (a.T <= 2) {
     GLM_LOGITS(2)
   } else {
     GLM_LOGITS(8)
   }
 #undef GLM_LOGITS
   GLM_LAUNCH_CHECK("route_logits_kernel");
+  return GLM_OK;
+}
+
+int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d, const float *w,
+                            const float *bias, int E, int k, int n_group, int topk_group,
+                            int norm, float scale, float *logits, float *weights,
+                            uint32_t *indices, int32_t *counts, int32_t *offsets, int32_t *perm,
+                            int32_t *inv, int32_t *pair_token, int32_t *active,
+                            int32_t *num_active, int32_t *status, int4 *work,
+                            const uint16_t *sg, const uint16_t *su, const uint16_t *sd, int Is,
+                            float *gp, float *up, uint16_t *hs, float *yp, float limit) {
+  RouteArgs a{x,      w,      bias,   T,   d,          E,      k,          n_group,
+              topk_group, norm, scale, logits, weights, indices, counts, offsets,
+              perm,   inv,    pair_token, active, num_active, status, work};
+  const SharedArgs sh = make_shared_args(x, T, d, sg, su, sd, Is, gp, up, hs, yp, limit);
+  int rc = launch_route_logits(stream, a, sh);
+  if (rc) return rc;
   const int epl = (E + 63) / 64;
   const int e8 = epl <= 1 ? 1 : (epl <= 2 ? 2 : (epl <= 4 ? 4 : 8));
   const int cs = sg ? glm_decode_shared_cpws(Is) : 1;
@@ -713,5 +892,122 @@ int glm_fill_zero_launch(hipStream_t stream, void *p, size_t bytes) {
   hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
                      (uint32_t *)p, n);
   GLM_LAUNCH_CHECK("fill_zero_kernel");
+  return GLM_OK;
+}
+
+bool glm_pair_path_supported(int T, int d, int E, int k, int I, int Is) {
+  return T >= 1 && T <= kPairMaxT && k <= kPairMaxK && d % 16 == 0 &&
+         glm_decode_path_supported(T, d, E, k, I, Is);
+}
+
+// The three-kernel token-major layer (T <= 4): logits (+ shared gate/up),
+// selection + routed gate/up (+ shared down), down + combine.  The bf16 shared
+// expert rides along when sg is given; otherwise shared_ready (bf16 [T][d],
+// computed by the caller) or nothing is added.
+int glm_pair_path_launch(hipStream_t stream, const uint16_t *x, int T, int d, const float *w,
+                         const float *bias, int E, int k, int n_group, int topk_group, int norm,
+                         float scale, float *logits, float *weights, uint32_t *indices, int I,
+                         const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
+                         const uint8_t *us, const uint8_t *dw, const uint8_t *ds,
+                         const uint16_t *sg, const uint16_t *su, const uint16_t *sd, int Is,
+                         float *gp, float *up, uint16_t *hs, float *yp,
+                         const uint16_t *shared_ready, uint16_t *h, float limit, float *out) {
+  RouteArgs ra{};
+  ra.x = x;
+  ra.w = w;
+  ra.T = T;
+  ra.d = d;
+  ra.E = E;
+  ra.k = k;
+  ra.logits = logits;
+  const SharedArgs sh = make_shared_args(x, T, d, sg, su, sd, Is, gp, up, hs, yp, limit);
+  int rc = launch_route_logits(stream, ra, sh);
+  if (rc) return rc;
+
+  PairArgs a{};
+  a.logits = logits;
+  a.bias = bias;
+  a.T = T;
+  a.E = E;
+  a.k = k;
+  a.n_group = n_group;
+  a.topk_group = topk_group;
+  a.norm = norm;
+  a.scale = scale;
+  a.weights = weights;
+  a.indices = indices;
+  a.x = x;
+  a.gw = gw;
+  a.gs = gs;
+  a.uw = uw;
+  a.us = us;
+  a.w_stride = (long long)I * (d / 2);
+  a.s_stride = (long long)I * (d / 32);
+  a.d = d;
+  a.I = I;
+  a.h = h;
+  a.limit = glm_limit_bf16(limit);
+  a.routed_blocks = T * k * (I / 16);
+  const int epl = E <= 128 ? 2 : (E <= 256 ? 4 : 8);
+  const int cs = sg ? glm_decode_shared_cpws(Is) : 1;
+  const size_t lds2 = std::max(pair_gate_up_lds_bytes(d, epl), (size_t)T * cs * 128 * 2);
+  const dim3 g2(a.routed_blocks + sh.dn_blocks);
+#define GLM_PAIR_GU(EP, CS)                                                                    \
+  switch (d / 512) {                                                                           \
+    case 2: hipLaunchKernelGGL((select_gate_up_kernel<EP, 2, CS>), g2, dim3(256), lds2, stream, a, sh); break; \
+    case 4: hipLaunchKernelGGL((select_gate_up_kernel<EP, 4, CS>), g2, dim3(256), lds2, stream, a, sh); break; \
+    case 6: hipLaunchKernelGGL((select_gate_up_kernel<EP, 6, CS>), g2, dim3(256), lds2, stream, a, sh); break; \
+    default: hipLaunchKernelGGL((select_gate_up_kernel<EP, 8, CS>), g2, dim3(256), lds2, stream, a, sh); break; \
+  }
+#define GLM_PAIR_GU_CS(EP) \
+  if (cs == 1) {           \
+    GLM_PAIR_GU(EP, 1)     \
+  } else {                 \
+    GLM_PAIR_GU(EP, 2)     \
+  }
+  if (epl == 2) {
+    GLM_PAIR_GU_CS(2)
+  } else if (epl == 4) {
+    GLM_PAIR_GU_CS(4)
+  } else {
+    GLM_PAIR_GU_CS(8)
+  }
+#undef GLM_PAIR_GU_CS
+#undef GLM_PAIR_GU
+  GLM_LAUNCH_CHECK("select_gate_up_kernel");
+
+  PairDownArgs b{};
+  b.h = h;
+  b.weights = weights;
+  b.indices = indices;
+  b.dw = dw;
+  b.ds = ds;
+  b.w_stride = (long long)d * (I / 2);
+  b.s_stride = (long long)d * (I / 32);
+  b.T = T;
+  b.k = k;
+  b.I = I;
+  b.d = d;
+  b.shared = sg ? nullptr : shared_ready;
+  b.shared_parts = sg ? yp : nullptr;
+  b.nparts = sg ? sh.skd : 0;
+  b.out = out;
+  const size_t lds3 = (size_t)k * lds_row_stride(I) * 2;
+  const dim3 g3(T * (d / 16));
+#define GLM_PAIR_DN(JPW)                                                                       \
+  switch (I / 128) {                                                                           \
+    case 1: hipLaunchKernelGGL((down_combine_kernel<1, JPW>), g3, dim3(256), lds3, stream, b); break; \
+    case 2: hipLaunchKernelGGL((down_combine_kernel<2, JPW>), g3, dim3(256), lds3, stream, b); break; \
+    case 4: hipLaunchKernelGGL((down_combine_kernel<4, JPW>), g3, dim3(256), lds3, stream, b); break; \
+    case 6: hipLaunchKernelGGL((down_combine_kernel<6, JPW>), g3, dim3(256), lds3, stream, b); break; \
+    default: hipLaunchKernelGGL((down_combine_kernel<8, JPW>), g3, dim3(256), lds3, stream, b); break; \
+  }
+  if (k <= 4) {
+    GLM_PAIR_DN(1)
+  } else {
+    GLM_PAIR_DN(2)
+  }
+#undef GLM_PAIR_DN
+  GLM_LAUNCH_CHECK("down_combine_kernel");
   return GLM_OK;
 }

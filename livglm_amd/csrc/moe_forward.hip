@@ -50,6 +50,15 @@ int glm_mlp_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, i
 int glm_combine_launch(hipStream_t stream, const uint16_t *y, const int32_t *inv, const float *w,
                        const uint16_t *shared, int T, int k, int d, float *out);
 bool glm_decode_path_supported(int T, int d, int E, int k, int I, int Is);
+bool glm_pair_path_supported(int T, int d, int E, int k, int I, int Is);
+int glm_pair_path_launch(hipStream_t stream, const uint16_t *x, int T, int d, const float *w,
+                         const float *bias, int E, int k, int n_group, int topk_group, int norm,
+                         float scale, float *logits, float *weights, uint32_t *indices, int I,
+                         const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
+                         const uint8_t *us, const uint8_t *dw, const uint8_t *ds,
+                         const uint16_t *sg, const uint16_t *su, const uint16_t *sd, int Is,
+                         float *gp, float *up, uint16_t *hs, float *yp,
+                         const uint16_t *shared_ready, uint16_t *h, float limit, float *out);
 int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d, const float *w,
                             const float *bias, int E, int k, int n_group, int topk_group,
                             int norm, float scale, float *logits, float *weights,
@@ -205,10 +214,28 @@ extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
   const int Is = has_shared ? I_shared : 0;
   const bool shared_bf16 = has_shared && shared_fmt == GLM_FMT_BF16;
   const uint16_t *shared_ready = shared_in;  // caller-computed shared output, if any
-  if (glm_decode_path_supported(T, d, E, top_k, I, shared_bf16 && !shared_in ? Is : 0)) {
+  const bool fuse_shared = shared_bf16 && !shared_in;
+  if (glm_pair_path_supported(T, d, E, top_k, I, fuse_shared ? Is : 0)) {
+    // a few tokens: three token-major kernels, no dispatch
+    if (has_shared && !shared_in && !shared_bf16) {
+      rc = glm_mlp_launch(stream, x, T, d, I_shared, shared_fmt, shared_gate, shared_gate_scales,
+                          shared_up, shared_up_scales, shared_down, shared_down_scales,
+                          swiglu_limit, w.shared_h, w.shared_out);
+      if (rc) return rc;
+      shared_ready = w.shared_out;
+    }
+    return glm_pair_path_launch(
+        stream, x, T, d, router_weight, router_bias, E, top_k, n_group, topk_group,
+        norm_topk_prob, routed_scaling_factor, w.logits, wts, idx, I, gate_packed, gate_scales,
+        up_packed, up_scales, down_packed, down_scales,
+        fuse_shared ? (const uint16_t *)shared_gate : nullptr,
+        fuse_shared ? (const uint16_t *)shared_up : nullptr,
+        fuse_shared ? (const uint16_t *)shared_down : nullptr, Is, w.gp, w.up, w.shared_h, w.yp,
+        shared_ready, w.h, swiglu_limit, out);
+  }
+  if (glm_decode_path_supported(T, d, E, top_k, I, fuse_shared ? Is : 0)) {
     // decode: five short kernels, no host synchronisation; the bf16 shared
     // expert rides in the two routing kernels
-    const bool fuse_shared = shared_bf16 && !shared_in;
     rc = glm_route_decode_launch(
         stream, x, T, d, router_weight, router_bias, E, top_k, n_group, topk_group,
         norm_topk_prob, routed_scaling_factor, w.logits, wts, idx, w.counts, w.offsets, w.perm,

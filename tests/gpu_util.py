@@ -66,8 +66,9 @@ def workspace(nbytes: int) -> torch.Tensor:
 
 def run_layer(dl: dict[str, torch.Tensor], shape, T: int | None = None, shared: bool = True,
               bias: torch.Tensor | None = None, ws: torch.Tensor | None = None,
-              shared_in: torch.Tensor | None = None):
-    """glm_moe_forward on uploaded layer tensors; returns (out, weights, indices)."""
+              shared_in: torch.Tensor | None = None, shared_fmt: int = native.GLM_FMT_BF16):
+    """glm_moe_forward on uploaded layer tensors; returns (out, weights, indices).
+    An MX shared expert takes its scales from dl["shared.gate.scales"] etc."""
     T = dl["x"].shape[0] if T is None else T
     d, E, k, I, Is = shape.d, shape.E, shape.k, shape.I, shape.I_shared
     lib = native.load()
@@ -82,8 +83,10 @@ def run_layer(dl: dict[str, torch.Tensor], shape, T: int | None = None, shared: 
             shape.topk_group, int(shape.norm_topk_prob), shape.routed_scaling_factor, I]
     args += [p(dl[key]) for key in BANK_KEYS]
     if shared:
-        args += [Is, native.GLM_FMT_BF16, p(dl["shared.gate"]), None, p(dl["shared.up"]), None,
-                 p(dl["shared.down"]), None, p(shared_in)]
+        sc = {key: (p(dl[key + ".scales"]) if shared_fmt != native.GLM_FMT_BF16 else None)
+              for key in ("shared.gate", "shared.up", "shared.down")}
+        args += [Is, shared_fmt, p(dl["shared.gate"]), sc["shared.gate"], p(dl["shared.up"]),
+                 sc["shared.up"], p(dl["shared.down"]), sc["shared.down"], p(shared_in)]
     else:
         args += [0, native.GLM_FMT_BF16, None, None, None, None, None, None, p(shared_in)]
     args += [shape.swiglu_limit, p(ws), ws_bytes, p(out), p(w), p(idx)]

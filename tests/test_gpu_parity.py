@@ -352,6 +352,56 @@ def test_moe_layer_parity(gu, name):
     assert O.rel_l2(gu.host(out), want) < REL_L2
 
 
+# Shapes around the few-token (T <= 4, k <= 8) and decode (T <= 64) kernel
+# paths: expert counts per lane 1..8, k not a multiple of 4, idle waves, group
+# masks, the smallest and largest chunk counts, with and without the shared expert.
+SMALL_LAYERS = [
+    # T, d, E, k, I, Is, (n_group, topk_group)
+    (1, 1024, 64, 6, 256, 256, (1, 1)),
+    (3, 1024, 256, 8, 512, 128, (8, 4)),
+    (4, 3072, 32, 4, 768, 0, (4, 2)),
+    (2, 4096, 16, 3, 1024, 512, (1, 1)),
+    (4, 2048, 448, 8, 128, 256, (1, 1)),
+    (5, 1024, 64, 6, 256, 256, (1, 1)),
+    (9, 2048, 96, 5, 384, 0, (3, 2)),
+]
+
+
+@pytest.mark.parametrize("T,d,E,k,I,Is,groups", SMALL_LAYERS)
+def test_moe_layer_small_shapes(gu, T, d, E, k, I, Is, groups):
+    shape = MoEShape("small", T, d, E, k, I, Is, n_group=groups[0], topk_group=groups[1])
+    layer = make_layer(shape, 900 + T * 7 + k)
+    want, inter = _oracle_layer(layer, shape, shared=Is > 0)
+    out, w, idx = gu.run_layer(gu.upload_layer(layer), shape, shared=Is > 0)
+    got_idx = gu.host(idx).astype(np.uint32)
+    _check_indices(got_idx, inter["indices"], inter["choice"], k)
+    same = np.all(got_idx == inter["indices"], axis=1)
+    assert same.sum() >= T - 1
+    np.testing.assert_allclose(gu.host(w)[same], inter["weights"][same], rtol=2e-6, atol=1e-7)
+    assert O.rel_l2(gu.host(out)[same], want[same]) < REL_L2
+
+
+@pytest.mark.parametrize("T", [2, 8])
+def test_moe_layer_mxfp8_shared_expert(gu, T):
+    # an MXFP8 shared expert runs as its own dense MLP before the routed kernels
+    shape = MoEShape("mx8shared", T, 2048, 128, 8, 768, 768)
+    layer = make_layer(shape, 4242 + T)
+    mats = []
+    for key in ("shared.gate", "shared.up", "shared.down"):
+        codes, scales = O.quantize_mx(layer[key], 8, O.MX_RULE_NEAREST)
+        layer[key] = codes
+        layer[key + ".scales"] = scales
+        mats.append(O.dequant_mxfp8(codes, scales))
+    x = O.bf16_bits_to_f32(layer["x"])
+    want, inter = O.moe_layer(x, layer["router_weight"], layer["router_bias"], _bank(layer),
+                              tuple(mats), top_k=shape.k, n_group=1, topk_group=1,
+                              norm_topk_prob=True, routed_scaling_factor=2.5, swiglu_limit=10.0,
+                              return_intermediates=True)
+    out, _, idx = gu.run_layer(gu.upload_layer(layer), shape, shared_fmt=native.GLM_FMT_MXFP8)
+    assert np.array_equal(gu.host(idx).astype(np.uint32), inter["indices"])
+    assert O.rel_l2(gu.host(out), want) < REL_L2
+
+
 def test_moe_layer_prefill_sampled(gu):
     shape = SHAPES["prefill_t4096"]
     layer = make_layer(shape, 5303)
