@@ -1,12 +1,16 @@
 // Building blocks of the weight-streaming MFMA tiles (decode GEMV / skinny GEMM).
 //
 // A wave owns a 16-row tile of W and a K range of CPW chunks of 128.  For
-// chunk c, lane (r = l & 15, q = l >> 4) holds the weights of row r at
-// K = c*128 + 32q .. +31 -- exactly one E8M0 group -- which the gfx950
-// scaled converts turn into four bf16x8 MFMA A-fragments (values exact in
-// bf16).  The B operand is one activation row per token column r (the same
-// K positions), so v_mfma_f32_16x16x32_bf16 does the whole K reduction:
-//   MFMA i, slot s of lane (r, q)  <->  K = c*128 + 32q + 8i + s.
+// chunk c, lane (r = l & 15, q = l >> 4) holds 32 consecutive weights of row
+// r -- exactly one E8M0 group -- which the gfx950 scaled converts turn into
+// four bf16x8 MFMA A-fragments (values exact in bf16).  The B operand is one
+// activation row per token column r at the same K positions, so
+// v_mfma_f32_16x16x32_bf16 does the whole K reduction:
+//   MFMA i, slot s of lane (r, q)  <->  K = kbase + chunk_k(c, q) + 8i + s.
+// chunk_k is c*128 + 32q, except for MXFP4 with an even chunk count, where
+// chunks pair up as (c>>1)*256 + 64q + 32(c&1): the four lanes of a row then
+// read one whole 128-byte line per chunk pair (two 16-byte loads each) rather
+// than half a line per load, which the memory system serves faster.
 // Output lane (r, q) holds rows 4q..4q+3 of the tile for token column r.
 #pragma once
 
@@ -41,19 +45,39 @@ struct WChunk<FMT_BF16> {
   glm_u32x4 v[4];
 };
 
+// The 32 weights of this lane starting at K = kl.
 template <int FMT>
-__device__ __forceinline__ WChunk<FMT> load_chunk(const uint8_t *wrow, int k0, int q) {
+__device__ __forceinline__ WChunk<FMT> load_chunk_at(const uint8_t *wrow, int kl) {
   WChunk<FMT> w;
   if constexpr (FMT == FMT_MXFP4) {
-    w.c = load_stream(wrow + (k0 >> 1) + 16 * q);
+    w.c = load_stream(wrow + (kl >> 1));
   } else if constexpr (FMT == FMT_MXFP8) {
-    w.c0 = load_stream(wrow + k0 + 32 * q);
-    w.c1 = load_stream(wrow + k0 + 32 * q + 16);
+    w.c0 = load_stream(wrow + kl);
+    w.c1 = load_stream(wrow + kl + 16);
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w.v[i] = load_stream(wrow + 2 * (k0 + 32 * q) + 16 * i);
+    for (int i = 0; i < 4; ++i) w.v[i] = load_stream(wrow + 2 * kl + 16 * i);
   }
   return w;
+}
+
+template <int FMT>
+__device__ __forceinline__ WChunk<FMT> load_chunk(const uint8_t *wrow, int k0, int q) {
+  return load_chunk_at<FMT>(wrow, k0 + 32 * q);
+}
+
+template <int FMT, int CPW>
+__host__ __device__ constexpr bool paired_chunks() {
+  return FMT == FMT_MXFP4 && CPW % 2 == 0;
+}
+
+// First K (relative to the wave's kbase) of lane q's 32 weights in chunk c.
+template <int FMT, int CPW>
+__device__ __forceinline__ int chunk_k(int c, int q) {
+  if constexpr (paired_chunks<FMT, CPW>())
+    return (c >> 1) * 256 + 64 * q + 32 * (c & 1);
+  else
+    return c * 128 + 32 * q;
 }
 
 template <int FMT>
@@ -86,8 +110,17 @@ __host__ __device__ constexpr int bf16_batch(int cpw, int max_batch) {
 template <int FMT, int NPROJ, int CPW>
 struct WaveWeights {
   WChunk<FMT> w[NPROJ][CPW];
-  uint32_t sd[NPROJ][CPW];  // scale dwords: byte q of dword c is lane q's group of chunk c
+  uint32_t sd[NPROJ][CPW];  // scale dword holding lane q's group of chunk c (see scale_byte)
 };
+
+// Lane q's E8M0 byte of chunk c within the dword loaded for it.
+template <int FMT, int CPW>
+__device__ __forceinline__ uint32_t scale_byte(uint32_t sd, int c, int q) {
+  if constexpr (paired_chunks<FMT, CPW>())
+    return (sd >> (8 * (2 * (q & 1) + (c & 1)))) & 0xffu;
+  else
+    return (sd >> (8 * q)) & 0xffu;
+}
 
 template <int FMT, int NPROJ, int CPW>
 __device__ __forceinline__ void load_wave_weights(WaveWeights<FMT, NPROJ, CPW> &ww,
@@ -95,15 +128,40 @@ __device__ __forceinline__ void load_wave_weights(WaveWeights<FMT, NPROJ, CPW> &
                                                   const uint8_t *const srow[NPROJ], int kbase,
                                                   int q) {
   static_assert(FMT != FMT_BF16, "bf16 weights are streamed in batches by wave_mma");
+  // Scales first, then the chunks in the order the MFMAs consume them: loads
+  // complete in issue order, so chunk 0 can be converted while later chunks
+  // are still in flight.
+#pragma unroll
+  for (int p = 0; p < NPROJ; ++p) {
+    const uint32_t *s = reinterpret_cast<const uint32_t *>(srow[p] + (kbase >> 5));
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      if constexpr (paired_chunks<FMT, CPW>()) {
+        // groups of chunk pair m: 8 bytes at m*8; lane q's two are bytes 2q, 2q+1
+        if ((c & 1) == 0) ww.sd[p][c] = s[(c >> 1) * 2 + (q >> 1)];
+        else ww.sd[p][c] = ww.sd[p][c - 1];
+      } else {
+        ww.sd[p][c] = s[c];
+      }
+    }
+  }
 #pragma unroll
   for (int c = 0; c < CPW; ++c)
 #pragma unroll
-    for (int p = 0; p < NPROJ; ++p) ww.w[p][c] = load_chunk<FMT>(wrow[p], kbase + c * 128, q);
+    for (int p = 0; p < NPROJ; ++p)
+      ww.w[p][c] = load_chunk_at<FMT>(wrow[p], kbase + chunk_k<FMT, CPW>(c, q));
+}
+
+// B fragments of this lane's 32 activations starting at K = kl.
+__device__ __forceinline__ void load_act_frags_at(const uint16_t *act, int kl, glm_bf16x8 xb[4]) {
+  if (act != nullptr) {
+    const glm_bf16x8 *src = reinterpret_cast<const glm_bf16x8 *>(act + kl);
 #pragma unroll
-  for (int p = 0; p < NPROJ; ++p)
+    for (int i = 0; i < 4; ++i) xb[i] = src[i];
+  } else {
 #pragma unroll
-    for (int c = 0; c < CPW; ++c)
-      ww.sd[p][c] = reinterpret_cast<const uint32_t *>(srow[p] + (kbase >> 5))[c];
+    for (int i = 0; i < 4; ++i) xb[i] = glm_bf16x8{};
+  }
 }
 
 __device__ __forceinline__ void load_act_frags(const uint16_t *act, int k0, int q,
@@ -125,13 +183,14 @@ __device__ __forceinline__ void mma_wave_weights(const WaveWeights<FMT, NPROJ, C
                                                  glm_f32x4 acc[NPROJ]) {
   glm_bf16x8 xb[CPW][4];
 #pragma unroll
-  for (int c = 0; c < CPW; ++c) load_act_frags(act, kbase + c * 128, q, xb[c]);
+  for (int c = 0; c < CPW; ++c)
+    load_act_frags_at(act == nullptr ? nullptr : act + kbase + chunk_k<FMT, CPW>(c, q), 0, xb[c]);
 #pragma unroll
   for (int c = 0; c < CPW; ++c) {
 #pragma unroll
     for (int p = 0; p < NPROJ; ++p) {
       glm_bf16x8 a[4];
-      chunk_frags<FMT>(ww.w[p][c], (ww.sd[p][c] >> (8 * q)) & 0xffu, a);
+      chunk_frags<FMT>(ww.w[p][c], scale_byte<FMT, CPW>(ww.sd[p][c], c, q), a);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], xb[c][i], acc[p], 0, 0, 0);
@@ -149,19 +208,11 @@ __device__ __forceinline__ void mma_wave_weights_lds(const WaveWeights<FMT, NPRO
 #pragma unroll
   for (int c = 0; c < CPW; ++c) {
     glm_bf16x8 xb[4];
-    if (s_row != nullptr) {
-      const glm_bf16x8 *src =
-          reinterpret_cast<const glm_bf16x8 *>(s_row + kbase + c * 128 + 32 * q);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) xb[i] = src[i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) xb[i] = glm_bf16x8{};
-    }
+    load_act_frags_at(s_row == nullptr ? nullptr : s_row + kbase + chunk_k<FMT, CPW>(c, q), 0, xb);
 #pragma unroll
     for (int p = 0; p < NPROJ; ++p) {
       glm_bf16x8 a[4];
-      chunk_frags<FMT>(ww.w[p][c], (ww.sd[p][c] >> (8 * q)) & 0xffu, a);
+      chunk_frags<FMT>(ww.w[p][c], scale_byte<FMT, CPW>(ww.sd[p][c], c, q), a);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], xb[i], acc[p], 0, 0, 0);

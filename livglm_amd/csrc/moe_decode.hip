@@ -22,10 +22,10 @@
 //                             selects token t's experts from its logits, then
 //                             the block computes gate/up + SwiGLU of expert j
 //                             for that token; extra blocks: shared down tiles.
-//   3. down_combine_kernel    block = (token, 16 rows of d): each wave runs the
-//                             down projection of k/4 of the token's experts,
-//                             and the weighted merge + shared add happen in
-//                             LDS in the combine's order.
+//   3. down_combine_kernel    block = (token, 16 rows of d): wave j runs the
+//                             down projection of the token's expert j, and the
+//                             weighted merge + shared add happen in LDS in the
+//                             combine's order.
 //
 // Every kernel boundary is a stream-ordered dependency; nothing synchronises
 // across blocks inside a kernel, and every reduction runs in one fixed order.
@@ -62,39 +62,27 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Sortable key of a (choice, expert) pair: larger key = better candidate
-// (larger value; on equal values the larger index, as a stable ascending
-// argsort ranks it, moe.py:33-34).  -inf sorts below every finite value.
-__device__ __forceinline__ uint64_t choice_key(float v, int e) {
-  const uint32_t b = __float_as_uint(v);
-  const uint32_t u = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  return ((uint64_t)u << 32) | (uint32_t)e;
-}
-
 template <int CTRL>
-__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xf, 0xf, false);
-  const uint32_t hi =
-      (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, false);
-  return ((uint64_t)hi << 32) | lo;
+__device__ __forceinline__ int dpp_i32(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, true);
 }
 
-__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
-  return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l) << 32) |
-         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+// Maximum of an int over the wave: DPP within each row of 16 lanes (quad
+// swaps, then row rotations by 4 and 8), then the four row maxima in SALU.
+__device__ __forceinline__ int wave_max_i32(int v) {
+  v = max(v, dpp_i32<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = max(v, dpp_i32<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = max(v, dpp_i32<0x124>(v));  // row_ror:4
+  v = max(v, dpp_i32<0x128>(v));  // row_ror:8
+  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
 
-__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-
-// Maximum of a u64 over the wave: DPP within each row of 16 lanes (quad
-// swaps, then row rotations by 4 and 8), then the four row maxima.
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  v = max_u64(v, dpp_u64<0xB1>(v));   // quad_perm [1,0,3,2]
-  v = max_u64(v, dpp_u64<0x4E>(v));   // quad_perm [2,3,0,1]
-  v = max_u64(v, dpp_u64<0x124>(v));  // row_ror:4
-  v = max_u64(v, dpp_u64<0x128>(v));  // row_ror:8
-  return max_u64(max_u64(readlane_u64(v, 0), readlane_u64(v, 16)),
-                 max_u64(readlane_u64(v, 32), readlane_u64(v, 48)));
+// Signed-int key with the order of a non-NaN float (-0 must be folded to +0
+// first so that equal floats have equal keys).
+__device__ __forceinline__ int order_key(float v) {
+  const int b = __float_as_int(v);
+  return b >= 0 ? b : b ^ 0x7fffffff;
 }
 
 // Top-k selection of one token by one wave (moe.py:39-62).  Lane l holds
@@ -154,24 +142,52 @@ __device__ void select_token(const float *logits_row, const float *bias, int E, 
       if (e < E && !s_keep[e / per]) choice[i] = -INFINITY;
     }
   }
-  // k rounds of a wave-wide max over the candidates' keys; the winner of
-  // round r lands in ascending column k-1-r and drops out (key 0).
-  uint64_t key[EPL];
+  // k rounds: the wave maximum of the remaining choices, then, among the
+  // experts holding it, the largest index (a stable ascending argsort ranks
+  // equal values by index, moe.py:33-34).  The winner of round r lands in
+  // ascending column k-1-r and drops out.  NaN choices rank as -inf; absent
+  // and chosen experts hold INT_MIN, below every real key.
+  int key[EPL];
 #pragma unroll
-  for (int i = 0; i < EPL; ++i) key[i] = lane + 64 * i < E ? choice_key(choice[i], lane + 64 * i) : 0;
+  for (int i = 0; i < EPL; ++i) {
+    const float c = choice[i] != choice[i] ? -INFINITY : choice[i] + 0.0f;  // NaN -> -inf, -0 -> +0
+    key[i] = lane + 64 * i < E ? order_key(c) : INT_MIN;
+  }
+  // Branch-free rounds: lane k-1-r keeps round r's expert and score.
+  int my_idx = 0;
+  float my_w = 0.0f;
   for (int r = 0; r < k; ++r) {
-    uint64_t best = key[0];
+    int m = key[0];
 #pragma unroll
-    for (int i = 1; i < EPL; ++i) best = key[i] > best ? key[i] : best;
-    const uint64_t win = wave_max_u64(best);
+    for (int i = 1; i < EPL; ++i) m = max(m, key[i]);
+    const int best = wave_max_i32(m);
+    unsigned long long bal = 0ull;
+    int slot = 0;
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
-      if (key[i] == win) {
-        s_isel[k - 1 - r] = lane + 64 * i;
-        s_wsel[k - 1 - r] = score[i];
-        key[i] = 0;
+      const unsigned long long b = __ballot(key[i] == best);
+      if (b != 0ull) {  // wave-uniform: the highest matching slot wins
+        bal = b;
+        slot = i;
       }
     }
+    const int wl = 63 - __clzll((long long)bal);
+    float sc = score[0];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      if (i == slot) {
+        sc = score[i];
+        if (lane == wl) key[i] = INT_MIN;
+      }
+    }
+    const float wsc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc), wl));
+    const bool mine = lane == k - 1 - r;
+    my_idx = mine ? wl + 64 * slot : my_idx;
+    my_w = mine ? wsc : my_w;
+  }
+  if (lane < k) {
+    s_isel[lane] = my_idx;
+    s_wsel[lane] = my_w;
   }
   wave_lds_sync();
   // every lane forms the same sequential sum; lane j < k writes column j
@@ -186,6 +202,48 @@ __device__ void select_token(const float *logits_row, const float *bias, int E, 
     pair_idx[lane] = s_isel[lane];
   }
   wave_lds_sync();
+}
+
+// Block-wide top-k of one token without group masks (n_group == 1, E <= 256),
+// for the token-major path where every block needs one token's choice: an
+// expert's rank is the number of experts that beat it -- a larger choice, or an
+// equal choice and a larger index, as the stable ascending argsort of
+// moe.py:33-34 orders them -- counted by all 256 threads at once (two per
+// expert when E <= 128).  The expert of rank r lands in column k-1-r: s_sel[j]
+// gets column j's expert, s_wsel[j] its sigmoid score.  NaN choices rank as
+// -inf.  Called uniformly by the block; three barriers inside.
+__device__ void select_ranked(const float *logits_row, const float *bias, int E, int k,
+                              long long *s_key, float *s_score, int *s_cnt, int *s_sel,
+                              float *s_wsel) {
+  const int tid = threadIdx.x;
+  if (tid < E) {
+    const float sc = sigmoid_f32(logits_row[tid]);
+    const float ch = sc + bias[tid];
+    const float c = ch != ch ? -INFINITY : ch + 0.0f;  // NaN -> -inf, -0 -> +0
+    s_key[tid] = ((long long)order_key(c) << 32) | (unsigned)tid;
+    s_score[tid] = sc;
+  }
+  __syncthreads();
+  const bool split = E <= 128;
+  const int c = split ? (tid & 127) : tid;
+  const int o0 = split ? (tid >> 7) * 64 : 0;
+  const int o1 = split ? min(o0 + 64, E) : E;
+  int cnt = 0;
+  if (c < E) {
+    const long long kc = s_key[c];
+#pragma unroll 8
+    for (int o = o0; o < o1; ++o) cnt += s_key[o] > kc ? 1 : 0;  // o is wave-uniform: broadcast
+  }
+  s_cnt[tid] = cnt;
+  __syncthreads();
+  if (tid < E) {
+    const int rank = split ? s_cnt[tid] + s_cnt[tid + 128] : s_cnt[tid];
+    if (rank < k) {
+      s_sel[k - 1 - rank] = tid;
+      s_wsel[k - 1 - rank] = s_score[tid];
+    }
+  }
+  __syncthreads();
 }
 
 // Exclusive scan over a 256-thread block (4 waves); *total gets the sum.
@@ -596,16 +654,43 @@ __global__ __launch_bounds__(256) void select_gate_up_kernel(PairArgs a, SharedA
   const int tile = blockIdx.x % tiles;
   const int pr = blockIdx.x / tiles;  // pair t*k + j
   const int t = pr / k, j = pr % k;
+  const bool first = j == 0 && tile == 0;  // one block per token publishes the route
   uint16_t *s_x = s_dyn;  // token t's row
-  stage_rows(s_x, a.x + (size_t)t * d, nullptr, 1, d);
-  if (wave == 0) {
-    const bool first = j == 0 && tile == 0;  // one block per token publishes the route
-    float *scratch = reinterpret_cast<float *>(s_dyn + lds_row_stride(d));
-    select_token<EPL>(a.logits + (size_t)t * E, a.bias, E, k, a.n_group, a.topk_group, a.norm,
-                      a.scale, first ? a.weights + (size_t)t * k : nullptr,
-                      first ? a.indices + (size_t)t * k : nullptr, s_sel, scratch, lane);
+  if (a.n_group == 1 && E <= 256) {
+    // all waves rank the experts; the token row is staged meanwhile
+    __shared__ long long s_key[256];
+    __shared__ float s_score[256];
+    __shared__ int s_cnt[256];
+    __shared__ float s_wsel[kPairMaxK];
+    const glm_u32x4 *src = reinterpret_cast<const glm_u32x4 *>(a.x + (size_t)t * d);
+    for (int i = threadIdx.x; i < d / 8; i += blockDim.x)
+      reinterpret_cast<glm_u32x4 *>(s_x)[i] = src[i];
+    select_ranked(a.logits + (size_t)t * E, a.bias, E, k, s_key, s_score, s_cnt, s_sel, s_wsel);
+    if (first && wave == 0) {
+      // every lane forms the same sequential sum (moe.py:53-57); lane j < k writes column j
+      const float wl = lane < k ? s_wsel[lane] : 0.0f;
+      float total = 0.0f;
+      if (a.norm)
+        for (int jj = 0; jj < k; ++jj)
+          total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), jj));
+      if (lane < k) {
+        a.weights[(size_t)t * k + lane] = (a.norm ? wl / (total + 1e-20f) : wl) * a.scale;
+        a.indices[(size_t)t * k + lane] = (uint32_t)s_sel[lane];
+      }
+    }
+  } else {
+    if (wave > 0) {  // waves 1-3 stage the token row while wave 0 selects
+      const glm_u32x4 *src = reinterpret_cast<const glm_u32x4 *>(a.x + (size_t)t * d);
+      for (int i = threadIdx.x - 64; i < d / 8; i += blockDim.x - 64)
+        reinterpret_cast<glm_u32x4 *>(s_x)[i] = src[i];
+    } else {
+      float *scratch = reinterpret_cast<float *>(s_dyn + lds_row_stride(d));
+      select_token<EPL>(a.logits + (size_t)t * E, a.bias, E, k, a.n_group, a.topk_group, a.norm,
+                        a.scale, first ? a.weights + (size_t)t * k : nullptr,
+                        first ? a.indices + (size_t)t * k : nullptr, s_sel, scratch, lane);
+    }
+    __syncthreads();
   }
-  __syncthreads();
   const long long e = s_sel[j];
   const int row0 = tile * 16;
   const int kbase = wave * CPW * 128;
@@ -641,31 +726,30 @@ struct PairDownArgs {
 
 // Down projection of all k experts of one token on 16 rows of d, merged in
 // the combine's order: out = sum_j f32(bf16(y_j)) * w_j (sequential j, no
-// contraction) + shared, where shared = bf16 of its partial sums added in order.
-template <int CPW_R, int JPW>
-__global__ __launch_bounds__(256) void down_combine_kernel(PairDownArgs a) {
+// contraction) + shared, where shared = bf16 of its partial sums added in
+// order.  Wave j (of max(k, 4)) owns expert j over the full K = I.
+template <int CPW_R>
+__global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ __attribute__((aligned(16))) uint16_t s_h[];  // [k][lds_row_stride(I)]
   __shared__ float s_p[kPairMaxK][16];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, j = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int k = a.k, d = a.d, I = a.I;
   const int tiles = d / 16;
   const int t = blockIdx.x / tiles;
   const int row0 = (blockIdx.x % tiles) * 16;
-  WaveWeights<FMT_MXFP4, 1, CPW_R> ww[JPW];
-  float wj[JPW];
-#pragma unroll
-  for (int s = 0; s < JPW; ++s) {
-    const int j = wave + 4 * s;
-    wj[s] = 0.0f;
-    if (j < k) {
-      const long long e = a.indices[(size_t)t * k + j];
-      wj[s] = a.weights[(size_t)t * k + j];
-      const uint8_t *wrow[1] = {a.dw + e * a.w_stride + (size_t)(row0 + r) * (I / 2)};
-      const uint8_t *srow[1] = {a.ds + e * a.s_stride + (size_t)(row0 + r) * (I / 32)};
-      load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww[s], wrow, srow, 0, q);
-    }
+  // h rows first: they do not depend on the route, and LDS staging must not
+  // queue behind the weight stream
+  stage_rows(s_h, a.h + (size_t)t * k * I, nullptr, k, I);
+  WaveWeights<FMT_MXFP4, 1, CPW_R> ww;
+  float wj = 0.0f;
+  if (j < k) {
+    const long long e = a.indices[(size_t)t * k + j];
+    wj = a.weights[(size_t)t * k + j];
+    const uint8_t *wrow[1] = {a.dw + e * a.w_stride + (size_t)(row0 + r) * (I / 2)};
+    const uint8_t *srow[1] = {a.ds + e * a.s_stride + (size_t)(row0 + r) * (I / 32)};
+    load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
   }
   // the shared expert's contribution to these 16 outputs (thread c < 16)
   float shared_v = 0.0f;
@@ -679,25 +763,20 @@ __global__ __launch_bounds__(256) void down_combine_kernel(PairDownArgs a) {
       shared_v = bf16_to_f32(a.shared[(size_t)t * d + c]);
     }
   }
-  stage_rows(s_h, a.h + (size_t)t * k * I, nullptr, k, I);
   __syncthreads();
+  if (j < k) {
+    glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
+    mma_wave_weights_lds<FMT_MXFP4, 1, CPW_R>(ww, 0, q, r == 0 ? s_h + j * lds_row_stride(I) : nullptr,
+                                              acc);
+    if (r == 0) {
 #pragma unroll
-  for (int s = 0; s < JPW; ++s) {
-    const int j = wave + 4 * s;
-    if (j < k) {
-      glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
-      mma_wave_weights_lds<FMT_MXFP4, 1, CPW_R>(
-          ww[s], 0, q, r == 0 ? s_h + j * lds_row_stride(I) : nullptr, acc);
-      if (r == 0) {
-#pragma unroll
-        for (int m = 0; m < 4; ++m) s_p[j][4 * q + m] = bf16_round(acc[0][m]) * wj[s];
-      }
+      for (int m = 0; m < 4; ++m) s_p[j][4 * q + m] = bf16_round(acc[0][m]) * wj;
     }
   }
   __syncthreads();
   if (threadIdx.x < 16) {
     float o = 0.0f;
-    for (int j = 0; j < k; ++j) o = o + s_p[j][threadIdx.x];
+    for (int jj = 0; jj < k; ++jj) o = o + s_p[jj][threadIdx.x];
     if (a.shared_parts != nullptr || a.shared != nullptr) o = o + shared_v;
     a.out[(size_t)t * d + c] = o;
   }
@@ -993,21 +1072,14 @@ int glm_pair_path_launch(hipStream_t stream, const uint16_t *x, int T, int d, co
   b.nparts = sg ? sh.skd : 0;
   b.out = out;
   const size_t lds3 = (size_t)k * lds_row_stride(I) * 2;
-  const dim3 g3(T * (d / 16));
-#define GLM_PAIR_DN(JPW)                                                                       \
-  switch (I / 128) {                                                                           \
-    case 1: hipLaunchKernelGGL((down_combine_kernel<1, JPW>), g3, dim3(256), lds3, stream, b); break; \
-    case 2: hipLaunchKernelGGL((down_combine_kernel<2, JPW>), g3, dim3(256), lds3, stream, b); break; \
-    case 4: hipLaunchKernelGGL((down_combine_kernel<4, JPW>), g3, dim3(256), lds3, stream, b); break; \
-    case 6: hipLaunchKernelGGL((down_combine_kernel<6, JPW>), g3, dim3(256), lds3, stream, b); break; \
-    default: hipLaunchKernelGGL((down_combine_kernel<8, JPW>), g3, dim3(256), lds3, stream, b); break; \
+  const dim3 g3(T * (d / 16)), b3(64 * std::max(k, 4));
+  switch (I / 128) {
+    case 1: hipLaunchKernelGGL((down_combine_kernel<1>), g3, b3, lds3, stream, b); break;
+    case 2: hipLaunchKernelGGL((down_combine_kernel<2>), g3, b3, lds3, stream, b); break;
+    case 4: hipLaunchKernelGGL((down_combine_kernel<4>), g3, b3, lds3, stream, b); break;
+    case 6: hipLaunchKernelGGL((down_combine_kernel<6>), g3, b3, lds3, stream, b); break;
+    default: hipLaunchKernelGGL((down_combine_kernel<8>), g3, b3, lds3, stream, b); break;
   }
-  if (k <= 4) {
-    GLM_PAIR_DN(1)
-  } else {
-    GLM_PAIR_DN(2)
-  }
-#undef GLM_PAIR_DN
   GLM_LAUNCH_CHECK("down_combine_kernel");
   return GLM_OK;
 }

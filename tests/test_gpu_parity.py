@@ -296,6 +296,45 @@ def test_routed_experts_generic_shapes(gu):
         assert np.mean(y_got == y_want) > 0.95
 
 
+def _swiglu_gpu(gu, g_bits, u_bits, limit):
+    torch = _torch()
+    out = torch.empty(g_bits.size, dtype=torch.bfloat16, device="cuda")
+    gu.call("glm_limited_swiglu", gu.stream(), gu.p(gu.to_dev(g_bits)), gu.p(gu.to_dev(u_bits)),
+            g_bits.size, limit, gu.p(out))
+    return gu.bf16_bits(out)
+
+
+def test_limited_swiglu_rounding_bit_exact(gu):
+    # gates in [9, 10] have bf16(sigmoid) == 1 exactly, so each output is the
+    # round-to-nearest-even bf16 of the exact f32 product g*u: ties, subnormal
+    # and normal results, both signs
+    rng = np.random.default_rng(17)
+    n = 1 << 16
+    g = O.f32_to_bf16_bits(rng.uniform(9.0, 10.0, n).astype(np.float32))
+    u = np.concatenate([rng.normal(0, 1, n // 4), rng.normal(0, 1, n // 4) * 1e-38,
+                        rng.normal(0, 1, n // 4) * 1e-36, rng.uniform(-10, 10, n // 4)])
+    u = O.f32_to_bf16_bits(u.astype(np.float32))
+    want = O.f32_to_bf16_bits(O.limited_swiglu_bf16(O.bf16_bits_to_f32(g),
+                                                    O.bf16_bits_to_f32(u), 10.0))
+    got = _swiglu_gpu(gu, g, u, 10.0)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_limited_swiglu_general(gu):
+    # any gate: the f32 sigmoid may differ from the oracle's exp by an ulp, which
+    # moves bf16(sigmoid) only when it lies on a rounding boundary
+    rng = np.random.default_rng(18)
+    n = 1 << 16
+    g = O.f32_to_bf16_bits((rng.normal(0, 4, n)).astype(np.float32))
+    u = O.f32_to_bf16_bits((rng.normal(0, 4, n)).astype(np.float32))
+    for limit in (7.0, 0.0):
+        want = O.f32_to_bf16_bits(O.limited_swiglu_bf16(O.bf16_bits_to_f32(g),
+                                                        O.bf16_bits_to_f32(u), limit))
+        got = _swiglu_gpu(gu, g, u, limit)
+        assert np.mean(got == want) > 0.999
+        assert np.max(np.abs(got.astype(np.int32) - want.astype(np.int32))) <= 1
+
+
 def test_combine_bit_exact(gu):
     torch = _torch()
     rng = np.random.default_rng(3)
