@@ -1,25 +1,35 @@
 """Benchmark of the MI355X routed-MoE layer (one GPU).
 
-A step is one MoE layer forward (router -> dispatch -> MXFP4 gate/up + SwiGLU
--> down -> shared expert -> combine) over one batch of synthetic tokens whose
-weights are already resident in HBM.  Steps rotate over several independent
-layer banks (>= 2 GB in total) and token batches so that expert reads come from
-HBM rather than the 256 MB Infinity Cache.  The timed steps run as one HIP
-graph, bracketed by synchronisation and HIP events.
+A step is one MoE layer forward over one batch of synthetic tokens whose
+weights are already resident in HBM: router -> top-k -> MXFP4 gate/up + SwiGLU
+-> down -> bf16 shared expert -> weighted combine (with T <= 4 tokens the layer
+runs token-major in three kernels; larger batches add the dispatch).  Steps
+rotate over several independent layer banks (>= 4 GB in total) and token
+batches so that expert reads come from HBM rather than the 256 MB Infinity
+Cache.  The timed steps run as one HIP graph, bracketed by synchronisation and
+HIP events.
 
-Prints one JSON line: the layer's tokens/s (``value``), plus the roofline of
-the dominant kernel (the routed gate/up MXFP4 GEMV, timed live with HIP events
-over a graph of back-to-back launches) and the CPU baseline (the C restatement
-in oracle/, OpenMP, on this host) on a bounded sample of the same workload.
+Prints one JSON line: the layer's tokens/s (``value``), the roofline of the
+dominant kernel (the routed MXFP4 gate/up kernel, timed live with HIP events
+over a graph of back-to-back launches; its HBM traffic from two rocprofv3
+counter passes, FETCH_SIZE then WRITE_SIZE, scaled by the same counters over a
+copy of known size), and the CPU baseline (the C restatement in oracle/,
+OpenMP, on this host) on a bounded sample of the same workload.
 """
 
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import math
 import os
+import shutil
+import signal
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -29,7 +39,7 @@ for _p in (ROOT, os.path.join(ROOT, "src")):
 
 METRIC = "MoE layer tokens/s; decode expert HBM GB/s; MXFP4 MFMA util at T=4096"
 HBM_PEAK_GBPS = 8000.0
-MFMA_PEAK = {"bf16": 2500.0, "fp8": 5000.0, "fp4": 10100.0}  # TFLOP/s, dense
+COPY_BYTES = 256 << 20  # counter calibration: one device copy of this size
 
 
 def parse_args():
@@ -38,181 +48,233 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--workload", default="verify_t2",
-                    help="decode_t1 | verify_t2 | batch_t64 | prefill_t4096")
+                    help="decode_t1 | verify_t2 | batch_t64")
     ap.add_argument("--min-rotation-gb", type=float, default=4.0,
                     help="total size of the distinct layer banks the steps rotate over")
     ap.add_argument("--kernel-launches", type=int, default=128)
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="budget of the CPU-baseline sample (0 disables it)")
+    ap.add_argument("--traffic", type=int, default=1,
+                    help="1: measure the dominant kernel's HBM traffic with rocprofv3 counters")
     ap.add_argument("--seed", type=int, default=5301)
+    # internal: the child runs of the counter passes
+    ap.add_argument("--mode", default="full", choices=["full", "kernel", "copy"],
+                    help=argparse.SUPPRESS)
     return ap.parse_args()
+
+
+class Setup:
+    """Resident layer banks, token batches and per-launch routes of one workload."""
+
+    def __init__(self, args, torch, np):
+        from livglm_amd import native
+        from livglm_amd.workloads import BANK_KEYS, SHAPES
+
+        self.torch, self.np, self.native, self.keys = torch, np, native, BANK_KEYS
+        self.lib = native.load()
+        self.shape = shape = SHAPES[args.workload]
+        T, d, E, k, I, Is = shape.T, shape.d, shape.E, shape.k, shape.I, shape.I_shared
+        self.T, self.d, self.E, self.k, self.I, self.Is = T, d, E, k, I, Is
+        self.dev = dev = torch.device("cuda:0")
+        torch.cuda.set_device(dev)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(args.seed)
+        self.layer_bytes = shape.bank_bytes + 3 * Is * d * 2 + E * d * 4
+        self.n_banks = max(2, math.ceil(args.min_rotation_gb * 1e9 / self.layer_bytes))
+        self.n_inputs = 64
+
+        def randbytes(*s):
+            return torch.randint(0, 256, s, dtype=torch.uint8, device=dev, generator=gen)
+
+        def randscales(*s):
+            return torch.randint(119, 128, s, dtype=torch.uint8, device=dev, generator=gen)
+
+        def bf16(*s):
+            return (torch.randn(s, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+
+        self.banks = []
+        for _ in range(self.n_banks):
+            b = {
+                "gate_proj.weight_packed": randbytes(E, I, d // 2),
+                "gate_proj.weight_scale": randscales(E, I, d // 32),
+                "up_proj.weight_packed": randbytes(E, I, d // 2),
+                "up_proj.weight_scale": randscales(E, I, d // 32),
+                "down_proj.weight_packed": randbytes(E, d, I // 2),
+                "down_proj.weight_scale": randscales(E, d, I // 32),
+                "router_weight": torch.randn((E, d), device=dev, generator=gen) * 0.02,
+                "router_bias": torch.zeros(E, device=dev),
+                "shared.gate": bf16(Is, d),
+                "shared.up": bf16(Is, d),
+                "shared.down": bf16(d, Is),
+            }
+            if shape.routing == "zipf":
+                from livglm_amd.workloads import zipf_bias
+                b["router_bias"] = torch.from_numpy(
+                    zipf_bias(E, np.random.default_rng(args.seed + len(self.banks)))).to(dev)
+            self.banks.append(b)
+        self.xs = torch.randn((self.n_inputs, T, d), device=dev, generator=gen).to(torch.bfloat16)
+        self.few_token = T <= 4 and k <= 8  # the layer runs token-major (no dispatch)
+
+    @property
+    def stream(self) -> int:
+        """The current stream at call time (graph capture switches it)."""
+        return self.torch.cuda.current_stream().cuda_stream
+
+    # ------------------------------------------------------------ dominant kernel
+    def kernel_plans(self, R: int) -> None:
+        """Routes launch r's batch once (router, plus the dispatch where the
+        kernel needs it)."""
+        torch, native = self.torch, self.native
+        T, d, E, k, P = self.T, self.d, self.E, self.k, self.T * self.k
+        i32 = dict(dtype=torch.int32, device=self.dev)
+        self.plans = []
+        for r in range(R):
+            b, x = self.banks[r % self.n_banks], self.xs[r % self.n_inputs]
+            pl = {"logits": torch.empty((T, E), dtype=torch.float32, device=self.dev),
+                  "w": torch.empty((T, k), dtype=torch.float32, device=self.dev),
+                  "ix": torch.empty((T, k), **i32)}
+            native.call("glm_router_topk", self.stream, x.data_ptr(), T, d,
+                        b["router_weight"].data_ptr(), b["router_bias"].data_ptr(), E, k,
+                        self.shape.n_group, self.shape.topk_group, 1,
+                        self.shape.routed_scaling_factor, pl["logits"].data_ptr(),
+                        pl["w"].data_ptr(), pl["ix"].data_ptr())
+            if not self.few_token:
+                pl.update({n: torch.empty(sz, **i32) for n, sz in
+                           [("counts", E), ("offsets", E + 1), ("perm", P), ("inv", P),
+                            ("tok", P), ("active", E), ("nact", 1), ("work", 4 * E),
+                            ("status", 1)]})
+                native.call("glm_moe_dispatch", self.stream, pl["ix"].data_ptr(), T, k, E,
+                            *(pl[n].data_ptr() for n in ("counts", "offsets", "perm", "inv",
+                                                          "tok", "active", "nact", "work",
+                                                          "status")))
+            self.plans.append(pl)
+        torch.cuda.synchronize()
+        self.unique = [len(self.np.unique(pl["ix"].cpu().numpy())) for pl in self.plans]
+        self.h = torch.empty((P, self.I), dtype=torch.bfloat16, device=self.dev)
+        self.w_k = torch.empty((T, k), dtype=torch.float32, device=self.dev)
+        self.i_k = torch.empty((T, k), **i32)
+
+    def gate_up(self, r: int) -> None:
+        b, pl, x = self.banks[r % self.n_banks], self.plans[r], self.xs[r % self.n_inputs]
+        sh, native = self.shape, self.native
+        if self.few_token:
+            native.call("glm_route_gate_up", self.stream, pl["logits"].data_ptr(),
+                        b["router_bias"].data_ptr(), self.T, self.E, self.k, sh.n_group,
+                        sh.topk_group, 1, sh.routed_scaling_factor, x.data_ptr(), self.d, self.I,
+                        *(b[key].data_ptr() for key in self.keys[:4]), sh.swiglu_limit,
+                        self.w_k.data_ptr(), self.i_k.data_ptr(), self.h.data_ptr())
+        else:
+            native.call("glm_expert_gate_up", self.stream, x.data_ptr(), self.T, self.d, self.I,
+                        self.E, self.k, *(b[key].data_ptr() for key in self.keys[:4]),
+                        pl["tok"].data_ptr(), pl["work"].data_ptr(), sh.swiglu_limit,
+                        self.h.data_ptr())
+
+    def kernel_name(self) -> str:
+        """The dominant kernel's instantiation, as rocprofv3 names it."""
+        d, E = self.d, self.E
+        if self.few_token:
+            epl = 2 if E <= 128 else (4 if E <= 256 else 8)
+            return f"select_gate_up_kernel<{epl}, {d // 512}, 1>"
+        return f"decode_gate_up_kernel<{d // 512}>"
+
+    def kernel_bytes(self, r: int) -> int:
+        """Algorithmic bytes of launch r: the codes and E8M0 scales of the
+        gate and up projections of every distinct routed expert, once."""
+        proj = self.I * self.d // 2 + self.I * self.d // 32
+        return self.unique[r] * 2 * proj
 
 
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU runs are not part of "
-                                   "it (see DESIGN.md: how the layer would shard by expert)",
+                                   "it (DESIGN.md describes how the layer would shard by expert)",
                           "n_gpus": args.gpus}))
         return 2
 
     import numpy as np
     import torch
 
-    from livglm_amd import native
-    from livglm_amd.workloads import BANK_KEYS, SHAPES
-
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         return 1
-    lib = native.load()
-    shape = SHAPES[args.workload]
-    T, d, E, k, I, Is = shape.T, shape.d, shape.E, shape.k, shape.I, shape.I_shared
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(args.seed)
+    if args.mode == "copy":
+        return copy_probe(torch)
+    S = Setup(args, torch, np)
+    R = args.kernel_launches
+    S.kernel_plans(R)
+    if args.mode == "kernel":
+        for r in range(R):
+            S.gate_up(r)
+        torch.cuda.synchronize()
+        return 0
 
-    # ------------------------------------------------------------ resident layer banks
-    layer_bytes = shape.bank_bytes + 3 * Is * d * 2 + E * d * 4
-    n_banks = max(2, math.ceil(args.min_rotation_gb * 1e9 / layer_bytes))
-    n_inputs = 64
-
-    def randbytes(*s):
-        return torch.randint(0, 256, s, dtype=torch.uint8, device=dev, generator=gen)
-
-    def randscales(*s):
-        return torch.randint(119, 128, s, dtype=torch.uint8, device=dev, generator=gen)
-
-    banks = []
-    for _ in range(n_banks):
-        b = {
-            "gate_proj.weight_packed": randbytes(E, I, d // 2),
-            "gate_proj.weight_scale": randscales(E, I, d // 32),
-            "up_proj.weight_packed": randbytes(E, I, d // 2),
-            "up_proj.weight_scale": randscales(E, I, d // 32),
-            "down_proj.weight_packed": randbytes(E, d, I // 2),
-            "down_proj.weight_scale": randscales(E, d, I // 32),
-            "router_weight": torch.randn((E, d), device=dev, generator=gen) * 0.02,
-            "router_bias": torch.zeros(E, device=dev),
-            "shared.gate": (torch.randn((Is, d), device=dev, generator=gen) * 0.02).to(torch.bfloat16),
-            "shared.up": (torch.randn((Is, d), device=dev, generator=gen) * 0.02).to(torch.bfloat16),
-            "shared.down": (torch.randn((d, Is), device=dev, generator=gen) * 0.02).to(torch.bfloat16),
-        }
-        if shape.routing == "zipf":
-            from livglm_amd.workloads import zipf_bias
-            b["router_bias"] = torch.from_numpy(
-                zipf_bias(E, np.random.default_rng(args.seed + len(banks)))).to(dev)
-        banks.append(b)
-    xs = torch.randn((n_inputs, T, d), device=dev, generator=gen).to(torch.bfloat16)
-
-    ws_bytes = lib.glm_moe_workspace_bytes(T, d, E, k, I, Is)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    native.call("glm_moe_workspace_init", torch.cuda.current_stream().cuda_stream, ws.data_ptr(),
-                ws_bytes)
-    out = torch.empty((T, d), dtype=torch.float32, device=dev)
-    wts = torch.empty((T, k), dtype=torch.float32, device=dev)
-    idx = torch.empty((T, k), dtype=torch.int32, device=dev)
+    native, keys = S.native, S.keys
+    T, d, E, k, I, Is, shape = S.T, S.d, S.E, S.k, S.I, S.Is, S.shape
+    ws_bytes = S.lib.glm_moe_workspace_bytes(T, d, E, k, I, Is)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=S.dev)
+    native.call("glm_moe_workspace_init", S.stream, ws.data_ptr(), ws_bytes)
+    out = torch.empty((T, d), dtype=torch.float32, device=S.dev)
+    wts = torch.empty((T, k), dtype=torch.float32, device=S.dev)
+    idx = torch.empty((T, k), dtype=torch.int32, device=S.dev)
 
     def layer_step(s: int) -> None:
-        b = banks[s % n_banks]
-        x = xs[s % n_inputs]
+        b = S.banks[s % S.n_banks]
+        x = S.xs[s % S.n_inputs]
         native.call(
-            "glm_moe_forward", torch.cuda.current_stream().cuda_stream, x.data_ptr(), T, d,
-            b["router_weight"].data_ptr(), b["router_bias"].data_ptr(), E, k, shape.n_group,
-            shape.topk_group, int(shape.norm_topk_prob), shape.routed_scaling_factor, I,
-            *(b[key].data_ptr() for key in BANK_KEYS), Is, native.GLM_FMT_BF16,
+            "glm_moe_forward", S.stream, x.data_ptr(), T, d, b["router_weight"].data_ptr(),
+            b["router_bias"].data_ptr(), E, k, shape.n_group, shape.topk_group,
+            int(shape.norm_topk_prob), shape.routed_scaling_factor, I,
+            *(b[key].data_ptr() for key in keys), Is, native.GLM_FMT_BF16,
             b["shared.gate"].data_ptr(), None, b["shared.up"].data_ptr(), None,
             b["shared.down"].data_ptr(), None, None, shape.swiglu_limit, ws.data_ptr(), ws_bytes,
             out.data_ptr(), wts.data_ptr(), idx.data_ptr())
 
-    def capture(first: int, count: int):
+    def capture(fn, first: int, count: int):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for s in range(first, first + count):
-                layer_step(s)
+                fn(s)
         return g
 
+    def timed(g, count: int):
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        wall0 = time.perf_counter()
+        ev0.record()
+        g.replay()
+        ev1.record()
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) / count, time.perf_counter() - wall0
+
     # eager pass over every bank first (validates the launches outside capture)
-    for s in range(n_banks):
+    for s in range(S.n_banks):
         layer_step(s)
     torch.cuda.synchronize()
 
     # ------------------------------------------------------------ timed layer steps
     if args.warmup > 0:
-        gw = capture(0, args.warmup)
-        gw.replay()
-    gt = capture(args.warmup, args.steps)
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    wall0 = time.perf_counter()
-    ev0.record()
-    gt.replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    elapsed_ms = ev0.elapsed_time(ev1)
-    ms_per_step = elapsed_ms / args.steps
-    tokens_per_s = T * args.steps / (elapsed_ms / 1e3)
+        capture(layer_step, 0, args.warmup).replay()
+    ms_per_step, wall = timed(capture(layer_step, args.warmup, args.steps), args.steps)
+    tokens_per_s = T / (ms_per_step / 1e3)
 
-    # ------------------------------------------------------------ dominant kernel: gate/up
-    # Route each launch's batch once (router + dispatch) so the plans exist,
-    # then time a graph of back-to-back gate/up launches with HIP events.
-    R = args.kernel_launches
-    P = T * k
-    i32 = dict(dtype=torch.int32, device=dev)
-    plans = []
-    for r in range(R):
-        b = banks[r % n_banks]
-        x = xs[r % n_inputs]
-        lg = torch.empty((T, E), dtype=torch.float32, device=dev)
-        w_ = torch.empty((T, k), dtype=torch.float32, device=dev)
-        ix = torch.empty((T, k), **i32)
-        native.call("glm_router_topk", torch.cuda.current_stream().cuda_stream, x.data_ptr(), T,
-                    d, b["router_weight"].data_ptr(), b["router_bias"].data_ptr(), E, k,
-                    shape.n_group, shape.topk_group, 1, shape.routed_scaling_factor,
-                    lg.data_ptr(), w_.data_ptr(), ix.data_ptr())
-        pl = {n: torch.empty(sz, **i32) for n, sz in
-              [("counts", E), ("offsets", E + 1), ("perm", P), ("inv", P), ("tok", P),
-               ("active", E), ("nact", 1), ("work", 4 * E), ("status", 1)]}
-        native.call("glm_moe_dispatch", torch.cuda.current_stream().cuda_stream, ix.data_ptr(),
-                    T, k, E, *(pl[n].data_ptr() for n in ("counts", "offsets", "perm", "inv",
-                                                           "tok", "active", "nact", "work",
-                                                           "status")))
-        plans.append(pl)
-    torch.cuda.synchronize()
-    unique = [int(pl["nact"].item()) for pl in plans]
-    h = torch.empty((P, I), dtype=torch.bfloat16, device=dev)
-
-    def gate_up(r: int) -> None:
-        b, pl = banks[r % n_banks], plans[r]
-        native.call("glm_expert_gate_up", torch.cuda.current_stream().cuda_stream,
-                    xs[r % n_inputs].data_ptr(), T, d, I, E, k,
-                    *(b[key].data_ptr() for key in BANK_KEYS[:4]), pl["tok"].data_ptr(),
-                    pl["work"].data_ptr(), shape.swiglu_limit, h.data_ptr())
-
-    gk = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(gk):
-        for r in range(R):
-            gate_up(r)
+    # ------------------------------------------------------------ dominant kernel
+    gk = capture(S.gate_up, 0, R)
     gk.replay()
-    torch.cuda.synchronize()
-    ek0, ek1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ek0.record()
-    gk.replay()
-    ek1.record()
-    torch.cuda.synchronize()
-    k_ms = ek0.elapsed_time(ek1) / R
-    proj_bytes = I * d // 2 + I * d // 32  # one projection of one expert
-    gateup_bytes = [u * 2 * proj_bytes for u in unique]
-    bytes_per_launch = sum(gateup_bytes) / R
+    k_ms, _ = timed(gk, R)
+    bytes_per_launch = sum(S.kernel_bytes(r) for r in range(R)) / R
     achieved = bytes_per_launch / (k_ms / 1e3) / 1e9
+    del gk
+    torch.cuda.synchronize()
+
+    traffic, traffic_note = None, "not measured (--traffic 0)"
+    if args.traffic:
+        traffic, traffic_note = measure_traffic(args, S.kernel_name())
 
     # ------------------------------------------------------------ CPU baseline
     cpu = None
     if args.cpu_seconds > 0:
-        cpu = cpu_baseline(shape, banks[0], xs, args.cpu_seconds)
+        cpu = cpu_baseline(shape, S.banks[0], S.xs, args.cpu_seconds)
 
     line = {
         "metric": METRIC,
@@ -230,27 +292,98 @@ def main() -> int:
         "config": {
             "workload": f"{shape.name}: MoE layer T={T} d={d} E={E} top-{k} I={I} "
                         f"(MXFP4 group-32 experts, bf16 shared expert I={Is})",
-            "tokens_per_step": T, "weights": "mxfp4-e2m1+e8m0", "mfma": "bf16 x dequantised mxfp4",
-            "layer_banks": n_banks, "rotation_bytes": n_banks * layer_bytes,
-            "graph_steps": args.steps, "wall_s": round(wall, 4),
+            "tokens_per_step": T, "weights": "mxfp4-e2m1+e8m0",
+            "mfma": "bf16 x dequantised mxfp4", "layer_banks": S.n_banks,
+            "rotation_bytes": S.n_banks * S.layer_bytes, "graph_steps": args.steps,
+            "wall_s": round(wall, 4),
         },
         "decode_expert_hbm_gbps": round(achieved, 1),
         "roofline": {
-            "kernel": "decode_gate_up_kernel<4, false> (routed MXFP4 gate+up+SwiGLU)",
+            "kernel": S.kernel_name() + (" (few-token selection + routed MXFP4 gate/up + SwiGLU)"
+                                         if S.few_token else
+                                         " (routed MXFP4 gate/up + SwiGLU)"),
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_note": traffic_note,
             "bytes_per_launch": round(bytes_per_launch),
             "avg_launch_us": round(k_ms * 1e3, 3),
-            "unique_experts_per_launch": round(sum(unique) / R, 2),
+            "launches": R,
+            "unique_experts_per_launch": round(sum(S.unique) / R, 2),
         },
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
     return 0
+
+
+def copy_probe(torch) -> int:
+    """Counter calibration run: four device copies of COPY_BYTES."""
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return 0
+
+
+def _counter_pass(counter: str, child_args: list[str]) -> dict[str, list[float]]:
+    """One rocprofv3 counter pass over a child run of this script; returns
+    {kernel name: per-dispatch values (KiB)}."""
+    out = tempfile.mkdtemp(prefix="glm_pmc_", dir="/tmp")
+    env = dict(os.environ, TMPDIR="/tmp")
+    cmd = ["rocprofv3", "--pmc", counter, "-f", "csv", "-d", out, "-o", "run", "--",
+           sys.executable, os.path.abspath(__file__)] + child_args
+    print(f"bench: counter pass {counter} over {' '.join(child_args)}", file=sys.stderr,
+          flush=True)
+    try:
+        # own process group, so that a pass over its time limit ends with its children
+        proc = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL,
+                                stderr=subprocess.DEVNULL, start_new_session=True)
+        try:
+            proc.wait(timeout=120)
+        except subprocess.TimeoutExpired:
+            os.killpg(proc.pid, signal.SIGKILL)
+            proc.wait()
+            return {}
+        vals: dict[str, list[float]] = {}
+        for path in glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True):
+            with open(path) as f:
+                for row in csv.DictReader(f):
+                    if row.get("Counter_Name") == counter:
+                        vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+        return vals
+    finally:
+        shutil.rmtree(out, ignore_errors=True)
+
+
+def measure_traffic(args, kernel_name: str):
+    """HBM bytes per launch of the dominant kernel: FETCH_SIZE and WRITE_SIZE
+    (KiB per dispatch) in two passes over a run of its launches, each scaled by
+    what the same counter reads for a device copy of COPY_BYTES."""
+    if shutil.which("rocprofv3") is None:
+        return None, "rocprofv3 not found"
+    child = ["--mode", "kernel", "--workload", args.workload, "--kernel-launches", "32",
+             "--seed", str(args.seed), "--min-rotation-gb", str(args.min_rotation_gb)]
+    res = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        copy_vals = [v for name, vs in _counter_pass(counter, ["--mode", "copy"]).items()
+                     if "copy" in name.lower() for v in vs]
+        kern = [v for name, vs in _counter_pass(counter, child).items() if kernel_name in name
+                for v in vs]
+        if not copy_vals or not kern or max(copy_vals) <= 0:
+            return None, f"{counter}: no counter rows (copy {len(copy_vals)}, kernel {len(kern)})"
+        scale = COPY_BYTES / (max(copy_vals) * 1024.0)
+        res[counter] = (sum(kern) / len(kern) * 1024.0 * scale, scale, len(kern))
+    fetch, write = res["FETCH_SIZE"], res["WRITE_SIZE"]
+    note = (f"FETCH_SIZE x {fetch[1]:.3f} + WRITE_SIZE x {write[1]:.3f} (scales from a "
+            f"{COPY_BYTES >> 20} MiB device copy), mean over {fetch[2]} dispatches: "
+            f"read {fetch[0] / 1e6:.2f} MB, write {write[0] / 1e6:.3f} MB")
+    return round(fetch[0] + write[0]), note
 
 
 def cpu_baseline(shape, bank, xs, budget_s: float):

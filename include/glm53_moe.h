@@ -104,6 +104,25 @@ int glm_expert_gate_up(void *stream, const uint16_t *x, int T, int d, int I, int
                        uint16_t *h);
 
 /*
+ * Few-token selection + routed gate/up, token-major (no dispatch).  For each
+ * pair (t, j): token t's experts are chosen from its router logits exactly as
+ * glm_router_topk chooses them (TopKRouter.__call__, moe.py:36-63), and
+ * h[t*k + j] = limited SwiGLU of expert indices[t][j]'s gate/up projections
+ * of x[t] (native_expert_ssd.py:696-706, expert_ssd.py:103-107).
+ * logits f32 [T][E] (as glm_router_topk writes them); weights f32 [T][k] and
+ * indices u32 [T][k] are written as glm_router_topk writes them; h bf16
+ * [T*k][I] in pair order.
+ * Limits: T <= 4, k <= 8, E <= 448, d / 512 in {2, 4, 6, 8},
+ * I / 128 in {1, 2, 4, 6, 8}, plus the router's limits.
+ */
+int glm_route_gate_up(void *stream, const float *logits, const float *bias, int T, int E,
+                      int top_k, int n_group, int topk_group, int norm_topk_prob,
+                      float routed_scaling_factor, const uint16_t *x, int d, int I,
+                      const uint8_t *gate_packed, const uint8_t *gate_scales,
+                      const uint8_t *up_packed, const uint8_t *up_scales, float swiglu_limit,
+                      float *weights, uint32_t *indices, uint16_t *h);
+
+/*
  * Routed down projection.  Replaces mx._expert_ssd_mxfp4_masked_qmv
  * (native_expert_ssd.py:707-717) and gather_qmm(down) (native_expert_ssd.py:743).
  * h bf16 [T*k][I] (sorted order); y bf16 [T*k][d] (sorted order).

@@ -974,6 +974,40 @@ int glm_fill_zero_launch(hipStream_t stream, void *p, size_t bytes) {
   return GLM_OK;
 }
 
+// Selection + routed gate/up (+ the shared expert's down tiles of sh, cs
+// chunks per tile) of the token-major path.
+static int launch_select_gate_up(hipStream_t stream, const PairArgs &a, const SharedArgs &sh,
+                                 int cs) {
+  const int d = a.d, E = a.E, T = a.T;
+  const int epl = E <= 128 ? 2 : (E <= 256 ? 4 : 8);
+  const size_t lds2 = std::max(pair_gate_up_lds_bytes(d, epl), (size_t)T * cs * 128 * 2);
+  const dim3 g2(a.routed_blocks + sh.dn_blocks);
+#define GLM_PAIR_GU(EP, CS)                                                                    \
+  switch (d / 512) {                                                                           \
+    case 2: hipLaunchKernelGGL((select_gate_up_kernel<EP, 2, CS>), g2, dim3(256), lds2, stream, a, sh); break; \
+    case 4: hipLaunchKernelGGL((select_gate_up_kernel<EP, 4, CS>), g2, dim3(256), lds2, stream, a, sh); break; \
+    case 6: hipLaunchKernelGGL((select_gate_up_kernel<EP, 6, CS>), g2, dim3(256), lds2, stream, a, sh); break; \
+    default: hipLaunchKernelGGL((select_gate_up_kernel<EP, 8, CS>), g2, dim3(256), lds2, stream, a, sh); break; \
+  }
+#define GLM_PAIR_GU_CS(EP) \
+  if (cs == 1) {           \
+    GLM_PAIR_GU(EP, 1)     \
+  } else {                 \
+    GLM_PAIR_GU(EP, 2)     \
+  }
+  if (epl == 2) {
+    GLM_PAIR_GU_CS(2)
+  } else if (epl == 4) {
+    GLM_PAIR_GU_CS(4)
+  } else {
+    GLM_PAIR_GU_CS(8)
+  }
+#undef GLM_PAIR_GU_CS
+#undef GLM_PAIR_GU
+  GLM_LAUNCH_CHECK("select_gate_up_kernel");
+  return GLM_OK;
+}
+
 bool glm_pair_path_supported(int T, int d, int E, int k, int I, int Is) {
   return T >= 1 && T <= kPairMaxT && k <= kPairMaxK && d % 16 == 0 &&
          glm_decode_path_supported(T, d, E, k, I, Is);
@@ -1027,33 +1061,8 @@ int glm_pair_path_launch(hipStream_t stream, const uint16_t *x, int T, int d, co
   a.h = h;
   a.limit = glm_limit_bf16(limit);
   a.routed_blocks = T * k * (I / 16);
-  const int epl = E <= 128 ? 2 : (E <= 256 ? 4 : 8);
-  const int cs = sg ? glm_decode_shared_cpws(Is) : 1;
-  const size_t lds2 = std::max(pair_gate_up_lds_bytes(d, epl), (size_t)T * cs * 128 * 2);
-  const dim3 g2(a.routed_blocks + sh.dn_blocks);
-#define GLM_PAIR_GU(EP, CS)                                                                    \
-  switch (d / 512) {                                                                           \
-    case 2: hipLaunchKernelGGL((select_gate_up_kernel<EP, 2, CS>), g2, dim3(256), lds2, stream, a, sh); break; \
-    case 4: hipLaunchKernelGGL((select_gate_up_kernel<EP, 4, CS>), g2, dim3(256), lds2, stream, a, sh); break; \
-    case 6: hipLaunchKernelGGL((select_gate_up_kernel<EP, 6, CS>), g2, dim3(256), lds2, stream, a, sh); break; \
-    default: hipLaunchKernelGGL((select_gate_up_kernel<EP, 8, CS>), g2, dim3(256), lds2, stream, a, sh); break; \
-  }
-#define GLM_PAIR_GU_CS(EP) \
-  if (cs == 1) {           \
-    GLM_PAIR_GU(EP, 1)     \
-  } else {                 \
-    GLM_PAIR_GU(EP, 2)     \
-  }
-  if (epl == 2) {
-    GLM_PAIR_GU_CS(2)
-  } else if (epl == 4) {
-    GLM_PAIR_GU_CS(4)
-  } else {
-    GLM_PAIR_GU_CS(8)
-  }
-#undef GLM_PAIR_GU_CS
-#undef GLM_PAIR_GU
-  GLM_LAUNCH_CHECK("select_gate_up_kernel");
+  rc = launch_select_gate_up(stream, a, sh, sg ? glm_decode_shared_cpws(Is) : 1);
+  if (rc) return rc;
 
   PairDownArgs b{};
   b.h = h;
@@ -1082,4 +1091,58 @@ int glm_pair_path_launch(hipStream_t stream, const uint16_t *x, int T, int d, co
   }
   GLM_LAUNCH_CHECK("down_combine_kernel");
   return GLM_OK;
+}
+
+int glm_router_validate(const void *x, int T, int d, const void *weight, const void *bias, int E,
+                        int k, int n_group, int topk_group, const void *weights,
+                        const void *indices);
+
+extern "C" int glm_route_gate_up(void *stream, const float *logits, const float *bias, int T,
+                                 int E, int top_k, int n_group, int topk_group, int norm_topk_prob,
+                                 float routed_scaling_factor, const uint16_t *x, int d, int I,
+                                 const uint8_t *gate_packed, const uint8_t *gate_scales,
+                                 const uint8_t *up_packed, const uint8_t *up_scales,
+                                 float swiglu_limit, float *weights, uint32_t *indices,
+                                 uint16_t *h) {
+  glm::clear_error();
+  // the router's own checks (logits stand in for its x and weight)
+  int rc = glm_router_validate(logits, T, 4, logits, bias, E, top_k, n_group, topk_group, weights,
+                               indices);
+  if (rc != GLM_OK) return rc;
+  GLM_REQUIRE(x && gate_packed && gate_scales && up_packed && up_scales && h,
+              GLM_ERR_INVALID_ARGUMENT, "route_gate_up: null pointer argument");
+  GLM_REQUIRE(glm_aligned16({x, gate_packed, gate_scales, up_packed, up_scales, h}),
+              GLM_ERR_INVALID_ARGUMENT, "route_gate_up: buffers must be 16-byte aligned");
+  GLM_REQUIRE(T <= kPairMaxT && top_k <= kPairMaxK && glm_pair_path_supported(T > 0 ? T : 1, d, E, top_k, I, 0),
+              GLM_ERR_UNSUPPORTED_SHAPE,
+              "route_gate_up: unsupported shape T=%d d=%d E=%d k=%d I=%d (T <= 4, k <= 8, "
+              "E <= 448, d/512 in {2,4,6,8}, I/128 in {1,2,4,6,8})",
+              T, d, E, top_k, I);
+  if (T == 0) return GLM_OK;
+  PairArgs a{};
+  a.logits = logits;
+  a.bias = bias;
+  a.T = T;
+  a.E = E;
+  a.k = top_k;
+  a.n_group = n_group;
+  a.topk_group = topk_group;
+  a.norm = norm_topk_prob;
+  a.scale = routed_scaling_factor;
+  a.weights = weights;
+  a.indices = indices;
+  a.x = x;
+  a.gw = gate_packed;
+  a.gs = gate_scales;
+  a.uw = up_packed;
+  a.us = up_scales;
+  a.w_stride = (long long)I * (d / 2);
+  a.s_stride = (long long)I * (d / 32);
+  a.d = d;
+  a.I = I;
+  a.h = h;
+  a.limit = glm_limit_bf16(swiglu_limit);
+  a.routed_blocks = T * top_k * (I / 16);
+  SharedArgs sh{};
+  return launch_select_gate_up((hipStream_t)stream, a, sh, 1);
 }

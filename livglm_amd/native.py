@@ -41,6 +41,8 @@ SIGNATURES = {
     "glm_router_topk": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _i, _f, _p, _p, _p]),
     "glm_moe_dispatch": (_i, [_p, _p, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p]),
     "glm_expert_gate_up": (_i, [_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _f, _p]),
+    "glm_route_gate_up": (_i, [_p, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p, _i, _i, _p, _p, _p, _p,
+                               _f, _p, _p, _p]),
     "glm_expert_down": (_i, [_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _p]),
     "glm_moe_combine": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _p]),
     "glm_linear": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _p]),

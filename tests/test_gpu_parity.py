@@ -286,6 +286,38 @@ def test_routed_experts_parity(gu, name, T):
     assert np.mean(y_got == y_want) > 0.97
 
 
+@pytest.mark.parametrize("name,T,E", [("decode_t1", None, None), ("verify_t2", None, None),
+                                      ("verify_t2", 4, 256), ("verify_t2", 3, 300)])
+def test_route_gate_up_parity(gu, name, T, E):
+    # few-token fused selection + gate/up: routing bit-exact with the router,
+    # h in pair order within the bf16 tolerance of the oracle
+    torch = _torch()
+    base = SHAPES[name]
+    shape = MoEShape(base.name, base.T if T is None else T, base.d, E or base.E, base.k, base.I,
+                     base.I_shared)
+    layer = make_layer(shape, 61 + shape.T + shape.E)
+    T, k, E, d, I = shape.T, shape.k, shape.E, shape.d, shape.I
+    x = O.bf16_bits_to_f32(layer["x"])
+    logits, w_want, idx_want, _ = O.router(x, layer["router_weight"], layer["router_bias"],
+                                           top_k=k, n_group=1, topk_group=1,
+                                           norm_topk_prob=True, routed_scaling_factor=2.5)
+    _, inter = O.routed_experts(x, idx_want, _bank(layer), shape.swiglu_limit,
+                                return_intermediates=True)
+    dl = gu.upload_layer({key: layer[key] for key in ("x", "router_bias") + BANK_KEYS})
+    d_logits = gu.to_dev(np.asarray(logits, np.float32))
+    h = torch.empty((T * k, I), dtype=torch.bfloat16, device="cuda")
+    w = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    idx = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    gu.call("glm_route_gate_up", gu.stream(), gu.p(d_logits), gu.p(dl["router_bias"]), T, E, k,
+            1, 1, 1, 2.5, gu.p(dl["x"]), d, I, *(gu.p(dl[key]) for key in BANK_KEYS[:4]),
+            shape.swiglu_limit, gu.p(w), gu.p(idx), gu.p(h))
+    assert np.array_equal(gu.host(idx).astype(np.uint32), idx_want)
+    np.testing.assert_allclose(gu.host(w), w_want, rtol=2e-6, atol=1e-7)
+    h_got = O.bf16_bits_to_f32(gu.bf16_bits(h)).reshape(T, k, I)
+    assert O.rel_l2(h_got, inter["h"]) < REL_L2
+    assert np.mean(h_got == inter["h"]) > 0.97
+
+
 def test_routed_experts_generic_shapes(gu):
     # tiny geometry of the reference's tests (tests/helpers.py: d=32, I=32) and
     # one more that is not a multiple of the 128-wide MFMA chunk
