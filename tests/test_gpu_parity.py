@@ -473,6 +473,20 @@ def test_moe_layer_mxfp8_shared_expert(gu, T):
     assert O.rel_l2(gu.host(out), want) < REL_L2
 
 
+def test_moe_layer_golden_vectors(gu):
+    # the committed fixture (tests/golden/moe_small.npz): d=256 runs the general
+    # kernels, with group-limited routing
+    import os
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                             "moe_small.npz"))
+    shape = MoEShape("golden", 3, 256, 8, 2, 128, 128, n_group=2, topk_group=1)
+    layer = {key: z[key] for key in z.files if not key.startswith("expected.")}
+    out, w, idx = gu.run_layer(gu.upload_layer(layer), shape)
+    assert np.array_equal(gu.host(idx).astype(np.uint32), z["expected.indices"])
+    np.testing.assert_allclose(gu.host(w), z["expected.weights"], rtol=2e-6, atol=1e-7)
+    assert O.rel_l2(gu.host(out), z["expected.out"]) < REL_L2
+
+
 def test_moe_layer_prefill_sampled(gu):
     shape = SHAPES["prefill_t4096"]
     layer = make_layer(shape, 5303)
