@@ -47,7 +47,8 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     const uint32_t *__restrict__ idx, int P, int k, int E, int32_t *__restrict__ counts,
     int32_t *__restrict__ offsets, int32_t *__restrict__ perm, int32_t *__restrict__ inv,
     int32_t *__restrict__ pair_token, int32_t *__restrict__ active,
-    int32_t *__restrict__ num_active, int4 *__restrict__ work, int32_t *__restrict__ status) {
+    int32_t *__restrict__ num_active, int4 *__restrict__ work, int32_t *__restrict__ status,
+    int tile_rows, int4 *__restrict__ tiles, int32_t *__restrict__ num_tiles) {
   extern __shared__ uint32_t smem[];
   uint32_t *cnt = smem;
   uint32_t *off = cnt + E;
@@ -70,8 +71,10 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
   }
   __syncthreads();
 
-  // offsets = exclusive scan of counts; active = compacted ids with count > 0.
-  int carry = 0, carry_active = 0;
+  // offsets = exclusive scan of counts; active = compacted ids with count > 0;
+  // optionally the row tiles of the grouped GEMMs (tile_rows rows each, in
+  // expert order): {expert, first sorted position, rows, 0}.
+  int carry = 0, carry_active = 0, carry_tiles = 0;
   for (int e0 = 0; e0 < E; e0 += kDispatchThreads) {
     const int e = e0 + tid;
     const int c = e < E ? (int)cnt[e] : 0;
@@ -79,6 +82,9 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     const int ex = block_exclusive_scan(c, s_scan, &tot);
     int tot_a = 0;
     const int ex_a = block_exclusive_scan(c > 0 ? 1 : 0, s_scan, &tot_a);
+    const int nt = tiles != nullptr ? (c + tile_rows - 1) / tile_rows : 0;
+    int tot_t = 0;
+    const int ex_t = block_exclusive_scan(nt, s_scan, &tot_t);
     if (e < E) {
       off[e] = carry + ex;
       offsets[e] = carry + ex;
@@ -87,14 +93,19 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
         active[carry_active + ex_a] = e;
         work[carry_active + ex_a] = make_int4(e, carry + ex, c, 0);
       }
+      for (int i = 0; i < nt; ++i)
+        tiles[carry_tiles + ex_t + i] =
+            make_int4(e, carry + ex + i * tile_rows, min(tile_rows, c - i * tile_rows), 0);
     }
     carry += tot;
     carry_active += tot_a;
+    carry_tiles += tot_t;
   }
   if (tid == 0) {
     offsets[E] = carry;
     num_active[0] = carry_active;
     status[0] = s_bad;
+    if (num_tiles != nullptr) num_tiles[0] = carry_tiles;
   }
   for (int e = carry_active + tid; e < E; e += kDispatchThreads) {
     active[e] = -1;
@@ -143,14 +154,17 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
 
 size_t glm_dispatch_lds_bytes(int E) { return (size_t)E * (3 + 32) * sizeof(uint32_t); }
 
+// tiles/num_tiles (optional): row tiles of tile_rows rows for the grouped
+// GEMMs; tiles needs room for ceil(T*k / tile_rows) + E entries.
 int glm_dispatch_launch(hipStream_t stream, const uint32_t *indices, int T, int k, int E,
                         int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
                         int32_t *pair_token, int32_t *active, int32_t *num_active, int4 *work,
-                        int32_t *status) {
+                        int32_t *status, int tile_rows, int4 *tiles, int32_t *num_tiles) {
   const int P = T * k;
   hipLaunchKernelGGL(glm::dispatch_kernel, dim3(1), dim3(glm::kDispatchThreads),
                      glm_dispatch_lds_bytes(E), stream, indices, P, k, E, counts, offsets, perm,
-                     inv, pair_token, active, num_active, work, status);
+                     inv, pair_token, active, num_active, work, status, tile_rows, tiles,
+                     num_tiles);
   GLM_LAUNCH_CHECK("dispatch_kernel");
   return GLM_OK;
 }
@@ -171,5 +185,6 @@ extern "C" int glm_moe_dispatch(void *stream, const uint32_t *indices, int T, in
   GLM_REQUIRE(glm_aligned16({work}), GLM_ERR_INVALID_ARGUMENT,
               "dispatch: work must be 16-byte aligned");
   return glm_dispatch_launch((hipStream_t)stream, indices, T, top_k, E, counts, offsets, perm,
-                             inv, pair_token, active, num_active, (int4 *)work, status);
+                             inv, pair_token, active, num_active, (int4 *)work, status, 0,
+                             nullptr, nullptr);
 }

@@ -79,9 +79,11 @@ __device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to
 
 // E8M0 byte -> f32 scale 2^(e-127) (byte 255 = NaN).
 __device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
-  if (e == 0) return __uint_as_float(0x00400000u);  // 2^-127, subnormal
-  if (e == 255) return __uint_as_float(0x7fc00000u);
-  return __uint_as_float(e << 23);
+  // branch-free: two selects on the shifted exponent
+  uint32_t u = e << 23;
+  u = e == 0u ? 0x00400000u : u;    // 2^-127, subnormal
+  u = e == 255u ? 0x7fc00000u : u;  // NaN
+  return __uint_as_float(u);
 }
 
 // sigmoid in f32: y = 1/(1+exp(|x|)); x<0 ? y : 1-y.

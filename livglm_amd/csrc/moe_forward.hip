@@ -38,7 +38,16 @@ int glm_router_launch(hipStream_t stream, const uint16_t *x, int T, int d, const
 int glm_dispatch_launch(hipStream_t stream, const uint32_t *indices, int T, int k, int E,
                         int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
                         int32_t *pair_token, int32_t *active, int32_t *num_active, int4 *work,
-                        int32_t *status);
+                        int32_t *status, int tile_rows, int4 *tiles, int32_t *num_tiles);
+int glm_grouped_tile_rows();
+bool glm_grouped_supported(int d, int I);
+int glm_grouped_gate_up_launch(hipStream_t stream, const uint16_t *x, const int32_t *pair_token,
+                               const int4 *tiles, const int32_t *num_tiles, int max_tiles, int d,
+                               int I, const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
+                               const uint8_t *us, uint16_t *h, float limit);
+int glm_grouped_down_launch(hipStream_t stream, const uint16_t *h, const int4 *tiles,
+                            const int32_t *num_tiles, int max_tiles, int I, int d,
+                            const uint8_t *dw, const uint8_t *ds, uint16_t *y);
 int glm_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int E, int k,
                        const uint8_t *gw, const uint8_t *gs, const uint8_t *uw, const uint8_t *us,
                        const int32_t *pair_token, const int4 *work, float limit, uint16_t *h);
@@ -106,6 +115,9 @@ struct Workspace {
   uint16_t *shared_h;
   uint16_t *shared_out;
   int4 *work;
+  int4 *tiles;         // grouped-GEMM row tiles {expert, first position, rows, 0}
+  int32_t *num_tiles;
+  int max_tiles;
   float *gp, *up;  // decode shared-expert gate/up partials [skq][T][Is]
   float *yp;       // decode shared-expert down partials [skd][T][d]
   size_t bytes;
@@ -137,6 +149,9 @@ Workspace carve(char *base, int T, int d, int E, int k, int I, int Is) {
   w.shared_h = (uint16_t *)take((size_t)T * (Is > 0 ? Is : 0) * 2);
   w.shared_out = (uint16_t *)take((size_t)T * (Is > 0 ? d : 0) * 2);
   w.work = (int4 *)take((size_t)E * sizeof(int4));
+  w.max_tiles = (int)((P + glm_grouped_tile_rows() - 1) / glm_grouped_tile_rows()) + E;
+  w.tiles = (int4 *)take((size_t)w.max_tiles * sizeof(int4));
+  w.num_tiles = (int32_t *)take(4);
   const size_t tis = (size_t)T * (Is > 0 ? Is : 0) * 4;
   const int skq = d % 512 == 0 ? d / 512 : 1;
   const int skd = Is >= 128 ? Is / 128 : 1;  // bound on the down K split
@@ -266,13 +281,27 @@ extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
   rc = glm_router_launch(stream, x, T, d, router_weight, router_bias, E, top_k, n_group,
                          topk_group, norm_topk_prob, routed_scaling_factor, w.logits, wts, idx);
   if (rc) return rc;
+  // general path: dispatch, then the grouped MFMA GEMMs over row tiles when
+  // the shape allows, else the tiled GEMV kernels over the work list
+  const bool grouped = glm_grouped_supported(d, I);
   rc = glm_dispatch_launch(stream, idx, T, top_k, E, w.counts, w.offsets, w.perm, w.inv,
-                           w.pair_token, w.active, w.num_active, w.work, w.status);
+                           w.pair_token, w.active, w.num_active, w.work, w.status,
+                           grouped ? glm_grouped_tile_rows() : 0, grouped ? w.tiles : nullptr,
+                           grouped ? w.num_tiles : nullptr);
   if (rc) return rc;
-  rc = glm_gate_up_launch(stream, x, T, d, I, E, top_k, gate_packed, gate_scales, up_packed,
-                          up_scales, w.pair_token, w.work, swiglu_limit, w.h);
-  if (rc) return rc;
-  rc = glm_down_launch(stream, w.h, T, top_k, I, d, E, down_packed, down_scales, w.work, w.y);
+  if (grouped) {
+    rc = glm_grouped_gate_up_launch(stream, x, w.pair_token, w.tiles, w.num_tiles, w.max_tiles,
+                                    d, I, gate_packed, gate_scales, up_packed, up_scales, w.h,
+                                    swiglu_limit);
+    if (rc) return rc;
+    rc = glm_grouped_down_launch(stream, w.h, w.tiles, w.num_tiles, w.max_tiles, I, d,
+                                 down_packed, down_scales, w.y);
+  } else {
+    rc = glm_gate_up_launch(stream, x, T, d, I, E, top_k, gate_packed, gate_scales, up_packed,
+                            up_scales, w.pair_token, w.work, swiglu_limit, w.h);
+    if (rc) return rc;
+    rc = glm_down_launch(stream, w.h, T, top_k, I, d, E, down_packed, down_scales, w.work, w.y);
+  }
   if (rc) return rc;
   if (has_shared && !shared_in) {
     rc = glm_mlp_launch(stream, x, T, d, I_shared, shared_fmt, shared_gate, shared_gate_scales,

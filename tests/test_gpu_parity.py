@@ -435,6 +435,10 @@ SMALL_LAYERS = [
     (4, 2048, 448, 8, 128, 256, (1, 1)),
     (5, 1024, 64, 6, 256, 256, (1, 1)),
     (9, 2048, 96, 5, 384, 0, (3, 2)),
+    # grouped MFMA GEMMs (T > 64): partial tiles, experts spanning two tiles
+    (96, 1024, 16, 4, 256, 256, (1, 1)),
+    (600, 1024, 16, 4, 256, 256, (1, 1)),
+    (200, 2048, 64, 8, 768, 0, (4, 2)),
 ]
 
 
@@ -449,6 +453,22 @@ def test_moe_layer_small_shapes(gu, T, d, E, k, I, Is, groups):
     same = np.all(got_idx == inter["indices"], axis=1)
     assert same.sum() >= T - 1
     np.testing.assert_allclose(gu.host(w)[same], inter["weights"][same], rtol=2e-6, atol=1e-7)
+    assert O.rel_l2(gu.host(out)[same], want[same]) < REL_L2
+
+
+def test_moe_layer_grouped_skewed_routing(gu):
+    # Zipf-biased routing: a few experts take several 128-row tiles, many take
+    # one partial tile or none
+    shape = MoEShape("skew", 512, 1024, 32, 4, 256, 256, routing="zipf")
+    layer = make_layer(shape, 4711)
+    want, inter = _oracle_layer(layer, shape)
+    counts = np.bincount(inter["indices"].reshape(-1).astype(np.int64), minlength=shape.E)
+    assert counts.max() > 256
+    out, w, idx = gu.run_layer(gu.upload_layer(layer), shape)
+    got_idx = gu.host(idx).astype(np.uint32)
+    _check_indices(got_idx, inter["indices"], inter["choice"], shape.k)
+    same = np.all(got_idx == inter["indices"], axis=1)
+    assert same.mean() > 0.99
     assert O.rel_l2(gu.host(out)[same], want[same]) < REL_L2
 
 
