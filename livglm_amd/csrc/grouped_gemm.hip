@@ -24,11 +24,15 @@
 namespace glm {
 
 constexpr int kTileM = 128;            // token rows per tile
-constexpr int kTileW = 256;            // weight rows per workgroup
 constexpr int kChunkK = 128;           // K per stage
 constexpr int kXStride = kChunkK + 8;  // staged activation row, bf16 elements
 constexpr int kWStride = 80;           // staged weight row, bytes (64 B of codes + pad)
-constexpr int kStageBytes = kTileM * kXStride * 2 + kTileW * kWStride + kTileW * 4;
+
+// Weight rows per workgroup for RT row tiles per wave (4 waves along the rows).
+__host__ __device__ constexpr int tile_w(int RT) { return RT * 64; }
+__host__ __device__ constexpr int stage_bytes(int RT) {
+  return kTileM * kXStride * 2 + tile_w(RT) * kWStride + tile_w(RT) * 4;
+}
 
 struct GroupedArgs {
   const uint16_t *act;       // gate/up: x [T][K]; down: h [P][K]
@@ -54,8 +58,11 @@ constexpr int kXcds = 8;
 
 constexpr int kThreads = 512;  // 8 waves: 4 along the weight rows x 2 along the tokens
 
-template <int NPROJ>
+template <int NPROJ, int RT>
 __global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a) {
+  constexpr int kTileW = tile_w(RT);
+  constexpr int kStageBytes = stage_bytes(RT);
+  constexpr int HALF = RT / 2;  // gate/up: row tiles per projection per wave
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int nft = a.feature_tiles;
   const int items = *a.num_tiles * nft;
@@ -89,30 +96,32 @@ __global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a
     const long long arow = a.act_index != nullptr ? a.act_index[pos] : pos;
     xsrc[j] = a.act + arow * K + (tid & 15) * 8;
   }
-  // weights: piece j = row (tid >> 2) + 128 j, 16 bytes at (tid & 3); scales: row tid < 256
-  const uint8_t *wsrc[2];
+  // weights: piece j = row (tid >> 2) + 128 j, 16 bytes at (tid & 3); scales:
+  // row tid < kTileW
+  constexpr int WP = kTileW / 128;  // weight pieces per thread
+  const uint8_t *wsrc[WP];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < WP; ++j) {
     const int wrow = (tid >> 2) + 128 * j;
-    const int p = NPROJ == 2 ? wrow / 128 : 0;
-    const int frow = f0 + (NPROJ == 2 ? wrow % 128 : wrow);
+    const int p = NPROJ == 2 ? wrow / (kTileW / 2) : 0;
+    const int frow = f0 + (NPROJ == 2 ? wrow % (kTileW / 2) : wrow);
     wsrc[j] = a.w[p] + e * a.w_stride + (size_t)frow * (K / 2) + (tid & 3) * 16;
   }
   const uint8_t *ssrc;
   {
     const int srow = tid & (kTileW - 1);
-    const int p = NPROJ == 2 ? srow / 128 : 0;
-    const int frow = f0 + (NPROJ == 2 ? srow % 128 : srow);
+    const int p = NPROJ == 2 ? srow / (kTileW / 2) : 0;
+    const int frow = f0 + (NPROJ == 2 ? srow % (kTileW / 2) : srow);
     ssrc = a.s[p] + e * a.s_stride + (size_t)frow * (K / 32);
   }
 
-  glm_u32x4 stx[4], stw[2];
+  glm_u32x4 stx[4], stw[WP];
   uint32_t sts = 0;
   auto load_stage = [&](int c) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) stx[j] = *reinterpret_cast<const glm_u32x4 *>(xsrc[j] + c * kChunkK);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) stw[j] = load_stream(wsrc[j] + c * (kChunkK / 2));
+    for (int j = 0; j < WP; ++j) stw[j] = load_stream(wsrc[j] + c * (kChunkK / 2));
     if (tid < kTileW) sts = *reinterpret_cast<const uint32_t *>(ssrc + c * (kChunkK / 32));
   };
   auto store_stage = [&](int buf) {
@@ -124,21 +133,22 @@ __global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a
     for (int j = 0; j < 4; ++j)
       *reinterpret_cast<glm_u32x4 *>(sx + ((tid >> 4) + 32 * j) * kXStride + (tid & 15) * 8) = stx[j];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < WP; ++j)
       *reinterpret_cast<glm_u32x4 *>(sw + ((tid >> 2) + 128 * j) * kWStride + (tid & 3) * 16) = stw[j];
     if (tid < kTileW) ss[tid] = sts;
   };
 
-  glm_f32x4 acc[4][4];
+  glm_f32x4 acc[RT][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < RT; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = glm_f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // this wave's 4 weight-row tiles within the 256 staged rows (gate/up: two
-  // gate tiles then the up tiles of the same features)
+  // this wave's RT weight-row tiles within the staged rows (gate/up: RT/2 gate
+  // tiles, then the up tiles of the same features)
   auto wrow_of = [&](int rt) {
-    return NPROJ == 2 ? (rt / 2) * 128 + wf * 32 + (rt % 2) * 16 : wf * 64 + rt * 16;
+    return NPROJ == 2 ? (rt / HALF) * (kTileW / 2) + wf * HALF * 16 + (rt % HALF) * 16
+                      : wf * RT * 16 + rt * 16;
   };
 
   // MFMAs of one staged chunk
@@ -147,27 +157,31 @@ __global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a
     const uint16_t *sx = reinterpret_cast<const uint16_t *>(base);
     const uint8_t *sw = base + kTileM * kXStride * 2;
     const uint32_t *ss = reinterpret_cast<const uint32_t *>(sw + kTileW * kWStride);
-    glm_u32x4 raw[4];
-    float scale[4];
+    glm_u32x4 raw[RT];
+    float scale[RT];
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       const int wr = wrow_of(rt) + r;
       raw[rt] = *reinterpret_cast<const glm_u32x4 *>(sw + wr * kWStride + 16 * q);
       scale[rt] = e8m0_to_f32((ss[wr] >> (8 * q)) & 0xffu);
     }
+    // every B fragment of the chunk is read up front (LDS returns in order, so
+    // the MFMAs of step i wait only for the reads of steps <= i)
+    glm_bf16x8 xb[4][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      glm_bf16x8 xb[4];
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct)
-        xb[ct] = *reinterpret_cast<const glm_bf16x8 *>(sx + (wt * 64 + ct * 16 + r) * kXStride +
-                                                       32 * q + 8 * i);
+        xb[i][ct] = *reinterpret_cast<const glm_bf16x8 *>(sx + (wt * 64 + ct * 16 + r) * kXStride +
+                                                          32 * q + 8 * i);
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt) {
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
         const glm_bf16x8 af = mxfp4_word_to_bf16x8(raw[rt][i], scale[rt]);
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct)
-          acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, xb[ct], acc[rt][ct], 0, 0, 0);
+          acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, xb[i][ct], acc[rt][ct], 0, 0, 0);
       }
     }
   };
@@ -194,21 +208,21 @@ __global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a
     uint16_t *orow = a.out + (size_t)(pos0 + row) * a.N;
     if constexpr (NPROJ == 2) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < HALF; ++i) {
         uint32_t o[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m)
-          o[m] = f32_to_bf16(limited_swiglu(bf16_round(acc[i][ct][m]), bf16_round(acc[2 + i][ct][m]),
-                                            a.limit));
-        store_rows4(orow + f0 + wf * 32 + i * 16 + 4 * q, o);
+          o[m] = f32_to_bf16(limited_swiglu(bf16_round(acc[i][ct][m]),
+                                            bf16_round(acc[HALF + i][ct][m]), a.limit));
+        store_rows4(orow + f0 + wf * HALF * 16 + i * 16 + 4 * q, o);
       }
     } else {
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt) {
+      for (int rt = 0; rt < RT; ++rt) {
         uint32_t o[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) o[m] = f32_to_bf16(acc[rt][ct][m]);
-        store_rows4(orow + f0 + wf * 64 + rt * 16 + 4 * q, o);
+        store_rows4(orow + f0 + wf * RT * 16 + rt * 16 + 4 * q, o);
       }
     }
   }
@@ -220,23 +234,24 @@ using namespace glm;
 
 int glm_grouped_tile_rows() { return kTileM; }
 
-// Whether the grouped GEMMs cover these shapes: gate/up K = d, N = I (128-wide
-// feature tiles per projection); down K = I, N = d (256-wide tiles).
+// Whether the grouped GEMMs cover these shapes: gate/up K = d, N = I in
+// feature tiles of 128 per projection; down K = I, N = d in tiles of 256.
 bool glm_grouped_supported(int d, int I) {
   return d % kChunkK == 0 && I % kChunkK == 0 && I % 128 == 0 && d % 256 == 0;
 }
 
 static int grouped_launch(hipStream_t stream, GroupedArgs a, int nproj, int max_tiles) {
-  a.feature_tiles = nproj == 2 ? a.N / 128 : a.N / 256;
+  constexpr int rt = 4;  // 8 row tiles per wave would need more than 256 registers
+  a.feature_tiles = a.N / (nproj == 2 ? tile_w(rt) / 2 : tile_w(rt));
   // XCD x handles items [x * per, (x + 1) * per) with per <= ceil(max_items / 8),
   // at linear ids x + 8k: the grid must reach 8 * ceil(max_items / 8)
   const long long max_items = (long long)max_tiles * a.feature_tiles;
   const dim3 grid((unsigned)(((max_items + kXcds - 1) / kXcds) * kXcds));
-  const size_t lds = 2 * (size_t)kStageBytes;
+  const size_t lds = 2 * (size_t)stage_bytes(rt);
   if (nproj == 2)
-    hipLaunchKernelGGL(grouped_mx_gemm_kernel<2>, grid, dim3(kThreads), lds, stream, a);
+    hipLaunchKernelGGL((grouped_mx_gemm_kernel<2, rt>), grid, dim3(kThreads), lds, stream, a);
   else
-    hipLaunchKernelGGL(grouped_mx_gemm_kernel<1>, grid, dim3(kThreads), lds, stream, a);
+    hipLaunchKernelGGL((grouped_mx_gemm_kernel<1, rt>), grid, dim3(kThreads), lds, stream, a);
   GLM_LAUNCH_CHECK("grouped_mx_gemm_kernel");
   return GLM_OK;
 }
