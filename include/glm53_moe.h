@@ -133,6 +133,39 @@ int glm_expert_down(void *stream, const uint16_t *h, int T, int top_k, int I, in
                     uint16_t *y);
 
 /*
+ * Row tiles of the grouped GEMMs below, from a dispatch work list: every
+ * active slot u (work[u] = {expert, first sorted position, rows, 0}) gives
+ * ceil(rows / 128) tiles {expert, first position, rows <= 128, 0}, in slot
+ * order.  tiles int4 [max_tiles] with max_tiles >= ceil(T*k / 128) + E;
+ * num_tiles [1].  No reference counterpart: it feeds the prefill GEMMs below.
+ */
+int glm_moe_tiles(void *stream, const int32_t *work, int E, int32_t *tiles, int32_t *num_tiles);
+
+/*
+ * Prefill routed gate/up as grouped GEMMs on MFMA over the row tiles of
+ * glm_moe_tiles.  Replaces gather_qmm(gate/up) + limited_swiglu over all
+ * (t, j) pairs (native_expert_ssd.py:726-741, expert_ssd.py:103-107,185-186).
+ * Same inputs and output as glm_expert_gate_up: h bf16 [T*k][I] in sorted
+ * order, token rows through pair_token.
+ * Limits: d % 256 == 0, I % 128 == 0.
+ */
+int glm_expert_gate_up_grouped(void *stream, const uint16_t *x, int d, int I,
+                               const uint8_t *gate_packed, const uint8_t *gate_scales,
+                               const uint8_t *up_packed, const uint8_t *up_scales,
+                               const int32_t *pair_token, const int32_t *tiles,
+                               const int32_t *num_tiles, int max_tiles, float swiglu_limit,
+                               uint16_t *h);
+
+/*
+ * Prefill routed down projection as grouped GEMMs (native_expert_ssd.py:743).
+ * y bf16 [T*k][d] in sorted order.  Limits: d % 256 == 0, I % 128 == 0.
+ */
+int glm_expert_down_grouped(void *stream, const uint16_t *h, int I, int d,
+                            const uint8_t *down_packed, const uint8_t *down_scales,
+                            const int32_t *tiles, const int32_t *num_tiles, int max_tiles,
+                            uint16_t *y);
+
+/*
  * Weighted combine + shared add (moe.py:198-201):
  * out[t] = sum_{j=0..k-1} f32(y[inv[t*k+j]]) * weights[t*k+j]  (sequential j)
  *          + f32(shared[t])    (shared may be NULL).

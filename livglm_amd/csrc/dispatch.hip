@@ -150,17 +150,214 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Multi-workgroup dispatch for many pairs: the pairs are cut into chunks of
+// 1024 (one workgroup each).  (1) every chunk counts its experts; (2) one
+// workgroup turns the chunk counts into expert offsets and per-chunk bases
+// (bases[c][e] = offsets[e] + pairs of expert e in chunks < c), plus the work
+// list and row tiles; (3) every chunk ranks its pairs stably within the chunk
+// (bitmap popcount, as above) and scatters them to bases[c][e] + rank.  The
+// result is identical to the single-workgroup dispatch.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(
+    const uint32_t *__restrict__ idx, int P, int E, int32_t *__restrict__ chunk_counts) {
+  extern __shared__ uint32_t cnt[];  // [E]
+  __shared__ int s_bad;
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += kDispatchThreads) cnt[e] = 0;
+  if (tid == 0) s_bad = 0;
+  __syncthreads();
+  const int p = blockIdx.x * kDispatchThreads + tid;
+  if (p < P) {
+    const uint32_t e = idx[p];
+    if (e < (uint32_t)E) atomicAdd(&cnt[e], 1u);
+    else s_bad = 1;
+  }
+  __syncthreads();
+  int32_t *row = chunk_counts + (size_t)blockIdx.x * (E + 1);
+  for (int e = tid; e < E; e += kDispatchThreads) row[e] = (int)cnt[e];
+  if (tid == 0) row[E] = s_bad;
+}
+
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_scan_kernel(
+    int32_t *__restrict__ chunk_counts, int nchunks, int E, int32_t *__restrict__ counts,
+    int32_t *__restrict__ offsets, int32_t *__restrict__ active, int32_t *__restrict__ num_active,
+    int4 *__restrict__ work, int32_t *__restrict__ status, int tile_rows,
+    int4 *__restrict__ tiles, int32_t *__restrict__ num_tiles) {
+  __shared__ int s_scan[kDispatchThreads / 64 + 1];
+  const int tid = threadIdx.x;
+  // per expert: running sum over chunks (chunk_counts[c][e] becomes the
+  // exclusive base within the expert); bad flags OR-ed by thread 0
+  int bad = 0;
+  if (tid == 0)
+    for (int c = 0; c < nchunks; ++c) bad |= chunk_counts[(size_t)c * (E + 1) + E];
+  int carry = 0, carry_active = 0, carry_tiles = 0;
+  for (int e0 = 0; e0 < E; e0 += kDispatchThreads) {
+    const int e = e0 + tid;
+    int c_e = 0;
+    if (e < E) {
+      // 16 chunks at a time: their loads are issued together before any store
+      for (int c0 = 0; c0 < nchunks; c0 += 16) {
+        int n[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          n[j] = c0 + j < nchunks ? chunk_counts[(size_t)(c0 + j) * (E + 1) + e] : 0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          if (c0 + j < nchunks) chunk_counts[(size_t)(c0 + j) * (E + 1) + e] = c_e;
+          c_e += n[j];
+        }
+      }
+    }
+    int tot = 0;
+    const int ex = block_exclusive_scan(c_e, s_scan, &tot);
+    int tot_a = 0;
+    const int ex_a = block_exclusive_scan(c_e > 0 ? 1 : 0, s_scan, &tot_a);
+    const int nt = tiles != nullptr ? (c_e + tile_rows - 1) / tile_rows : 0;
+    int tot_t = 0;
+    const int ex_t = block_exclusive_scan(nt, s_scan, &tot_t);
+    if (e < E) {
+      const int off = carry + ex;
+      offsets[e] = off;
+      counts[e] = c_e;
+      for (int c0 = 0; c0 < nchunks; c0 += 16) {
+        int v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          v[j] = c0 + j < nchunks ? chunk_counts[(size_t)(c0 + j) * (E + 1) + e] : 0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (c0 + j < nchunks) chunk_counts[(size_t)(c0 + j) * (E + 1) + e] = v[j] + off;
+      }
+      if (c_e > 0) {
+        active[carry_active + ex_a] = e;
+        work[carry_active + ex_a] = make_int4(e, off, c_e, 0);
+      }
+      for (int i = 0; i < nt; ++i)
+        tiles[carry_tiles + ex_t + i] =
+            make_int4(e, off + i * tile_rows, min(tile_rows, c_e - i * tile_rows), 0);
+    }
+    carry += tot;
+    carry_active += tot_a;
+    carry_tiles += tot_t;
+  }
+  if (tid == 0) {
+    offsets[E] = carry;
+    num_active[0] = carry_active;
+    status[0] = bad;
+    if (num_tiles != nullptr) num_tiles[0] = carry_tiles;
+  }
+  for (int e = carry_active + tid; e < E; e += kDispatchThreads) {
+    active[e] = -1;
+    work[e] = make_int4(-1, 0, 0, 0);
+  }
+}
+
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_scatter_kernel(
+    const uint32_t *__restrict__ idx, int P, int k, int E,
+    const int32_t *__restrict__ chunk_bases, int32_t *__restrict__ perm,
+    int32_t *__restrict__ inv, int32_t *__restrict__ pair_token) {
+  extern __shared__ uint32_t bits[];  // [E][32]
+  const int tid = threadIdx.x;
+  for (int w = tid; w < E * 32; w += kDispatchThreads) bits[w] = 0;
+  __syncthreads();
+  const int p = blockIdx.x * kDispatchThreads + tid;
+  uint32_t e = 0xffffffffu;
+  if (p < P) {
+    e = idx[p];
+    if (e < (uint32_t)E) atomicOr(&bits[e * 32 + (tid >> 5)], 1u << (tid & 31));
+  }
+  __syncthreads();
+  if (p < P) {
+    if (e < (uint32_t)E) {
+      const uint32_t *row = bits + e * 32;
+      int r = chunk_bases[(size_t)blockIdx.x * (E + 1) + e];
+      const int word = tid >> 5;
+      for (int w = 0; w < word; ++w) r += __popc(row[w]);
+      r += __popc(row[word] & ((1u << (tid & 31)) - 1u));
+      perm[r] = p;
+      inv[p] = r;
+      pair_token[r] = p / k;
+    } else {
+      inv[p] = -1;
+    }
+  }
+}
+
+// Row tiles of the grouped GEMMs from a work list (one workgroup): slot u of
+// {expert, first position, rows, 0} gives ceil(rows / tile_rows) tiles.
+__global__ __launch_bounds__(kDispatchThreads) void tiles_from_work_kernel(
+    const int4 *__restrict__ work, int E, int tile_rows, int4 *__restrict__ tiles,
+    int32_t *__restrict__ num_tiles) {
+  __shared__ int s_scan[kDispatchThreads / 64 + 1];
+  const int tid = threadIdx.x;
+  int carry = 0;
+  for (int u0 = 0; u0 < E; u0 += kDispatchThreads) {
+    const int u = u0 + tid;
+    const int4 wk = u < E ? work[u] : make_int4(-1, 0, 0, 0);
+    const int n = wk.x >= 0 ? wk.z : 0;
+    const int nt = (n + tile_rows - 1) / tile_rows;
+    int tot = 0;
+    const int ex = block_exclusive_scan(nt, s_scan, &tot);
+    for (int i = 0; i < nt; ++i)
+      tiles[carry + ex + i] = make_int4(wk.x, wk.y + i * tile_rows, min(tile_rows, n - i * tile_rows), 0);
+    carry += tot;
+  }
+  if (tid == 0) num_tiles[0] = carry;
+}
+
 }  // namespace glm
 
+int glm_grouped_tile_rows();
+
+extern "C" int glm_moe_tiles(void *stream, const int32_t *work, int E, int32_t *tiles,
+                             int32_t *num_tiles) {
+  glm::clear_error();
+  GLM_REQUIRE(work && tiles && num_tiles, GLM_ERR_INVALID_ARGUMENT, "moe_tiles: null pointer");
+  GLM_REQUIRE(E >= 1, GLM_ERR_INVALID_ARGUMENT, "moe_tiles: invalid E=%d", E);
+  GLM_REQUIRE(glm_aligned16({work, tiles}), GLM_ERR_INVALID_ARGUMENT,
+              "moe_tiles: work and tiles must be 16-byte aligned");
+  hipLaunchKernelGGL(glm::tiles_from_work_kernel, dim3(1), dim3(glm::kDispatchThreads), 0,
+                     (hipStream_t)stream, reinterpret_cast<const int4 *>(work), E,
+                     glm_grouped_tile_rows(), reinterpret_cast<int4 *>(tiles), num_tiles);
+  GLM_LAUNCH_CHECK("tiles_from_work_kernel");
+  return GLM_OK;
+}
+
 size_t glm_dispatch_lds_bytes(int E) { return (size_t)E * (3 + 32) * sizeof(uint32_t); }
+
+// Pairs above which the dispatch runs on many workgroups (it then needs
+// glm_dispatch_chunk_ints(P, E) ints of scratch).
+constexpr int kMultiDispatchPairs = 4096;
+size_t glm_dispatch_chunk_ints(long long P, int E) {
+  return P > kMultiDispatchPairs
+             ? (size_t)((P + glm::kDispatchThreads - 1) / glm::kDispatchThreads) * (E + 1)
+             : 0;
+}
 
 // tiles/num_tiles (optional): row tiles of tile_rows rows for the grouped
 // GEMMs; tiles needs room for ceil(T*k / tile_rows) + E entries.
 int glm_dispatch_launch(hipStream_t stream, const uint32_t *indices, int T, int k, int E,
                         int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
                         int32_t *pair_token, int32_t *active, int32_t *num_active, int4 *work,
-                        int32_t *status, int tile_rows, int4 *tiles, int32_t *num_tiles) {
+                        int32_t *status, int tile_rows, int4 *tiles, int32_t *num_tiles,
+                        int32_t *chunk_scratch) {
   const int P = T * k;
+  if (chunk_scratch != nullptr && P > kMultiDispatchPairs) {
+    const int nchunks = (P + glm::kDispatchThreads - 1) / glm::kDispatchThreads;
+    hipLaunchKernelGGL(glm::dispatch_count_kernel, dim3(nchunks), dim3(glm::kDispatchThreads),
+                       (size_t)E * 4, stream, indices, P, E, chunk_scratch);
+    GLM_LAUNCH_CHECK("dispatch_count_kernel");
+    hipLaunchKernelGGL(glm::dispatch_scan_kernel, dim3(1), dim3(glm::kDispatchThreads), 0,
+                       stream, chunk_scratch, nchunks, E, counts, offsets, active, num_active,
+                       work, status, tile_rows, tiles, num_tiles);
+    GLM_LAUNCH_CHECK("dispatch_scan_kernel");
+    hipLaunchKernelGGL(glm::dispatch_scatter_kernel, dim3(nchunks), dim3(glm::kDispatchThreads),
+                       (size_t)E * 32 * 4, stream, indices, P, k, E, chunk_scratch, perm, inv,
+                       pair_token);
+    GLM_LAUNCH_CHECK("dispatch_scatter_kernel");
+    return GLM_OK;
+  }
   hipLaunchKernelGGL(glm::dispatch_kernel, dim3(1), dim3(glm::kDispatchThreads),
                      glm_dispatch_lds_bytes(E), stream, indices, P, k, E, counts, offsets, perm,
                      inv, pair_token, active, num_active, work, status, tile_rows, tiles,
@@ -186,5 +383,5 @@ extern "C" int glm_moe_dispatch(void *stream, const uint32_t *indices, int T, in
               "dispatch: work must be 16-byte aligned");
   return glm_dispatch_launch((hipStream_t)stream, indices, T, top_k, E, counts, offsets, perm,
                              inv, pair_token, active, num_active, (int4 *)work, status, 0,
-                             nullptr, nullptr);
+                             nullptr, nullptr, nullptr);
 }

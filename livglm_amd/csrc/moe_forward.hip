@@ -38,7 +38,9 @@ int glm_router_launch(hipStream_t stream, const uint16_t *x, int T, int d, const
 int glm_dispatch_launch(hipStream_t stream, const uint32_t *indices, int T, int k, int E,
                         int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
                         int32_t *pair_token, int32_t *active, int32_t *num_active, int4 *work,
-                        int32_t *status, int tile_rows, int4 *tiles, int32_t *num_tiles);
+                        int32_t *status, int tile_rows, int4 *tiles, int32_t *num_tiles,
+                        int32_t *chunk_scratch);
+size_t glm_dispatch_chunk_ints(long long P, int E);
 int glm_grouped_tile_rows();
 bool glm_grouped_supported(int d, int I);
 int glm_grouped_gate_up_launch(hipStream_t stream, const uint16_t *x, const int32_t *pair_token,
@@ -116,6 +118,7 @@ struct Workspace {
   uint16_t *shared_out;
   int4 *work;
   int4 *tiles;         // grouped-GEMM row tiles {expert, first position, rows, 0}
+  int32_t *chunk_counts;  // multi-workgroup dispatch: per-chunk expert counts, then bases
   int32_t *num_tiles;
   int max_tiles;
   float *gp, *up;  // decode shared-expert gate/up partials [skq][T][Is]
@@ -152,6 +155,7 @@ Workspace carve(char *base, int T, int d, int E, int k, int I, int Is) {
   w.max_tiles = (int)((P + glm_grouped_tile_rows() - 1) / glm_grouped_tile_rows()) + E;
   w.tiles = (int4 *)take((size_t)w.max_tiles * sizeof(int4));
   w.num_tiles = (int32_t *)take(4);
+  w.chunk_counts = (int32_t *)take(glm_dispatch_chunk_ints((long long)P, E) * 4);
   const size_t tis = (size_t)T * (Is > 0 ? Is : 0) * 4;
   const int skq = d % 512 == 0 ? d / 512 : 1;
   const int skd = Is >= 128 ? Is / 128 : 1;  // bound on the down K split
@@ -287,7 +291,7 @@ extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
   rc = glm_dispatch_launch(stream, idx, T, top_k, E, w.counts, w.offsets, w.perm, w.inv,
                            w.pair_token, w.active, w.num_active, w.work, w.status,
                            grouped ? glm_grouped_tile_rows() : 0, grouped ? w.tiles : nullptr,
-                           grouped ? w.num_tiles : nullptr);
+                           grouped ? w.num_tiles : nullptr, w.chunk_counts);
   if (rc) return rc;
   if (grouped) {
     rc = glm_grouped_gate_up_launch(stream, x, w.pair_token, w.tiles, w.num_tiles, w.max_tiles,

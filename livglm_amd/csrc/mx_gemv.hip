@@ -473,9 +473,18 @@ int glm_linear_launch(hipStream_t stream, const uint16_t *x, int T, int in_dims,
   return glm_gemv_launch(stream, fmt, 1, a, T > 0 ? 1 : 0);
 }
 
+bool glm_grouped_dense_mlp_supported(int T, int d, int I, int fmt);
+int glm_grouped_dense_mlp_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I,
+                                 const uint16_t *gw, const uint16_t *uw, const uint16_t *dw,
+                                 float limit, uint16_t *h, uint16_t *out);
+
 int glm_mlp_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int fmt,
                    const void *gw, const uint8_t *gs, const void *uw, const uint8_t *us,
                    const void *dw, const uint8_t *ds, float limit, uint16_t *h, uint16_t *out) {
+  if (glm_grouped_dense_mlp_supported(T, d, I, fmt))  // many tokens: tiled MFMA GEMMs
+    return glm_grouped_dense_mlp_launch(stream, x, T, d, I, static_cast<const uint16_t *>(gw),
+                                        static_cast<const uint16_t *>(uw),
+                                        static_cast<const uint16_t *>(dw), limit, h, out);
   GemvArgs a{};
   a.act = x;
   a.w[0] = static_cast<const uint8_t *>(gw);

@@ -318,6 +318,43 @@ def test_route_gate_up_parity(gu, name, T, E):
     assert np.mean(h_got == inter["h"]) > 0.97
 
 
+def test_grouped_expert_gemms_parity(gu):
+    # prefill grouped GEMMs through the C ABI: dispatch -> tiles -> gate/up -> down
+    torch = _torch()
+    shape = MoEShape("grouped", 400, 1024, 32, 4, 256, 0)
+    layer = make_layer(shape, 1717)
+    T, k, E, d, I = shape.T, shape.k, shape.E, shape.d, shape.I
+    x = O.bf16_bits_to_f32(layer["x"])
+    _, _, idx, _ = O.router(x, layer["router_weight"], layer["router_bias"], top_k=k, n_group=1,
+                            topk_group=1, norm_topk_prob=True, routed_scaling_factor=2.5)
+    y_want, inter = O.routed_experts(x, idx, _bank(layer), shape.swiglu_limit,
+                                     return_intermediates=True)
+    counts, offsets, perm, inv, active = O.dispatch(idx, E)
+    dl = gu.upload_layer({key: layer[key] for key in ("x",) + BANK_KEYS})
+    P = T * k
+    max_tiles = (P + 127) // 128 + E
+    work = gu.to_dev(_work_list(counts, offsets, active, E))
+    tiles = torch.empty((max_tiles, 4), dtype=torch.int32, device="cuda")
+    ntiles = torch.empty(1, dtype=torch.int32, device="cuda")
+    gu.call("glm_moe_tiles", gu.stream(), gu.p(work), E, gu.p(tiles), gu.p(ntiles))
+    want_tiles = [(e, int(offsets[e]) + i, min(128, int(counts[e]) - i))
+                  for e in active for i in range(0, int(counts[e]), 128)]
+    assert int(gu.host(ntiles)[0]) == len(want_tiles)
+    assert [tuple(int(v) for v in t[:3]) for t in gu.host(tiles)[:len(want_tiles)]] == want_tiles
+    d_tok = gu.to_dev((perm // k).astype(np.int32))
+    h = torch.empty((P, I), dtype=torch.bfloat16, device="cuda")
+    y = torch.empty((P, d), dtype=torch.bfloat16, device="cuda")
+    gu.call("glm_expert_gate_up_grouped", gu.stream(), gu.p(dl["x"]), d, I,
+            *(gu.p(dl[key]) for key in BANK_KEYS[:4]), gu.p(d_tok), gu.p(tiles), gu.p(ntiles),
+            max_tiles, shape.swiglu_limit, gu.p(h))
+    gu.call("glm_expert_down_grouped", gu.stream(), gu.p(h), I, d, gu.p(dl[BANK_KEYS[4]]),
+            gu.p(dl[BANK_KEYS[5]]), gu.p(tiles), gu.p(ntiles), max_tiles, gu.p(y))
+    h_got = O.bf16_bits_to_f32(gu.bf16_bits(h))[inv].reshape(T, k, I)
+    y_got = O.bf16_bits_to_f32(gu.bf16_bits(y))[inv].reshape(T, k, d)
+    assert O.rel_l2(h_got, inter["h"]) < REL_L2 and np.mean(h_got == inter["h"]) > 0.97
+    assert O.rel_l2(y_got, y_want) < REL_L2 and np.mean(y_got == y_want) > 0.97
+
+
 def test_routed_experts_generic_shapes(gu):
     # tiny geometry of the reference's tests (tests/helpers.py: d=32, I=32) and
     # one more that is not a multiple of the 128-wide MFMA chunk
@@ -382,11 +419,13 @@ def test_combine_bit_exact(gu):
     np.testing.assert_array_equal(gu.host(out).view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("fmt", [native.GLM_FMT_BF16, native.GLM_FMT_MXFP8])
-def test_dense_mlp_parity(gu, fmt):
+@pytest.mark.parametrize("fmt,T", [(native.GLM_FMT_BF16, 3), (native.GLM_FMT_MXFP8, 3),
+                                   (native.GLM_FMT_BF16, 300)])
+def test_dense_mlp_parity(gu, fmt, T):
+    # T=300 runs the tiled MFMA GEMMs (dense mode of the grouped kernels)
     torch = _torch()
     rng = np.random.default_rng(21)
-    T, d, I = 3, 2048, 768
+    d, I = 2048, 768
     ws = [O.f32_to_bf16_bits(rng.normal(0, 0.02, s).astype(np.float32)) for s in [(I, d), (I, d), (d, I)]]
     x = O.f32_to_bf16_bits(rng.normal(0, 1, (T, d)).astype(np.float32))
     if fmt == native.GLM_FMT_BF16:
@@ -439,6 +478,8 @@ SMALL_LAYERS = [
     (96, 1024, 16, 4, 256, 256, (1, 1)),
     (600, 1024, 16, 4, 256, 256, (1, 1)),
     (200, 2048, 64, 8, 768, 0, (4, 2)),
+    # many pairs: the multi-workgroup dispatch (6 chunks of 1024 pairs, the last partial)
+    (700, 1024, 32, 8, 256, 0, (1, 1)),
 ]
 
 
