@@ -80,8 +80,12 @@ class Setup:
         torch.cuda.set_device(dev)
         gen = torch.Generator(device=dev)
         gen.manual_seed(args.seed)
+        self.layers = shape.layers
         self.layer_bytes = shape.bank_bytes + 3 * Is * d * 2 + E * d * 4
-        self.n_banks = max(2, math.ceil(args.min_rotation_gb * 1e9 / self.layer_bytes))
+        if self.layers > 1:
+            self.layer_bytes += d * d + d * d // 32  # the resident MXFP8 linear
+        self.n_banks = max(2, self.layers,
+                           math.ceil(args.min_rotation_gb * 1e9 / self.layer_bytes))
         self.n_inputs = 64
 
         def randbytes(*s):
@@ -112,12 +116,36 @@ class Setup:
                 from livglm_amd.workloads import zipf_bias
                 b["router_bias"] = torch.from_numpy(
                     zipf_bias(E, np.random.default_rng(args.seed + len(self.banks)))).to(dev)
+            if self.layers > 1:
+                # the resident linear as the reference builds it at start-up:
+                # bf16 N(0, 0.02) quantised to MXFP8 (layers.py:72-99)
+                w = bf16(d, d)
+                b["linear.codes"] = torch.empty((d, d), dtype=torch.uint8, device=dev)
+                b["linear.scales"] = torch.empty((d, d // 32), dtype=torch.uint8, device=dev)
+                native.call("glm_mx_quantize", self.stream, w.data_ptr(), d, d,
+                            native.GLM_FMT_MXFP8, native.GLM_MX_RULE_NEAREST,
+                            b["linear.codes"].data_ptr(), b["linear.scales"].data_ptr())
+                del w
             self.banks.append(b)
+        self.trace = None
+        if shape.routing == "markov":
+            # per (step, layer) bias rows that keep each expert of the previous
+            # step with probability 0.7
+            from livglm_amd.workloads import markov_bias_trace
+            n = max(1, args.warmup + args.steps)
+            self.trace = torch.from_numpy(markov_bias_trace(
+                E, k, self.n_banks, n, np.random.default_rng(args.seed))).to(dev)
         self.xs = torch.randn((self.n_inputs, T, d), device=dev, generator=gen).to(torch.bfloat16)
         # the layer's routed gate/up kernel: token-major for a few tokens, tiled
         # GEMV up to 64 tokens, grouped MFMA GEMMs beyond
         self.few_token = T <= 4 and k <= 8
         self.grouped = T > 64
+
+    def bias(self, step: int, layer: int):
+        """The router bias of one layer at one step."""
+        if self.trace is None:
+            return self.banks[layer]["router_bias"]
+        return self.trace[step % self.trace.shape[0], layer]
 
     @property
     def stream(self) -> int:
@@ -137,9 +165,10 @@ class Setup:
             b, x = self.banks[r % self.n_banks], self.xs[r % self.n_inputs]
             pl = {"logits": torch.empty((T, E), dtype=torch.float32, device=self.dev),
                   "w": torch.empty((T, k), dtype=torch.float32, device=self.dev),
-                  "ix": torch.empty((T, k), **i32)}
+                  "ix": torch.empty((T, k), **i32),
+                  "bias": self.bias(r // self.n_banks, r % self.n_banks)}
             native.call("glm_router_topk", self.stream, x.data_ptr(), T, d,
-                        b["router_weight"].data_ptr(), b["router_bias"].data_ptr(), E, k,
+                        b["router_weight"].data_ptr(), pl["bias"].data_ptr(), E, k,
                         self.shape.n_group, self.shape.topk_group, 1,
                         self.shape.routed_scaling_factor, pl["logits"].data_ptr(),
                         pl["w"].data_ptr(), pl["ix"].data_ptr())
@@ -174,7 +203,7 @@ class Setup:
                         sh.swiglu_limit, self.h.data_ptr())
         elif self.few_token:
             native.call("glm_route_gate_up", self.stream, pl["logits"].data_ptr(),
-                        b["router_bias"].data_ptr(), self.T, self.E, self.k, sh.n_group,
+                        pl["bias"].data_ptr(), self.T, self.E, self.k, sh.n_group,
                         sh.topk_group, 1, sh.routed_scaling_factor, x.data_ptr(), self.d, self.I,
                         *(b[key].data_ptr() for key in self.keys[:4]), sh.swiglu_limit,
                         self.w_k.data_ptr(), self.i_k.data_ptr(), self.h.data_ptr())
@@ -240,17 +269,36 @@ def main() -> int:
     wts = torch.empty((T, k), dtype=torch.float32, device=S.dev)
     idx = torch.empty((T, k), dtype=torch.int32, device=S.dev)
 
-    def layer_step(s: int) -> None:
-        b = S.banks[s % S.n_banks]
-        x = S.xs[s % S.n_inputs]
+    def moe(x, layer: int, step: int) -> None:
+        b = S.banks[layer]
         native.call(
             "glm_moe_forward", S.stream, x.data_ptr(), T, d, b["router_weight"].data_ptr(),
-            b["router_bias"].data_ptr(), E, k, shape.n_group, shape.topk_group,
+            S.bias(step, layer).data_ptr(), E, k, shape.n_group, shape.topk_group,
             int(shape.norm_topk_prob), shape.routed_scaling_factor, I,
             *(b[key].data_ptr() for key in keys), Is, native.GLM_FMT_BF16,
             b["shared.gate"].data_ptr(), None, b["shared.up"].data_ptr(), None,
             b["shared.down"].data_ptr(), None, None, shape.swiglu_limit, ws.data_ptr(), ws_bytes,
             out.data_ptr(), wts.data_ptr(), idx.data_ptr())
+
+    def layer_step(s: int) -> None:
+        moe(S.xs[s % S.n_inputs], s % S.n_banks, s)
+
+    act = torch.empty((T, d), dtype=torch.bfloat16, device=S.dev)
+    carry = [torch.empty((T, d), dtype=torch.bfloat16, device=S.dev) for _ in range(2)]
+
+    def stack_step(s: int) -> None:
+        """One decode step through the layer stack: per layer the resident
+        MXFP8 linear, then the MoE layer on its output; the f32 MoE output,
+        rounded to bf16, is the next layer's input (a stand-in for the
+        decoder's residual and norm, which are not part of this path)."""
+        x = S.xs[s % S.n_inputs]
+        for layer in range(S.layers):
+            b = S.banks[layer]
+            native.call("glm_linear", S.stream, x.data_ptr(), T, d, b["linear.codes"].data_ptr(),
+                        b["linear.scales"].data_ptr(), native.GLM_FMT_MXFP8, d, act.data_ptr())
+            moe(act, layer, s)
+            x = carry[layer & 1]
+            x.copy_(out)
 
     def capture(fn, first: int, count: int):
         g = torch.cuda.CUDAGraph()
@@ -269,15 +317,32 @@ def main() -> int:
         torch.cuda.synchronize()
         return ev0.elapsed_time(ev1) / count, time.perf_counter() - wall0
 
-    # eager pass over every bank first (validates the launches outside capture)
-    for s in range(S.n_banks):
-        layer_step(s)
-    torch.cuda.synchronize()
-
-    # ------------------------------------------------------------ timed layer steps
-    if args.warmup > 0:
-        capture(layer_step, 0, args.warmup).replay()
-    ms_per_step, wall = timed(capture(layer_step, args.warmup, args.steps), args.steps)
+    # ------------------------------------------------------------ timed steps
+    if S.layers > 1:
+        stack_step(0)  # eager pass (validates the launches outside capture)
+        torch.cuda.synchronize()
+        # one graph per decode step (each step has its own routing biases)
+        graphs = [capture(stack_step, s, 1) for s in range(args.warmup + args.steps)]
+        for g in graphs[:args.warmup]:
+            g.replay()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        wall0 = time.perf_counter()
+        ev0.record()
+        for g in graphs[args.warmup:]:
+            g.replay()
+        ev1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - wall0
+        ms_per_step = ev0.elapsed_time(ev1) / args.steps
+        del graphs
+    else:
+        for s in range(S.n_banks):  # eager pass over every bank first
+            layer_step(s)
+        torch.cuda.synchronize()
+        if args.warmup > 0:
+            capture(layer_step, 0, args.warmup).replay()
+        ms_per_step, wall = timed(capture(layer_step, args.warmup, args.steps), args.steps)
     tokens_per_s = T / (ms_per_step / 1e3)
 
     # ------------------------------------------------------------ dominant kernel
@@ -297,7 +362,8 @@ def main() -> int:
     # ------------------------------------------------------------ CPU baseline
     cpu = None
     if args.cpu_seconds > 0:
-        cpu = cpu_baseline(shape, S.banks[0], S.xs, args.cpu_seconds)
+        cpu = cpu_baseline(shape, S.banks[0], S.xs, args.cpu_seconds,
+                           None if S.trace is None else S.trace[0, 0])
 
     line = {
         "metric": METRIC,
@@ -313,8 +379,13 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": f"{shape.name}: MoE layer T={T} d={d} E={E} top-{k} I={I} "
-                        f"(MXFP4 group-32 experts, bf16 shared expert I={Is})",
+            "workload": (f"{shape.name}: {S.layers} layers x (MXFP8 {d}x{d} resident linear + "
+                         f"MoE layer T={T} d={d} E={E} top-{k} I={I}, MXFP4 group-32 experts, "
+                         f"bf16 shared expert I={Is}), Markov routing keeping 70% of the "
+                         f"previous step's experts, one token per step"
+                         if S.layers > 1 else
+                         f"{shape.name}: MoE layer T={T} d={d} E={E} top-{k} I={I} "
+                         f"(MXFP4 group-32 experts, bf16 shared expert I={Is})"),
             "tokens_per_step": T, "weights": "mxfp4-e2m1+e8m0",
             "mfma": "bf16 x dequantised mxfp4", "layer_banks": S.n_banks,
             "rotation_bytes": S.n_banks * S.layer_bytes, "graph_steps": args.steps,
@@ -330,6 +401,16 @@ def main() -> int:
         line["mxfp4_mfma_util"] = round(tflops / MFMA_PEAK_TFLOPS["fp4"], 4)
     else:
         line["decode_expert_hbm_gbps"] = round(achieved, 1)
+    if S.layers > 1:
+        # bytes one decode step reads: every layer's k experts (Markov
+        # routing at T=1 picks k distinct ones), shared expert, linear, router
+        expert = S.layers * k * shape.expert_bytes
+        other = S.layers * (3 * Is * d * 2 + d * d + d * d // 32 + E * d * 4)
+        sec = ms_per_step / 1e3
+        line["stack"] = {"layers": S.layers, "us_per_layer": round(ms_per_step * 1e3 / S.layers, 3),
+                         "expert_bytes_per_step": expert, "all_bytes_per_step": expert + other,
+                         "expert_hbm_gbps": round(expert / sec / 1e9, 1),
+                         "all_hbm_gbps": round((expert + other) / sec / 1e9, 1)}
     line["cpu_baseline"] = cpu
     print(json.dumps(line))
     return 0
@@ -419,9 +500,11 @@ def measure_traffic(args, kernel_name: str):
     return round(fetch[0] + write[0]), note
 
 
-def cpu_baseline(shape, bank, xs, budget_s: float):
+def cpu_baseline(shape, bank, xs, budget_s: float, bias=None):
     """The C restatement (oracle/libmoe_cpu.so, OpenMP over this host's cores)
-    on one resident layer: as many layer steps as fit in ``budget_s``."""
+    on one resident layer: as many layer steps as fit in ``budget_s``.  For a
+    layer stack, one step is the resident MXFP8 linear + the MoE layer, and
+    the stack's rate is that of ``shape.layers`` such steps per token."""
     import numpy as np
     import torch
 
@@ -434,16 +517,32 @@ def cpu_baseline(shape, bank, xs, budget_s: float):
     host = {key: bank[key].cpu().numpy() for key in bank if not key.startswith("shared")}
     for key in ("shared.gate", "shared.up", "shared.down"):
         host[key] = bank[key].view(torch.int16).cpu().numpy().view(np.uint16)
+    if bias is not None:
+        host["router_bias"] = bias.cpu().numpy()
     xs_h = xs.view(torch.int16).cpu().numpy().view(np.uint16)
+    stack = shape.layers > 1
     steps = 0
     t0 = time.perf_counter()
     while True:
-        host["x"] = xs_h[steps % xs_h.shape[0]]
+        x = xs_h[steps % xs_h.shape[0]]
+        if stack:
+            x = cpu_oracle.linear_mxfp8(x, host["linear.codes"], host["linear.scales"])
+        host["x"] = x
         cpu_oracle.moe_layer(host, shape)
         steps += 1
         el = time.perf_counter() - t0
         if el >= budget_s or steps >= 10000:
             break
+    if stack:
+        return {
+            "value": round(steps / (el * shape.layers), 3),
+            "unit": "tokens/s",
+            "cores": cpu_oracle.threads(),
+            "kind": "port",
+            "sample": f"{steps} single-layer steps (MXFP8 {shape.d}x{shape.d} linear + MoE layer, "
+                      f"T={shape.T}) on one resident layer in {el:.2f} s; tokens/s = 1 / "
+                      f"({shape.layers} x mean layer time); C restatement (not MLX), OpenMP",
+        }
     return {
         "value": round(shape.T * steps / el, 2),
         "unit": "tokens/s",
@@ -452,7 +551,6 @@ def cpu_baseline(shape, bank, xs, budget_s: float):
         "sample": f"{steps} layer steps of {shape.name} (T={shape.T}) on one resident layer "
                   f"in {el:.2f} s; C restatement (not MLX), OpenMP",
     }
-
 
 if __name__ == "__main__":
     sys.exit(main())

@@ -27,6 +27,8 @@ def load():
         lib.moe_cpu_layer.restype = _i
         lib.moe_cpu_layer.argtypes = [_p, _i, _i, _p, _p, _i, _i, _i, _i, _i, _f, _i,
                                       _p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _f, _p, _p, _p]
+        lib.moe_cpu_linear_mxfp8.restype = _i
+        lib.moe_cpu_linear_mxfp8.argtypes = [_p, _i, _i, _p, _p, _i, _p]
         _lib = lib
     return _lib
 
@@ -60,3 +62,20 @@ def moe_layer(layer: dict, shape, shared: bool = True):
     if rc != 0:
         raise RuntimeError("moe_cpu_layer rejected its arguments")
     return out, w, idx
+
+
+def linear_mxfp8(x: np.ndarray, codes: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """Resident MXFP8 linear on host arrays: x bf16 bits [T, in], codes u8
+    [out, in], scales u8 [out, in/32]; returns bf16 bits [T, out]."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.uint8)
+    T, n_in = x.shape
+    n_out = codes.shape[0]
+    if codes.shape != (n_out, n_in) or scales.shape != (n_out, n_in // 32):
+        raise ValueError("MXFP8 codes/scales do not match the input width")
+    y = np.empty((T, n_out), np.uint16)
+    if load().moe_cpu_linear_mxfp8(_ptr(x), T, n_in, _ptr(codes), _ptr(scales), n_out,
+                                    _ptr(y)) != 0:
+        raise RuntimeError("moe_cpu_linear_mxfp8 rejected its arguments")
+    return y

@@ -241,3 +241,41 @@ int moe_cpu_layer(const uint16_t *x, int T, int d, const float *rw, const float 
   free(xf), free(h), free(y), free(cnt), free(pairs), free(shared), free(hs);
   return 0;
 }
+
+/* E4M3FN element value (fp8.py:13-30): bias 7, subnormals below 2^-6,
+ * 0x7F / 0xFF NaN. */
+static float e4m3fn(uint8_t c) {
+  const int e = (c >> 3) & 15, m = c & 7;
+  float v;
+  if (e == 15 && m == 7) v = NAN;
+  else if (e == 0) v = ldexpf((float)m / 8.0f, -6);
+  else v = ldexpf(1.0f + (float)m / 8.0f, e - 7);
+  return (c & 0x80) ? -v : v;
+}
+
+/* Resident MXFP8 linear y = bf16(x . deq(W)^T) (layers.py:56-65): codes
+ * [out][in] E4M3FN, scales [out][in/32] E8M0, x and y bf16. */
+int moe_cpu_linear_mxfp8(const uint16_t *x, int T, int in_dims, const uint8_t *codes,
+                         const uint8_t *scales, int out_dims, uint16_t *y) {
+  if (T < 0 || in_dims % 32 || out_dims < 1) return -1;
+  float lut[256];
+  for (int c = 0; c < 256; ++c) lut[c] = e4m3fn((uint8_t)c);
+  float *xf = (float *)malloc(sizeof(float) * (size_t)(T > 0 ? T : 1) * in_dims);
+  for (size_t i = 0; i < (size_t)T * in_dims; ++i) xf[i] = bf16_to_f32(x[i]);
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int t = 0; t < T; ++t)
+    for (int o = 0; o < out_dims; ++o) {
+      const uint8_t *row = codes + (size_t)o * in_dims;
+      const float *xv = xf + (size_t)t * in_dims;
+      float total = 0.0f;
+      for (int g = 0; g < in_dims / 32; ++g) {
+        float lane[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int i = 0; i < 32; ++i) lane[i & 7] += lut[row[g * 32 + i]] * xv[g * 32 + i];
+        float part = ((lane[0] + lane[1]) + (lane[2] + lane[3])) + ((lane[4] + lane[5]) + (lane[6] + lane[7]));
+        total += part * e8m0(scales[(size_t)o * (in_dims / 32) + g]);
+      }
+      y[(size_t)t * out_dims + o] = f32_to_bf16(total);
+    }
+  free(xf);
+  return 0;
+}

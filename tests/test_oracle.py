@@ -431,3 +431,59 @@ def test_oracle_reproduces_committed_golden_layer():
     for key, value in mf.expected(layer).items():
         assert value.dtype == z[key].dtype and np.array_equal(value.view(np.uint8),
                                                               z[key].view(np.uint8)), key
+
+
+# --------------------------------------------------------------------------- C restatement
+
+
+@pytest.fixture(scope="module")
+def cpu_twin():
+    import os
+    from oracle import build, cpu
+    if not os.path.exists(cpu.LIB):
+        build.build()
+    cpu.load()
+    return cpu
+
+
+@pytest.mark.parametrize("n_group,topk_group,shared", [(1, 1, True), (4, 2, True), (2, 1, False)])
+def test_c_restatement_matches_numpy_layer(cpu_twin, n_group, topk_group, shared):
+    # the C twin (bench.py's CPU baseline) against the numpy oracle on one layer
+    from livglm_amd.workloads import MoEShape
+    rng = np.random.default_rng(90 + n_group)
+    shape = MoEShape("tiny", T=6, d=128, E=16, k=4, I=64, I_shared=64 if shared else 0,
+                     n_group=n_group, topk_group=topk_group)
+    bank = _tiny_bank(rng, shape.E, shape.d, shape.I)
+    x = O.f32_to_bf16_bits(rng.normal(0, 1, (shape.T, shape.d)).astype(np.float32))
+    W = rng.normal(0, 0.02, (shape.E, shape.d)).astype(np.float32)
+    b = rng.normal(0, 0.1, shape.E).astype(np.float32)
+    sw = [O.f32_to_bf16_bits(rng.normal(0, 0.02, s).astype(np.float32))
+          for s in [(64, shape.d), (64, shape.d), (shape.d, 64)]]
+    layer = {"x": x, "router_weight": W, "router_bias": b,
+             "shared.gate": sw[0], "shared.up": sw[1], "shared.down": sw[2]}
+    layer.update(zip(("gate_proj.weight_packed", "gate_proj.weight_scale", "up_proj.weight_packed",
+                      "up_proj.weight_scale", "down_proj.weight_packed", "down_proj.weight_scale"),
+                     (bank.gate_w, bank.gate_s, bank.up_w, bank.up_s, bank.down_w,
+                      bank.down_s)))
+    out, w, idx = cpu_twin.moe_layer(layer, shape, shared=shared)
+    want, inter = O.moe_layer(O.bf16_bits_to_f32(x), W, b, bank,
+                              tuple(O.bf16_bits_to_f32(s) for s in sw) if shared else None,
+                              top_k=shape.k, n_group=n_group, topk_group=topk_group,
+                              norm_topk_prob=True, routed_scaling_factor=2.5, swiglu_limit=10.0,
+                              return_intermediates=True)
+    assert np.array_equal(idx, inter["indices"])
+    np.testing.assert_allclose(w, inter["weights"], rtol=1e-6)
+    assert O.rel_l2(out, want) < 1e-5  # f32 lane sums vs exact products: last-bit differences
+
+
+def test_c_restatement_mxfp8_linear(cpu_twin):
+    rng = np.random.default_rng(5308)
+    w = O.f32_to_bf16_bits(rng.normal(0, 0.05, (96, 256)).astype(np.float32))
+    x = O.f32_to_bf16_bits(rng.normal(0, 1, (3, 256)).astype(np.float32))
+    codes, scales = O.quantize_mx(w, 8, O.MX_RULE_NEAREST)
+    got = O.bf16_bits_to_f32(cpu_twin.linear_mxfp8(x, codes, scales))
+    want = O.linear_bf16(O.bf16_bits_to_f32(x), O.dequant_mxfp8(codes, scales))
+    assert O.rel_l2(got, want) < 1e-5
+    assert np.mean(got == want) > 0.95
+    with pytest.raises(ValueError):
+        cpu_twin.linear_mxfp8(x[:, :128], codes, scales)
