@@ -161,6 +161,7 @@ class Setup:
         i32 = dict(dtype=torch.int32, device=self.dev)
         self.max_tiles = (P + 127) // 128 + E
         self.plans = []
+        self.x_splits = {}
         for r in range(R):
             b, x = self.banks[r % self.n_banks], self.xs[r % self.n_inputs]
             pl = {"logits": torch.empty((T, E), dtype=torch.float32, device=self.dev),
@@ -182,6 +183,14 @@ class Setup:
                                                           "tok", "active", "nact", "work",
                                                           "status")))
             if self.grouped:
+                # the grouped GEMM reads the activations as their FP8 split
+                xi = r % self.n_inputs
+                if xi not in self.x_splits:
+                    buf = torch.empty(self.lib.glm_act_split_bytes(T, d), dtype=torch.uint8,
+                                      device=self.dev)
+                    native.call("glm_act_split_fp8", self.stream, x.data_ptr(), T, d,
+                                buf.data_ptr())
+                    self.x_splits[xi] = buf
                 pl["tiles"] = torch.empty((self.max_tiles, 4), **i32)
                 pl["ntiles"] = torch.empty(1, **i32)
                 native.call("glm_moe_tiles", self.stream, pl["work"].data_ptr(), E,
@@ -197,7 +206,8 @@ class Setup:
         b, pl, x = self.banks[r % self.n_banks], self.plans[r], self.xs[r % self.n_inputs]
         sh, native = self.shape, self.native
         if self.grouped:
-            native.call("glm_expert_gate_up_grouped", self.stream, x.data_ptr(), self.d, self.I,
+            native.call("glm_expert_gate_up_grouped", self.stream,
+                        self.x_splits[r % self.n_inputs].data_ptr(), self.T, self.d, self.I,
                         *(b[key].data_ptr() for key in self.keys[:4]), pl["tok"].data_ptr(),
                         pl["tiles"].data_ptr(), pl["ntiles"].data_ptr(), self.max_tiles,
                         sh.swiglu_limit, self.h.data_ptr())
@@ -217,7 +227,7 @@ class Setup:
         """The dominant kernel's instantiation, as rocprofv3 names it."""
         d, E = self.d, self.E
         if self.grouped:
-            return "grouped_mx_gemm_kernel<2, 2>"
+            return "grouped_f8f4_kernel<2>"
         if self.few_token:
             epl = 2 if E <= 128 else (4 if E <= 256 else 8)
             return f"select_gate_up_kernel<{epl}, {d // 512}, 1>"
@@ -387,7 +397,8 @@ def main() -> int:
                          f"{shape.name}: MoE layer T={T} d={d} E={E} top-{k} I={I} "
                          f"(MXFP4 group-32 experts, bf16 shared expert I={Is})"),
             "tokens_per_step": T, "weights": "mxfp4-e2m1+e8m0",
-            "mfma": "bf16 x dequantised mxfp4", "layer_banks": S.n_banks,
+            "mfma": ("fp8 hi/lo split x mxfp4, block-scaled" if S.grouped
+                     else "bf16 x dequantised mxfp4"), "layer_banks": S.n_banks,
             "rotation_bytes": S.n_banks * S.layer_bytes, "graph_steps": args.steps,
             "wall_s": round(wall, 4),
         },
@@ -423,10 +434,17 @@ def roofline(S, achieved, tflops, bytes_per_launch, k_ms, R, traffic, traffic_no
               "bytes_per_launch": round(bytes_per_launch), "avg_launch_us": round(k_ms * 1e3, 3),
               "launches": R, "unique_experts_per_launch": round(sum(S.unique) / R, 2)}
     if S.grouped:
-        return {"kernel": S.kernel_name() + " (grouped MXFP4 gate/up + SwiGLU GEMMs, bf16 MFMA)",
+        # two block-scaled FP8 x FP4 MFMAs (activation hi and lo parts) per
+        # algorithmic product at the 5 PFLOP/s FP8 rate: 2.5 PFLOP/s of
+        # algorithmic work at most, the bf16 peak
+        return {"kernel": S.kernel_name() + " (grouped MXFP4 gate/up + SwiGLU GEMMs, block-scaled "
+                                            "FP8 x FP4 MFMA on the exact hi/lo split of x)",
                 "bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_PEAK_TFLOPS["bf16"],
                 "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS["bf16"], 4),
-                "flops_per_launch": S.kernel_flops(), **common}
+                "flops_per_launch": S.kernel_flops(),
+                "peak_note": "algorithmic FLOPs; the kernel issues two FP8 x FP4 MFMAs per "
+                             "product at the 5.0 PFLOP/s dense FP8 rate",
+                **common}
     return {"kernel": S.kernel_name() + (" (few-token selection + routed MXFP4 gate/up + SwiGLU)"
                                          if S.few_token else
                                          " (routed MXFP4 gate/up + SwiGLU)"),

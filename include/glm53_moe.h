@@ -142,14 +142,33 @@ int glm_expert_down(void *stream, const uint16_t *h, int T, int top_k, int I, in
 int glm_moe_tiles(void *stream, const int32_t *work, int E, int32_t *tiles, int32_t *num_tiles);
 
 /*
- * Prefill routed gate/up as grouped GEMMs on MFMA over the row tiles of
- * glm_moe_tiles.  Replaces gather_qmm(gate/up) + limited_swiglu over all
- * (t, j) pairs (native_expert_ssd.py:726-741, expert_ssd.py:103-107,185-186).
- * Same inputs and output as glm_expert_gate_up: h bf16 [T*k][I] in sorted
- * order, token rows through pair_token.
- * Limits: d % 256 == 0, I % 128 == 0.
+ * Exact two-term FP8 split of bf16 activations for the block-scaled MFMA
+ * GEMMs below.  For every 32-element group of a row:
+ *   x = hi * 2^(shi - 127) + lo * 2^(slo - 127),
+ * hi, lo E4M3FN codes (hi rounded to nearest-even, lo the rounded residual),
+ * shi, slo E8M0, each the smallest scale that keeps its group within 448.
+ * A bf16 element has 8 significant bits and each code holds 4, so elements
+ * within ~14 binades of their group's maximum are reproduced exactly; smaller
+ * ones err by < 2^-22 of that maximum.
+ * split: one buffer of glm_act_split_bytes(rows, K) bytes holding hi
+ * [rows][K], lo [rows][K], shi [rows][K/32], slo [rows][K/32], each 256-byte
+ * aligned.  No reference counterpart: it is the activation operand format of
+ * the grouped GEMMs.  Limits: K % 32 == 0.
  */
-int glm_expert_gate_up_grouped(void *stream, const uint16_t *x, int d, int I,
+size_t glm_act_split_bytes(int rows, int K);
+int glm_act_split_fp8(void *stream, const uint16_t *x, int rows, int K, void *split);
+
+/*
+ * Prefill routed gate/up as grouped GEMMs over the row tiles of
+ * glm_moe_tiles, on the block-scaled MFMA: MXFP4 weights as stored, the
+ * activations as their FP8 split.  Replaces gather_qmm(gate/up) +
+ * limited_swiglu over all (t, j) pairs (native_expert_ssd.py:726-741,
+ * expert_ssd.py:103-107,185-186).
+ * x_split: glm_act_split_fp8 of x bf16 [T][d].  h bf16 [T*k][I] in sorted
+ * order, token rows through pair_token (as glm_expert_gate_up).
+ * Limits: d % 512 == 0, I % 256 == 0.
+ */
+int glm_expert_gate_up_grouped(void *stream, const void *x_split, int T, int d, int I,
                                const uint8_t *gate_packed, const uint8_t *gate_scales,
                                const uint8_t *up_packed, const uint8_t *up_scales,
                                const int32_t *pair_token, const int32_t *tiles,
@@ -158,9 +177,10 @@ int glm_expert_gate_up_grouped(void *stream, const uint16_t *x, int d, int I,
 
 /*
  * Prefill routed down projection as grouped GEMMs (native_expert_ssd.py:743).
- * y bf16 [T*k][d] in sorted order.  Limits: d % 256 == 0, I % 128 == 0.
+ * h_split: glm_act_split_fp8 of h bf16 [P = T*k][I] (sorted order).
+ * y bf16 [P][d] in sorted order.  Limits: d % 512 == 0, I % 256 == 0.
  */
-int glm_expert_down_grouped(void *stream, const uint16_t *h, int I, int d,
+int glm_expert_down_grouped(void *stream, const void *h_split, int P, int I, int d,
                             const uint8_t *down_packed, const uint8_t *down_scales,
                             const int32_t *tiles, const int32_t *num_tiles, int max_tiles,
                             uint16_t *y);

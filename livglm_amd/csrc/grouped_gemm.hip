@@ -38,23 +38,49 @@ namespace glm {
 constexpr int kTileM = 128;    // token rows per tile
 constexpr int kTileW = 256;    // weight rows per workgroup
 constexpr int kThreads = 512;  // 8 waves: 4 along the weight rows x 2 along the tokens
+constexpr int kWaves = kThreads / 64;
 constexpr int kXcds = 8;
+constexpr int kStages = 3;     // LDS ring: two chunks in flight while one is consumed
 
+// One K chunk of a workgroup's operands in LDS, unpadded and XOR-swizzled in
+// 16-byte pieces so that the MFMA operand reads (16 rows x one piece column)
+// hit distinct banks:
+//   activations  [kTileM rows][kChunk bf16]   piece p of row R at p ^ xswz(R)
+//   weights      [kTileW rows][kWRowBytes]    piece p of row R at p ^ wswz(R)
+//   scales       [kTileW rows] u32            (MXFP4: the chunk's 4 E8M0 bytes)
+// Direct global->LDS loads write one wave's 64 x 16 bytes contiguously, so a
+// lane's LDS slot is fixed by its lane id; each lane fetches the global piece
+// that belongs in its slot.
 template <int WFMT>
 struct GroupedLayout {
   static constexpr int kChunk = WFMT == FMT_MXFP4 ? 128 : 64;  // K per stage
-  static constexpr int kXStride = kChunk + 8;                  // staged activation row, bf16
+  static constexpr int kXRowBytes = kChunk * 2;
   static constexpr int kWRowBytes = WFMT == FMT_MXFP4 ? kChunk / 2 : kChunk * 2;
-  static constexpr int kWStride = kWRowBytes + 16;             // staged weight row, bytes
-  static constexpr int kXBytes = kTileM * kXStride * 2;
-  static constexpr int kWBytes = kTileW * kWStride;
+  static constexpr int kXBytes = kTileM * kXRowBytes;
+  static constexpr int kWBytes = kTileW * kWRowBytes;
   static constexpr int kSBytes = WFMT == FMT_MXFP4 ? kTileW * 4 : 0;
   static constexpr int kStageBytes = kXBytes + kWBytes + kSBytes;
-  static constexpr int kXPerRow = kChunk / 8;  // 16-byte pieces per staged row
+  static constexpr int kXPerRow = kXRowBytes / 16;  // pieces per row
   static constexpr int kWPerRow = kWRowBytes / 16;
-  static constexpr int kXPieces = kTileM * kXPerRow / kThreads;  // pieces per thread
-  static constexpr int kWPieces = kTileW * kWPerRow / kThreads;
+  static constexpr int kXLoads = kXBytes / (kThreads * 16);  // 16-byte loads per thread
+  static constexpr int kWLoads = kWBytes / (kThreads * 16);
+  static constexpr int kSLoads = WFMT == FMT_MXFP4 ? 1 : 0;  // 4-byte loads per thread
+  static constexpr int kLoads = kXLoads + kWLoads + kSLoads;  // per chunk, per thread
+  static_assert(kXBytes % (kThreads * 16) == 0 && kWBytes % (kThreads * 16) == 0, "staging");
+  static_assert(kStages * kStageBytes <= 160 * 1024, "LDS ring exceeds 160 KB");
+
+  // 256-byte activation rows: 16 pieces, swizzle over the row's low 4 bits;
+  // 128-byte rows: 8 pieces, the low 3 bits.
+  __device__ static int xswz(int row) { return kXPerRow == 16 ? (row & 15) : (row & 7); }
+  // 64-byte MXFP4 weight rows pair up in 128 bytes: swizzle by row / 2.
+  __device__ static int wswz(int row) { return kWPerRow == 4 ? ((row >> 1) & 3) : (row & 7); }
 };
+
+// s_waitcnt immediate that waits for the vector-memory counter to reach n
+// (at most n of this wave's loads outstanding) and leaves the others alone.
+__host__ __device__ constexpr int vmcnt_imm(int n) {
+  return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
+}
 
 struct GroupedArgs {
   const uint16_t *act;       // gate/up: x [T][K]; down: h [P][K]
@@ -70,6 +96,25 @@ struct GroupedArgs {
   uint16_t *out;             // bf16 [rows][N]
   float limit;               // bf16-rounded SwiGLU limit (gate/up)
 };
+
+// Direct global->LDS loads: lane i's 16 (4) bytes land at lds + 16 i (4 i);
+// the LDS address is wave-uniform.
+__device__ __forceinline__ void load16_to_lds(const void *src, void *lds) {
+  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+}
+__device__ __forceinline__ void load4_to_lds(const void *src, void *lds) {
+  __builtin_amdgcn_global_load_lds(src, lds, 4, 0, 0);
+}
+
+// Workgroup barrier without a memory fence: the direct-to-LDS loads are
+// waited for explicitly (vmcnt) before it, and a fence here would make the
+// compiler wait for every load in flight, including the prefetched chunks.
+// The empty asm statements keep the compiler from moving LDS accesses across.
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 template <int NPROJ, int WFMT>
 __global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a) {
@@ -100,70 +145,51 @@ __global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a
   const int f0 = ftile * (kTileW / NPROJ);
   const int wrow_bytes = WFMT == FMT_MXFP4 ? K / 2 : K * 2;
 
-  // ---- staging assignment (fixed over the K loop)
-  // activations: piece j = row tid / kXPerRow + j * (kThreads / kXPerRow), 16
-  // bytes at column tid % kXPerRow.  Rows past the tile's end re-read its first
-  // row: MFMA columns are independent and those columns are never stored.
-  const uint16_t *xsrc[L::kXPieces];
+  // ---- load assignment (fixed over the K loop).  Load j of wave w fills the
+  // (j * kWaves + w)-th 1 KB block of the stage region.
+  const uint8_t *xsrc[L::kXLoads];
 #pragma unroll
-  for (int j = 0; j < L::kXPieces; ++j) {
-    const int row = tid / L::kXPerRow + j * (kThreads / L::kXPerRow);
+  for (int j = 0; j < L::kXLoads; ++j) {
+    const int slot = (j * kWaves + wave) * 64 + lane;  // 16-byte slot in the region
+    const int row = slot / L::kXPerRow, piece = (slot % L::kXPerRow) ^ L::xswz(row);
+    // rows past the tile's end re-read its first row: MFMA columns are
+    // independent and those columns are never stored
     const int pos = pos0 + (row < rows ? row : 0);
     const long long arow = a.act_index != nullptr ? a.act_index[pos] : pos;
-    xsrc[j] = a.act + arow * K + (tid % L::kXPerRow) * 8;
+    xsrc[j] = reinterpret_cast<const uint8_t *>(a.act + arow * K) + piece * 16;
   }
-  // weights: piece j = row tid / kWPerRow + j * (kThreads / kWPerRow); scales: row tid < kTileW
-  const uint8_t *wsrc[L::kWPieces];
+  const uint8_t *wsrc[L::kWLoads];
 #pragma unroll
-  for (int j = 0; j < L::kWPieces; ++j) {
-    const int wrow = tid / L::kWPerRow + j * (kThreads / L::kWPerRow);
-    const int p = NPROJ == 2 ? wrow / (kTileW / 2) : 0;
-    const int frow = f0 + (NPROJ == 2 ? wrow % (kTileW / 2) : wrow);
-    wsrc[j] = a.w[p] + e * a.w_stride + (size_t)frow * wrow_bytes + (tid % L::kWPerRow) * 16;
+  for (int j = 0; j < L::kWLoads; ++j) {
+    const int slot = (j * kWaves + wave) * 64 + lane;
+    const int row = slot / L::kWPerRow, piece = (slot % L::kWPerRow) ^ L::wswz(row);
+    // (a select, not a.w[p]: a lane-varying index into the kernel arguments
+    // becomes a vector memory load)
+    const uint8_t *wbase = NPROJ == 2 && row >= kTileW / 2 ? a.w[1] : a.w[0];
+    const int frow = f0 + (NPROJ == 2 ? row % (kTileW / 2) : row);
+    wsrc[j] = wbase + e * a.w_stride + (size_t)frow * wrow_bytes + piece * 16;
   }
   const uint8_t *ssrc = nullptr;
   if constexpr (WFMT == FMT_MXFP4) {
-    const int srow = tid & (kTileW - 1);
-    const int p = NPROJ == 2 ? srow / (kTileW / 2) : 0;
-    const int frow = f0 + (NPROJ == 2 ? srow % (kTileW / 2) : srow);
-    ssrc = a.s[p] + e * a.s_stride + (size_t)frow * (K / 32);
+    // 4 waves cover the 256 rows' scale dwords; waves 4..7 load the same
+    // bytes again so every wave issues the same number of loads per chunk
+    const int row = (wave & 3) * 64 + lane;
+    const uint8_t *sbase = NPROJ == 2 && row >= kTileW / 2 ? a.s[1] : a.s[0];
+    const int frow = f0 + (NPROJ == 2 ? row % (kTileW / 2) : row);
+    ssrc = sbase + e * a.s_stride + (size_t)frow * (K / 32);
   }
 
-  // one chunk's staged operands in registers
-  struct Stage {
-    glm_u32x4 x[L::kXPieces], w[L::kWPieces];
-    uint32_t s;
-  };
-  auto load_stage = [&](int c, Stage &st) {
+  // Direct global->LDS loads of chunk c into ring stage `stage`.
+  auto issue = [&](int c, int stage) {
+    uint8_t *base = smem + stage * L::kStageBytes;
 #pragma unroll
-    for (int j = 0; j < L::kXPieces; ++j)
-      st.x[j] = *reinterpret_cast<const glm_u32x4 *>(xsrc[j] + c * L::kChunk);
+    for (int j = 0; j < L::kXLoads; ++j)
+      load16_to_lds(xsrc[j] + c * L::kXRowBytes, base + (j * kWaves + wave) * 1024);
 #pragma unroll
-    for (int j = 0; j < L::kWPieces; ++j) st.w[j] = load_stream(wsrc[j] + c * L::kWRowBytes);
-    st.s = 0;
+    for (int j = 0; j < L::kWLoads; ++j)
+      load16_to_lds(wsrc[j] + c * L::kWRowBytes, base + L::kXBytes + (j * kWaves + wave) * 1024);
     if constexpr (WFMT == FMT_MXFP4)
-      if (tid < kTileW) st.s = *reinterpret_cast<const uint32_t *>(ssrc + c * (L::kChunk / 32));
-  };
-  auto store_stage = [&](int buf, const Stage &st) {
-    uint8_t *base = smem + buf * L::kStageBytes;
-    uint16_t *sx = reinterpret_cast<uint16_t *>(base);
-    uint8_t *sw = base + L::kXBytes;
-#pragma unroll
-    for (int j = 0; j < L::kXPieces; ++j)
-      *reinterpret_cast<glm_u32x4 *>(sx +
-                                     (tid / L::kXPerRow + j * (kThreads / L::kXPerRow)) *
-                                         L::kXStride +
-                                     (tid % L::kXPerRow) * 8) = st.x[j];
-#pragma unroll
-    for (int j = 0; j < L::kWPieces; ++j)
-      *reinterpret_cast<glm_u32x4 *>(sw +
-                                     (tid / L::kWPerRow + j * (kThreads / L::kWPerRow)) *
-                                         L::kWStride +
-                                     (tid % L::kWPerRow) * 16) = st.w[j];
-    if constexpr (WFMT == FMT_MXFP4) {
-      uint32_t *ss = reinterpret_cast<uint32_t *>(sw + L::kWBytes);
-      if (tid < kTileW) ss[tid] = st.s;
-    }
+      load4_to_lds(ssrc + c * 4, base + L::kXBytes + L::kWBytes + (wave & 3) * 256);
   };
 
   glm_f32x4 acc[4][4];
@@ -177,11 +203,12 @@ __global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a
   auto wrow_of = [&](int rt) {
     return NPROJ == 2 ? (rt / 2) * (kTileW / 2) + wf * 32 + (rt % 2) * 16 : wf * 64 + rt * 16;
   };
-
-  // MFMAs of one staged chunk
-  auto compute = [&](int buf) {
-    const uint8_t *base = smem + buf * L::kStageBytes;
-    const uint16_t *sx = reinterpret_cast<const uint16_t *>(base);
+  // MFMAs of one staged chunk.  MXFP4: MFMA i, slot s of lane (r, q) is
+  // K = 32q + 8i + s (lane q's 16 weight bytes are one whole E8M0 group);
+  // bf16: K = 32i + 8q + s.
+  auto compute = [&](int stage) {
+    const uint8_t *base = smem + stage * L::kStageBytes;
+    const uint8_t *sx = base;
     const uint8_t *sw = base + L::kXBytes;
     if constexpr (WFMT == FMT_MXFP4) {
       const uint32_t *ss = reinterpret_cast<const uint32_t *>(sw + L::kWBytes);
@@ -190,16 +217,19 @@ __global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt) {
         const int wr = wrow_of(rt) + r;
-        raw[rt] = *reinterpret_cast<const glm_u32x4 *>(sw + wr * L::kWStride + 16 * q);
+        raw[rt] = *reinterpret_cast<const glm_u32x4 *>(sw + wr * L::kWRowBytes +
+                                                       16 * (q ^ L::wswz(wr)));
         scale[rt] = e8m0_to_f32((ss[wr] >> (8 * q)) & 0xffu);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         glm_bf16x8 xb[4];
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
-          xb[ct] = *reinterpret_cast<const glm_bf16x8 *>(
-              sx + (wt * 64 + ct * 16 + r) * L::kXStride + 32 * q + 8 * i);
+        for (int ct = 0; ct < 4; ++ct) {
+          const int xr = wt * 64 + ct * 16 + r;
+          xb[ct] = *reinterpret_cast<const glm_bf16x8 *>(sx + xr * L::kXRowBytes +
+                                                         16 * ((4 * q + i) ^ L::xswz(xr)));
+        }
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
           const glm_bf16x8 af = mxfp4_word_to_bf16x8(raw[rt][i], scale[rt]);
@@ -213,13 +243,17 @@ __global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a
       for (int i = 0; i < L::kChunk / 32; ++i) {
         glm_bf16x8 xb[4], af[4];
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
-          xb[ct] = *reinterpret_cast<const glm_bf16x8 *>(
-              sx + (wt * 64 + ct * 16 + r) * L::kXStride + 32 * i + 8 * q);
+        for (int ct = 0; ct < 4; ++ct) {
+          const int xr = wt * 64 + ct * 16 + r;
+          xb[ct] = *reinterpret_cast<const glm_bf16x8 *>(sx + xr * L::kXRowBytes +
+                                                         16 * ((4 * i + q) ^ L::xswz(xr)));
+        }
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt)
-          af[rt] = *reinterpret_cast<const glm_bf16x8 *>(sw + (wrow_of(rt) + r) * L::kWStride +
-                                                         64 * i + 16 * q);
+        for (int rt = 0; rt < 4; ++rt) {
+          const int wr = wrow_of(rt) + r;
+          af[rt] = *reinterpret_cast<const glm_bf16x8 *>(sw + wr * L::kWRowBytes +
+                                                         16 * ((4 * i + q) ^ L::wswz(wr)));
+        }
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
@@ -230,19 +264,20 @@ __global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a
     }
   };
 
-  Stage st;
-  load_stage(0, st);
-  store_stage(0, st);
-  __syncthreads();
-  // steady state: next chunk's loads in flight during this chunk's MFMAs; the
-  // last chunk is peeled so the loop body has no conditional work
-  for (int c = 0; c + 1 < nchunks; ++c) {
-    load_stage(c + 1, st);
-    compute(c & 1);
-    store_stage((c + 1) & 1, st);
-    __syncthreads();
+  // Ring: chunks c + 1 and c + 2 are in flight while chunk c is consumed.  The
+  // barrier of iteration c also guarantees that every wave has finished
+  // chunk c - 1, whose stage the loads of chunk c + 2 overwrite.
+  issue(0, 0);
+  if (nchunks > 1) issue(1, 1);
+  for (int c = 0; c < nchunks; ++c) {
+    if (c + 1 < nchunks)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(L::kLoads));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    ring_barrier();
+    if (c + 2 < nchunks) issue(c + 2, (c + 2) % kStages);
+    compute(c % kStages);
   }
-  compute((nchunks - 1) & 1);
 
   // ---- epilogue: lane (r, q) of tile (rt, ct) holds features 4q..4q+3 of the
   // row tile for token column r
@@ -273,6 +308,319 @@ __global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a
   }
 }
 
+// ---------------------------------------------------------------------------
+// Routed expert GEMMs on the block-scaled MFMA
+// (v_mfma_scale_f32_16x16x128_f8f6f4): MXFP4 weights enter as they are stored
+// (E2M1 codes + their E8M0 group scales), the bf16 activations as an exact
+// two-term FP8 split
+//     x = hi * 2^(shi - 127) + lo * 2^(slo - 127)     per 32-element group,
+// hi, lo E4M3FN codes with their own E8M0 scales.  hi holds the top 4
+// significant bits of each element, lo the remaining <= 4 (a bf16 element has
+// 8), so the split reproduces every element exactly unless it lies ~14
+// binades below its group's maximum, where the error stays below 2^-22 of
+// that maximum.  Each 16x16x128 output block is then two MFMAs (hi, lo)
+// accumulating in f32: no dequantisation instructions at all.
+//
+// Operand layout of the 16x16x128 MFMA, lane (i = l % 16, g = l / 16):
+//   A = weights (E2M1, 16 bytes): weight row i, K [32g, 32g + 32) -- exactly
+//       one stored MXFP4 group, so lane g's 16 bytes come straight from the
+//       row and its scale operand is that group's E8M0 byte;
+//   B = activations (E4M3, 32 bytes): token i, K [16g, 16g + 16) in bytes
+//       0..15 and K [64 + 16g, 64 + 16g + 16) in bytes 16..31; scale operand:
+//       token i's E8M0 byte of group g (K [32g, 32g + 32));
+//   D: lane holds weight rows 4g..4g+3 of token column i.
+// ---------------------------------------------------------------------------
+
+// Byte offsets of an activation split of `rows` x K: hi codes, lo codes,
+// hi scales, lo scales, each 256-byte aligned.
+struct SplitLayout {
+  size_t lo, shi, slo, total;
+  __host__ __device__ SplitLayout(long long rows, int K) {
+    const size_t codes = ((size_t)rows * K + 255) & ~(size_t)255;
+    const size_t scales = ((size_t)rows * (K / 32) + 255) & ~(size_t)255;
+    lo = codes;
+    shi = 2 * codes;
+    slo = 2 * codes + scales;
+    total = 2 * codes + 2 * scales;
+  }
+};
+
+// E8M0 exponent byte for a group whose largest magnitude is amax: the
+// smallest 2^(b - 127) with amax / 2^(b - 127) <= 448 (E4M3FN's maximum).
+__device__ __forceinline__ int split_scale_byte(float amax) {
+  if (!(amax > 0.0f)) return 127;
+  int e;
+  const float m = frexpf(amax, &e);  // amax = m 2^e, m in [0.5, 1)
+  const int k = m <= 0.875f ? e - 9 : e - 8;
+  return min(max(k + 127, 0), 254);
+}
+
+// One thread per 32-element group: hi/lo E4M3FN codes and their scales.
+__global__ __launch_bounds__(256) void act_split_kernel(const uint16_t *x, long long groups,
+                                                        uint8_t *hi, uint8_t *lo, uint8_t *shi,
+                                                        uint8_t *slo) {
+  const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= groups) return;
+  const glm_u32x4 *src = reinterpret_cast<const glm_u32x4 *>(x + g * 32);
+  float v[32];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const glm_u32x4 w = src[j];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      v[8 * j + 2 * h] = __uint_as_float(w[h] << 16);
+      v[8 * j + 2 * h + 1] = __uint_as_float(w[h] & 0xffff0000u);
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+  const int bh = split_scale_byte(amax);
+  uint32_t ch[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j], 127 - bh),
+                                            ldexpf(v[4 * j + 1], 127 - bh), 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j + 2], 127 - bh),
+                                        ldexpf(v[4 * j + 3], 127 - bh), w, true);
+    ch[j] = (uint32_t)w;
+  }
+  // residuals (exact in f32) and their own scale
+  float ramax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int w = (int)ch[j];
+    v[4 * j] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 0), bh - 127);
+    v[4 * j + 1] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 1), bh - 127);
+    v[4 * j + 2] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 2), bh - 127);
+    v[4 * j + 3] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 3), bh - 127);
+  }
+#pragma unroll
+  for (int j = 0; j < 32; ++j) ramax = fmaxf(ramax, fabsf(v[j]));
+  const int bl = split_scale_byte(ramax);
+  uint32_t cl[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j], 127 - bl),
+                                            ldexpf(v[4 * j + 1], 127 - bl), 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j + 2], 127 - bl),
+                                        ldexpf(v[4 * j + 3], 127 - bl), w, true);
+    cl[j] = (uint32_t)w;
+  }
+  glm_u32x4 *dh = reinterpret_cast<glm_u32x4 *>(hi + g * 32);
+  glm_u32x4 *dl = reinterpret_cast<glm_u32x4 *>(lo + g * 32);
+  dh[0] = glm_u32x4{ch[0], ch[1], ch[2], ch[3]};
+  dh[1] = glm_u32x4{ch[4], ch[5], ch[6], ch[7]};
+  dl[0] = glm_u32x4{cl[0], cl[1], cl[2], cl[3]};
+  dl[1] = glm_u32x4{cl[4], cl[5], cl[6], cl[7]};
+  shi[g] = (uint8_t)bh;
+  slo[g] = (uint8_t)bl;
+}
+
+struct SplitArgs {
+  const uint8_t *xhi, *xlo;    // activation codes [rows][K]
+  const uint8_t *xshi, *xslo;  // activation scales [rows][K/32]
+  const int32_t *act_index;    // sorted position -> activation row (nullptr: the position)
+  const int4 *tiles;           // {expert, first sorted position, rows, 0}
+  const int32_t *num_tiles;
+  const uint8_t *w[2];         // stacked MXFP4 weights [E][N][K/2] per projection
+  const uint8_t *s[2];         // stacked E8M0 scales [E][N][K/32]
+  long long w_stride, s_stride;
+  int N, K;
+  int feature_tiles;
+  uint16_t *out;               // bf16 [rows][N]
+  float limit;
+};
+
+// Workgroup tile of the block-scaled GEMMs: 128 token rows x 512 weight rows
+// (gate/up: 256 features of each projection), 8 waves as 4 (weight rows) x
+// 2 (tokens), each wave 128 weight rows x 64 tokens = 8 x 4 MFMA blocks.  The
+// activations cost 2 bytes per element (hi + lo) against the weights' half
+// byte, so the tile is wide along the weights: per 128-K chunk a workgroup
+// stages 64 KB of operands for 2 x 128 x 512 x 128 MACs.
+constexpr int kSplitTileW = 512;
+constexpr int kSplitStages = 2;  // double buffer: chunk c + 1 lands while c is consumed
+
+// LDS stage (one 128-K chunk):
+//   activations  [128 rows][hi 128 B | lo 128 B], piece p of row R at p ^ (R & 15)
+//   act. scales  hi [128 rows] u32, lo [128 rows] u32 (the chunk's 4 E8M0 bytes)
+//   weights      [512 rows][64 B], piece p of row R at p ^ ((R >> 1) & 3)
+//   w. scales    [512 rows] u32
+struct SplitStage {
+  static constexpr int kChunk = 128;
+  static constexpr int kXBytes = kTileM * 256;
+  static constexpr int kXSBytes = 2 * kTileM * 4;
+  static constexpr int kWBytes = kSplitTileW * 64;
+  static constexpr int kWSBytes = kSplitTileW * 4;
+  static constexpr int kX = 0, kXS = kXBytes, kW = kXS + kXSBytes, kWS = kW + kWBytes;
+  static constexpr int kBytes = kWS + kWSBytes;
+  static constexpr int kXLoads = kXBytes / (kThreads * 16);  // 4
+  static constexpr int kWLoads = kWBytes / (kThreads * 16);  // 4
+  // + two scale dwords per thread: one of the weight scales (8 waves x 64
+  // rows), one of the activation scales (waves 0-3; waves 4-7 repeat them so
+  // every wave issues the same count)
+  static constexpr int kLoads = kXLoads + kWLoads + 2;
+  static_assert(kSplitStages * kBytes <= 160 * 1024, "LDS stages exceed 160 KB");
+};
+
+typedef int glm_i32x8 __attribute__((ext_vector_type(8)));
+
+template <int NPROJ>
+__global__ __launch_bounds__(kThreads) void grouped_f8f4_kernel(SplitArgs a) {
+  using S = SplitStage;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int nft = a.feature_tiles;
+  const int ntiles = *a.num_tiles;
+  const int items = ntiles * nft;
+  const int lin = blockIdx.x;
+  const int per_xcd = (items + kXcds - 1) / kXcds;
+  const int k_on_xcd = lin / kXcds;
+  const int item = (lin % kXcds) * per_xcd + k_on_xcd;
+  if (k_on_xcd >= per_xcd || item >= items) return;
+  const int tile_id = item / nft, ftile = item % nft;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int wf = wave & 3, wt = wave >> 2;
+  const int4 tile = a.tiles[tile_id];
+  const long long e = tile.x;
+  const int pos0 = tile.y, rows = tile.z;
+  const int K = a.K;
+  const int nchunks = K / S::kChunk;
+  constexpr int kHalf = kSplitTileW / 2;
+  const int f0 = ftile * (kSplitTileW / NPROJ);
+  auto act_row = [&](int row) -> long long {
+    const int pos = pos0 + (row < rows ? row : 0);  // past the end: re-read row 0
+    return a.act_index != nullptr ? a.act_index[pos] : pos;
+  };
+  // staged weight row R -> (projection, feature row)
+  auto w_base = [&](int row, const uint8_t *const *arr) {
+    return NPROJ == 2 && row >= kHalf ? arr[1] : arr[0];
+  };
+  auto w_feature = [&](int row) { return f0 + (NPROJ == 2 ? row % kHalf : row); };
+
+  // ---- load assignment (fixed over the K loop).  Load j of wave w fills the
+  // (j * 8 + w)-th 1 KB block of its region.
+  const uint8_t *xsrc[S::kXLoads];
+#pragma unroll
+  for (int j = 0; j < S::kXLoads; ++j) {
+    const int slot = (j * kWaves + wave) * 64 + lane;
+    const int row = slot / 16, piece = (slot % 16) ^ (row & 15);
+    xsrc[j] = (piece < 8 ? a.xhi : a.xlo) + act_row(row) * K + (piece & 7) * 16;
+  }
+  const uint8_t *wsrc[S::kWLoads];
+#pragma unroll
+  for (int j = 0; j < S::kWLoads; ++j) {
+    const int slot = (j * kWaves + wave) * 64 + lane;
+    const int row = slot / 4, piece = (slot % 4) ^ ((row >> 1) & 3);
+    wsrc[j] = w_base(row, a.w) + e * a.w_stride + (size_t)w_feature(row) * (K / 2) + piece * 16;
+  }
+  const int wsrow = wave * 64 + lane;
+  const uint8_t *wssrc =
+      w_base(wsrow, a.s) + e * a.s_stride + (size_t)w_feature(wsrow) * (K / 32);
+  const int xj = wave & 3;  // hi rows 0-63, hi 64-127, lo 0-63, lo 64-127
+  const uint8_t *xssrc = (xj < 2 ? a.xshi : a.xslo) + act_row((xj & 1) * 64 + lane) * (K / 32);
+
+  auto issue = [&](int c, int stage) {
+    uint8_t *base = smem + stage * S::kBytes;
+#pragma unroll
+    for (int j = 0; j < S::kXLoads; ++j)
+      load16_to_lds(xsrc[j] + c * 128, base + S::kX + (j * kWaves + wave) * 1024);
+#pragma unroll
+    for (int j = 0; j < S::kWLoads; ++j)
+      load16_to_lds(wsrc[j] + c * 64, base + S::kW + (j * kWaves + wave) * 1024);
+    load4_to_lds(wssrc + c * 4, base + S::kWS + wave * 256);
+    load4_to_lds(xssrc + c * 4, base + S::kXS + xj * 256);
+  };
+
+  // this wave's weight-row blocks: 8 of 16 rows (gate/up: 4 gate blocks, then
+  // the 4 up blocks of the same features)
+  auto wrow_of = [&](int rt) {
+    return NPROJ == 2 ? (rt / 4) * kHalf + wf * 64 + (rt % 4) * 16 : wf * 128 + rt * 16;
+  };
+
+  glm_f32x4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = glm_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // MFMAs of one staged chunk: for each activation fragment (hi/lo x 4 token
+  // blocks) 8 MFMAs, one per weight-row block.
+  auto compute = [&](int stage) {
+    const uint8_t *base = smem + stage * S::kBytes;
+    glm_i32x8 wa[8];
+    int wsc[8];
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt) {
+      const int wr = wrow_of(rt) + r;
+      const glm_u32x4 v = *reinterpret_cast<const glm_u32x4 *>(base + S::kW + wr * 64 +
+                                                             16 * (q ^ ((wr >> 1) & 3)));
+      wa[rt] = glm_i32x8{(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
+      wsc[rt] = (int)(reinterpret_cast<const uint32_t *>(base + S::kWS)[wr] >> (8 * q));
+    }
+#pragma unroll
+    for (int part = 0; part < 2; ++part) {  // hi, then lo
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const int xr = wt * 64 + ct * 16 + r;
+        const uint8_t *xrow = base + S::kX + xr * 256;
+        const glm_u32x4 b0 =
+            *reinterpret_cast<const glm_u32x4 *>(xrow + 16 * ((8 * part + q) ^ (xr & 15)));
+        const glm_u32x4 b1 =
+            *reinterpret_cast<const glm_u32x4 *>(xrow + 16 * ((8 * part + 4 + q) ^ (xr & 15)));
+        const glm_i32x8 xb = glm_i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3],
+                                       (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+        const int xsc =
+            (int)(reinterpret_cast<const uint32_t *>(base + S::kXS)[part * kTileM + xr] >> (8 * q));
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt)
+          acc[rt][ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              wa[rt], xb, acc[rt][ct], 4, 0, 0, wsc[rt], 0, xsc);
+      }
+    }
+  };
+
+  // Double buffer: the loads of chunk c + 1 are issued after the barrier that
+  // follows every wave's chunk c - 1 (whose stage they overwrite) and land
+  // while chunk c is consumed.
+  issue(0, 0);
+  for (int c = 0; c < nchunks; ++c) {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    ring_barrier();
+    if (c + 1 < nchunks) issue(c + 1, (c + 1) % kSplitStages);
+    compute(c % kSplitStages);
+  }
+
+  // ---- epilogue: lane (r, q) of block (rt, ct) holds weight rows 4q..4q+3 of
+  // the block for token column r
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    const int row = wt * 64 + ct * 16 + r;
+    if (row >= rows) continue;
+    uint16_t *orow = a.out + (size_t)(pos0 + row) * a.N;
+    if constexpr (NPROJ == 2) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t o[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          o[m] = f32_to_bf16(limited_swiglu(bf16_round(acc[i][ct][m]),
+                                            bf16_round(acc[4 + i][ct][m]), a.limit));
+        store_rows4(orow + f0 + wf * 64 + i * 16 + 4 * q, o);
+      }
+    } else {
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt) {
+        uint32_t o[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) o[m] = f32_to_bf16(acc[rt][ct][m]);
+        store_rows4(orow + f0 + wf * 128 + rt * 16 + 4 * q, o);
+      }
+    }
+  }
+}
+
 }  // namespace glm
 
 using namespace glm;
@@ -282,7 +630,7 @@ int glm_grouped_tile_rows() { return kTileM; }
 // Whether the grouped GEMMs cover these shapes: gate/up K = d, N = I in
 // feature tiles of 128 per projection; down K = I, N = d in tiles of 256.
 bool glm_grouped_supported(int d, int I) {
-  return d % 128 == 0 && I % 128 == 0 && d % 256 == 0;
+  return d % 512 == 0 && I % 256 == 0;
 }
 
 static int grouped_launch(hipStream_t stream, GroupedArgs a, int nproj, int wfmt, int max_tiles) {
@@ -292,7 +640,7 @@ static int grouped_launch(hipStream_t stream, GroupedArgs a, int nproj, int wfmt
   const long long max_items = (long long)max_tiles * a.feature_tiles;
   const dim3 grid((unsigned)(((max_items + kXcds - 1) / kXcds) * kXcds));
   if (wfmt == FMT_MXFP4) {
-    const size_t lds = 2 * (size_t)GroupedLayout<FMT_MXFP4>::kStageBytes;
+    const size_t lds = kStages * (size_t)GroupedLayout<FMT_MXFP4>::kStageBytes;
     if (nproj == 2)
       hipLaunchKernelGGL((grouped_mx_gemm_kernel<2, FMT_MXFP4>), grid, dim3(kThreads), lds,
                          stream, a);
@@ -300,7 +648,7 @@ static int grouped_launch(hipStream_t stream, GroupedArgs a, int nproj, int wfmt
       hipLaunchKernelGGL((grouped_mx_gemm_kernel<1, FMT_MXFP4>), grid, dim3(kThreads), lds,
                          stream, a);
   } else {
-    const size_t lds = 2 * (size_t)GroupedLayout<FMT_BF16>::kStageBytes;
+    const size_t lds = kStages * (size_t)GroupedLayout<FMT_BF16>::kStageBytes;
     if (nproj == 2)
       hipLaunchKernelGGL((grouped_mx_gemm_kernel<2, FMT_BF16>), grid, dim3(kThreads), lds,
                          stream, a);
@@ -312,12 +660,51 @@ static int grouped_launch(hipStream_t stream, GroupedArgs a, int nproj, int wfmt
   return GLM_OK;
 }
 
-int glm_grouped_gate_up_launch(hipStream_t stream, const uint16_t *x, const int32_t *pair_token,
-                               const int4 *tiles, const int32_t *num_tiles, int max_tiles, int d,
-                               int I, const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
+size_t glm_act_split_bytes(long long rows, int K) { return SplitLayout(rows, K).total; }
+
+// bf16 activations [rows][K] -> their hi/lo FP8 split (layout SplitLayout).
+int glm_act_split_launch(hipStream_t stream, const uint16_t *x, long long rows, int K,
+                         void *split) {
+  const long long groups = rows * (K / 32);
+  if (groups <= 0) return GLM_OK;
+  const SplitLayout L(rows, K);
+  uint8_t *base = static_cast<uint8_t *>(split);
+  hipLaunchKernelGGL(act_split_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0,
+                     stream, x, groups, base, base + L.lo, base + L.shi, base + L.slo);
+  GLM_LAUNCH_CHECK("act_split_kernel");
+  return GLM_OK;
+}
+
+static int split_launch(hipStream_t stream, SplitArgs a, int nproj, int max_tiles) {
+  a.feature_tiles = a.N / (nproj == 2 ? kSplitTileW / 2 : kSplitTileW);
+  const long long max_items = (long long)max_tiles * a.feature_tiles;
+  const dim3 grid((unsigned)(((max_items + kXcds - 1) / kXcds) * kXcds));
+  const size_t lds = kSplitStages * (size_t)SplitStage::kBytes;
+  if (nproj == 2)
+    hipLaunchKernelGGL(grouped_f8f4_kernel<2>, grid, dim3(kThreads), lds, stream, a);
+  else
+    hipLaunchKernelGGL(grouped_f8f4_kernel<1>, grid, dim3(kThreads), lds, stream, a);
+  GLM_LAUNCH_CHECK("grouped_f8f4_kernel");
+  return GLM_OK;
+}
+
+static void set_split(SplitArgs &a, const void *split, long long rows, int K) {
+  const SplitLayout L(rows, K);
+  const uint8_t *base = static_cast<const uint8_t *>(split);
+  a.xhi = base;
+  a.xlo = base + L.lo;
+  a.xshi = base + L.shi;
+  a.xslo = base + L.slo;
+}
+
+// x_split: the split of the T token rows of x (d columns).
+int glm_grouped_gate_up_launch(hipStream_t stream, const void *x_split, int T,
+                               const int32_t *pair_token, const int4 *tiles,
+                               const int32_t *num_tiles, int max_tiles, int d, int I,
+                               const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
                                const uint8_t *us, uint16_t *h, float limit) {
-  GroupedArgs a{};
-  a.act = x;
+  SplitArgs a{};
+  set_split(a, x_split, T, d);
   a.act_index = pair_token;
   a.tiles = tiles;
   a.num_tiles = num_tiles;
@@ -331,14 +718,15 @@ int glm_grouped_gate_up_launch(hipStream_t stream, const uint16_t *x, const int3
   a.K = d;
   a.out = h;
   a.limit = glm_limit_bf16(limit);
-  return grouped_launch(stream, a, 2, FMT_MXFP4, max_tiles);
+  return split_launch(stream, a, 2, max_tiles);
 }
 
-int glm_grouped_down_launch(hipStream_t stream, const uint16_t *h, const int4 *tiles,
-                            const int32_t *num_tiles, int max_tiles, int I, int d,
-                            const uint8_t *dw, const uint8_t *ds, uint16_t *y) {
-  GroupedArgs a{};
-  a.act = h;
+// h_split: the split of the P sorted rows of h (I columns).
+int glm_grouped_down_launch(hipStream_t stream, const void *h_split, long long P,
+                            const int4 *tiles, const int32_t *num_tiles, int max_tiles, int I,
+                            int d, const uint8_t *dw, const uint8_t *ds, uint16_t *y) {
+  SplitArgs a{};
+  set_split(a, h_split, P, I);
   a.act_index = nullptr;
   a.tiles = tiles;
   a.num_tiles = num_tiles;
@@ -349,7 +737,7 @@ int glm_grouped_down_launch(hipStream_t stream, const uint16_t *h, const int4 *t
   a.N = d;
   a.K = I;
   a.out = y;
-  return grouped_launch(stream, a, 1, FMT_MXFP4, max_tiles);
+  return split_launch(stream, a, 1, max_tiles);
 }
 
 // Dense bf16 SwiGLU MLP over T token rows (the shared expert at many tokens):
@@ -385,41 +773,59 @@ int glm_grouped_dense_mlp_launch(hipStream_t stream, const uint16_t *x, int T, i
 
 bool glm_grouped_supported(int d, int I);
 
-extern "C" int glm_expert_gate_up_grouped(void *stream, const uint16_t *x, int d, int I,
+extern "C" size_t glm_act_split_bytes(int rows, int K) {
+  if (rows < 0 || K <= 0 || K % 32 != 0) return 0;
+  return glm_act_split_bytes((long long)rows, K);
+}
+
+extern "C" int glm_act_split_fp8(void *stream, const uint16_t *x, int rows, int K, void *split) {
+  glm::clear_error();
+  GLM_REQUIRE(x && split, GLM_ERR_INVALID_ARGUMENT, "act_split_fp8: null pointer argument");
+  GLM_REQUIRE(rows >= 0 && K > 0 && K % 32 == 0, GLM_ERR_INVALID_ARGUMENT,
+              "act_split_fp8: needs rows >= 0 and K %% 32 == 0 (rows=%d K=%d)", rows, K);
+  GLM_REQUIRE(glm_aligned16({x, split}), GLM_ERR_INVALID_ARGUMENT,
+              "act_split_fp8: buffers must be 16-byte aligned");
+  return glm_act_split_launch((hipStream_t)stream, x, rows, K, split);
+}
+
+extern "C" int glm_expert_gate_up_grouped(void *stream, const void *x_split, int T, int d, int I,
                                           const uint8_t *gate_packed, const uint8_t *gate_scales,
                                           const uint8_t *up_packed, const uint8_t *up_scales,
                                           const int32_t *pair_token, const int32_t *tiles,
                                           const int32_t *num_tiles, int max_tiles,
                                           float swiglu_limit, uint16_t *h) {
   glm::clear_error();
-  GLM_REQUIRE(x && gate_packed && gate_scales && up_packed && up_scales && pair_token && tiles &&
-                  num_tiles && h,
+  GLM_REQUIRE(x_split && gate_packed && gate_scales && up_packed && up_scales && pair_token &&
+                  tiles && num_tiles && h,
               GLM_ERR_INVALID_ARGUMENT, "expert_gate_up_grouped: null pointer argument");
-  GLM_REQUIRE(max_tiles >= 0, GLM_ERR_INVALID_ARGUMENT, "expert_gate_up_grouped: max_tiles < 0");
+  GLM_REQUIRE(max_tiles >= 0 && T >= 0, GLM_ERR_INVALID_ARGUMENT,
+              "expert_gate_up_grouped: max_tiles < 0 or T < 0");
   GLM_REQUIRE(glm_grouped_supported(d, I), GLM_ERR_UNSUPPORTED_SHAPE,
-              "expert_gate_up_grouped: needs d %% 256 == 0 and I %% 128 == 0 (d=%d I=%d)", d, I);
-  GLM_REQUIRE(glm_aligned16({x, gate_packed, up_packed, tiles, h}), GLM_ERR_INVALID_ARGUMENT,
-              "expert_gate_up_grouped: buffers must be 16-byte aligned");
-  if (max_tiles == 0) return GLM_OK;
-  return glm_grouped_gate_up_launch((hipStream_t)stream, x, pair_token,
+              "expert_gate_up_grouped: needs d %% 512 == 0 and I %% 256 == 0 (d=%d I=%d)", d, I);
+  GLM_REQUIRE(glm_aligned16({x_split, gate_packed, up_packed, tiles, h}),
+              GLM_ERR_INVALID_ARGUMENT, "expert_gate_up_grouped: buffers must be 16-byte aligned");
+  if (max_tiles == 0 || T == 0) return GLM_OK;
+  return glm_grouped_gate_up_launch((hipStream_t)stream, x_split, T, pair_token,
                                     reinterpret_cast<const int4 *>(tiles), num_tiles, max_tiles,
                                     d, I, gate_packed, gate_scales, up_packed, up_scales, h,
                                     swiglu_limit);
 }
 
-extern "C" int glm_expert_down_grouped(void *stream, const uint16_t *h, int I, int d,
+extern "C" int glm_expert_down_grouped(void *stream, const void *h_split, int P, int I, int d,
                                        const uint8_t *down_packed, const uint8_t *down_scales,
                                        const int32_t *tiles, const int32_t *num_tiles,
                                        int max_tiles, uint16_t *y) {
   glm::clear_error();
-  GLM_REQUIRE(h && down_packed && down_scales && tiles && num_tiles && y,
+  GLM_REQUIRE(h_split && down_packed && down_scales && tiles && num_tiles && y,
               GLM_ERR_INVALID_ARGUMENT, "expert_down_grouped: null pointer argument");
-  GLM_REQUIRE(max_tiles >= 0, GLM_ERR_INVALID_ARGUMENT, "expert_down_grouped: max_tiles < 0");
+  GLM_REQUIRE(max_tiles >= 0 && P >= 0, GLM_ERR_INVALID_ARGUMENT,
+              "expert_down_grouped: max_tiles < 0 or P < 0");
   GLM_REQUIRE(glm_grouped_supported(d, I), GLM_ERR_UNSUPPORTED_SHAPE,
-              "expert_down_grouped: needs d %% 256 == 0 and I %% 128 == 0 (d=%d I=%d)", d, I);
-  GLM_REQUIRE(glm_aligned16({h, down_packed, tiles, y}), GLM_ERR_INVALID_ARGUMENT,
+              "expert_down_grouped: needs d %% 512 == 0 and I %% 256 == 0 (d=%d I=%d)", d, I);
+  GLM_REQUIRE(glm_aligned16({h_split, down_packed, tiles, y}), GLM_ERR_INVALID_ARGUMENT,
               "expert_down_grouped: buffers must be 16-byte aligned");
-  if (max_tiles == 0) return GLM_OK;
-  return glm_grouped_down_launch((hipStream_t)stream, h, reinterpret_cast<const int4 *>(tiles),
-                                 num_tiles, max_tiles, I, d, down_packed, down_scales, y);
+  if (max_tiles == 0 || P == 0) return GLM_OK;
+  return glm_grouped_down_launch((hipStream_t)stream, h_split, P,
+                                 reinterpret_cast<const int4 *>(tiles), num_tiles, max_tiles, I,
+                                 d, down_packed, down_scales, y);
 }

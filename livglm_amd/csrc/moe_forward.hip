@@ -43,13 +43,17 @@ int glm_dispatch_launch(hipStream_t stream, const uint32_t *indices, int T, int 
 size_t glm_dispatch_chunk_ints(long long P, int E);
 int glm_grouped_tile_rows();
 bool glm_grouped_supported(int d, int I);
-int glm_grouped_gate_up_launch(hipStream_t stream, const uint16_t *x, const int32_t *pair_token,
-                               const int4 *tiles, const int32_t *num_tiles, int max_tiles, int d,
-                               int I, const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
+size_t glm_act_split_bytes(long long rows, int K);
+int glm_act_split_launch(hipStream_t stream, const uint16_t *x, long long rows, int K,
+                         void *split);
+int glm_grouped_gate_up_launch(hipStream_t stream, const void *x_split, int T,
+                               const int32_t *pair_token, const int4 *tiles,
+                               const int32_t *num_tiles, int max_tiles, int d, int I,
+                               const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
                                const uint8_t *us, uint16_t *h, float limit);
-int glm_grouped_down_launch(hipStream_t stream, const uint16_t *h, const int4 *tiles,
-                            const int32_t *num_tiles, int max_tiles, int I, int d,
-                            const uint8_t *dw, const uint8_t *ds, uint16_t *y);
+int glm_grouped_down_launch(hipStream_t stream, const void *h_split, long long P,
+                            const int4 *tiles, const int32_t *num_tiles, int max_tiles, int I,
+                            int d, const uint8_t *dw, const uint8_t *ds, uint16_t *y);
 int glm_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int E, int k,
                        const uint8_t *gw, const uint8_t *gs, const uint8_t *uw, const uint8_t *us,
                        const int32_t *pair_token, const int4 *work, float limit, uint16_t *h);
@@ -121,6 +125,8 @@ struct Workspace {
   int32_t *chunk_counts;  // multi-workgroup dispatch: per-chunk expert counts, then bases
   int32_t *num_tiles;
   int max_tiles;
+  void *x_split;   // grouped GEMMs: FP8 hi/lo split of x [T][d] and of h [P][I]
+  void *h_split;
   float *gp, *up;  // decode shared-expert gate/up partials [skq][T][Is]
   float *yp;       // decode shared-expert down partials [skd][T][d]
   size_t bytes;
@@ -156,6 +162,10 @@ Workspace carve(char *base, int T, int d, int E, int k, int I, int Is) {
   w.tiles = (int4 *)take((size_t)w.max_tiles * sizeof(int4));
   w.num_tiles = (int32_t *)take(4);
   w.chunk_counts = (int32_t *)take(glm_dispatch_chunk_ints((long long)P, E) * 4);
+  if (d % 32 == 0 && I % 32 == 0) {
+    w.x_split = take(glm_act_split_bytes((long long)T, d));
+    w.h_split = take(glm_act_split_bytes((long long)P, I));
+  }
   const size_t tis = (size_t)T * (Is > 0 ? Is : 0) * 4;
   const int skq = d % 512 == 0 ? d / 512 : 1;
   const int skd = Is >= 128 ? Is / 128 : 1;  // bound on the down K split
@@ -294,12 +304,16 @@ extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
                            grouped ? w.num_tiles : nullptr, w.chunk_counts);
   if (rc) return rc;
   if (grouped) {
-    rc = glm_grouped_gate_up_launch(stream, x, w.pair_token, w.tiles, w.num_tiles, w.max_tiles,
-                                    d, I, gate_packed, gate_scales, up_packed, up_scales, w.h,
-                                    swiglu_limit);
+    rc = glm_act_split_launch(stream, x, T, d, w.x_split);
     if (rc) return rc;
-    rc = glm_grouped_down_launch(stream, w.h, w.tiles, w.num_tiles, w.max_tiles, I, d,
-                                 down_packed, down_scales, w.y);
+    rc = glm_grouped_gate_up_launch(stream, w.x_split, T, w.pair_token, w.tiles, w.num_tiles,
+                                    w.max_tiles, d, I, gate_packed, gate_scales, up_packed,
+                                    up_scales, w.h, swiglu_limit);
+    if (rc) return rc;
+    rc = glm_act_split_launch(stream, w.h, (long long)T * top_k, I, w.h_split);
+    if (rc) return rc;
+    rc = glm_grouped_down_launch(stream, w.h_split, (long long)T * top_k, w.tiles, w.num_tiles,
+                                 w.max_tiles, I, d, down_packed, down_scales, w.y);
   } else {
     rc = glm_gate_up_launch(stream, x, T, d, I, E, top_k, gate_packed, gate_scales, up_packed,
                             up_scales, w.pair_token, w.work, swiglu_limit, w.h);

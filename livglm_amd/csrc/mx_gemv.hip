@@ -161,21 +161,31 @@ __global__ __launch_bounds__(512) void mx_gemv_kernel(const GemvArgs args) {
 
   for (int p0 = 0; p0 < n; p0 += 16 * kMaxTiles) {
     const int ntiles = min(kMaxTiles, (n - p0 + 15) >> 4);
-    // Issue every weight load of this wave first.
+    // Activation row of this lane's token column, per tile.  Columns past the
+    // last row read a valid row (the last one) instead of branching: an MFMA
+    // output column depends only on its own B column, and those columns are
+    // never stored.  Branch-free loads let every load below be in flight at
+    // once.
+    int arow[kMaxTiles];
+#pragma unroll
+    for (int tt = 0; tt < kMaxTiles; ++tt) {
+      const int pair = min(p0 + tt * 16 + r, n - 1);
+      arow[tt] = args.act_index ? args.act_index[base + pair] : base + pair;
+    }
+    // Issue every weight load of this wave, then tile 0's activation
+    // fragments for all chunks, before the first wait.
     Raw<FMT> raw[NPROJ][CPW];
 #pragma unroll
     for (int c = 0; c < CPW; ++c)
 #pragma unroll
       for (int p = 0; p < NPROJ; ++p) raw[p][c] = load_raw<FMT>(wrow[p], srow[p], kbase + c * 128, q);
-
-    // Activation row of this lane's token column, per tile (-1 = padding).
-    int arow[kMaxTiles];
+    glm_bf16x8 b0[CPW][4];
 #pragma unroll
-    for (int tt = 0; tt < kMaxTiles; ++tt) {
-      const int pair = p0 + tt * 16 + r;
-      arow[tt] = -1;
-      if (tt < ntiles && pair < n)
-        arow[tt] = args.act_index ? args.act_index[base + pair] : base + pair;
+    for (int c = 0; c < CPW; ++c) {
+      const glm_bf16x8 *src = reinterpret_cast<const glm_bf16x8 *>(
+          args.act + (long long)arow[0] * K + kbase + c * 128 + 32 * q);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) b0[c][i] = src[i];
     }
 
     glm_f32x4 acc[kMaxTiles][NPROJ];
@@ -191,18 +201,18 @@ __global__ __launch_bounds__(512) void mx_gemv_kernel(const GemvArgs args) {
       for (int p = 0; p < NPROJ; ++p) to_frags<FMT>(raw[p][c], a[p]);
       const int k0 = kbase + c * 128 + 32 * q;
 #pragma unroll
-      for (int tt = 0; tt < kMaxTiles; ++tt) {
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int p = 0; p < NPROJ; ++p)
+          acc[0][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[p][i], b0[c][i], acc[0][p], 0, 0, 0);
+#pragma unroll
+      for (int tt = 1; tt < kMaxTiles; ++tt) {
         if (tt < ntiles) {
+          const glm_bf16x8 *src =
+              reinterpret_cast<const glm_bf16x8 *>(args.act + (long long)arow[tt] * K + k0);
           glm_bf16x8 b[4];
-          if (arow[tt] >= 0) {
-            const glm_bf16x8 *src =
-                reinterpret_cast<const glm_bf16x8 *>(args.act + (long long)arow[tt] * K + k0);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) b[i] = src[i];
-          } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) b[i] = glm_bf16x8{};
-          }
+          for (int i = 0; i < 4; ++i) b[i] = src[i];
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll

@@ -45,8 +45,11 @@ SIGNATURES = {
                                _f, _p, _p, _p]),
     "glm_expert_down": (_i, [_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _p]),
     "glm_moe_tiles": (_i, [_p, _p, _i, _p, _p]),
-    "glm_expert_gate_up_grouped": (_i, [_p, _p, _i, _i, _p, _p, _p, _p, _p, _p, _p, _i, _f, _p]),
-    "glm_expert_down_grouped": (_i, [_p, _p, _i, _i, _p, _p, _p, _p, _i, _p]),
+    "glm_act_split_bytes": (_sz, [_i, _i]),
+    "glm_act_split_fp8": (_i, [_p, _p, _i, _i, _p]),
+    "glm_expert_gate_up_grouped": (_i, [_p, _p, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _i, _f,
+                                        _p]),
+    "glm_expert_down_grouped": (_i, [_p, _p, _i, _i, _i, _p, _p, _p, _p, _i, _p]),
     "glm_moe_combine": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _p]),
     "glm_linear": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _p]),
     "glm_dense_mlp": (_i, [_p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _f, _p, _p]),

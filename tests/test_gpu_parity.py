@@ -344,15 +344,75 @@ def test_grouped_expert_gemms_parity(gu):
     d_tok = gu.to_dev((perm // k).astype(np.int32))
     h = torch.empty((P, I), dtype=torch.bfloat16, device="cuda")
     y = torch.empty((P, d), dtype=torch.bfloat16, device="cuda")
-    gu.call("glm_expert_gate_up_grouped", gu.stream(), gu.p(dl["x"]), d, I,
+    lib = native.load()
+    x_split = gu.workspace(lib.glm_act_split_bytes(T, d))
+    h_split = gu.workspace(lib.glm_act_split_bytes(P, I))
+    gu.call("glm_act_split_fp8", gu.stream(), gu.p(dl["x"]), T, d, gu.p(x_split))
+    gu.call("glm_expert_gate_up_grouped", gu.stream(), gu.p(x_split), T, d, I,
             *(gu.p(dl[key]) for key in BANK_KEYS[:4]), gu.p(d_tok), gu.p(tiles), gu.p(ntiles),
             max_tiles, shape.swiglu_limit, gu.p(h))
-    gu.call("glm_expert_down_grouped", gu.stream(), gu.p(h), I, d, gu.p(dl[BANK_KEYS[4]]),
-            gu.p(dl[BANK_KEYS[5]]), gu.p(tiles), gu.p(ntiles), max_tiles, gu.p(y))
+    gu.call("glm_act_split_fp8", gu.stream(), gu.p(h), P, I, gu.p(h_split))
+    gu.call("glm_expert_down_grouped", gu.stream(), gu.p(h_split), P, I, d,
+            gu.p(dl[BANK_KEYS[4]]), gu.p(dl[BANK_KEYS[5]]), gu.p(tiles), gu.p(ntiles), max_tiles,
+            gu.p(y))
     h_got = O.bf16_bits_to_f32(gu.bf16_bits(h))[inv].reshape(T, k, I)
     y_got = O.bf16_bits_to_f32(gu.bf16_bits(y))[inv].reshape(T, k, d)
     assert O.rel_l2(h_got, inter["h"]) < REL_L2 and np.mean(h_got == inter["h"]) > 0.97
     assert O.rel_l2(y_got, y_want) < REL_L2 and np.mean(y_got == y_want) > 0.97
+
+
+def _split_model(xb, K):
+    """numpy model of the FP8 activation split: per 32-element group the
+    smallest E8M0 scale keeping the group within 448, hi = RNE E4M3FN of the
+    scaled group, lo = RNE E4M3FN of the exact residual under its own scale."""
+    x = O.bf16_bits_to_f32(xb).reshape(-1, K // 32, 32)
+
+    def scale_byte(amax):
+        m, e = np.frexp(amax.astype(np.float64))
+        k = np.where(m <= 0.875, e - 9, e - 8)
+        return np.where(amax > 0, np.clip(k + 127, 0, 254), 127).astype(np.int64)
+
+    bh = scale_byte(np.abs(x).max(axis=2))
+    hi = O.e4m3fn_encode(np.ldexp(x, (127 - bh)[..., None]))
+    back = (O.e4m3fn_table()[hi].astype(np.float64) * np.ldexp(1.0, bh - 127)[..., None])
+    r = (x.astype(np.float64) - back).astype(np.float32)
+    bl = scale_byte(np.abs(r).max(axis=2))
+    lo = O.e4m3fn_encode(np.ldexp(r, (127 - bl)[..., None]))
+    return hi.reshape(-1, K), lo.reshape(-1, K), bh.astype(np.uint8), bl.astype(np.uint8)
+
+
+def _split_parts(buf, rows, K):
+    def up(v):
+        return (v + 255) // 256 * 256
+    raw = buf.cpu().numpy()
+    c, sc = up(rows * K), up(rows * K // 32)
+    return (raw[:rows * K].reshape(rows, K), raw[c:c + rows * K].reshape(rows, K),
+            raw[2 * c:2 * c + rows * K // 32].reshape(rows, K // 32),
+            raw[2 * c + sc:2 * c + sc + rows * K // 32].reshape(rows, K // 32))
+
+
+def test_act_split_fp8_exact(gu):
+    # the FP8 split of bf16 activations: codes and scales bit-exact against
+    # the numpy model, and hi + lo reproduce every element exactly for
+    # normal-range data (groups of N(0, s) with s over 12 binades, zero groups,
+    # single-element groups)
+    rng = np.random.default_rng(29)
+    rows, K = 96, 512
+    x = rng.normal(0, 1, (rows, K // 32, 32)) * np.ldexp(1.0, rng.integers(-6, 6, (rows, K // 32, 1)))
+    x[0, :3] = 0.0
+    x[1, 0, 1:] = 0.0
+    xb = O.f32_to_bf16_bits(x.reshape(rows, K).astype(np.float32))
+    lib = native.load()
+    buf = gu.workspace(lib.glm_act_split_bytes(rows, K))
+    gu.call("glm_act_split_fp8", gu.stream(), gu.p(gu.to_dev(xb)), rows, K, gu.p(buf))
+    hi, lo, shi, slo = _split_parts(buf, rows, K)
+    w_hi, w_lo, w_shi, w_slo = _split_model(xb, K)
+    assert np.array_equal(shi, w_shi.reshape(rows, -1)) and np.array_equal(slo, w_slo.reshape(rows, -1))
+    assert np.array_equal(hi, w_hi) and np.array_equal(lo, w_lo)
+    tab = O.e4m3fn_table().astype(np.float64)
+    recon = (tab[hi].reshape(rows, -1, 32) * np.ldexp(1.0, shi.astype(np.int64) - 127)[..., None]
+             + tab[lo].reshape(rows, -1, 32) * np.ldexp(1.0, slo.astype(np.int64) - 127)[..., None])
+    assert np.array_equal(recon.reshape(rows, K), O.bf16_bits_to_f32(xb).astype(np.float64))
 
 
 def test_routed_experts_generic_shapes(gu):
