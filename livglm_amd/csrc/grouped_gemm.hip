@@ -106,6 +106,22 @@ __device__ __forceinline__ void load4_to_lds(const void *src, void *lds) {
   __builtin_amdgcn_global_load_lds(src, lds, 4, 0, 0);
 }
 
+// Buffer-resource forms: a wave-uniform base and size in scalar registers,
+// a 32-bit per-lane offset and a uniform per-chunk offset; reads past the
+// size return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ void buf16_to_lds(__amdgpu_buffer_rsrc_t rs, void *lds, uint32_t voff,
+                                             uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void buf4_to_lds(__amdgpu_buffer_rsrc_t rs, void *lds, uint32_t voff,
+                                            uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds, 4, voff, soff, 0, 0);
+}
+
 // Workgroup barrier without a memory fence: the direct-to-LDS loads are
 // waited for explicitly (vmcnt) before it, and a fence here would make the
 // compiler wait for every load in flight, including the prefetched chunks.
@@ -420,6 +436,7 @@ __global__ __launch_bounds__(256) void act_split_kernel(const uint16_t *x, long 
 struct SplitArgs {
   const uint8_t *xhi, *xlo;    // activation codes [rows][K]
   const uint8_t *xshi, *xslo;  // activation scales [rows][K/32]
+  uint32_t split_bytes;        // the split buffer starting at xhi (SplitLayout)
   const int32_t *act_index;    // sorted position -> activation row (nullptr: the position)
   const int4 *tiles;           // {expert, first sorted position, rows, 0}
   const int32_t *num_tiles;
@@ -433,12 +450,15 @@ struct SplitArgs {
 };
 
 // Workgroup tile of the block-scaled GEMMs: 128 token rows x 512 weight rows
-// (gate/up: 256 features of each projection), 8 waves as 4 (weight rows) x
-// 2 (tokens), each wave 128 weight rows x 64 tokens = 8 x 4 MFMA blocks.  The
+// (gate/up: 256 features of each projection), 16 waves as 8 (weight rows) x
+// 2 (tokens), each wave 64 weight rows x 64 tokens = 4 x 4 MFMA blocks.  The
 // activations cost 2 bytes per element (hi + lo) against the weights' half
 // byte, so the tile is wide along the weights: per 128-K chunk a workgroup
-// stages 64 KB of operands for 2 x 128 x 512 x 128 MACs.
+// stages 67 KB of operands for 2 x 128 x 512 x 128 MACs.  Four waves per SIMD
+// hide each other's LDS reads behind their MFMAs.
 constexpr int kSplitTileW = 512;
+constexpr int kSplitThreads = 1024;
+constexpr int kSplitWaves = kSplitThreads / 64;
 constexpr int kSplitStages = 2;  // double buffer: chunk c + 1 lands while c is consumed
 
 // LDS stage (one 128-K chunk):
@@ -454,19 +474,20 @@ struct SplitStage {
   static constexpr int kWSBytes = kSplitTileW * 4;
   static constexpr int kX = 0, kXS = kXBytes, kW = kXS + kXSBytes, kWS = kW + kWBytes;
   static constexpr int kBytes = kWS + kWSBytes;
-  static constexpr int kXLoads = kXBytes / (kThreads * 16);  // 4
-  static constexpr int kWLoads = kWBytes / (kThreads * 16);  // 4
-  // + two scale dwords per thread: one of the weight scales (8 waves x 64
-  // rows), one of the activation scales (waves 0-3; waves 4-7 repeat them so
-  // every wave issues the same count)
-  static constexpr int kLoads = kXLoads + kWLoads + 2;
+  static constexpr int kXLoads = kXBytes / (kSplitThreads * 16);  // 2
+  static constexpr int kWLoads = kWBytes / (kSplitThreads * 16);  // 2
+  // + one scale dword per thread: waves 0-7 the weight scales (64 rows each),
+  // waves 8-11 the activation scales, waves 12-15 the same again (so every
+  // wave issues the same count)
+  static constexpr int kLoads = kXLoads + kWLoads + 1;
   static_assert(kSplitStages * kBytes <= 160 * 1024, "LDS stages exceed 160 KB");
+  static_assert(kWSBytes == 8 * 256 && kXSBytes == 4 * 256, "scale loads per wave");
 };
 
 typedef int glm_i32x8 __attribute__((ext_vector_type(8)));
 
 template <int NPROJ>
-__global__ __launch_bounds__(kThreads) void grouped_f8f4_kernel(SplitArgs a) {
+__global__ __launch_bounds__(kSplitThreads) void grouped_f8f4_kernel(SplitArgs a) {
   using S = SplitStage;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int nft = a.feature_tiles;
@@ -481,7 +502,8 @@ __global__ __launch_bounds__(kThreads) void grouped_f8f4_kernel(SplitArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int wf = wave & 3, wt = wave >> 2;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform copy
+  const int wf = wv & 7, wt = wv >> 3;
   const int4 tile = a.tiles[tile_id];
   const long long e = tile.x;
   const int pos0 = tile.y, rows = tile.z;
@@ -500,83 +522,115 @@ __global__ __launch_bounds__(kThreads) void grouped_f8f4_kernel(SplitArgs a) {
   auto w_feature = [&](int row) { return f0 + (NPROJ == 2 ? row % kHalf : row); };
 
   // ---- load assignment (fixed over the K loop).  Load j of wave w fills the
-  // (j * 8 + w)-th 1 KB block of its region.
-  const uint8_t *xsrc[S::kXLoads];
+  // (j * 16 + w)-th 1 KB block of its region.  Bases are wave-uniform buffer
+  // resources, per-lane offsets 32-bit; the chunk advances the uniform offset.
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.xhi, a.split_bytes);
+  const uint32_t lo_off = (uint32_t)(a.xlo - a.xhi);
+  uint32_t xoff[S::kXLoads];
 #pragma unroll
   for (int j = 0; j < S::kXLoads; ++j) {
-    const int slot = (j * kWaves + wave) * 64 + lane;
+    const int slot = (j * kSplitWaves + wave) * 64 + lane;
     const int row = slot / 16, piece = (slot % 16) ^ (row & 15);
-    xsrc[j] = (piece < 8 ? a.xhi : a.xlo) + act_row(row) * K + (piece & 7) * 16;
+    xoff[j] = (piece < 8 ? 0u : lo_off) + (uint32_t)act_row(row) * (uint32_t)K + (piece & 7) * 16;
   }
-  const uint8_t *wsrc[S::kWLoads];
+  // weight load j covers staged rows [256 j, 256 j + 256): one projection
+  const uint32_t wproj_bytes = (uint32_t)a.N * (uint32_t)(K / 2);
+  __amdgpu_buffer_rsrc_t wrs[S::kWLoads];
+  uint32_t woff[S::kWLoads];
 #pragma unroll
   for (int j = 0; j < S::kWLoads; ++j) {
-    const int slot = (j * kWaves + wave) * 64 + lane;
+    const int slot = (j * kSplitWaves + wave) * 64 + lane;
     const int row = slot / 4, piece = (slot % 4) ^ ((row >> 1) & 3);
-    wsrc[j] = w_base(row, a.w) + e * a.w_stride + (size_t)w_feature(row) * (K / 2) + piece * 16;
+    wrs[j] = make_rsrc(a.w[NPROJ == 2 ? j : 0] + e * a.w_stride, wproj_bytes);
+    woff[j] = (uint32_t)w_feature(row) * (uint32_t)(K / 2) + piece * 16;
   }
-  const int wsrow = wave * 64 + lane;
-  const uint8_t *wssrc =
-      w_base(wsrow, a.s) + e * a.s_stride + (size_t)w_feature(wsrow) * (K / 32);
-  const int xj = wave & 3;  // hi rows 0-63, hi 64-127, lo 0-63, lo 64-127
-  const uint8_t *xssrc = (xj < 2 ? a.xshi : a.xslo) + act_row((xj & 1) * 64 + lane) * (K / 32);
+  static_assert(S::kWLoads == 2 && kSplitWaves * 64 / 4 == kHalf, "one projection per load");
+  __amdgpu_buffer_rsrc_t srs;
+  uint32_t soff;
+  int sdst;
+  if (wv < 8) {
+    // weight scales: waves 0-3 the first 256 staged rows, 4-7 the second
+    const int row = wv * 64 + lane;
+    srs = make_rsrc(a.s[NPROJ == 2 && wv >= 4 ? 1 : 0] + e * a.s_stride,
+                    (uint32_t)a.N * (uint32_t)(K / 32));
+    soff = (uint32_t)w_feature(row) * (uint32_t)(K / 32);
+    sdst = S::kWS + wv * 256;
+  } else {
+    const int xj = wv & 3;  // hi rows 0-63, hi 64-127, lo 0-63, lo 64-127
+    srs = xrs;
+    soff = (uint32_t)((xj < 2 ? a.xshi : a.xslo) - a.xhi) +
+           (uint32_t)act_row((xj & 1) * 64 + lane) * (uint32_t)(K / 32);
+    sdst = S::kXS + xj * 256;
+  }
 
   auto issue = [&](int c, int stage) {
     uint8_t *base = smem + stage * S::kBytes;
 #pragma unroll
     for (int j = 0; j < S::kXLoads; ++j)
-      load16_to_lds(xsrc[j] + c * 128, base + S::kX + (j * kWaves + wave) * 1024);
+      buf16_to_lds(xrs, base + S::kX + (j * kSplitWaves + wv) * 1024, xoff[j], c * 128);
 #pragma unroll
     for (int j = 0; j < S::kWLoads; ++j)
-      load16_to_lds(wsrc[j] + c * 64, base + S::kW + (j * kWaves + wave) * 1024);
-    load4_to_lds(wssrc + c * 4, base + S::kWS + wave * 256);
-    load4_to_lds(xssrc + c * 4, base + S::kXS + xj * 256);
+      buf16_to_lds(wrs[j], base + S::kW + (j * kSplitWaves + wv) * 1024, woff[j], c * 64);
+    buf4_to_lds(srs, base + sdst, soff, c * 4);
   };
 
-  // this wave's weight-row blocks: 8 of 16 rows (gate/up: 4 gate blocks, then
-  // the 4 up blocks of the same features)
+  // this wave's weight-row blocks: 4 of 16 rows (gate/up: 2 gate blocks, then
+  // the 2 up blocks of the same features)
   auto wrow_of = [&](int rt) {
-    return NPROJ == 2 ? (rt / 4) * kHalf + wf * 64 + (rt % 4) * 16 : wf * 128 + rt * 16;
+    return NPROJ == 2 ? (rt / 2) * kHalf + wf * 32 + (rt % 2) * 16 : wf * 64 + rt * 16;
   };
 
-  glm_f32x4 acc[8][4];
+  glm_f32x4 acc[4][4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = glm_f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Lane-dependent parts of the LDS operand addresses.  Every block starts at
+  // a multiple of 16 rows, so a lane's swizzle depends on r alone: activation
+  // row 16m + r, piece p sits at (16m + r) * 256 + 16 (p ^ r); weight row
+  // 16m + r, piece q at (16m + r) * 64 + 16 (q ^ ((r >> 1) & 3)).
+  const uint32_t xl_hi0 = r * 256 + 16 * (q ^ r), xl_hi1 = r * 256 + 16 * ((4 + q) ^ r);
+  const uint32_t xl_lo0 = r * 256 + 16 * ((8 + q) ^ r), xl_lo1 = r * 256 + 16 * ((12 + q) ^ r);
+  const uint32_t wl = r * 64 + 16 * (q ^ ((r >> 1) & 3));
+  const uint32_t sl = r * 4;
+
   // MFMAs of one staged chunk: for each activation fragment (hi/lo x 4 token
-  // blocks) 8 MFMAs, one per weight-row block.
+  // blocks) 4 MFMAs, one per weight-row block.
   auto compute = [&](int stage) {
     const uint8_t *base = smem + stage * S::kBytes;
-    glm_i32x8 wa[8];
-    int wsc[8];
+    glm_i32x8 wa[4];
+    int wsc[4];
 #pragma unroll
-    for (int rt = 0; rt < 8; ++rt) {
-      const int wr = wrow_of(rt) + r;
-      const glm_u32x4 v = *reinterpret_cast<const glm_u32x4 *>(base + S::kW + wr * 64 +
-                                                             16 * (q ^ ((wr >> 1) & 3)));
+    for (int rt = 0; rt < 4; ++rt) {
+      const int w16 = wrow_of(rt);  // first row of the block
+      const glm_u32x4 v = *reinterpret_cast<const glm_u32x4 *>(base + S::kW + w16 * 64 + wl);
       wa[rt] = glm_i32x8{(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
-      wsc[rt] = (int)(reinterpret_cast<const uint32_t *>(base + S::kWS)[wr] >> (8 * q));
+      wsc[rt] = (int)(*reinterpret_cast<const uint32_t *>(base + S::kWS + w16 * 4 + sl) >> (8 * q));
     }
 #pragma unroll
     for (int part = 0; part < 2; ++part) {  // hi, then lo
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct) {
-        const int xr = wt * 64 + ct * 16 + r;
-        const uint8_t *xrow = base + S::kX + xr * 256;
+        // token blocks wholly past the tile's rows (the last, partial tile of
+        // an expert) are skipped: their columns are never stored
+        if (wt * 64 + ct * 16 >= rows) continue;
+        const uint8_t *xblk = base + S::kX + (wt * 64 + ct * 16) * 256;
         const glm_u32x4 b0 =
-            *reinterpret_cast<const glm_u32x4 *>(xrow + 16 * ((8 * part + q) ^ (xr & 15)));
+            *reinterpret_cast<const glm_u32x4 *>(xblk + (part ? xl_lo0 : xl_hi0));
         const glm_u32x4 b1 =
-            *reinterpret_cast<const glm_u32x4 *>(xrow + 16 * ((8 * part + 4 + q) ^ (xr & 15)));
+            *reinterpret_cast<const glm_u32x4 *>(xblk + (part ? xl_lo1 : xl_hi1));
         const glm_i32x8 xb = glm_i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3],
                                        (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
-        const int xsc =
-            (int)(reinterpret_cast<const uint32_t *>(base + S::kXS)[part * kTileM + xr] >> (8 * q));
+        const int xsc = (int)(*reinterpret_cast<const uint32_t *>(
+                                  base + S::kXS + (part * kTileM + wt * 64 + ct * 16) * 4 + sl) >>
+                              (8 * q));
 #pragma unroll
-        for (int rt = 0; rt < 8; ++rt)
+        for (int rt = 0; rt < 4; ++rt)
           acc[rt][ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
               wa[rt], xb, acc[rt][ct], 4, 0, 0, wsc[rt], 0, xsc);
+        // one fragment in flight at a time: bounds the live registers
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
@@ -601,21 +655,21 @@ __global__ __launch_bounds__(kThreads) void grouped_f8f4_kernel(SplitArgs a) {
     uint16_t *orow = a.out + (size_t)(pos0 + row) * a.N;
     if constexpr (NPROJ == 2) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 2; ++i) {
         uint32_t o[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m)
           o[m] = f32_to_bf16(limited_swiglu(bf16_round(acc[i][ct][m]),
-                                            bf16_round(acc[4 + i][ct][m]), a.limit));
-        store_rows4(orow + f0 + wf * 64 + i * 16 + 4 * q, o);
+                                            bf16_round(acc[2 + i][ct][m]), a.limit));
+        store_rows4(orow + f0 + wf * 32 + i * 16 + 4 * q, o);
       }
     } else {
 #pragma unroll
-      for (int rt = 0; rt < 8; ++rt) {
+      for (int rt = 0; rt < 4; ++rt) {
         uint32_t o[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) o[m] = f32_to_bf16(acc[rt][ct][m]);
-        store_rows4(orow + f0 + wf * 128 + rt * 16 + 4 * q, o);
+        store_rows4(orow + f0 + wf * 64 + rt * 16 + 4 * q, o);
       }
     }
   }
@@ -681,9 +735,9 @@ static int split_launch(hipStream_t stream, SplitArgs a, int nproj, int max_tile
   const dim3 grid((unsigned)(((max_items + kXcds - 1) / kXcds) * kXcds));
   const size_t lds = kSplitStages * (size_t)SplitStage::kBytes;
   if (nproj == 2)
-    hipLaunchKernelGGL(grouped_f8f4_kernel<2>, grid, dim3(kThreads), lds, stream, a);
+    hipLaunchKernelGGL(grouped_f8f4_kernel<2>, grid, dim3(kSplitThreads), lds, stream, a);
   else
-    hipLaunchKernelGGL(grouped_f8f4_kernel<1>, grid, dim3(kThreads), lds, stream, a);
+    hipLaunchKernelGGL(grouped_f8f4_kernel<1>, grid, dim3(kSplitThreads), lds, stream, a);
   GLM_LAUNCH_CHECK("grouped_f8f4_kernel");
   return GLM_OK;
 }
@@ -691,6 +745,7 @@ static int split_launch(hipStream_t stream, SplitArgs a, int nproj, int max_tile
 static void set_split(SplitArgs &a, const void *split, long long rows, int K) {
   const SplitLayout L(rows, K);
   const uint8_t *base = static_cast<const uint8_t *>(split);
+  a.split_bytes = (uint32_t)L.total;
   a.xhi = base;
   a.xlo = base + L.lo;
   a.xshi = base + L.shi;
