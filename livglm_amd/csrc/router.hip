@@ -52,31 +52,37 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t *__re
 // ---------------------------------------------------------------------------
 // Logits for many tokens on MFMA: v_mfma_f32_16x16x4_f32 forms exact f32
 // products of f32(x) and W and accumulates them in f32 (only the summation
-// order differs from a sequential dot product).  Workgroup = 32 tokens x 64
-// experts; wave (wt, we) owns 16 tokens x 32 experts (two 16 x 16 tiles).
-// MFMA i of a 32-wide K step takes K = k0 + 8q + i in lane (r, q)'s slot, so
-// a lane loads 8 consecutive x (16 B of bf16) and 8 consecutive W (32 B) per
-// step.  Rows past T or E are clamped for the loads and never stored.
+// order differs from a sequential dot product).  Workgroup = 16 tokens x 32
+// experts (two 16 x 16 tiles); its 4 waves split K into quarters, so 4 waves
+// share each SIMD and hide each other's L2 latency, and the quarters' partial
+// sums are added in wave order through LDS.  MFMA i of a 32-wide K step takes
+// K = k0 + 8q + i in lane (r, q)'s slot, so a lane loads 8 consecutive x
+// (16 B of bf16) and 8 consecutive W (32 B) per step.  Rows past T or E are
+// clamped for the loads and never stored.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t *__restrict__ x,
-                                                          const float *__restrict__ w, int T,
-                                                          int d, int E,
-                                                          float *__restrict__ logits) {
+constexpr int kRouterKSplit = 4;
+
+__global__ __launch_bounds__(64 * kRouterKSplit) void router_gemm_kernel(
+    const uint16_t *__restrict__ x, const float *__restrict__ w, int T, int d, int E,
+    float *__restrict__ logits) {
+  __shared__ glm_f32x4 red[kRouterKSplit - 1][2][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int t0 = blockIdx.x * 32 + (wave & 1) * 16;
-  const int e0 = blockIdx.y * 64 + (wave >> 1) * 32;
-  const uint16_t *xr = x + (size_t)min(t0 + r, T - 1) * d + 8 * q;
-  const float *wr0 = w + (size_t)min(e0 + r, E - 1) * d + 8 * q;
-  const float *wr1 = w + (size_t)min(e0 + 16 + r, E - 1) * d + 8 * q;
+  const int t0 = blockIdx.x * 16;
+  const int e0 = blockIdx.y * 32;
+  const int kq = d / kRouterKSplit;  // this wave's K range [wave * kq, (wave + 1) * kq)
+  const int kb = wave * kq;
+  const uint16_t *xr = x + (size_t)min(t0 + r, T - 1) * d + kb + 8 * q;
+  const float *wr0 = w + (size_t)min(e0 + r, E - 1) * d + kb + 8 * q;
+  const float *wr1 = w + (size_t)min(e0 + 16 + r, E - 1) * d + kb + 8 * q;
   glm_f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   glm_u32x4 xv = *reinterpret_cast<const glm_u32x4 *>(xr);
   float4 wa0 = *reinterpret_cast<const float4 *>(wr0), wb0 = *reinterpret_cast<const float4 *>(wr0 + 4);
   float4 wa1 = *reinterpret_cast<const float4 *>(wr1), wb1 = *reinterpret_cast<const float4 *>(wr1 + 4);
-  for (int k0 = 0; k0 < d; k0 += 32) {
+  for (int k0 = 0; k0 < kq; k0 += 32) {
     const glm_u32x4 cx = xv;
     const float4 ca0 = wa0, cb0 = wb0, ca1 = wa1, cb1 = wb1;
-    if (k0 + 32 < d) {  // next step's operands in flight during this step's MFMAs
+    if (k0 + 32 < kq) {  // next step's operands in flight during this step's MFMAs
       xv = *reinterpret_cast<const glm_u32x4 *>(xr + k0 + 32);
       wa0 = *reinterpret_cast<const float4 *>(wr0 + k0 + 32);
       wb0 = *reinterpret_cast<const float4 *>(wr0 + k0 + 36);
@@ -95,7 +101,18 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t *__rest
       acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[i], w1[i], acc1, 0, 0, 0);
     }
   }
-  // lane (r, q) holds tokens 4q..4q+3 of the wave's 16 for experts e0 + r, e0 + 16 + r
+  if (wave > 0) {
+    red[wave - 1][0][lane] = acc0;
+    red[wave - 1][1][lane] = acc1;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int j = 0; j < kRouterKSplit - 1; ++j) {
+    acc0 += red[j][0][lane];
+    acc1 += red[j][1][lane];
+  }
+  // lane (r, q) holds tokens 4q..4q+3 of the 16 for experts e0 + r, e0 + 16 + r
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     const int t = t0 + 4 * q + m;
@@ -230,10 +247,10 @@ int glm_router_launch(hipStream_t stream, const uint16_t *x, int T, int d, const
                       float scale, float *logits, float *weights, uint32_t *indices) {
   using namespace glm;
   if (T == 0) return GLM_OK;
-  if (T >= 64 && d % 32 == 0) {
-    dim3 grid((T + 31) / 32, (E + 63) / 64);
-    hipLaunchKernelGGL(router_gemm_kernel, grid, dim3(256), 0, stream, x, weight, T, d, E,
-                       logits);
+  if (T >= 64 && d % (32 * kRouterKSplit) == 0) {
+    dim3 grid((T + 15) / 16, (E + 31) / 32);
+    hipLaunchKernelGGL(router_gemm_kernel, grid, dim3(64 * kRouterKSplit), 0, stream, x, weight,
+                       T, d, E, logits);
   } else if (T <= 2) {
     dim3 grid((E + 3) / 4, (T + 1) / 2);
     hipLaunchKernelGGL(router_logits_kernel<2>, grid, dim3(256), 0, stream, x, weight, T, d, E,
