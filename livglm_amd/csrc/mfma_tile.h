@@ -153,27 +153,21 @@ __device__ __forceinline__ void load_wave_weights(WaveWeights<FMT, NPROJ, CPW> &
 }
 
 // B fragments of this lane's 32 activations starting at K = kl.
+// Activation fragments of one lane column.  `act` must point at a valid row:
+// a padding column reads any valid row instead of branching (an MFMA output
+// column depends only on its own B column, and padding columns are never
+// stored), so the loads of every lane go out together.
 __device__ __forceinline__ void load_act_frags_at(const uint16_t *act, int kl, glm_bf16x8 xb[4]) {
-  if (act != nullptr) {
-    const glm_bf16x8 *src = reinterpret_cast<const glm_bf16x8 *>(act + kl);
+  const glm_bf16x8 *src = reinterpret_cast<const glm_bf16x8 *>(act + kl);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xb[i] = src[i];
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) xb[i] = glm_bf16x8{};
-  }
+  for (int i = 0; i < 4; ++i) xb[i] = src[i];
 }
 
 __device__ __forceinline__ void load_act_frags(const uint16_t *act, int k0, int q,
                                                glm_bf16x8 xb[4]) {
-  if (act != nullptr) {
-    const glm_bf16x8 *src = reinterpret_cast<const glm_bf16x8 *>(act + k0 + 32 * q);
+  const glm_bf16x8 *src = reinterpret_cast<const glm_bf16x8 *>(act + k0 + 32 * q);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xb[i] = src[i];
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) xb[i] = glm_bf16x8{};
-  }
+  for (int i = 0; i < 4; ++i) xb[i] = src[i];
 }
 
 // MFMAs of preloaded MX weights against one activation row per lane column.
@@ -184,7 +178,7 @@ __device__ __forceinline__ void mma_wave_weights(const WaveWeights<FMT, NPROJ, C
   glm_bf16x8 xb[CPW][4];
 #pragma unroll
   for (int c = 0; c < CPW; ++c)
-    load_act_frags_at(act == nullptr ? nullptr : act + kbase + chunk_k<FMT, CPW>(c, q), 0, xb[c]);
+    load_act_frags_at(act + kbase + chunk_k<FMT, CPW>(c, q), 0, xb[c]);
 #pragma unroll
   for (int c = 0; c < CPW; ++c) {
 #pragma unroll
@@ -208,7 +202,7 @@ __device__ __forceinline__ void mma_wave_weights_lds(const WaveWeights<FMT, NPRO
 #pragma unroll
   for (int c = 0; c < CPW; ++c) {
     glm_bf16x8 xb[4];
-    load_act_frags_at(s_row == nullptr ? nullptr : s_row + kbase + chunk_k<FMT, CPW>(c, q), 0, xb);
+    load_act_frags_at(s_row + kbase + chunk_k<FMT, CPW>(c, q), 0, xb);
 #pragma unroll
     for (int p = 0; p < NPROJ; ++p) {
       glm_bf16x8 a[4];

@@ -31,12 +31,16 @@
 // across blocks inside a kernel, and every reduction runs in one fixed order.
 #include "mfma_tile.h"
 
+int glm_router_select_launch(hipStream_t stream, const float *logits, const float *bias, int T,
+                             int E, int k, int n_group, int topk_group, int norm, float scale,
+                             float *weights, uint32_t *indices);
+
 namespace glm {
 
 constexpr int kRouteThreads = 256;
 constexpr int kMaxFusedPairs = 512;  // T*k handled by the fused route kernel
 constexpr int kFusedMaxE = 448;
-constexpr int kStageTokens = 8;  // activation rows per LDS staging batch
+constexpr int kStageTokens = 16;  // activation rows per LDS staging batch (the MFMA's 16 columns)
 
 struct RouteArgs {
   const uint16_t *x;
@@ -49,6 +53,7 @@ struct RouteArgs {
   uint32_t *indices;
   int32_t *counts, *offsets, *perm, *inv, *pair_token, *active, *num_active, *status;
   int4 *work;
+  int presel;  // select_dispatch_kernel: indices already selected (router_select_kernel)
 };
 
 __device__ __forceinline__ bool better(float v1, int i1, float v2, int i2) {
@@ -300,7 +305,7 @@ __device__ void shared_gate_up_tile(const SharedArgs &a, int b, glm_f32x4 *red) 
     const uint8_t *wrow[2] = {a.sg + (size_t)(row0 + r) * d * 2, a.su + (size_t)(row0 + r) * d * 2};
     for (int p0 = 0; p0 < a.T; p0 += 16) {
       const int t = p0 + r;
-      const uint16_t *act = t < a.T ? a.x + (size_t)t * d : nullptr;
+      const uint16_t *act = a.x + (size_t)min(t, a.T - 1) * d;  // padding: any valid row
       glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
       wave_mma<FMT_BF16, 2, 1>(wrow, srow, kbase, q, act, acc);
       if (ksplit_reduce<2>(acc, red, wave, 4, lane) && t < a.T) {
@@ -315,7 +320,7 @@ __device__ void shared_gate_up_tile(const SharedArgs &a, int b, glm_f32x4 *red) 
     const uint8_t *wrow[2] = {a.sg + (size_t)(row0 + r) * d * 2, a.su + (size_t)(row0 + r) * d * 2};
     for (int p0 = 0; p0 < a.T; p0 += 16) {
       const int t = p0 + r;
-      const uint16_t *act = t < a.T ? a.x + (size_t)t * d : nullptr;
+      const uint16_t *act = a.x + (size_t)min(t, a.T - 1) * d;  // padding: any valid row
       glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
       wave_mma<FMT_BF16, 2, CPW>(wrow, srow, kbase, q, act, acc);
       if (ksplit_reduce<2>(acc, red, wave, 4, lane) && t < a.T) {
@@ -355,8 +360,8 @@ __device__ void shared_down_tile(const SharedArgs &a, int b, uint16_t *s_h) {
   for (int p0 = 0; p0 < a.T; p0 += 16) {
     const int t = p0 + r;
     glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
-    const uint16_t *act = t >= a.T ? nullptr
-                          : (a.skq > 1 ? s_h + (size_t)t * KS : a.hs + (size_t)t * a.Is + kbase);
+    const int tc = min(t, a.T - 1);  // padding columns read a valid row
+    const uint16_t *act = a.skq > 1 ? s_h + (size_t)tc * KS : a.hs + (size_t)tc * a.Is + kbase;
     wave_mma<FMT_BF16, 1, CPW_S>(wrow, srow, 0, q, act, acc);
     if (t < a.T)
       *reinterpret_cast<glm_f32x4 *>(a.yp + ((size_t)kd * a.T + t) * d + row0 + 4 * q) = acc[0];
@@ -386,16 +391,16 @@ __global__ __launch_bounds__(kRouteThreads) void route_logits_kernel(RouteArgs a
       const float4 wv = *reinterpret_cast<const float4 *>(wrow + kk);
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
-        if (t0 + t < T) {
-          const uint2 xv =
-              *reinterpret_cast<const uint2 *>(a.x + (size_t)(t0 + t) * d + wave * kq + kk);
-          float s = acc[t];
-          s = fmaf(bf16_to_f32(xv.x & 0xffffu), wv.x, s);
-          s = fmaf(bf16_to_f32(xv.x >> 16), wv.y, s);
-          s = fmaf(bf16_to_f32(xv.y & 0xffffu), wv.z, s);
-          s = fmaf(bf16_to_f32(xv.y >> 16), wv.w, s);
-          acc[t] = s;
-        }
+        // tokens past T re-read the last row (never stored): branch-free
+        // loads are all in flight at once
+        const int tt = min(t0 + t, T - 1);
+        const uint2 xv = *reinterpret_cast<const uint2 *>(a.x + (size_t)tt * d + wave * kq + kk);
+        float s = acc[t];
+        s = fmaf(bf16_to_f32(xv.x & 0xffffu), wv.x, s);
+        s = fmaf(bf16_to_f32(xv.x >> 16), wv.y, s);
+        s = fmaf(bf16_to_f32(xv.y & 0xffffu), wv.z, s);
+        s = fmaf(bf16_to_f32(xv.y >> 16), wv.w, s);
+        acc[t] = s;
       }
     }
 #pragma unroll
@@ -434,11 +439,16 @@ __global__ __launch_bounds__(kRouteThreads) void select_dispatch_kernel(RouteArg
 
   for (int i = threadIdx.x; i < E; i += kRouteThreads) cnt[i] = 0;
   for (int i = threadIdx.x; i < E * 16; i += kRouteThreads) bits[i] = 0;
-  // top-k per token (wave w: tokens w, w+4, ...)
-  for (int t = wave; t < T; t += 4)
-    select_token<EPL>(a.logits + (size_t)t * E, a.bias, E, k, a.n_group, a.topk_group, a.norm,
-                      a.scale, a.weights + (size_t)t * k, a.indices + (size_t)t * k,
-                      s_idx + t * k, wave_scratch, lane);
+  if (a.presel) {
+    // many tokens: the selection ran one wave per token in its own kernel
+    for (int p = threadIdx.x; p < P; p += kRouteThreads) s_idx[p] = (int)a.indices[p];
+  } else {
+    // top-k per token (wave w: tokens w, w+4, ...)
+    for (int t = wave; t < T; t += 4)
+      select_token<EPL>(a.logits + (size_t)t * E, a.bias, E, k, a.n_group, a.topk_group, a.norm,
+                        a.scale, a.weights + (size_t)t * k, a.indices + (size_t)t * k,
+                        s_idx + t * k, wave_scratch, lane);
+  }
   __syncthreads();
 
   for (int p = threadIdx.x; p < P; p += kRouteThreads) {
@@ -544,17 +554,18 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(GateUpArgs a) {
                             a.uw + e * a.w_stride + (size_t)(row0 + r) * (d / 2)};
   const uint8_t *srow[2] = {a.gs + e * a.s_stride + (size_t)(row0 + r) * (d / 32),
                             a.us + e * a.s_stride + (size_t)(row0 + r) * (d / 32)};
+  // the weight stream first, once for all token batches; the first batch's
+  // staging overlaps with it
+  WaveWeights<FMT_MXFP4, 2, CPW> ww;
+  load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
   for (int p0 = 0; p0 < n; p0 += a.tp) {
     const int rows = min(a.tp, n - p0);
-    // weight stream first; the token staging overlaps with it
-    WaveWeights<FMT_MXFP4, 2, CPW> ww;
-    load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
     if (p0 > 0) __syncthreads();
     stage_rows(s_x, a.x, a.pair_token + base + p0, rows, d);
     __syncthreads();
     glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
     mma_wave_weights_lds<FMT_MXFP4, 2, CPW>(ww, kbase, q,
-                                            r < rows ? s_x + r * lds_row_stride(d) : nullptr, acc);
+                                            s_x + min(r, rows - 1) * lds_row_stride(d), acc);
     if (ksplit_reduce<2>(acc, red, wave, 4, lane) && r < rows) {
       uint32_t o[4];
 #pragma unroll
@@ -592,16 +603,16 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DownArgs a) {
   if (e < 0 || n <= 0) return;
   const uint8_t *wrow[1] = {a.dw + e * a.w_stride + (size_t)(row0 + r) * (a.I / 2)};
   const uint8_t *srow[1] = {a.ds + e * a.s_stride + (size_t)(row0 + r) * (a.I / 32)};
+  WaveWeights<FMT_MXFP4, 1, CPW_R> ww;  // loaded once for all token batches
+  load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
   for (int p0 = 0; p0 < n; p0 += a.tp) {
     const int rows = min(a.tp, n - p0);
-    WaveWeights<FMT_MXFP4, 1, CPW_R> ww;
-    load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
     if (p0 > 0) __syncthreads();
     stage_rows(s_x, a.h + (size_t)(base + p0) * a.I, nullptr, rows, a.I);
     __syncthreads();
     glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
     mma_wave_weights_lds<FMT_MXFP4, 1, CPW_R>(ww, 0, q,
-                                              r < rows ? s_x + r * lds_row_stride(a.I) : nullptr, acc);
+                                              s_x + min(r, rows - 1) * lds_row_stride(a.I), acc);
     if (r < rows) {
       uint32_t o[4];
 #pragma unroll
@@ -701,7 +712,7 @@ __global__ __launch_bounds__(256) void select_gate_up_kernel(PairArgs a, SharedA
   WaveWeights<FMT_MXFP4, 2, CPW> ww;
   load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
   glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
-  mma_wave_weights_lds<FMT_MXFP4, 2, CPW>(ww, kbase, q, r == 0 ? s_x : nullptr, acc);
+  mma_wave_weights_lds<FMT_MXFP4, 2, CPW>(ww, kbase, q, s_x, acc);  // column 0 is stored
   if (ksplit_reduce<2>(acc, red, wave, 4, lane) && r == 0) {
     uint32_t o[4];
 #pragma unroll
@@ -766,8 +777,8 @@ __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
   __syncthreads();
   if (j < k) {
     glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
-    mma_wave_weights_lds<FMT_MXFP4, 1, CPW_R>(ww, 0, q, r == 0 ? s_h + j * lds_row_stride(I) : nullptr,
-                                              acc);
+    mma_wave_weights_lds<FMT_MXFP4, 1, CPW_R>(ww, 0, q, s_h + j * lds_row_stride(I),
+                                              acc);  // column 0 is stored
     if (r == 0) {
 #pragma unroll
       for (int m = 0; m < 4; ++m) s_p[j][4 * q + m] = bf16_round(acc[0][m]) * wj;
@@ -858,10 +869,15 @@ static int launch_route_logits(hipStream_t stream, const RouteArgs &a, const Sha
     case 6: hipLaunchKernelGGL((route_logits_kernel<TT, 6>), g1, dim3(kRouteThreads), 0, stream, a, sh); break; \
     default: hipLaunchKernelGGL((route_logits_kernel<TT, 8>), g1, dim3(kRouteThreads), 0, stream, a, sh); break; \
   }
+  // tokens per pass over the expert's router row
   if (a.T <= 2) {
     GLM_LOGITS(2)
-  } else {
+  } else if (a.T <= 8) {
     GLM_LOGITS(8)
+  } else if (a.T <= 16) {
+    GLM_LOGITS(16)
+  } else {
+    GLM_LOGITS(32)
   }
 #undef GLM_LOGITS
   GLM_LAUNCH_CHECK("route_logits_kernel");
@@ -878,10 +894,17 @@ int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d,
                             float *gp, float *up, uint16_t *hs, float *yp, float limit) {
   RouteArgs a{x,      w,      bias,   T,   d,          E,      k,          n_group,
               topk_group, norm, scale, logits, weights, indices, counts, offsets,
-              perm,   inv,    pair_token, active, num_active, status, work};
+              perm,   inv,    pair_token, active, num_active, status, work, 0};
   const SharedArgs sh = make_shared_args(x, T, d, sg, su, sd, Is, gp, up, hs, yp, limit);
   int rc = launch_route_logits(stream, a, sh);
   if (rc) return rc;
+  // beyond a few tokens per wave the selection runs one wave per token first
+  if (T > 8) {
+    rc = glm_router_select_launch(stream, logits, bias, T, E, k, n_group, topk_group, norm, scale,
+                                  weights, indices);
+    if (rc) return rc;
+    a.presel = 1;
+  }
   const int epl = (E + 63) / 64;
   const int e8 = epl <= 1 ? 1 : (epl <= 2 ? 2 : (epl <= 4 ? 4 : 8));
   const int cs = sg ? glm_decode_shared_cpws(Is) : 1;

@@ -242,6 +242,26 @@ __global__ __launch_bounds__(64) void router_select_kernel(
 }  // namespace glm
 
 // Launches the router; `logits` must be a valid [T][E] buffer here.
+// Top-k selection of precomputed logits, one wave per token.
+int glm_router_select_launch(hipStream_t stream, const float *logits, const float *bias, int T,
+                             int E, int k, int n_group, int topk_group, int norm, float scale,
+                             float *weights, uint32_t *indices) {
+  using namespace glm;
+  if (T == 0) return GLM_OK;
+  const int epl = (E + 63) / 64;
+#define GLM_SELECT(N)                                                                         \
+  hipLaunchKernelGGL(router_select_kernel<N>, dim3(T), dim3(64), 0, stream, logits, bias, T, \
+                     E, k, n_group, topk_group, norm, scale, weights, indices)
+  if (epl <= 1) GLM_SELECT(1);
+  else if (epl <= 2) GLM_SELECT(2);
+  else if (epl <= 4) GLM_SELECT(4);
+  else if (epl <= 8) GLM_SELECT(8);
+  else GLM_SELECT(16);
+#undef GLM_SELECT
+  GLM_LAUNCH_CHECK("router_select_kernel");
+  return GLM_OK;
+}
+
 int glm_router_launch(hipStream_t stream, const uint16_t *x, int T, int d, const float *weight,
                       const float *bias, int E, int k, int n_group, int topk_group, int norm,
                       float scale, float *logits, float *weights, uint32_t *indices) {
@@ -261,18 +281,8 @@ int glm_router_launch(hipStream_t stream, const uint16_t *x, int T, int d, const
                        logits);
   }
   GLM_LAUNCH_CHECK("router_logits_kernel");
-  const int epl = (E + 63) / 64;
-#define GLM_SELECT(N)                                                                         \
-  hipLaunchKernelGGL(router_select_kernel<N>, dim3(T), dim3(64), 0, stream, logits, bias, T, \
-                     E, k, n_group, topk_group, norm, scale, weights, indices)
-  if (epl <= 1) GLM_SELECT(1);
-  else if (epl <= 2) GLM_SELECT(2);
-  else if (epl <= 4) GLM_SELECT(4);
-  else if (epl <= 8) GLM_SELECT(8);
-  else GLM_SELECT(16);
-#undef GLM_SELECT
-  GLM_LAUNCH_CHECK("router_select_kernel");
-  return GLM_OK;
+  return glm_router_select_launch(stream, logits, bias, T, E, k, n_group, topk_group, norm, scale,
+                                  weights, indices);
 }
 
 int glm_router_validate(const void *x, int T, int d, const void *weight, const void *bias, int E,
