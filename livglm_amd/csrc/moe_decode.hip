@@ -34,13 +34,15 @@
 int glm_router_select_launch(hipStream_t stream, const float *logits, const float *bias, int T,
                              int E, int k, int n_group, int topk_group, int norm, float scale,
                              float *weights, uint32_t *indices);
+int glm_router_logits_launch(hipStream_t stream, const uint16_t *x, int T, int d,
+                             const float *weight, int E, float *logits);
+bool glm_router_gemm_supported(int T, int d);
 
 namespace glm {
 
 constexpr int kRouteThreads = 256;
 constexpr int kMaxFusedPairs = 512;  // T*k handled by the fused route kernel
 constexpr int kFusedMaxE = 448;
-constexpr int kStageTokens = 16;  // activation rows per LDS staging batch (the MFMA's 16 columns)
 
 struct RouteArgs {
   const uint16_t *x;
@@ -54,6 +56,7 @@ struct RouteArgs {
   int32_t *counts, *offsets, *perm, *inv, *pair_token, *active, *num_active, *status;
   int4 *work;
   int presel;  // select_dispatch_kernel: indices already selected (router_select_kernel)
+  int logits_done;  // route_logits_kernel: logits already computed; run the shared blocks only
 };
 
 __device__ __forceinline__ bool better(float v1, int i1, float v2, int i2) {
@@ -315,10 +318,12 @@ __device__ void shared_gate_up_tile(const SharedArgs &a, int b, glm_f32x4 *red) 
       }
     }
   } else {
-    const int row0 = b * 16;
+    // full-K tiles, one block per (16-row tile, group of 16 tokens)
+    const int tiles = a.Is / 16;
+    const int row0 = (b % tiles) * 16;
     const int kbase = wave * CPW * 128;
     const uint8_t *wrow[2] = {a.sg + (size_t)(row0 + r) * d * 2, a.su + (size_t)(row0 + r) * d * 2};
-    for (int p0 = 0; p0 < a.T; p0 += 16) {
+    for (int p0 = (b / tiles) * 16; p0 < min(a.T, (b / tiles) * 16 + 16); p0 += 16) {
       const int t = p0 + r;
       const uint16_t *act = a.x + (size_t)min(t, a.T - 1) * d;  // padding: any valid row
       glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
@@ -340,6 +345,11 @@ __device__ void shared_down_tile(const SharedArgs &a, int b, uint16_t *s_h) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int d = a.d;
+  // with full-K gate/up tiles (skq == 1) the blocks also split the tokens
+  // into groups of 16
+  const int per_group = (d / 64) * a.skd;
+  const int tgroup = a.skq > 1 ? 0 : b / per_group;
+  b = a.skq > 1 ? b : b % per_group;
   const int tile = b / a.skd, kd = b % a.skd;
   const int row0 = tile * 64 + wave * 16;
   const int kbase = kd * KS;
@@ -357,7 +367,8 @@ __device__ void shared_down_tile(const SharedArgs &a, int b, uint16_t *s_h) {
   }
   const uint8_t *wrow[1] = {a.sd + ((size_t)(row0 + r) * a.Is + kbase) * 2};
   const uint8_t *srow[1] = {nullptr};
-  for (int p0 = 0; p0 < a.T; p0 += 16) {
+  const int p_end = a.skq > 1 ? a.T : min(a.T, tgroup * 16 + 16);
+  for (int p0 = tgroup * 16; p0 < p_end; p0 += 16) {
     const int t = p0 + r;
     glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
     const int tc = min(t, a.T - 1);  // padding columns read a valid row
@@ -375,7 +386,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_logits_kernel(RouteArgs a
   __shared__ float s_part[4][TT];
   __shared__ glm_f32x4 red[3 * 2 * 64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int e = blockIdx.x;
+  const int e = blockIdx.x + (a.logits_done ? a.E : 0);
   const int T = a.T, d = a.d, E = a.E;
   if (e >= E) {
     shared_gate_up_tile<CPW>(sh, e - E, red);
@@ -531,15 +542,14 @@ struct GateUpArgs {
   int I, d;
   uint16_t *h;  // [P][I]
   float limit;
-  int tp;  // token rows staged in LDS per batch
 };
 
 // Routed gate/up: block b = (work slot b / (I/16), 16-row tile); 4 waves split
-// d.  The expert's token rows are staged in LDS, `tp` at a time (weights are
-// re-read from L2 for each further batch of tp tokens).
+// d.  The weights are loaded once; the expert's tokens go through in batches
+// of 16 (the MFMA's columns), each lane column reading its token's row from
+// global memory.
 template <int CPW>
 __global__ __launch_bounds__(256) void decode_gate_up_kernel(GateUpArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t s_x[];  // [tp][lds_row_stride(d)]
   __shared__ glm_f32x4 red[3 * 2 * 64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
@@ -554,18 +564,16 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(GateUpArgs a) {
                             a.uw + e * a.w_stride + (size_t)(row0 + r) * (d / 2)};
   const uint8_t *srow[2] = {a.gs + e * a.s_stride + (size_t)(row0 + r) * (d / 32),
                             a.us + e * a.s_stride + (size_t)(row0 + r) * (d / 32)};
-  // the weight stream first, once for all token batches; the first batch's
-  // staging overlaps with it
+  // the weight stream once for all token batches; lane column r reads its
+  // token's row straight from global memory (L2-resident), in flight with
+  // the weights
   WaveWeights<FMT_MXFP4, 2, CPW> ww;
   load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
-  for (int p0 = 0; p0 < n; p0 += a.tp) {
-    const int rows = min(a.tp, n - p0);
-    if (p0 > 0) __syncthreads();
-    stage_rows(s_x, a.x, a.pair_token + base + p0, rows, d);
-    __syncthreads();
+  for (int p0 = 0; p0 < n; p0 += 16) {
+    const int rows = min(16, n - p0);
+    const uint16_t *act = a.x + (size_t)a.pair_token[base + p0 + min(r, rows - 1)] * d;
     glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
-    mma_wave_weights_lds<FMT_MXFP4, 2, CPW>(ww, kbase, q,
-                                            s_x + min(r, rows - 1) * lds_row_stride(d), acc);
+    mma_wave_weights<FMT_MXFP4, 2, CPW>(ww, kbase, q, act, acc);
     if (ksplit_reduce<2>(acc, red, wave, 4, lane) && r < rows) {
       uint32_t o[4];
 #pragma unroll
@@ -576,6 +584,8 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(GateUpArgs a) {
   }
 }
 
+constexpr int kDownStageRows = 16;  // h rows per LDS batch (the MFMA's 16 columns)
+
 struct DownArgs {
   const uint16_t *h;
   const int4 *work;
@@ -584,15 +594,15 @@ struct DownArgs {
   long long w_stride, s_stride;
   int I, d;
   uint16_t *y;  // [P][d]
-  int tp;  // h rows staged in LDS per batch
 };
 
 // Routed down: block b = (work slot b / (d/64), 64-row tile); each wave owns
-// 16 output rows over the full K = I.  The slot's h rows are staged in LDS,
-// `tp` at a time.
+// 16 output rows over the full K = I.  The weights are loaded once; the
+// slot's h rows go through in batches of 16, staged in LDS (all four waves
+// read every row).
 template <int CPW_R>
 __global__ __launch_bounds__(256) void decode_down_kernel(DownArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t s_x[];  // [tp][lds_row_stride(I)]
+  extern __shared__ __attribute__((aligned(16))) uint16_t s_x[];  // [16][lds_row_stride(I)]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int d = a.d;
@@ -605,8 +615,8 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DownArgs a) {
   const uint8_t *srow[1] = {a.ds + e * a.s_stride + (size_t)(row0 + r) * (a.I / 32)};
   WaveWeights<FMT_MXFP4, 1, CPW_R> ww;  // loaded once for all token batches
   load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
-  for (int p0 = 0; p0 < n; p0 += a.tp) {
-    const int rows = min(a.tp, n - p0);
+  for (int p0 = 0; p0 < n; p0 += kDownStageRows) {
+    const int rows = min(kDownStageRows, n - p0);
     if (p0 > 0) __syncthreads();
     stage_rows(s_x, a.h + (size_t)(base + p0) * a.I, nullptr, rows, a.I);
     __syncthreads();
@@ -848,8 +858,10 @@ static SharedArgs make_shared_args(const uint16_t *x, int T, int d, const uint16
   sh.Is = sg ? Is : 0;
   sh.skq = glm_decode_shared_skq(T, d);
   sh.skd = sg ? glm_decode_shared_skd(Is) : 1;
-  sh.gu_blocks = sg ? (Is / 16) * sh.skq : 0;
-  sh.dn_blocks = sg ? (d / 64) * sh.skd : 0;
+  // full-K tiles (skq == 1) split the tokens into groups of 16 across blocks
+  const int tgroups = sh.skq > 1 ? 1 : (T + 15) / 16;
+  sh.gu_blocks = sg ? (Is / 16) * sh.skq * tgroups : 0;
+  sh.dn_blocks = sg ? (d / 64) * sh.skd * tgroups : 0;
   sh.gp = gp;
   sh.up = up;
   sh.hs = hs;
@@ -861,7 +873,8 @@ static SharedArgs make_shared_args(const uint16_t *x, int T, int d, const uint16
 // Router logits for every token, plus the shared expert's gate/up tiles.
 static int launch_route_logits(hipStream_t stream, const RouteArgs &a, const SharedArgs &sh) {
   const int cpw = a.d / 512;
-  const dim3 g1(a.E + sh.gu_blocks);
+  const dim3 g1((a.logits_done ? 0 : a.E) + sh.gu_blocks);
+  if (g1.x == 0) return GLM_OK;
 #define GLM_LOGITS(TT)                                                                          \
   switch (cpw) {                                                                                \
     case 2: hipLaunchKernelGGL((route_logits_kernel<TT, 2>), g1, dim3(kRouteThreads), 0, stream, a, sh); break; \
@@ -894,9 +907,15 @@ int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d,
                             float *gp, float *up, uint16_t *hs, float *yp, float limit) {
   RouteArgs a{x,      w,      bias,   T,   d,          E,      k,          n_group,
               topk_group, norm, scale, logits, weights, indices, counts, offsets,
-              perm,   inv,    pair_token, active, num_active, status, work, 0};
+              perm,   inv,    pair_token, active, num_active, status, work, 0, 0};
   const SharedArgs sh = make_shared_args(x, T, d, sg, su, sd, Is, gp, up, hs, yp, limit);
-  int rc = launch_route_logits(stream, a, sh);
+  int rc;
+  if (glm_router_gemm_supported(T, d)) {  // many tokens: the logits on MFMA in their own kernel
+    rc = glm_router_logits_launch(stream, x, T, d, w, E, logits);
+    if (rc) return rc;
+    a.logits_done = 1;
+  }
+  rc = launch_route_logits(stream, a, sh);
   if (rc) return rc;
   // beyond a few tokens per wave the selection runs one wave per token first
   if (T > 8) {
@@ -943,8 +962,7 @@ int glm_decode_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int 
   a.d = d;
   a.h = h;
   a.limit = glm_limit_bf16(limit);
-  a.tp = std::min(T, kStageTokens);
-  const size_t lds = (size_t)a.tp * lds_row_stride(d) * 2;
+  const size_t lds = 0;
   const int blocks = a.slots * (I / 16);
   switch (d / 512) {
     case 2: hipLaunchKernelGGL(decode_gate_up_kernel<2>, dim3(blocks), dim3(256), lds, stream, a); break;
@@ -971,8 +989,7 @@ int glm_decode_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, 
   a.I = I;
   a.d = d;
   a.y = y;
-  a.tp = std::min(T * k, kStageTokens);
-  const size_t lds = (size_t)a.tp * lds_row_stride(I) * 2;
+  const size_t lds = (size_t)std::min(T * k, kDownStageRows) * lds_row_stride(I) * 2;
   const int blocks = a.slots * (d / 64);
   switch (I / 128) {
     case 1: hipLaunchKernelGGL(decode_down_kernel<1>, dim3(blocks), dim3(256), lds, stream, a); break;

@@ -53,24 +53,24 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t *__re
 // Logits for many tokens on MFMA: v_mfma_f32_16x16x4_f32 forms exact f32
 // products of f32(x) and W and accumulates them in f32 (only the summation
 // order differs from a sequential dot product).  Workgroup = 16 tokens x 32
-// experts (two 16 x 16 tiles); its 4 waves split K into quarters, so 4 waves
-// share each SIMD and hide each other's L2 latency, and the quarters' partial
+// experts (two 16 x 16 tiles); its KSPLIT waves split K into equal ranges
+// (4 for many tokens, 16 for fewer, where the grid is small), so several
+// waves share each SIMD and hide each other's L2 latency, and the partial
 // sums are added in wave order through LDS.  MFMA i of a 32-wide K step takes
 // K = k0 + 8q + i in lane (r, q)'s slot, so a lane loads 8 consecutive x
 // (16 B of bf16) and 8 consecutive W (32 B) per step.  Rows past T or E are
 // clamped for the loads and never stored.
 // ---------------------------------------------------------------------------
-constexpr int kRouterKSplit = 4;
-
-__global__ __launch_bounds__(64 * kRouterKSplit) void router_gemm_kernel(
+template <int KSPLIT>
+__global__ __launch_bounds__(64 * KSPLIT) void router_gemm_kernel(
     const uint16_t *__restrict__ x, const float *__restrict__ w, int T, int d, int E,
     float *__restrict__ logits) {
-  __shared__ glm_f32x4 red[kRouterKSplit - 1][2][64];
+  __shared__ glm_f32x4 red[KSPLIT - 1][2][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int t0 = blockIdx.x * 16;
   const int e0 = blockIdx.y * 32;
-  const int kq = d / kRouterKSplit;  // this wave's K range [wave * kq, (wave + 1) * kq)
+  const int kq = d / KSPLIT;  // this wave's K range [wave * kq, (wave + 1) * kq)
   const int kb = wave * kq;
   const uint16_t *xr = x + (size_t)min(t0 + r, T - 1) * d + kb + 8 * q;
   const float *wr0 = w + (size_t)min(e0 + r, E - 1) * d + kb + 8 * q;
@@ -108,7 +108,7 @@ __global__ __launch_bounds__(64 * kRouterKSplit) void router_gemm_kernel(
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
-  for (int j = 0; j < kRouterKSplit - 1; ++j) {
+  for (int j = 0; j < KSPLIT - 1; ++j) {
     acc0 += red[j][0][lane];
     acc1 += red[j][1][lane];
   }
@@ -242,6 +242,29 @@ __global__ __launch_bounds__(64) void router_select_kernel(
 }  // namespace glm
 
 // Launches the router; `logits` must be a valid [T][E] buffer here.
+// Router logits only (no selection): the MFMA kernel for 16 or more tokens.
+bool glm_router_gemm_supported(int T, int d) {
+  return (T >= 256 && d % (32 * 4) == 0) || (T >= 16 && d % (32 * 16) == 0);
+}
+
+int glm_router_logits_launch(hipStream_t stream, const uint16_t *x, int T, int d,
+                             const float *weight, int E, float *logits) {
+  using namespace glm;
+  if (!glm_router_gemm_supported(T, d)) {
+    glm::set_error("router logits: unsupported T=%d d=%d", T, d);
+    return GLM_ERR_UNSUPPORTED_SHAPE;
+  }
+  dim3 grid((T + 15) / 16, (E + 31) / 32);
+  if (T >= 256 && d % (32 * 4) == 0)
+    hipLaunchKernelGGL(router_gemm_kernel<4>, grid, dim3(256), 0, stream, x, weight, T, d, E,
+                       logits);
+  else
+    hipLaunchKernelGGL(router_gemm_kernel<16>, grid, dim3(1024), 0, stream, x, weight, T, d, E,
+                       logits);
+  GLM_LAUNCH_CHECK("router_gemm_kernel");
+  return GLM_OK;
+}
+
 // Top-k selection of precomputed logits, one wave per token.
 int glm_router_select_launch(hipStream_t stream, const float *logits, const float *bias, int T,
                              int E, int k, int n_group, int topk_group, int norm, float scale,
@@ -267,10 +290,9 @@ int glm_router_launch(hipStream_t stream, const uint16_t *x, int T, int d, const
                       float scale, float *logits, float *weights, uint32_t *indices) {
   using namespace glm;
   if (T == 0) return GLM_OK;
-  if (T >= 64 && d % (32 * kRouterKSplit) == 0) {
-    dim3 grid((T + 15) / 16, (E + 31) / 32);
-    hipLaunchKernelGGL(router_gemm_kernel, grid, dim3(64 * kRouterKSplit), 0, stream, x, weight,
-                       T, d, E, logits);
+  if (glm_router_gemm_supported(T, d)) {
+    const int rc = glm_router_logits_launch(stream, x, T, d, weight, E, logits);
+    if (rc) return rc;
   } else if (T <= 2) {
     dim3 grid((E + 3) / 4, (T + 1) / 2);
     hipLaunchKernelGGL(router_logits_kernel<2>, grid, dim3(256), 0, stream, x, weight, T, d, E,
