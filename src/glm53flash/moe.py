@@ -124,6 +124,10 @@ class ExpertSSDMoE:
         out = torch.empty((T, d), dtype=torch.float32, device=dev)
         weights = torch.empty((T, k), dtype=torch.float32, device=dev)
         indices = torch.empty((T, k), dtype=torch.int32, device=dev)
+        if T == 0:  # an empty batch: empty results, nothing to launch
+            self.last_weights = weights
+            self.last_indices = indices
+            return out.reshape(original_shape)
         ws = self._workspace_for(T, dev)
         gw, gs = bank.projection("gate_proj")
         uw, us = bank.projection("up_proj")

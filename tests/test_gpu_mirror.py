@@ -172,3 +172,14 @@ def test_dense_mlp_and_swiglu_wrappers(gu):
     want_h = O.f32_to_bf16_bits(O.limited_swiglu_bf16(O.bf16_bits_to_f32(g),
                                                       O.bf16_bits_to_f32(u), 10.0))
     assert np.array_equal(h, want_h)
+
+
+def test_expert_ssd_moe_empty_batch(gu):
+    # an empty token batch returns an empty f32 result of the input's shape
+    import torch
+    shape = SHAPES["verify_t2"]
+    moe, dl = _moe(gu, shape, make_layer(shape, 7400))
+    x = torch.empty((1, 0, shape.d), dtype=torch.bfloat16, device="cuda")
+    out = moe(x)
+    assert out.dtype == torch.float32 and tuple(out.shape) == (1, 0, shape.d)
+    assert moe.last_route == ()

@@ -540,6 +540,10 @@ SMALL_LAYERS = [
     (200, 2048, 64, 8, 768, 0, (4, 2)),
     # many pairs: the multi-workgroup dispatch (6 chunks of 1024 pairs, the last partial)
     (700, 1024, 32, 8, 256, 0, (1, 1)),
+    # the decode path beyond 16 tokens (MFMA router, per-token selection, token groups)
+    (40, 1024, 64, 8, 512, 512, (1, 1)),
+    # k = 64, every expert of E = 64 chosen by every token (the top-k upper bound)
+    (3, 256, 64, 64, 64, 64, (1, 1)),
 ]
 
 

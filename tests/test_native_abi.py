@@ -96,3 +96,60 @@ def test_moe_forward_rejects_small_workspace(lib):
              1024, fake, None, None]
     msg = _expect(native.GLM_ERR_WORKSPACE, "glm_moe_forward", *args)
     assert "workspace" in msg
+
+
+def _forward_args(T, d=2048, E=128, k=8, I=768, *, workspace_bytes=None, shared_fmt=None,
+                  shared_scales=False, ptr=None):
+    fake = ptr or ctypes.c_void_p(0x1000)  # never dereferenced: the call returns before launching
+    lib = native.load()
+    if workspace_bytes is None:
+        workspace_bytes = lib.glm_moe_workspace_bytes(max(T, 0), d, E, k, I, 768)
+    fmt = native.GLM_FMT_BF16 if shared_fmt is None else shared_fmt
+    sc = fake if shared_scales else None
+    args = [None, fake, T, d, fake, fake, E, k, 1, 1, 1, 2.5, I] + [fake] * 6
+    args += [768, fmt, fake, sc, fake, sc, fake, sc, None, 10.0, fake, workspace_bytes, fake,
+             None, None]
+    return args
+
+
+def test_empty_batch_is_a_no_op(lib):
+    # T = 0 validates and returns without touching the device
+    assert lib.glm_moe_forward(*_forward_args(0)) == native.GLM_OK
+    fake = ctypes.c_void_p(0x1000)
+    assert lib.glm_router_topk(None, fake, 0, 2048, fake, fake, 128, 8, 1, 1, 1, 2.5, fake, fake,
+                               fake) == native.GLM_OK
+    assert lib.glm_act_split_fp8(None, fake, 0, 2048, fake) == native.GLM_OK
+
+
+def test_moe_forward_rejects_bad_arguments(lib):
+    cases = [
+        (native.GLM_ERR_INVALID_ARGUMENT, _forward_args(-1), "invalid sizes"),
+        (native.GLM_ERR_UNSUPPORTED_SHAPE, _forward_args(2, d=1000), "multiples of 32"),
+        (native.GLM_ERR_UNSUPPORTED_SHAPE, _forward_args(2, E=449, k=8), "exceeds 448"),
+        (native.GLM_ERR_INVALID_ARGUMENT, _forward_args(2, E=4, k=8), None),
+        (native.GLM_ERR_INVALID_ARGUMENT, _forward_args(2, shared_fmt=7), "shared format"),
+        (native.GLM_ERR_INVALID_ARGUMENT, _forward_args(2, shared_fmt=native.GLM_FMT_MXFP8),
+         "scales"),
+        (native.GLM_ERR_INVALID_ARGUMENT, _forward_args(2, ptr=ctypes.c_void_p(0x1004)),
+         "aligned"),
+    ]
+    for code, args, text in cases:
+        msg = _expect(code, "glm_moe_forward", *args)
+        if text:
+            assert text in msg, msg
+
+
+def test_prefill_entry_points_reject_bad_shapes(lib):
+    fake = ctypes.c_void_p(0x1000)
+    assert lib.glm_act_split_bytes(4, 33) == 0 and lib.glm_act_split_bytes(-1, 64) == 0
+    assert lib.glm_act_split_bytes(4, 64) % 256 == 0
+    _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_act_split_fp8", None, fake, 4, 48, fake)
+    _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_act_split_fp8", None, None, 4, 64, fake)
+    msg = _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_expert_gate_up_grouped", None, fake, 8,
+                  1024, 384, fake, fake, fake, fake, fake, fake, fake, 16, 10.0, fake)
+    assert "I % 256" in msg
+    _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_expert_down_grouped", None, fake, 64, 256,
+            768, fake, fake, fake, fake, 16, fake)
+    # the token-major gate/up takes at most 4 tokens and 8 experts per token
+    _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_route_gate_up", None, fake, fake, 5, 128, 8, 1,
+            1, 1, 2.5, fake, 2048, 768, fake, fake, fake, fake, 10.0, fake, fake, fake)
