@@ -571,6 +571,14 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(GateUpArgs a) {
   load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
   for (int p0 = 0; p0 < n; p0 += 16) {
     const int rows = min(16, n - p0);
+    // Opaque to the compiler per batch: the weights' conversion stays inside
+    // the loop, after this batch's activation loads are issued, instead of
+    // being hoisted in front of it (that would pin 128 registers of
+    // converted weights and serialise the activation loads).
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int c = 0; c < CPW; ++c) asm volatile("" : "+v"(ww.w[p][c].c));
     const uint16_t *act = a.x + (size_t)a.pair_token[base + p0 + min(r, rows - 1)] * d;
     glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
     mma_wave_weights<FMT_MXFP4, 2, CPW>(ww, kbase, q, act, acc);
