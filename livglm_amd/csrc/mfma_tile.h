@@ -150,6 +150,10 @@ __device__ __forceinline__ void load_wave_weights(WaveWeights<FMT, NPROJ, CPW> &
 #pragma unroll
     for (int p = 0; p < NPROJ; ++p)
       ww.w[p][c] = load_chunk_at<FMT>(wrow[p], kbase + chunk_k<FMT, CPW>(c, q));
+  // every load above is issued before anything that follows: the scheduler
+  // would otherwise sink some of them behind the first MFMAs, which costs a
+  // second memory round trip
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // B fragments of this lane's 32 activations starting at K = kl.
