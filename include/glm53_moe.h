@@ -205,6 +205,16 @@ int glm_linear(void *stream, const uint16_t *x, int T, int in_dims, const void *
                const uint8_t *scales, int fmt, int out_dims, uint16_t *y);
 
 /*
+ * glm_linear on an f32 input: every x value is rounded to bf16 (RNE) as it
+ * is read, so the result equals glm_linear of the bf16 cast of x -- the cast
+ * the decoder applies to its f32 residual before the native path
+ * (native_expert_ssd.py:655-658), fused into the linear.
+ * x f32 [T][in].  Limits: T <= 4, in % 32 == 0, out % 8 == 0.
+ */
+int glm_linear_f32(void *stream, const float *x, int T, int in_dims, const void *weight,
+                   const uint8_t *scales, int fmt, int out_dims, uint16_t *y);
+
+/*
  * Dense SwiGLU MLP (the shared expert).  Replaces DenseMLP.__call__
  * (layers.py:160-171): out = down(limited_swiglu(gate(x), up(x))).
  * All three weights share `fmt`.  h is caller scratch bf16 [T][I].

@@ -274,6 +274,142 @@ __global__ __launch_bounds__(512) void mx_gemv_kernel(const GemvArgs args) {
 }
 
 // ---------------------------------------------------------------------------
+// Few-token linear on the vector ALUs (T <= 4).  With one to four token rows
+// an MFMA tile computes 16 columns for each one kept, and its 16-row tiles
+// would leave half of the CUs idle at N = 2048, so each wave owns two output
+// rows here and a block of four waves eight: lane l takes the 32-wide K
+// slices l, l + 64, ... of both rows (one 32-byte load per row for MXFP8),
+// converts them to bf16 (exact) and forms packed bf16 dot products with each
+// token's slice; the 64 lane partials are added in a fixed butterfly order.
+// XF32: x is f32 and every value is rounded to bf16 (RNE) as it is read.
+// ---------------------------------------------------------------------------
+constexpr int kRowsPerWave = 2;
+constexpr int kLinearMaxT = 4;
+
+struct LinearRowsArgs {
+  const void *x;
+  int T, K, N;
+  const uint8_t *w, *s;
+  uint16_t *y;
+};
+
+__device__ __forceinline__ glm_bf16x2 bf16_pair(const glm_bf16x8 &v, int p) {
+  glm_bf16x2 r;
+  r[0] = v[2 * p];
+  r[1] = v[2 * p + 1];
+  return r;
+}
+
+__device__ __forceinline__ glm_u32x4 nt_load16(const uint8_t *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const glm_u32x4 *>(p));
+}
+
+// One lane's 32-wide K slice of one weight row, as loaded.
+template <int FMT>
+struct RowSlice {
+  glm_u32x4 c[FMT == FMT_MXFP8 ? 2 : (FMT == FMT_MXFP4 ? 1 : 4)];
+  uint32_t s;
+};
+
+template <int FMT>
+__device__ __forceinline__ RowSlice<FMT> load_slice(const uint8_t *wrow, const uint8_t *srow, int sl) {
+  RowSlice<FMT> r;
+  constexpr int n = FMT == FMT_MXFP8 ? 2 : (FMT == FMT_MXFP4 ? 1 : 4);
+#pragma unroll
+  for (int i = 0; i < n; ++i) r.c[i] = nt_load16(wrow + (size_t)sl * 16 * n + 16 * i);
+  r.s = FMT == FMT_BF16 ? 0u : srow[sl];
+  return r;
+}
+
+template <int FMT>
+__device__ __forceinline__ void slice_bf16(const RowSlice<FMT> &r, glm_bf16x8 out[4]) {
+  if constexpr (FMT == FMT_MXFP8) {
+    const float sc = e8m0_to_f32(r.s);
+    out[0] = mxfp8_words_to_bf16x8(r.c[0][0], r.c[0][1], sc);
+    out[1] = mxfp8_words_to_bf16x8(r.c[0][2], r.c[0][3], sc);
+    out[2] = mxfp8_words_to_bf16x8(r.c[1][0], r.c[1][1], sc);
+    out[3] = mxfp8_words_to_bf16x8(r.c[1][2], r.c[1][3], sc);
+  } else if constexpr (FMT == FMT_MXFP4) {
+    const float sc = e8m0_to_f32(r.s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = mxfp4_word_to_bf16x8(r.c[0][i], sc);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = __builtin_bit_cast(glm_bf16x8, r.c[i]);
+  }
+}
+
+template <bool XF32>
+__device__ __forceinline__ void slice_act(const void *x, size_t off, glm_bf16x8 out[4]) {
+  if constexpr (XF32) {
+    const glm_f32x4 *p = reinterpret_cast<const glm_f32x4 *>(static_cast<const float *>(x) + off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const glm_f32x4 a = p[2 * i], b = p[2 * i + 1];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        out[i][m] = (__bf16)a[m];
+        out[i][4 + m] = (__bf16)b[m];
+      }
+    }
+  } else {
+    const glm_bf16x8 *p = reinterpret_cast<const glm_bf16x8 *>(static_cast<const uint16_t *>(x) + off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = p[i];
+  }
+}
+
+template <int FMT, bool XF32>
+__global__ __launch_bounds__(256) void linear_rows_kernel(const LinearRowsArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kRowsPerWave;
+  const int K = a.K, rb = row_bytes(FMT, K);
+  float acc[kRowsPerWave][kLinearMaxT];
+#pragma unroll
+  for (int rr = 0; rr < kRowsPerWave; ++rr)
+#pragma unroll
+    for (int t = 0; t < kLinearMaxT; ++t) acc[rr][t] = 0.0f;
+  for (int sl = lane; sl < K / 32; sl += 64) {
+    // the weight slices and token 0's slice go out together, before any wait
+    RowSlice<FMT> raw[kRowsPerWave];
+#pragma unroll
+    for (int rr = 0; rr < kRowsPerWave; ++rr)
+      raw[rr] = load_slice<FMT>(a.w + (size_t)(row0 + rr) * rb,
+                                FMT == FMT_BF16 ? nullptr : a.s + (size_t)(row0 + rr) * (K / 32), sl);
+    glm_bf16x8 xv[4];
+    slice_act<XF32>(a.x, (size_t)sl * 32, xv);
+    __builtin_amdgcn_sched_barrier(0);
+    glm_bf16x8 wv[kRowsPerWave][4];
+#pragma unroll
+    for (int rr = 0; rr < kRowsPerWave; ++rr) slice_bf16<FMT>(raw[rr], wv[rr]);
+#pragma unroll
+    for (int t = 0; t < kLinearMaxT; ++t) {
+      if (t < a.T) {
+        if (t > 0) slice_act<XF32>(a.x, (size_t)t * K + sl * 32, xv);
+#pragma unroll
+        for (int rr = 0; rr < kRowsPerWave; ++rr)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+              acc[rr][t] = __builtin_amdgcn_fdot2_f32_bf16(bf16_pair(wv[rr][i], p),
+                                                           bf16_pair(xv[i], p), acc[rr][t], false);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kLinearMaxT; ++t) {
+    if (t < a.T) {
+#pragma unroll
+      for (int rr = 0; rr < kRowsPerWave; ++rr) {
+        const float v = wave_sum(acc[rr][t]);
+        if (lane == 0) a.y[(size_t)t * a.N + row0 + rr] = (uint16_t)f32_to_bf16(v);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Generic fallback for shapes the MFMA tiling does not cover (K % 128 or
 // N % 16 non-zero; e.g. the tiny test geometries).  One thread per output.
 // ---------------------------------------------------------------------------
@@ -469,9 +605,32 @@ int glm_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, 
   return glm_gemv_launch(stream, GLM_FMT_MXFP4, 1, a, slots);
 }
 
+// Whether the few-token vector-ALU linear covers this call.
+static bool linear_rows_supported(int T, int in_dims, int out_dims) {
+  return T >= 1 && T <= glm::kLinearMaxT && in_dims % 32 == 0 &&
+         out_dims % (4 * glm::kRowsPerWave) == 0;
+}
+
+template <bool XF32>
+static int launch_linear_rows(hipStream_t stream, const void *x, int T, int in_dims,
+                              const void *weight, const uint8_t *scales, int fmt, int out_dims,
+                              uint16_t *y) {
+  const glm::LinearRowsArgs a{x, T, in_dims, out_dims, static_cast<const uint8_t *>(weight), scales, y};
+  const dim3 grid(out_dims / (4 * glm::kRowsPerWave)), block(256);
+  switch (fmt) {
+    case GLM_FMT_MXFP4: hipLaunchKernelGGL((glm::linear_rows_kernel<GLM_FMT_MXFP4, XF32>), grid, block, 0, stream, a); break;
+    case GLM_FMT_MXFP8: hipLaunchKernelGGL((glm::linear_rows_kernel<GLM_FMT_MXFP8, XF32>), grid, block, 0, stream, a); break;
+    default: hipLaunchKernelGGL((glm::linear_rows_kernel<GLM_FMT_BF16, XF32>), grid, block, 0, stream, a); break;
+  }
+  GLM_LAUNCH_CHECK("linear_rows_kernel");
+  return GLM_OK;
+}
+
 int glm_linear_launch(hipStream_t stream, const uint16_t *x, int T, int in_dims,
                       const void *weight, const uint8_t *scales, int fmt, int out_dims,
                       uint16_t *y) {
+  if (linear_rows_supported(T, in_dims, out_dims))
+    return launch_linear_rows<false>(stream, x, T, in_dims, weight, scales, fmt, out_dims, y);
   GemvArgs a{};
   a.act = x;
   a.w[0] = a.w[1] = static_cast<const uint8_t *>(weight);
@@ -570,6 +729,26 @@ extern "C" int glm_linear(void *stream, const uint16_t *x, int T, int in_dims, c
   GLM_REQUIRE(glm_aligned16({x, weight, y}), GLM_ERR_INVALID_ARGUMENT,
               "linear: buffers must be 16-byte aligned");
   return glm_linear_launch((hipStream_t)stream, x, T, in_dims, weight, scales, fmt, out_dims, y);
+}
+
+extern "C" int glm_linear_f32(void *stream, const float *x, int T, int in_dims, const void *weight,
+                              const uint8_t *scales, int fmt, int out_dims, uint16_t *y) {
+  glm::clear_error();
+  int rc = check_fmt(fmt);
+  if (rc) return rc;
+  GLM_REQUIRE(x && weight && y && (fmt == GLM_FMT_BF16 || scales), GLM_ERR_INVALID_ARGUMENT,
+              "linear_f32: null pointer argument");
+  GLM_REQUIRE(T >= 0, GLM_ERR_INVALID_ARGUMENT, "linear_f32: negative T");
+  rc = check_mx_geometry("linear_f32", fmt, in_dims, out_dims);
+  if (rc) return rc;
+  GLM_REQUIRE(glm_aligned16({x, weight, y}), GLM_ERR_INVALID_ARGUMENT,
+              "linear_f32: buffers must be 16-byte aligned");
+  if (T == 0) return GLM_OK;
+  GLM_REQUIRE(linear_rows_supported(T, in_dims, out_dims), GLM_ERR_UNSUPPORTED_SHAPE,
+              "linear_f32: T=%d out=%d unsupported (T <= %d, out a multiple of %d)", T, out_dims,
+              glm::kLinearMaxT, 4 * glm::kRowsPerWave);
+  return launch_linear_rows<true>((hipStream_t)stream, x, T, in_dims, weight, scales, fmt,
+                                  out_dims, y);
 }
 
 extern "C" int glm_dense_mlp(void *stream, const uint16_t *x, int T, int d, int I, int fmt,

@@ -506,6 +506,42 @@ def test_dense_mlp_parity(gu, fmt, T):
     assert np.mean(got == want) > 0.97
 
 
+@pytest.mark.parametrize("fmt", [native.GLM_FMT_MXFP8, native.GLM_FMT_MXFP4, native.GLM_FMT_BF16])
+@pytest.mark.parametrize("T", [1, 3, 4, 5, 20])
+def test_linear_parity_and_f32_input(gu, fmt, T):
+    # T <= 4 runs the vector-ALU rows kernel, T > 4 the MFMA tiles; the f32
+    # entry point must equal glm_linear of the bf16 cast bit for bit
+    torch = _torch()
+    rng = np.random.default_rng(5310 + T)
+    out_f, in_f = 1024, 2048
+    w = O.f32_to_bf16_bits(rng.normal(0, 0.02, (out_f, in_f)).astype(np.float32))
+    if fmt == native.GLM_FMT_BF16:
+        mat, codes, scales = O.bf16_bits_to_f32(w), gu.to_dev(w), None
+    else:
+        c, sc = O.quantize_mx(w, 8 if fmt == native.GLM_FMT_MXFP8 else 4, O.MX_RULE_NEAREST)
+        mat = O.dequant_mxfp8(c, sc) if fmt == native.GLM_FMT_MXFP8 else O.dequant_mxfp4(c, sc)
+        codes, scales = gu.to_dev(c), gu.to_dev(sc)
+    x32 = (rng.normal(0, 1, (T, in_f)) * (1 + 2.0 ** -12)).astype(np.float32)  # not bf16 values
+    xb = O.f32_to_bf16_bits(x32)
+    want = O.linear_bf16(O.bf16_bits_to_f32(xb), mat)
+    y = torch.empty((T, out_f), dtype=torch.bfloat16, device="cuda")
+    gu.call("glm_linear", gu.stream(), gu.p(gu.to_dev(xb)), T, in_f, gu.p(codes), gu.p(scales),
+            fmt, out_f, gu.p(y))
+    got = O.bf16_bits_to_f32(gu.bf16_bits(y))
+    assert O.rel_l2(got, want) < REL_L2
+    assert np.mean(got == want) > 0.97
+    y32 = torch.empty_like(y)
+    x32_dev = torch.from_numpy(x32).cuda()
+    if T <= 4:
+        gu.call("glm_linear_f32", gu.stream(), gu.p(x32_dev), T, in_f, gu.p(codes), gu.p(scales),
+                fmt, out_f, gu.p(y32))
+        assert np.array_equal(gu.bf16_bits(y32), gu.bf16_bits(y))
+    else:
+        rc = native.load().glm_linear_f32(gu.stream(), gu.p(x32_dev), T, in_f, gu.p(codes),
+                                          gu.p(scales), fmt, out_f, gu.p(y32))
+        assert rc == native.GLM_ERR_UNSUPPORTED_SHAPE
+
+
 # --------------------------------------------------------------------------- whole layer
 
 

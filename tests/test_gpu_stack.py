@@ -66,7 +66,9 @@ def _step(st, step):
         dl = dev["layers"][layer]
         codes, scales = dev["lin"][layer]
         a = torch.empty((s.T, s.d), dtype=torch.bfloat16, device="cuda")
-        native.call("glm_linear", stream, x.data_ptr(), s.T, s.d, codes.data_ptr(),
+        # layers past the first read the previous f32 output, rounded as read
+        fn = "glm_linear" if x.dtype == torch.bfloat16 else "glm_linear_f32"
+        native.call(fn, stream, x.data_ptr(), s.T, s.d, codes.data_ptr(),
                     scales.data_ptr(), native.GLM_FMT_MXFP8, s.d, a.data_ptr())
         out = torch.empty((s.T, s.d), dtype=torch.float32, device="cuda")
         w = torch.empty((s.T, s.k), dtype=torch.float32, device="cuda")
@@ -80,7 +82,7 @@ def _step(st, step):
                     bufs["ws"].data_ptr(), bufs["ws_bytes"], out.data_ptr(), w.data_ptr(),
                     idx.data_ptr())
         records.append((x, a, out, w, idx))
-        x = out.to(torch.bfloat16)  # the next layer's bf16 input
+        x = out  # the next layer's input, f32
     return records
 
 
@@ -93,7 +95,7 @@ def test_stack_layers_match_oracle_on_their_inputs(stack):
         recs = _step(stack, step)
         torch.cuda.synchronize()
         for layer, (x, a, out, w, idx) in enumerate(recs):
-            xb = gu.bf16_bits(x)
+            xb = gu.bf16_bits(x.to(torch.bfloat16))  # what the linear reads
             codes, scales = lin[layer]
             a_want = O.linear_bf16(O.bf16_bits_to_f32(xb), O.dequant_mxfp8(codes, scales))
             a_got = O.bf16_bits_to_f32(gu.bf16_bits(a))
