@@ -285,6 +285,8 @@ __device__ __forceinline__ int scan256(int v, int *s_tmp, int *total) {
 // tiles are 64 rows x Is/skd and write f32 partial sums [skd][T][d] that the
 // combine adds in order (all partial sums are exact f32 reductions of
 // disjoint K ranges, so the result is the f32 dot product rounded once).
+constexpr int kMaxSkq = 8;  // gate/up K ranges of the few-token shared tiles (d <= 4096)
+
 struct SharedArgs {
   const uint16_t *x;
   const uint8_t *sg, *su, *sd;  // bf16 gate/up [Is][d], down [d][Is] (sg == nullptr: none)
@@ -354,25 +356,65 @@ __device__ void shared_down_tile(const SharedArgs &a, int b, uint16_t *s_h) {
   const int row0 = tile * 64 + wave * 16;
   const int kbase = kd * KS;
   if (a.skq > 1) {
-    for (int i = threadIdx.x; i < a.T * KS; i += 256) {
-      const int t = i / KS, kk = kbase + i % KS;
-      float g = 0.0f, u = 0.0f;
-      for (int qq = 0; qq < a.skq; ++qq) {
-        g += a.gp[((size_t)qq * a.T + t) * a.Is + kk];
-        u += a.up[((size_t)qq * a.T + t) * a.Is + kk];
+    // few tokens (one group of 16): the tile's weights go out first -- they
+    // depend on nothing -- then the gate/up partial sums, two elements per
+    // thread at a time with every K range's load in flight together (ranges
+    // past skq re-read the last and are not added)
+    const uint8_t *wp = a.sd + ((size_t)(row0 + r) * a.Is + kbase) * 2;
+    WChunk<FMT_BF16> w[CPW_S];
+#pragma unroll
+    for (int c = 0; c < CPW_S; ++c) w[c] = load_chunk<FMT_BF16>(wp, c * 128, q);
+    for (int i0 = 0; i0 < a.T * KS; i0 += 512) {
+      float gv[2][kMaxSkq], uv[2][kMaxSkq];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int i = min(i0 + (int)threadIdx.x + 256 * u, a.T * KS - 1);
+        const int t = i / KS, kk = kbase + i % KS;
+#pragma unroll
+        for (int qq = 0; qq < kMaxSkq; ++qq) {
+          const size_t o = ((size_t)min(qq, a.skq - 1) * a.T + t) * a.Is + kk;
+          gv[u][qq] = a.gp[o];
+          uv[u][qq] = a.up[o];
+        }
       }
-      s_h[i] = (uint16_t)f32_to_bf16(limited_swiglu(bf16_round(g), bf16_round(u), a.limit));
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int i = i0 + (int)threadIdx.x + 256 * u;
+        float g = gv[u][0], up = uv[u][0];
+#pragma unroll
+        for (int qq = 1; qq < kMaxSkq; ++qq) {
+          if (qq < a.skq) {
+            g += gv[u][qq];
+            up += uv[u][qq];
+          }
+        }
+        if (i < a.T * KS)
+          s_h[i] = (uint16_t)f32_to_bf16(limited_swiglu(bf16_round(g), bf16_round(up), a.limit));
+      }
     }
     __syncthreads();
+    const int t = r;
+    const uint16_t *act = s_h + (size_t)min(t, a.T - 1) * KS;  // padding columns read a valid row
+    glm_f32x4 acc = glm_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < CPW_S; ++c) {
+      glm_bf16x8 wa[4], xb[4];
+      chunk_frags<FMT_BF16>(w[c], 0u, wa);
+      load_act_frags(act, c * 128, q, xb);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[i], xb[i], acc, 0, 0, 0);
+    }
+    if (t < a.T)
+      *reinterpret_cast<glm_f32x4 *>(a.yp + ((size_t)kd * a.T + t) * d + row0 + 4 * q) = acc;
+    return;
   }
   const uint8_t *wrow[1] = {a.sd + ((size_t)(row0 + r) * a.Is + kbase) * 2};
   const uint8_t *srow[1] = {nullptr};
-  const int p_end = a.skq > 1 ? a.T : min(a.T, tgroup * 16 + 16);
-  for (int p0 = tgroup * 16; p0 < p_end; p0 += 16) {
+  for (int p0 = tgroup * 16; p0 < min(a.T, tgroup * 16 + 16); p0 += 16) {
     const int t = p0 + r;
     glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
     const int tc = min(t, a.T - 1);  // padding columns read a valid row
-    const uint16_t *act = a.skq > 1 ? s_h + (size_t)tc * KS : a.hs + (size_t)tc * a.Is + kbase;
+    const uint16_t *act = a.hs + (size_t)tc * a.Is + kbase;
     wave_mma<FMT_BF16, 1, CPW_S>(wrow, srow, 0, q, act, acc);
     if (t < a.T)
       *reinterpret_cast<glm_f32x4 *>(a.yp + ((size_t)kd * a.T + t) * d + row0 + 4 * q) = acc[0];
@@ -645,6 +687,9 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DownArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int kPairMaxT = 4;
 constexpr int kPairMaxK = 8;
+// 16-byte pieces of h per thread in down_combine_kernel: k*I/8 pieces over
+// 64*max(k, 4) threads is at most I/512 <= 2 (I <= 1024)
+constexpr int kMaxHPieces = 2;
 
 struct PairArgs {
   const float *logits, *bias;
@@ -762,23 +807,42 @@ __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ __attribute__((aligned(16))) uint16_t s_h[];  // [k][lds_row_stride(I)]
   __shared__ float s_p[kPairMaxK][16];
-  const int lane = threadIdx.x & 63, j = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, q = lane >> 4;
   const int k = a.k, d = a.d, I = a.I;
   const int tiles = d / 16;
   const int t = blockIdx.x / tiles;
   const int row0 = (blockIdx.x % tiles) * 16;
-  // h rows first: they do not depend on the route, and LDS staging must not
-  // queue behind the weight stream
-  stage_rows(s_h, a.h + (size_t)t * k * I, nullptr, k, I);
-  WaveWeights<FMT_MXFP4, 1, CPW_R> ww;
+  // Every load goes out before the first wait: the wave's route, the h rows
+  // (into registers; past the rows the index is clamped so that no load
+  // depends on the lane), then the weights, whose addresses wait only for
+  // the route; the h rows reach LDS after that.
+  long long e = 0;
   float wj = 0.0f;
   if (j < k) {
-    const long long e = a.indices[(size_t)t * k + j];
+    e = a.indices[(size_t)t * k + j];
     wj = a.weights[(size_t)t * k + j];
+  }
+  const int per_row = I / 8, nh = k * per_row;  // 16-byte pieces of the k rows of h
+  const uint16_t *hsrc = a.h + (size_t)t * k * I;
+  glm_u32x4 hv[kMaxHPieces];
+#pragma unroll
+  for (int u = 0; u < kMaxHPieces; ++u) {
+    const int i = min((int)threadIdx.x + (int)blockDim.x * u, nh - 1);
+    hv[u] = *reinterpret_cast<const glm_u32x4 *>(hsrc + (size_t)i * 8);
+  }
+  WaveWeights<FMT_MXFP4, 1, CPW_R> ww;
+  if (j < k) {
     const uint8_t *wrow[1] = {a.dw + e * a.w_stride + (size_t)(row0 + r) * (I / 2)};
     const uint8_t *srow[1] = {a.ds + e * a.s_stride + (size_t)(row0 + r) * (I / 32)};
     load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
+  }
+#pragma unroll
+  for (int u = 0; u < kMaxHPieces; ++u) {
+    const int i = (int)threadIdx.x + (int)blockDim.x * u;
+    if (i < nh)
+      *reinterpret_cast<glm_u32x4 *>(s_h + (i / per_row) * lds_row_stride(I) + (i % per_row) * 8) = hv[u];
   }
   // the shared expert's contribution to these 16 outputs (thread c < 16)
   float shared_v = 0.0f;
