@@ -52,7 +52,9 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t *__re
 // ---------------------------------------------------------------------------
 // Logits for many tokens on MFMA: v_mfma_f32_16x16x4_f32 forms exact f32
 // products of f32(x) and W and accumulates them in f32 (only the summation
-// order differs from a sequential dot product).  Workgroup = 16 tokens x 32
+// order differs from a sequential dot product: each wave keeps the even and
+// the odd K positions of a step in separate accumulators, added at the end).
+// Workgroup = 16 tokens x 32
 // experts (two 16 x 16 tiles); its KSPLIT waves split K into equal ranges
 // (4 for many tokens, 16 for fewer, where the grid is small), so several
 // waves share each SIMD and hide each other's L2 latency, and the partial
@@ -61,7 +63,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t *__re
 // (16 B of bf16) and 8 consecutive W (32 B) per step.  Rows past T or E are
 // clamped for the loads and never stored.
 // ---------------------------------------------------------------------------
-template <int KSPLIT>
+template <int KSPLIT, int PD>
 __global__ __launch_bounds__(64 * KSPLIT) void router_gemm_kernel(
     const uint16_t *__restrict__ x, const float *__restrict__ w, int T, int d, int E,
     float *__restrict__ logits) {
@@ -70,37 +72,56 @@ __global__ __launch_bounds__(64 * KSPLIT) void router_gemm_kernel(
   const int r = lane & 15, q = lane >> 4;
   const int t0 = blockIdx.x * 16;
   const int e0 = blockIdx.y * 32;
-  const int kq = d / KSPLIT;  // this wave's K range [wave * kq, (wave + 1) * kq)
+  const int kq = d / KSPLIT;  // this wave's K range [wave * kq, (wave + 1) * kq), a multiple of 32 * PD
   const int kb = wave * kq;
   const uint16_t *xr = x + (size_t)min(t0 + r, T - 1) * d + kb + 8 * q;
   const float *wr0 = w + (size_t)min(e0 + r, E - 1) * d + kb + 8 * q;
   const float *wr1 = w + (size_t)min(e0 + 16 + r, E - 1) * d + kb + 8 * q;
   glm_f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  glm_u32x4 xv = *reinterpret_cast<const glm_u32x4 *>(xr);
-  float4 wa0 = *reinterpret_cast<const float4 *>(wr0), wb0 = *reinterpret_cast<const float4 *>(wr0 + 4);
-  float4 wa1 = *reinterpret_cast<const float4 *>(wr1), wb1 = *reinterpret_cast<const float4 *>(wr1 + 4);
-  for (int k0 = 0; k0 < kq; k0 += 32) {
-    const glm_u32x4 cx = xv;
-    const float4 ca0 = wa0, cb0 = wb0, ca1 = wa1, cb1 = wb1;
-    if (k0 + 32 < kq) {  // next step's operands in flight during this step's MFMAs
-      xv = *reinterpret_cast<const glm_u32x4 *>(xr + k0 + 32);
-      wa0 = *reinterpret_cast<const float4 *>(wr0 + k0 + 32);
-      wb0 = *reinterpret_cast<const float4 *>(wr0 + k0 + 36);
-      wa1 = *reinterpret_cast<const float4 *>(wr1 + k0 + 32);
-      wb1 = *reinterpret_cast<const float4 *>(wr1 + k0 + 36);
-    }
-    const float xf[8] = {bf16_to_f32(cx[0] & 0xffffu), bf16_to_f32(cx[0] >> 16),
-                         bf16_to_f32(cx[1] & 0xffffu), bf16_to_f32(cx[1] >> 16),
-                         bf16_to_f32(cx[2] & 0xffffu), bf16_to_f32(cx[2] >> 16),
-                         bf16_to_f32(cx[3] & 0xffffu), bf16_to_f32(cx[3] >> 16)};
-    const float w0[8] = {ca0.x, ca0.y, ca0.z, ca0.w, cb0.x, cb0.y, cb0.z, cb0.w};
-    const float w1[8] = {ca1.x, ca1.y, ca1.z, ca1.w, cb1.x, cb1.y, cb1.z, cb1.w};
+  glm_f32x4 acc2 = {0.f, 0.f, 0.f, 0.f}, acc3 = {0.f, 0.f, 0.f, 0.f};
+  // a ring of PD steps of operands in registers: step s + PD is in flight
+  // while step s feeds the MFMAs (L2 latency spans many steps' MFMAs)
+  glm_u32x4 xv[PD];
+  float4 wa0[PD], wb0[PD], wa1[PD], wb1[PD];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[i], w0[i], acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[i], w1[i], acc1, 0, 0, 0);
+  for (int i = 0; i < PD; ++i) {
+    xv[i] = *reinterpret_cast<const glm_u32x4 *>(xr + 32 * i);
+    wa0[i] = *reinterpret_cast<const float4 *>(wr0 + 32 * i);
+    wb0[i] = *reinterpret_cast<const float4 *>(wr0 + 32 * i + 4);
+    wa1[i] = *reinterpret_cast<const float4 *>(wr1 + 32 * i);
+    wb1[i] = *reinterpret_cast<const float4 *>(wr1 + 32 * i + 4);
+  }
+  for (int k0 = 0; k0 < kq; k0 += 32 * PD) {
+#pragma unroll
+    for (int i = 0; i < PD; ++i) {
+      const glm_u32x4 cx = xv[i];
+      const float4 ca0 = wa0[i], cb0 = wb0[i], ca1 = wa1[i], cb1 = wb1[i];
+      const int kn = k0 + 32 * (i + PD);
+      if (kn < kq) {
+        xv[i] = *reinterpret_cast<const glm_u32x4 *>(xr + kn);
+        wa0[i] = *reinterpret_cast<const float4 *>(wr0 + kn);
+        wb0[i] = *reinterpret_cast<const float4 *>(wr0 + kn + 4);
+        wa1[i] = *reinterpret_cast<const float4 *>(wr1 + kn);
+        wb1[i] = *reinterpret_cast<const float4 *>(wr1 + kn + 4);
+      }
+      const float xf[8] = {bf16_to_f32(cx[0] & 0xffffu), bf16_to_f32(cx[0] >> 16),
+                           bf16_to_f32(cx[1] & 0xffffu), bf16_to_f32(cx[1] >> 16),
+                           bf16_to_f32(cx[2] & 0xffffu), bf16_to_f32(cx[2] >> 16),
+                           bf16_to_f32(cx[3] & 0xffffu), bf16_to_f32(cx[3] >> 16)};
+      const float w0[8] = {ca0.x, ca0.y, ca0.z, ca0.w, cb0.x, cb0.y, cb0.z, cb0.w};
+      const float w1[8] = {ca1.x, ca1.y, ca1.z, ca1.w, cb1.x, cb1.y, cb1.z, cb1.w};
+      // four independent accumulation chains keep the MFMA pipeline full
+#pragma unroll
+      for (int m = 0; m < 8; m += 2) {
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[m], w0[m], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[m], w1[m], acc1, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[m + 1], w0[m + 1], acc2, 0, 0, 0);
+        acc3 = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[m + 1], w1[m + 1], acc3, 0, 0, 0);
+      }
     }
   }
+  acc0 += acc2;
+  acc1 += acc3;
   if (wave > 0) {
     red[wave - 1][0][lane] = acc0;
     red[wave - 1][1][lane] = acc1;
@@ -255,12 +276,18 @@ int glm_router_logits_launch(hipStream_t stream, const uint16_t *x, int T, int d
     return GLM_ERR_UNSUPPORTED_SHAPE;
   }
   dim3 grid((T + 15) / 16, (E + 31) / 32);
-  if (T >= 256 && d % (32 * 4) == 0)
-    hipLaunchKernelGGL(router_gemm_kernel<4>, grid, dim3(256), 0, stream, x, weight, T, d, E,
-                       logits);
-  else
-    hipLaunchKernelGGL(router_gemm_kernel<16>, grid, dim3(1024), 0, stream, x, weight, T, d, E,
-                       logits);
+  // prefetch depth: 32-wide K steps in flight per wave, where its K range allows
+  if (T >= 256 && d % (32 * 4) == 0) {
+    if (d % (32 * 4 * 4) == 0)
+      hipLaunchKernelGGL((router_gemm_kernel<4, 4>), grid, dim3(256), 0, stream, x, weight, T, d, E, logits);
+    else
+      hipLaunchKernelGGL((router_gemm_kernel<4, 1>), grid, dim3(256), 0, stream, x, weight, T, d, E, logits);
+  } else {
+    if (d % (32 * 16 * 2) == 0)  // 1024-thread blocks: at most 128 registers, so two steps
+      hipLaunchKernelGGL((router_gemm_kernel<16, 2>), grid, dim3(1024), 0, stream, x, weight, T, d, E, logits);
+    else
+      hipLaunchKernelGGL((router_gemm_kernel<16, 1>), grid, dim3(1024), 0, stream, x, weight, T, d, E, logits);
+  }
   GLM_LAUNCH_CHECK("router_gemm_kernel");
   return GLM_OK;
 }
