@@ -608,29 +608,42 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f4_kernel(SplitArgs a
       wa[rt] = glm_i32x8{(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
       wsc[rt] = (int)(*reinterpret_cast<const uint32_t *>(base + S::kWS + w16 * 4 + sl) >> (8 * q));
     }
+    // activation fragment f = (part, ct) of this chunk: hi then lo, 4 token
+    // blocks each
+    auto xfrag = [&](int f, glm_i32x8 &xb, int &xsc) {
+      const int part = f >> 2, ct = f & 3;
+      const uint8_t *xblk = base + S::kX + (wt * 64 + ct * 16) * 256;
+      const glm_u32x4 b0 = *reinterpret_cast<const glm_u32x4 *>(xblk + (part ? xl_lo0 : xl_hi0));
+      const glm_u32x4 b1 = *reinterpret_cast<const glm_u32x4 *>(xblk + (part ? xl_lo1 : xl_hi1));
+      xb = glm_i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3],
+                     (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+      xsc = (int)(*reinterpret_cast<const uint32_t *>(
+                      base + S::kXS + (part * kTileM + wt * 64 + ct * 16) * 4 + sl) >>
+                  (8 * q));
+    };
+    // Fragment f + 1 is read from LDS before fragment f's MFMAs issue, so
+    // its latency hides behind them; one fragment ahead bounds the live
+    // registers.
+    glm_i32x8 xb;
+    int xsc;
+    xfrag(0, xb, xsc);
 #pragma unroll
-    for (int part = 0; part < 2; ++part) {  // hi, then lo
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        // token blocks wholly past the tile's rows (the last, partial tile of
-        // an expert) are skipped: their columns are never stored
-        if (wt * 64 + ct * 16 >= rows) continue;
-        const uint8_t *xblk = base + S::kX + (wt * 64 + ct * 16) * 256;
-        const glm_u32x4 b0 =
-            *reinterpret_cast<const glm_u32x4 *>(xblk + (part ? xl_lo0 : xl_hi0));
-        const glm_u32x4 b1 =
-            *reinterpret_cast<const glm_u32x4 *>(xblk + (part ? xl_lo1 : xl_hi1));
-        const glm_i32x8 xb = glm_i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3],
-                                       (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
-        const int xsc = (int)(*reinterpret_cast<const uint32_t *>(
-                                  base + S::kXS + (part * kTileM + wt * 64 + ct * 16) * 4 + sl) >>
-                              (8 * q));
+    for (int f = 0; f < 8; ++f) {
+      glm_i32x8 xn;
+      int xscn = 0;
+      if (f + 1 < 8) xfrag(f + 1, xn, xscn);
+      // token blocks wholly past the tile's rows (the last, partial tile of
+      // an expert) are skipped: their columns are never stored
+      if (wt * 64 + (f & 3) * 16 < rows) {
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt)
-          acc[rt][ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              wa[rt], xb, acc[rt][ct], 4, 0, 0, wsc[rt], 0, xsc);
-        // one fragment in flight at a time: bounds the live registers
-        __builtin_amdgcn_sched_barrier(0);
+          acc[rt][f & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              wa[rt], xb, acc[rt][f & 3], 4, 0, 0, wsc[rt], 0, xsc);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (f + 1 < 8) {
+        xb = xn;
+        xsc = xscn;
       }
     }
   };
