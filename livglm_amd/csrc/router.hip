@@ -1,6 +1,7 @@
 // Router: logits GEMV + sigmoid/bias/group-mask/top-k/normalise.
 // Restates TopKRouter.__call__ (moe.py:36-63) for gfx950.
 #include "glm_common.h"
+#include "topk_select.h"
 
 namespace glm {
 
@@ -143,122 +144,25 @@ __global__ __launch_bounds__(64 * KSPLIT) void router_gemm_kernel(
   }
 }
 
-// Lexicographic "better" for (value, index): larger value; on a tie the
-// larger index (a stable ascending argsort puts it last, moe.py:33-34).
-__device__ __forceinline__ bool better(float v1, int i1, float v2, int i2) {
-  return v1 > v2 || (v1 == v2 && i1 > i2);
-}
-
 // ---------------------------------------------------------------------------
-// Selection: one wave per token.  Lane l holds experts l + 64 i.
+// Selection: one wave per token (select_token), four tokens per workgroup.
 // ---------------------------------------------------------------------------
 template <int EPL>
-__global__ __launch_bounds__(64) void router_select_kernel(
+__global__ __launch_bounds__(256) void router_select_kernel(
     const float *__restrict__ logits, const float *__restrict__ bias, int T, int E, int k,
     int n_group, int topk_group, int norm, float scale, float *__restrict__ weights,
     uint32_t *__restrict__ indices) {
-  __shared__ float s_choice[64 * EPL];
-  __shared__ float s_gscore[64];
-  __shared__ int s_gkeep[64];
-  __shared__ float s_wsel[64];
-  __shared__ int s_isel[64];
-  const int t = blockIdx.x;
-  const int lane = threadIdx.x;
-  if (t >= T) return;
-  float score[EPL], choice[EPL];
-  bool taken[EPL];
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    const int e = lane + 64 * i;
-    taken[i] = false;
-    if (e < E) {
-      const float l = logits[(size_t)t * E + e];
-      score[i] = sigmoid_f32(l);
-      choice[i] = score[i] + bias[e];
-    } else {
-      score[i] = 0.0f;
-      choice[i] = -INFINITY;
-      taken[i] = true;  // never selectable
-    }
-  }
-  if (n_group > 1) {
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) s_choice[lane + 64 * i] = choice[i];
-    __syncthreads();
-    const int per = E / n_group;
-    if (lane < n_group) {
-      float top1 = -INFINITY, top2 = -INFINITY;
-      for (int q = 0; q < per; ++q) {
-        const float v = s_choice[lane * per + q];
-        if (v > top1) {
-          top2 = top1;
-          top1 = v;
-        } else if (v > top2) {
-          top2 = v;
-        }
-      }
-      s_gscore[lane] = top2 + top1;
-    }
-    __syncthreads();
-    if (lane < n_group) {
-      const float mine = s_gscore[lane];
-      int rank = 0;
-      for (int g = 0; g < n_group; ++g)
-        if (better(s_gscore[g], g, mine, lane)) ++rank;
-      s_gkeep[lane] = rank < topk_group;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      const int e = lane + 64 * i;
-      if (e < E && !s_gkeep[e / per]) choice[i] = -INFINITY;
-    }
-  }
-  // k rounds of wave-wide argmax; round r fills ascending position k-1-r.
-  for (int r = 0; r < k; ++r) {
-    float bv = -INFINITY, bs = 0.0f;
-    int bi = -1;
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      const int e = lane + 64 * i;
-      if (!taken[i] && (bi < 0 || better(choice[i], e, bv, bi))) {
-        bv = choice[i];
-        bi = e;
-        bs = score[i];
-      }
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      const float os = __shfl_xor(bs, off, 64);
-      if (oi >= 0 && (bi < 0 || better(ov, oi, bv, bi))) {
-        bv = ov;
-        bi = oi;
-        bs = os;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < EPL; ++i)
-      if (lane + 64 * i == bi) taken[i] = true;
-    if (lane == 0) {
-      s_isel[k - 1 - r] = bi;
-      s_wsel[k - 1 - r] = bs;
-    }
-  }
-  __syncthreads();
-  if (lane == 0) {
-    float total = 0.0f;
-    if (norm)
-      for (int j = 0; j < k; ++j) total += s_wsel[j];
-    for (int j = 0; j < k; ++j) {
-      float wj = s_wsel[j];
-      if (norm) wj = wj / (total + 1e-20f);
-      weights[(size_t)t * k + j] = wj * scale;
-      indices[(size_t)t * k + j] = (uint32_t)s_isel[j];
-    }
-  }
+  __shared__ float scratch[4][64 * EPL + 256];
+  __shared__ int sel[4][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;  // wave-uniform; the selection synchronises one wave only
+  select_token<EPL>(logits + (size_t)t * E, bias, E, k, n_group, topk_group, norm, scale,
+                    weights + (size_t)t * k, indices + (size_t)t * k, sel[wave], scratch[wave],
+                    lane);
 }
+
 
 }  // namespace glm
 
@@ -300,7 +204,7 @@ int glm_router_select_launch(hipStream_t stream, const float *logits, const floa
   if (T == 0) return GLM_OK;
   const int epl = (E + 63) / 64;
 #define GLM_SELECT(N)                                                                         \
-  hipLaunchKernelGGL(router_select_kernel<N>, dim3(T), dim3(64), 0, stream, logits, bias, T, \
+  hipLaunchKernelGGL(router_select_kernel<N>, dim3((T + 3) / 4), dim3(256), 0, stream, logits, bias, T, \
                      E, k, n_group, topk_group, norm, scale, weights, indices)
   if (epl <= 1) GLM_SELECT(1);
   else if (epl <= 2) GLM_SELECT(2);
