@@ -433,6 +433,50 @@ __global__ __launch_bounds__(256) void act_split_kernel(const uint16_t *x, long 
   slo[g] = (uint8_t)bl;
 }
 
+// The split of one 32-element scale group held 8 per lane by the four lanes
+// q = 0..3 of a lane row (lanes r, r + 16, r + 32, r + 48); v holds this
+// lane's elements 16 i + 4 q + m at v[4 i + m].  Same arithmetic as
+// act_split_kernel: ch[i] / cl[i] are the hi / lo codes of elements
+// 16 i + 4 q .. + 3, bh / bl the group's scale bytes.
+__device__ __forceinline__ void split_group_part(float v[8], int q, uint32_t ch[2], uint32_t cl[2],
+                                                 int *bh_out, int *bl_out) {
+  (void)q;
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+  amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+  const int bh = split_scale_byte(amax);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i], 127 - bh), ldexpf(v[4 * i + 1], 127 - bh),
+                                            0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i + 2], 127 - bh),
+                                        ldexpf(v[4 * i + 3], 127 - bh), w, true);
+    ch[i] = (uint32_t)w;
+    v[4 * i] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 0), bh - 127);
+    v[4 * i + 1] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 1), bh - 127);
+    v[4 * i + 2] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 2), bh - 127);
+    v[4 * i + 3] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 3), bh - 127);
+  }
+  float ramax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ramax = fmaxf(ramax, fabsf(v[j]));
+  ramax = fmaxf(ramax, __shfl_xor(ramax, 16, 64));
+  ramax = fmaxf(ramax, __shfl_xor(ramax, 32, 64));
+  const int bl = split_scale_byte(ramax);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i], 127 - bl), ldexpf(v[4 * i + 1], 127 - bl),
+                                            0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i + 2], 127 - bl),
+                                        ldexpf(v[4 * i + 3], 127 - bl), w, true);
+    cl[i] = (uint32_t)w;
+  }
+  *bh_out = bh;
+  *bl_out = bl;
+}
+
 struct SplitArgs {
   const uint8_t *xhi, *xlo;    // activation codes [rows][K]
   const uint8_t *xshi, *xslo;  // activation scales [rows][K/32]
@@ -447,6 +491,10 @@ struct SplitArgs {
   int feature_tiles;
   uint16_t *out;               // bf16 [rows][N]
   float limit;
+  // gate/up: when set, the epilogue writes the FP8 hi/lo split of h (the down
+  // GEMM's input, SplitLayout(out_rows, N)) instead of h itself
+  uint8_t *out_split;
+  long long out_rows;
 };
 
 // Workgroup tile of the block-scaled GEMMs: 128 token rows x 512 weight rows
@@ -661,6 +709,46 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f4_kernel(SplitArgs a
 
   // ---- epilogue: lane (r, q) of block (rt, ct) holds weight rows 4q..4q+3 of
   // the block for token column r
+  if constexpr (NPROJ == 2) {
+    if (a.out_split != nullptr) {
+      // h's FP8 hi/lo split, exactly as act_split_kernel forms it from the
+      // bf16 h: the wave's 32 features f0 + 32 wf + [0, 32) of a token are one
+      // scale group, held 8 per lane by the four lanes (r, q = 0..3); the
+      // group maxima are exchanged across them (the shuffles run on every
+      // lane, the stores only for real rows)
+      const SplitLayout L(a.out_rows, a.N);
+      const int g0 = f0 + wf * 32;
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const int row = wt * 64 + ct * 16 + r;
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+            v[4 * i + m] = bf16_round(limited_swiglu(bf16_round(acc[i][ct][m]),
+                                                     bf16_round(acc[2 + i][ct][m]), a.limit));
+        uint32_t ch[2], cl[2];
+        int bh, bl;
+        split_group_part(v, q, ch, cl, &bh, &bl);
+        if (row < rows) {
+          const size_t prow = (size_t)(pos0 + row);
+          uint8_t *hi = a.out_split + prow * a.N + g0;
+          uint8_t *lo = a.out_split + L.lo + prow * a.N + g0;
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            *reinterpret_cast<uint32_t *>(hi + i * 16 + 4 * q) = ch[i];
+            *reinterpret_cast<uint32_t *>(lo + i * 16 + 4 * q) = cl[i];
+          }
+          if (q == 0) {
+            a.out_split[L.shi + prow * (a.N / 32) + g0 / 32] = (uint8_t)bh;
+            a.out_split[L.slo + prow * (a.N / 32) + g0 / 32] = (uint8_t)bl;
+          }
+        }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) {
     const int row = wt * 64 + ct * 16 + r;
@@ -770,9 +858,12 @@ int glm_grouped_gate_up_launch(hipStream_t stream, const void *x_split, int T,
                                const int32_t *pair_token, const int4 *tiles,
                                const int32_t *num_tiles, int max_tiles, int d, int I,
                                const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
-                               const uint8_t *us, uint16_t *h, float limit) {
+                               const uint8_t *us, uint16_t *h, float limit, void *h_split,
+                               long long P) {
   SplitArgs a{};
   set_split(a, x_split, T, d);
+  a.out_split = static_cast<uint8_t *>(h_split);  // when set: the split of h [P][I], not h
+  a.out_rows = P;
   a.act_index = pair_token;
   a.tiles = tiles;
   a.num_tiles = num_tiles;
@@ -876,7 +967,7 @@ extern "C" int glm_expert_gate_up_grouped(void *stream, const void *x_split, int
   return glm_grouped_gate_up_launch((hipStream_t)stream, x_split, T, pair_token,
                                     reinterpret_cast<const int4 *>(tiles), num_tiles, max_tiles,
                                     d, I, gate_packed, gate_scales, up_packed, up_scales, h,
-                                    swiglu_limit);
+                                    swiglu_limit, nullptr, 0);
 }
 
 extern "C" int glm_expert_down_grouped(void *stream, const void *h_split, int P, int I, int d,

@@ -50,7 +50,8 @@ int glm_grouped_gate_up_launch(hipStream_t stream, const void *x_split, int T,
                                const int32_t *pair_token, const int4 *tiles,
                                const int32_t *num_tiles, int max_tiles, int d, int I,
                                const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
-                               const uint8_t *us, uint16_t *h, float limit);
+                               const uint8_t *us, uint16_t *h, float limit, void *h_split,
+                               long long P);
 int glm_grouped_down_launch(hipStream_t stream, const void *h_split, long long P,
                             const int4 *tiles, const int32_t *num_tiles, int max_tiles, int I,
                             int d, const uint8_t *dw, const uint8_t *ds, uint16_t *y);
@@ -308,10 +309,8 @@ extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
     if (rc) return rc;
     rc = glm_grouped_gate_up_launch(stream, w.x_split, T, w.pair_token, w.tiles, w.num_tiles,
                                     w.max_tiles, d, I, gate_packed, gate_scales, up_packed,
-                                    up_scales, w.h, swiglu_limit);
-    if (rc) return rc;
-    rc = glm_act_split_launch(stream, w.h, (long long)T * top_k, I, w.h_split);
-    if (rc) return rc;
+                                    up_scales, w.h, swiglu_limit, w.h_split, (long long)T * top_k);
+    if (rc) return rc;  // the gate/up epilogue writes h's FP8 split for the down GEMM
     rc = glm_grouped_down_launch(stream, w.h_split, (long long)T * top_k, w.tiles, w.num_tiles,
                                  w.max_tiles, I, d, down_packed, down_scales, w.y);
   } else {

@@ -361,6 +361,59 @@ def test_grouped_expert_gemms_parity(gu):
     assert O.rel_l2(y_got, y_want) < REL_L2 and np.mean(y_got == y_want) > 0.97
 
 
+def test_moe_forward_grouped_equals_public_composition(gu):
+    # glm_moe_forward's grouped path (multi-workgroup dispatch, h split fused
+    # into the gate/up epilogue) must equal, bit for bit, the public entry
+    # points composed by hand: router, dispatch, tiles, x split, gate/up to
+    # bf16 h, split of h, down, combine
+    torch = _torch()
+    shape = MoEShape("grouped", 400, 1024, 32, 4, 256, 0)
+    layer = make_layer(shape, 1718)
+    T, k, E, d, I = shape.T, shape.k, shape.E, shape.d, shape.I
+    P = T * k
+    dl = gu.upload_layer(layer)
+    lib = native.load()
+    ws_bytes = lib.glm_moe_workspace_bytes(T, d, E, k, I, 0)
+    ws = gu.workspace(ws_bytes)
+    out = torch.empty((T, d), dtype=torch.float32, device="cuda")
+    gu.call("glm_moe_forward", gu.stream(), gu.p(dl["x"]), T, d, gu.p(dl["router_weight"]),
+            gu.p(dl["router_bias"]), E, k, 1, 1, 1, shape.routed_scaling_factor, I,
+            *(gu.p(dl[key]) for key in BANK_KEYS), 0, native.GLM_FMT_BF16, None, None, None,
+            None, None, None, None, shape.swiglu_limit, gu.p(ws), ws_bytes, gu.p(out), None,
+            None)
+    f32 = dict(dtype=torch.float32, device="cuda")
+    i32 = dict(dtype=torch.int32, device="cuda")
+    logits, wts = torch.empty((T, E), **f32), torch.empty((T, k), **f32)
+    idx = torch.empty((T, k), **i32)
+    gu.call("glm_router_topk", gu.stream(), gu.p(dl["x"]), T, d, gu.p(dl["router_weight"]),
+            gu.p(dl["router_bias"]), E, k, 1, 1, 1, shape.routed_scaling_factor, gu.p(logits),
+            gu.p(wts), gu.p(idx))
+    b = {n: torch.empty((s,), **i32) for n, s in
+         [("counts", E), ("offsets", E + 1), ("perm", P), ("inv", P), ("tok", P), ("active", E),
+          ("num_active", 1), ("work", 4 * E), ("status", 1)]}
+    gu.call("glm_moe_dispatch", gu.stream(), gu.p(idx), T, k, E, *(gu.p(b[n]) for n in
+            ("counts", "offsets", "perm", "inv", "tok", "active", "num_active", "work", "status")))
+    max_tiles = (P + 127) // 128 + E
+    tiles, ntiles = torch.empty((max_tiles, 4), **i32), torch.empty(1, **i32)
+    gu.call("glm_moe_tiles", gu.stream(), gu.p(b["work"]), E, gu.p(tiles), gu.p(ntiles))
+    x_split = gu.workspace(lib.glm_act_split_bytes(T, d))
+    h_split = gu.workspace(lib.glm_act_split_bytes(P, I))
+    h = torch.empty((P, I), dtype=torch.bfloat16, device="cuda")
+    y = torch.empty((P, d), dtype=torch.bfloat16, device="cuda")
+    gu.call("glm_act_split_fp8", gu.stream(), gu.p(dl["x"]), T, d, gu.p(x_split))
+    gu.call("glm_expert_gate_up_grouped", gu.stream(), gu.p(x_split), T, d, I,
+            *(gu.p(dl[key]) for key in BANK_KEYS[:4]), gu.p(b["tok"]), gu.p(tiles), gu.p(ntiles),
+            max_tiles, shape.swiglu_limit, gu.p(h))
+    gu.call("glm_act_split_fp8", gu.stream(), gu.p(h), P, I, gu.p(h_split))
+    gu.call("glm_expert_down_grouped", gu.stream(), gu.p(h_split), P, I, d,
+            gu.p(dl[BANK_KEYS[4]]), gu.p(dl[BANK_KEYS[5]]), gu.p(tiles), gu.p(ntiles), max_tiles,
+            gu.p(y))
+    want = torch.empty((T, d), **f32)
+    gu.call("glm_moe_combine", gu.stream(), gu.p(y), gu.p(b["inv"]), gu.p(wts), None, T, k, d,
+            gu.p(want))
+    assert np.array_equal(gu.host(out).view(np.uint32), gu.host(want).view(np.uint32))
+
+
 def _split_model(xb, K):
     """numpy model of the FP8 activation split: per 32-element group the
     smallest E8M0 scale keeping the group within 448, hi = RNE E4M3FN of the
