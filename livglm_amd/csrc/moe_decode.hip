@@ -18,7 +18,7 @@
 // dispatch altogether:
 //
 //   1. route_logits_kernel    as above.
-//   2. select_gate_up_kernel  block = (pair t*k + j, 16-row tile): wave 0
+//   2. select_gate_up_kernel  block = (pair t*k + j, 16-row tile): every wave
 //                             selects token t's experts from its logits, then
 //                             the block computes gate/up + SwiGLU of expert j
 //                             for that token; extra blocks: shared down tiles.
@@ -59,48 +59,6 @@ struct RouteArgs {
   int presel;  // select_dispatch_kernel: indices already selected (router_select_kernel)
   int logits_done;  // route_logits_kernel: logits already computed; run the shared blocks only
 };
-
-// Block-wide top-k of one token without group masks (n_group == 1, E <= 256),
-// for the token-major path where every block needs one token's choice: an
-// expert's rank is the number of experts that beat it -- a larger choice, or an
-// equal choice and a larger index, as the stable ascending argsort of
-// moe.py:33-34 orders them -- counted by all 256 threads at once (two per
-// expert when E <= 128).  The expert of rank r lands in column k-1-r: s_sel[j]
-// gets column j's expert, s_wsel[j] its sigmoid score.  NaN choices rank as
-// -inf.  Called uniformly by the block; three barriers inside.
-__device__ void select_ranked(const float *logits_row, const float *bias, int E, int k,
-                              long long *s_key, float *s_score, int *s_cnt, int *s_sel,
-                              float *s_wsel) {
-  const int tid = threadIdx.x;
-  if (tid < E) {
-    const float sc = sigmoid_f32(logits_row[tid]);
-    const float ch = sc + bias[tid];
-    const float c = ch != ch ? -INFINITY : ch + 0.0f;  // NaN -> -inf, -0 -> +0
-    s_key[tid] = ((long long)order_key(c) << 32) | (unsigned)tid;
-    s_score[tid] = sc;
-  }
-  __syncthreads();
-  const bool split = E <= 128;
-  const int c = split ? (tid & 127) : tid;
-  const int o0 = split ? (tid >> 7) * 64 : 0;
-  const int o1 = split ? min(o0 + 64, E) : E;
-  int cnt = 0;
-  if (c < E) {
-    const long long kc = s_key[c];
-#pragma unroll 8
-    for (int o = o0; o < o1; ++o) cnt += s_key[o] > kc ? 1 : 0;  // o is wave-uniform: broadcast
-  }
-  s_cnt[tid] = cnt;
-  __syncthreads();
-  if (tid < E) {
-    const int rank = split ? s_cnt[tid] + s_cnt[tid + 128] : s_cnt[tid];
-    if (rank < k) {
-      s_sel[k - 1 - rank] = tid;
-      s_wsel[k - 1 - rank] = s_score[tid];
-    }
-  }
-  __syncthreads();
-}
 
 // Exclusive scan over a 256-thread block (4 waves); *total gets the sum.
 __device__ __forceinline__ int scan256(int v, int *s_tmp, int *total) {
@@ -554,17 +512,17 @@ struct PairArgs {
   int routed_blocks;
 };
 
-// LDS bytes of select_gate_up_kernel: the token row, then wave 0's
-// selection scratch; shared down tiles reuse the area for their activations.
+// LDS bytes of select_gate_up_kernel: the token row, then each of the four
+// waves' selection scratch and choice; shared down tiles reuse the area for
+// their activations.
 __host__ __device__ constexpr size_t pair_gate_up_lds_bytes(int d, int EPL) {
-  return (size_t)lds_row_stride(d) * 2 + (size_t)(64 * EPL + 256) * 4;
+  return (size_t)lds_row_stride(d) * 2 + (size_t)4 * (64 * EPL + 256 + 64) * 4;
 }
 
 template <int EPL, int CPW, int CPW_S>
 __global__ __launch_bounds__(256) void select_gate_up_kernel(PairArgs a, SharedArgs sh) {
   extern __shared__ __attribute__((aligned(16))) uint16_t s_dyn[];
   __shared__ glm_f32x4 red[3 * 2 * 64];
-  __shared__ int s_sel[kPairMaxK];
   if ((int)blockIdx.x >= a.routed_blocks) {
     shared_down_tile<CPW_S>(sh, blockIdx.x - a.routed_blocks, s_dyn);
     return;
@@ -577,45 +535,27 @@ __global__ __launch_bounds__(256) void select_gate_up_kernel(PairArgs a, SharedA
   const int pr = blockIdx.x / tiles;  // pair t*k + j
   const int t = pr / k, j = pr % k;
   const bool first = j == 0 && tile == 0;  // one block per token publishes the route
+  // Each wave stages the K range of token t's row that it multiplies and
+  // selects the token's experts itself (moe.py:39-62; every wave reaches the
+  // same choice), so no block barrier stands between the route and the
+  // weight loads.  Wave 0 of one block per token publishes the route.
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
   uint16_t *s_x = s_dyn;  // token t's row
-  if (a.n_group == 1 && E <= 256) {
-    // all waves rank the experts; the token row is staged meanwhile
-    __shared__ long long s_key[256];
-    __shared__ float s_score[256];
-    __shared__ int s_cnt[256];
-    __shared__ float s_wsel[kPairMaxK];
-    const glm_u32x4 *src = reinterpret_cast<const glm_u32x4 *>(a.x + (size_t)t * d);
-    for (int i = threadIdx.x; i < d / 8; i += blockDim.x)
-      reinterpret_cast<glm_u32x4 *>(s_x)[i] = src[i];
-    select_ranked(a.logits + (size_t)t * E, a.bias, E, k, s_key, s_score, s_cnt, s_sel, s_wsel);
-    if (first && wave == 0) {
-      // every lane forms the same sequential sum (moe.py:53-57); lane j < k writes column j
-      const float wl = lane < k ? s_wsel[lane] : 0.0f;
-      float total = 0.0f;
-      if (a.norm)
-        for (int jj = 0; jj < k; ++jj)
-          total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), jj));
-      if (lane < k) {
-        a.weights[(size_t)t * k + lane] = (a.norm ? wl / (total + 1e-20f) : wl) * a.scale;
-        a.indices[(size_t)t * k + lane] = (uint32_t)s_sel[lane];
-      }
-    }
-  } else {
-    if (wave > 0) {  // waves 1-3 stage the token row while wave 0 selects
-      const glm_u32x4 *src = reinterpret_cast<const glm_u32x4 *>(a.x + (size_t)t * d);
-      for (int i = threadIdx.x - 64; i < d / 8; i += blockDim.x - 64)
-        reinterpret_cast<glm_u32x4 *>(s_x)[i] = src[i];
-    } else {
-      float *scratch = reinterpret_cast<float *>(s_dyn + lds_row_stride(d));
-      select_token<EPL>(a.logits + (size_t)t * E, a.bias, E, k, a.n_group, a.topk_group, a.norm,
-                        a.scale, first ? a.weights + (size_t)t * k : nullptr,
-                        first ? a.indices + (size_t)t * k : nullptr, s_sel, scratch, lane);
-    }
-    __syncthreads();
+  {
+    const glm_u32x4 *src = reinterpret_cast<const glm_u32x4 *>(a.x + (size_t)t * d + wv * CPW * 128);
+    glm_u32x4 *dst = reinterpret_cast<glm_u32x4 *>(s_x + wv * CPW * 128);
+    for (int i = lane; i < CPW * 16; i += 64) dst[i] = src[i];
   }
-  const long long e = s_sel[j];
+  float *scratch = reinterpret_cast<float *>(s_dyn + lds_row_stride(d)) + wv * (64 * EPL + 256 + 64);
+  int *s_selw = reinterpret_cast<int *>(scratch + 64 * EPL + 256);
+  const bool publish = first && wv == 0;
+  select_token<EPL>(a.logits + (size_t)t * E, a.bias, E, k, a.n_group, a.topk_group, a.norm,
+                    a.scale, publish ? a.weights + (size_t)t * k : nullptr,
+                    publish ? a.indices + (size_t)t * k : nullptr, s_selw, scratch, lane);
+  wave_lds_sync();  // the staged row and the choice, for this wave
+  const long long e = s_selw[j];
   const int row0 = tile * 16;
-  const int kbase = wave * CPW * 128;
+  const int kbase = wv * CPW * 128;
   const uint8_t *wrow[2] = {a.gw + e * a.w_stride + (size_t)(row0 + r) * (d / 2),
                             a.uw + e * a.w_stride + (size_t)(row0 + r) * (d / 2)};
   const uint8_t *srow[2] = {a.gs + e * a.s_stride + (size_t)(row0 + r) * (d / 32),
