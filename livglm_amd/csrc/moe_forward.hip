@@ -34,7 +34,10 @@ int glm_router_validate(const void *x, int T, int d, const void *weight, const v
                         const void *indices);
 int glm_router_launch(hipStream_t stream, const uint16_t *x, int T, int d, const float *weight,
                       const float *bias, int E, int k, int n_group, int topk_group, int norm,
-                      float scale, float *logits, float *weights, uint32_t *indices);
+                      float scale, float *logits, float *weights, uint32_t *indices,
+                      uint16_t *wsplit);
+bool glm_router_split_supported(int T, int d);
+size_t glm_router_split_bytes(int E, int d);
 int glm_dispatch_launch(hipStream_t stream, const uint32_t *indices, int T, int k, int E,
                         int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
                         int32_t *pair_token, int32_t *active, int32_t *num_active, int4 *work,
@@ -130,6 +133,7 @@ struct Workspace {
   void *h_split;
   float *gp, *up;  // decode shared-expert gate/up partials [skq][T][Is]
   float *yp;       // decode shared-expert down partials [skd][T][d]
+  uint16_t *router_split;  // many tokens: the router weights split into three bf16 parts
   size_t bytes;
 };
 
@@ -173,6 +177,8 @@ Workspace carve(char *base, int T, int d, int E, int k, int I, int Is) {
   w.gp = (float *)take(tis * skq);
   w.up = (float *)take(tis * skq);
   w.yp = (float *)take((size_t)T * (Is > 0 ? d : 0) * 4 * skd);
+  w.router_split =
+      (uint16_t *)take(glm_router_split_supported(T, d) ? glm_router_split_bytes(E, d) : 0);
   w.bytes = off;
   return w;
 }
@@ -294,7 +300,8 @@ extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
     return glm_combine_launch(stream, w.y, w.inv, wts, shared_ready, T, top_k, d, out);
   }
   rc = glm_router_launch(stream, x, T, d, router_weight, router_bias, E, top_k, n_group,
-                         topk_group, norm_topk_prob, routed_scaling_factor, w.logits, wts, idx);
+                         topk_group, norm_topk_prob, routed_scaling_factor, w.logits, wts, idx,
+                         w.router_split);
   if (rc) return rc;
   // general path: dispatch, then the grouped MFMA GEMMs over row tiles when
   // the shape allows, else the tiled GEMV kernels over the work list

@@ -145,6 +145,103 @@ __global__ __launch_bounds__(64 * KSPLIT) void router_gemm_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Logits for many tokens on bf16 MFMA.  The f32 router weights are first split
+// exactly into three bf16 parts, w = w0 + w1 + w2 (w0 = bf16(w), w1 =
+// bf16(w - w0), w2 = w - w0 - w1; the f32 significand's 24 bits fit three
+// bf16 significands), so x . w = x . w0 + x . w1 + x . w2 with every product
+// exact (bf16 x bf16) and f32 accumulation: the f32 dot product up to the
+// summation order, at the bf16 MFMA rate (a 32-wide K step is three bf16
+// MFMAs per tile instead of eight f32 ones).
+// Workgroup = 64 tokens x 32 experts (4 x 2 tiles), 8 waves split K; each
+// wave keeps the next step's operands in flight, and the partial sums are
+// added in wave order through LDS, one tile per wave.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void router_weight_split_kernel(const float *__restrict__ w,
+                                                                  long long n,
+                                                                  uint16_t *__restrict__ ws) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float v = w[i];
+  const uint32_t b0 = f32_to_bf16(v);
+  const float r1 = v - bf16_to_f32(b0);
+  const uint32_t b1 = f32_to_bf16(r1);
+  const float r2 = r1 - bf16_to_f32(b1);
+  ws[i] = (uint16_t)b0;
+  ws[n + i] = (uint16_t)b1;
+  ws[2 * n + i] = (uint16_t)f32_to_bf16(r2);
+}
+
+constexpr int kSplitRouterWaves = 8;
+
+__global__ __launch_bounds__(64 * kSplitRouterWaves) void router_gemm_bf16x3_kernel(
+    const uint16_t *__restrict__ x, const uint16_t *__restrict__ ws, int T, int d, int E,
+    float *__restrict__ logits) {
+  __shared__ glm_f32x4 red[kSplitRouterWaves][8][64];  // [wave][tile][lane], 64 KB
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, q = lane >> 4;
+  const int t0 = blockIdx.x * 64;
+  const int e0 = blockIdx.y * 32;
+  const int kq = d / kSplitRouterWaves;  // this wave's K range, a multiple of 64
+  const int kb = wave * kq + 8 * q;
+  const size_t plane = (size_t)E * d;
+  const uint16_t *xr[4], *wr[2];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) xr[tt] = x + (size_t)min(t0 + 16 * tt + r, T - 1) * d + kb;
+#pragma unroll
+  for (int et = 0; et < 2; ++et) wr[et] = ws + (size_t)min(e0 + 16 * et + r, E - 1) * d + kb;
+  glm_f32x4 acc[4][2];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int et = 0; et < 2; ++et) acc[tt][et] = glm_f32x4{0.f, 0.f, 0.f, 0.f};
+  // operands of a 32-wide K step: 4 token fragments, 2 x 3 weight fragments
+  auto load = [&](int k0, glm_bf16x8 xa[4], glm_bf16x8 wb[2][3]) {
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) xa[tt] = *reinterpret_cast<const glm_bf16x8 *>(xr[tt] + k0);
+#pragma unroll
+    for (int et = 0; et < 2; ++et)
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+        wb[et][p] = *reinterpret_cast<const glm_bf16x8 *>(wr[et] + p * plane + k0);
+  };
+  glm_bf16x8 xa[2][4], wb[2][2][3];
+  load(0, xa[0], wb[0]);
+  for (int k0 = 0; k0 < kq; k0 += 64) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int kn = k0 + 32 * (h + 1);
+      if (kn < kq) load(kn, xa[h ^ 1], wb[h ^ 1]);
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+          for (int et = 0; et < 2; ++et)
+            acc[tt][et] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[h][tt], wb[h][et][p],
+                                                                  acc[tt][et], 0, 0, 0);
+    }
+  }
+  // wave w adds tile w of every wave in wave order
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int et = 0; et < 2; ++et) red[wave][tt * 2 + et][lane] = acc[tt][et];
+  __syncthreads();
+  const int tile = wave, tt = tile >> 1, et = tile & 1;
+  glm_f32x4 sum = red[0][tile][lane];
+#pragma unroll
+  for (int w = 1; w < kSplitRouterWaves; ++w) sum += red[w][tile][lane];
+  // lane (r, q) holds tokens 4q..4q+3 of the tile for expert e0 + 16 et + r
+  const int e = e0 + 16 * et + r;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int t = t0 + 16 * tt + 4 * q + m;
+    if (t < T && e < E) logits[(size_t)t * E + e] = sum[m];
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Selection: one wave per token (select_token), four tokens per workgroup.
 // ---------------------------------------------------------------------------
 template <int EPL>
@@ -216,12 +313,29 @@ int glm_router_select_launch(hipStream_t stream, const float *logits, const floa
   return GLM_OK;
 }
 
+// Whether the bf16-split router GEMM covers this call (it needs
+// glm_router_split_bytes of scratch for the split weights).
+bool glm_router_split_supported(int T, int d) {
+  return T >= 256 && d % (64 * glm::kSplitRouterWaves) == 0;
+}
+
+size_t glm_router_split_bytes(int E, int d) { return (size_t)3 * E * d * 2; }
+
 int glm_router_launch(hipStream_t stream, const uint16_t *x, int T, int d, const float *weight,
                       const float *bias, int E, int k, int n_group, int topk_group, int norm,
-                      float scale, float *logits, float *weights, uint32_t *indices) {
+                      float scale, float *logits, float *weights, uint32_t *indices,
+                      uint16_t *wsplit) {
   using namespace glm;
   if (T == 0) return GLM_OK;
-  if (glm_router_gemm_supported(T, d)) {
+  if (wsplit != nullptr && glm_router_split_supported(T, d)) {
+    const long long n = (long long)E * d;
+    hipLaunchKernelGGL(router_weight_split_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       stream, weight, n, wsplit);
+    GLM_LAUNCH_CHECK("router_weight_split_kernel");
+    const dim3 grid((T + 63) / 64, (E + 31) / 32);
+    hipLaunchKernelGGL(router_gemm_bf16x3_kernel, grid, dim3(64 * kSplitRouterWaves), 0, stream, x,
+                       wsplit, T, d, E, logits);
+  } else if (glm_router_gemm_supported(T, d)) {
     const int rc = glm_router_logits_launch(stream, x, T, d, weight, E, logits);
     if (rc) return rc;
   } else if (T <= 2) {
@@ -271,5 +385,5 @@ extern "C" int glm_router_topk(void *stream, const uint16_t *x, int T, int d, co
               "router: logits buffer is required by this entry point");
   return glm_router_launch((hipStream_t)stream, x, T, d, weight, bias, E, top_k, n_group,
                            topk_group, norm_topk_prob, routed_scaling_factor, logits, weights,
-                           indices);
+                           indices, nullptr);
 }

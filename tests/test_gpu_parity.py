@@ -364,8 +364,10 @@ def test_grouped_expert_gemms_parity(gu):
 def test_moe_forward_grouped_equals_public_composition(gu):
     # glm_moe_forward's grouped path (multi-workgroup dispatch, h split fused
     # into the gate/up epilogue) must equal, bit for bit, the public entry
-    # points composed by hand: router, dispatch, tiles, x split, gate/up to
-    # bf16 h, split of h, down, combine
+    # points composed by hand on the forward's own route: dispatch, tiles, x
+    # split, gate/up to bf16 h, split of h, down, combine.  Its route (bf16
+    # MFMA on the f32 router weights split three ways) is checked against the
+    # oracle's.
     torch = _torch()
     shape = MoEShape("grouped", 400, 1024, 32, 4, 256, 0)
     layer = make_layer(shape, 1718)
@@ -375,19 +377,25 @@ def test_moe_forward_grouped_equals_public_composition(gu):
     lib = native.load()
     ws_bytes = lib.glm_moe_workspace_bytes(T, d, E, k, I, 0)
     ws = gu.workspace(ws_bytes)
-    out = torch.empty((T, d), dtype=torch.float32, device="cuda")
+    f32 = dict(dtype=torch.float32, device="cuda")
+    i32 = dict(dtype=torch.int32, device="cuda")
+    out = torch.empty((T, d), **f32)
+    wts, idx = torch.empty((T, k), **f32), torch.empty((T, k), **i32)
     gu.call("glm_moe_forward", gu.stream(), gu.p(dl["x"]), T, d, gu.p(dl["router_weight"]),
             gu.p(dl["router_bias"]), E, k, 1, 1, 1, shape.routed_scaling_factor, I,
             *(gu.p(dl[key]) for key in BANK_KEYS), 0, native.GLM_FMT_BF16, None, None, None,
-            None, None, None, None, shape.swiglu_limit, gu.p(ws), ws_bytes, gu.p(out), None,
-            None)
-    f32 = dict(dtype=torch.float32, device="cuda")
-    i32 = dict(dtype=torch.int32, device="cuda")
-    logits, wts = torch.empty((T, E), **f32), torch.empty((T, k), **f32)
-    idx = torch.empty((T, k), **i32)
-    gu.call("glm_router_topk", gu.stream(), gu.p(dl["x"]), T, d, gu.p(dl["router_weight"]),
-            gu.p(dl["router_bias"]), E, k, 1, 1, 1, shape.routed_scaling_factor, gu.p(logits),
-            gu.p(wts), gu.p(idx))
+            None, None, None, None, shape.swiglu_limit, gu.p(ws), ws_bytes, gu.p(out), gu.p(wts),
+            gu.p(idx))
+    # the forward's route against the oracle's: same experts wherever the
+    # top-k margin is clear, weights to f32 rounding
+    _, w_want, i_want, choice = O.router(O.bf16_bits_to_f32(layer["x"]), layer["router_weight"],
+                                         layer["router_bias"], top_k=k, n_group=1, topk_group=1,
+                                         norm_topk_prob=True,
+                                         routed_scaling_factor=shape.routed_scaling_factor)
+    got_i = gu.host(idx).astype(np.uint32)
+    assert _check_indices(got_i, i_want, choice, k) <= max(1, T // 100)
+    same = np.all(got_i == i_want, axis=1)
+    np.testing.assert_allclose(gu.host(wts)[same], w_want[same], rtol=2e-6, atol=1e-7)
     b = {n: torch.empty((s,), **i32) for n, s in
          [("counts", E), ("offsets", E + 1), ("perm", P), ("inv", P), ("tok", P), ("active", E),
           ("num_active", 1), ("work", 4 * E), ("status", 1)]}
