@@ -248,8 +248,8 @@ class Setup:
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; multi-GPU runs are not part of "
-                                   "it (DESIGN.md describes how the layer would shard by expert)",
+        print(json.dumps({"error": "this benchmark runs the MoE layer on one GPU; runs over "
+                                   "several GPUs (the layer sharded by expert) are not supported",
                           "n_gpus": args.gpus}))
         return 2
 

@@ -146,12 +146,13 @@ __global__ __launch_bounds__(64 * KSPLIT) void router_gemm_kernel(
 
 // ---------------------------------------------------------------------------
 // Logits for many tokens on bf16 MFMA.  The f32 router weights are first split
-// exactly into three bf16 parts, w = w0 + w1 + w2 (w0 = bf16(w), w1 =
-// bf16(w - w0), w2 = w - w0 - w1; the f32 significand's 24 bits fit three
-// bf16 significands), so x . w = x . w0 + x . w1 + x . w2 with every product
-// exact (bf16 x bf16) and f32 accumulation: the f32 dot product up to the
-// summation order, at the bf16 MFMA rate (a 32-wide K step is three bf16
-// MFMAs per tile instead of eight f32 ones).
+// into three bf16 parts, w = w0 + w1 + w2 (w0 = bf16(w), w1 = bf16(w - w0),
+// w2 = bf16(w - w0 - w1); the f32 significand's 24 bits fit three bf16
+// significands, exactly for 2^-100 <= |w| < 2^127 and to within 2^-133 below),
+// so x . w = x . w0 + x . w1 + x . w2 with every product exact (bf16 x bf16)
+// and f32 accumulation: the f32 dot product up to the summation order, at the
+// bf16 MFMA rate (a 32-wide K step is three bf16 MFMAs per tile instead of
+// eight f32 ones).
 // Workgroup = 64 tokens x 32 experts (4 x 2 tiles), 8 waves split K; each
 // wave keeps the next step's operands in flight, and the partial sums are
 // added in wave order through LDS, one tile per wave.

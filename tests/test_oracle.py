@@ -487,3 +487,28 @@ def test_c_restatement_mxfp8_linear(cpu_twin):
     assert np.mean(got == want) > 0.95
     with pytest.raises(ValueError):
         cpu_twin.linear_mxfp8(x[:, :128], codes, scales)
+
+
+def test_three_way_bf16_split_of_f32_is_exact():
+    # the many-token router GEMM multiplies x by w0, w1 and w2 with
+    # w0 = bf16(w), w1 = bf16(w - w0), w2 = bf16(w - w0 - w1) (round to nearest
+    # even) and adds the products in f32; that equals x . w up to f32
+    # summation order when w0 + w1 + w2 == w.  Exact for 2^-100 <= |w| <
+    # 2^127 (the remainders stay normal bf16 numbers); below, the error is
+    # under 2^-133, far under any f32 logit's resolution.
+    rng = np.random.default_rng(91)
+    w = np.concatenate([rng.normal(0, 0.02, 200000), rng.normal(0, 1, 50000),
+                        rng.uniform(-1e30, 1e30, 1000),
+                        np.ldexp(rng.uniform(1, 2, 2000), rng.integers(-100, 127, 2000)),
+                        [0.0, -0.0, 1.0, -1.0]]).astype(np.float32)
+    tiny = np.ldexp(rng.uniform(-1, 1, 2000), rng.integers(-149, -100, 2000)).astype(np.float32)
+
+    def split(v):
+        w0 = O.bf16_round(v)
+        r1 = (v - w0).astype(np.float32)
+        w1 = O.bf16_round(r1)
+        w2 = O.bf16_round((r1 - w1).astype(np.float32))
+        return w0.astype(np.float64) + w1.astype(np.float64) + w2.astype(np.float64)
+
+    assert np.array_equal(split(w), w.astype(np.float64))
+    assert np.max(np.abs(split(tiny) - tiny.astype(np.float64))) < 2.0 ** -133
