@@ -350,11 +350,21 @@ __global__ __launch_bounds__(kRouteThreads) void select_dispatch_kernel(RouteArg
     a.status[0] = 0;
   }
   __syncthreads();
+  // The work slots go busiest expert first (ties by expert id): the routed
+  // kernels' workgroups run in slot order, and a popular expert's tiles, which
+  // loop over several token batches, would otherwise start last and set the
+  // launch's tail.  `active` stays ascending.
   for (int u = threadIdx.x; u < E; u += kRouteThreads) {
     if (u < tot_act) {
       const int ee = s_active[u];
+      const int c = cnt[ee];
+      int slot = 0;
+      for (int v = 0; v < tot_act; ++v) {
+        const int cv = cnt[s_active[v]];
+        slot += (cv > c || (cv == c && v < u)) ? 1 : 0;
+      }
       a.active[u] = ee;
-      a.work[u] = make_int4(ee, off[ee], cnt[ee], 0);
+      a.work[slot] = make_int4(ee, off[ee], c, 0);
     } else {
       a.active[u] = -1;
       a.work[u] = make_int4(-1, 0, 0, 0);
