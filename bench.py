@@ -49,7 +49,8 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--workload", default="verify_t2",
-                    help="decode_t1 | verify_t2 | batch_t64")
+                    help="decode_t1 | verify_t2 | batch_t64 | prefill_t4096 | stack42_t1 | "
+                         "bank_load")
     ap.add_argument("--min-rotation-gb", type=float, default=4.0,
                     help="total size of the distinct layer banks the steps rotate over")
     ap.add_argument("--kernel-launches", type=int, default=128)
@@ -58,6 +59,10 @@ def parse_args():
     ap.add_argument("--traffic", type=int, default=1,
                     help="1: measure the dominant kernel's HBM traffic with rocprofv3 counters")
     ap.add_argument("--seed", type=int, default=5301)
+    ap.add_argument("--load-layers", type=int, default=8,
+                    help="bank_load: layers of the synthetic checkpoint (320 MB each)")
+    ap.add_argument("--load-threads", type=int, default=16,
+                    help="bank_load: native read threads")
     # internal: the child runs of the counter passes
     ap.add_argument("--mode", default="full", choices=["full", "kernel", "copy"],
                     help=argparse.SUPPRESS)
@@ -261,6 +266,8 @@ def main() -> int:
         return 1
     if args.mode == "copy":
         return copy_probe(torch)
+    if args.workload == "bank_load":
+        return bank_load_bench(args, torch, np)
     S = Setup(args, torch, np)
     R = args.kernel_launches
     S.kernel_plans(R)
@@ -449,6 +456,170 @@ def roofline(S, achieved, tflops, bytes_per_launch, k_ms, R, traffic, traffic_no
                                          " (routed MXFP4 gate/up + SwiGLU)"),
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4), **common}
+
+
+def bank_load_bench(args, torch, np) -> int:
+    """Checkpoint shards -> HBM banks: writes a synthetic routed-expert
+    checkpoint at the verify_t2 geometry (one 320 MB shard per layer), then
+    loads every layer into its own HBM bank twice -- from the page cache
+    (``value``) and after the shards' pages were dropped (``cold_gbps``, the
+    storage's rate).  The device side's kernel, the scatter of staged records
+    into the bank tensors, is timed with HIP events on its stream."""
+    from glm53flash.bank_loader import ExpertBankLoader
+    from glm53flash.contract import ModelContract
+    from glm53flash.expert_source import build_native_expert_source_plan
+    from glm53flash.expert_ssd import HBMExpertBank
+    from glm53flash.model_config import GLMTextConfig
+    from livglm_amd import native
+    from livglm_amd.workloads import SHAPES, write_expert_checkpoint
+
+    shape = SHAPES["verify_t2"]
+    layers = list(range(3, 3 + max(1, args.load_layers)))
+    chunk = 256 << 20
+    root = tempfile.mkdtemp(prefix="glm_ckpt_", dir=os.environ.get("TMPDIR", "/tmp"))
+    try:
+        t0 = time.perf_counter()
+        payload = write_expert_checkpoint(root, shape, layers, args.seed)
+        print(f"bank_load: wrote {payload / 1e9:.2f} GB in {time.perf_counter() - t0:.1f} s",
+              file=sys.stderr, flush=True)
+        cfg = GLMTextConfig(hidden_size=shape.d, moe_intermediate_size=shape.I,
+                            n_routed_experts=shape.E)
+        plan = build_native_expert_source_plan(ModelContract.from_model_dir(root), cfg,
+                                               first_layer=layers[0], last_layer=layers[-1])
+        banks = [HBMExpertBank(layer=l, num_experts=shape.E, hidden_size=shape.d,
+                               intermediate_size=shape.I, swiglu_limit=shape.swiglu_limit,
+                               device="cuda") for l in layers]
+        loader = ExpertBankLoader(plan, threads=args.load_threads, chunk_bytes=chunk)
+        loader.load(banks[0])  # staging allocation, first touch of the banks
+
+        def load_all():
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            stats = [loader.load(b) for b in banks]
+            torch.cuda.synchronize()
+            return time.perf_counter() - t, stats
+
+        warm_s, stats = load_all()
+        print(f"bank_load: page cache -> HBM {payload / warm_s / 1e9:.2f} GB/s", file=sys.stderr,
+              flush=True)
+        shards = sorted({r.shard_name for p in plan.packs for r in p.read_ranges})
+
+        def drop_pages():
+            for shard in shards:
+                fd = os.open(os.path.join(root, shard), os.O_RDONLY)
+                try:
+                    os.fsync(fd)
+                    os.posix_fadvise(fd, 0, 0, os.POSIX_FADV_DONTNEED)
+                finally:
+                    os.close(fd)
+
+        for b in banks:  # the cold pass must refill, not find the right bytes already there
+            for t in b.tensors.values():
+                t.zero_()
+        drop_pages()
+        cold_s, _ = load_all()
+        print(f"bank_load: storage -> HBM {payload / cold_s / 1e9:.2f} GB/s", file=sys.stderr,
+              flush=True)
+        # every slot of the first and the last layer against the shard bytes
+        blob = np.fromfile(os.path.join(root, shards[0]), dtype=np.uint8,
+                           offset=plan.expert(layers[0], 0).read_ranges[0].absolute_offset)
+        blob = blob[:shape.E * shape.expert_bytes].reshape(shape.E, shape.expert_bytes)
+        checked = 0
+        for b in (banks[0], banks[-1]):
+            for t in plan.expert(b.layer, 0).tensors:
+                rel = t.absolute_offset - plan.expert(b.layer, 0).read_ranges[0].absolute_offset
+                want = blob[:, rel:rel + t.byte_length]
+                got = b.tensors[t.bank_name].cpu().numpy().reshape(shape.E, -1)
+                if not np.array_equal(got, want):
+                    raise SystemExit(f"bank_load: layer {b.layer} {t.bank_name} differs")
+                checked += want.size
+        # host side alone: the native reader into pinned memory
+        host = torch.empty(chunk, dtype=torch.uint8, pin_memory=True)
+        rng0 = plan.expert(layers[0], 0).read_ranges[0].absolute_offset
+        n_read = min(chunk, shape.E * shape.expert_bytes)
+        offs = np.array([rng0], dtype=np.int64)
+        lens = np.array([n_read], dtype=np.int64)
+        ptrs = np.array([host.data_ptr()], dtype=np.uint64)
+        path = os.path.join(root, shards[0]).encode()
+        native.call("glm_file_read_ranges", path, 1, offs.ctypes.data, lens.ctypes.data,
+                    ptrs.ctypes.data, args.load_threads, 0)
+        t = time.perf_counter()
+        for _ in range(4):
+            native.call("glm_file_read_ranges", path, 1, offs.ctypes.data, lens.ctypes.data,
+                        ptrs.ctypes.data, args.load_threads, 0)
+        read_gbps = 4 * n_read / (time.perf_counter() - t) / 1e9
+        # host -> device link: pinned staging to device staging
+        dev = torch.empty(chunk, dtype=torch.uint8, device="cuda")
+        stream = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        dev.copy_(host, non_blocking=True)
+        e0.record(stream)
+        for _ in range(4):
+            dev.copy_(host, non_blocking=True)
+        e1.record(stream)
+        e1.synchronize()
+        h2d_gbps = 4 * chunk / (e0.elapsed_time(e1) / 1e3) / 1e9
+        # the scatter kernel alone: the first 96 experts of a staged layer
+        # (one 240 MB chunk) into bank 0, 8 launches between HIP events
+        n_exp = min(shape.E, chunk // shape.expert_bytes)
+        segs = []
+        for e in range(n_exp):
+            for tns in plan.expert(layers[0], e).tensors:
+                rel = tns.absolute_offset - rng0
+                bank_t = banks[0].tensors[tns.bank_name]
+                segs.append((rel, bank_t.data_ptr() + e * (bank_t.numel() // shape.E),
+                             tns.byte_length))
+        table = np.array(segs, dtype=np.int64)
+        dtab = torch.empty(table.size, dtype=torch.int64, device="cuda")
+        staged = n_exp * shape.expert_bytes
+        args_s = (stream.cuda_stream, dev.data_ptr(), staged, table.ctypes.data, len(segs),
+                  dtab.data_ptr())
+        native.call("glm_bank_scatter", *args_s)
+        e0.record(stream)
+        launches = 8
+        for _ in range(launches):
+            native.call("glm_bank_scatter", *args_s)
+        e1.record(stream)
+        e1.synchronize()
+        k_s = e0.elapsed_time(e1) / 1e3 / launches
+        moved = 2 * staged  # each byte read once and written once
+        achieved = moved / k_s / 1e9
+        loader.close()
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+    line = {
+        "metric": "expert bank load GB/s (checkpoint shards -> HBM-resident expert banks)",
+        "value": round(payload / warm_s / 1e9, 3),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": len(layers),
+        "warmup": 1,
+        "ms_per_step": round(warm_s * 1e3 / len(layers), 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"bank_load: {len(layers)} layers x {shape.E} experts x "
+                         f"{shape.expert_bytes} B (MXFP4 d={shape.d} I={shape.I}), one "
+                         f"safetensors shard per layer, read from the page cache"),
+            "payload_bytes": payload, "read_threads": args.load_threads, "chunk_bytes": chunk,
+            "reads_per_layer": stats[0].reads, "chunks_per_layer": stats[0].chunks,
+            "verified_bytes": checked,
+        },
+        "cold_gbps": round(payload / cold_s / 1e9, 3),
+        "host_read_gbps": round(read_gbps, 3),
+        "h2d_gbps": round(h2d_gbps, 3),
+        "roofline": {"kernel": "bank_scatter_kernel (staged records -> bank slots)",
+                     "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "bytes_per_launch": moved, "avg_launch_us": round(k_s * 1e6, 3),
+                     "launches": launches},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line))
+    return 0
 
 
 def copy_probe(torch) -> int:

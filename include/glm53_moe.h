@@ -289,6 +289,38 @@ int glm_moe_forward(void *stream, const uint16_t *x, int T, int d, const float *
                     size_t workspace_bytes, float *out, float *weights_out,
                     uint32_t *indices_out);
 
+/* ------------------------------------------------------------ expert bank loading */
+
+/* glm_file_read_ranges flag: drop the file's page-cache pages of the ranges
+ * after reading them (the intent of the reference's no_file_cache option,
+ * native_expert_ssd.py:102,337). */
+#define GLM_READ_DROP_CACHE 1
+
+/*
+ * Reads n byte ranges of one file into host memory: dst[i] receives bytes
+ * [offset[i], offset[i] + length[i]).  `threads` worker threads (1..256) pread
+ * pieces of at most 8 MiB.  Replaces the file side of the reference's direct
+ * expert reader, mx._open_expert_safetensors_direct (native_expert_ssd.py:
+ * 320-339) + mx._expert_ssd_direct_load_into (native_expert_ssd.py:379-385).
+ * Host-only: no GPU call.  Fails (GLM_ERR_INVALID_ARGUMENT) on an unreadable
+ * file, a range past its end or a short read.
+ */
+int glm_file_read_ranges(const char *path, int n, const int64_t *offset, const int64_t *length,
+                         void *const *dst, int threads, int flags);
+
+/*
+ * Moves n segments out of a device staging buffer on `stream`: segments is a
+ * HOST table int64 [n][3] of {source offset in staging, destination device
+ * address, bytes}; it is validated against staging_bytes and copied to
+ * device_table (device memory of at least 24 n bytes, owned by the caller and
+ * kept until the stream has run the copy).  Replaces the device side of
+ * mx._expert_ssd_direct_load_into (native_expert_ssd.py:379-385), which wrote
+ * one expert's six tensors into its slot (allocate_slots,
+ * native_expert_ssd.py:352-363); here one launch fills many experts' slots.
+ */
+int glm_bank_scatter(void *stream, const uint8_t *staging, int64_t staging_bytes,
+                     const int64_t *segments, int n, int64_t *device_table);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,6 +26,8 @@ GLM_FMT_MXFP4 = 2
 GLM_MX_RULE_NEAREST = 0
 GLM_MX_RULE_OCP = 1
 
+GLM_READ_DROP_CACHE = 1
+
 ABI_VERSION = 1
 
 _p = ctypes.c_void_p
@@ -62,6 +64,8 @@ SIGNATURES = {
     "glm_moe_forward": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _i, _f, _i,
                              _p, _p, _p, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p, _p, _p,
                              _f, _p, _sz, _p, _p, _p]),
+    "glm_file_read_ranges": (_i, [ctypes.c_char_p, _i, _p, _p, _p, _i, _i]),
+    "glm_bank_scatter": (_i, [_p, _p, _i64, _p, _i, _p]),
 }
 
 

@@ -131,3 +131,48 @@ def make_layer(shape: MoEShape, seed: int, *, T: int | None = None) -> dict[str,
 
 BANK_KEYS = ("gate_proj.weight_packed", "gate_proj.weight_scale", "up_proj.weight_packed",
              "up_proj.weight_scale", "down_proj.weight_packed", "down_proj.weight_scale")
+
+
+def write_expert_checkpoint(root: str, shape: MoEShape, layers, seed: int) -> int:
+    """Writes a routed-expert checkpoint for ``layers`` (one safetensors shard
+    per layer, experts in id order, each expert's six U8 tensors adjacent in
+    the reference's canonical order) plus ``model.safetensors.index.json`` and
+    ``config.json``.  Every layer stores the same random bank (one layer's
+    bytes drawn once); returns the payload bytes written."""
+    import json
+    import os
+    import struct
+
+    rng = np.random.default_rng(seed)
+    d, I, E = shape.d, shape.I, shape.E
+    parts = []
+    for comp in ("down_proj", "gate_proj", "up_proj"):
+        rows, cols = (d, I) if comp == "down_proj" else (I, d)
+        parts.append((comp, "weight_packed", (rows, cols // 2)))
+        parts.append((comp, "weight_scale", (rows, cols // 32)))
+    record = sum(r * c for _, _, (r, c) in parts)
+    blob = rng.integers(0, 256, E * record, dtype=np.uint8)
+    os.makedirs(root, exist_ok=True)
+    weight_map = {}
+    for layer in layers:
+        header, offset = {}, 0
+        for e in range(E):
+            for comp, part, (r, c) in parts:
+                name = f"model.language_model.layers.{layer}.mlp.experts.{e}.{comp}.{part}"
+                header[name] = {"dtype": "U8", "shape": [r, c],
+                                "data_offsets": [offset, offset + r * c]}
+                offset += r * c
+        raw = json.dumps(header).encode()
+        raw += b" " * (-len(raw) % 8)
+        shard = f"model-layer{layer:02d}.safetensors"
+        with open(os.path.join(root, shard), "wb") as f:
+            f.write(struct.pack("<Q", len(raw)))
+            f.write(raw)
+            blob.tofile(f)
+        weight_map.update({name: shard for name in header})
+    with open(os.path.join(root, "model.safetensors.index.json"), "w") as f:
+        json.dump({"metadata": {}, "weight_map": weight_map}, f)
+    with open(os.path.join(root, "config.json"), "w") as f:
+        json.dump({"text_config": {"hidden_size": d, "moe_intermediate_size": I,
+                                   "n_routed_experts": E}}, f)
+    return len(layers) * E * record

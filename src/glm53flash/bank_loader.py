@@ -1,0 +1,226 @@
+"""Checkpoint shards -> HBM expert banks.
+
+The reference refills a bounded per-layer slot cache from SSD, one expert at a
+time, on a route miss (``native_expert_ssd.py:280-387``: one direct reader per
+shard, ``load_into(expert, slot, destinations)``).  Every expert of a layer is
+resident in HBM here, so a layer is loaded once, in bulk:
+
+1. the layer's per-expert read ranges (one contiguous record per expert in a
+   native checkpoint) are sorted by shard offset and packed into staging
+   chunks; ranges that follow each other in the file become one read;
+2. ``glm_file_read_ranges`` preads a chunk into pinned host memory with a pool
+   of native threads;
+3. one host-to-device copy moves the chunk to device staging, and
+   ``glm_bank_scatter`` moves every tensor of every record to its expert's
+   slot in the stacked bank tensors.
+
+Two chunk buffers alternate, so the threads read chunk c + 1 while the GPU
+copies and scatters chunk c.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+import os
+import time
+
+import numpy as np
+import torch
+
+from . import _native as N
+from .contract import ContractError
+from .expert_source import NativeExpertSourcePlan, expected_shape
+from .expert_ssd import HBMExpertBank
+
+_ALIGN = 256  # staging offset of every read: keeps 16-byte tensors 16-byte aligned
+
+
+@dataclass(frozen=True)
+class BankLoadStats:
+    layer: int
+    experts: int
+    bytes: int          # payload bytes placed in the bank
+    read_bytes: int     # bytes read from the shards
+    reads: int          # pread ranges (after merging adjacent records)
+    chunks: int
+    seconds: float
+
+    @property
+    def gb_per_s(self) -> float:
+        return self.bytes / self.seconds / 1e9 if self.seconds > 0 else float("inf")
+
+
+@dataclass
+class _Read:
+    shard: str
+    offset: int
+    length: int
+    staging: int
+
+
+class ExpertBankLoader:
+    """Loads whole layers of a :class:`NativeExpertSourcePlan` into
+    :class:`HBMExpertBank` objects.  The staging buffers (two pinned host and
+    two device chunks of ``chunk_bytes``) are allocated on first use and kept
+    for later layers; ``close()`` releases them."""
+
+    def __init__(self, plan: NativeExpertSourcePlan, *, threads: int = 16,
+                 chunk_bytes: int = 256 << 20, drop_cache: bool = False):
+        if threads < 1:
+            raise ContractError("the loader needs at least one read thread")
+        if chunk_bytes < _ALIGN:
+            raise ContractError(f"chunk_bytes must be at least {_ALIGN}")
+        self.plan = plan
+        self.threads = int(threads)
+        largest = max((r.byte_length for p in plan.packs for r in p.read_ranges), default=0)
+        # a chunk holds at least the largest single read
+        self.chunk_bytes = max(int(chunk_bytes), _round_up(largest, _ALIGN))
+        self.flags = N.native.GLM_READ_DROP_CACHE if drop_cache else 0
+        self._host: list[torch.Tensor] = []
+        self._dev: list[torch.Tensor] = []
+        self._tables: list[torch.Tensor] = []
+        self._events: list[torch.cuda.Event | None] = []
+        self._keep: list[object] = [None, None]  # host tables in flight per buffer
+
+    def _buffers(self, device: torch.device, segments: int) -> None:
+        if not self._host or self._dev[0].device != device:
+            self._host = [torch.empty(self.chunk_bytes, dtype=torch.uint8, pin_memory=True)
+                          for _ in range(2)]
+            self._dev = [torch.empty(self.chunk_bytes, dtype=torch.uint8, device=device)
+                         for _ in range(2)]
+            self._tables = []
+            self._events = [None, None]
+        if not self._tables or self._tables[0].numel() < 3 * segments:
+            self._tables = [torch.empty(3 * max(segments, 64), dtype=torch.int64, device=device)
+                            for _ in range(2)]
+
+    def close(self) -> None:
+        for ev in self._events:
+            if ev is not None:
+                ev.synchronize()
+        self._host, self._dev, self._tables, self._events = [], [], [], []
+        self._keep = [None, None]
+
+    def _chunks(self, layer: int) -> list[list[tuple[int, object]]]:
+        """The layer's (expert, read range) units in shard-offset order, packed
+        into chunks of at most chunk_bytes staged bytes (one shard per chunk)."""
+        units = [(src.expert, rng) for src in self.plan.layer_sources(layer)
+                 for rng in src.read_ranges]
+        units.sort(key=lambda u: (u[1].shard_name, u[1].absolute_offset))
+        chunks: list[list[tuple[int, object]]] = []
+        used = 0
+        for unit in units:
+            rng = unit[1]
+            size = _round_up(rng.byte_length, _ALIGN)
+            if (not chunks or used + size > self.chunk_bytes
+                    or chunks[-1][-1][1].shard_name != rng.shard_name):
+                chunks.append([])
+                used = 0
+            chunks[-1].append(unit)
+            used += size
+        return chunks
+
+    def load(self, bank: HBMExpertBank, layer: int | None = None) -> BankLoadStats:
+        """Fills every expert slot of ``bank`` from layer ``layer`` (default:
+        ``bank.layer``) of the plan; returns once the bank is complete."""
+        layer = bank.layer if layer is None else layer
+        plan = self.plan
+        if bank.num_experts != plan.experts_per_layer:
+            raise ContractError(f"bank holds {bank.num_experts} experts, the checkpoint layer "
+                                f"{plan.experts_per_layer}")
+        bank._require_active()
+        shapes = bank.shapes()
+        for name, shape in shapes.items():
+            comp, part = name.split(".")
+            want = expected_shape(comp, part, hidden_size=bank.hidden_size,
+                                  intermediate_size=bank.intermediate_size)
+            if tuple(shape[1:]) != want:
+                raise ContractError(f"bank tensor {name} has rows {shape[1:]}, expected {want}")
+        for src in plan.layer_sources(layer):
+            for t in src.tensors:
+                if tuple(t.source_shape) != tuple(shapes[t.bank_name][1:]):
+                    raise ContractError(f"{t.source_name} has shape {t.source_shape}, the bank "
+                                        f"expects {shapes[t.bank_name][1:]}")
+        device = bank.tensors[next(iter(shapes))].device
+        slot_bytes = {name: int(np.prod(shape[1:])) for name, shape in shapes.items()}
+        base = {name: bank.tensors[name].data_ptr() for name in shapes}
+        chunks = self._chunks(layer)
+        self._buffers(device, max((sum(len(r.tensors) for _, r in c) for c in chunks), default=1))
+        stream = torch.cuda.current_stream(device)
+        t0 = time.perf_counter()
+        total = reads_total = 0
+        for c, chunk in enumerate(chunks):
+            slot = c % 2
+            if self._events[slot] is not None:
+                self._events[slot].synchronize()  # buffers of chunk c - 2 are free again
+            # merge records that follow each other in the file into one read
+            reads: list[_Read] = []
+            segments: list[tuple[int, int, int]] = []
+            staged = 0
+            for expert, rng in chunk:
+                if reads and reads[-1].offset + reads[-1].length == rng.absolute_offset:
+                    at = reads[-1].staging + reads[-1].length
+                    reads[-1].length += rng.byte_length
+                    staged = at + rng.byte_length
+                else:
+                    at = _round_up(staged, _ALIGN)
+                    reads.append(_Read(rng.shard_name, rng.absolute_offset, rng.byte_length, at))
+                    staged = at + rng.byte_length
+                for t in rng.tensors:
+                    dst = base[t.bank_name] + expert * slot_bytes[t.bank_name]
+                    segments.append((at + rng.relative_offset(t), dst, t.byte_length))
+                    total += t.byte_length
+            if staged > self.chunk_bytes:
+                raise AssertionError("staging chunk overflow")
+            host = self._host[slot]
+            offsets = np.array([r.offset for r in reads], dtype=np.int64)
+            lengths = np.array([r.length for r in reads], dtype=np.int64)
+            dsts = (np.array([r.staging for r in reads], dtype=np.int64)
+                    + host.data_ptr()).astype(np.uint64)
+            path = os.fspath(plan_shard_path(plan, reads[0].shard))
+            N.call("glm_file_read_ranges", path.encode(), len(reads), offsets.ctypes.data,
+                   lengths.ctypes.data, dsts.ctypes.data, self.threads, self.flags)
+            reads_total += len(reads)
+            dev = self._dev[slot]
+            dev[:staged].copy_(host[:staged], non_blocking=True)
+            table = np.ascontiguousarray(np.array(segments, dtype=np.int64).reshape(-1, 3))
+            N.call("glm_bank_scatter", stream.cuda_stream, dev.data_ptr(), staged,
+                   table.ctypes.data, table.shape[0], self._tables[slot].data_ptr())
+            ev = torch.cuda.Event()
+            ev.record(stream)
+            self._events[slot] = ev
+            self._keep[slot] = table
+        for ev in self._events:
+            if ev is not None:
+                ev.synchronize()
+        seconds = time.perf_counter() - t0
+        read_bytes = sum(r.byte_length for src in plan.layer_sources(layer) for r in src.read_ranges)
+        return BankLoadStats(layer=layer, experts=plan.experts_per_layer, bytes=total,
+                             read_bytes=read_bytes, reads=reads_total, chunks=len(chunks),
+                             seconds=seconds)
+
+
+def plan_shard_path(plan: NativeExpertSourcePlan, shard_name: str) -> str:
+    return os.path.join(plan.model_dir, shard_name)
+
+
+def _round_up(v: int, a: int) -> int:
+    return (v + a - 1) // a * a
+
+
+def load_layer_bank(plan: NativeExpertSourcePlan, layer: int, *, swiglu_limit: float,
+                    hidden_size: int, intermediate_size: int,
+                    device: torch.device | str | None = None,
+                    loader: ExpertBankLoader | None = None) -> HBMExpertBank:
+    """A new :class:`HBMExpertBank` for ``layer`` filled from the checkpoint."""
+    bank = HBMExpertBank(layer=layer, num_experts=plan.experts_per_layer,
+                         hidden_size=hidden_size, intermediate_size=intermediate_size,
+                         swiglu_limit=swiglu_limit, device=device)
+    own = loader is None
+    loader = loader or ExpertBankLoader(plan)
+    try:
+        loader.load(bank)
+    finally:
+        if own:
+            loader.close()
+    return bank
