@@ -475,7 +475,7 @@ def bank_load_bench(args, torch, np) -> int:
 
     shape = SHAPES["verify_t2"]
     layers = list(range(3, 3 + max(1, args.load_layers)))
-    chunk = 256 << 20
+    chunk = 64 << 20
     root = tempfile.mkdtemp(prefix="glm_ckpt_", dir=os.environ.get("TMPDIR", "/tmp"))
     try:
         t0 = time.perf_counter()
@@ -495,7 +495,7 @@ def bank_load_bench(args, torch, np) -> int:
         def load_all():
             torch.cuda.synchronize()
             t = time.perf_counter()
-            stats = [loader.load(b) for b in banks]
+            stats = loader.load_many(banks)
             torch.cuda.synchronize()
             return time.perf_counter() - t, stats
 
@@ -559,8 +559,8 @@ def bank_load_bench(args, torch, np) -> int:
         e1.record(stream)
         e1.synchronize()
         h2d_gbps = 4 * chunk / (e0.elapsed_time(e1) / 1e3) / 1e9
-        # the scatter kernel alone: the first 96 experts of a staged layer
-        # (one 240 MB chunk) into bank 0, 8 launches between HIP events
+        # the scatter kernel alone: the experts of one staged chunk into bank
+        # 0, 8 launches between HIP events
         n_exp = min(shape.E, chunk // shape.expert_bytes)
         segs = []
         for e in range(n_exp):
@@ -605,7 +605,7 @@ def bank_load_bench(args, torch, np) -> int:
                          f"{shape.expert_bytes} B (MXFP4 d={shape.d} I={shape.I}), one "
                          f"safetensors shard per layer, read from the page cache"),
             "payload_bytes": payload, "read_threads": args.load_threads, "chunk_bytes": chunk,
-            "reads_per_layer": stats[0].reads, "chunks_per_layer": stats[0].chunks,
+            "reads": stats.reads, "chunks": stats.chunks,
             "verified_bytes": checked,
         },
         "cold_gbps": round(payload / cold_s / 1e9, 3),

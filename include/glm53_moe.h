@@ -299,7 +299,7 @@ int glm_moe_forward(void *stream, const uint16_t *x, int T, int d, const float *
 /*
  * Reads n byte ranges of one file into host memory: dst[i] receives bytes
  * [offset[i], offset[i] + length[i]).  `threads` worker threads (1..256) pread
- * pieces of at most 8 MiB.  Replaces the file side of the reference's direct
+ * pieces of at most 2 MiB.  Replaces the file side of the reference's direct
  * expert reader, mx._open_expert_safetensors_direct (native_expert_ssd.py:
  * 320-339) + mx._expert_ssd_direct_load_into (native_expert_ssd.py:379-385).
  * Host-only: no GPU call.  Fails (GLM_ERR_INVALID_ARGUMENT) on an unreadable

@@ -24,7 +24,7 @@
 
 namespace glm {
 
-constexpr long long kReadPiece = 8ll << 20;  // one pread call at most
+constexpr long long kReadPiece = 2ll << 20;  // one pread call at most
 constexpr int kScatterThreads = 256;
 constexpr long long kScatterBlockBytes = 64ll << 10;  // bytes per workgroup
 constexpr int kMaxSegmentsPerLaunch = 65535;          // grid.y

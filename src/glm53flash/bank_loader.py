@@ -15,7 +15,8 @@ resident in HBM here, so a layer is loaded once, in bulk:
    slot in the stacked bank tensors.
 
 Two chunk buffers alternate, so the threads read chunk c + 1 while the GPU
-copies and scatters chunk c.
+copies and scatters chunk c; ``load_many`` streams several layers through one
+pipeline, so it drains once, at the end.
 """
 
 from __future__ import annotations
@@ -37,9 +38,9 @@ _ALIGN = 256  # staging offset of every read: keeps 16-byte tensors 16-byte alig
 
 @dataclass(frozen=True)
 class BankLoadStats:
-    layer: int
-    experts: int
-    bytes: int          # payload bytes placed in the bank
+    layers: tuple[int, ...]
+    experts: int        # expert slots filled
+    bytes: int          # payload bytes placed in the banks
     read_bytes: int     # bytes read from the shards
     reads: int          # pread ranges (after merging adjacent records)
     chunks: int
@@ -65,7 +66,7 @@ class ExpertBankLoader:
     for later layers; ``close()`` releases them."""
 
     def __init__(self, plan: NativeExpertSourcePlan, *, threads: int = 16,
-                 chunk_bytes: int = 256 << 20, drop_cache: bool = False):
+                 chunk_bytes: int = 64 << 20, drop_cache: bool = False):
         if threads < 1:
             raise ContractError("the loader needs at least one read thread")
         if chunk_bytes < _ALIGN:
@@ -120,10 +121,7 @@ class ExpertBankLoader:
             used += size
         return chunks
 
-    def load(self, bank: HBMExpertBank, layer: int | None = None) -> BankLoadStats:
-        """Fills every expert slot of ``bank`` from layer ``layer`` (default:
-        ``bank.layer``) of the plan; returns once the bank is complete."""
-        layer = bank.layer if layer is None else layer
+    def _check(self, bank: HBMExpertBank, layer: int) -> None:
         plan = self.plan
         if bank.num_experts != plan.experts_per_layer:
             raise ContractError(f"bank holds {bank.num_experts} experts, the checkpoint layer "
@@ -141,15 +139,38 @@ class ExpertBankLoader:
                 if tuple(t.source_shape) != tuple(shapes[t.bank_name][1:]):
                     raise ContractError(f"{t.source_name} has shape {t.source_shape}, the bank "
                                         f"expects {shapes[t.bank_name][1:]}")
-        device = bank.tensors[next(iter(shapes))].device
-        slot_bytes = {name: int(np.prod(shape[1:])) for name, shape in shapes.items()}
-        base = {name: bank.tensors[name].data_ptr() for name in shapes}
-        chunks = self._chunks(layer)
-        self._buffers(device, max((sum(len(r.tensors) for _, r in c) for c in chunks), default=1))
+
+    def load(self, bank: HBMExpertBank, layer: int | None = None) -> BankLoadStats:
+        """Fills every expert slot of ``bank`` from layer ``layer`` (default:
+        ``bank.layer``) of the plan; returns once the bank is complete."""
+        return self.load_many([bank], None if layer is None else [layer])
+
+    def load_many(self, banks, layers=None) -> BankLoadStats:
+        """Fills each bank from its layer (default: each bank's ``layer``), all
+        layers through one pipeline; returns once every bank is complete."""
+        banks = list(banks)
+        layers = [b.layer for b in banks] if layers is None else list(layers)
+        if len(layers) != len(banks):
+            raise ContractError("one layer per bank")
+        if not banks:
+            return BankLoadStats((), 0, 0, 0, 0, 0, 0.0)
+        for bank, layer in zip(banks, layers):
+            self._check(bank, layer)
+        devices = {b.tensors[next(iter(b.shapes()))].device for b in banks}
+        if len(devices) != 1:
+            raise ContractError("the banks of one load_many call must share a device")
+        (device,) = devices
+        work = []  # (bank base pointers, slot bytes, chunk)
+        for bank, layer in zip(banks, layers):
+            shapes = bank.shapes()
+            slot_bytes = {name: int(np.prod(shape[1:])) for name, shape in shapes.items()}
+            base = {name: bank.tensors[name].data_ptr() for name in shapes}
+            work.extend((base, slot_bytes, chunk) for chunk in self._chunks(layer))
+        self._buffers(device, max(sum(len(r.tensors) for _, r in c) for _, _, c in work))
         stream = torch.cuda.current_stream(device)
         t0 = time.perf_counter()
         total = reads_total = 0
-        for c, chunk in enumerate(chunks):
+        for c, (base, slot_bytes, chunk) in enumerate(work):
             slot = c % 2
             if self._events[slot] is not None:
                 self._events[slot].synchronize()  # buffers of chunk c - 2 are free again
@@ -177,7 +198,7 @@ class ExpertBankLoader:
             lengths = np.array([r.length for r in reads], dtype=np.int64)
             dsts = (np.array([r.staging for r in reads], dtype=np.int64)
                     + host.data_ptr()).astype(np.uint64)
-            path = os.fspath(plan_shard_path(plan, reads[0].shard))
+            path = os.fspath(plan_shard_path(self.plan, reads[0].shard))
             N.call("glm_file_read_ranges", path.encode(), len(reads), offsets.ctypes.data,
                    lengths.ctypes.data, dsts.ctypes.data, self.threads, self.flags)
             reads_total += len(reads)
@@ -194,10 +215,11 @@ class ExpertBankLoader:
             if ev is not None:
                 ev.synchronize()
         seconds = time.perf_counter() - t0
-        read_bytes = sum(r.byte_length for src in plan.layer_sources(layer) for r in src.read_ranges)
-        return BankLoadStats(layer=layer, experts=plan.experts_per_layer, bytes=total,
-                             read_bytes=read_bytes, reads=reads_total, chunks=len(chunks),
-                             seconds=seconds)
+        read_bytes = sum(r.byte_length for layer in layers
+                         for src in self.plan.layer_sources(layer) for r in src.read_ranges)
+        return BankLoadStats(layers=tuple(layers), experts=len(layers) * self.plan.experts_per_layer,
+                             bytes=total, read_bytes=read_bytes, reads=reads_total,
+                             chunks=len(work), seconds=seconds)
 
 
 def plan_shard_path(plan: NativeExpertSourcePlan, shard_name: str) -> str:

@@ -198,7 +198,7 @@ def _read(native, path, offsets, lengths, threads=4, flags=0):
 def test_native_range_reader_reads_exact_bytes(tmp_path):
     native = _lib()
     rng = np.random.default_rng(7)
-    data = rng.integers(0, 256, 20 << 20, dtype=np.uint8)  # 20 MiB: several 8 MiB pieces
+    data = rng.integers(0, 256, 20 << 20, dtype=np.uint8)  # 20 MiB: many 2 MiB pieces
     path = str(tmp_path / "blob.bin")
     data.tofile(path)
     offsets = [0, 3, (8 << 20) - 5, 12345, len(data) - 17, 100]

@@ -43,11 +43,17 @@ def test_loader_fills_every_slot_exactly(gu, tmp_path, misalign):
     plan = _plan(str(tmp_path), E, d, I, layers)
     # three records per chunk: several chunks, both buffers reused
     loader = ExpertBankLoader(plan, threads=4, chunk_bytes=3 * record + 512)
-    for layer in layers:
-        bank = HBMExpertBank(layer=layer, num_experts=E, hidden_size=d, intermediate_size=I,
-                             swiglu_limit=10.0, device="cuda")
-        stats = loader.load(bank)
-        assert stats.bytes == E * record and stats.experts == E and stats.chunks >= 4
+    banks = [HBMExpertBank(layer=layer, num_experts=E, hidden_size=d, intermediate_size=I,
+                           swiglu_limit=10.0, device="cuda") for layer in layers]
+    if misalign:
+        # both layers through one pipeline
+        stats = loader.load_many(banks)
+        assert stats.bytes == len(layers) * E * record and stats.chunks >= 8
+    else:
+        for bank in banks:
+            stats = loader.load(bank)
+            assert stats.bytes == E * record and stats.experts == E and stats.chunks >= 4
+    for layer, bank in zip(layers, banks):
         for comp in COMPONENTS:
             for part in PARTS:
                 got = gu.host(bank.tensors[f"{comp}.{part}"])
