@@ -89,6 +89,9 @@ class Setup:
         self.layer_bytes = shape.bank_bytes + 3 * Is * d * 2 + E * d * 4
         if self.layers > 1:
             self.layer_bytes += d * d + d * d // 32  # the resident MXFP8 linear
+        self.hc = hc = shape.hc
+        if hc:
+            self.layer_bytes += (2 * hc + hc * hc) * hc * d * 4 + d * 4  # fn + norm weight
         self.n_banks = max(2, self.layers,
                            math.ceil(args.min_rotation_gb * 1e9 / self.layer_bytes))
         self.n_inputs = 64
@@ -121,6 +124,14 @@ class Setup:
                 from livglm_amd.workloads import zipf_bias
                 b["router_bias"] = torch.from_numpy(
                     zipf_bias(E, np.random.default_rng(args.seed + len(self.banks)))).to(dev)
+            if hc:
+                # the FFN site's hyper-connection weights and post-attention norm
+                M = 2 * hc + hc * hc
+                b["hc.fn"] = torch.randn((M, hc * d), device=dev, generator=gen) * 0.02
+                b["hc.base"] = torch.randn(M, device=dev, generator=gen) * 0.5
+                b["hc.scale"] = torch.rand(3, device=dev, generator=gen) + 0.5
+                b["norm.weight"] = (1.0 + 0.1 * torch.randn(d, device=dev, generator=gen)).to(
+                    torch.bfloat16).to(torch.float32)
             if self.layers > 1:
                 # the resident linear as the reference builds it at start-up:
                 # bf16 N(0, 0.02) quantised to MXFP8 (layers.py:72-99)
@@ -141,6 +152,8 @@ class Setup:
             self.trace = torch.from_numpy(markov_bias_trace(
                 E, k, self.n_banks, n, np.random.default_rng(args.seed))).to(dev)
         self.xs = torch.randn((self.n_inputs, T, d), device=dev, generator=gen).to(torch.bfloat16)
+        if hc:
+            self.streams = torch.randn((self.n_inputs, T, hc, d), device=dev, generator=gen)
         # the layer's routed gate/up kernel: token-major for a few tokens, tiled
         # GEMV up to 64 tokens, grouped MFMA GEMMs beyond
         self.few_token = T <= 4 and k <= 8
@@ -300,6 +313,28 @@ def main() -> int:
     def layer_step(s: int) -> None:
         moe(S.xs[s % S.n_inputs], s % S.n_banks, s)
 
+    if S.hc:
+        # the decoder FFN site: hyper-connection + post-attention norm (one call,
+        # bf16 output), the MoE layer on it, hyper_residual
+        hc = S.hc
+        hc_ws_bytes = S.lib.glm_hc_workspace_bytes(T, hc, d)
+        hc_ws = torch.empty(max(hc_ws_bytes, 256), dtype=torch.uint8, device=S.dev)
+        post = torch.empty((T, hc), dtype=torch.float32, device=S.dev)
+        comb = torch.empty((T, hc, hc), dtype=torch.float32, device=S.dev)
+        normed = torch.empty((T, d), dtype=torch.bfloat16, device=S.dev)
+        site_out = torch.empty((T, hc, d), dtype=torch.float32, device=S.dev)
+
+        def layer_step(s: int) -> None:  # noqa: F811 -- the FFN site replaces the bare layer
+            b = S.banks[s % S.n_banks]
+            streams = S.streams[s % S.n_inputs]
+            native.call("glm_hc_pre", S.stream, streams.data_ptr(), T, hc, d,
+                        b["hc.fn"].data_ptr(), b["hc.base"].data_ptr(), b["hc.scale"].data_ptr(),
+                        20, 1e-6, 1e-6, b["norm.weight"].data_ptr(), 1e-6, 0, hc_ws.data_ptr(),
+                        hc_ws.numel(), post.data_ptr(), comb.data_ptr(), None, normed.data_ptr())
+            moe(normed, s % S.n_banks, s)
+            native.call("glm_hc_post", S.stream, streams.data_ptr(), T, hc, d, out.data_ptr(),
+                        post.data_ptr(), comb.data_ptr(), 0, site_out.data_ptr())
+
     act = torch.empty((T, d), dtype=torch.bfloat16, device=S.dev)
 
     def stack_step(s: int) -> None:
@@ -379,7 +414,8 @@ def main() -> int:
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(shape, S.banks[0], S.xs, args.cpu_seconds,
-                           None if S.trace is None else S.trace[0, 0])
+                           None if S.trace is None else S.trace[0, 0],
+                           S.streams if S.hc else None)
 
     line = {
         "metric": METRIC,
@@ -395,7 +431,12 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": (f"{shape.name}: {S.layers} layers x (MXFP8 {d}x{d} resident linear + "
+            "workload": (f"{shape.name}: decoder FFN site, hyper-connection of {S.hc} f32 "
+                         f"residual streams (20 Sinkhorn rounds) + RMSNorm + MoE layer T={T} "
+                         f"d={d} E={E} top-{k} I={I} (MXFP4 group-32 experts, bf16 shared "
+                         f"expert I={Is}) + hyper_residual"
+                         if S.hc else
+                         f"{shape.name}: {S.layers} layers x (MXFP8 {d}x{d} resident linear + "
                          f"MoE layer T={T} d={d} E={E} top-{k} I={I}, MXFP4 group-32 experts, "
                          f"bf16 shared expert I={Is}), Markov routing keeping 70% of the "
                          f"previous step's experts, one token per step"
@@ -688,11 +729,13 @@ def measure_traffic(args, kernel_name: str):
     return round(fetch[0] + write[0]), note
 
 
-def cpu_baseline(shape, bank, xs, budget_s: float, bias=None):
+def cpu_baseline(shape, bank, xs, budget_s: float, bias=None, streams=None):
     """The C restatement (oracle/libmoe_cpu.so, OpenMP over this host's cores)
     on one resident layer: as many layer steps as fit in ``budget_s``.  For a
     layer stack, one step is the resident MXFP8 linear + the MoE layer, and
-    the stack's rate is that of ``shape.layers`` such steps per token."""
+    the stack's rate is that of ``shape.layers`` such steps per token.  For the
+    FFN site the hyper-connection, norm and hyper_residual run in the numpy
+    oracle around the C MoE layer."""
     import numpy as np
     import torch
 
@@ -709,14 +752,27 @@ def cpu_baseline(shape, bank, xs, budget_s: float, bias=None):
         host["router_bias"] = bias.cpu().numpy()
     xs_h = xs.view(torch.int16).cpu().numpy().view(np.uint16)
     stack = shape.layers > 1
+    site = shape.hc > 0
+    if site:
+        from oracle import mhc_oracle as H
+        from oracle import moe_oracle as O
+        st_h = streams.cpu().numpy()
     steps = 0
     t0 = time.perf_counter()
     while True:
         x = xs_h[steps % xs_h.shape[0]]
         if stack:
             x = cpu_oracle.linear_mxfp8(x, host["linear.codes"], host["linear.scales"])
+        if site:
+            st = st_h[steps % st_h.shape[0]]
+            post, comb, collapsed = H.hyper_connection(
+                st, host["hc.fn"], host["hc.base"], host["hc.scale"], sinkhorn_iters=20,
+                rms_eps=1e-6, hc_eps=1e-6)
+            x = O.f32_to_bf16_bits(H.rms_norm(collapsed, host["norm.weight"], 1e-6))
         host["x"] = x
-        cpu_oracle.moe_layer(host, shape)
+        y = cpu_oracle.moe_layer(host, shape)[0]
+        if site:
+            H.hyper_residual(st, y, post, comb)
         steps += 1
         el = time.perf_counter() - t0
         if el >= budget_s or steps >= 10000:
@@ -737,7 +793,9 @@ def cpu_baseline(shape, bank, xs, budget_s: float, bias=None):
         "cores": cpu_oracle.threads(),
         "kind": "port",
         "sample": f"{steps} layer steps of {shape.name} (T={shape.T}) on one resident layer "
-                  f"in {el:.2f} s; C restatement (not MLX), OpenMP",
+                  f"in {el:.2f} s; C restatement (not MLX), OpenMP"
+                  + ("; hyper-connection, norm and hyper_residual in the numpy oracle"
+                     if site else ""),
     }
 
 if __name__ == "__main__":

@@ -289,6 +289,63 @@ int glm_moe_forward(void *stream, const uint16_t *x, int T, int d, const float *
                     size_t workspace_bytes, float *out, float *weights_out,
                     uint32_t *indices_out);
 
+/* ------------------------------------------------------------ decoder FFN site */
+
+/* glm_hc_pre / glm_hc_post flag: the streams are bf16 in the model (passed
+ * here as their exact f32 values); the reference's rounding points of that
+ * dtype apply (collapsed rounded to bf16; in hyper_residual post, comb and the
+ * mixing sum rounded to bf16, mhc.py:46,57-59). */
+#define GLM_HC_BF16_STREAMS 1
+
+/*
+ * Workspace bytes of glm_hc_pre (per-slice partial sums of the hyper-connection
+ * GEMV); 0 for invalid sizes.
+ */
+size_t glm_hc_workspace_bytes(int T, int hc, int d);
+
+/*
+ * The FFN-site hyper-connection of a decoder layer, HyperConnection.__call__
+ * (mhc.py:23-48; the layer's ffn_hc, model.py:59,134), with the
+ * post-attention RMSNorm (model.py:57,135; layers.py:119-131) fused:
+ *   flat = rms_norm(streams[t] flattened, eps = rms_eps)   (unweighted)
+ *   mixed = flat @ fn^T, split into pre/post/comb parts of hc, hc, hc*hc
+ *   pre  = sigmoid(mixed_pre * scale[0] + base_pre) + hc_eps
+ *   post = 2 sigmoid(mixed_post * scale[1] + base_post)             -> post [T][hc]
+ *   comb = softmax_rows(mixed_comb * scale[2] + base_comb) + hc_eps, then a
+ *          column normalisation and sinkhorn_iters - 1 (row, column) rounds,
+ *          each x / (sum + hc_eps)                                  -> comb [T][hc][hc]
+ *   collapsed = sum_i pre[i] streams[t][i]                          -> collapsed [T][d] (may be NULL)
+ *   normed = bf16(rms_norm(collapsed) * norm_weight)               -> normed [T][d] (may be NULL;
+ *            norm_weight f32 [d] or NULL for an unweighted norm, eps = norm_eps)
+ * streams f32 [T][hc][d]; fn f32 [2 hc + hc^2][hc d]; base f32 [2 hc + hc^2];
+ * scale f32 [3].  The reference routes the two-row case of the GEMV to
+ * mx._expert_ssd_two_row_gemv (mhc.py:28-32).  Limits: hc <= 8, d % 4 == 0,
+ * d <= 8192.
+ */
+int glm_hc_pre(void *stream, const float *streams, int T, int hc, int d, const float *fn,
+               const float *base, const float *scale, int sinkhorn_iters, float rms_eps,
+               float hc_eps, const float *norm_weight, float norm_eps, int flags, void *workspace,
+               size_t workspace_bytes, float *post, float *comb, float *collapsed,
+               uint16_t *normed);
+
+/*
+ * hyper_residual (mhc.py:51-60):
+ *   out[t][j] = post[t][j] * y[t] + sum_i comb[t][i][j] * residual[t][i]
+ * residual f32 [T][hc][d], y f32 [T][d] (the MoE layer's output), post f32
+ * [T][hc], comb f32 [T][hc][hc] -> out f32 [T][hc][d].  flags: GLM_HC_BF16_STREAMS
+ * when the residual streams are bf16 in the model (residual passed as f32).
+ */
+int glm_hc_post(void *stream, const float *residual, int T, int hc, int d, const float *y,
+                const float *post, const float *comb, int flags, float *out);
+
+/*
+ * RMSNorm (layers.py:119-131) and UnweightedRMSNorm (layers.py:134-140) of
+ * f32 rows: out = x * (1 / sqrt(mean(x^2) + eps)) * weight (weight f32 [d] or
+ * NULL); written as f32 (out) and/or rounded to bf16 (out_bf16).  d % 4 == 0.
+ */
+int glm_rms_norm(void *stream, const float *x, int T, int d, const float *weight, float eps,
+                 float *out, uint16_t *out_bf16);
+
 /* ------------------------------------------------------------ expert bank loading */
 
 /* glm_file_read_ranges flag: drop the file's page-cache pages of the ranges

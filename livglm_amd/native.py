@@ -27,6 +27,7 @@ GLM_MX_RULE_NEAREST = 0
 GLM_MX_RULE_OCP = 1
 
 GLM_READ_DROP_CACHE = 1
+GLM_HC_BF16_STREAMS = 1
 
 ABI_VERSION = 1
 
@@ -64,6 +65,11 @@ SIGNATURES = {
     "glm_moe_forward": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _i, _f, _i,
                              _p, _p, _p, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p, _p, _p,
                              _f, _p, _sz, _p, _p, _p]),
+    "glm_hc_workspace_bytes": (_sz, [_i, _i, _i]),
+    "glm_hc_pre": (_i, [_p, _p, _i, _i, _i, _p, _p, _p, _i, _f, _f, _p, _f, _i, _p, _sz, _p, _p,
+                        _p, _p]),
+    "glm_hc_post": (_i, [_p, _p, _i, _i, _i, _p, _p, _p, _i, _p]),
+    "glm_rms_norm": (_i, [_p, _p, _i, _i, _p, _f, _p, _p]),
     "glm_file_read_ranges": (_i, [ctypes.c_char_p, _i, _p, _p, _p, _i, _i]),
     "glm_bank_scatter": (_i, [_p, _p, _i64, _p, _i, _p]),
 }

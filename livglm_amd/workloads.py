@@ -8,6 +8,9 @@ Shapes follow the routed-MoE layer of GLM-5.3-Flash at benchmark geometry:
 * ``prefill_t4096`` T=4096, as verify_t2, near-uniform routing
 * ``stack42_t1``   T=1, 42 layers of (2048x2048 MXFP8 resident linear + MoE
   as verify_t2), 256 decode steps, Markov routing with 70% expert reuse
+* ``ffn_t2``       the decoder FFN site at verify_t2: hyper-connection of 4 f32
+  residual streams (20 Sinkhorn rounds) + post-attention RMSNorm + the MoE
+  layer + hyper_residual
 
 Expert weights: uniform random E2M1 codes (uniform bytes) and E8M0 scale
 bytes uniform in [119, 127].  Activations bf16 N(0, 1).  Router weight f32
@@ -38,6 +41,7 @@ class MoEShape:
     norm_topk_prob: bool = True
     layers: int = 1
     steps: int = 1
+    hc: int = 0  # > 0: the decoder FFN site (hyper-connection of hc streams + norm) around it
 
     @property
     def expert_bytes(self) -> int:
@@ -57,6 +61,7 @@ SHAPES = {
     "prefill_t4096": MoEShape("prefill_t4096", T=4096, d=2048, E=128, k=8, I=768, I_shared=768),
     "stack42_t1": MoEShape("stack42_t1", T=1, d=2048, E=128, k=8, I=768, I_shared=768,
                            routing="markov", layers=42, steps=256),
+    "ffn_t2": MoEShape("ffn_t2", T=2, d=2048, E=128, k=8, I=768, I_shared=768, hc=4),
 }
 
 SCALE_LO, SCALE_HI = 119, 127  # inclusive E8M0 range of the synthetic scales
@@ -176,3 +181,23 @@ def write_expert_checkpoint(root: str, shape: MoEShape, layers, seed: int) -> in
         json.dump({"text_config": {"hidden_size": d, "moe_intermediate_size": I,
                                    "n_routed_experts": E}}, f)
     return len(layers) * E * record
+
+
+def make_hc(T: int, hc: int, d: int, seed: int, *, bf16_streams: bool = False):
+    """Hyper-connection inputs of a decoder FFN site: streams f32 [T, hc, d]
+    N(0, 1) (bf16-representable when ``bf16_streams``), fn f32
+    [2 hc + hc^2, hc d] N(0, 0.02), base N(0, 0.5), scale U(0.5, 1.5), and the
+    post-attention norm weight (bf16-representable, around 1)."""
+    rng = np.random.default_rng(seed)
+    M = 2 * hc + hc * hc
+    streams = rng.standard_normal((T, hc, d), dtype=np.float32)
+    if bf16_streams:
+        streams = (f32_to_bf16_bits(streams).astype(np.uint32) << 16).view(np.float32)
+    norm = rng.normal(1.0, 0.1, d).astype(np.float32)
+    return {
+        "streams": np.ascontiguousarray(streams),
+        "fn": rng.normal(0.0, 0.02, (M, hc * d)).astype(np.float32),
+        "base": rng.normal(0.0, 0.5, M).astype(np.float32),
+        "scale": rng.uniform(0.5, 1.5, 3).astype(np.float32),
+        "norm_weight": (f32_to_bf16_bits(norm).astype(np.uint32) << 16).view(np.float32),
+    }

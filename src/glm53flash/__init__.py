@@ -6,7 +6,9 @@ Host-side mirror of the reference's MoE interface (``moe.py``, ``expert_ssd.py``
 """
 
 __all__ = [
+    "bank_loader",
     "contract",
+    "expert_source",
     "expert_ssd",
     "layers",
     "model_config",

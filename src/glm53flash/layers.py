@@ -132,3 +132,59 @@ class DenseMLP:
                N.ptr(self.down_proj.scales), float(self.swiglu_limit), h.data_ptr(),
                out.data_ptr())
         return out.reshape(*x.shape[:-1], self.hidden_size)
+
+
+def _f32_param(value, cache: dict, slot: str, name: str) -> torch.Tensor:
+    """The f32 device copy of a norm-style parameter (exact for bf16; the
+    tensor itself when it is f32), cached in ``cache[slot]`` until the
+    parameter is replaced or modified in place."""
+    value = require_weight(value, name)
+    key = (id(value), value._version, value.data_ptr())
+    hit = cache.get(slot)
+    if hit is None or hit[0] != key:
+        N.require_device(value, name, (torch.float32, torch.bfloat16))
+        hit = (key, value.to(torch.float32).contiguous())
+        cache[slot] = hit
+    return hit[1]
+
+
+class RMSNorm:
+    """``mx.fast.rms_norm(x, weight, eps)`` (``layers.py:119-131``): ``x * (1 /
+    sqrt(mean(x^2) + eps)) * weight`` over the last axis, computed in f32; the
+    output has the input's dtype (f32 or bf16)."""
+
+    def __init__(self, dims: int, eps: float):
+        self.dims = dims
+        self.eps = eps
+        self.weight = None
+        self._f32: dict = {}
+
+    def weight_f32(self) -> torch.Tensor:
+        return _f32_param(self.weight, self._f32, "weight", "rms_norm.weight")
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        return _rms_norm(x, self.dims, self.weight_f32(), self.eps)
+
+
+class UnweightedRMSNorm:
+    """``layers.py:134-140``: the RMS norm of ``x`` cast to f32, no weight; f32 out."""
+
+    def __init__(self, eps: float):
+        self.eps = eps
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        return _rms_norm(x.to(torch.float32), x.shape[-1], None, self.eps)
+
+
+def _rms_norm(x: torch.Tensor, d: int, weight: torch.Tensor | None, eps: float) -> torch.Tensor:
+    N.require_device(x, "x", (torch.float32, torch.bfloat16))
+    if x.shape[-1] != d:
+        raise ContractError(f"rms_norm over {d} features got rows of {x.shape[-1]}")
+    rows = x.reshape(-1, d)
+    xf = rows if rows.dtype == torch.float32 else rows.to(torch.float32)
+    out = torch.empty(xf.shape, dtype=x.dtype, device=x.device)
+    f32 = out if x.dtype == torch.float32 else None
+    b16 = out if x.dtype == torch.bfloat16 else None
+    N.call("glm_rms_norm", N.stream_of(x), xf.data_ptr(), xf.shape[0], d, N.ptr(weight),
+           float(eps), N.ptr(f32), N.ptr(b16))
+    return out.reshape(x.shape)

@@ -94,6 +94,12 @@ class GLMTextConfig:
             hidden_act=str(text.get("hidden_act", "silu")),
             scoring_func=str(text.get("scoring_func", "sigmoid")),
             topk_method=str(text.get("topk_method", "noaux_tc")),
+            # the decoder FFN site's hyper-connection and norm (model_config.py:102-105);
+            # optional here, so that MoE-only configs stay valid
+            rms_norm_eps=float(text.get("rms_norm_eps", 1e-6)),
+            hc_mult=int(text.get("hc_mult", 1)),
+            hc_sinkhorn_iters=int(text.get("hc_sinkhorn_iters", 1)),
+            hc_eps=float(text.get("hc_eps", 1e-6)),
         )
         result.validate()
         return result
@@ -114,3 +120,5 @@ class GLMTextConfig:
             raise ContractError("router groups must contain at least two experts")
         if self.hidden_size % 32 or self.moe_intermediate_size % 32:
             raise ContractError("group-32 MX experts need hidden and intermediate sizes % 32 == 0")
+        if self.hc_mult < 1 or self.hc_sinkhorn_iters < 1:
+            raise ContractError("hyper-connection settings must be positive")
