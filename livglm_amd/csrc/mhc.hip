@@ -23,12 +23,18 @@
 #include "glm_common.h"
 #include "topk_select.h"  // wave_lds_sync
 
+// Every product and sum is rounded on its own, as the reference's separate
+// array operations are (no fused multiply-add).
+#pragma clang fp contract(off)
+
 namespace glm {
 
 constexpr int kHcThreads = 256;
-constexpr int kHcSlice = 256;        // columns of hc*d per hc_mix workgroup
+constexpr int kHcSlice = 256;        // columns of hc*d per hc_mix chunk
+constexpr int kHcMaxSlices = 64;     // hc_mix workgroups along K (chunks beyond loop)
 constexpr int kHcTokens = 4;         // tokens per hc_mix workgroup
 constexpr int kHcMaxMult = 8;        // hc <= 8: M = 2 hc + hc^2 <= 80
+constexpr int kHcMaxM = 2 * kHcMaxMult + kHcMaxMult * kHcMaxMult;
 constexpr int kHcMaxD = 8192;        // collapsed row kept in LDS (32 KB)
 
 __device__ __forceinline__ void lds_sync() { __syncthreads(); }
@@ -45,8 +51,14 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
   return s;
 }
 
-// partial[s][t][m] = sum over columns of slice s of x[t][k] fn[m][k] (m < M),
-// partial[s][t][M] = sum of x[t][k]^2.
+// partial[s][t][m] = sum over the columns of workgroup s of x[t][k] fn[m][k]
+// (m < M); partial[s][t][M] = the sum of x[t][k]^2 over them.  Workgroup s
+// takes the 256-column chunks s, s + S, ... of the K = hc d columns; wave w
+// owns the rows w, w + 4, ... (ROWS at most).  Every load of a chunk -- the
+// token rows and all of the wave's fn rows -- is issued before any product,
+// and lanes keep running sums, so a workgroup waits on memory once per chunk
+// and reduces across lanes once at the end.
+template <int ROWS>
 __global__ __launch_bounds__(kHcThreads) void hc_mix_kernel(const float *x, const float *fn, int T,
                                                             int K, int M, float *partial) {
   const int s = blockIdx.x, S = gridDim.x;
@@ -54,34 +66,62 @@ __global__ __launch_bounds__(kHcThreads) void hc_mix_kernel(const float *x, cons
   const int nt = min(kHcTokens, T - t0);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int k = s * kHcSlice + 4 * lane;
-  const bool in = k < K;  // K % 4 == 0: a lane's 4 columns are all in or all out
-  glm_f32x4 xv[kHcTokens];
+  const int nchunks = (K + kHcSlice - 1) / kHcSlice;
+  float acc[ROWS][kHcTokens], sq[kHcTokens];
 #pragma unroll
   for (int t = 0; t < kHcTokens; ++t) {
-    xv[t] = glm_f32x4{0.f, 0.f, 0.f, 0.f};
-    if (t < nt && in)
-      xv[t] = *reinterpret_cast<const glm_f32x4 *>(x + (size_t)(t0 + t) * K + k);
+    sq[t] = 0.f;
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) acc[r][t] = 0.f;
   }
-  if (wave == 0) {
+  for (int c = s; c < nchunks; c += S) {
+    const int k = c * kHcSlice + 4 * lane;
+    const bool in = k < K;  // K % 4 == 0: a lane's 4 columns are all in or all out
+    glm_f32x4 xv[kHcTokens], w[ROWS];
 #pragma unroll
     for (int t = 0; t < kHcTokens; ++t) {
-      const float q = wave_sum(xv[t][0] * xv[t][0] + xv[t][1] * xv[t][1] +
-                               xv[t][2] * xv[t][2] + xv[t][3] * xv[t][3]);
-      if (lane == 0 && t < nt) partial[((size_t)s * T + t0 + t) * (M + 1) + M] = q;
+      xv[t] = glm_f32x4{0.f, 0.f, 0.f, 0.f};
+      if (t < nt && in)
+        xv[t] = *reinterpret_cast<const glm_f32x4 *>(x + (size_t)(t0 + t) * K + k);
     }
-  }
-  for (int m = wave; m < M; m += kHcThreads / 64) {
-    glm_f32x4 w = glm_f32x4{0.f, 0.f, 0.f, 0.f};
-    if (in) w = *reinterpret_cast<const glm_f32x4 *>(fn + (size_t)m * K + k);
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      const int m = wave + 4 * r;
+      w[r] = glm_f32x4{0.f, 0.f, 0.f, 0.f};
+      if (m < M && in) w[r] = *reinterpret_cast<const glm_f32x4 *>(fn + (size_t)m * K + k);
+    }
 #pragma unroll
     for (int t = 0; t < kHcTokens; ++t) {
-      const float p = wave_sum(xv[t][0] * w[0] + xv[t][1] * w[1] + xv[t][2] * w[2] +
-                               xv[t][3] * w[3]);
-      if (lane == 0 && t < nt) partial[((size_t)s * T + t0 + t) * (M + 1) + m] = p;
+      sq[t] += xv[t][0] * xv[t][0] + xv[t][1] * xv[t][1] + xv[t][2] * xv[t][2] +
+               xv[t][3] * xv[t][3];
+#pragma unroll
+      for (int r = 0; r < ROWS; ++r)
+        acc[r][t] += xv[t][0] * w[r][0] + xv[t][1] * w[r][1] + xv[t][2] * w[r][2] +
+                     xv[t][3] * w[r][3];
     }
   }
-  (void)S;
+#pragma unroll
+  for (int t = 0; t < kHcTokens; ++t) {
+    if (t >= nt) break;  // uniform
+    float *out = partial + ((size_t)s * T + t0 + t) * (M + 1);
+    if (wave == 0) {
+      const float q = wave_sum(sq[t]);
+      if (lane == 0) out[M] = q;
+    }
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      const int m = wave + 4 * r;
+      if (m >= M) break;  // uniform
+      const float p = wave_sum(acc[r][t]);
+      if (lane == 0) out[m] = p;
+    }
+  }
+}
+
+// A gate logit as the reference forms it: (mixed * inv_rms) * scale + base
+// (mhc.py:38-41).
+__device__ __forceinline__ float gate_logit(float raw, float inv, float scale, float base) {
+  return raw * inv * scale + base;
 }
 
 struct HcFinishArgs {
@@ -96,8 +136,71 @@ struct HcFinishArgs {
   uint16_t *normed;                // bf16 [T][d] or nullptr
 };
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(dpp_i32<CTRL>(__float_as_int(v)));
+}
+
+// Sums and maxima over the hc x hc mixing matrix held one entry per lane
+// (lane = i hc + j, lanes >= hc^2 idle).  hc = 2, 4: DPP lane moves within a
+// row of 16 lanes (quad swaps along a matrix row, row rotations by 8 then 4
+// down a column of hc = 4); hc = 8: xor shuffles; other hc: through LDS in
+// ascending order.  Every lane of a row (column) ends with the same value.
+struct HcMatrix {
+  enum Mode { kDpp, kShuffle, kLds };
+  int hc;
+  Mode mode;
+  bool mine;
+  int i, j, lane;
+  float *lds;  // hc^2 floats
+
+  __device__ static float op(float a, float b, bool max) { return max ? fmaxf(a, b) : a + b; }
+
+  __device__ float row_reduce(float v, bool max) const {
+    if (mode == kDpp) {
+      if (hc >= 2) v = op(v, dpp_f32<0xB1>(v), max);  // quad_perm [1,0,3,2]: column j ^ 1
+      if (hc == 4) v = op(v, dpp_f32<0x4E>(v), max);  // quad_perm [2,3,0,1]: column j ^ 2
+      return v;
+    }
+    if (mode == kShuffle) {
+      for (int off = 1; off < hc; off <<= 1) v = op(v, __shfl_xor(v, off), max);
+      return v;
+    }
+    wave_lds_sync();
+    if (mine) lds[lane] = v;
+    wave_lds_sync();
+    if (!mine) return v;
+    float r = lds[i * hc];
+    for (int q = 1; q < hc; ++q) r = op(r, lds[i * hc + q], max);
+    return r;
+  }
+
+  __device__ float col_sum(float v) const {
+    if (mode == kDpp) {
+      if (hc == 2) v += dpp_f32<0x4E>(v);  // row i ^ 1 (lanes two apart)
+      if (hc == 4) {
+        v += dpp_f32<0x128>(v);  // row_ror:8: rows i and i ^ 2
+        v += dpp_f32<0x124>(v);  // row_ror:4: the other pair
+      }
+      return v;
+    }
+    if (mode == kShuffle) {
+      for (int off = hc; off < hc * hc; off <<= 1) v += __shfl_xor(v, off);
+      return v;
+    }
+    wave_lds_sync();
+    if (mine) lds[lane] = v;
+    wave_lds_sync();
+    if (!mine) return v;
+    float r = lds[j];
+    for (int q = 1; q < hc; ++q) r += lds[q * hc + j];
+    return r;
+  }
+};
+
 __global__ __launch_bounds__(kHcThreads) void hc_finish_kernel(HcFinishArgs a) {
-  __shared__ float mixed[2 * kHcMaxMult + kHcMaxMult * kHcMaxMult + 1];
+  __shared__ float pbuf[kHcMaxSlices * (kHcMaxM + 1)];
+  __shared__ float mixed[kHcMaxM + 1];
   __shared__ float cm[kHcMaxMult * kHcMaxMult];
   __shared__ float pre[kHcMaxMult];
   __shared__ float red[4];
@@ -106,9 +209,39 @@ __global__ __launch_bounds__(kHcThreads) void hc_finish_kernel(HcFinishArgs a) {
   const int hc = a.hc, d = a.d, M = 2 * hc + hc * hc;
   const int K = hc * d;
   const int tid = threadIdx.x;
+  // the first pass of the collapsed sum reads its streams now: they do not
+  // depend on the gates, so their latency hides behind everything before it
+  const float *st = a.streams + (size_t)t * K;
+  glm_f32x4 sv[2][kHcMaxMult];
+  auto load_streams = [&](int c0) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = c0 + u * 4 * kHcThreads;
+#pragma unroll
+      for (int i = 0; i < kHcMaxMult; ++i)
+        if (i < hc && c < d) sv[u][i] = *reinterpret_cast<const glm_f32x4 *>(st + (size_t)i * d + c);
+    }
+  };
+  load_streams(4 * tid);
+  // the per-workgroup partials of hc_mix: all loads issued together, then
+  // summed in workgroup order from LDS
+  const int n = a.S * (M + 1);
+  for (int q0 = tid; q0 < n; q0 += 4 * kHcThreads) {
+    float v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int q = q0 + u * kHcThreads;
+      v[u] = 0.f;
+      if (q < n) v[u] = a.partial[((size_t)(q / (M + 1)) * a.T + t) * (M + 1) + q % (M + 1)];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (q0 + u * kHcThreads < n) pbuf[q0 + u * kHcThreads] = v[u];
+  }
+  lds_sync();
   if (tid <= M) {
     float acc = 0.f;
-    for (int s = 0; s < a.S; ++s) acc += a.partial[((size_t)s * a.T + t) * (M + 1) + tid];
+    for (int s = 0; s < a.S; ++s) acc += pbuf[s * (M + 1) + tid];
     mixed[tid] = acc;
   }
   lds_sync();
@@ -116,65 +249,56 @@ __global__ __launch_bounds__(kHcThreads) void hc_finish_kernel(HcFinishArgs a) {
     // flat = streams * inv_rms, mixed = flat @ fn^T = inv_rms * (streams @ fn^T)
     const float inv = 1.0f / sqrtf(mixed[M] / (float)K + a.rms_eps);
     const int lane = tid;
-    const int i = lane / hc, j = lane % hc;
-    const bool mine = lane < hc * hc;
+    const HcMatrix::Mode mode = hc <= 2 || hc == 4 ? HcMatrix::kDpp
+                                : hc == 8            ? HcMatrix::kShuffle
+                                                     : HcMatrix::kLds;
+    const HcMatrix mat{hc, mode, lane < hc * hc, lane / hc, lane % hc, lane, cm};
     if (lane < hc) {
-      const float p = sigmoid_f32(mixed[lane] * inv * a.scale[0] + a.base[lane]) + a.hc_eps;
+      const float p = sigmoid_f32(gate_logit(mixed[lane], inv, a.scale[0], a.base[lane])) +
+                      a.hc_eps;
       pre[lane] = p;
       a.post[(size_t)t * hc + lane] =
-          2.0f * sigmoid_f32(mixed[hc + lane] * inv * a.scale[1] + a.base[hc + lane]);
+          2.0f * sigmoid_f32(gate_logit(mixed[hc + lane], inv, a.scale[1], a.base[hc + lane]));
     }
     float c = 0.f;
-    if (mine) c = mixed[2 * hc + lane] * inv * a.scale[2] + a.base[2 * hc + lane];
-    // row softmax (mhc.py:41), then + eps and the column normalisation
-    if (mine) cm[lane] = c;
-    wave_lds_sync();
-    if (mine) {
-      float mx = cm[i * hc];
-      for (int q = 1; q < hc; ++q) mx = fmaxf(mx, cm[i * hc + q]);
-      c = expf(c - mx);
-    }
-    wave_lds_sync();
-    if (mine) cm[lane] = c;
-    wave_lds_sync();
-    if (mine) {
-      float sum = 0.f;
-      for (int q = 0; q < hc; ++q) sum += cm[i * hc + q];
-      c = c / sum + a.hc_eps;
-    }
-    auto normalise = [&](bool by_column) {
-      wave_lds_sync();
-      if (mine) cm[lane] = c;
-      wave_lds_sync();
-      if (mine) {
-        float sum = 0.f;
-        for (int q = 0; q < hc; ++q) sum += by_column ? cm[q * hc + j] : cm[i * hc + q];
-        c = c / (sum + a.hc_eps);
-      }
-    };
-    normalise(true);
+    if (mat.mine) c = gate_logit(mixed[2 * hc + lane], inv, a.scale[2], a.base[2 * hc + lane]);
+    // row softmax (mhc.py:41) + eps, the column normalisation, then
+    // iters - 1 rounds of (row, column) normalisation (mhc.py:42-45)
+    const float mx = mat.row_reduce(c, true);
+    c = expf(c - mx);
+    c = c / mat.row_reduce(c, false) + a.hc_eps;
+    c = c / (mat.col_sum(c) + a.hc_eps);
     for (int it = 1; it < a.iters; ++it) {
-      normalise(false);
-      normalise(true);
+      c = c / (mat.row_reduce(c, false) + a.hc_eps);
+      c = c / (mat.col_sum(c) + a.hc_eps);
     }
-    if (mine) a.comb[(size_t)t * hc * hc + lane] = c;
+    if (mat.mine) a.comb[(size_t)t * hc * hc + lane] = c;
   }
   lds_sync();
-  // collapsed[c] = sum_i pre[i] streams[t][i][c] (i ascending)
-  const float *st = a.streams + (size_t)t * K;
+  // collapsed[c] = sum_i pre[i] streams[t][i][c] (i ascending); two column
+  // groups per pass with all their stream loads issued together
   float sq = 0.f;
-  for (int c = 4 * tid; c < d; c += 4 * kHcThreads) {
-    glm_f32x4 v = glm_f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int i = 0; i < hc; ++i) {
-      const glm_f32x4 s = *reinterpret_cast<const glm_f32x4 *>(st + (size_t)i * d + c);
-      const float p = pre[i];
-      v = glm_f32x4{v[0] + p * s[0], v[1] + p * s[1], v[2] + p * s[2], v[3] + p * s[3]};
+  for (int c0 = 4 * tid; c0 < d; c0 += 8 * kHcThreads) {
+    if (c0 != 4 * tid) load_streams(c0);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = c0 + u * 4 * kHcThreads;
+      if (c >= d) break;
+      glm_f32x4 v = glm_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < kHcMaxMult; ++i) {
+        if (i < hc) {
+          const float p = pre[i];
+          v = glm_f32x4{v[0] + p * sv[u][i][0], v[1] + p * sv[u][i][1], v[2] + p * sv[u][i][2],
+                        v[3] + p * sv[u][i][3]};
+        }
+      }
+      if (a.bf16_streams)
+        v = glm_f32x4{bf16_round(v[0]), bf16_round(v[1]), bf16_round(v[2]), bf16_round(v[3])};
+      *reinterpret_cast<glm_f32x4 *>(row + c) = v;
+      if (a.collapsed) *reinterpret_cast<glm_f32x4 *>(a.collapsed + (size_t)t * d + c) = v;
+      sq += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
     }
-    if (a.bf16_streams)
-      v = glm_f32x4{bf16_round(v[0]), bf16_round(v[1]), bf16_round(v[2]), bf16_round(v[3])};
-    *reinterpret_cast<glm_f32x4 *>(row + c) = v;
-    if (a.collapsed) *reinterpret_cast<glm_f32x4 *>(a.collapsed + (size_t)t * d + c) = v;
-    sq += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
   }
   if (a.normed == nullptr) return;
   // post-attention RMSNorm of the collapsed row, rounded to bf16
@@ -261,7 +385,9 @@ __global__ __launch_bounds__(kHcThreads) void rms_norm_kernel(const float *x, in
   }
 }
 
-static int hc_slices(int hc, int d) { return (hc * d + kHcSlice - 1) / kHcSlice; }
+static int hc_slices(int hc, int d) {
+  return std::min(kHcMaxSlices, (hc * d + kHcSlice - 1) / kHcSlice);
+}
 
 static int check_hc(const char *who, int T, int hc, int d) {
   GLM_REQUIRE(T >= 0 && hc >= 1 && d >= 1, GLM_ERR_INVALID_ARGUMENT, "%s: invalid sizes", who);
@@ -306,8 +432,17 @@ extern "C" int glm_hc_pre(void *stream, const float *streams, int T, int hc, int
   const int M = 2 * hc + hc * hc;
   const int S = hc_slices(hc, d);
   float *partial = static_cast<float *>(workspace);
-  hipLaunchKernelGGL(hc_mix_kernel, dim3(S, (T + kHcTokens - 1) / kHcTokens), dim3(kHcThreads), 0,
-                     (hipStream_t)stream, streams, fn, T, hc * d, M, partial);
+  const dim3 mix_grid(S, (T + kHcTokens - 1) / kHcTokens);
+  const int rows = (M + 3) / 4;  // fn rows per wave
+  if (rows <= 2)
+    hipLaunchKernelGGL(hc_mix_kernel<2>, mix_grid, dim3(kHcThreads), 0, (hipStream_t)stream,
+                       streams, fn, T, hc * d, M, partial);
+  else if (rows <= 6)
+    hipLaunchKernelGGL(hc_mix_kernel<6>, mix_grid, dim3(kHcThreads), 0, (hipStream_t)stream,
+                       streams, fn, T, hc * d, M, partial);
+  else
+    hipLaunchKernelGGL(hc_mix_kernel<20>, mix_grid, dim3(kHcThreads), 0, (hipStream_t)stream,
+                       streams, fn, T, hc * d, M, partial);
   GLM_LAUNCH_CHECK("hc_mix_kernel");
   HcFinishArgs a{streams, partial, base, scale, norm_weight, T, hc, d, S, sinkhorn_iters,
                  (flags & GLM_HC_BF16_STREAMS) != 0, rms_eps, hc_eps, norm_eps, post, comb,

