@@ -378,6 +378,25 @@ int glm_file_read_ranges(const char *path, int n, const int64_t *offset, const i
 int glm_bank_scatter(void *stream, const uint8_t *staging, int64_t staging_bytes,
                      const int64_t *segments, int n, int64_t *device_table);
 
+/*
+ * Decodes n ScaleX Mode-A scale records (scale_codec.py:35-91,151-201) that
+ * sit in a device staging buffer into raw E8M0 bytes.  records is a HOST
+ * table int64 [n][13]: staging offset, encoded bytes, raw bytes, codec (0 raw,
+ * 1 one bit, 2 two bits), palette (4 bytes, little-endian), primary bytes,
+ * exception count, then (destination, bytes) for the gate, down and up scale
+ * tensors of the expert, which receive the raw bytes in that order.  The
+ * table is checked (lengths consistent with the codec, destinations covering
+ * the raw bytes, records inside staging_bytes) and copied to device_table
+ * (device memory of at least 104 n bytes, kept until the stream has run the
+ * copy).  Exception positions must be ascending (the caller checks them; an
+ * unordered list decodes wrongly but stays in bounds).  Replaces the per-call
+ * Mode-B decode of the reference's ScaleX kernels (native_expert_ssd.py:
+ * 653-694, docs/scalex-mode-b.md:29-33): here scales are decoded once, when
+ * the layer is loaded into HBM.
+ */
+int glm_scalex_decode(void *stream, const uint8_t *staging, int64_t staging_bytes,
+                      const int64_t *records, int n, int64_t *device_table);
+
 #ifdef __cplusplus
 }
 #endif

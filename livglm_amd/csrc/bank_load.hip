@@ -53,9 +53,124 @@ __global__ __launch_bounds__(kScatterThreads) void bank_scatter_kernel(const uin
   for (long long i = tail + threadIdx.x; i < end; i += kScatterThreads) dst[i] = src[i];
 }
 
+// ScaleX Mode-A records (scale_codec.py:35-91) decoded into raw E8M0 bytes.
+// Table row (13 x int64): staging offset of the record, encoded bytes, raw
+// bytes, codec (0 raw, 1 one bit, 2 two bits), the four palette bytes packed
+// little-endian, primary bytes, exception count, then three (destination,
+// bytes) pairs that receive the raw bytes in order (gate, down, up scales).
+constexpr int kScalexCols = 13;
+constexpr int kScalexHeader = 24;
+constexpr int kScalexBlock = 4096;  // scales per workgroup
+
+__device__ __forceinline__ uint32_t load_u32_le(const uint8_t *p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+__global__ __launch_bounds__(kScatterThreads) void scalex_decode_kernel(const uint8_t *staging,
+                                                                        const int64_t *table) {
+  __shared__ uint32_t epos[kScalexBlock];
+  __shared__ uint8_t eval[kScalexBlock];
+  __shared__ long long erange[2];
+  const int64_t *row = table + (long long)kScalexCols * blockIdx.y;
+  const long long raw = row[2];
+  const long long b0 = (long long)blockIdx.x * kScalexBlock;
+  if (b0 >= raw) return;
+  const long long b1 = b0 + kScalexBlock < raw ? b0 + kScalexBlock : raw;
+  const uint8_t *primary = staging + row[0] + kScalexHeader;
+  const int codec = (int)row[3];
+  const uint32_t palette = (uint32_t)row[4];
+  const long long nexc = row[6];
+  const uint8_t *pos = primary + row[5];  // u32 little-endian each, ascending
+  const uint8_t *vals = pos + 4 * nexc;
+  // this workgroup's exceptions: [lower_bound(b0), lower_bound(b1))
+  if (threadIdx.x < 2) {
+    const long long key = threadIdx.x == 0 ? b0 : b1;
+    long long lo = 0, hi = nexc;
+    while (lo < hi) {
+      const long long mid = (lo + hi) >> 1;
+      if ((long long)load_u32_le(pos + 4 * mid) < key) lo = mid + 1;
+      else hi = mid;
+    }
+    erange[threadIdx.x] = lo;
+  }
+  __syncthreads();
+  const long long e0 = erange[0];
+  long long ne = erange[1] - e0;
+  ne = ne < 0 ? 0 : (ne > kScalexBlock ? kScalexBlock : ne);  // bounded even if unsorted
+  for (int q = threadIdx.x; q < ne; q += kScatterThreads) {
+    epos[q] = load_u32_le(pos + 4 * (e0 + q));
+    eval[q] = vals[e0 + q];
+  }
+  __syncthreads();
+  const long long n0 = row[8], n1 = row[10];
+  uint8_t *d0 = reinterpret_cast<uint8_t *>(row[7]);
+  uint8_t *d1 = reinterpret_cast<uint8_t *>(row[9]);
+  uint8_t *d2 = reinterpret_cast<uint8_t *>(row[11]);
+  for (long long p = b0 + threadIdx.x; p < b1; p += kScatterThreads) {
+    uint32_t v;
+    if (codec == 0) v = primary[p];
+    else if (codec == 1) v = palette >> (8 * ((primary[p >> 3] >> (p & 7)) & 1));
+    else v = palette >> (8 * ((primary[p >> 2] >> (2 * (p & 3))) & 3));
+    int lo = 0, hi = (int)ne;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if ((long long)epos[mid] < p) lo = mid + 1;
+      else hi = mid;
+    }
+    if (lo < ne && (long long)epos[lo] == p) v = eval[lo];
+    if (p < n0) d0[p] = (uint8_t)v;
+    else if (p < n0 + n1) d1[p - n0] = (uint8_t)v;
+    else d2[p - n0 - n1] = (uint8_t)v;
+  }
+}
+
 }  // namespace glm
 
 using namespace glm;
+
+extern "C" int glm_scalex_decode(void *stream, const uint8_t *staging, int64_t staging_bytes,
+                                 const int64_t *records, int n, int64_t *device_table) {
+  glm::clear_error();
+  GLM_REQUIRE(n >= 0 && staging_bytes >= 0, GLM_ERR_INVALID_ARGUMENT,
+              "scalex_decode: negative record count or staging size");
+  if (n == 0) return GLM_OK;
+  GLM_REQUIRE(staging && records && device_table, GLM_ERR_INVALID_ARGUMENT,
+              "scalex_decode: null pointer");
+  long long max_raw = 0;
+  for (int i = 0; i < n; ++i) {
+    const int64_t *r = records + (long long)kScalexCols * i;
+    const long long off = r[0], enc = r[1], raw = r[2], primary = r[5], exc = r[6];
+    const int codec = (int)r[3];
+    GLM_REQUIRE(off >= 0 && enc >= kScalexHeader && off + enc <= staging_bytes,
+                GLM_ERR_INVALID_ARGUMENT, "scalex_decode: record %d is outside the staging buffer",
+                i);
+    GLM_REQUIRE(raw >= 1 && primary >= 0 && exc >= 0 && kScalexHeader + primary + 5 * exc == enc,
+                GLM_ERR_INVALID_ARGUMENT, "scalex_decode: record %d has an inconsistent length",
+                i);
+    const long long want = codec == 0 ? raw : codec == 1 ? (raw + 7) / 8 : (raw + 3) / 4;
+    GLM_REQUIRE(codec >= 0 && codec <= 2 && primary == want && (codec != 0 || exc == 0),
+                GLM_ERR_INVALID_ARGUMENT, "scalex_decode: record %d has a bad codec or primary size",
+                i);
+    GLM_REQUIRE(r[8] >= 0 && r[10] >= 0 && r[12] >= 0 && r[8] + r[10] + r[12] == raw,
+                GLM_ERR_INVALID_ARGUMENT, "scalex_decode: record %d destinations do not cover it",
+                i);
+    GLM_REQUIRE((r[8] == 0 || r[7]) && (r[10] == 0 || r[9]) && (r[12] == 0 || r[11]),
+                GLM_ERR_INVALID_ARGUMENT, "scalex_decode: record %d has a null destination", i);
+    max_raw = std::max(max_raw, raw);
+  }
+  const long long blocks = (max_raw + kScalexBlock - 1) / kScalexBlock;
+  GLM_REQUIRE(blocks <= 0x7fffffffll, GLM_ERR_UNSUPPORTED_SHAPE, "scalex_decode: record too large");
+  GLM_HIP_CHECK(hipMemcpyAsync(device_table, records, (size_t)n * kScalexCols * sizeof(int64_t),
+                               hipMemcpyHostToDevice, (hipStream_t)stream));
+  for (int first = 0; first < n; first += kMaxSegmentsPerLaunch) {
+    const int count = std::min(kMaxSegmentsPerLaunch, n - first);
+    hipLaunchKernelGGL(scalex_decode_kernel, dim3((unsigned)blocks, (unsigned)count),
+                       dim3(kScatterThreads), 0, (hipStream_t)stream, staging,
+                       device_table + (long long)kScalexCols * first);
+    GLM_LAUNCH_CHECK("scalex_decode_kernel");
+  }
+  return GLM_OK;
+}
 
 extern "C" int glm_file_read_ranges(const char *path, int n, const int64_t *offset,
                                     const int64_t *length, void *const *dst, int threads,

@@ -72,6 +72,7 @@ SIGNATURES = {
     "glm_rms_norm": (_i, [_p, _p, _i, _i, _p, _f, _p, _p]),
     "glm_file_read_ranges": (_i, [ctypes.c_char_p, _i, _p, _p, _p, _i, _i]),
     "glm_bank_scatter": (_i, [_p, _p, _i64, _p, _i, _p]),
+    "glm_scalex_decode": (_i, [_p, _p, _i64, _p, _i, _p]),
 }
 
 

@@ -12,7 +12,10 @@ resident in HBM here, so a layer is loaded once, in bulk:
    of native threads;
 3. one host-to-device copy moves the chunk to device staging, and
    ``glm_bank_scatter`` moves every tensor of every record to its expert's
-   slot in the stacked bank tensors.
+   slot in the stacked bank tensors.  Records of a ScaleX layer shard carry
+   their scales coded (``scale_codec.py``): their weights are scattered the
+   same way and ``glm_scalex_decode`` writes the decoded scales into the
+   bank, once, at load time (the reference decodes them in every GEMV).
 
 Two chunk buffers alternate, so the threads read chunk c + 1 while the GPU
 copies and scatters chunk c; ``load_many`` streams several layers through one
@@ -32,6 +35,9 @@ from . import _native as N
 from .contract import ContractError
 from .expert_source import NativeExpertSourcePlan, expected_shape
 from .expert_ssd import HBMExpertBank
+from .scale_codec import A_ONE_BIT, A_RAW, A_TWO_BIT, ScaleCodecError, validate_mode_a
+
+_CODECS = {"raw": A_RAW, "one_bit": A_ONE_BIT, "two_bit": A_TWO_BIT}
 
 _ALIGN = 256  # staging offset of every read: keeps 16-byte tensors 16-byte aligned
 
@@ -80,6 +86,7 @@ class ExpertBankLoader:
         self._host: list[torch.Tensor] = []
         self._dev: list[torch.Tensor] = []
         self._tables: list[torch.Tensor] = []
+        self._dtables: list[torch.Tensor] = []
         self._events: list[torch.cuda.Event | None] = []
         self._keep: list[object] = [None, None]  # host tables in flight per buffer
 
@@ -90,23 +97,27 @@ class ExpertBankLoader:
             self._dev = [torch.empty(self.chunk_bytes, dtype=torch.uint8, device=device)
                          for _ in range(2)]
             self._tables = []
+            self._dtables = []
             self._events = [None, None]
         if not self._tables or self._tables[0].numel() < 3 * segments:
             self._tables = [torch.empty(3 * max(segments, 64), dtype=torch.int64, device=device)
                             for _ in range(2)]
+        if not self._dtables or self._dtables[0].numel() < 13 * segments:
+            self._dtables = [torch.empty(13 * max(segments, 64), dtype=torch.int64, device=device)
+                             for _ in range(2)]
 
     def close(self) -> None:
         for ev in self._events:
             if ev is not None:
                 ev.synchronize()
-        self._host, self._dev, self._tables, self._events = [], [], [], []
+        self._host, self._dev, self._tables, self._dtables, self._events = [], [], [], [], []
         self._keep = [None, None]
 
-    def _chunks(self, layer: int) -> list[list[tuple[int, object]]]:
-        """The layer's (expert, read range) units in shard-offset order, packed
-        into chunks of at most chunk_bytes staged bytes (one shard per chunk)."""
-        units = [(src.expert, rng) for src in self.plan.layer_sources(layer)
-                 for rng in src.read_ranges]
+    def _chunks(self, layer: int) -> list[list[tuple[object, object]]]:
+        """The layer's (expert source, read range) units in shard-offset order,
+        packed into chunks of at most chunk_bytes staged bytes (one shard per
+        chunk)."""
+        units = [(src, rng) for src in self.plan.layer_sources(layer) for rng in src.read_ranges]
         units.sort(key=lambda u: (u[1].shard_name, u[1].absolute_offset))
         chunks: list[list[tuple[int, object]]] = []
         used = 0
@@ -177,8 +188,10 @@ class ExpertBankLoader:
             # merge records that follow each other in the file into one read
             reads: list[_Read] = []
             segments: list[tuple[int, int, int]] = []
+            coded: list[tuple[int, object]] = []  # (staging offset, ScaleX record)
             staged = 0
-            for expert, rng in chunk:
+            for src, rng in chunk:
+                expert = src.expert
                 if reads and reads[-1].offset + reads[-1].length == rng.absolute_offset:
                     at = reads[-1].staging + reads[-1].length
                     reads[-1].length += rng.byte_length
@@ -187,10 +200,22 @@ class ExpertBankLoader:
                     at = _round_up(staged, _ALIGN)
                     reads.append(_Read(rng.shard_name, rng.absolute_offset, rng.byte_length, at))
                     staged = at + rng.byte_length
-                for t in rng.tensors:
-                    dst = base[t.bank_name] + expert * slot_bytes[t.bank_name]
-                    segments.append((at + rng.relative_offset(t), dst, t.byte_length))
-                    total += t.byte_length
+                rec = src.scalex_record
+                if rec is None:
+                    for t in rng.tensors:
+                        dst = base[t.bank_name] + expert * slot_bytes[t.bank_name]
+                        segments.append((at + rng.relative_offset(t), dst, t.byte_length))
+                        total += t.byte_length
+                else:
+                    # coded scales, then the gate, down and up weights
+                    w_at = at + rec.encoded_bytes
+                    for name, n in zip(rec.weight_names, rec.weight_nbytes):
+                        key = _bank_key(name)
+                        segments.append((w_at, base[key] + expert * slot_bytes[key], n))
+                        w_at += n
+                        total += n
+                    coded.append((at, rec, expert))
+                    total += rec.decoded_bytes
             if staged > self.chunk_bytes:
                 raise AssertionError("staging chunk overflow")
             host = self._host[slot]
@@ -202,15 +227,19 @@ class ExpertBankLoader:
             N.call("glm_file_read_ranges", path.encode(), len(reads), offsets.ctypes.data,
                    lengths.ctypes.data, dsts.ctypes.data, self.threads, self.flags)
             reads_total += len(reads)
+            decode = self._decode_rows(host, coded, base, slot_bytes)
             dev = self._dev[slot]
             dev[:staged].copy_(host[:staged], non_blocking=True)
             table = np.ascontiguousarray(np.array(segments, dtype=np.int64).reshape(-1, 3))
             N.call("glm_bank_scatter", stream.cuda_stream, dev.data_ptr(), staged,
                    table.ctypes.data, table.shape[0], self._tables[slot].data_ptr())
+            if decode is not None:
+                N.call("glm_scalex_decode", stream.cuda_stream, dev.data_ptr(), staged,
+                       decode.ctypes.data, decode.shape[0], self._dtables[slot].data_ptr())
             ev = torch.cuda.Event()
             ev.record(stream)
             self._events[slot] = ev
-            self._keep[slot] = table
+            self._keep[slot] = (table, decode)
         for ev in self._events:
             if ev is not None:
                 ev.synchronize()
@@ -220,6 +249,39 @@ class ExpertBankLoader:
         return BankLoadStats(layers=tuple(layers), experts=len(layers) * self.plan.experts_per_layer,
                              bytes=total, read_bytes=read_bytes, reads=reads_total,
                              chunks=len(work), seconds=seconds)
+
+
+    def _decode_rows(self, host: torch.Tensor, coded, base, slot_bytes):
+        """The glm_scalex_decode table of a chunk's ScaleX records, each record
+        checked on the host copy first (header, codec, primary length, ascending
+        exception positions)."""
+        if not coded:
+            return None
+        buf = host.numpy()
+        rows = []
+        for at, rec, expert in coded:
+            try:
+                info = validate_mode_a(buf[at:at + rec.encoded_bytes])
+            except ScaleCodecError as exc:
+                raise ContractError(f"ScaleX record of expert {expert}: {exc}") from exc
+            if info.raw_bytes != rec.decoded_bytes or info.codec != rec.codec:
+                raise ContractError(f"ScaleX record metadata changed for expert {expert}")
+            p = info.palette
+            row = [at, rec.encoded_bytes, rec.decoded_bytes, _CODECS[info.codec],
+                   p[0] | (p[1] << 8) | (p[2] << 16) | (p[3] << 24), info.primary_bytes,
+                   info.exceptions]
+            for name, n in zip(rec.scale_names, rec.scale_nbytes):
+                key = _bank_key(name)
+                if n != slot_bytes[key]:
+                    raise ContractError(f"{name} holds {n} bytes, the bank slot {slot_bytes[key]}")
+                row += [base[key] + expert * slot_bytes[key], n]
+            rows.append(row)
+        return np.ascontiguousarray(np.array(rows, dtype=np.int64))
+
+
+def _bank_key(tensor_name: str) -> str:
+    """``...experts.<e>.<component>.<part>`` -> ``<component>.<part>``."""
+    return ".".join(tensor_name.rsplit(".", 2)[-2:])
 
 
 def plan_shard_path(plan: NativeExpertSourcePlan, shard_name: str) -> str:

@@ -120,6 +120,7 @@ class ModelContract:
         self.weight_map: dict[str, str] = dict(weight_map)
         self._headers: dict[str, tuple[int, dict[str, Any]]] = {}
         self._sources: dict[str, TensorSource] = {}
+        self._scalex: dict[str, Any] = {}
 
     @classmethod
     def from_model_dir(cls, model_dir: str | os.PathLike) -> "ModelContract":
@@ -170,15 +171,33 @@ class ModelContract:
     def shard_path(self, shard_name: str) -> Path:
         return self.model_dir / shard_name
 
+    def scalex_layout(self, shard_name: str):
+        """The ScaleX layout of a shard, or None for a native safetensors shard
+        (``contract.py:312-320``)."""
+        if shard_name not in self._scalex:
+            from .scalex_container import ScaleXContainerError, is_scalex_layer, read_scalex_layout
+            path = self.shard_path(shard_name)
+            try:
+                self._scalex[shard_name] = (read_scalex_layout(path) if is_scalex_layer(path)
+                                            else None)
+            except ScaleXContainerError as exc:
+                raise ContractError(str(exc)) from exc
+        return self._scalex[shard_name]
+
     def _header(self, shard_name: str) -> tuple[int, dict[str, Any]]:
+        """(data base, header) of a shard; for a ScaleX shard the embedded
+        original header, whose offsets address the original file
+        (``contract.py:293-310``)."""
         cached = self._headers.get(shard_name)
         if cached is not None:
             return cached
         path = self.shard_path(shard_name)
         if not path.is_file():
             raise ContractError(f"indexed shard is missing: {path}")
+        layout = self.scalex_layout(shard_name)
         try:
-            cached = local_safetensors_header(path)
+            cached = (local_safetensors_header(path) if layout is None
+                      else (layout.virtual_data_base, layout.virtual_header))
         except (OSError, ValueError) as exc:
             raise ContractError(f"cannot read safetensors header: {path}") from exc
         self._headers[shard_name] = cached
@@ -210,7 +229,10 @@ class ModelContract:
         if start < 0 or byte_length != expected:
             raise ContractError(f"invalid tensor byte range for {name}: {byte_length} != {expected}")
         absolute_offset = data_base + start
-        if absolute_offset + byte_length > self.shard_path(shard_name).stat().st_size:
+        layout = self.scalex_layout(shard_name)
+        size = (layout.original_bytes if layout is not None
+                else self.shard_path(shard_name).stat().st_size)
+        if absolute_offset + byte_length > size:
             raise ContractError(f"tensor exceeds shard size: {name}")
         source = TensorSource(name=name, shard_name=shard_name, absolute_offset=absolute_offset,
                               byte_length=byte_length, dtype=dtype, shape=shape)

@@ -6,9 +6,9 @@ per (layer, expert) the six U8 tensors in canonical order -- components
 (``contract.py:25-26``) -- with their shard byte ranges, their shape checks,
 and the expert's coalesced read ranges.  A checkpoint at the real geometry
 stores each expert as one contiguous 13,369,344-byte record, so one read
-covers it (``expert_source.py:365-381``).  The reference's ScaleX Mode-B
-re-encoded shards (``expert_source.py:296-337``) are not supported: only the
-native MXFP4 layout is planned here.
+covers it (``expert_source.py:365-381``).  In a ScaleX layer shard an expert is
+one physical record too -- its coded scales then its gate, down and up weights
+(``expert_source.py:306-337``) -- read as one range.
 """
 
 from __future__ import annotations
@@ -76,6 +76,7 @@ class NativeExpertSource:
     expert: int
     tensors: tuple[ExpertTensorSource, ...]
     read_ranges: tuple[ExpertReadRange, ...]
+    scalex_record: object = None  # a ScaleXRecord for a ScaleX shard
 
     @property
     def payload_bytes(self) -> int:
@@ -133,14 +134,24 @@ class NativeExpertSourcePlan:
 
     @property
     def scalex_mode_b(self) -> bool:
-        return False
+        return bool(self.packs) and self.packs[0].scalex_record is not None
 
     @property
     def source_format(self) -> str:
-        return "native_mxfp4"
+        return "livglm_scalex_mode_b" if self.scalex_mode_b else "native_mxfp4"
 
     def slot_bytes(self, layer: int) -> int:
-        sizes = {self.expert(layer, e).payload_bytes for e in range(self.experts_per_layer)}
+        """Bytes of one slot row as the reference sizes it (``expert_source.py:112-130``):
+        weights plus the largest Mode-B row for ScaleX layers.  The HBM bank
+        itself always holds decoded scales (``payload_bytes``)."""
+        sources = self.layer_sources(layer)
+        if self.scalex_mode_b:
+            if any(s.scalex_record is None for s in sources):
+                raise ContractError(f"layer {layer} mixes ScaleX and native experts")
+            weights = sum(t.byte_length for t in sources[0].tensors
+                          if t.destination_name.endswith(".weight"))
+            return weights + max(s.scalex_record.mode_b_row_bytes for s in sources)
+        sizes = {s.payload_bytes for s in sources}
         if len(sizes) != 1:
             raise ContractError(f"layer {layer} expert row sizes are not uniform")
         return next(iter(sizes))
@@ -267,22 +278,43 @@ def build_native_expert_source_plan(contract: ModelContract, config: GLMTextConf
                             f"native MXFP4 shape mismatch for {name}: {source.shape} != {want}")
                     tensors.append(_destination(source, component, part))
             tensor_tuple = tuple(tensors)
-            if len({t.shard_name for t in tensor_tuple}) != 1:
+            shards = {t.shard_name for t in tensor_tuple}
+            if len(shards) != 1:
                 raise ContractError(f"expert {layer}/{expert} spans multiple shards")
+            shard = shards.pop()
+            layout = contract.scalex_layout(shard)
+            record = None
+            if layout is None:
+                ranges = coalesce(tensor_tuple)
+            else:
+                if layout.layer != layer:
+                    raise ContractError(f"ScaleX layer identity changed: {layout.layer} != {layer}")
+                try:
+                    record = layout.record(expert)
+                except Exception as exc:  # ScaleXContainerError
+                    raise ContractError(str(exc)) from exc
+                by_name = {t.source_name: t for t in tensor_tuple}
+                ranges = (ExpertReadRange(shard, record.absolute_offset, record.physical_bytes,
+                                          tuple(by_name[n] for n in record.weight_names)),)
             packs.append(NativeExpertSource(layer=layer, expert=expert, tensors=tensor_tuple,
-                                            read_ranges=coalesce(tensor_tuple)))
+                                            read_ranges=ranges, scalex_record=record))
     plan = NativeExpertSourcePlan(model_dir=str(contract.model_dir), first_layer=first_layer,
                                   last_layer=last_layer,
                                   experts_per_layer=config.n_routed_experts, packs=tuple(packs))
     expected = (last_layer - first_layer + 1) * config.n_routed_experts
     if plan.expert_count != expected or plan.tensor_count != expected * 6:
         raise ContractError("native expert source inventory is incomplete")
+    if len({p.scalex_record is not None for p in plan.packs}) != 1:
+        raise ContractError("routed layers mix ScaleX and native MXFP4 shards")
     if (first_layer == FIRST_MOE_LAYER and last_layer == LAST_MAIN_LAYER
             and config.n_routed_experts == EXPERTS_PER_LAYER):
         if plan.uniform_pack_bytes != REAL_EXPERT_RECORD_BYTES:
             raise ContractError(f"native expert record size changed: {plan.uniform_pack_bytes}")
         if plan.uniform_read_count != 1:
             raise ContractError("native GLM experts are no longer exact one-range records")
-        if plan.read_bytes != plan.payload_bytes:
+        if plan.scalex_mode_b:
+            if plan.read_bytes >= plan.payload_bytes:
+                raise ContractError("ScaleX expert payload did not shrink")
+        elif plan.read_bytes != plan.payload_bytes:
             raise ContractError("native GLM expert read bytes changed")
     return plan

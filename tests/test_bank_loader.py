@@ -238,7 +238,7 @@ def test_loader_chunks_cover_each_record_once(tmp_path):
                                            first_layer=3, last_layer=3)
     loader = ExpertBankLoader(plan, chunk_bytes=3 * RECORD)
     chunks = loader._chunks(3)
-    units = [(e, r.absolute_offset, r.shard_name) for c in chunks for e, r in c]
+    units = [(src.expert, r.absolute_offset, r.shard_name) for c in chunks for src, r in c]
     assert sorted(e for e, _, _ in units) == list(range(E))
     for c in chunks:
         assert len({r.shard_name for _, r in c}) == 1

@@ -124,3 +124,35 @@ def test_bank_scatter_segments_of_any_alignment(gu):
     with pytest.raises(gu.native.NativeError, match="outside"):
         gu.native.call("glm_bank_scatter", gu.stream(), staging.data_ptr(), staging_np.size,
                        bad.ctypes.data, 1, dtab.data_ptr())
+
+
+@pytest.mark.parametrize("scales", ["two_value", "uniform"])
+def test_scalex_layer_loads_the_same_bank(gu, tmp_path, scales):
+    """A ScaleX layer shard (coded scales, decoded on the GPU while loading)
+    fills the bank with exactly the bytes of the native checkpoint.  "uniform"
+    scales make the codec keep raw records; "two_value" ones code one bit per
+    scale with exceptions."""
+    from glm53flash.bank_loader import ExpertBankLoader
+    from glm53flash.expert_ssd import HBMExpertBank
+    E, d, I, layers = 10, 512, 256, (5, 6)
+    print(f"scalex loader: scales={scales} E={E} d={d} I={I}", flush=True)
+    arrays = make_checkpoint(str(tmp_path), layers=layers, E=E, d=d, I=I, extras=False,
+                             shuffle=False, scales=scales, scalex=True, seed=5320)
+    plan = _plan(str(tmp_path), E, d, I, layers)
+    assert plan.scalex_mode_b
+    codecs = {p.scalex_record.codec for p in plan.packs}
+    assert codecs == ({"one_bit"} if scales == "two_value" else {"raw"})
+    record = plan.packs[0].scalex_record.physical_bytes
+    loader = ExpertBankLoader(plan, threads=4, chunk_bytes=3 * record + 4096)
+    banks = [HBMExpertBank(layer=layer, num_experts=E, hidden_size=d, intermediate_size=I,
+                           swiglu_limit=10.0, device="cuda") for layer in layers]
+    stats = loader.load_many(banks)
+    assert stats.bytes == len(layers) * E * 3 * I * d * 17 // 32
+    assert stats.read_bytes < stats.bytes or scales == "uniform"
+    for layer, bank in zip(layers, banks):
+        for comp in COMPONENTS:
+            for part in PARTS:
+                got = gu.host(bank.tensors[f"{comp}.{part}"])
+                want = np.stack([arrays[(layer, e)][(comp, part)] for e in range(E)])
+                assert np.array_equal(got, want), (layer, comp, part)
+    loader.close()
