@@ -63,6 +63,8 @@ def parse_args():
                     help="bank_load: layers of the synthetic checkpoint (320 MB each)")
     ap.add_argument("--load-threads", type=int, default=16,
                     help="bank_load: native read threads")
+    ap.add_argument("--scalex", type=int, default=0,
+                    help="bank_load: 1 = ScaleX layer shards (coded scales, decoded on the GPU)")
     # internal: the child runs of the counter passes
     ap.add_argument("--mode", default="full", choices=["full", "kernel", "copy"],
                     help=argparse.SUPPRESS)
@@ -520,7 +522,14 @@ def bank_load_bench(args, torch, np) -> int:
     root = tempfile.mkdtemp(prefix="glm_ckpt_", dir=os.environ.get("TMPDIR", "/tmp"))
     try:
         t0 = time.perf_counter()
-        payload = write_expert_checkpoint(root, shape, layers, args.seed)
+        payload = write_expert_checkpoint(root, shape, layers, args.seed,
+                                          two_value_scales=bool(args.scalex))
+        if args.scalex:
+            from glm53flash.scalex_container import compress_scalex_layer
+            for layer in layers:
+                shard = os.path.join(root, f"model-layer{layer:02d}.safetensors")
+                compress_scalex_layer(shard, shard + ".sx", layer=layer, experts=shape.E)
+                os.replace(shard + ".sx", shard)
         print(f"bank_load: wrote {payload / 1e9:.2f} GB in {time.perf_counter() - t0:.1f} s",
               file=sys.stderr, flush=True)
         cfg = GLMTextConfig(hidden_size=shape.d, moe_intermediate_size=shape.I,
@@ -562,18 +571,32 @@ def bank_load_bench(args, torch, np) -> int:
         print(f"bank_load: storage -> HBM {payload / cold_s / 1e9:.2f} GB/s", file=sys.stderr,
               flush=True)
         # every slot of the first and the last layer against the shard bytes
-        blob = np.fromfile(os.path.join(root, shards[0]), dtype=np.uint8,
-                           offset=plan.expert(layers[0], 0).read_ranges[0].absolute_offset)
-        blob = blob[:shape.E * shape.expert_bytes].reshape(shape.E, shape.expert_bytes)
-        checked = 0
-        for b in (banks[0], banks[-1]):
-            for t in plan.expert(b.layer, 0).tensors:
-                rel = t.absolute_offset - plan.expert(b.layer, 0).read_ranges[0].absolute_offset
-                want = blob[:, rel:rel + t.byte_length]
-                got = b.tensors[t.bank_name].cpu().numpy().reshape(shape.E, -1)
-                if not np.array_equal(got, want):
-                    raise SystemExit(f"bank_load: layer {b.layer} {t.bank_name} differs")
-                checked += want.size
+        # (a ScaleX shard: against the tensors its reader rebuilds)
+        if args.scalex:
+            from glm53flash.scalex_container import read_scalex_layout, read_scalex_tensor
+            checked = 0
+            for b in (banks[0], banks[-1]):
+                layout = read_scalex_layout(os.path.join(root, shards[0 if b is banks[0] else -1]))
+                for e in (0, shape.E // 2, shape.E - 1):
+                    for t in plan.expert(b.layer, e).tensors:
+                        want = np.frombuffer(read_scalex_tensor(layout, t.source_name), np.uint8)
+                        got = b.tensors[t.bank_name][e].cpu().numpy().reshape(-1)
+                        if not np.array_equal(got, want):
+                            raise SystemExit(f"bank_load: layer {b.layer} {t.source_name} differs")
+                        checked += want.size
+        else:
+            blob = np.fromfile(os.path.join(root, shards[0]), dtype=np.uint8,
+                               offset=plan.expert(layers[0], 0).read_ranges[0].absolute_offset)
+            blob = blob[:shape.E * shape.expert_bytes].reshape(shape.E, shape.expert_bytes)
+            checked = 0
+            for b in (banks[0], banks[-1]):
+                for t in plan.expert(b.layer, 0).tensors:
+                    rel = t.absolute_offset - plan.expert(b.layer, 0).read_ranges[0].absolute_offset
+                    want = blob[:, rel:rel + t.byte_length]
+                    got = b.tensors[t.bank_name].cpu().numpy().reshape(shape.E, -1)
+                    if not np.array_equal(got, want):
+                        raise SystemExit(f"bank_load: layer {b.layer} {t.bank_name} differs")
+                    checked += want.size
         # host side alone: the native reader into pinned memory
         host = torch.empty(chunk, dtype=torch.uint8, pin_memory=True)
         rng0 = plan.expert(layers[0], 0).read_ranges[0].absolute_offset
@@ -603,13 +626,13 @@ def bank_load_bench(args, torch, np) -> int:
         # the scatter kernel alone: the experts of one staged chunk into bank
         # 0, 8 launches between HIP events
         n_exp = min(shape.E, chunk // shape.expert_bytes)
-        segs = []
+        segs = []  # records staged back to back in the checkpoint's tensor order
         for e in range(n_exp):
-            for tns in plan.expert(layers[0], e).tensors:
-                rel = tns.absolute_offset - rng0
-                bank_t = banks[0].tensors[tns.bank_name]
-                segs.append((rel, bank_t.data_ptr() + e * (bank_t.numel() // shape.E),
-                             tns.byte_length))
+            rel = e * shape.expert_bytes
+            for key, bank_t in banks[0].tensors.items():
+                n_slot = bank_t.numel() // shape.E
+                segs.append((rel, bank_t.data_ptr() + e * n_slot, n_slot))
+                rel += n_slot
         table = np.array(segs, dtype=np.int64)
         dtab = torch.empty(table.size, dtype=torch.int64, device="cuda")
         staged = n_exp * shape.expert_bytes
@@ -644,7 +667,10 @@ def bank_load_bench(args, torch, np) -> int:
         "config": {
             "workload": (f"bank_load: {len(layers)} layers x {shape.E} experts x "
                          f"{shape.expert_bytes} B (MXFP4 d={shape.d} I={shape.I}), one "
-                         f"safetensors shard per layer, read from the page cache"),
+                         + ("ScaleX layer shard per layer (scales coded, decoded on the GPU)"
+                            if args.scalex else "safetensors shard per layer")
+                         + ", read from the page cache"),
+            "read_bytes": stats.read_bytes,
             "payload_bytes": payload, "read_threads": args.load_threads, "chunk_bytes": chunk,
             "reads": stats.reads, "chunks": stats.chunks,
             "verified_bytes": checked,

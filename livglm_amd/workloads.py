@@ -138,12 +138,16 @@ BANK_KEYS = ("gate_proj.weight_packed", "gate_proj.weight_scale", "up_proj.weigh
              "up_proj.weight_scale", "down_proj.weight_packed", "down_proj.weight_scale")
 
 
-def write_expert_checkpoint(root: str, shape: MoEShape, layers, seed: int) -> int:
+def write_expert_checkpoint(root: str, shape: MoEShape, layers, seed: int,
+                            two_value_scales: bool = False) -> int:
     """Writes a routed-expert checkpoint for ``layers`` (one safetensors shard
     per layer, experts in id order, each expert's six U8 tensors adjacent in
     the reference's canonical order) plus ``model.safetensors.index.json`` and
     ``config.json``.  Every layer stores the same random bank (one layer's
-    bytes drawn once); returns the payload bytes written."""
+    bytes drawn once); returns the payload bytes written.  Scales are uniform
+    bytes, or with ``two_value_scales`` 120/121 with 1 % of other values in
+    [119, 127] (the mix of the real checkpoint, which ScaleX codes with one bit
+    per scale)."""
     import json
     import os
     import struct
@@ -157,6 +161,16 @@ def write_expert_checkpoint(root: str, shape: MoEShape, layers, seed: int) -> in
         parts.append((comp, "weight_scale", (rows, cols // 32)))
     record = sum(r * c for _, _, (r, c) in parts)
     blob = rng.integers(0, 256, E * record, dtype=np.uint8)
+    if two_value_scales:
+        rec = blob.reshape(E, record)
+        at = 0
+        for _, part, (r, c) in parts:
+            if part == "weight_scale":
+                sc = rng.choice(np.array([120, 121], np.uint8), (E, r * c))
+                odd = rng.random((E, r * c)) < 0.01
+                sc[odd] = rng.integers(119, 128, int(odd.sum()), dtype=np.uint8)
+                rec[:, at:at + r * c] = sc
+            at += r * c
     os.makedirs(root, exist_ok=True)
     weight_map = {}
     for layer in layers:
