@@ -153,3 +153,38 @@ def test_prefill_entry_points_reject_bad_shapes(lib):
     # the token-major gate/up takes at most 4 tokens and 8 experts per token
     _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_route_gate_up", None, fake, fake, 5, 128, 8, 1,
             1, 1, 2.5, fake, 2048, 768, fake, fake, fake, fake, 10.0, fake, fake, fake)
+
+
+def test_ffn_site_and_loader_entry_points_reject_bad_arguments(lib):
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    assert lib.glm_hc_workspace_bytes(2, 4, 2048) == 32 * 2 * 25 * 4
+    assert lib.glm_hc_workspace_bytes(2, 9, 2048) == 0
+    msg = _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_hc_pre", None, fake, 2, 9, 2048, fake,
+                  fake, fake, 20, 1e-6, 1e-6, None, 1e-6, 0, fake, 1 << 20, fake, fake, None, None)
+    assert "hc_mult" in msg
+    _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_hc_pre", None, fake, 2, 4, 2050, fake, fake,
+            fake, 20, 1e-6, 1e-6, None, 1e-6, 0, fake, 1 << 20, fake, fake, None, None)
+    _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_hc_pre", None, fake, 2, 4, 2048, fake, fake,
+            fake, 0, 1e-6, 1e-6, None, 1e-6, 0, fake, 1 << 20, fake, fake, None, None)
+    _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_hc_pre", None, fake, 2, 4, 2048, fake, fake,
+            fake, 20, 1e-6, 1e-6, None, 1e-6, 4, fake, 1 << 20, fake, fake, None, None)
+    _expect(native.GLM_ERR_WORKSPACE, "glm_hc_pre", None, fake, 2, 4, 2048, fake, fake, fake, 20,
+            1e-6, 1e-6, None, 1e-6, 0, fake, 64, fake, fake, None, None)
+    _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_hc_post", None, None, 2, 4, 2048, fake, fake,
+            fake, 0, fake)
+    _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_rms_norm", None, fake, 2, 30, None, 1e-6,
+            fake, None)
+    # a segment past the staging buffer, and a ScaleX record whose lengths disagree
+    seg = (ctypes.c_int64 * 3)(100, 0x2000, 200)
+    msg = _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_bank_scatter", None, fake, 256,
+                  ctypes.cast(seg, ctypes.c_void_p), 1, fake)
+    assert "outside" in msg
+    rec = (ctypes.c_int64 * 13)(0, 24 + 8 + 5, 64, 1, 0, 9, 1, 0x2000, 64, 0x3000, 0, 0x4000, 0)
+    msg = _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_scalex_decode", None, fake, 4096,
+                  ctypes.cast(rec, ctypes.c_void_p), 1, fake)
+    assert "length" in msg
+    rec[5] = 8
+    rec[8] = 63  # destinations cover 63 of 64 bytes
+    msg = _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_scalex_decode", None, fake, 4096,
+                  ctypes.cast(rec, ctypes.c_void_p), 1, fake)
+    assert "cover" in msg
