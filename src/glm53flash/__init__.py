@@ -1,8 +1,10 @@
 """MI355X-native routed-MoE layer for livglm's GLM-5.3-Flash.
 
 Host-side mirror of the reference's MoE interface (``moe.py``, ``expert_ssd.py``,
-``layers.py``) on torch tensors, computed by the HIP library ``libglm53moe.so``
-(``livglm_amd``).  Every expert is resident in HBM.
+``layers.py``), of the decoder FFN site around it (``mhc.py``, ``model.py``) and
+of its checkpoint side (``contract.py``, ``expert_source.py``, ``scale_codec.py``,
+``scalex_container.py``) on torch tensors, computed by the HIP library
+``libglm53moe.so`` (``livglm_amd``).  Every expert is resident in HBM.
 """
 
 __all__ = [
@@ -11,6 +13,10 @@ __all__ = [
     "expert_source",
     "expert_ssd",
     "layers",
+    "mhc",
+    "model",
     "model_config",
     "moe",
+    "scale_codec",
+    "scalex_container",
 ]

@@ -14,7 +14,7 @@ import torch
 
 from . import _native as N
 from .contract import ContractError
-from .layers import RMSNorm, _f32_param, require_weight
+from .layers import RMSNorm, _f32_param
 from .model_config import GLMTextConfig
 
 _STREAM_DTYPES = (torch.float32, torch.bfloat16)
@@ -119,4 +119,4 @@ def hyper_residual(residual: torch.Tensor, sublayer_output: torch.Tensor, post: 
     return out.reshape(residual.shape)
 
 
-__all__ = ["HyperConnection", "hyper_residual", "require_weight"]
+__all__ = ["HyperConnection", "hyper_residual"]
