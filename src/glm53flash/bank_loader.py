@@ -17,8 +17,8 @@ resident in HBM here, so a layer is loaded once, in bulk:
    same way and ``glm_scalex_decode`` writes the decoded scales into the
    bank, once, at load time (the reference decodes them in every GEMV).
 
-Two chunk buffers alternate, so the threads read chunk c + 1 while the GPU
-copies and scatters chunk c; ``load_many`` streams several layers through one
+Three chunk buffers rotate, so the threads read chunks c + 1 and c + 2 while
+the GPU copies and scatters chunk c; ``load_many`` streams several layers through one
 pipeline, so it drains once, at the end.
 """
 
@@ -67,16 +67,19 @@ class _Read:
 
 class ExpertBankLoader:
     """Loads whole layers of a :class:`NativeExpertSourcePlan` into
-    :class:`HBMExpertBank` objects.  The staging buffers (two pinned host and
-    two device chunks of ``chunk_bytes``) are allocated on first use and kept
+    :class:`HBMExpertBank` objects.  The staging buffers (``buffers`` pinned
+    host and device chunks of ``chunk_bytes``) are allocated on first use and kept
     for later layers; ``close()`` releases them."""
 
     def __init__(self, plan: NativeExpertSourcePlan, *, threads: int = 16,
-                 chunk_bytes: int = 64 << 20, drop_cache: bool = False):
+                 chunk_bytes: int = 64 << 20, drop_cache: bool = False, buffers: int = 3):
         if threads < 1:
             raise ContractError("the loader needs at least one read thread")
         if chunk_bytes < _ALIGN:
             raise ContractError(f"chunk_bytes must be at least {_ALIGN}")
+        if buffers < 2:
+            raise ContractError("the loader needs at least two staging buffers")
+        self.nbuf = int(buffers)
         self.plan = plan
         self.threads = int(threads)
         largest = max((r.byte_length for p in plan.packs for r in p.read_ranges), default=0)
@@ -88,30 +91,30 @@ class ExpertBankLoader:
         self._tables: list[torch.Tensor] = []
         self._dtables: list[torch.Tensor] = []
         self._events: list[torch.cuda.Event | None] = []
-        self._keep: list[object] = [None, None]  # host tables in flight per buffer
+        self._keep: list[object] = [None] * self.nbuf  # host tables in flight per buffer
 
     def _buffers(self, device: torch.device, segments: int) -> None:
         if not self._host or self._dev[0].device != device:
             self._host = [torch.empty(self.chunk_bytes, dtype=torch.uint8, pin_memory=True)
-                          for _ in range(2)]
+                          for _ in range(self.nbuf)]
             self._dev = [torch.empty(self.chunk_bytes, dtype=torch.uint8, device=device)
-                         for _ in range(2)]
+                         for _ in range(self.nbuf)]
             self._tables = []
             self._dtables = []
-            self._events = [None, None]
+            self._events = [None] * self.nbuf
         if not self._tables or self._tables[0].numel() < 3 * segments:
             self._tables = [torch.empty(3 * max(segments, 64), dtype=torch.int64, device=device)
-                            for _ in range(2)]
+                            for _ in range(self.nbuf)]
         if not self._dtables or self._dtables[0].numel() < 13 * segments:
             self._dtables = [torch.empty(13 * max(segments, 64), dtype=torch.int64, device=device)
-                             for _ in range(2)]
+                             for _ in range(self.nbuf)]
 
     def close(self) -> None:
         for ev in self._events:
             if ev is not None:
                 ev.synchronize()
         self._host, self._dev, self._tables, self._dtables, self._events = [], [], [], [], []
-        self._keep = [None, None]
+        self._keep = [None] * self.nbuf
 
     def _chunks(self, layer: int) -> list[list[tuple[object, object]]]:
         """The layer's (expert source, read range) units in shard-offset order,
@@ -182,9 +185,9 @@ class ExpertBankLoader:
         t0 = time.perf_counter()
         total = reads_total = 0
         for c, (base, slot_bytes, chunk) in enumerate(work):
-            slot = c % 2
+            slot = c % self.nbuf
             if self._events[slot] is not None:
-                self._events[slot].synchronize()  # buffers of chunk c - 2 are free again
+                self._events[slot].synchronize()  # the buffers of chunk c - nbuf are free again
             # merge records that follow each other in the file into one read
             reads: list[_Read] = []
             segments: list[tuple[int, int, int]] = []
