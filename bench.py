@@ -333,9 +333,17 @@ def main() -> int:
                         b["hc.fn"].data_ptr(), b["hc.base"].data_ptr(), b["hc.scale"].data_ptr(),
                         20, 1e-6, 1e-6, b["norm.weight"].data_ptr(), 1e-6, 0, hc_ws.data_ptr(),
                         hc_ws.numel(), post.data_ptr(), comb.data_ptr(), None, normed.data_ptr())
-            moe(normed, s % S.n_banks, s)
-            native.call("glm_hc_post", S.stream, streams.data_ptr(), T, hc, d, out.data_ptr(),
-                        post.data_ptr(), comb.data_ptr(), 0, site_out.data_ptr())
+            # the MoE layer with hyper_residual in its last kernel
+            lb = s % S.n_banks
+            native.call(
+                "glm_moe_forward_hc", S.stream, normed.data_ptr(), T, d,
+                b["router_weight"].data_ptr(), S.bias(s, lb).data_ptr(), E, k, shape.n_group,
+                shape.topk_group, int(shape.norm_topk_prob), shape.routed_scaling_factor, I,
+                *(b[key].data_ptr() for key in keys), Is, native.GLM_FMT_BF16,
+                b["shared.gate"].data_ptr(), None, b["shared.up"].data_ptr(), None,
+                b["shared.down"].data_ptr(), None, None, shape.swiglu_limit, ws.data_ptr(),
+                ws_bytes, out.data_ptr(), wts.data_ptr(), idx.data_ptr(), streams.data_ptr(), hc,
+                post.data_ptr(), comb.data_ptr(), 0, site_out.data_ptr())
 
     act = torch.empty((T, d), dtype=torch.bfloat16, device=S.dev)
 

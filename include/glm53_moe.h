@@ -339,6 +339,31 @@ int glm_hc_post(void *stream, const float *residual, int T, int hc, int d, const
                 const float *post, const float *comb, int flags, float *out);
 
 /*
+ * glm_moe_forward followed by the FFN site's hyper_residual (model.py:136,
+ * mhc.py:51-60) on its output:
+ *   hc_out[t][j] = post[t][j] * out[t] + sum_i comb[t][i][j] * residual[t][i]
+ * residual f32 [T][hc][d] (the streams the site started from), post f32
+ * [T][hc] and comb f32 [T][hc][hc] from glm_hc_pre; hc_out f32 [T][hc][d];
+ * flags as glm_hc_post.  `out` is written too.  On the few-token path the
+ * update runs inside the layer's last kernel (one launch less than
+ * glm_moe_forward + glm_hc_post); otherwise it is a separate launch.  Same
+ * limits as glm_moe_forward, hc <= 8.
+ */
+int glm_moe_forward_hc(void *stream, const uint16_t *x, int T, int d, const float *router_weight,
+                       const float *router_bias, int E, int top_k, int n_group, int topk_group,
+                       int norm_topk_prob, float routed_scaling_factor, int I,
+                       const uint8_t *gate_packed, const uint8_t *gate_scales,
+                       const uint8_t *up_packed, const uint8_t *up_scales,
+                       const uint8_t *down_packed, const uint8_t *down_scales, int I_shared,
+                       int shared_fmt, const void *shared_gate, const uint8_t *shared_gate_scales,
+                       const void *shared_up, const uint8_t *shared_up_scales,
+                       const void *shared_down, const uint8_t *shared_down_scales,
+                       const uint16_t *shared_in, float swiglu_limit, void *workspace,
+                       size_t workspace_bytes, float *out, float *weights_out,
+                       uint32_t *indices_out, const float *residual, int hc, const float *post,
+                       const float *comb, int flags, float *hc_out);
+
+/*
  * RMSNorm (layers.py:119-131) and UnweightedRMSNorm (layers.py:134-140) of
  * f32 rows: out = x * (1 / sqrt(mean(x^2) + eps)) * weight (weight f32 [d] or
  * NULL); written as f32 (out) and/or rounded to bf16 (out_bf16).  d % 4 == 0.

@@ -17,6 +17,14 @@ namespace glm {
 void set_error(const char *fmt, ...);
 void clear_error();
 
+// hyper_residual of the decoder FFN site, fused into the MoE layer's last
+// kernel (glm_moe_forward_hc): out[t][j] = post[t][j] y[t] + sum_i comb[t][i][j] res[t][i]
+struct HcFuse {
+  const float *res, *post, *comb;  // [T][hc][d], [T][hc], [T][hc][hc]
+  float *out;                      // [T][hc][d]
+  int hc, bf16;                    // bf16: GLM_HC_BF16_STREAMS rounding points
+};
+
 }  // namespace glm
 
 #define GLM_REQUIRE(cond, code, ...)  \

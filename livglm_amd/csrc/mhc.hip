@@ -453,6 +453,20 @@ extern "C" int glm_hc_pre(void *stream, const float *streams, int T, int hc, int
   return GLM_OK;
 }
 
+// hyper_residual launch for the MoE forward's paths that do not fuse it
+int glm_hc_post_launch(hipStream_t stream, const glm::HcFuse &f, const float *y, int T, int d) {
+  const int per_block = 4 * kHcThreads;
+  const dim3 grid((d + per_block - 1) / per_block, T);
+  if (f.bf16)
+    hipLaunchKernelGGL(hc_post_kernel<true>, grid, dim3(kHcThreads), 0, stream, f.res, y, f.post,
+                       f.comb, f.hc, d, f.out);
+  else
+    hipLaunchKernelGGL(hc_post_kernel<false>, grid, dim3(kHcThreads), 0, stream, f.res, y, f.post,
+                       f.comb, f.hc, d, f.out);
+  GLM_LAUNCH_CHECK("hc_post_kernel");
+  return GLM_OK;
+}
+
 extern "C" int glm_hc_post(void *stream, const float *residual, int T, int hc, int d,
                            const float *y, const float *post, const float *comb, int flags,
                            float *out) {

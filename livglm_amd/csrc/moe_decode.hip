@@ -594,7 +594,14 @@ struct PairDownArgs {
   const float *shared_parts;   // its f32 K-range partial sums [nparts][T][d], or neither
   int nparts;
   float *out;  // [T][d] f32
+  // optional hyper_residual of the decoder FFN site (hc_out != nullptr):
+  // hc_out[t][j] = post[t][j] out[t] + sum_i comb[t][i][j] hc_res[t][i]
+  const float *hc_res, *hc_post, *hc_comb;  // [T][hc][d], [T][hc], [T][hc][hc]
+  float *hc_out;                            // [T][hc][d]
+  int hc, hc_bf16;                          // hc_bf16: bf16 streams (GLM_HC_BF16_STREAMS)
 };
+
+constexpr int kPairMaxHc = 8;
 
 // Down projection of all k experts of one token on 16 rows of d, merged in
 // the combine's order: out = sum_j f32(bf16(y_j)) * w_j (sequential j, no
@@ -645,6 +652,22 @@ __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
   // the shared expert's contribution to these 16 outputs (thread c < 16)
   float shared_v = 0.0f;
   const int c = row0 + threadIdx.x;
+  // the FFN site's residual streams for these outputs, and its gates
+  __shared__ float s_hc[kPairMaxHc + kPairMaxHc * kPairMaxHc];
+  float rv[kPairMaxHc];
+  const int hc = a.hc;
+  if (a.hc_out != nullptr) {
+    if (threadIdx.x < 16) {
+#pragma unroll
+      for (int i = 0; i < kPairMaxHc; ++i)
+        rv[i] = i < hc ? a.hc_res[((size_t)t * hc + i) * d + c] : 0.0f;
+    }
+    const int ns = hc + hc * hc;
+    if ((int)threadIdx.x >= 64 && (int)threadIdx.x < 64 + ns) {
+      const int i = threadIdx.x - 64;
+      s_hc[i] = i < hc ? a.hc_post[(size_t)t * hc + i] : a.hc_comb[(size_t)t * hc * hc + i - hc];
+    }
+  }
   if (threadIdx.x < 16) {
     if (a.shared_parts != nullptr) {
       float sp = a.shared_parts[(size_t)t * d + c];
@@ -670,6 +693,26 @@ __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
     for (int jj = 0; jj < k; ++jj) o = o + s_p[jj][threadIdx.x];
     if (a.shared_parts != nullptr || a.shared != nullptr) o = o + shared_v;
     a.out[(size_t)t * d + c] = o;
+    if (a.hc_out != nullptr) {
+      // hyper_residual (mhc.py:51-60): the placement and the mixing sum
+      // rounded as separate operations; bf16 streams round post, comb and the
+      // mixing sum to bf16
+      for (int jj = 0; jj < hc; ++jj) {
+        float pj = s_hc[jj];
+        if (a.hc_bf16) pj = bf16_round(pj);
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kPairMaxHc; ++i) {
+          if (i < hc) {
+            float w = s_hc[hc + i * hc + jj];
+            if (a.hc_bf16) w = bf16_round(w);
+            m = m + w * rv[i];
+          }
+        }
+        if (a.hc_bf16) m = bf16_round(m);
+        a.hc_out[((size_t)t * hc + jj) * d + c] = pj * o + m;
+      }
+    }
   }
 }
 
@@ -934,7 +977,8 @@ int glm_pair_path_launch(hipStream_t stream, const uint16_t *x, int T, int d, co
                          const uint8_t *us, const uint8_t *dw, const uint8_t *ds,
                          const uint16_t *sg, const uint16_t *su, const uint16_t *sd, int Is,
                          float *gp, float *up, uint16_t *hs, float *yp,
-                         const uint16_t *shared_ready, uint16_t *h, float limit, float *out) {
+                         const uint16_t *shared_ready, uint16_t *h, float limit, float *out,
+                         const glm::HcFuse *hc) {
   RouteArgs ra{};
   ra.x = x;
   ra.w = w;
@@ -990,6 +1034,14 @@ int glm_pair_path_launch(hipStream_t stream, const uint16_t *x, int T, int d, co
   b.shared_parts = sg ? yp : nullptr;
   b.nparts = sg ? sh.skd : 0;
   b.out = out;
+  if (hc != nullptr) {
+    b.hc_res = hc->res;
+    b.hc_post = hc->post;
+    b.hc_comb = hc->comb;
+    b.hc_out = hc->out;
+    b.hc = hc->hc;
+    b.hc_bf16 = hc->bf16;
+  }
   const size_t lds3 = (size_t)k * lds_row_stride(I) * 2;
   const dim3 g3(T * (d / 16)), b3(64 * std::max(k, 4));
   switch (I / 128) {

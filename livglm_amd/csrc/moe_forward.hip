@@ -77,7 +77,8 @@ int glm_pair_path_launch(hipStream_t stream, const uint16_t *x, int T, int d, co
                          const uint8_t *us, const uint8_t *dw, const uint8_t *ds,
                          const uint16_t *sg, const uint16_t *su, const uint16_t *sd, int Is,
                          float *gp, float *up, uint16_t *hs, float *yp,
-                         const uint16_t *shared_ready, uint16_t *h, float limit, float *out);
+                         const uint16_t *shared_ready, uint16_t *h, float limit, float *out,
+                         const glm::HcFuse *hc);
 int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d, const float *w,
                             const float *bias, int E, int k, int n_group, int topk_group,
                             int norm, float scale, float *logits, float *weights,
@@ -198,6 +199,22 @@ extern "C" int glm_moe_workspace_init(void *stream, void *workspace, size_t work
   return glm_fill_zero_launch((hipStream_t)stream, workspace, workspace_bytes);
 }
 
+int glm_hc_post_launch(hipStream_t stream, const glm::HcFuse &f, const float *y, int T, int d);
+
+static int moe_forward_core(void *stream_v, const uint16_t *x, int T, int d,
+                            const float *router_weight, const float *router_bias, int E,
+                            int top_k, int n_group, int topk_group, int norm_topk_prob,
+                            float routed_scaling_factor, int I, const uint8_t *gate_packed,
+                            const uint8_t *gate_scales, const uint8_t *up_packed,
+                            const uint8_t *up_scales, const uint8_t *down_packed,
+                            const uint8_t *down_scales, int I_shared, int shared_fmt,
+                            const void *shared_gate, const uint8_t *shared_gate_scales,
+                            const void *shared_up, const uint8_t *shared_up_scales,
+                            const void *shared_down, const uint8_t *shared_down_scales,
+                            const uint16_t *shared_in, float swiglu_limit, void *workspace,
+                            size_t workspace_bytes, float *out, float *weights_out,
+                            uint32_t *indices_out, const glm::HcFuse *hc, bool *hc_done);
+
 extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
                                const float *router_weight, const float *router_bias, int E,
                                int top_k, int n_group, int topk_group, int norm_topk_prob,
@@ -212,6 +229,66 @@ extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
                                size_t workspace_bytes, float *out, float *weights_out,
                                uint32_t *indices_out) {
   glm::clear_error();
+  bool done = false;
+  return moe_forward_core(stream_v, x, T, d, router_weight, router_bias, E, top_k, n_group,
+                          topk_group, norm_topk_prob, routed_scaling_factor, I, gate_packed,
+                          gate_scales, up_packed, up_scales, down_packed, down_scales, I_shared,
+                          shared_fmt, shared_gate, shared_gate_scales, shared_up,
+                          shared_up_scales, shared_down, shared_down_scales, shared_in,
+                          swiglu_limit, workspace, workspace_bytes, out, weights_out, indices_out,
+                          nullptr, &done);
+}
+
+extern "C" int glm_moe_forward_hc(void *stream_v, const uint16_t *x, int T, int d,
+                                  const float *router_weight, const float *router_bias, int E,
+                                  int top_k, int n_group, int topk_group, int norm_topk_prob,
+                                  float routed_scaling_factor, int I, const uint8_t *gate_packed,
+                                  const uint8_t *gate_scales, const uint8_t *up_packed,
+                                  const uint8_t *up_scales, const uint8_t *down_packed,
+                                  const uint8_t *down_scales, int I_shared, int shared_fmt,
+                                  const void *shared_gate, const uint8_t *shared_gate_scales,
+                                  const void *shared_up, const uint8_t *shared_up_scales,
+                                  const void *shared_down, const uint8_t *shared_down_scales,
+                                  const uint16_t *shared_in, float swiglu_limit, void *workspace,
+                                  size_t workspace_bytes, float *out, float *weights_out,
+                                  uint32_t *indices_out, const float *residual, int hc,
+                                  const float *post, const float *comb, int flags,
+                                  float *hc_out) {
+  glm::clear_error();
+  GLM_REQUIRE(residual && post && comb && hc_out, GLM_ERR_INVALID_ARGUMENT,
+              "moe_forward_hc: null hyper-connection argument");
+  GLM_REQUIRE(hc >= 1 && hc <= 8, GLM_ERR_UNSUPPORTED_SHAPE, "moe_forward_hc: hc_mult %d > 8",
+              hc);
+  GLM_REQUIRE((flags & ~GLM_HC_BF16_STREAMS) == 0, GLM_ERR_INVALID_ARGUMENT,
+              "moe_forward_hc: unknown flags %d", flags);
+  GLM_REQUIRE(d % 4 == 0 && glm_aligned16({residual, hc_out}), GLM_ERR_INVALID_ARGUMENT,
+              "moe_forward_hc: residual and hc_out must be 16-byte aligned, d %% 4 == 0");
+  const glm::HcFuse f{residual, post, comb, hc_out, hc, (flags & GLM_HC_BF16_STREAMS) != 0};
+  bool done = false;
+  int rc = moe_forward_core(stream_v, x, T, d, router_weight, router_bias, E, top_k, n_group,
+                            topk_group, norm_topk_prob, routed_scaling_factor, I, gate_packed,
+                            gate_scales, up_packed, up_scales, down_packed, down_scales,
+                            I_shared, shared_fmt, shared_gate, shared_gate_scales, shared_up,
+                            shared_up_scales, shared_down, shared_down_scales, shared_in,
+                            swiglu_limit, workspace, workspace_bytes, out, weights_out,
+                            indices_out, &f, &done);
+  if (rc != GLM_OK || done || T == 0) return rc;
+  return glm_hc_post_launch((hipStream_t)stream_v, f, out, T, d);
+}
+
+static int moe_forward_core(void *stream_v, const uint16_t *x, int T, int d,
+                            const float *router_weight, const float *router_bias, int E,
+                            int top_k, int n_group, int topk_group, int norm_topk_prob,
+                            float routed_scaling_factor, int I, const uint8_t *gate_packed,
+                            const uint8_t *gate_scales, const uint8_t *up_packed,
+                            const uint8_t *up_scales, const uint8_t *down_packed,
+                            const uint8_t *down_scales, int I_shared, int shared_fmt,
+                            const void *shared_gate, const uint8_t *shared_gate_scales,
+                            const void *shared_up, const uint8_t *shared_up_scales,
+                            const void *shared_down, const uint8_t *shared_down_scales,
+                            const uint16_t *shared_in, float swiglu_limit, void *workspace,
+                            size_t workspace_bytes, float *out, float *weights_out,
+                            uint32_t *indices_out, const glm::HcFuse *hc, bool *hc_done) {
   hipStream_t stream = (hipStream_t)stream_v;
   GLM_REQUIRE(x && router_weight && router_bias && gate_packed && gate_scales && up_packed &&
                   up_scales && down_packed && down_scales && workspace && out,
@@ -260,14 +337,16 @@ extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
       if (rc) return rc;
       shared_ready = w.shared_out;
     }
-    return glm_pair_path_launch(
+    rc = glm_pair_path_launch(
         stream, x, T, d, router_weight, router_bias, E, top_k, n_group, topk_group,
         norm_topk_prob, routed_scaling_factor, w.logits, wts, idx, I, gate_packed, gate_scales,
         up_packed, up_scales, down_packed, down_scales,
         fuse_shared ? (const uint16_t *)shared_gate : nullptr,
         fuse_shared ? (const uint16_t *)shared_up : nullptr,
         fuse_shared ? (const uint16_t *)shared_down : nullptr, Is, w.gp, w.up, w.shared_h, w.yp,
-        shared_ready, w.h, swiglu_limit, out);
+        shared_ready, w.h, swiglu_limit, out, hc);
+    *hc_done = hc != nullptr;  // fused into the down + combine kernel
+    return rc;
   }
   if (glm_decode_path_supported(T, d, E, top_k, I, fuse_shared ? Is : 0)) {
     // decode: five short kernels, no host synchronisation; the bf16 shared

@@ -65,6 +65,9 @@ SIGNATURES = {
     "glm_moe_forward": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _i, _f, _i,
                              _p, _p, _p, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p, _p, _p,
                              _f, _p, _sz, _p, _p, _p]),
+    "glm_moe_forward_hc": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _i, _f, _i,
+                                _p, _p, _p, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p, _p, _p,
+                                _f, _p, _sz, _p, _p, _p, _p, _i, _p, _p, _i, _p]),
     "glm_hc_workspace_bytes": (_sz, [_i, _i, _i]),
     "glm_hc_pre": (_i, [_p, _p, _i, _i, _i, _p, _p, _p, _i, _f, _f, _p, _f, _i, _p, _sz, _p, _p,
                         _p, _p]),

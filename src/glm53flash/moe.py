@@ -103,6 +103,17 @@ class ExpertSSDMoE:
         return ws
 
     def __call__(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        return self._forward(hidden_states, None)
+
+    def with_hyper_residual(self, hidden_states: torch.Tensor, residual: torch.Tensor,
+                            post: torch.Tensor, comb: torch.Tensor,
+                            bf16_streams: bool = False) -> torch.Tensor:
+        """The layer followed by the FFN site's ``hyper_residual(residual, y,
+        post, comb)`` (``mhc.py:51-60``) in one library call
+        (``glm_moe_forward_hc``); ``residual`` f32 ``[T, hc, d]``."""
+        return self._forward(hidden_states, (residual, post, comb, bf16_streams))
+
+    def _forward(self, hidden_states: torch.Tensor, hc) -> torch.Tensor:
         cfg = self.config
         d = self.hidden_size
         original_shape = hidden_states.shape
@@ -124,15 +135,29 @@ class ExpertSSDMoE:
         out = torch.empty((T, d), dtype=torch.float32, device=dev)
         weights = torch.empty((T, k), dtype=torch.float32, device=dev)
         indices = torch.empty((T, k), dtype=torch.int32, device=dev)
+        hc_args, hc_out = (), None
+        if hc is not None:
+            residual, post, comb, bf16_streams = hc
+            N.require_device(residual, "residual", (torch.float32,))
+            hcm = residual.shape[-2]
+            if residual.numel() != T * hcm * d or post.numel() != T * hcm or \
+                    comb.numel() != T * hcm * hcm:
+                raise ContractError("residual, post and comb do not match the layer's tokens")
+            N.require_device(post, "post", (torch.float32,))
+            N.require_device(comb, "comb", (torch.float32,))
+            hc_out = torch.empty((T, hcm, d), dtype=torch.float32, device=dev)
+            hc_args = (residual.data_ptr(), hcm, post.data_ptr(), comb.data_ptr(),
+                       N.native.GLM_HC_BF16_STREAMS if bf16_streams else 0, hc_out.data_ptr())
         if T == 0:  # an empty batch: empty results, nothing to launch
             self.last_weights = weights
             self.last_indices = indices
-            return out.reshape(original_shape)
+            return out.reshape(original_shape) if hc is None else hc_out
         ws = self._workspace_for(T, dev)
         gw, gs = bank.projection("gate_proj")
         uw, us = bank.projection("up_proj")
         dw, ds = bank.projection("down_proj")
-        N.call("glm_moe_forward", N.stream_of(rows), rows.data_ptr(), T, d, rw.data_ptr(),
+        N.call("glm_moe_forward" if hc is None else "glm_moe_forward_hc",
+               N.stream_of(rows), rows.data_ptr(), T, d, rw.data_ptr(),
                rb.data_ptr(), cfg.n_routed_experts, k, cfg.n_group, cfg.topk_group,
                int(cfg.norm_topk_prob), float(cfg.routed_scaling_factor),
                cfg.moe_intermediate_size, gw.data_ptr(), gs.data_ptr(), uw.data_ptr(),
@@ -140,10 +165,10 @@ class ExpertSSDMoE:
                sg.data_ptr(), N.ptr(shared.gate_proj.scales), su.data_ptr(),
                N.ptr(shared.up_proj.scales), sd.data_ptr(), N.ptr(shared.down_proj.scales), None,
                float(cfg.swiglu_limit), ws.data_ptr(), ws.numel(), out.data_ptr(),
-               weights.data_ptr(), indices.data_ptr())
+               weights.data_ptr(), indices.data_ptr(), *hc_args)
         self.last_weights = weights
         self.last_indices = indices
-        return out.reshape(original_shape)
+        return out.reshape(original_shape) if hc is None else hc_out
 
     @property
     def last_route(self) -> tuple[int, ...]:

@@ -208,3 +208,41 @@ def test_moe_ffn_site_matches_oracle(gu, bf16):
     np.testing.assert_allclose(
         gu.host(normed), H.rms_norm(gu.host(collapsed.float()).reshape(shape.T, shape.d),
                                     h["norm_weight"], 1e-6), rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("T,bf16", [(2, False), (2, True), (20, False)])
+def test_moe_forward_hc_equals_forward_then_hc_post(gu, T, bf16):
+    """glm_moe_forward_hc (the update inside the layer's last kernel at T <= 4,
+    a separate launch at T = 20) is bit-identical to glm_moe_forward followed
+    by glm_hc_post."""
+    import torch
+    shape = SHAPES["verify_t2"]
+    hc = 4
+    print(f"moe_forward_hc T={T} bf16={bf16}", flush=True)
+    layer = make_layer(shape, 5800 + T + bf16, T=T)
+    dl = gu.upload_layer(layer)
+    h = make_hc(T, hc, shape.d, 5801 + T, bf16_streams=bf16)
+    post, comb, _ = H.hyper_connection(h["streams"], h["fn"], h["base"], h["scale"],
+                                       sinkhorn_iters=20, rms_eps=1e-6, hc_eps=1e-6)
+    res, post_d, comb_d = gu.to_dev(h["streams"]), gu.to_dev(post), gu.to_dev(comb)
+    flags = gu.native.GLM_HC_BF16_STREAMS if bf16 else 0
+    out, _, _ = gu.run_layer(dl, shape, T=T)
+    ref = torch.empty((T, hc, shape.d), dtype=torch.float32, device="cuda")
+    gu.call("glm_hc_post", gu.stream(), gu.p(res), T, hc, shape.d, gu.p(out), gu.p(post_d),
+            gu.p(comb_d), flags, gu.p(ref))
+    d, E, k, I, Is = shape.d, shape.E, shape.k, shape.I, shape.I_shared
+    lib = gu.native.load()
+    ws_bytes = lib.glm_moe_workspace_bytes(T, d, E, k, I, Is)
+    ws = gu.workspace(ws_bytes)
+    out2 = torch.empty((T, d), dtype=torch.float32, device="cuda")
+    hc_out = torch.empty((T, hc, d), dtype=torch.float32, device="cuda")
+    args = [gu.stream(), gu.p(dl["x"]), T, d, gu.p(dl["router_weight"]), gu.p(dl["router_bias"]),
+            E, k, shape.n_group, shape.topk_group, int(shape.norm_topk_prob),
+            shape.routed_scaling_factor, I, *(gu.p(dl[key]) for key in BANK_KEYS), Is,
+            gu.native.GLM_FMT_BF16, gu.p(dl["shared.gate"]), None, gu.p(dl["shared.up"]), None,
+            gu.p(dl["shared.down"]), None, None, shape.swiglu_limit, gu.p(ws), ws_bytes,
+            gu.p(out2), None, None, gu.p(res), hc, gu.p(post_d), gu.p(comb_d), flags,
+            gu.p(hc_out)]
+    gu.call("glm_moe_forward_hc", *args)
+    assert np.array_equal(gu.host(out2).view(np.uint32), gu.host(out).view(np.uint32))
+    assert np.array_equal(gu.host(hc_out).view(np.uint32), gu.host(ref).view(np.uint32))
