@@ -691,7 +691,11 @@ def bank_load_bench(args, torch, np) -> int:
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
                      "bytes_per_launch": moved, "avg_launch_us": round(k_s * 1e6, 3),
                      "launches": launches},
-        "cpu_baseline": None,
+        # what a CPU-only loader does: the native reader filling host memory
+        "cpu_baseline": {"value": round(read_gbps, 3), "unit": "GB/s", "cores": args.load_threads,
+                         "kind": "port",
+                         "sample": f"4 reads of one {n_read} B range of a shard in the page cache "
+                                   "into pinned host memory (glm_file_read_ranges)"},
     }
     print(json.dumps(line))
     return 0

@@ -210,15 +210,16 @@ def test_moe_ffn_site_matches_oracle(gu, bf16):
                                     h["norm_weight"], 1e-6), rtol=2e-6, atol=1e-7)
 
 
-@pytest.mark.parametrize("T,bf16", [(2, False), (2, True), (20, False)])
-def test_moe_forward_hc_equals_forward_then_hc_post(gu, T, bf16):
+@pytest.mark.parametrize("name,T,bf16,hc", [("verify_t2", 2, False, 4), ("verify_t2", 2, True, 4),
+                                            ("verify_t2", 20, False, 4), ("decode_t1", 1, False, 4),
+                                            ("decode_t1", 3, False, 8)])
+def test_moe_forward_hc_equals_forward_then_hc_post(gu, name, T, bf16, hc):
     """glm_moe_forward_hc (the update inside the layer's last kernel at T <= 4,
     a separate launch at T = 20) is bit-identical to glm_moe_forward followed
-    by glm_hc_post."""
+    by glm_hc_post; decode_t1 runs the fused kernel with k = 2 (256 threads)."""
     import torch
-    shape = SHAPES["verify_t2"]
-    hc = 4
-    print(f"moe_forward_hc T={T} bf16={bf16}", flush=True)
+    shape = SHAPES[name]
+    print(f"moe_forward_hc {name} T={T} bf16={bf16} hc={hc}", flush=True)
     layer = make_layer(shape, 5800 + T + bf16, T=T)
     dl = gu.upload_layer(layer)
     h = make_hc(T, hc, shape.d, 5801 + T, bf16_streams=bf16)
