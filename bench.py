@@ -693,7 +693,7 @@ def bank_load_bench(args, torch, np) -> int:
                      "launches": launches},
         # what a CPU-only loader does: the native reader filling host memory
         "cpu_baseline": {"value": round(read_gbps, 3), "unit": "GB/s", "cores": args.load_threads,
-                         "kind": "port",
+                         **host_cpu(), "kind": "port",
                          "sample": f"4 reads of one {n_read} B range of a shard in the page cache "
                                    "into pinned host memory (glm_file_read_ranges)"},
     }
@@ -767,6 +767,20 @@ def measure_traffic(args, kernel_name: str):
     return round(fetch[0] + write[0]), note
 
 
+def host_cpu() -> dict:
+    """The host the CPU baseline ran on: logical CPUs and the CPU model."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu_model": model}
+
+
 def cpu_baseline(shape, bank, xs, budget_s: float, bias=None, streams=None):
     """The C restatement (oracle/libmoe_cpu.so, OpenMP over this host's cores)
     on one resident layer: as many layer steps as fit in ``budget_s``.  For a
@@ -820,6 +834,7 @@ def cpu_baseline(shape, bank, xs, budget_s: float, bias=None, streams=None):
             "value": round(steps / (el * shape.layers), 3),
             "unit": "tokens/s",
             "cores": cpu_oracle.threads(),
+            **host_cpu(),
             "kind": "port",
             "sample": f"{steps} single-layer steps (MXFP8 {shape.d}x{shape.d} linear + MoE layer, "
                       f"T={shape.T}) on one resident layer in {el:.2f} s; tokens/s = 1 / "
@@ -829,6 +844,7 @@ def cpu_baseline(shape, bank, xs, budget_s: float, bias=None, streams=None):
         "value": round(shape.T * steps / el, 2),
         "unit": "tokens/s",
         "cores": cpu_oracle.threads(),
+        **host_cpu(),
         "kind": "port",
         "sample": f"{steps} layer steps of {shape.name} (T={shape.T}) on one resident layer "
                   f"in {el:.2f} s; C restatement (not MLX), OpenMP"
