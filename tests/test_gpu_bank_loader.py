@@ -156,3 +156,27 @@ def test_scalex_layer_loads_the_same_bank(gu, tmp_path, scales):
                 want = np.stack([arrays[(layer, e)][(comp, part)] for e in range(E)])
                 assert np.array_equal(got, want), (layer, comp, part)
     loader.close()
+
+
+def test_loader_at_the_real_record_size(gu, tmp_path):
+    """d = 4096, I = 2048: one expert is the real checkpoint's 13,369,344-byte
+    record (expert_source.py:370); two records per staging chunk."""
+    from glm53flash.bank_loader import ExpertBankLoader
+    from glm53flash.expert_ssd import HBMExpertBank
+    E, d, I, layer = 4, 4096, 2048, 3
+    print(f"bank loader real record: E={E} d={d} I={I}", flush=True)
+    arrays = make_checkpoint(str(tmp_path), layers=(layer,), E=E, d=d, I=I, extras=False,
+                             seed=5330)
+    plan = _plan(str(tmp_path), E, d, I, (layer,))
+    assert plan.uniform_pack_bytes == 13_369_344 and plan.uniform_read_count == 1
+    loader = ExpertBankLoader(plan, chunk_bytes=30 << 20)
+    bank = HBMExpertBank(layer=layer, num_experts=E, hidden_size=d, intermediate_size=I,
+                         swiglu_limit=10.0, device="cuda")
+    stats = loader.load(bank)
+    assert stats.chunks == 2 and stats.bytes == E * 13_369_344
+    for comp in COMPONENTS:
+        for part in PARTS:
+            got = gu.host(bank.tensors[f"{comp}.{part}"])
+            want = np.stack([arrays[(layer, e)][(comp, part)] for e in range(E)])
+            assert np.array_equal(got, want), (comp, part)
+    loader.close()
