@@ -641,6 +641,9 @@ SMALL_LAYERS = [
     (40, 1024, 64, 8, 512, 512, (1, 1)),
     # k = 64, every expert of E = 64 chosen by every token (the top-k upper bound)
     (3, 256, 64, 64, 64, 64, (1, 1)),
+    # the real GLM expert geometry (d = 4096, I = 2048: 16 chunks of 128 in the
+    # down projection, beyond the decode kernels' templates): the general path
+    (2, 4096, 24, 8, 2048, 2048, (1, 1)),
 ]
 
 
