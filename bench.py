@@ -158,7 +158,11 @@ class Setup:
             self.streams = torch.randn((self.n_inputs, T, hc, d), device=dev, generator=gen)
         # the layer's routed gate/up kernel: token-major for a few tokens, tiled
         # GEMV up to 64 tokens, grouped MFMA GEMMs beyond
-        self.few_token = T <= 4 and k <= 8
+        # the token-major and decode kernels cover d / 512 and I / 128 in
+        # {1, 2, 4, 6, 8} chunks; other shapes run on the general GEMV kernels
+        self.decode_kernels = (d % 512 == 0 and d // 512 in (2, 4, 6, 8) and I % 128 == 0
+                               and I // 128 in (1, 2, 4, 6, 8))
+        self.few_token = T <= 4 and k <= 8 and self.decode_kernels
         self.grouped = T > 64
 
     def bias(self, step: int, layer: int):
@@ -251,6 +255,8 @@ class Setup:
         if self.few_token:
             epl = 2 if E <= 128 else (4 if E <= 256 else 8)
             return f"select_gate_up_kernel<{epl}, {d // 512}, 1>"
+        if not self.decode_kernels:
+            return "mx_gemv_kernel"
         return f"decode_gate_up_kernel<{d // 512}>"
 
     def kernel_flops(self) -> int:

@@ -484,16 +484,21 @@ using glm::GemvArgs;
 static bool choose_split(int fmt, int nproj, int K, int *ksplit, int *cpw) {
   if (K % 128 != 0) return false;
   const int kc = K / 128;
-  const int max_cpw = (fmt == GLM_FMT_BF16 && nproj == 2) ? 2 : 4;
-  // Prefer a 4-wave split, then 2, 8, 1; within that the largest cpw that fits.
-  const int splits[] = {4, 2, 8, 1, 3, 6};
-  for (int s : splits) {
-    if (kc % s) continue;
-    const int c = kc / s;
-    if (c >= 1 && c <= max_cpw) {
-      *ksplit = s;
-      *cpw = c;
-      return true;
+  // bf16 gate/up holds two projections of bf16 rows: 2 chunks per wave keep
+  // it at 3 waves per SIMD; 4 chunks (244 registers, 2 waves per SIMD) only
+  // when no split with 2 fits (K = 4096 and beyond)
+  const bool bf16_pair = fmt == GLM_FMT_BF16 && nproj == 2;
+  for (int max_cpw : {bf16_pair ? 2 : 4, 4}) {
+    // Prefer a 4-wave split, then 2, 8, 1; within that the largest cpw that fits.
+    const int splits[] = {4, 2, 8, 1, 3, 6};
+    for (int s : splits) {
+      if (kc % s) continue;
+      const int c = kc / s;
+      if (c >= 1 && c <= max_cpw) {
+        *ksplit = s;
+        *cpw = c;
+        return true;
+      }
     }
   }
   return false;

@@ -8,6 +8,8 @@ Shapes follow the routed-MoE layer of GLM-5.3-Flash at benchmark geometry:
 * ``prefill_t4096`` T=4096, as verify_t2, near-uniform routing
 * ``stack42_t1``   T=1, 42 layers of (2048x2048 MXFP8 resident linear + MoE
   as verify_t2), 256 decode steps, Markov routing with 70% expert reuse
+* ``real_t2``      T=2 at the real GLM expert geometry: d=4096, E=288, k=8,
+  I=2048 (bf16 shared expert I=2048)
 * ``ffn_t2``       the decoder FFN site at verify_t2: hyper-connection of 4 f32
   residual streams (20 Sinkhorn rounds) + post-attention RMSNorm + the MoE
   layer + hyper_residual
@@ -62,6 +64,7 @@ SHAPES = {
     "stack42_t1": MoEShape("stack42_t1", T=1, d=2048, E=128, k=8, I=768, I_shared=768,
                            routing="markov", layers=42, steps=256),
     "ffn_t2": MoEShape("ffn_t2", T=2, d=2048, E=128, k=8, I=768, I_shared=768, hc=4),
+    "real_t2": MoEShape("real_t2", T=2, d=4096, E=288, k=8, I=2048, I_shared=2048),
 }
 
 SCALE_LO, SCALE_HI = 119, 127  # inclusive E8M0 range of the synthetic scales
