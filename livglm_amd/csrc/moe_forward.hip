@@ -382,9 +382,11 @@ static int moe_forward_core(void *stream_v, const uint16_t *x, int T, int d,
                          topk_group, norm_topk_prob, routed_scaling_factor, w.logits, wts, idx,
                          w.router_split);
   if (rc) return rc;
-  // general path: dispatch, then the grouped MFMA GEMMs over row tiles when
-  // the shape allows, else the tiled GEMV kernels over the work list
-  const bool grouped = glm_grouped_supported(d, I);
+  // general path: dispatch, then the grouped MFMA GEMMs over 128-row tiles
+  // for more than 64 tokens when the shape allows, else the tiled GEMV
+  // kernels over the work list (a few tokens in a 128-row tile would be
+  // mostly padding)
+  const bool grouped = glm_grouped_supported(d, I) && T > 64;
   rc = glm_dispatch_launch(stream, idx, T, top_k, E, w.counts, w.offsets, w.perm, w.inv,
                            w.pair_token, w.active, w.num_active, w.work, w.status,
                            grouped ? glm_grouped_tile_rows() : 0, grouped ? w.tiles : nullptr,
