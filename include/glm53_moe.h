@@ -289,6 +289,40 @@ int glm_moe_forward(void *stream, const uint16_t *x, int T, int d, const float *
                     size_t workspace_bytes, float *out, float *weights_out,
                     uint32_t *indices_out);
 
+/* Size of the device array behind glm_moe_forward_noalloc (per device). */
+#define GLM_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/*
+ * glm_moe_forward without a workspace argument, for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  No counterpart in the reference.
+ * The layer's workspace is a file-scope device array of
+ * GLM_NOALLOC_SCRATCH_BYTES inside the library: every device that loads the
+ * library holds its own copy until the process ends, and its address is
+ * looked up once per device, on the first call with that device current.
+ * Sizes whose workspace (glm_moe_workspace_bytes) exceeds the array are
+ * rejected with GLM_ERR_WORKSPACE before any device work; decode sizes fit
+ * (T = 64 at d 2048, E 128, k 8, I 768, I_shared 768 needs 8.7 MiB; T = 64 at
+ * d 4096, E 288, I 2048 needs 33.4 MiB), 4096-token prefill does not.
+ * `stream` must belong to the current device.  Nothing in the array needs to
+ * start at zero; each call leaves its contents there.  All calls on one
+ * device share the array, so calls that overlap on a device race: issue them
+ * on one stream (or order them).  Allocates and frees nothing.  Arguments and
+ * results otherwise as glm_moe_forward.
+ */
+int glm_moe_forward_noalloc(void *stream, const uint16_t *x, int T, int d,
+                            const float *router_weight, const float *router_bias, int E,
+                            int top_k, int n_group, int topk_group, int norm_topk_prob,
+                            float routed_scaling_factor, int I, const uint8_t *gate_packed,
+                            const uint8_t *gate_scales, const uint8_t *up_packed,
+                            const uint8_t *up_scales, const uint8_t *down_packed,
+                            const uint8_t *down_scales, int I_shared, int shared_fmt,
+                            const void *shared_gate, const uint8_t *shared_gate_scales,
+                            const void *shared_up, const uint8_t *shared_up_scales,
+                            const void *shared_down, const uint8_t *shared_down_scales,
+                            const uint16_t *shared_in, float swiglu_limit, float *out,
+                            float *weights_out, uint32_t *indices_out);
+
 /* ------------------------------------------------------------ decoder FFN site */
 
 /* glm_hc_pre / glm_hc_post flag: the streams are bf16 in the model (passed

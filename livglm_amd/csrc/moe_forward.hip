@@ -1,5 +1,6 @@
 // Whole routed-MoE layer (ExpertSSDMoE._call_impl, moe.py:123-201) on one
 // stream, plus the library's error plumbing and version query.
+#include <mutex>
 #include <string>
 
 #include "glm_common.h"
@@ -186,6 +187,49 @@ Workspace carve(char *base, int T, int d, int E, int k, int I, int Is) {
 
 }  // namespace
 
+// ---------------------------------------------------------------- static scratch
+
+// The workspace of glm_moe_forward_noalloc: a file-scope device array, one
+// copy per device that loads the library, held until the process ends.  On
+// the host, `scratch` names a stand-in, not the device copy: host code only
+// ever uses the address hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) unsigned char scratch[GLM_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device ordinal
+
+// The device address of `scratch` on the current device, looked up once per
+// device (with that device current).  The stream must belong to that device:
+// its kernels would otherwise take another device's address.
+int noalloc_scratch(hipStream_t stream, void **out) {
+  int dev = -1;
+  GLM_HIP_CHECK(hipGetDevice(&dev));
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    GLM_HIP_CHECK(hipStreamGetDevice(stream, &sdev));
+    GLM_REQUIRE(sdev == dev, GLM_ERR_INVALID_ARGUMENT,
+                "moe_forward_noalloc: the stream belongs to device %d but device %d is current",
+                (int)sdev, dev);
+  }
+  GLM_REQUIRE(dev >= 0 && dev < kMaxDevices, GLM_ERR_INVALID_ARGUMENT,
+              "moe_forward_noalloc: device ordinal %d is out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *ptr = nullptr;
+    GLM_HIP_CHECK(hipGetSymbolAddress((void **)&ptr, HIP_SYMBOL(scratch)));
+    GLM_REQUIRE(ptr != nullptr && (reinterpret_cast<uintptr_t>(ptr) & 255u) == 0, GLM_ERR_HIP,
+                "moe_forward_noalloc: unusable scratch address on device %d", dev);
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return GLM_OK;
+}
+
+}  // namespace
+
 extern "C" size_t glm_moe_workspace_bytes(int T, int d, int E, int top_k, int I, int I_shared) {
   if (T < 0 || d <= 0 || E <= 0 || top_k <= 0 || I <= 0) return 0;
   return carve(nullptr, T, d, E, top_k, I, I_shared).bytes;
@@ -213,7 +257,8 @@ static int moe_forward_core(void *stream_v, const uint16_t *x, int T, int d,
                             const void *shared_down, const uint8_t *shared_down_scales,
                             const uint16_t *shared_in, float swiglu_limit, void *workspace,
                             size_t workspace_bytes, float *out, float *weights_out,
-                            uint32_t *indices_out, const glm::HcFuse *hc, bool *hc_done);
+                            uint32_t *indices_out, const glm::HcFuse *hc, bool *hc_done,
+                            bool noalloc);
 
 extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
                                const float *router_weight, const float *router_bias, int E,
@@ -236,7 +281,27 @@ extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
                           shared_fmt, shared_gate, shared_gate_scales, shared_up,
                           shared_up_scales, shared_down, shared_down_scales, shared_in,
                           swiglu_limit, workspace, workspace_bytes, out, weights_out, indices_out,
-                          nullptr, &done);
+                          nullptr, &done, false);
+}
+
+extern "C" int glm_moe_forward_noalloc(
+    void *stream_v, const uint16_t *x, int T, int d, const float *router_weight,
+    const float *router_bias, int E, int top_k, int n_group, int topk_group, int norm_topk_prob,
+    float routed_scaling_factor, int I, const uint8_t *gate_packed, const uint8_t *gate_scales,
+    const uint8_t *up_packed, const uint8_t *up_scales, const uint8_t *down_packed,
+    const uint8_t *down_scales, int I_shared, int shared_fmt, const void *shared_gate,
+    const uint8_t *shared_gate_scales, const void *shared_up, const uint8_t *shared_up_scales,
+    const void *shared_down, const uint8_t *shared_down_scales, const uint16_t *shared_in,
+    float swiglu_limit, float *out, float *weights_out, uint32_t *indices_out) {
+  glm::clear_error();
+  bool done = false;
+  return moe_forward_core(stream_v, x, T, d, router_weight, router_bias, E, top_k, n_group,
+                          topk_group, norm_topk_prob, routed_scaling_factor, I, gate_packed,
+                          gate_scales, up_packed, up_scales, down_packed, down_scales, I_shared,
+                          shared_fmt, shared_gate, shared_gate_scales, shared_up,
+                          shared_up_scales, shared_down, shared_down_scales, shared_in,
+                          swiglu_limit, nullptr, 0, out, weights_out, indices_out, nullptr, &done,
+                          true);
 }
 
 extern "C" int glm_moe_forward_hc(void *stream_v, const uint16_t *x, int T, int d,
@@ -271,7 +336,7 @@ extern "C" int glm_moe_forward_hc(void *stream_v, const uint16_t *x, int T, int 
                             I_shared, shared_fmt, shared_gate, shared_gate_scales, shared_up,
                             shared_up_scales, shared_down, shared_down_scales, shared_in,
                             swiglu_limit, workspace, workspace_bytes, out, weights_out,
-                            indices_out, &f, &done);
+                            indices_out, &f, &done, false);
   if (rc != GLM_OK || done || T == 0) return rc;
   return glm_hc_post_launch((hipStream_t)stream_v, f, out, T, d);
 }
@@ -288,10 +353,11 @@ static int moe_forward_core(void *stream_v, const uint16_t *x, int T, int d,
                             const void *shared_down, const uint8_t *shared_down_scales,
                             const uint16_t *shared_in, float swiglu_limit, void *workspace,
                             size_t workspace_bytes, float *out, float *weights_out,
-                            uint32_t *indices_out, const glm::HcFuse *hc, bool *hc_done) {
+                            uint32_t *indices_out, const glm::HcFuse *hc, bool *hc_done,
+                            bool noalloc) {
   hipStream_t stream = (hipStream_t)stream_v;
   GLM_REQUIRE(x && router_weight && router_bias && gate_packed && gate_scales && up_packed &&
-                  up_scales && down_packed && down_scales && workspace && out,
+                  up_scales && down_packed && down_scales && (workspace || noalloc) && out,
               GLM_ERR_INVALID_ARGUMENT, "moe_forward: null pointer argument");
   GLM_REQUIRE(T >= 0 && d > 0 && E > 0 && top_k > 0 && I > 0, GLM_ERR_INVALID_ARGUMENT,
               "moe_forward: invalid sizes T=%d d=%d E=%d k=%d I=%d", T, d, E, top_k, I);
@@ -316,10 +382,21 @@ static int moe_forward_core(void *stream_v, const uint16_t *x, int T, int d,
                               weights_out, indices_out}),
               GLM_ERR_INVALID_ARGUMENT, "moe_forward: buffers must be 16-byte aligned");
   const Workspace need = carve(nullptr, T, d, E, top_k, I, has_shared ? I_shared : 0);
-  GLM_REQUIRE(workspace_bytes >= need.bytes, GLM_ERR_WORKSPACE,
-              "moe_forward: workspace of %zu bytes is below the %zu required", workspace_bytes,
-              need.bytes);
+  if (noalloc) {
+    GLM_REQUIRE(need.bytes <= (size_t)GLM_NOALLOC_SCRATCH_BYTES, GLM_ERR_WORKSPACE,
+                "moe_forward_noalloc: these sizes need %zu bytes of workspace, above the "
+                "%zu-byte scratch array",
+                need.bytes, (size_t)GLM_NOALLOC_SCRATCH_BYTES);
+  } else {
+    GLM_REQUIRE(workspace_bytes >= need.bytes, GLM_ERR_WORKSPACE,
+                "moe_forward: workspace of %zu bytes is below the %zu required", workspace_bytes,
+                need.bytes);
+  }
   if (T == 0) return GLM_OK;
+  if (noalloc) {
+    rc = noalloc_scratch(stream, &workspace);
+    if (rc != GLM_OK) return rc;
+  }
   Workspace w = carve((char *)workspace, T, d, E, top_k, I, has_shared ? I_shared : 0);
   float *wts = weights_out ? weights_out : w.weights;
   uint32_t *idx = indices_out ? indices_out : w.indices;

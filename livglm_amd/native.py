@@ -28,6 +28,7 @@ GLM_MX_RULE_OCP = 1
 
 GLM_READ_DROP_CACHE = 1
 GLM_HC_BF16_STREAMS = 1
+GLM_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 ABI_VERSION = 1
 
@@ -65,6 +66,9 @@ SIGNATURES = {
     "glm_moe_forward": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _i, _f, _i,
                              _p, _p, _p, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p, _p, _p,
                              _f, _p, _sz, _p, _p, _p]),
+    "glm_moe_forward_noalloc": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _i, _f, _i,
+                                     _p, _p, _p, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p, _p,
+                                     _p, _f, _p, _p, _p]),
     "glm_moe_forward_hc": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _i, _f, _i,
                                 _p, _p, _p, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p, _p, _p,
                                 _f, _p, _sz, _p, _p, _p, _p, _i, _p, _p, _i, _p]),
