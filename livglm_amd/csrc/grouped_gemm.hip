@@ -817,6 +817,12 @@ static int grouped_launch(hipStream_t stream, GroupedArgs a, int nproj, int wfmt
 
 size_t glm_act_split_bytes(long long rows, int K) { return SplitLayout(rows, K).total; }
 
+// The block-scaled GEMMs read a split through one buffer resource with 32-bit
+// offsets: the whole split must stay below 4 GiB.
+bool glm_split_fits(long long rows, int K) {
+  return rows >= 0 && K > 0 && SplitLayout(rows, K).total <= 0xffffffffull;
+}
+
 // bf16 activations [rows][K] -> their hi/lo FP8 split (layout SplitLayout).
 int glm_act_split_launch(hipStream_t stream, const uint16_t *x, long long rows, int K,
                          void *split) {
@@ -963,6 +969,8 @@ extern "C" int glm_expert_gate_up_grouped(void *stream, const void *x_split, int
               "expert_gate_up_grouped: needs d %% 512 == 0 and I %% 256 == 0 (d=%d I=%d)", d, I);
   GLM_REQUIRE(glm_aligned16({x_split, gate_packed, up_packed, tiles, h}),
               GLM_ERR_INVALID_ARGUMENT, "expert_gate_up_grouped: buffers must be 16-byte aligned");
+  GLM_REQUIRE(glm_split_fits(T, d), GLM_ERR_UNSUPPORTED_SHAPE,
+              "expert_gate_up_grouped: the split of %d x %d activations exceeds 4 GiB", T, d);
   if (max_tiles == 0 || T == 0) return GLM_OK;
   return glm_grouped_gate_up_launch((hipStream_t)stream, x_split, T, pair_token,
                                     reinterpret_cast<const int4 *>(tiles), num_tiles, max_tiles,
@@ -983,6 +991,8 @@ extern "C" int glm_expert_down_grouped(void *stream, const void *h_split, int P,
               "expert_down_grouped: needs d %% 512 == 0 and I %% 256 == 0 (d=%d I=%d)", d, I);
   GLM_REQUIRE(glm_aligned16({h_split, down_packed, tiles, y}), GLM_ERR_INVALID_ARGUMENT,
               "expert_down_grouped: buffers must be 16-byte aligned");
+  GLM_REQUIRE(glm_split_fits(P, I), GLM_ERR_UNSUPPORTED_SHAPE,
+              "expert_down_grouped: the split of %d x %d activations exceeds 4 GiB", P, I);
   if (max_tiles == 0 || P == 0) return GLM_OK;
   return glm_grouped_down_launch((hipStream_t)stream, h_split, P,
                                  reinterpret_cast<const int4 *>(tiles), num_tiles, max_tiles, I,

@@ -47,6 +47,7 @@ int glm_dispatch_launch(hipStream_t stream, const uint32_t *indices, int T, int 
 size_t glm_dispatch_chunk_ints(long long P, int E);
 int glm_grouped_tile_rows();
 bool glm_grouped_supported(int d, int I);
+bool glm_split_fits(long long rows, int K);
 size_t glm_act_split_bytes(long long rows, int K);
 int glm_act_split_launch(hipStream_t stream, const uint16_t *x, long long rows, int K,
                          void *split);
@@ -361,6 +362,8 @@ static int moe_forward_core(void *stream_v, const uint16_t *x, int T, int d,
               GLM_ERR_INVALID_ARGUMENT, "moe_forward: null pointer argument");
   GLM_REQUIRE(T >= 0 && d > 0 && E > 0 && top_k > 0 && I > 0, GLM_ERR_INVALID_ARGUMENT,
               "moe_forward: invalid sizes T=%d d=%d E=%d k=%d I=%d", T, d, E, top_k, I);
+  GLM_REQUIRE((long long)T * top_k < (1LL << 30), GLM_ERR_UNSUPPORTED_SHAPE,
+              "moe_forward: T*k = %lld pairs exceeds 2^30", (long long)T * top_k);
   GLM_REQUIRE(d % 32 == 0 && I % 32 == 0, GLM_ERR_UNSUPPORTED_SHAPE,
               "moe_forward: d=%d and I=%d must be multiples of 32", d, I);
   GLM_REQUIRE(E <= 448, GLM_ERR_UNSUPPORTED_SHAPE, "moe_forward: E=%d exceeds 448", E);
@@ -463,7 +466,10 @@ static int moe_forward_core(void *stream_v, const uint16_t *x, int T, int d,
   // for more than 64 tokens when the shape allows, else the tiled GEMV
   // kernels over the work list (a few tokens in a 128-row tile would be
   // mostly padding)
-  const bool grouped = glm_grouped_supported(d, I) && T > 64;
+  // (the grouped GEMMs address the FP8 splits of x and h with 32-bit offsets:
+  // beyond 4 GiB of split the layer stays on the GEMV kernels)
+  const bool grouped = glm_grouped_supported(d, I) && T > 64 && glm_split_fits(T, d) &&
+                       glm_split_fits((long long)T * top_k, I);
   rc = glm_dispatch_launch(stream, idx, T, top_k, E, w.counts, w.offsets, w.perm, w.inv,
                            w.pair_token, w.active, w.num_active, w.work, w.status,
                            grouped ? glm_grouped_tile_rows() : 0, grouped ? w.tiles : nullptr,

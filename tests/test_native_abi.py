@@ -188,3 +188,20 @@ def test_ffn_site_and_loader_entry_points_reject_bad_arguments(lib):
     msg = _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_scalex_decode", None, fake, 4096,
                   ctypes.cast(rec, ctypes.c_void_p), 1, fake)
     assert "cover" in msg
+
+
+def test_split_beyond_32_bit_offsets_is_rejected_on_host(lib):
+    # the grouped GEMMs address an activation split through 32-bit offsets: a
+    # split above 4 GiB is refused instead of read as zeros past the limit
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    assert lib.glm_act_split_bytes(600000, 4096) > (1 << 32)
+    msg = _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_expert_gate_up_grouped", None, fake,
+                  600000, 4096, 2048, fake, fake, fake, fake, fake, fake, fake, 16, 10.0, fake)
+    assert "4 GiB" in msg
+    msg = _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_expert_down_grouped", None, fake,
+                  1100000, 2048, 4096, fake, fake, fake, fake, 16, fake)
+    assert "4 GiB" in msg
+    # the layer refuses more than 2^30 (token, expert) pairs before sizing anything
+    msg = _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_moe_forward",
+                  *_forward_args(1 << 27, workspace_bytes=1 << 40))
+    assert "2^30" in msg
