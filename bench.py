@@ -9,12 +9,22 @@ batches so that expert reads come from HBM rather than the 256 MB Infinity
 Cache.  The timed steps run as one HIP graph, bracketed by synchronisation and
 HIP events.
 
-Prints one JSON line: the layer's tokens/s (``value``), the roofline of the
-dominant kernel (the routed MXFP4 gate/up kernel, timed live with HIP events
-over a graph of back-to-back launches; its HBM traffic from two rocprofv3
-counter passes, FETCH_SIZE then WRITE_SIZE, scaled by the same counters over a
-copy of known size), and the CPU baseline (the C restatement in oracle/,
-OpenMP, on this host) on a bounded sample of the same workload.
+Prints one JSON line.  With the default workload (T=2, d=2048, E=128, top-8,
+I=768) it carries the metric's three parts:
+  * ``value``: the layer's tokens/s;
+  * ``decode_expert_hbm_gbps``: the distinct selected experts' MXFP4 bytes of
+    a step over the layer step's device time (its fraction of 8 TB/s beside
+    it), and ``roofline``: the dominant kernel (the routed MXFP4 gate/up kernel,
+    timed live with HIP events over a graph of back-to-back launches; its HBM
+    traffic from two rocprofv3 counter passes, FETCH_SIZE then WRITE_SIZE,
+    scaled by the same counters over a copy of known size);
+  * ``mxfp4_mfma_util`` and ``prefill``: the 4096-token layer's grouped gate/up
+    GEMM, algorithmic FLOPs per second over the 10.1 PFLOP/s dense MXFP4 peak,
+    with the MFMA operations the rocprofv3 MOPS counters report beside it;
+  * ``stack``: the 42-layer decode stack (MXFP8 resident linear + MoE layer per
+    layer, one token per step, Markov routing) per step;
+and the CPU baseline (the C restatement in oracle/, OpenMP, on this host) on a
+bounded sample of the default workload.
 """
 
 from __future__ import annotations
@@ -54,6 +64,9 @@ def parse_args():
     ap.add_argument("--min-rotation-gb", type=float, default=4.0,
                     help="total size of the distinct layer banks the steps rotate over")
     ap.add_argument("--kernel-launches", type=int, default=128)
+    ap.add_argument("--legs", default="auto", choices=["auto", "none"],
+                    help="auto: with the verify_t2 workload, also measure the 4096-token "
+                         "prefill (MXFP4 MFMA utilisation) and the 42-layer decode stack")
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="budget of the CPU-baseline sample (0 disables it)")
     ap.add_argument("--traffic", type=int, default=1,
@@ -74,13 +87,15 @@ def parse_args():
 class Setup:
     """Resident layer banks, token batches and per-launch routes of one workload."""
 
-    def __init__(self, args, torch, np):
+    def __init__(self, args, torch, np, workload: str, steps: int, warmup: int,
+                 min_rotation_gb: float):
         from livglm_amd import native
         from livglm_amd.workloads import BANK_KEYS, SHAPES
 
         self.torch, self.np, self.native, self.keys = torch, np, native, BANK_KEYS
         self.lib = native.load()
-        self.shape = shape = SHAPES[args.workload]
+        self.workload = workload
+        self.shape = shape = SHAPES[workload]
         T, d, E, k, I, Is = shape.T, shape.d, shape.E, shape.k, shape.I, shape.I_shared
         self.T, self.d, self.E, self.k, self.I, self.Is = T, d, E, k, I, Is
         self.dev = dev = torch.device("cuda:0")
@@ -94,8 +109,7 @@ class Setup:
         self.hc = hc = shape.hc
         if hc:
             self.layer_bytes += (2 * hc + hc * hc) * hc * d * 4 + d * 4  # fn + norm weight
-        self.n_banks = max(2, self.layers,
-                           math.ceil(args.min_rotation_gb * 1e9 / self.layer_bytes))
+        self.n_banks = max(2, self.layers, math.ceil(min_rotation_gb * 1e9 / self.layer_bytes))
         self.n_inputs = 64
 
         def randbytes(*s):
@@ -150,7 +164,7 @@ class Setup:
             # per (step, layer) bias rows that keep each expert of the previous
             # step with probability 0.7
             from livglm_amd.workloads import markov_bias_trace
-            n = max(1, args.warmup + args.steps)
+            n = max(1, warmup + steps)
             self.trace = torch.from_numpy(markov_bias_trace(
                 E, k, self.n_banks, n, np.random.default_rng(args.seed))).to(dev)
         self.xs = torch.randn((self.n_inputs, T, d), device=dev, generator=gen).to(torch.bfloat16)
@@ -271,33 +285,15 @@ class Setup:
         return self.unique[r] * 2 * proj
 
 
-def main() -> int:
-    args = parse_args()
-    if args.gpus != 1:
-        print(json.dumps({"error": "this benchmark runs the MoE layer on one GPU; runs over "
-                                   "several GPUs (the layer sharded by expert) are not supported",
-                          "n_gpus": args.gpus}))
-        return 2
-
-    import numpy as np
-    import torch
-
-    if not torch.cuda.is_available():
-        print(json.dumps({"error": "no GPU visible"}))
-        return 1
-    if args.mode == "copy":
-        return copy_probe(torch)
-    if args.workload == "bank_load":
-        return bank_load_bench(args, torch, np)
-    S = Setup(args, torch, np)
-    R = args.kernel_launches
+def measure(args, torch, np, workload: str, *, steps: int, warmup: int, traffic: bool,
+            cpu_seconds: float, kernel_launches: int, min_rotation_gb: float) -> dict:
+    """One workload: the timed layer steps (one HIP graph, or one per decode step
+    for the layer stack), the dominant kernel live with HIP events, optionally
+    its HBM traffic (counter passes) and the CPU baseline.  Frees its device
+    memory before returning."""
+    S = Setup(args, torch, np, workload, steps, warmup, min_rotation_gb)
+    R = kernel_launches
     S.kernel_plans(R)
-    if args.mode == "kernel":
-        for r in range(R):
-            S.gate_up(r)
-        torch.cuda.synchronize()
-        return 0
-
     native, keys = S.native, S.keys
     T, d, E, k, I, Is, shape = S.T, S.d, S.E, S.k, S.I, S.Is, S.shape
     ws_bytes = S.lib.glm_moe_workspace_bytes(T, d, E, k, I, Is)
@@ -385,31 +381,38 @@ def main() -> int:
         return ev0.elapsed_time(ev1) / count, time.perf_counter() - wall0
 
     # ------------------------------------------------------------ timed steps
+    unique_per_step = None
     if S.layers > 1:
         stack_step(0)  # eager pass (validates the launches outside capture)
         torch.cuda.synchronize()
         # one graph per decode step (each step has its own routing biases)
-        graphs = [capture(stack_step, s, 1) for s in range(args.warmup + args.steps)]
-        for g in graphs[:args.warmup]:
+        graphs = [capture(stack_step, s, 1) for s in range(warmup + steps)]
+        for g in graphs[:warmup]:
             g.replay()
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         wall0 = time.perf_counter()
         ev0.record()
-        for g in graphs[args.warmup:]:
+        for g in graphs[warmup:]:
             g.replay()
         ev1.record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - wall0
-        ms_per_step = ev0.elapsed_time(ev1) / args.steps
+        ms_per_step = ev0.elapsed_time(ev1) / steps
         del graphs
     else:
         for s in range(S.n_banks):  # eager pass over every bank first
             layer_step(s)
         torch.cuda.synchronize()
-        if args.warmup > 0:
-            capture(layer_step, 0, args.warmup).replay()
-        ms_per_step, wall = timed(capture(layer_step, args.warmup, args.steps), args.steps)
+        # the distinct experts each timed step routes to (an eager run of the
+        # same steps: same banks, inputs and biases)
+        unique_per_step = []
+        for s in range(warmup, warmup + steps):
+            layer_step(s)
+            unique_per_step.append(len(np.unique(idx.cpu().numpy())))
+        if warmup > 0:
+            capture(layer_step, 0, warmup).replay()
+        ms_per_step, wall = timed(capture(layer_step, warmup, steps), steps)
     tokens_per_s = T / (ms_per_step / 1e3)
 
     # ------------------------------------------------------------ dominant kernel
@@ -422,91 +425,199 @@ def main() -> int:
     del gk
     torch.cuda.synchronize()
 
-    traffic, traffic_note = None, "not measured (--traffic 0)"
-    if args.traffic:
-        traffic, traffic_note = measure_traffic(args, S.kernel_name())
+    traffic_v, traffic_note = None, "not measured (--traffic 0)"
+    if traffic:
+        traffic_v, traffic_note = measure_traffic(args, workload, S.kernel_name())
 
-    # ------------------------------------------------------------ CPU baseline
     cpu = None
-    if args.cpu_seconds > 0:
-        cpu = cpu_baseline(shape, S.banks[0], S.xs, args.cpu_seconds,
+    if cpu_seconds > 0:
+        cpu = cpu_baseline(shape, S.banks[0], S.xs, cpu_seconds,
                            None if S.trace is None else S.trace[0, 0],
                            S.streams if S.hc else None)
 
-    line = {
-        "metric": METRIC,
-        "value": round(tokens_per_s, 1),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
-        "config": {
-            "workload": (f"{shape.name}: decoder FFN site, hyper-connection of {S.hc} f32 "
-                         f"residual streams (20 Sinkhorn rounds) + RMSNorm + MoE layer T={T} "
-                         f"d={d} E={E} top-{k} I={I} (MXFP4 group-32 experts, bf16 shared "
-                         f"expert I={Is}) + hyper_residual"
-                         if S.hc else
-                         f"{shape.name}: {S.layers} layers x (MXFP8 {d}x{d} resident linear + "
-                         f"MoE layer T={T} d={d} E={E} top-{k} I={I}, MXFP4 group-32 experts, "
-                         f"bf16 shared expert I={Is}), Markov routing keeping 70% of the "
-                         f"previous step's experts, one token per step"
-                         if S.layers > 1 else
-                         f"{shape.name}: MoE layer T={T} d={d} E={E} top-{k} I={I} "
-                         f"(MXFP4 group-32 experts, bf16 shared expert I={Is})"),
-            "tokens_per_step": T, "weights": "mxfp4-e2m1+e8m0",
-            "mfma": ("fp8 hi/lo split x mxfp4, block-scaled" if S.grouped
-                     else "bf16 x dequantised mxfp4"), "layer_banks": S.n_banks,
-            "rotation_bytes": S.n_banks * S.layer_bytes, "graph_steps": args.steps,
-            "wall_s": round(wall, 4),
-        },
-        "roofline": roofline(S, achieved, tflops, bytes_per_launch, k_ms, R, traffic,
+    res = {
+        "workload": workload, "shape": shape, "tokens_per_s": tokens_per_s,
+        "ms_per_step": ms_per_step, "wall": wall, "grouped": S.grouped, "few_token": S.few_token,
+        "layers": S.layers, "hc": S.hc, "n_banks": S.n_banks,
+        "rotation_bytes": S.n_banks * S.layer_bytes, "kernel_name": S.kernel_name(),
+        "roofline": roofline(S, achieved, tflops, bytes_per_launch, k_ms, R, traffic_v,
                              traffic_note),
+        "kernel_tflops": tflops, "kernel_ms": k_ms, "kernel_flops": S.kernel_flops(),
+        "cpu": cpu,
     }
-    if S.grouped:
-        # the grouped GEMM runs bf16 MFMA on exactly dequantised MXFP4 weights;
-        # its share of the MXFP4 dense peak is what the metric names
-        line["prefill_mfma_tflops"] = round(tflops, 1)
-        line["mxfp4_mfma_util"] = round(tflops / MFMA_PEAK_TFLOPS["fp4"], 4)
-    else:
-        line["decode_expert_hbm_gbps"] = round(achieved, 1)
+    if unique_per_step and not S.grouped:
+        # the layer-level decode rate: the selected experts' bytes of a step
+        # over the whole step's device time (router -> gate/up -> down ->
+        # combine, shared expert included)
+        u = sum(unique_per_step) / len(unique_per_step)
+        res["unique_experts_per_step"] = u
+        res["layer_expert_gbps"] = u * shape.expert_bytes / (ms_per_step / 1e3) / 1e9
     if S.layers > 1:
         # bytes one decode step reads: every layer's k experts (Markov
         # routing at T=1 picks k distinct ones), shared expert, linear, router
         expert = S.layers * k * shape.expert_bytes
         other = S.layers * (3 * Is * d * 2 + d * d + d * d // 32 + E * d * 4)
         sec = ms_per_step / 1e3
-        line["stack"] = {"layers": S.layers, "us_per_layer": round(ms_per_step * 1e3 / S.layers, 3),
-                         "expert_bytes_per_step": expert, "all_bytes_per_step": expert + other,
-                         "expert_hbm_gbps": round(expert / sec / 1e9, 1),
-                         "all_hbm_gbps": round((expert + other) / sec / 1e9, 1)}
-    line["cpu_baseline"] = cpu
+        res["stack"] = {"layers": S.layers,
+                        "us_per_layer": round(ms_per_step * 1e3 / S.layers, 3),
+                        "expert_bytes_per_step": expert, "all_bytes_per_step": expert + other,
+                        "expert_hbm_gbps": round(expert / sec / 1e9, 1),
+                        "expert_hbm_frac": round(expert / sec / 1e9 / HBM_PEAK_GBPS, 4),
+                        "all_hbm_gbps": round((expert + other) / sec / 1e9, 1)}
+    del S, ws, out, wts, idx, act
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return res
+
+
+def describe(r: dict) -> str:
+    """The workload's configuration in words."""
+    sh, T = r["shape"], r["shape"].T
+    if r["hc"]:
+        return (f"{sh.name}: decoder FFN site, hyper-connection of {r['hc']} f32 residual "
+                f"streams (20 Sinkhorn rounds) + RMSNorm + MoE layer T={T} d={sh.d} E={sh.E} "
+                f"top-{sh.k} I={sh.I} (MXFP4 group-32 experts, bf16 shared expert "
+                f"I={sh.I_shared}) + hyper_residual")
+    if r["layers"] > 1:
+        return (f"{sh.name}: {r['layers']} layers x (MXFP8 {sh.d}x{sh.d} resident linear + "
+                f"MoE layer T={T} d={sh.d} E={sh.E} top-{sh.k} I={sh.I}, MXFP4 group-32 experts, "
+                f"bf16 shared expert I={sh.I_shared}), Markov routing keeping 70% of the "
+                f"previous step's experts, one token per step")
+    return (f"{sh.name}: MoE layer T={T} d={sh.d} E={sh.E} top-{sh.k} I={sh.I} "
+            f"(MXFP4 group-32 experts, bf16 shared expert I={sh.I_shared})")
+
+
+def prefill_leg(r: dict, counters: dict | None) -> dict:
+    """The metric's third part: the T=4096 grouped gate/up GEMM's MXFP4 MFMA
+    utilisation -- algorithmic FLOPs (two projections x 2 d I per (token,
+    expert) pair) per second over the 10.1 PFLOP/s dense FP4 peak, and the
+    executed MFMA operations the counters report over the same launches."""
+    peak = MFMA_PEAK_TFLOPS["fp4"]
+    alg = r["kernel_tflops"]
+    leg = {
+        "workload": describe(r), "tokens_per_s": round(r["tokens_per_s"], 1),
+        "ms_per_step": round(r["ms_per_step"], 5), "kernel": r["kernel_name"],
+        "avg_launch_us": round(r["kernel_ms"] * 1e3, 3),
+        "algorithmic_flops_per_launch": r["kernel_flops"],
+        "algorithmic_tflops": round(alg, 1), "fp4_peak_tflops": peak,
+        "mxfp4_mfma_util": round(alg / peak, 4),
+        # the split design issues two FP8 x FP4 MFMAs (x's hi and lo parts) per
+        # product at the 5.0 PFLOP/s FP8 rate: 2.5 PFLOP/s of algorithmic work
+        # at most
+        "design_ceiling_tflops": MFMA_PEAK_TFLOPS["bf16"],
+        "frac_of_design_ceiling": round(alg / MFMA_PEAK_TFLOPS["bf16"], 4),
+    }
+    if counters:
+        leg["counters"] = counters
+        ex = counters.get("executed_flops_per_launch")
+        if ex:
+            ex_tf = ex / (r["kernel_ms"] / 1e3) / 1e12
+            leg["executed_tflops"] = round(ex_tf, 1)
+            leg["executed_frac_of_fp4_peak"] = round(ex_tf / peak, 4)
+            leg["executed_frac_of_fp8_peak"] = round(ex_tf / MFMA_PEAK_TFLOPS["fp8"], 4)
+    return leg
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this benchmark runs the MoE layer on one GPU; runs over "
+                                   "several GPUs (the layer sharded by expert) are not supported",
+                          "n_gpus": args.gpus}))
+        return 2
+
+    import numpy as np
+    import torch
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        return 1
+    if args.mode == "copy":
+        return copy_probe(torch)
+    if args.workload == "bank_load":
+        return bank_load_bench(args, torch, np)
+    if args.mode == "kernel":
+        S = Setup(args, torch, np, args.workload, args.steps, args.warmup, args.min_rotation_gb)
+        S.kernel_plans(args.kernel_launches)
+        for r in range(args.kernel_launches):
+            S.gate_up(r)
+        torch.cuda.synchronize()
+        return 0
+
+    r = measure(args, torch, np, args.workload, steps=args.steps, warmup=args.warmup,
+                traffic=bool(args.traffic), cpu_seconds=args.cpu_seconds,
+                kernel_launches=args.kernel_launches, min_rotation_gb=args.min_rotation_gb)
+    legs = args.legs == "auto" and args.workload == "verify_t2"
+    line = {
+        "metric": METRIC,
+        "value": round(r["tokens_per_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": describe(r),
+            "tokens_per_step": r["shape"].T, "weights": "mxfp4-e2m1+e8m0",
+            "mfma": ("fp8 hi/lo split x mxfp4, block-scaled" if r["grouped"]
+                     else "bf16 x dequantised mxfp4"), "layer_banks": r["n_banks"],
+            "rotation_bytes": r["rotation_bytes"], "graph_steps": args.steps,
+            "wall_s": round(r["wall"], 4),
+        },
+        "roofline": r["roofline"],
+    }
+    if "layer_expert_gbps" in r:
+        # selected-expert bytes over the layer step's whole device time
+        line["decode_expert_hbm_gbps"] = round(r["layer_expert_gbps"], 1)
+        line["decode_expert_hbm_frac"] = round(r["layer_expert_gbps"] / HBM_PEAK_GBPS, 4)
+        line["decode_unique_experts_per_step"] = round(r["unique_experts_per_step"], 2)
+    if r["grouped"]:
+        line["prefill"] = prefill_leg(r, mfma_counters(args, r["workload"], r["kernel_name"])
+                                      if args.traffic else None)
+        line["mxfp4_mfma_util"] = line["prefill"]["mxfp4_mfma_util"]
+    if "stack" in r:
+        line["stack"] = r["stack"]
+    if legs:
+        # the metric's other parts in the same run: the T=4096 prefill layer
+        # (MXFP4 MFMA utilisation of its grouped GEMM) and the 42-layer decode
+        # stack, each on its own banks
+        pf = measure(args, torch, np, "prefill_t4096", steps=args.steps, warmup=args.warmup,
+                     traffic=False, cpu_seconds=0.0, kernel_launches=32, min_rotation_gb=0.0)
+        line["prefill"] = prefill_leg(pf, mfma_counters(args, "prefill_t4096", pf["kernel_name"])
+                                      if args.traffic else None)
+        line["mxfp4_mfma_util"] = line["prefill"]["mxfp4_mfma_util"]
+        st = measure(args, torch, np, "stack42_t1", steps=args.steps, warmup=args.warmup,
+                     traffic=False, cpu_seconds=0.0, kernel_launches=64, min_rotation_gb=0.0)
+        line["stack"] = {"workload": describe(st), "tokens_per_s": round(st["tokens_per_s"], 1),
+                         "ms_per_step": round(st["ms_per_step"], 5), **st["stack"]}
+    line["cpu_baseline"] = r["cpu"]
     print(json.dumps(line))
     return 0
 
 
 def roofline(S, achieved, tflops, bytes_per_launch, k_ms, R, traffic, traffic_note):
-    """The dominant kernel against its bound: HBM for the decode GEMVs, bf16
-    MFMA for the grouped prefill GEMM."""
+    """The dominant kernel against its bound: HBM for the decode GEMVs, the
+    dense MXFP4 MFMA peak for the grouped prefill GEMM."""
     common = {"traffic": traffic, "traffic_note": traffic_note,
               "bytes_per_launch": round(bytes_per_launch), "avg_launch_us": round(k_ms * 1e3, 3),
               "launches": R, "unique_experts_per_launch": round(sum(S.unique) / R, 2)}
     if S.grouped:
-        # two block-scaled FP8 x FP4 MFMAs (activation hi and lo parts) per
-        # algorithmic product at the 5 PFLOP/s FP8 rate: 2.5 PFLOP/s of
-        # algorithmic work at most, the bf16 peak
+        # algorithmic FLOPs over the 10.1 PFLOP/s dense MXFP4 peak; the kernel
+        # runs block-scaled FP8 x FP4 MFMAs on the exact hi/lo split of the
+        # activations, two per product at the 5.0 PFLOP/s FP8 rate, so its own
+        # ceiling is 2.5 PFLOP/s of algorithmic work (reported beside it)
         return {"kernel": S.kernel_name() + " (grouped MXFP4 gate/up + SwiGLU GEMMs, block-scaled "
                                             "FP8 x FP4 MFMA on the exact hi/lo split of x)",
-                "bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_PEAK_TFLOPS["bf16"],
-                "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS["bf16"], 4),
+                "bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_PEAK_TFLOPS["fp4"],
+                "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS["fp4"], 4),
                 "flops_per_launch": S.kernel_flops(),
-                "peak_note": "algorithmic FLOPs; the kernel issues two FP8 x FP4 MFMAs per "
-                             "product at the 5.0 PFLOP/s dense FP8 rate",
+                "design_ceiling": MFMA_PEAK_TFLOPS["bf16"],
+                "frac_of_design_ceiling": round(tflops / MFMA_PEAK_TFLOPS["bf16"], 4),
                 **common}
     return {"kernel": S.kernel_name() + (" (few-token selection + routed MXFP4 gate/up + SwiGLU)"
                                          if S.few_token else
@@ -718,15 +829,15 @@ def copy_probe(torch) -> int:
     return 0
 
 
-def _counter_pass(counter: str, child_args: list[str]) -> dict[str, list[float]]:
+def _counter_pass(counters: list[str], child_args: list[str]) -> dict[str, dict[str, list[float]]]:
     """One rocprofv3 counter pass over a child run of this script; returns
-    {kernel name: per-dispatch values (KiB)}."""
+    {counter: {kernel name: per-dispatch values}}."""
     out = tempfile.mkdtemp(prefix="glm_pmc_", dir="/tmp")
     env = dict(os.environ, TMPDIR="/tmp")
-    cmd = ["rocprofv3", "--pmc", counter, "-f", "csv", "-d", out, "-o", "run", "--",
+    cmd = ["rocprofv3", "--pmc", *counters, "-f", "csv", "-d", out, "-o", "run", "--",
            sys.executable, os.path.abspath(__file__)] + child_args
-    print(f"bench: counter pass {counter} over {' '.join(child_args)}", file=sys.stderr,
-          flush=True)
+    print(f"bench: counter pass {' '.join(counters)} over {' '.join(child_args)}",
+          file=sys.stderr, flush=True)
     try:
         # own process group, so that a pass over its time limit ends with its children
         proc = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL,
@@ -737,31 +848,36 @@ def _counter_pass(counter: str, child_args: list[str]) -> dict[str, list[float]]
             os.killpg(proc.pid, signal.SIGKILL)
             proc.wait()
             return {}
-        vals: dict[str, list[float]] = {}
+        vals: dict[str, dict[str, list[float]]] = {}
         for path in glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True):
             with open(path) as f:
                 for row in csv.DictReader(f):
-                    if row.get("Counter_Name") == counter:
-                        vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+                    if row.get("Counter_Name") in counters:
+                        vals.setdefault(row["Counter_Name"], {}).setdefault(
+                            row["Kernel_Name"], []).append(float(row["Counter_Value"]))
         return vals
     finally:
         shutil.rmtree(out, ignore_errors=True)
 
 
-def measure_traffic(args, kernel_name: str):
+def _kernel_child(args, workload: str, launches: int, rotation_gb: float) -> list[str]:
+    return ["--mode", "kernel", "--workload", workload, "--kernel-launches", str(launches),
+            "--seed", str(args.seed), "--min-rotation-gb", str(rotation_gb)]
+
+
+def measure_traffic(args, workload: str, kernel_name: str):
     """HBM bytes per launch of the dominant kernel: FETCH_SIZE and WRITE_SIZE
     (KiB per dispatch) in two passes over a run of its launches, each scaled by
     what the same counter reads for a device copy of COPY_BYTES."""
     if shutil.which("rocprofv3") is None:
         return None, "rocprofv3 not found"
-    child = ["--mode", "kernel", "--workload", args.workload, "--kernel-launches", "32",
-             "--seed", str(args.seed), "--min-rotation-gb", str(args.min_rotation_gb)]
+    child = _kernel_child(args, workload, 32, args.min_rotation_gb)
     res = {}
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-        copy_vals = [v for name, vs in _counter_pass(counter, ["--mode", "copy"]).items()
-                     if "copy" in name.lower() for v in vs]
-        kern = [v for name, vs in _counter_pass(counter, child).items() if kernel_name in name
-                for v in vs]
+        copy_vals = [v for name, vs in _counter_pass([counter], ["--mode", "copy"]).get(
+            counter, {}).items() if "copy" in name.lower() for v in vs]
+        kern = [v for name, vs in _counter_pass([counter], child).get(counter, {}).items()
+                if kernel_name in name for v in vs]
         if not copy_vals or not kern or max(copy_vals) <= 0:
             return None, f"{counter}: no counter rows (copy {len(copy_vals)}, kernel {len(kern)})"
         scale = COPY_BYTES / (max(copy_vals) * 1024.0)
@@ -771,6 +887,33 @@ def measure_traffic(args, kernel_name: str):
             f"{COPY_BYTES >> 20} MiB device copy), mean over {fetch[2]} dispatches: "
             f"read {fetch[0] / 1e6:.2f} MB, write {write[0] / 1e6:.3f} MB")
     return round(fetch[0] + write[0]), note
+
+
+MFMA_COUNTERS = ["SQ_INSTS_VALU_MFMA_MOPS_F8", "SQ_INSTS_VALU_MFMA_MOPS_F6F4",
+                 "SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE"]
+
+
+def mfma_counters(args, workload: str, kernel_name: str) -> dict | None:
+    """MFMA work of the grouped GEMM from one counter pass: the MOPS counters
+    count 512 floating-point operations each (F8 covers the FP8 x FP4 forms,
+    F6F4 the FP4/FP6-only forms), so executed FLOPs per launch = 512 x (F8 +
+    F6F4); SQ_VALU_MFMA_BUSY_CYCLES sums the MFMA pipes' busy cycles over all
+    SIMDs."""
+    if shutil.which("rocprofv3") is None:
+        return None
+    vals = _counter_pass(MFMA_COUNTERS, _kernel_child(args, workload, 8, 0.0))
+    per = {}
+    for c in MFMA_COUNTERS:
+        v = [x for name, xs in vals.get(c, {}).items() if kernel_name in name for x in xs]
+        if not v:
+            return {"error": f"no {c} rows for {kernel_name}"}
+        per[c] = sum(v) / len(v)
+    executed = 512.0 * (per["SQ_INSTS_VALU_MFMA_MOPS_F8"] + per["SQ_INSTS_VALU_MFMA_MOPS_F6F4"])
+    return {"mops_f8_per_launch": per["SQ_INSTS_VALU_MFMA_MOPS_F8"],
+            "mops_f6f4_per_launch": per["SQ_INSTS_VALU_MFMA_MOPS_F6F4"],
+            "mfma_busy_cycles_per_launch": per["SQ_VALU_MFMA_BUSY_CYCLES"],
+            "executed_flops_per_launch": executed, "launches": 8,
+            "note": "rocprofv3 --pmc " + " ".join(MFMA_COUNTERS) + " over 8 launches"}
 
 
 def host_cpu() -> dict:
