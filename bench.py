@@ -634,10 +634,9 @@ def bank_load_bench(args, torch, np) -> int:
     storage's rate).  The device side's kernel, the scatter of staged records
     into the bank tensors, is timed with HIP events on its stream."""
     from glm53flash.bank_loader import ExpertBankLoader
-    from glm53flash.contract import ModelContract
-    from glm53flash.expert_source import build_native_expert_source_plan
+    from glm53flash.bank_plan import plan_expert_banks
+    from glm53flash.checkpoint import ShardIndex
     from glm53flash.expert_ssd import HBMExpertBank
-    from glm53flash.model_config import GLMTextConfig
     from livglm_amd import native
     from livglm_amd.workloads import SHAPES, write_expert_checkpoint
 
@@ -650,17 +649,15 @@ def bank_load_bench(args, torch, np) -> int:
         payload = write_expert_checkpoint(root, shape, layers, args.seed,
                                           two_value_scales=bool(args.scalex))
         if args.scalex:
-            from glm53flash.scalex_container import compress_scalex_layer
+            from glm53flash.scalex_layer import write_scalex_layer
             for layer in layers:
                 shard = os.path.join(root, f"model-layer{layer:02d}.safetensors")
-                compress_scalex_layer(shard, shard + ".sx", layer=layer, experts=shape.E)
+                write_scalex_layer(shard, shard + ".sx", layer=layer, experts=shape.E)
                 os.replace(shard + ".sx", shard)
         print(f"bank_load: wrote {payload / 1e9:.2f} GB in {time.perf_counter() - t0:.1f} s",
               file=sys.stderr, flush=True)
-        cfg = GLMTextConfig(hidden_size=shape.d, moe_intermediate_size=shape.I,
-                            n_routed_experts=shape.E)
-        plan = build_native_expert_source_plan(ModelContract.from_model_dir(root), cfg,
-                                               first_layer=layers[0], last_layer=layers[-1])
+        plan = plan_expert_banks(ShardIndex.open(root), hidden_size=shape.d,
+                                 intermediate_size=shape.I, experts=shape.E, layers=layers)
         banks = [HBMExpertBank(layer=l, num_experts=shape.E, hidden_size=shape.d,
                                intermediate_size=shape.I, swiglu_limit=shape.swiglu_limit,
                                device="cuda") for l in layers]
@@ -677,7 +674,7 @@ def bank_load_bench(args, torch, np) -> int:
         warm_s, stats = load_all()
         print(f"bank_load: page cache -> HBM {payload / warm_s / 1e9:.2f} GB/s", file=sys.stderr,
               flush=True)
-        shards = sorted({r.shard_name for p in plan.packs for r in p.read_ranges})
+        shards = list(plan.shards)
 
         def drop_pages():
             for shard in shards:
@@ -698,33 +695,36 @@ def bank_load_bench(args, torch, np) -> int:
         # every slot of the first and the last layer against the shard bytes
         # (a ScaleX shard: against the tensors its reader rebuilds)
         if args.scalex:
-            from glm53flash.scalex_container import read_scalex_layout, read_scalex_tensor
+            from glm53flash.bank_plan import BANK_KEYS, expert_tensor_name
+            from glm53flash.scalex_layer import ScaleXLayer
             checked = 0
             for b in (banks[0], banks[-1]):
-                layout = read_scalex_layout(os.path.join(root, shards[0 if b is banks[0] else -1]))
+                layout = ScaleXLayer.read(os.path.join(root, shards[0 if b is banks[0] else -1]))
                 for e in (0, shape.E // 2, shape.E - 1):
-                    for t in plan.expert(b.layer, e).tensors:
-                        want = np.frombuffer(read_scalex_tensor(layout, t.source_name), np.uint8)
-                        got = b.tensors[t.bank_name][e].cpu().numpy().reshape(-1)
+                    for key in BANK_KEYS:
+                        tname = expert_tensor_name(b.layer, e, *key.split("."))
+                        want = np.frombuffer(layout.tensor_bytes(tname), np.uint8)
+                        got = b.tensors[key][e].cpu().numpy().reshape(-1)
                         if not np.array_equal(got, want):
-                            raise SystemExit(f"bank_load: layer {b.layer} {t.source_name} differs")
+                            raise SystemExit(f"bank_load: layer {b.layer} {tname} differs")
                         checked += want.size
         else:
+            first = plan.expert(layers[0], 0).reads[0]
             blob = np.fromfile(os.path.join(root, shards[0]), dtype=np.uint8,
-                               offset=plan.expert(layers[0], 0).read_ranges[0].absolute_offset)
+                               offset=first.offset)
             blob = blob[:shape.E * shape.expert_bytes].reshape(shape.E, shape.expert_bytes)
             checked = 0
             for b in (banks[0], banks[-1]):
-                for t in plan.expert(b.layer, 0).tensors:
-                    rel = t.absolute_offset - plan.expert(b.layer, 0).read_ranges[0].absolute_offset
-                    want = blob[:, rel:rel + t.byte_length]
-                    got = b.tensors[t.bank_name].cpu().numpy().reshape(shape.E, -1)
+                # every layer stores the same bank, expert records back to back
+                for seg in first.segments:
+                    want = blob[:, seg.at:seg.at + seg.nbytes]
+                    got = b.tensors[seg.key].cpu().numpy().reshape(shape.E, -1)
                     if not np.array_equal(got, want):
-                        raise SystemExit(f"bank_load: layer {b.layer} {t.bank_name} differs")
+                        raise SystemExit(f"bank_load: layer {b.layer} {seg.key} differs")
                     checked += want.size
         # host side alone: the native reader into pinned memory
         host = torch.empty(chunk, dtype=torch.uint8, pin_memory=True)
-        rng0 = plan.expert(layers[0], 0).read_ranges[0].absolute_offset
+        rng0 = plan.expert(layers[0], 0).reads[0].offset
         n_read = min(chunk, shape.E * shape.expert_bytes)
         offs = np.array([rng0], dtype=np.int64)
         lens = np.array([n_read], dtype=np.int64)

@@ -33,9 +33,10 @@ import torch
 
 from . import _native as N
 from .contract import ContractError
-from .expert_source import NativeExpertSourcePlan, expected_shape
+from .bank_plan import BankPlan, slot_shape
 from .expert_ssd import HBMExpertBank
 from .scale_codec import A_ONE_BIT, A_RAW, A_TWO_BIT, ScaleCodecError, validate_mode_a
+from .scalex_layer import RECORD_ORDER
 
 _CODECS = {"raw": A_RAW, "one_bit": A_ONE_BIT, "two_bit": A_TWO_BIT}
 
@@ -66,12 +67,12 @@ class _Read:
 
 
 class ExpertBankLoader:
-    """Loads whole layers of a :class:`NativeExpertSourcePlan` into
+    """Loads whole layers of a :class:`BankPlan` into
     :class:`HBMExpertBank` objects.  The staging buffers (``buffers`` pinned
     host and device chunks of ``chunk_bytes``) are allocated on first use and kept
     for later layers; ``close()`` releases them."""
 
-    def __init__(self, plan: NativeExpertSourcePlan, *, threads: int = 16,
+    def __init__(self, plan: BankPlan, *, threads: int = 16,
                  chunk_bytes: int = 64 << 20, drop_cache: bool = False, buffers: int = 3):
         if threads < 1:
             raise ContractError("the loader needs at least one read thread")
@@ -82,7 +83,7 @@ class ExpertBankLoader:
         self.nbuf = int(buffers)
         self.plan = plan
         self.threads = int(threads)
-        largest = max((r.byte_length for p in plan.packs for r in p.read_ranges), default=0)
+        largest = max((r.nbytes for x in plan.loads for r in x.reads), default=0)
         # a chunk holds at least the largest single read
         self.chunk_bytes = max(int(chunk_bytes), _round_up(largest, _ALIGN))
         self.flags = N.native.GLM_READ_DROP_CACHE if drop_cache else 0
@@ -117,18 +118,18 @@ class ExpertBankLoader:
         self._keep = [None] * self.nbuf
 
     def _chunks(self, layer: int) -> list[list[tuple[object, object]]]:
-        """The layer's (expert source, read range) units in shard-offset order,
+        """The layer's (expert load, read) units in shard-offset order,
         packed into chunks of at most chunk_bytes staged bytes (one shard per
         chunk)."""
-        units = [(src, rng) for src in self.plan.layer_sources(layer) for rng in src.read_ranges]
-        units.sort(key=lambda u: (u[1].shard_name, u[1].absolute_offset))
-        chunks: list[list[tuple[int, object]]] = []
+        units = [(x, rd) for x in self.plan.layer_loads(layer) for rd in x.reads]
+        units.sort(key=lambda u: (u[1].shard, u[1].offset))
+        chunks: list[list[tuple[object, object]]] = []
         used = 0
         for unit in units:
-            rng = unit[1]
-            size = _round_up(rng.byte_length, _ALIGN)
+            rd = unit[1]
+            size = _round_up(rd.nbytes, _ALIGN)
             if (not chunks or used + size > self.chunk_bytes
-                    or chunks[-1][-1][1].shard_name != rng.shard_name):
+                    or chunks[-1][-1][1].shard != rd.shard):
                 chunks.append([])
                 used = 0
             chunks[-1].append(unit)
@@ -137,22 +138,19 @@ class ExpertBankLoader:
 
     def _check(self, bank: HBMExpertBank, layer: int) -> None:
         plan = self.plan
-        if bank.num_experts != plan.experts_per_layer:
-            raise ContractError(f"bank holds {bank.num_experts} experts, the checkpoint layer "
-                                f"{plan.experts_per_layer}")
+        if bank.num_experts != plan.experts:
+            raise ContractError(f"bank holds {bank.num_experts} experts, the plan {plan.experts}")
+        if (bank.hidden_size, bank.intermediate_size) != (plan.hidden_size,
+                                                          plan.intermediate_size):
+            raise ContractError(f"bank geometry d {bank.hidden_size} I {bank.intermediate_size} "
+                                f"differs from the plan's d {plan.hidden_size} "
+                                f"I {plan.intermediate_size}")
         bank._require_active()
-        shapes = bank.shapes()
-        for name, shape in shapes.items():
-            comp, part = name.split(".")
-            want = expected_shape(comp, part, hidden_size=bank.hidden_size,
-                                  intermediate_size=bank.intermediate_size)
+        for name, shape in bank.shapes().items():
+            want = slot_shape(name, plan.hidden_size, plan.intermediate_size)
             if tuple(shape[1:]) != want:
                 raise ContractError(f"bank tensor {name} has rows {shape[1:]}, expected {want}")
-        for src in plan.layer_sources(layer):
-            for t in src.tensors:
-                if tuple(t.source_shape) != tuple(shapes[t.bank_name][1:]):
-                    raise ContractError(f"{t.source_name} has shape {t.source_shape}, the bank "
-                                        f"expects {shapes[t.bank_name][1:]}")
+        plan.layer_loads(layer)  # the layer must be planned
 
     def load(self, bank: HBMExpertBank, layer: int | None = None) -> BankLoadStats:
         """Fills every expert slot of ``bank`` from layer ``layer`` (default:
@@ -180,7 +178,7 @@ class ExpertBankLoader:
             slot_bytes = {name: int(np.prod(shape[1:])) for name, shape in shapes.items()}
             base = {name: bank.tensors[name].data_ptr() for name in shapes}
             work.extend((base, slot_bytes, chunk) for chunk in self._chunks(layer))
-        self._buffers(device, max(sum(len(r.tensors) for _, r in c) for _, _, c in work))
+        self._buffers(device, max(sum(len(r.segments) for _, r in c) for _, _, c in work))
         stream = torch.cuda.current_stream(device)
         t0 = time.perf_counter()
         total = reads_total = 0
@@ -193,32 +191,24 @@ class ExpertBankLoader:
             segments: list[tuple[int, int, int]] = []
             coded: list[tuple[int, object]] = []  # (staging offset, ScaleX record)
             staged = 0
-            for src, rng in chunk:
-                expert = src.expert
-                if reads and reads[-1].offset + reads[-1].length == rng.absolute_offset:
+            for x, rd in chunk:
+                expert = x.expert
+                if reads and reads[-1].offset + reads[-1].length == rd.offset:
                     at = reads[-1].staging + reads[-1].length
-                    reads[-1].length += rng.byte_length
-                    staged = at + rng.byte_length
+                    reads[-1].length += rd.nbytes
+                    staged = at + rd.nbytes
                 else:
                     at = _round_up(staged, _ALIGN)
-                    reads.append(_Read(rng.shard_name, rng.absolute_offset, rng.byte_length, at))
-                    staged = at + rng.byte_length
-                rec = src.scalex_record
-                if rec is None:
-                    for t in rng.tensors:
-                        dst = base[t.bank_name] + expert * slot_bytes[t.bank_name]
-                        segments.append((at + rng.relative_offset(t), dst, t.byte_length))
-                        total += t.byte_length
-                else:
-                    # coded scales, then the gate, down and up weights
-                    w_at = at + rec.encoded_bytes
-                    for name, n in zip(rec.weight_names, rec.weight_nbytes):
-                        key = _bank_key(name)
-                        segments.append((w_at, base[key] + expert * slot_bytes[key], n))
-                        w_at += n
-                        total += n
-                    coded.append((at, rec, expert))
-                    total += rec.decoded_bytes
+                    reads.append(_Read(rd.shard, rd.offset, rd.nbytes, at))
+                    staged = at + rd.nbytes
+                for seg in rd.segments:
+                    segments.append((at + seg.at, base[seg.key] + expert * slot_bytes[seg.key],
+                                     seg.nbytes))
+                    total += seg.nbytes
+                if x.coded is not None:
+                    # a ScaleX record: its coded scales open the read
+                    coded.append((at, x.coded, expert))
+                    total += x.coded.decoded_bytes
             if staged > self.chunk_bytes:
                 raise AssertionError("staging chunk overflow")
             host = self._host[slot]
@@ -226,7 +216,7 @@ class ExpertBankLoader:
             lengths = np.array([r.length for r in reads], dtype=np.int64)
             dsts = (np.array([r.staging for r in reads], dtype=np.int64)
                     + host.data_ptr()).astype(np.uint64)
-            path = os.fspath(plan_shard_path(self.plan, reads[0].shard))
+            path = os.fspath(self.plan.shard_path(reads[0].shard))
             N.call("glm_file_read_ranges", path.encode(), len(reads), offsets.ctypes.data,
                    lengths.ctypes.data, dsts.ctypes.data, self.threads, self.flags)
             reads_total += len(reads)
@@ -247,9 +237,8 @@ class ExpertBankLoader:
             if ev is not None:
                 ev.synchronize()
         seconds = time.perf_counter() - t0
-        read_bytes = sum(r.byte_length for layer in layers
-                         for src in self.plan.layer_sources(layer) for r in src.read_ranges)
-        return BankLoadStats(layers=tuple(layers), experts=len(layers) * self.plan.experts_per_layer,
+        read_bytes = sum(x.read_bytes for layer in layers for x in self.plan.layer_loads(layer))
+        return BankLoadStats(layers=tuple(layers), experts=len(layers) * self.plan.experts,
                              bytes=total, read_bytes=read_bytes, reads=reads_total,
                              chunks=len(work), seconds=seconds)
 
@@ -264,44 +253,37 @@ class ExpertBankLoader:
         rows = []
         for at, rec, expert in coded:
             try:
-                info = validate_mode_a(buf[at:at + rec.encoded_bytes])
+                info = validate_mode_a(buf[at:at + rec.coded_bytes])
             except ScaleCodecError as exc:
                 raise ContractError(f"ScaleX record of expert {expert}: {exc}") from exc
             if info.raw_bytes != rec.decoded_bytes or info.codec != rec.codec:
-                raise ContractError(f"ScaleX record metadata changed for expert {expert}")
+                raise ContractError(f"expert {expert}'s coded scales are {info.codec} of "
+                                    f"{info.raw_bytes} B, its record says {rec.codec} of "
+                                    f"{rec.decoded_bytes} B")
             p = info.palette
-            row = [at, rec.encoded_bytes, rec.decoded_bytes, _CODECS[info.codec],
+            row = [at, rec.coded_bytes, rec.decoded_bytes, _CODECS[info.codec],
                    p[0] | (p[1] << 8) | (p[2] << 16) | (p[3] << 24), info.primary_bytes,
                    info.exceptions]
-            for name, n in zip(rec.scale_names, rec.scale_nbytes):
-                key = _bank_key(name)
+            for comp, n in zip(RECORD_ORDER, rec.scale_bytes):
+                key = f"{comp}.weight_scale"
                 if n != slot_bytes[key]:
-                    raise ContractError(f"{name} holds {n} bytes, the bank slot {slot_bytes[key]}")
+                    raise ContractError(f"expert {expert}'s {key} holds {n} bytes, the bank "
+                                        f"slot {slot_bytes[key]}")
                 row += [base[key] + expert * slot_bytes[key], n]
             rows.append(row)
         return np.ascontiguousarray(np.array(rows, dtype=np.int64))
-
-
-def _bank_key(tensor_name: str) -> str:
-    """``...experts.<e>.<component>.<part>`` -> ``<component>.<part>``."""
-    return ".".join(tensor_name.rsplit(".", 2)[-2:])
-
-
-def plan_shard_path(plan: NativeExpertSourcePlan, shard_name: str) -> str:
-    return os.path.join(plan.model_dir, shard_name)
 
 
 def _round_up(v: int, a: int) -> int:
     return (v + a - 1) // a * a
 
 
-def load_layer_bank(plan: NativeExpertSourcePlan, layer: int, *, swiglu_limit: float,
-                    hidden_size: int, intermediate_size: int,
+def load_layer_bank(plan: BankPlan, layer: int, *, swiglu_limit: float,
                     device: torch.device | str | None = None,
                     loader: ExpertBankLoader | None = None) -> HBMExpertBank:
     """A new :class:`HBMExpertBank` for ``layer`` filled from the checkpoint."""
-    bank = HBMExpertBank(layer=layer, num_experts=plan.experts_per_layer,
-                         hidden_size=hidden_size, intermediate_size=intermediate_size,
+    bank = HBMExpertBank(layer=layer, num_experts=plan.experts,
+                         hidden_size=plan.hidden_size, intermediate_size=plan.intermediate_size,
                          swiglu_limit=swiglu_limit, device=device)
     own = loader is None
     loader = loader or ExpertBankLoader(plan)

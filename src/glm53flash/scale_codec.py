@@ -83,12 +83,14 @@ def encode_mode_a(source: bytes) -> bytes:
 def inspect_mode_a(encoded) -> ModeAInfo:
     """Header fields of a record, checked against its length (``scale_codec.py:94-114``)."""
     if len(encoded) < MODE_A_HEADER.size:
-        raise ScaleCodecError("truncated Mode-A header")
+        raise ScaleCodecError(f"record of {len(encoded)} B is truncated: a Mode-A header takes "
+                              f"{MODE_A_HEADER.size}")
     magic, codec, p0, p1, p2, p3, raw, primary, exceptions = MODE_A_HEADER.unpack_from(encoded)
     if magic != MODE_A_MAGIC or codec not in CODEC_NAMES:
-        raise ScaleCodecError("invalid Mode-A header")
+        raise ScaleCodecError(f"not a Mode-A record (magic {magic!r}, codec {codec})")
     if MODE_A_HEADER.size + primary + 5 * exceptions != len(encoded):
-        raise ScaleCodecError("invalid Mode-A record length")
+        raise ScaleCodecError(f"record is {len(encoded)} B; its header describes "
+                              f"{MODE_A_HEADER.size + primary + 5 * exceptions} B")
     return ModeAInfo(raw_bytes=raw, encoded_bytes=len(encoded), codec=CODEC_NAMES[codec],
                      palette=(p0, p1, p2, p3), primary_bytes=primary, exceptions=exceptions)
 
@@ -100,15 +102,18 @@ def validate_mode_a(encoded) -> ModeAInfo:
     info = inspect_mode_a(encoded)
     if info.codec == "raw":
         if info.primary_bytes != info.raw_bytes or info.exceptions:
-            raise ScaleCodecError("invalid raw Mode-A record")
+            raise ScaleCodecError("a raw record must carry exactly its scale bytes and no "
+                                  "exceptions")
         return info
     bits = 1 if info.codec == "one_bit" else 2
     if info.primary_bytes != (info.raw_bytes * bits + 7) // 8:
-        raise ScaleCodecError("invalid Mode-A primary length")
+        raise ScaleCodecError(f"{info.codec} stream of {info.primary_bytes} B cannot code "
+                              f"{info.raw_bytes} scales")
     positions = np.frombuffer(encoded, dtype="<u4", count=info.exceptions,
                               offset=MODE_A_HEADER.size + info.primary_bytes)
     if info.exceptions and (positions[-1] >= info.raw_bytes or np.any(positions[1:] <= positions[:-1])):
-        raise ScaleCodecError("invalid Mode-A exception position")
+        raise ScaleCodecError("exception positions must ascend and stay below the scale "
+                              "count")
     return info
 
 
@@ -141,7 +146,7 @@ def mode_b_tile_prefix(encoded) -> bytes:
     (``scale_codec.py:117-141``)."""
     info = validate_mode_a(encoded)
     if info.exceptions > np.iinfo(np.uint16).max:
-        raise ScaleCodecError("Mode-B exception prefix exceeds uint16")
+        raise ScaleCodecError(f"{info.exceptions} exceptions overflow the u16 tile directory")
     positions = np.frombuffer(encoded, dtype="<u4", count=info.exceptions,
                               offset=MODE_A_HEADER.size + info.primary_bytes)
     tiles = (info.raw_bytes + MODE_B_TILE_SCALES - 1) // MODE_B_TILE_SCALES
@@ -152,7 +157,7 @@ def mode_b_tile_prefix(encoded) -> bytes:
 def mode_b_indexed_nbytes(encoded_bytes: int, raw_bytes: int) -> int:
     """``scale_codec.py:144-148``."""
     if encoded_bytes < MODE_A_HEADER.size or raw_bytes < 1:
-        raise ScaleCodecError("invalid Mode-B row geometry")
+        raise ScaleCodecError(f"no Mode-B row for {encoded_bytes} coded / {raw_bytes} raw bytes")
     tiles = (raw_bytes + MODE_B_TILE_SCALES - 1) // MODE_B_TILE_SCALES
     return encoded_bytes + (encoded_bytes & 1) + 2 * (tiles + 1)
 

@@ -1,8 +1,9 @@
-"""Checkpoint contract, expert source plan and the native range reader (CPU).
+"""Checkpoint index, bank load plan and the native range reader (CPU).
 
-The plan mirrors ``expert_source.py:270-381``; the shards are written by the
-test's own writer and by the ``safetensors`` library, whose reader is the
-independent check of the header parsing and byte ranges.
+The shards are written by the test's own writer and by the ``safetensors``
+library, whose reader is the independent check of the header parsing and
+byte ranges; every planned segment is checked against the bytes the writer
+put in the file.
 """
 
 from __future__ import annotations
@@ -16,17 +17,18 @@ import pytest
 
 from checkpoint_util import COMPONENTS, PARTS, make_checkpoint, name, write_safetensors
 
-from glm53flash.contract import (ContractError, ModelContract, local_safetensors_header,
-                                 routed_expert_parts)
-from glm53flash.expert_source import build_native_expert_source_plan, coalesce
-from glm53flash.model_config import GLMTextConfig
+from glm53flash.bank_plan import (REAL_RECORD_BYTES, _merge_adjacent, plan_expert_banks,
+                                  slot_shape)
+from glm53flash.checkpoint import ShardIndex, TensorRange, read_safetensors_header
+from glm53flash.contract import ContractError
 
 D, I, E = 64, 32, 12
 RECORD = 3 * I * D * 17 // 32
 
 
-def _config(E=E, d=D, I=I):
-    return GLMTextConfig(hidden_size=d, moe_intermediate_size=I, n_routed_experts=E)
+def _plan(root, layers=(3,), E=E, d=D, I=I):
+    return plan_expert_banks(ShardIndex.open(root), hidden_size=d, intermediate_size=I,
+                             experts=E, layers=layers)
 
 
 def _file_bytes(path, off, n):
@@ -43,7 +45,7 @@ def test_header_matches_the_safetensors_library(tmp_path):
                for e in range(3) for c in COMPONENTS for p in PARTS}
     path = str(tmp_path / "a.safetensors")
     st.save_file(tensors, path)
-    base, header = local_safetensors_header(path)
+    base, header = read_safetensors_header(path)
     for key, arr in tensors.items():
         start, end = header[key]["data_offsets"]
         assert _file_bytes(path, base + start, end - start) == arr.tobytes()
@@ -53,46 +55,39 @@ def test_header_matches_the_safetensors_library(tmp_path):
 
 def test_plan_locates_every_expert_record(tmp_path):
     arrays = make_checkpoint(str(tmp_path), layers=(3, 4), E=E, d=D, I=I)
-    contract = ModelContract.from_model_dir(tmp_path)
-    plan = build_native_expert_source_plan(contract, _config(), first_layer=3, last_layer=4)
-    assert plan.expert_count == 2 * E and plan.tensor_count == 12 * E
-    assert plan.uniform_pack_bytes == RECORD == plan.slot_bytes(3)
+    plan = _plan(tmp_path, layers=(3, 4))
+    assert len(plan.loads) == 2 * E and not plan.scalex
     # each expert's six tensors are adjacent in its shard: one read per record
-    assert plan.uniform_read_count == 1 and plan.read_bytes == plan.payload_bytes
+    assert plan.read_bytes == plan.bank_bytes == 2 * E * RECORD
     for layer in (3, 4):
         for e in range(E):
-            src = plan.expert(layer, e)
-            assert [t.source_name for t in src.tensors] == [
-                name(layer, e, c, p) for c in COMPONENTS for p in PARTS]
-            (rng,) = src.read_ranges
-            for t in src.tensors:
-                comp, part = t.bank_name.split(".")
-                path = os.path.join(plan.model_dir, t.shard_name)
+            x = plan.expert(layer, e)
+            assert (x.layer, x.expert) == (layer, e)
+            (rd,) = x.reads
+            assert rd.nbytes == RECORD
+            assert sorted(seg.key for seg in rd.segments) == sorted(
+                f"{c}.{p}" for c in COMPONENTS for p in PARTS)
+            path = plan.shard_path(rd.shard)
+            for seg in rd.segments:
+                comp, part = seg.key.split(".")
                 want = arrays[(layer, e)][(comp, part)]
-                assert t.byte_length == want.nbytes and t.source_shape == want.shape
-                assert _file_bytes(path, t.absolute_offset, t.byte_length) == want.tobytes()
-                assert 0 <= rng.relative_offset(t) < rng.byte_length
-            packed = [t for t in src.tensors if t.bank_name.endswith("weight_packed")]
-            assert all(t.mlx_dtype == "U32" and t.mlx_shape[-1] * 4 == t.source_shape[-1]
-                       for t in packed)
-    d = plan.as_dict()
-    assert d["uniform_pack_bytes"] == RECORD and d["layer_count"] == 2
-    assert d["source_format"] == "native_mxfp4" and not d["scalex_mode_b"]
+                assert want.shape == slot_shape(seg.key, D, I)
+                assert seg.nbytes == want.nbytes
+                assert _file_bytes(path, rd.offset + seg.at, seg.nbytes) == want.tobytes()
     with pytest.raises(ContractError):
         plan.expert(5, 0)
     with pytest.raises(ContractError):
         plan.expert(3, E)
 
 
-def test_coalesce_splits_at_gaps_and_shards():
-    from glm53flash.expert_source import ExpertTensorSource
+def test_adjacent_tensors_share_a_read_gaps_and_shards_split_them():
+    def t(shard, off, n, key="gate_proj.weight_packed"):
+        return TensorRange(f"x.{off}.{key}", shard, off, n, "U8", (n,))
 
-    def t(shard, off, n):
-        return ExpertTensorSource(f"x.{off}.weight_packed", "x", shard, off, n, (n,), "U8", (n,))
-
-    ranges = coalesce((t("b", 0, 4), t("a", 10, 5), t("a", 0, 10), t("a", 16, 2)))
-    assert [(r.shard_name, r.absolute_offset, r.byte_length, len(r.tensors)) for r in ranges] == [
-        ("a", 0, 15, 2), ("a", 16, 2, 1), ("b", 0, 4, 1)]
+    reads = _merge_adjacent([t("b", 0, 4), t("a", 10, 5), t("a", 0, 10), t("a", 16, 2)])
+    assert [(r.shard, r.offset, r.nbytes, [(s.at, s.nbytes) for s in r.segments])
+            for r in reads] == [("a", 0, 15, [(0, 10), (10, 5)]), ("a", 16, 2, [(0, 2)]),
+                                ("b", 0, 4, [(0, 4)])]
 
 
 def test_plan_rejects_broken_checkpoints(tmp_path):
@@ -104,7 +99,7 @@ def test_plan_rejects_broken_checkpoints(tmp_path):
     # wrong storage dtype
     root = fresh("dtype")
     shard = os.path.join(root, "model-layer3-00.safetensors")
-    base, header = local_safetensors_header(shard)
+    base, header = read_safetensors_header(shard)
     items = []
     for key, meta in sorted(header.items(), key=lambda kv: kv[1]["data_offsets"][0]):
         s, e = meta["data_offsets"]
@@ -115,19 +110,16 @@ def test_plan_rejects_broken_checkpoints(tmp_path):
             raw = raw.view(np.float32)
         items.append((key, raw.reshape(meta["shape"])))
     write_safetensors(shard, items)
-    with pytest.raises(ContractError, match="U8"):
-        build_native_expert_source_plan(ModelContract.from_model_dir(root), _config(E=4),
-                                        first_layer=3, last_layer=3)
+    with pytest.raises(ContractError, match="stored as I8"):
+        _plan(root, E=4)
     # config geometry differs from the stored shapes
     root = fresh("shape")
-    with pytest.raises(ContractError, match="shape mismatch"):
-        build_native_expert_source_plan(ModelContract.from_model_dir(root), _config(E=4, I=64),
-                                        first_layer=3, last_layer=3)
+    with pytest.raises(ContractError, match="geometry"):
+        _plan(root, E=4, I=64)
     # an expert that is not in the index
     root = fresh("missing")
-    with pytest.raises(ContractError, match="absent from model index"):
-        build_native_expert_source_plan(ModelContract.from_model_dir(root), _config(E=5),
-                                        first_layer=3, last_layer=3)
+    with pytest.raises(ContractError, match="not in the checkpoint index"):
+        _plan(root, E=5)
     # one expert split over two shards
     root = fresh("split")
     index_path = os.path.join(root, "model.safetensors.index.json")
@@ -137,41 +129,44 @@ def test_plan_rejects_broken_checkpoints(tmp_path):
     write_safetensors(os.path.join(root, "extra.safetensors"), [(moved, arr)])
     index["weight_map"][moved] = "extra.safetensors"
     json.dump(index, open(index_path, "w"))
-    with pytest.raises(ContractError, match="spans multiple shards"):
-        build_native_expert_source_plan(ModelContract.from_model_dir(root), _config(E=4),
-                                        first_layer=3, last_layer=3)
+    with pytest.raises(ContractError, match="split over shards"):
+        _plan(root, E=4)
     # a header whose byte range disagrees with dtype x shape
     root = fresh("range")
     shard = os.path.join(root, "model-layer3-00.safetensors")
-    base, header = local_safetensors_header(shard)
+    base, header = read_safetensors_header(shard)
     header[name(3, 0, "down_proj", "weight_scale")]["shape"] = [D, 2]
     raw = json.dumps(header).encode()
     raw += b" " * (base - 8 - len(raw))
     with open(shard, "r+b") as f:
         f.seek(8)
         f.write(raw)
-    with pytest.raises(ContractError, match="byte range"):
-        ModelContract.from_model_dir(root).tensor(name(3, 0, "down_proj", "weight_scale"))
+    with pytest.raises(ContractError, match="data_offsets"):
+        ShardIndex.open(root).locate(name(3, 0, "down_proj", "weight_scale"))
+    # a shard cut short: its last tensor runs past the end of the file
+    root = fresh("short")
+    shard = os.path.join(root, "model-layer3-00.safetensors")
+    os.truncate(shard, os.path.getsize(shard) - 1)
+    last = max(read_safetensors_header(shard)[1].items(),
+               key=lambda kv: kv[1]["data_offsets"][1])[0]
+    with pytest.raises(ContractError, match="run past"):
+        ShardIndex.open(root).locate(last)
     # metadata files
-    with pytest.raises(ContractError, match="incomplete"):
-        ModelContract.from_model_dir(tmp_path / "nothing")
-    with pytest.raises(ContractError, match="weight_map"):
-        ModelContract(tmp_path, {}, {"weight_map": {}})
+    with pytest.raises(ContractError, match="index.json"):
+        ShardIndex.open(tmp_path / "nothing")
+    with pytest.raises(ContractError, match="maps no tensors"):
+        ShardIndex(tmp_path, {})
 
 
-def test_partition_and_name_parts():
-    assert routed_expert_parts(name(7, 11, "up_proj", "weight_scale")) == (
-        7, 11, "up_proj", "weight_scale")
-    with pytest.raises(ContractError):
-        routed_expert_parts("model.language_model.layers.7.mlp.gate.weight")
-    P = ModelContract.partition
-    assert P(name(3, 0, "down_proj", "weight_packed")) == "routed"
-    assert P(name(45, 0, "down_proj", "weight_packed")) == "mtp"
-    assert P(name(2, 0, "down_proj", "weight_packed")) == "unknown"
-    assert P("model.language_model.layers.45.self_attn.q.weight") == "mtp"
-    assert P("model.language_model.embed_tokens.weight") == "resident"
-    assert P("lm_head.weight") == "resident"
-    assert P("model.visual.blocks.0.w") == "vision"
+def test_slot_shapes_and_the_real_record_size():
+    # gate/up: I rows of d inputs, down the transpose; codes two per byte, scales one per 32
+    assert slot_shape("gate_proj.weight_packed", 4096, 2048) == (2048, 2048)
+    assert slot_shape("down_proj.weight_scale", 4096, 2048) == (4096, 64)
+    real = sum(r * c for r, c in (slot_shape(f"{comp}.{part}", 4096, 2048)
+                                  for comp in COMPONENTS for part in PARTS))
+    assert real == REAL_RECORD_BYTES == 3 * 2048 * 4096 * 17 // 32
+    with pytest.raises(ContractError, match="multiple of 32"):
+        slot_shape("up_proj.weight_scale", 100, 64)
 
 
 # ---------------------------------------------------------------- native reader
@@ -234,16 +229,15 @@ def test_loader_chunks_cover_each_record_once(tmp_path):
     from glm53flash.bank_loader import ExpertBankLoader
 
     make_checkpoint(str(tmp_path), layers=(3,), E=E, d=D, I=I, shards_per_layer=2)
-    plan = build_native_expert_source_plan(ModelContract.from_model_dir(tmp_path), _config(),
-                                           first_layer=3, last_layer=3)
+    plan = _plan(tmp_path)
     loader = ExpertBankLoader(plan, chunk_bytes=3 * RECORD)
     chunks = loader._chunks(3)
-    units = [(src.expert, r.absolute_offset, r.shard_name) for c in chunks for src, r in c]
+    units = [(x.expert, r.offset, r.shard) for c in chunks for x, r in c]
     assert sorted(e for e, _, _ in units) == list(range(E))
     for c in chunks:
-        assert len({r.shard_name for _, r in c}) == 1
-        assert sum(-(-r.byte_length // 256) * 256 for _, r in c) <= loader.chunk_bytes
-        offs = [r.absolute_offset for _, r in c]
+        assert len({r.shard for _, r in c}) == 1
+        assert sum(-(-r.nbytes // 256) * 256 for _, r in c) <= loader.chunk_bytes
+        offs = [r.offset for _, r in c]
         assert offs == sorted(offs)
     # a chunk never holds less than the largest record
     assert ExpertBankLoader(plan, chunk_bytes=256).chunk_bytes >= RECORD

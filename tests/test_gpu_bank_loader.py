@@ -23,12 +23,10 @@ def gu():
 
 
 def _plan(root, E, d, I, layers):
-    from glm53flash.contract import ModelContract
-    from glm53flash.expert_source import build_native_expert_source_plan
-    from glm53flash.model_config import GLMTextConfig
-    cfg = GLMTextConfig(hidden_size=d, moe_intermediate_size=I, n_routed_experts=E)
-    return build_native_expert_source_plan(ModelContract.from_model_dir(root), cfg,
-                                           first_layer=layers[0], last_layer=layers[-1])
+    from glm53flash.bank_plan import plan_expert_banks
+    from glm53flash.checkpoint import ShardIndex
+    return plan_expert_banks(ShardIndex.open(root), hidden_size=d, intermediate_size=I,
+                             experts=E, layers=layers)
 
 
 @pytest.mark.parametrize("misalign", [False, True])
@@ -73,8 +71,7 @@ def test_loaded_bank_matches_a_bank_from_arrays(gu, tmp_path):
     print(f"bank loader forward: E={E} d={d} I={I} T={T} k={k}", flush=True)
     arrays = make_checkpoint(str(tmp_path), layers=(layer,), E=E, d=d, I=I, seed=5310)
     plan = _plan(str(tmp_path), E, d, I, (layer,))
-    loaded = load_layer_bank(plan, layer, swiglu_limit=10.0, hidden_size=d,
-                             intermediate_size=I, device="cuda")
+    loaded = load_layer_bank(plan, layer, swiglu_limit=10.0, device="cuda")
     stacked = {f"{c}.{p}": np.stack([arrays[(layer, e)][(c, p)] for e in range(E)])
                for c in COMPONENTS for p in PARTS}
     direct = HBMExpertBank(layer=layer, num_experts=E, hidden_size=d, intermediate_size=I,
@@ -139,10 +136,10 @@ def test_scalex_layer_loads_the_same_bank(gu, tmp_path, scales):
     arrays = make_checkpoint(str(tmp_path), layers=layers, E=E, d=d, I=I, extras=False,
                              shuffle=False, scales=scales, scalex=True, seed=5320)
     plan = _plan(str(tmp_path), E, d, I, layers)
-    assert plan.scalex_mode_b
-    codecs = {p.scalex_record.codec for p in plan.packs}
+    assert plan.scalex
+    codecs = {x.coded.codec for x in plan.loads}
     assert codecs == ({"one_bit"} if scales == "two_value" else {"raw"})
-    record = plan.packs[0].scalex_record.physical_bytes
+    record = plan.loads[0].coded.nbytes
     loader = ExpertBankLoader(plan, threads=4, chunk_bytes=3 * record + 4096)
     banks = [HBMExpertBank(layer=layer, num_experts=E, hidden_size=d, intermediate_size=I,
                            swiglu_limit=10.0, device="cuda") for layer in layers]
@@ -160,7 +157,7 @@ def test_scalex_layer_loads_the_same_bank(gu, tmp_path, scales):
 
 def test_loader_at_the_real_record_size(gu, tmp_path):
     """d = 4096, I = 2048: one expert is the real checkpoint's 13,369,344-byte
-    record (expert_source.py:370); two records per staging chunk."""
+    record (expert_source.py:370), read as one range; two records per staging chunk."""
     from glm53flash.bank_loader import ExpertBankLoader
     from glm53flash.expert_ssd import HBMExpertBank
     E, d, I, layer = 4, 4096, 2048, 3
@@ -168,7 +165,8 @@ def test_loader_at_the_real_record_size(gu, tmp_path):
     arrays = make_checkpoint(str(tmp_path), layers=(layer,), E=E, d=d, I=I, extras=False,
                              seed=5330)
     plan = _plan(str(tmp_path), E, d, I, (layer,))
-    assert plan.uniform_pack_bytes == 13_369_344 and plan.uniform_read_count == 1
+    assert all(len(x.reads) == 1 and x.read_bytes == x.bank_bytes == 13_369_344
+               for x in plan.loads)
     loader = ExpertBankLoader(plan, chunk_bytes=30 << 20)
     bank = HBMExpertBank(layer=layer, num_experts=E, hidden_size=d, intermediate_size=I,
                          swiglu_limit=10.0, device="cuda")

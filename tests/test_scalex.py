@@ -3,7 +3,7 @@
 The reference's own codec cases (``tests/test_scale_codec.py:13-34``), the
 header layout byte by byte, round trips at the real checkpoint's scale mix,
 the container written, read, verified against the original file's SHA-256,
-and planned through the checkpoint contract (``tests/test_scalex_container.py``).
+and planned through the bank load plan.
 """
 
 from __future__ import annotations
@@ -17,15 +17,13 @@ import pytest
 
 from checkpoint_util import COMPONENTS, make_checkpoint, name
 
-from glm53flash.contract import ContractError, ModelContract
-from glm53flash.expert_source import build_native_expert_source_plan
-from glm53flash.model_config import GLMTextConfig
+from glm53flash.bank_plan import plan_expert_banks
+from glm53flash.checkpoint import ShardIndex
+from glm53flash.contract import ContractError
 from glm53flash.scale_codec import (ScaleCodecError, decode_mode_a, encode_mode_a,
                                     encode_mode_b_row, inspect_mode_a, mode_b_indexed_nbytes,
                                     mode_b_tile_prefix, validate_mode_a)
-from glm53flash.scalex_container import (ScaleXContainerError, is_scalex_layer,
-                                         read_scalex_layout, read_scalex_tensor,
-                                         verify_scalex_layer)
+from glm53flash.scalex_layer import ScaleXError, ScaleXLayer, is_scalex_file
 
 
 @pytest.mark.parametrize(("values", "codec"), [
@@ -88,7 +86,7 @@ def test_round_trip_at_checkpoint_scale_mix():
     pos_at = 24 + 26  # 203 scales -> 26 primary bytes
     assert struct.unpack("<II", bad[pos_at:pos_at + 8]) == (200, 202)
     bad[pos_at:pos_at + 8] = struct.pack("<II", 202, 200)  # descending positions
-    with pytest.raises(ScaleCodecError, match="position"):
+    with pytest.raises(ScaleCodecError, match="positions must ascend"):
         validate_mode_a(bytes(bad))
 
 
@@ -102,45 +100,100 @@ def test_container_round_trip_and_plan(tmp_path):
                     shuffle=False, scalex=True)
     shard = coded / "model-layer3-00.safetensors"
     original = native / "model-layer3-00.safetensors"
-    assert is_scalex_layer(shard) and not is_scalex_layer(original)
-    assert verify_scalex_layer(shard) == hashlib.sha256(original.read_bytes()).hexdigest()
+    assert is_scalex_file(shard) and not is_scalex_file(original)
+    layout = ScaleXLayer.read(shard)
+    assert layout.verify() == hashlib.sha256(original.read_bytes()).hexdigest()
     assert shard.stat().st_size < original.stat().st_size
-    layout = read_scalex_layout(shard)
     assert layout.layer == 3 and layout.experts == E
     assert layout.records[0].codec == "one_bit"
     for e in range(E):
         for c in COMPONENTS:
             for p in ("weight_packed", "weight_scale"):
-                assert read_scalex_tensor(layout, name(3, e, c, p)) == arrays[(3, e)][(c, p)].tobytes()
-    cfg = GLMTextConfig(hidden_size=d, moe_intermediate_size=I, n_routed_experts=E)
-    contract = ModelContract.from_model_dir(coded)
-    plan = build_native_expert_source_plan(contract, cfg, first_layer=3, last_layer=4)
-    assert plan.scalex_mode_b and plan.source_format == "livglm_scalex_mode_b"
-    assert plan.read_bytes < plan.payload_bytes and plan.uniform_read_count == 1
-    src = plan.expert(3, 2)
-    rec = src.scalex_record
-    (rng_,) = src.read_ranges
-    assert rng_.absolute_offset == rec.absolute_offset and rng_.byte_length == rec.physical_bytes
-    assert [t.source_name for t in rng_.tensors] == list(rec.weight_names)
-    # the virtual tensor ranges still describe the original file
-    native_plan = build_native_expert_source_plan(ModelContract.from_model_dir(native), cfg,
-                                                  first_layer=3, last_layer=4)
-    assert [t.absolute_offset for t in src.tensors] == [
-        t.absolute_offset for t in native_plan.expert(3, 2).tensors]
+                assert layout.tensor_bytes(name(3, e, c, p)) == arrays[(3, e)][(c, p)].tobytes()
+    plan = plan_expert_banks(ShardIndex.open(coded), hidden_size=d, intermediate_size=I,
+                             experts=E, layers=layers)
+    assert plan.scalex and plan.read_bytes < plan.bank_bytes
+    x = plan.expert(3, 2)
+    rec = x.coded
+    (rd,) = x.reads
+    assert rd.offset == rec.offset and rd.nbytes == rec.nbytes
+    # weights follow the coded scales in gate, down, up order
+    assert [(s.key, s.at) for s in rd.segments] == [
+        ("gate_proj.weight_packed", rec.coded_bytes),
+        ("down_proj.weight_packed", rec.coded_bytes + rec.weight_bytes[0]),
+        ("up_proj.weight_packed", rec.coded_bytes + rec.weight_bytes[0] + rec.weight_bytes[1])]
+    with open(shard, "rb") as f:
+        f.seek(rd.offset + rd.segments[1].at)
+        assert f.read(rd.segments[1].nbytes) == arrays[(3, 2)][("down_proj",
+                                                               "weight_packed")].tobytes()
+    # the tensor ranges the index gives for a container describe the original file
+    coded_idx, native_idx = ShardIndex.open(coded), ShardIndex.open(native)
+    for c in COMPONENTS:
+        n = name(3, 2, c, "weight_scale")
+        assert coded_idx.locate(n) == native_idx.locate(n)
     # a damaged container is refused
     raw = bytearray(shard.read_bytes())
     raw[-1] ^= 1
     broken = tmp_path / "broken.safetensors"
     broken.write_bytes(bytes(raw))
-    with pytest.raises(ScaleXContainerError):
-        verify_scalex_layer(broken)
+    with pytest.raises(ScaleXError, match="original_sha256"):
+        ScaleXLayer.read(broken).verify()
     raw = bytearray(shard.read_bytes())
     raw[40] ^= 0xFF  # inside the JSON metadata
     broken.write_bytes(bytes(raw))
-    with pytest.raises(ScaleXContainerError):
-        read_scalex_layout(broken)
+    with pytest.raises(ScaleXError):
+        ScaleXLayer.read(broken)
     # mixing ScaleX and native layers is refused
     os.replace(native / "model-layer4-00.safetensors", coded / "model-layer4-00.safetensors")
     with pytest.raises(ContractError, match="mix"):
-        build_native_expert_source_plan(ModelContract.from_model_dir(coded), cfg,
-                                        first_layer=3, last_layer=4)
+        plan_expert_banks(ShardIndex.open(coded), hidden_size=d, intermediate_size=I,
+                          experts=E, layers=layers)
+
+
+def test_container_reader_checks(tmp_path):
+    """Metadata that disagrees with the stored data is refused with a reason."""
+    import json
+    import struct as st
+    from glm53flash.scalex_layer import PREFIX, write_scalex_layer
+    E, d, I = 3, 64, 64
+    root = tmp_path / "ck"
+    make_checkpoint(str(root), layers=(3,), E=E, d=d, I=I, extras=False, shuffle=False)
+    src = root / "model-layer3-00.safetensors"
+    good = tmp_path / "good.sx"
+    write_scalex_layer(src, good, layer=3, experts=E)
+    with pytest.raises(ScaleXError, match="already a ScaleX"):
+        write_scalex_layer(good, tmp_path / "again.sx", layer=3, experts=E)
+    with pytest.raises(ScaleXError, match="not exactly layer 4"):
+        write_scalex_layer(src, tmp_path / "wrong.sx", layer=4, experts=E)
+    blob = good.read_bytes()
+    magic, version, mlen, stored = PREFIX.unpack_from(blob)
+    meta = json.loads(blob[PREFIX.size:PREFIX.size + mlen])
+
+    def rewrite(change, label):
+        m = json.loads(json.dumps(meta))
+        change(m)
+        raw = json.dumps(m, sort_keys=True, separators=(",", ":")).encode()
+        out = tmp_path / f"{label}.sx"
+        out.write_bytes(PREFIX.pack(magic, version, len(raw), stored) + raw
+                        + blob[PREFIX.size + mlen:])
+        return out
+
+    cases = [
+        (lambda m: m.update(format="other"), "unusable 'format'"),
+        (lambda m: m["records"][1].update(stored_offset=m["records"][1]["stored_offset"] + 1),
+         "expected expert 1"),
+        (lambda m: m["records"][0].update(codec="three_bit"), "unusable 'codec'"),
+        (lambda m: m["records"][2]["scale_nbytes"].__setitem__(0, 7), "decoded_bytes"),
+        (lambda m: m.update(experts=4), "records for 4 experts"),
+        (lambda m: m["records"][0]["weight_names"].reverse(), "gate, down, up"),
+        (lambda m: m.pop("original_sha256"), "lacks 'original_sha256'"),
+    ]
+    for i, (change, text) in enumerate(cases):
+        with pytest.raises(ScaleXError, match=text):
+            ScaleXLayer.read(rewrite(change, f"c{i}"))
+    # a stored length that disagrees with the file
+    bad = tmp_path / "len.sx"
+    bad.write_bytes(PREFIX.pack(magic, version, mlen, stored + 1) + blob[PREFIX.size:])
+    with pytest.raises(ScaleXError, match="prefix promises"):
+        ScaleXLayer.read(bad)
+    assert st.calcsize("<8sIIQ") == PREFIX.size == 24
