@@ -172,10 +172,11 @@ class Setup:
             self.streams = torch.randn((self.n_inputs, T, hc, d), device=dev, generator=gen)
         # the layer's routed gate/up kernel: token-major for a few tokens, tiled
         # GEMV up to 64 tokens, grouped MFMA GEMMs beyond
-        # the token-major and decode kernels cover d / 512 and I / 128 in
-        # {1, 2, 4, 6, 8} chunks; other shapes run on the general GEMV kernels
+        # the token-major and decode kernels cover d / 512 in {2, 4, 6, 8} and
+        # I / 128 in {1, 2, 4, 6, 8, 16} chunks; other shapes run on the general
+        # GEMV kernels
         self.decode_kernels = (d % 512 == 0 and d // 512 in (2, 4, 6, 8) and I % 128 == 0
-                               and I // 128 in (1, 2, 4, 6, 8))
+                               and I // 128 in (1, 2, 4, 6, 8, 16))
         self.few_token = T <= 4 and k <= 8 and self.decode_kernels
         self.grouped = T > 64
 

@@ -113,7 +113,7 @@ int glm_expert_gate_up(void *stream, const uint16_t *x, int T, int d, int I, int
  * indices u32 [T][k] are written as glm_router_topk writes them; h bf16
  * [T*k][I] in pair order.
  * Limits: T <= 4, k <= 8, E <= 448, d / 512 in {2, 4, 6, 8},
- * I / 128 in {1, 2, 4, 6, 8}, plus the router's limits.
+ * I / 128 in {1, 2, 4, 6, 8, 16}, plus the router's limits.
  */
 int glm_route_gate_up(void *stream, const float *logits, const float *bias, int T, int E,
                       int top_k, int n_group, int topk_group, int norm_topk_prob,

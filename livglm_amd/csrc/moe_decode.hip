@@ -483,6 +483,12 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DownArgs a) {
   load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
   for (int p0 = 0; p0 < n; p0 += kDownStageRows) {
     const int rows = min(kDownStageRows, n - p0);
+    if constexpr (CPW_R > 8) {
+      // Opaque per batch: converted weights of 16 chunks would pin 256
+      // registers (one wave per SIMD) if hoisted out of the batch loop.
+#pragma unroll
+      for (int c = 0; c < CPW_R; ++c) asm volatile("" : "+v"(ww.w[0][c].c));
+    }
     if (p0 > 0) __syncthreads();
     stage_rows(s_x, a.h + (size_t)(base + p0) * a.I, nullptr, rows, a.I);
     __syncthreads();
@@ -504,8 +510,8 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DownArgs a) {
 constexpr int kPairMaxT = 4;
 constexpr int kPairMaxK = 8;
 // 16-byte pieces of h per thread in down_combine_kernel: k*I/8 pieces over
-// 64*max(k, 4) threads is at most I/512 <= 2 (I <= 1024)
-constexpr int kMaxHPieces = 2;
+// 64*max(k, 4) threads is at most I/512 = CPW_R/4 (I = 128 CPW_R)
+__host__ __device__ constexpr int h_pieces(int cpw_r) { return cpw_r < 4 ? 1 : (cpw_r + 3) / 4; }
 
 struct PairArgs {
   const float *logits, *bias;
@@ -631,9 +637,10 @@ __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
   }
   const int per_row = I / 8, nh = k * per_row;  // 16-byte pieces of the k rows of h
   const uint16_t *hsrc = a.h + (size_t)t * k * I;
-  glm_u32x4 hv[kMaxHPieces];
+  constexpr int kHP = h_pieces(CPW_R);
+  glm_u32x4 hv[kHP];
 #pragma unroll
-  for (int u = 0; u < kMaxHPieces; ++u) {
+  for (int u = 0; u < kHP; ++u) {
     const int i = min((int)threadIdx.x + (int)blockDim.x * u, nh - 1);
     hv[u] = *reinterpret_cast<const glm_u32x4 *>(hsrc + (size_t)i * 8);
   }
@@ -644,7 +651,7 @@ __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
     load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
   }
 #pragma unroll
-  for (int u = 0; u < kMaxHPieces; ++u) {
+  for (int u = 0; u < kHP; ++u) {
     const int i = (int)threadIdx.x + (int)blockDim.x * u;
     if (i < nh)
       *reinterpret_cast<glm_u32x4 *>(s_h + (i / per_row) * lds_row_stride(I) + (i % per_row) * 8) = hv[u];
@@ -732,23 +739,28 @@ size_t glm_select_dispatch_lds_bytes(int EPL) {
          (size_t)4 * (64 * EPL + 256) * 4;
 }
 
-// Whether the decode kernels cover this layer shape.
+// Whether the decode kernels cover this layer shape: gate/up waves take d/512
+// chunks of 128 (d / 4 per wave), down waves the whole K = I in I/128 chunks
+// (16 at the real expert geometry, I 2048); the shared expert's down tiles
+// take 1 or 2 chunks per K range.
 static bool chunk_count_ok(int c) { return c == 1 || c == 2 || c == 4 || c == 6 || c == 8; }
+static bool down_chunks_ok(int c) { return chunk_count_ok(c) || c == 16; }
+static bool shared_chunks_ok(int c) { return c == 1 || (c % 2 == 0 && c <= 16); }
 
 bool glm_decode_gate_up_supported(int d, int I) {
   return d % 512 == 0 && d / 512 >= 2 && chunk_count_ok(d / 512) && I % 16 == 0;
 }
 
 bool glm_decode_down_supported(int I, int d) {
-  return I % 128 == 0 && chunk_count_ok(I / 128) && d % 64 == 0;
+  return I % 128 == 0 && down_chunks_ok(I / 128) && d % 64 == 0;
 }
 
 bool glm_decode_path_supported(int T, int d, int E, int k, int I, int Is) {
   if (T < 1 || T > 64 || (long long)T * k > kMaxFusedPairs || E > kFusedMaxE) return false;
   // gate/up: 4 waves x CPW chunks of 128 over d; down: 64-row tiles of d
   if (d % 512 != 0 || !chunk_count_ok(d / 512) || d / 512 < 2) return false;
-  if (I % 128 != 0 || !chunk_count_ok(I / 128)) return false;
-  if (Is > 0 && (Is % 128 != 0 || !chunk_count_ok(Is / 128))) return false;
+  if (I % 128 != 0 || !down_chunks_ok(I / 128)) return false;
+  if (Is > 0 && (Is % 128 != 0 || !shared_chunks_ok(Is / 128))) return false;
   return true;
 }
 
@@ -910,6 +922,7 @@ int glm_decode_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, 
     case 4: hipLaunchKernelGGL(decode_down_kernel<4>, dim3(blocks), dim3(256), lds, stream, a); break;
     case 6: hipLaunchKernelGGL(decode_down_kernel<6>, dim3(blocks), dim3(256), lds, stream, a); break;
     case 8: hipLaunchKernelGGL(decode_down_kernel<8>, dim3(blocks), dim3(256), lds, stream, a); break;
+    case 16: hipLaunchKernelGGL(decode_down_kernel<16>, dim3(blocks), dim3(256), lds, stream, a); break;
     default: glm::set_error("decode down: unsupported I=%d", I); return GLM_ERR_UNSUPPORTED_SHAPE;
   }
   GLM_LAUNCH_CHECK("decode_down_kernel");
@@ -1049,7 +1062,8 @@ int glm_pair_path_launch(hipStream_t stream, const uint16_t *x, int T, int d, co
     case 2: hipLaunchKernelGGL((down_combine_kernel<2>), g3, b3, lds3, stream, b); break;
     case 4: hipLaunchKernelGGL((down_combine_kernel<4>), g3, b3, lds3, stream, b); break;
     case 6: hipLaunchKernelGGL((down_combine_kernel<6>), g3, b3, lds3, stream, b); break;
-    default: hipLaunchKernelGGL((down_combine_kernel<8>), g3, b3, lds3, stream, b); break;
+    case 8: hipLaunchKernelGGL((down_combine_kernel<8>), g3, b3, lds3, stream, b); break;
+    default: hipLaunchKernelGGL((down_combine_kernel<16>), g3, b3, lds3, stream, b); break;
   }
   GLM_LAUNCH_CHECK("down_combine_kernel");
   return GLM_OK;
@@ -1078,7 +1092,7 @@ extern "C" int glm_route_gate_up(void *stream, const float *logits, const float 
   GLM_REQUIRE(T <= kPairMaxT && top_k <= kPairMaxK && glm_pair_path_supported(T > 0 ? T : 1, d, E, top_k, I, 0),
               GLM_ERR_UNSUPPORTED_SHAPE,
               "route_gate_up: unsupported shape T=%d d=%d E=%d k=%d I=%d (T <= 4, k <= 8, "
-              "E <= 448, d/512 in {2,4,6,8}, I/128 in {1,2,4,6,8})",
+              "E <= 448, d/512 in {2,4,6,8}, I/128 in {1,2,4,6,8,16})",
               T, d, E, top_k, I);
   if (T == 0) return GLM_OK;
   PairArgs a{};

@@ -641,9 +641,8 @@ SMALL_LAYERS = [
     (40, 1024, 64, 8, 512, 512, (1, 1)),
     # k = 64, every expert of E = 64 chosen by every token (the top-k upper bound)
     (3, 256, 64, 64, 64, 64, (1, 1)),
-    # the real GLM expert geometry (d = 4096, I = 2048: 16 chunks of 128 in the
-    # down projection, beyond the decode kernels' templates): the general path
-    (2, 4096, 24, 8, 2048, 2048, (1, 1)),
+    # the real expert geometry with few experts (d = 4096, I = 2048, I_shared 1024)
+    (3, 4096, 24, 8, 2048, 1024, (1, 1)),
     # shapes the decode kernels do not cover (d / 512 = 3) but the grouped GEMMs
     # do: up to 64 tokens they run the tiled GEMV kernels over the work list with
     # many pairs per expert (several 16-token batches, the act_index loop), from
@@ -651,7 +650,10 @@ SMALL_LAYERS = [
     (40, 1536, 8, 8, 256, 256, (1, 1)),
     (64, 1536, 16, 8, 256, 256, (1, 1)),
     (65, 1536, 16, 8, 256, 256, (1, 1)),
-    # the real geometry at 64 tokens: ~21 pairs per expert on the GEMV kernels
+    # the real GLM expert geometry (d 4096, I 2048: 16 chunks of 128 in the down
+    # projection): E 288 on the few-token path; 64 tokens over 24 experts on the
+    # decode path (~21 pairs per expert, two 16-row h batches)
+    (2, 4096, 288, 8, 2048, 2048, (1, 1)),
     (64, 4096, 24, 8, 2048, 2048, (1, 1)),
 ]
 
