@@ -80,7 +80,11 @@ int glm_router_topk(void *stream, const uint16_t *x, int T, int d, const float *
  * (ids of experts with count > 0, ascending, then -1); num_active [1];
  * work [E][4] (per active slot u: {expert, offsets[expert], count, 0}; slots
  * u >= num_active hold {-1, 0, 0, 0}); status [1] (0, or 1 if an index >= E
- * was seen -- such pairs are dropped, inv = -1).
+ * was seen -- such pairs are dropped, inv = -1, and the sorted positions past
+ * offsets[E] hold -1 in perm and pair_token).  Up to 4096 pairs one
+ * workgroup sorts them; beyond, a chunk-parallel count / scan / scatter over
+ * 1024-pair chunks (pair_token serves as its scratch until it is filled last;
+ * the result is the same).
  * Limits: E <= 448 (one workgroup's LDS holds the per-expert bitmaps).
  */
 int glm_moe_dispatch(void *stream, const uint32_t *indices, int T, int top_k, int E,

@@ -5,6 +5,8 @@
 // the grouping stays on the device: pairs p = t*k + j are counting-sorted by
 // expert id, ties kept in ascending p, so each expert's rows are contiguous
 // for the expert kernels.
+#include <algorithm>
+
 #include "glm_common.h"
 
 namespace glm {
@@ -148,6 +150,11 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     }
     __syncthreads();
   }
+  // positions past the valid pairs (dropped indices >= E) hold -1
+  for (int pos = carry + tid; pos < P; pos += kDispatchThreads) {
+    perm[pos] = -1;
+    pair_token[pos] = -1;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -277,9 +284,26 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_scatter_kernel(
       r += __popc(row[word] & ((1u << (tid & 31)) - 1u));
       perm[r] = p;
       inv[p] = r;
-      pair_token[r] = p / k;
+      if (pair_token != nullptr) pair_token[r] = p / k;
     } else {
       inv[p] = -1;
+    }
+  }
+}
+
+// pair_token from perm once the scatter is done (the public dispatch keeps
+// the chunk counts in pair_token until then); positions past the valid pairs
+// hold -1 in both.
+__global__ void dispatch_tokens_kernel(const int32_t *__restrict__ offsets, int E, int P, int k,
+                                       int32_t *__restrict__ perm,
+                                       int32_t *__restrict__ pair_token) {
+  const int total = offsets[E];
+  for (int pos = blockIdx.x * blockDim.x + threadIdx.x; pos < P; pos += gridDim.x * blockDim.x) {
+    if (pos < total) {
+      pair_token[pos] = perm[pos] / k;
+    } else {
+      perm[pos] = -1;
+      pair_token[pos] = -1;
     }
   }
 }
@@ -337,14 +361,24 @@ size_t glm_dispatch_chunk_ints(long long P, int E) {
 
 // tiles/num_tiles (optional): row tiles of tile_rows rows for the grouped
 // GEMMs; tiles needs room for ceil(T*k / tile_rows) + E entries.
+// chunk_scratch: glm_dispatch_chunk_ints(P, E) ints for the multi-workgroup
+// dispatch; without it (the public entry point) the chunk counts live in
+// pair_token -- ceil(P / 1024) * (E + 1) <= P ints for E <= 448 and P > 4096
+// -- and pair_token is filled from perm at the end.
 int glm_dispatch_launch(hipStream_t stream, const uint32_t *indices, int T, int k, int E,
                         int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
                         int32_t *pair_token, int32_t *active, int32_t *num_active, int4 *work,
                         int32_t *status, int tile_rows, int4 *tiles, int32_t *num_tiles,
                         int32_t *chunk_scratch) {
   const int P = T * k;
-  if (chunk_scratch != nullptr && P > kMultiDispatchPairs) {
+  if (P > kMultiDispatchPairs) {
     const int nchunks = (P + glm::kDispatchThreads - 1) / glm::kDispatchThreads;
+    const bool in_place = chunk_scratch == nullptr;
+    if (in_place) {
+      GLM_REQUIRE((size_t)nchunks * (E + 1) <= (size_t)P, GLM_ERR_UNSUPPORTED_SHAPE,
+                  "dispatch: %d chunks x %d experts do not fit in pair_token", nchunks, E + 1);
+      chunk_scratch = pair_token;
+    }
     hipLaunchKernelGGL(glm::dispatch_count_kernel, dim3(nchunks), dim3(glm::kDispatchThreads),
                        (size_t)E * 4, stream, indices, P, E, chunk_scratch);
     GLM_LAUNCH_CHECK("dispatch_count_kernel");
@@ -354,8 +388,14 @@ int glm_dispatch_launch(hipStream_t stream, const uint32_t *indices, int T, int 
     GLM_LAUNCH_CHECK("dispatch_scan_kernel");
     hipLaunchKernelGGL(glm::dispatch_scatter_kernel, dim3(nchunks), dim3(glm::kDispatchThreads),
                        (size_t)E * 32 * 4, stream, indices, P, k, E, chunk_scratch, perm, inv,
-                       pair_token);
+                       in_place ? nullptr : pair_token);
     GLM_LAUNCH_CHECK("dispatch_scatter_kernel");
+    if (in_place) {
+      const int blocks = std::min((P + 255) / 256, 1024);
+      hipLaunchKernelGGL(glm::dispatch_tokens_kernel, dim3(blocks), dim3(256), 0, stream, offsets,
+                         E, P, k, perm, pair_token);
+      GLM_LAUNCH_CHECK("dispatch_tokens_kernel");
+    }
     return GLM_OK;
   }
   hipLaunchKernelGGL(glm::dispatch_kernel, dim3(1), dim3(glm::kDispatchThreads),

@@ -235,12 +235,30 @@ def test_dispatch_bit_exact(gu, T, k, E, kind):
     assert got["status"][0] == 0
 
 
-def test_dispatch_flags_out_of_range(gu):
-    idx = np.array([[0, 5], [3, 1]])
-    got = _dispatch(gu, idx, 4)
+@pytest.mark.parametrize("T,k,E", [(2, 2, 4), (900, 8, 32)])
+def test_dispatch_flags_out_of_range(gu, T, k, E):
+    # pairs with an index >= E are dropped on both the one-workgroup path and
+    # the chunk-parallel one (900 x 8 pairs): status 1, inv -1, the valid pairs
+    # sorted as if the others were absent, -1 past them in perm and pair_token
+    rng = np.random.default_rng(E + T)
+    idx = rng.integers(0, E, (T, k)).astype(np.int64)
+    bad = rng.random((T, k)) < 0.05
+    bad.flat[1] = True
+    idx[bad] = E + rng.integers(0, 3, int(bad.sum()))
+    got = _dispatch(gu, idx, E)
     assert got["status"][0] == 1
-    assert got["inv"][1] == -1
-    assert got["offsets"][-1] == 3
+    flat = idx.reshape(-1)
+    valid = np.flatnonzero(flat < E)
+    order = valid[np.argsort(flat[valid], kind="stable")]
+    n = len(order)
+    assert got["offsets"][-1] == n
+    np.testing.assert_array_equal(got["counts"], np.bincount(flat[valid], minlength=E))
+    np.testing.assert_array_equal(got["perm"][:n], order)
+    np.testing.assert_array_equal(got["pair_token"][:n], order // k)
+    assert np.all(got["perm"][n:] == -1) and np.all(got["pair_token"][n:] == -1)
+    inv = np.full(T * k, -1)
+    inv[order] = np.arange(n)
+    np.testing.assert_array_equal(got["inv"], inv)
 
 
 # --------------------------------------------------------------------------- experts
