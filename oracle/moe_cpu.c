@@ -98,6 +98,7 @@ static void route_token(const float *xf, int d, const float *rw, const float *rb
     float l = (float)acc;
     score[e] = sigmoid_f32(l);
     choice[e] = score[e] + rb[e];
+    if (choice[e] != choice[e]) choice[e] = -INFINITY; /* NaN ranks as -inf */
   }
   if (n_group > 1) {
     int per = E / n_group;

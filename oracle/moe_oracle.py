@@ -305,6 +305,11 @@ def router(x, weight, bias, *, top_k: int, n_group: int, topk_group: int,
     logits = _dot_f32(rows, W.T)
     scores = sigmoid_f32(logits)
     choice = (scores + np.asarray(bias, dtype=np.float32)).astype(np.float32)
+    # A NaN choice ranks as -inf (never chosen ahead of a finite one), in the
+    # group scores and in the top-k.  numpy's sort would put NaN last (chosen
+    # first); MLX's order for NaN is not pinned by anything in the reference,
+    # so this is the library's documented choice, shared with the kernels.
+    choice = np.where(np.isnan(choice), np.float32(-np.inf), choice).astype(np.float32)
     T = rows.shape[0]
     per_group = E // n_group
     grouped = choice.reshape(T, n_group, per_group)

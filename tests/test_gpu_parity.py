@@ -187,6 +187,38 @@ def test_router_reference_known_answer(gu):
     np.testing.assert_allclose(gu.host(w), [[1.25, 1.25]], atol=1e-6)
 
 
+@pytest.mark.parametrize("T,groups", [(2, (1, 1)), (40, (4, 2))])
+def test_router_nan_choice_ranks_as_minus_inf(gu, T, groups):
+    # a NaN router row (NaN logit, NaN choice) with a large bias: never chosen,
+    # by the router kernel and by the few-token / decode layer kernels, as in
+    # the oracle
+    torch = _torch()
+    shape = MoEShape("nan", T, 1024, 16, 4, 256, 0, n_group=groups[0], topk_group=groups[1])
+    layer = make_layer(shape, 4242)
+    layer["router_weight"][7, 5] = np.nan
+    layer["router_bias"][:] = 0.0
+    layer["router_bias"][7] = 5.0
+    x = O.bf16_bits_to_f32(layer["x"])
+    _, w, idx, choice = O.router(x, layer["router_weight"], layer["router_bias"], top_k=4,
+                                 n_group=groups[0], topk_group=groups[1], norm_topk_prob=True,
+                                 routed_scaling_factor=shape.routed_scaling_factor)
+    assert not (idx == 7).any()
+    dl = gu.upload_layer(layer)
+    g_logits = torch.empty((T, 16), dtype=torch.float32, device="cuda")
+    g_w = torch.empty((T, 4), dtype=torch.float32, device="cuda")
+    g_idx = torch.empty((T, 4), dtype=torch.int32, device="cuda")
+    gu.call("glm_router_topk", gu.stream(), gu.p(dl["x"]), T, 1024, gu.p(dl["router_weight"]),
+            gu.p(dl["router_bias"]), 16, 4, groups[0], groups[1], 1,
+            shape.routed_scaling_factor, gu.p(g_logits), gu.p(g_w), gu.p(g_idx))
+    got = gu.host(g_idx).astype(np.uint32)
+    assert not (got == 7).any()
+    _check_indices(got, idx, choice, 4)
+    _, _, l_idx = gu.run_layer(dl, shape, shared=False)
+    got_l = gu.host(l_idx).astype(np.uint32)
+    assert not (got_l == 7).any()
+    _check_indices(got_l, idx, choice, 4)
+
+
 def _work_list(counts, offsets, active, E):
     work = np.tile(np.array([-1, 0, 0, 0], np.int32), (E, 1))
     for u, e in enumerate(active):

@@ -306,6 +306,38 @@ def test_router_ties_rank_larger_index_last():
     assert idx.tolist() == [[2, 3]]
 
 
+def test_router_nan_choice_ranks_as_minus_inf():
+    # A NaN logit (NaN choice) is never chosen ahead of a finite choice, in the
+    # group scores or in the top-k; forced in only when fewer finite experts
+    # than k remain, by index like any other -inf.  The kernels do the same.
+    rng = np.random.default_rng(17)
+    T, d, E, k = 3, 32, 8, 3
+    x = O.bf16_round(rng.normal(0, 1, (T, d)).astype(np.float32))
+    W = rng.normal(0, 0.1, (E, d)).astype(np.float32)
+    W[5, 3] = np.nan  # expert 5's logit is NaN for every token
+    bias = np.zeros(E, np.float32)
+    bias[5] = 10.0  # would be the best by far if NaN ranked high
+    _, w, idx, choice = O.router(x, W, bias, top_k=k, n_group=1, topk_group=1,
+                                 norm_topk_prob=True, routed_scaling_factor=1.0)
+    assert not (idx == 5).any()
+    assert np.all(choice[:, 5] == -np.inf)
+    finite = np.delete(np.arange(E), 5)
+    c = O.router(x, np.delete(W, 5, axis=0), np.delete(bias, 5), top_k=k, n_group=1,
+                 topk_group=1, norm_topk_prob=True, routed_scaling_factor=1.0)
+    np.testing.assert_array_equal(idx, finite[c[2].astype(np.int64)])
+    # groups: the NaN expert's group scores only its finite members
+    _, _, gidx, _ = O.router(x, W, bias, top_k=2, n_group=4, topk_group=1,
+                             norm_topk_prob=True, routed_scaling_factor=1.0)
+    assert not (gidx == 5).any()
+    # all but two experts masked out of k = 3: the NaN one is forced in by index
+    W2 = np.full((4, d), np.nan, np.float32)
+    W2[1] = W[1]
+    W2[3] = W[3]
+    _, _, idx2, _ = O.router(x, W2, np.zeros(4, np.float32), top_k=3, n_group=1, topk_group=1,
+                             norm_topk_prob=False, routed_scaling_factor=1.0)
+    assert idx2[:, 0].tolist() == [2] * T  # the largest-index -inf expert ranks highest
+
+
 # --------------------------------------------------------------------------- dispatch
 
 
@@ -474,6 +506,30 @@ def test_c_restatement_matches_numpy_layer(cpu_twin, n_group, topk_group, shared
     assert np.array_equal(idx, inter["indices"])
     np.testing.assert_allclose(w, inter["weights"], rtol=1e-6)
     assert O.rel_l2(out, want) < 1e-5  # f32 lane sums vs exact products: last-bit differences
+
+
+def test_c_restatement_router_nan_choice(cpu_twin):
+    # a NaN router row: the C twin ranks the NaN choice as -inf, as the numpy
+    # oracle and the kernels do
+    from livglm_amd.workloads import MoEShape
+    rng = np.random.default_rng(33)
+    shape = MoEShape("tiny", T=4, d=128, E=16, k=4, I=64, I_shared=0, n_group=4, topk_group=2)
+    bank = _tiny_bank(rng, shape.E, shape.d, shape.I)
+    x = O.f32_to_bf16_bits(rng.normal(0, 1, (shape.T, shape.d)).astype(np.float32))
+    W = rng.normal(0, 0.02, (shape.E, shape.d)).astype(np.float32)
+    W[6, 0] = np.nan
+    b = np.zeros(shape.E, np.float32)
+    b[6] = 5.0
+    layer = {"x": x, "router_weight": W, "router_bias": b}
+    layer.update(zip(("gate_proj.weight_packed", "gate_proj.weight_scale", "up_proj.weight_packed",
+                      "up_proj.weight_scale", "down_proj.weight_packed", "down_proj.weight_scale"),
+                     (bank.gate_w, bank.gate_s, bank.up_w, bank.up_s, bank.down_w,
+                      bank.down_s)))
+    _, _, idx = cpu_twin.moe_layer(layer, shape, shared=False)
+    _, _, want, _ = O.router(O.bf16_bits_to_f32(x), W, b, top_k=shape.k, n_group=4, topk_group=2,
+                             norm_topk_prob=True, routed_scaling_factor=2.5)
+    assert not (want == 6).any()
+    np.testing.assert_array_equal(idx, want)
 
 
 def test_c_restatement_mxfp8_linear(cpu_twin):
