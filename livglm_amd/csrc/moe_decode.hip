@@ -526,6 +526,7 @@ struct PairArgs {
   uint16_t *h;  // [T*k][I] in pair order
   float limit;
   int routed_blocks;
+  int tpb;  // 16-row tiles of one pair per routed block (consecutive)
 };
 
 // LDS bytes of select_gate_up_kernel: the token row, then each of the four
@@ -546,11 +547,11 @@ __global__ __launch_bounds__(256) void select_gate_up_kernel(PairArgs a, SharedA
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int d = a.d, k = a.k, E = a.E;
-  const int tiles = a.I / 16;
-  const int tile = blockIdx.x % tiles;
-  const int pr = blockIdx.x / tiles;  // pair t*k + j
+  const int groups = a.I / 16 / a.tpb;     // blocks per pair
+  const int tile0 = (blockIdx.x % groups) * a.tpb;
+  const int pr = blockIdx.x / groups;  // pair t*k + j
   const int t = pr / k, j = pr % k;
-  const bool first = j == 0 && tile == 0;  // one block per token publishes the route
+  const bool first = j == 0 && tile0 == 0;  // one block per token publishes the route
   // Each wave stages the K range of token t's row that it multiplies and
   // selects the token's experts itself (moe.py:39-62; every wave reaches the
   // same choice), so no block barrier stands between the route and the
@@ -570,23 +571,49 @@ __global__ __launch_bounds__(256) void select_gate_up_kernel(PairArgs a, SharedA
                     publish ? a.indices + (size_t)t * k : nullptr, s_selw, scratch, lane);
   wave_lds_sync();  // the staged row and the choice, for this wave
   const long long e = s_selw[j];
-  const int row0 = tile * 16;
   const int kbase = wv * CPW * 128;
-  const uint8_t *wrow[2] = {a.gw + e * a.w_stride + (size_t)(row0 + r) * (d / 2),
-                            a.uw + e * a.w_stride + (size_t)(row0 + r) * (d / 2)};
-  const uint8_t *srow[2] = {a.gs + e * a.s_stride + (size_t)(row0 + r) * (d / 32),
-                            a.us + e * a.s_stride + (size_t)(row0 + r) * (d / 32)};
+  // the block's tiles in turn; the next tile's weights are issued as soon as
+  // the MFMAs have consumed this tile's registers, so the wave streams them
+  // back to back and the route above is paid once per block
+  const uint8_t *gw = a.gw + e * a.w_stride, *uw = a.uw + e * a.w_stride;
+  const uint8_t *gs = a.gs + e * a.s_stride, *us = a.us + e * a.s_stride;
   WaveWeights<FMT_MXFP4, 2, CPW> ww;
-  load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
-  glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
-  mma_wave_weights_lds<FMT_MXFP4, 2, CPW>(ww, kbase, q, s_x, acc);  // column 0 is stored
-  if (ksplit_reduce<2>(acc, red, wave, 4, lane) && r == 0) {
-    uint32_t o[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-      o[m] = f32_to_bf16(limited_swiglu(bf16_round(acc[0][m]), bf16_round(acc[1][m]), a.limit));
-    store_rows4(a.h + (size_t)pr * a.I + row0 + 4 * q, o);
+  {
+    const int row = tile0 * 16 + r;
+    const uint8_t *wrow[2] = {gw + (size_t)row * (d / 2), uw + (size_t)row * (d / 2)};
+    const uint8_t *srow[2] = {gs + (size_t)row * (d / 32), us + (size_t)row * (d / 32)};
+    load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
   }
+  for (int ti = 0; ti < a.tpb; ++ti) {
+    const int row0 = (tile0 + ti) * 16;
+    glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
+    mma_wave_weights_lds<FMT_MXFP4, 2, CPW>(ww, kbase, q, s_x, acc);  // column 0 is stored
+    if (ti + 1 < a.tpb) {
+      const int row = row0 + 16 + r;
+      const uint8_t *wrow[2] = {gw + (size_t)row * (d / 2), uw + (size_t)row * (d / 2)};
+      const uint8_t *srow[2] = {gs + (size_t)row * (d / 32), us + (size_t)row * (d / 32)};
+      load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
+    }
+    if (ksplit_reduce<2>(acc, red, wave, 4, lane) && r == 0) {
+      uint32_t o[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        o[m] = f32_to_bf16(limited_swiglu(bf16_round(acc[0][m]), bf16_round(acc[1][m]), a.limit));
+      store_rows4(a.h + (size_t)pr * a.I + row0 + 4 * q, o);
+    }
+  }
+}
+
+// 16-row tiles per routed block of select_gate_up_kernel: one while the grid
+// is small; with many tiles (the real expert geometry: 16 pairs x 128 tiles)
+// each block streams several consecutive tiles of its pair, so the grid fits
+// in one round of resident blocks and the token row + selection before the
+// first weight load is paid once per block, not once per tile.
+static int pair_tiles_per_block(int pairs, int I) {
+  const int tiles = I / 16;
+  int tpb = 1;
+  while (tpb < 8 && (long long)pairs * tiles / tpb > 768 && tiles % (2 * tpb) == 0) tpb *= 2;
+  return tpb;
 }
 
 struct PairDownArgs {
@@ -605,6 +632,7 @@ struct PairDownArgs {
   const float *hc_res, *hc_post, *hc_comb;  // [T][hc][d], [T][hc], [T][hc][hc]
   float *hc_out;                            // [T][hc][d]
   int hc, hc_bf16;                          // hc_bf16: bf16 streams (GLM_HC_BF16_STREAMS)
+  int tpb;  // 16-row tiles of d per block (consecutive)
 };
 
 constexpr int kPairMaxHc = 8;
@@ -622,13 +650,13 @@ __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
   const int j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, q = lane >> 4;
   const int k = a.k, d = a.d, I = a.I;
-  const int tiles = d / 16;
-  const int t = blockIdx.x / tiles;
-  const int row0 = (blockIdx.x % tiles) * 16;
+  const int groups = d / 16 / a.tpb;  // blocks per token
+  const int t = blockIdx.x / groups;
+  const int tile0 = (blockIdx.x % groups) * a.tpb;
   // Every load goes out before the first wait: the wave's route, the h rows
   // (into registers; past the rows the index is clamped so that no load
-  // depends on the lane), then the weights, whose addresses wait only for
-  // the route; the h rows reach LDS after that.
+  // depends on the lane), then the weights of the first tile, whose
+  // addresses wait only for the route; the h rows reach LDS after that.
   long long e = 0;
   float wj = 0.0f;
   if (j < k) {
@@ -644,10 +672,12 @@ __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
     const int i = min((int)threadIdx.x + (int)blockDim.x * u, nh - 1);
     hv[u] = *reinterpret_cast<const glm_u32x4 *>(hsrc + (size_t)i * 8);
   }
+  const uint8_t *dw = a.dw + e * a.w_stride, *ds = a.ds + e * a.s_stride;
   WaveWeights<FMT_MXFP4, 1, CPW_R> ww;
   if (j < k) {
-    const uint8_t *wrow[1] = {a.dw + e * a.w_stride + (size_t)(row0 + r) * (I / 2)};
-    const uint8_t *srow[1] = {a.ds + e * a.s_stride + (size_t)(row0 + r) * (I / 32)};
+    const int row = tile0 * 16 + r;
+    const uint8_t *wrow[1] = {dw + (size_t)row * (I / 2)};
+    const uint8_t *srow[1] = {ds + (size_t)row * (I / 32)};
     load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
   }
 #pragma unroll
@@ -656,68 +686,79 @@ __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
     if (i < nh)
       *reinterpret_cast<glm_u32x4 *>(s_h + (i / per_row) * lds_row_stride(I) + (i % per_row) * 8) = hv[u];
   }
-  // the shared expert's contribution to these 16 outputs (thread c < 16)
-  float shared_v = 0.0f;
-  const int c = row0 + threadIdx.x;
-  // the FFN site's residual streams for these outputs, and its gates
+  // the FFN site's gates for this token
   __shared__ float s_hc[kPairMaxHc + kPairMaxHc * kPairMaxHc];
-  float rv[kPairMaxHc];
   const int hc = a.hc;
   if (a.hc_out != nullptr) {
-    if (threadIdx.x < 16) {
-#pragma unroll
-      for (int i = 0; i < kPairMaxHc; ++i)
-        rv[i] = i < hc ? a.hc_res[((size_t)t * hc + i) * d + c] : 0.0f;
-    }
     const int ns = hc + hc * hc;
     if ((int)threadIdx.x >= 64 && (int)threadIdx.x < 64 + ns) {
       const int i = threadIdx.x - 64;
       s_hc[i] = i < hc ? a.hc_post[(size_t)t * hc + i] : a.hc_comb[(size_t)t * hc * hc + i - hc];
     }
   }
-  if (threadIdx.x < 16) {
-    if (a.shared_parts != nullptr) {
-      float sp = a.shared_parts[(size_t)t * d + c];
-      for (int qq = 1; qq < a.nparts; ++qq) sp = sp + a.shared_parts[((size_t)qq * a.T + t) * d + c];
-      shared_v = bf16_round(sp);
-    } else if (a.shared != nullptr) {
-      shared_v = bf16_to_f32(a.shared[(size_t)t * d + c]);
-    }
-  }
-  __syncthreads();
-  if (j < k) {
-    glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
-    mma_wave_weights_lds<FMT_MXFP4, 1, CPW_R>(ww, 0, q, s_h + j * lds_row_stride(I),
-                                              acc);  // column 0 is stored
-    if (r == 0) {
+  // the block's 16-row tiles in turn; the next tile's weights are issued as
+  // soon as the MFMAs have consumed this tile's registers
+  for (int ti = 0; ti < a.tpb; ++ti) {
+    const int row0 = (tile0 + ti) * 16;
+    const int c = row0 + threadIdx.x;  // output column of threads < 16
+    // the shared expert's contribution and the residual streams of these outputs
+    float shared_v = 0.0f;
+    float rv[kPairMaxHc];
+    if (threadIdx.x < 16) {
+      if (a.hc_out != nullptr) {
 #pragma unroll
-      for (int m = 0; m < 4; ++m) s_p[j][4 * q + m] = bf16_round(acc[0][m]) * wj;
+        for (int i = 0; i < kPairMaxHc; ++i)
+          rv[i] = i < hc ? a.hc_res[((size_t)t * hc + i) * d + c] : 0.0f;
+      }
+      if (a.shared_parts != nullptr) {
+        float sp = a.shared_parts[(size_t)t * d + c];
+        for (int qq = 1; qq < a.nparts; ++qq) sp = sp + a.shared_parts[((size_t)qq * a.T + t) * d + c];
+        shared_v = bf16_round(sp);
+      } else if (a.shared != nullptr) {
+        shared_v = bf16_to_f32(a.shared[(size_t)t * d + c]);
+      }
     }
-  }
-  __syncthreads();
-  if (threadIdx.x < 16) {
-    float o = 0.0f;
-    for (int jj = 0; jj < k; ++jj) o = o + s_p[jj][threadIdx.x];
-    if (a.shared_parts != nullptr || a.shared != nullptr) o = o + shared_v;
-    a.out[(size_t)t * d + c] = o;
-    if (a.hc_out != nullptr) {
-      // hyper_residual (mhc.py:51-60): the placement and the mixing sum
-      // rounded as separate operations; bf16 streams round post, comb and the
-      // mixing sum to bf16
-      for (int jj = 0; jj < hc; ++jj) {
-        float pj = s_hc[jj];
-        if (a.hc_bf16) pj = bf16_round(pj);
-        float m = 0.0f;
+    __syncthreads();  // h in LDS (first tile); s_p free again (later tiles)
+    if (j < k) {
+      glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
+      mma_wave_weights_lds<FMT_MXFP4, 1, CPW_R>(ww, 0, q, s_h + j * lds_row_stride(I),
+                                                acc);  // column 0 is stored
+      if (ti + 1 < a.tpb) {
+        const int row = row0 + 16 + r;
+        const uint8_t *wrow[1] = {dw + (size_t)row * (I / 2)};
+        const uint8_t *srow[1] = {ds + (size_t)row * (I / 32)};
+        load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
+      }
+      if (r == 0) {
 #pragma unroll
-        for (int i = 0; i < kPairMaxHc; ++i) {
-          if (i < hc) {
-            float w = s_hc[hc + i * hc + jj];
-            if (a.hc_bf16) w = bf16_round(w);
-            m = m + w * rv[i];
+        for (int m = 0; m < 4; ++m) s_p[j][4 * q + m] = bf16_round(acc[0][m]) * wj;
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < 16) {
+      float o = 0.0f;
+      for (int jj = 0; jj < k; ++jj) o = o + s_p[jj][threadIdx.x];
+      if (a.shared_parts != nullptr || a.shared != nullptr) o = o + shared_v;
+      a.out[(size_t)t * d + c] = o;
+      if (a.hc_out != nullptr) {
+        // hyper_residual (mhc.py:51-60): the placement and the mixing sum
+        // rounded as separate operations; bf16 streams round post, comb and
+        // the mixing sum to bf16
+        for (int jj = 0; jj < hc; ++jj) {
+          float pj = s_hc[jj];
+          if (a.hc_bf16) pj = bf16_round(pj);
+          float m = 0.0f;
+#pragma unroll
+          for (int i = 0; i < kPairMaxHc; ++i) {
+            if (i < hc) {
+              float w = s_hc[hc + i * hc + jj];
+              if (a.hc_bf16) w = bf16_round(w);
+              m = m + w * rv[i];
+            }
           }
+          if (a.hc_bf16) m = bf16_round(m);
+          a.hc_out[((size_t)t * hc + jj) * d + c] = pj * o + m;
         }
-        if (a.hc_bf16) m = bf16_round(m);
-        a.hc_out[((size_t)t * hc + jj) * d + c] = pj * o + m;
       }
     }
   }
@@ -1027,7 +1068,8 @@ int glm_pair_path_launch(hipStream_t stream, const uint16_t *x, int T, int d, co
   a.I = I;
   a.h = h;
   a.limit = glm_limit_bf16(limit);
-  a.routed_blocks = T * k * (I / 16);
+  a.tpb = pair_tiles_per_block(T * k, I);
+  a.routed_blocks = T * k * (I / 16) / a.tpb;
   rc = launch_select_gate_up(stream, a, sh, sg ? glm_decode_shared_cpws(Is) : 1);
   if (rc) return rc;
 
@@ -1055,8 +1097,12 @@ int glm_pair_path_launch(hipStream_t stream, const uint16_t *x, int T, int d, co
     b.hc = hc->hc;
     b.hc_bf16 = hc->bf16;
   }
+  // tiles per block: one while the grid is small; at the real expert
+  // geometry (d 4096) two, so the token's h rows and route load once per two tiles
+  b.tpb = 1;
+  while (b.tpb < 4 && T * (d / 16) / (2 * b.tpb) >= 256 && (d / 16) % (2 * b.tpb) == 0) b.tpb *= 2;
   const size_t lds3 = (size_t)k * lds_row_stride(I) * 2;
-  const dim3 g3(T * (d / 16)), b3(64 * std::max(k, 4));
+  const dim3 g3(T * (d / 16) / b.tpb), b3(64 * std::max(k, 4));
   switch (I / 128) {
     case 1: hipLaunchKernelGGL((down_combine_kernel<1>), g3, b3, lds3, stream, b); break;
     case 2: hipLaunchKernelGGL((down_combine_kernel<2>), g3, b3, lds3, stream, b); break;
@@ -1118,7 +1164,8 @@ extern "C" int glm_route_gate_up(void *stream, const float *logits, const float 
   a.I = I;
   a.h = h;
   a.limit = glm_limit_bf16(swiglu_limit);
-  a.routed_blocks = T * top_k * (I / 16);
+  a.tpb = pair_tiles_per_block(T * top_k, I);
+  a.routed_blocks = T * top_k * (I / 16) / a.tpb;
   SharedArgs sh{};
   return launch_select_gate_up((hipStream_t)stream, a, sh, 1);
 }
