@@ -51,6 +51,15 @@ METRIC = "MoE layer tokens/s; decode expert HBM GB/s; MXFP4 MFMA util at T=4096"
 HBM_PEAK_GBPS = 8000.0
 MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "fp8": 5000.0, "fp4": 10100.0}  # MI355X dense
 COPY_BYTES = 256 << 20  # counter calibration: one device copy of this size
+ACT_NAMES = {0: "fp8x2", 1: "fp6x2", 2: "fp4"}
+
+
+def design_ceiling(act_format: int) -> float:
+    """Algorithmic TFLOP/s the grouped GEMM's MFMAs allow in an activation
+    format: FP8 x FP4 twice per product (hi, lo) at the FP8 rate, FP6 x FP4
+    twice at the FP6 rate, FP4 x FP4 once."""
+    return {0: MFMA_PEAK_TFLOPS["fp8"] / 2, 1: MFMA_PEAK_TFLOPS["fp4"] / 2,
+            2: MFMA_PEAK_TFLOPS["fp4"]}[act_format]
 
 
 def parse_args():
@@ -72,6 +81,10 @@ def parse_args():
     ap.add_argument("--traffic", type=int, default=1,
                     help="1: measure the dominant kernel's HBM traffic with rocprofv3 counters")
     ap.add_argument("--seed", type=int, default=5301)
+    ap.add_argument("--act-format", default="fp8x2", choices=["fp8x2", "fp6x2", "fp4"],
+                    help="prefill: activation format of the timed grouped gate/up GEMM "
+                         "(fp8x2: the exact split the layer uses; fp6x2, fp4: the "
+                         "lower-precision variants)")
     ap.add_argument("--load-layers", type=int, default=8,
                     help="bank_load: layers of the synthetic checkpoint (320 MB each)")
     ap.add_argument("--load-threads", type=int, default=16,
@@ -179,6 +192,8 @@ class Setup:
                                and I // 128 in (1, 2, 4, 6, 8, 16))
         self.few_token = T <= 4 and k <= 8 and self.decode_kernels
         self.grouped = T > 64
+        self.act_format = {"fp8x2": native.GLM_ACT_FP8X2, "fp6x2": native.GLM_ACT_FP6X2,
+                           "fp4": native.GLM_ACT_FP4}[getattr(args, "act_format", "fp8x2")]
 
     def bias(self, step: int, layer: int):
         """The router bias of one layer at one step."""
@@ -222,13 +237,14 @@ class Setup:
                                                           "tok", "active", "nact", "work",
                                                           "status")))
             if self.grouped:
-                # the grouped GEMM reads the activations as their FP8 split
+                # the grouped GEMM reads the activations as their block-scaled
+                # split (the exact FP8 split unless --act-format says otherwise)
                 xi = r % self.n_inputs
                 if xi not in self.x_splits:
-                    buf = torch.empty(self.lib.glm_act_split_bytes(T, d), dtype=torch.uint8,
-                                      device=self.dev)
-                    native.call("glm_act_split_fp8", self.stream, x.data_ptr(), T, d,
-                                buf.data_ptr())
+                    buf = torch.empty(self.lib.glm_act_split_bytes_fmt(T, d, self.act_format),
+                                      dtype=torch.uint8, device=self.dev)
+                    native.call("glm_act_split", self.stream, x.data_ptr(), T, d,
+                                self.act_format, buf.data_ptr())
                     self.x_splits[xi] = buf
                 pl["tiles"] = torch.empty((self.max_tiles, 4), **i32)
                 pl["ntiles"] = torch.empty(1, **i32)
@@ -245,7 +261,7 @@ class Setup:
         b, pl, x = self.banks[r % self.n_banks], self.plans[r], self.xs[r % self.n_inputs]
         sh, native = self.shape, self.native
         if self.grouped:
-            native.call("glm_expert_gate_up_grouped", self.stream,
+            native.call("glm_expert_gate_up_grouped_fmt", self.stream, self.act_format,
                         self.x_splits[r % self.n_inputs].data_ptr(), self.T, self.d, self.I,
                         *(b[key].data_ptr() for key in self.keys[:4]), pl["tok"].data_ptr(),
                         pl["tiles"].data_ptr(), pl["ntiles"].data_ptr(), self.max_tiles,
@@ -266,7 +282,7 @@ class Setup:
         """The dominant kernel's instantiation, as rocprofv3 names it."""
         d, E = self.d, self.E
         if self.grouped:
-            return "grouped_f8f4_kernel<2>"
+            return f"grouped_f8f6f4_kernel<2, {self.act_format}>"
         if self.few_token:
             epl = 2 if E <= 128 else (4 if E <= 256 else 8)
             return f"select_gate_up_kernel<{epl}, {d // 512}, 1>"
@@ -444,6 +460,7 @@ def measure(args, torch, np, workload: str, *, steps: int, warmup: int, traffic:
         "roofline": roofline(S, achieved, tflops, bytes_per_launch, k_ms, R, traffic_v,
                              traffic_note),
         "kernel_tflops": tflops, "kernel_ms": k_ms, "kernel_flops": S.kernel_flops(),
+        "act_format": S.act_format,
         "cpu": cpu,
     }
     if unique_per_step and not S.grouped:
@@ -502,11 +519,12 @@ def prefill_leg(r: dict, counters: dict | None) -> dict:
         "algorithmic_flops_per_launch": r["kernel_flops"],
         "algorithmic_tflops": round(alg, 1), "fp4_peak_tflops": peak,
         "mxfp4_mfma_util": round(alg / peak, 4),
-        # the split design issues two FP8 x FP4 MFMAs (x's hi and lo parts) per
+        # the exact split issues two FP8 x FP4 MFMAs (x's hi and lo parts) per
         # product at the 5.0 PFLOP/s FP8 rate: 2.5 PFLOP/s of algorithmic work
-        # at most
-        "design_ceiling_tflops": MFMA_PEAK_TFLOPS["bf16"],
-        "frac_of_design_ceiling": round(alg / MFMA_PEAK_TFLOPS["bf16"], 4),
+        # at most (FP6 split: 5.05, FP4: 10.1)
+        "act_format": ACT_NAMES[r["act_format"]],
+        "design_ceiling_tflops": design_ceiling(r["act_format"]),
+        "frac_of_design_ceiling": round(alg / design_ceiling(r["act_format"]), 4),
     }
     if counters:
         leg["counters"] = counters
@@ -609,16 +627,18 @@ def roofline(S, achieved, tflops, bytes_per_launch, k_ms, R, traffic, traffic_no
               "launches": R, "unique_experts_per_launch": round(sum(S.unique) / R, 2)}
     if S.grouped:
         # algorithmic FLOPs over the 10.1 PFLOP/s dense MXFP4 peak; the kernel
-        # runs block-scaled FP8 x FP4 MFMAs on the exact hi/lo split of the
-        # activations, two per product at the 5.0 PFLOP/s FP8 rate, so its own
-        # ceiling is 2.5 PFLOP/s of algorithmic work (reported beside it)
+        # runs block-scaled MFMAs on a split of the activations: two FP8 x FP4
+        # per product at the 5.0 PFLOP/s FP8 rate for the exact split (a
+        # ceiling of 2.5 PFLOP/s of algorithmic work, reported beside it), two
+        # at the FP6 rate for the FP6 split, one at the FP4 rate for FP4
+        ceiling = design_ceiling(S.act_format)
         return {"kernel": S.kernel_name() + " (grouped MXFP4 gate/up + SwiGLU GEMMs, block-scaled "
-                                            "FP8 x FP4 MFMA on the exact hi/lo split of x)",
+                                            f"MFMA on the {ACT_NAMES[S.act_format]} split of x)",
                 "bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_PEAK_TFLOPS["fp4"],
                 "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS["fp4"], 4),
                 "flops_per_launch": S.kernel_flops(),
-                "design_ceiling": MFMA_PEAK_TFLOPS["bf16"],
-                "frac_of_design_ceiling": round(tflops / MFMA_PEAK_TFLOPS["bf16"], 4),
+                "design_ceiling": ceiling,
+                "frac_of_design_ceiling": round(tflops / ceiling, 4),
                 **common}
     return {"kernel": S.kernel_name() + (" (few-token selection + routed MXFP4 gate/up + SwiGLU)"
                                          if S.few_token else
@@ -863,7 +883,8 @@ def _counter_pass(counters: list[str], child_args: list[str]) -> dict[str, dict[
 
 def _kernel_child(args, workload: str, launches: int, rotation_gb: float) -> list[str]:
     return ["--mode", "kernel", "--workload", workload, "--kernel-launches", str(launches),
-            "--seed", str(args.seed), "--min-rotation-gb", str(rotation_gb)]
+            "--seed", str(args.seed), "--min-rotation-gb", str(rotation_gb),
+            "--act-format", args.act_format]
 
 
 def measure_traffic(args, workload: str, kernel_name: str):

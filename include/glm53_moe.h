@@ -163,6 +163,34 @@ size_t glm_act_split_bytes(int rows, int K);
 int glm_act_split_fp8(void *stream, const uint16_t *x, int rows, int K, void *split);
 
 /*
+ * Activation formats of the grouped GEMMs (act_format).  Every form is
+ * block-scaled over 32-element groups with E8M0 scales, each term's scale the
+ * smallest power of two that keeps the group within the element maximum:
+ *   GLM_ACT_FP8X2  the exact two-term E4M3FN split above; two MFMAs per
+ *                  block at the FP8 rate;
+ *   GLM_ACT_FP6X2  two E2M3 terms (hi, then the rounded exact residual):
+ *                  ~3e-4 relative error on Gaussian rows; two MFMAs at the
+ *                  FP6 rate (twice FP8's);
+ *   GLM_ACT_FP4    one E2M1 term: ~12 % relative error; one MFMA at the FP4
+ *                  rate.
+ * Split layout (glm_act_split_bytes_fmt(rows, K, fmt) bytes, regions 256-byte
+ * aligned): hi codes, lo codes, hi scales [rows][K/32], lo scales (FP4: codes,
+ * scales).  Code rows: FP8X2 [K] one byte per element; FP4 [K/2], two codes
+ * per byte, low nibble first; FP6X2 [K] in 128-byte chunks per 128 elements,
+ * group g's 32 codes packed 6 bits each, low bits first, bytes 0..15 at 16 g
+ * and bytes 16..23 at 64 + 16 g (the rest zero).
+ * No reference counterpart (the reference multiplies bf16 activations): the
+ * lower-precision forms are speed/accuracy variants of the grouped GEMMs.
+ * Limits: K % 32 == 0 (FP6X2: K % 128 == 0); glm_act_split_bytes_fmt returns
+ * 0 outside them.
+ */
+#define GLM_ACT_FP8X2 0
+#define GLM_ACT_FP6X2 1
+#define GLM_ACT_FP4 2
+size_t glm_act_split_bytes_fmt(int rows, int K, int act_format);
+int glm_act_split(void *stream, const uint16_t *x, int rows, int K, int act_format, void *split);
+
+/*
  * Prefill routed gate/up as grouped GEMMs over the row tiles of
  * glm_moe_tiles, on the block-scaled MFMA: MXFP4 weights as stored, the
  * activations as their FP8 split.  Replaces gather_qmm(gate/up) +
@@ -188,6 +216,23 @@ int glm_expert_down_grouped(void *stream, const void *h_split, int P, int I, int
                             const uint8_t *down_packed, const uint8_t *down_scales,
                             const int32_t *tiles, const int32_t *num_tiles, int max_tiles,
                             uint16_t *y);
+
+/*
+ * glm_expert_gate_up_grouped / glm_expert_down_grouped with the activations
+ * split in act_format (glm_act_split of x, of h).  GLM_ACT_FP8X2 is exactly
+ * the entry points above.  No reference counterpart: format variants of the
+ * same products (native_expert_ssd.py:726-743).
+ */
+int glm_expert_gate_up_grouped_fmt(void *stream, int act_format, const void *x_split, int T,
+                                   int d, int I, const uint8_t *gate_packed,
+                                   const uint8_t *gate_scales, const uint8_t *up_packed,
+                                   const uint8_t *up_scales, const int32_t *pair_token,
+                                   const int32_t *tiles, const int32_t *num_tiles, int max_tiles,
+                                   float swiglu_limit, uint16_t *h);
+int glm_expert_down_grouped_fmt(void *stream, int act_format, const void *h_split, int P, int I,
+                                int d, const uint8_t *down_packed, const uint8_t *down_scales,
+                                const int32_t *tiles, const int32_t *num_tiles, int max_tiles,
+                                uint16_t *y);
 
 /*
  * Weighted combine + shared add (moe.py:198-201):

@@ -100,6 +100,15 @@ __device__ __forceinline__ float sigmoid_f32(float x) {
   return x < 0.0f ? y : 1.0f - y;
 }
 
+// sigmoid with the hardware exp2 and reciprocal: within a few f32 ulp of
+// sigmoid_f32 (the bf16 rounding that follows absorbs that except within a
+// few ulp of a bf16 rounding tie), at a fraction of its instructions.
+__device__ __forceinline__ float sigmoid_fast(float x) {
+  const float e = __builtin_amdgcn_exp2f(fabsf(x) * 1.44269504088896341f);
+  const float y = __builtin_amdgcn_rcpf(1.0f + e);
+  return x < 0.0f ? y : 1.0f - y;
+}
+
 // limited_swiglu on one element with bf16 intermediates (expert_ssd.py:103-107):
 // g = min(g, L); u = clip(u, -L, L); h = bf16(bf16(g * bf16(sigmoid(g))) * u).
 __device__ __forceinline__ float limited_swiglu(float g, float u, float limit_bf16) {
@@ -108,6 +117,19 @@ __device__ __forceinline__ float limited_swiglu(float g, float u, float limit_bf
     u = fminf(fmaxf(u, -limit_bf16), limit_bf16);
   }
   float s = bf16_round(sigmoid_f32(g));
+  float a = bf16_round(g * s);
+  return bf16_round(a * u);
+}
+
+// limited_swiglu with sigmoid_fast, for the epilogues of the many-token GEMMs
+// (64 of them per lane there, where the exact sigmoid's dependent chains do
+// not hide behind two waves per SIMD).
+__device__ __forceinline__ float limited_swiglu_fast(float g, float u, float limit_bf16) {
+  if (limit_bf16 > 0.0f) {
+    g = fminf(g, limit_bf16);
+    u = fminf(fmaxf(u, -limit_bf16), limit_bf16);
+  }
+  float s = bf16_round(sigmoid_fast(g));
   float a = bf16_round(g * s);
   return bf16_round(a * u);
 }

@@ -327,49 +327,76 @@ __global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a
 // ---------------------------------------------------------------------------
 // Routed expert GEMMs on the block-scaled MFMA
 // (v_mfma_scale_f32_16x16x128_f8f6f4): MXFP4 weights enter as they are stored
-// (E2M1 codes + their E8M0 group scales), the bf16 activations as an exact
-// two-term FP8 split
-//     x = hi * 2^(shi - 127) + lo * 2^(slo - 127)     per 32-element group,
-// hi, lo E4M3FN codes with their own E8M0 scales.  hi holds the top 4
-// significant bits of each element, lo the remaining <= 4 (a bf16 element has
-// 8), so the split reproduces every element exactly unless it lies ~14
-// binades below its group's maximum, where the error stays below 2^-22 of
-// that maximum.  Each 16x16x128 output block is then two MFMAs (hi, lo)
-// accumulating in f32: no dequantisation instructions at all.
+// (E2M1 codes + their E8M0 group scales), the bf16 activations as a
+// block-scaled split (32-element groups, E8M0 scales) in one of three forms:
+//   ACT_FP8X2  x = hi * 2^(shi - 127) + lo * 2^(slo - 127), hi and lo E4M3FN.
+//              hi holds the top 4 significant bits of each element, lo the
+//              remaining <= 4 (a bf16 element has 8), so the split reproduces
+//              every element exactly unless it lies ~14 binades below its
+//              group's maximum, where the error stays below 2^-22 of that
+//              maximum.  Two MFMAs per output block at the FP8 rate.
+//   ACT_FP6X2  the same two-term form with E2M3 codes: ~3e-4 relative error
+//              on Gaussian rows, two MFMAs at the FP6 rate (twice FP8's).
+//   ACT_FP4    one E2M1 term: ~12 % relative error, one MFMA at the FP4 rate.
+// Each term's scale is the smallest power of two that keeps the group's
+// largest magnitude within the element format's maximum (448, 7.5, 6); lo
+// encodes the exact f32 residual x - hi.  The MFMAs accumulate in f32: no
+// dequantisation instructions at all.
 //
 // Operand layout of the 16x16x128 MFMA, lane (i = l % 16, g = l / 16):
 //   A = weights (E2M1, 16 bytes): weight row i, K [32g, 32g + 32) -- exactly
 //       one stored MXFP4 group, so lane g's 16 bytes come straight from the
 //       row and its scale operand is that group's E8M0 byte;
-//   B = activations (E4M3, 32 bytes): token i, K [16g, 16g + 16) in bytes
-//       0..15 and K [64 + 16g, 64 + 16g + 16) in bytes 16..31; scale operand:
-//       token i's E8M0 byte of group g (K [32g, 32g + 32));
+//   B = activations, token i: E4M3 (32 bytes) K [16g, 16g + 16) in bytes
+//       0..15 and K [64 + 16g, 64 + 16g + 16) in bytes 16..31; E2M3 (24
+//       bytes) and E2M1 (16 bytes) K [32g, 32g + 32), element s at bits
+//       [w s, w s + w) of the lane's registers; scale operand: token i's E8M0
+//       byte of group g (K [32g, 32g + 32));
 //   D: lane holds weight rows 4g..4g+3 of token column i.
 // ---------------------------------------------------------------------------
 
+// Activation formats of the block-scaled GEMMs (the C ABI's act_format).
+constexpr int ACT_FP8X2 = 0, ACT_FP6X2 = 1, ACT_FP4 = 2;
+
+__host__ __device__ constexpr int act_terms(int af) { return af == ACT_FP4 ? 1 : 2; }
+// Stored code bytes of one term per activation row of K elements.
+__host__ __device__ constexpr long long act_code_row(int K, int af) {
+  return af == ACT_FP4 ? K / 2 : K;
+}
+
 // Byte offsets of an activation split of `rows` x K: hi codes, lo codes,
-// hi scales, lo scales, each 256-byte aligned.
+// hi scales, lo scales, each 256-byte aligned (ACT_FP4: codes, scales).
+// Code rows: ACT_FP8X2 one byte per element; ACT_FP4 two per byte, low
+// nibble first (the MXFP4 weight layout); ACT_FP6X2 per 128-element chunk
+// 128 bytes: group g's 32 codes packed 6 bits each, low bits first, bytes
+// 0..15 at 16 g and bytes 16..23 at 64 + 16 g (so that the FP8 operand reads
+// -- 16 bytes at 16 g and at 64 + 16 g -- fetch a whole E2M3 operand; the
+// other 8 bytes are zero).
 struct SplitLayout {
   size_t lo, shi, slo, total;
-  __host__ __device__ SplitLayout(long long rows, int K) {
-    const size_t codes = ((size_t)rows * K + 255) & ~(size_t)255;
+  __host__ __device__ SplitLayout(long long rows, int K, int af = ACT_FP8X2) {
+    const size_t codes = ((size_t)(rows * act_code_row(K, af)) + 255) & ~(size_t)255;
     const size_t scales = ((size_t)rows * (K / 32) + 255) & ~(size_t)255;
+    const int n = act_terms(af);
     lo = codes;
-    shi = 2 * codes;
-    slo = 2 * codes + scales;
-    total = 2 * codes + 2 * scales;
+    shi = n * codes;
+    slo = shi + scales;  // ACT_FP4: past the end, unused
+    total = n * (codes + scales);
   }
 };
 
 // E8M0 exponent byte for a group whose largest magnitude is amax: the
-// smallest 2^(b - 127) with amax / 2^(b - 127) <= 448 (E4M3FN's maximum).
-__device__ __forceinline__ int split_scale_byte(float amax) {
+// smallest 2^(b - 127) with amax / 2^(b - 127) <= mmax 2^emax, the element
+// format's maximum (mmax in [0.5, 1)); 127 for an all-zero group.
+__device__ __forceinline__ int fit_scale_byte(float amax, float mmax, int emax) {
   if (!(amax > 0.0f)) return 127;
   int e;
   const float m = frexpf(amax, &e);  // amax = m 2^e, m in [0.5, 1)
-  const int k = m <= 0.875f ? e - 9 : e - 8;
+  const int k = m <= mmax ? e - emax : e - emax + 1;
   return min(max(k + 127, 0), 254);
 }
+// E4M3FN: maximum 448 = 0.875 2^9
+__device__ __forceinline__ int split_scale_byte(float amax) { return fit_scale_byte(amax, 0.875f, 9); }
 
 // One thread per 32-element group: hi/lo E4M3FN codes and their scales.
 __global__ __launch_bounds__(256) void act_split_kernel(const uint16_t *x, long long groups,
@@ -433,14 +460,96 @@ __global__ __launch_bounds__(256) void act_split_kernel(const uint16_t *x, long 
   slo[g] = (uint8_t)bl;
 }
 
+// E2M3 / E2M1 code of v 2^(127 - b), round to nearest even, saturating at the
+// format maximum; *back = the code's value times 2^(b - 127) (exact in f32).
+// E2M3 magnitudes are n / 8 below 2, n / 4 in [2, 4), n / 2 in [4, 7.5]
+// (codes n, n + 8, n + 16); E2M1's are n / 2, n, 2 n (codes n, n + 2, n + 4).
+template <int AF>
+__device__ __forceinline__ uint32_t lowp_code(float v, int b, float *back) {
+  constexpr float kMax = AF == ACT_FP6X2 ? 7.5f : 6.0f;
+  constexpr int kFrac = AF == ACT_FP6X2 ? 3 : 1;  // log2 of the quantum's inverse below 2
+  constexpr uint32_t kSign = AF == ACT_FP6X2 ? 0x20u : 0x8u;
+  const float y = fminf(ldexpf(fabsf(v), 127 - b), kMax);
+  const int e = y < 2.0f ? 0 : (y < 4.0f ? 1 : 2);
+  const float n = rintf(ldexpf(y, kFrac - e));
+  const uint32_t neg = __float_as_uint(v) >> 31;
+  const float mag = ldexpf(n, e - kFrac + b - 127);
+  *back = neg ? -mag : mag;
+  return ((uint32_t)n + (uint32_t)(e << kFrac)) | (neg ? kSign : 0u);
+}
+
+// Codes of one term of a group: E2M3 six bits each into 6 words, E2M1 four
+// bits into 4 words, element s at bits [w s, w s + w).
+template <int AF>
+__device__ __forceinline__ void lowp_term(float v[32], int b, uint32_t out[6]) {
+  constexpr int w = AF == ACT_FP6X2 ? 6 : 4;
+#pragma unroll
+  for (int j = 0; j < 6; ++j) out[j] = 0u;
+#pragma unroll
+  for (int s = 0; s < 32; ++s) {
+    float back;
+    const uint32_t c = lowp_code<AF>(v[s], b, &back);
+    v[s] -= back;  // the exact residual
+    const int pos = w * s;
+    out[pos >> 5] |= c << (pos & 31);
+    if ((pos & 31) + w > 32) out[(pos >> 5) + 1] |= c >> (32 - (pos & 31));
+  }
+}
+
+// One thread per 32-element group: the ACT_FP6X2 (hi, lo) or ACT_FP4 split.
+template <int AF>
+__global__ __launch_bounds__(256) void act_split_lowp_kernel(const uint16_t *x, long long groups,
+                                                             int K, uint8_t *hi, uint8_t *lo,
+                                                             uint8_t *shi, uint8_t *slo) {
+  constexpr float kMm = AF == ACT_FP6X2 ? 0.9375f : 0.75f;  // 7.5 = 0.9375 2^3, 6 = 0.75 2^3
+  const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= groups) return;
+  const glm_u32x4 *src = reinterpret_cast<const glm_u32x4 *>(x + g * 32);
+  float v[32];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const glm_u32x4 w = src[j];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      v[8 * j + 2 * h] = __uint_as_float(w[h] << 16);
+      v[8 * j + 2 * h + 1] = __uint_as_float(w[h] & 0xffff0000u);
+    }
+  }
+  const long long groups_per_row = K / 32;
+  const long long row = g / groups_per_row;
+  const int grp = (int)(g % groups_per_row);
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+  const int bh = fit_scale_byte(amax, kMm, 3);
+  uint32_t c[6];
+  lowp_term<AF>(v, bh, c);
+  shi[g] = (uint8_t)bh;
+  if constexpr (AF == ACT_FP4) {
+    *reinterpret_cast<glm_u32x4 *>(hi + row * (K / 2) + 16 * grp) = glm_u32x4{c[0], c[1], c[2], c[3]};
+  } else {
+    uint8_t *dh = hi + row * K + 128 * (grp >> 2) + 16 * (grp & 3);
+    *reinterpret_cast<glm_u32x4 *>(dh) = glm_u32x4{c[0], c[1], c[2], c[3]};
+    *reinterpret_cast<glm_u32x4 *>(dh + 64) = glm_u32x4{c[4], c[5], 0u, 0u};
+    float ramax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) ramax = fmaxf(ramax, fabsf(v[j]));
+    const int bl = fit_scale_byte(ramax, kMm, 3);
+    lowp_term<AF>(v, bl, c);
+    uint8_t *dl = lo + row * K + 128 * (grp >> 2) + 16 * (grp & 3);
+    *reinterpret_cast<glm_u32x4 *>(dl) = glm_u32x4{c[0], c[1], c[2], c[3]};
+    *reinterpret_cast<glm_u32x4 *>(dl + 64) = glm_u32x4{c[4], c[5], 0u, 0u};
+    slo[g] = (uint8_t)bl;
+  }
+}
+
 // The split of one 32-element scale group held 8 per lane by the four lanes
 // q = 0..3 of a lane row (lanes r, r + 16, r + 32, r + 48); v holds this
 // lane's elements 16 i + 4 q + m at v[4 i + m].  Same arithmetic as
 // act_split_kernel: ch[i] / cl[i] are the hi / lo codes of elements
 // 16 i + 4 q .. + 3, bh / bl the group's scale bytes.
-__device__ __forceinline__ void split_group_part(float v[8], int q, uint32_t ch[2], uint32_t cl[2],
+__device__ __forceinline__ void split_group_part(float v[8], uint32_t ch[2], uint32_t cl[2],
                                                  int *bh_out, int *bl_out) {
-  (void)q;
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
@@ -478,7 +587,7 @@ __device__ __forceinline__ void split_group_part(float v[8], int q, uint32_t ch[
 }
 
 struct SplitArgs {
-  const uint8_t *xhi, *xlo;    // activation codes [rows][K]
+  const uint8_t *xhi, *xlo;    // activation codes (SplitLayout)
   const uint8_t *xshi, *xslo;  // activation scales [rows][K/32]
   uint32_t split_bytes;        // the split buffer starting at xhi (SplitLayout)
   const int32_t *act_index;    // sorted position -> activation row (nullptr: the position)
@@ -491,8 +600,8 @@ struct SplitArgs {
   int feature_tiles;
   uint16_t *out;               // bf16 [rows][N]
   float limit;
-  // gate/up: when set, the epilogue writes the FP8 hi/lo split of h (the down
-  // GEMM's input, SplitLayout(out_rows, N)) instead of h itself
+  // gate/up, ACT_FP8X2: when set, the epilogue writes the FP8 hi/lo split of
+  // h (the down GEMM's input, SplitLayout(out_rows, N)) instead of h itself
   uint8_t *out_split;
   long long out_rows;
 };
@@ -500,43 +609,53 @@ struct SplitArgs {
 // Workgroup tile of the block-scaled GEMMs: 128 token rows x 512 weight rows
 // (gate/up: 256 features of each projection), 16 waves as 8 (weight rows) x
 // 2 (tokens), each wave 64 weight rows x 64 tokens = 4 x 4 MFMA blocks.  The
-// activations cost 2 bytes per element (hi + lo) against the weights' half
-// byte, so the tile is wide along the weights: per 128-K chunk a workgroup
-// stages 67 KB of operands for 2 x 128 x 512 x 128 MACs.  Four waves per SIMD
-// hide each other's LDS reads behind their MFMAs.
+// two-term activations cost 2 bytes per element (hi + lo) against the
+// weights' half byte, so the tile is wide along the weights: per 128-K chunk
+// a workgroup stages 67 KB of operands for 2 x 128 x 512 x 128 MACs.  Four
+// waves per SIMD hide each other's LDS reads behind their MFMAs, and sixteen
+// waves keep enough direct-to-LDS loads in flight (eight waves cap them near
+// 3.7 TB/s on gfx950).
 constexpr int kSplitTileW = 512;
 constexpr int kSplitThreads = 1024;
 constexpr int kSplitWaves = kSplitThreads / 64;
 constexpr int kSplitStages = 2;  // double buffer: chunk c + 1 lands while c is consumed
 
 // LDS stage (one 128-K chunk):
-//   activations  [128 rows][hi 128 B | lo 128 B], piece p of row R at p ^ (R & 15)
-//   act. scales  hi [128 rows] u32, lo [128 rows] u32 (the chunk's 4 E8M0 bytes)
+//   activations  two-term formats [128 rows][hi 128 B | lo 128 B], piece p of
+//                row R at p ^ (R & 15); ACT_FP4 [128 rows][64 B], piece p of
+//                row R at p ^ ((R >> 1) & 3)
+//   act. scales  [terms][128 rows] u32 (the chunk's 4 E8M0 bytes)
 //   weights      [512 rows][64 B], piece p of row R at p ^ ((R >> 1) & 3)
 //   w. scales    [512 rows] u32
+template <int AF>
 struct SplitStage {
-  static constexpr int kChunk = 128;
-  static constexpr int kXBytes = kTileM * 256;
-  static constexpr int kXSBytes = 2 * kTileM * 4;
+  static constexpr int kParts = act_terms(AF);
+  static constexpr int kXRow = AF == ACT_FP4 ? 64 : 256;
+  static constexpr int kXPieces = kXRow / 16;
+  static constexpr int kTermChunk = AF == ACT_FP4 ? 64 : 128;  // stored bytes per row and chunk
+  static constexpr int kXBytes = kTileM * kXRow;
+  static constexpr int kXSBytes = kParts * kTileM * 4;
   static constexpr int kWBytes = kSplitTileW * 64;
   static constexpr int kWSBytes = kSplitTileW * 4;
   static constexpr int kX = 0, kXS = kXBytes, kW = kXS + kXSBytes, kWS = kW + kWBytes;
   static constexpr int kBytes = kWS + kWSBytes;
-  static constexpr int kXLoads = kXBytes / (kSplitThreads * 16);  // 2
+  // 16-byte activation loads per thread (ACT_FP4: waves 0-7 load one each)
+  static constexpr int kXLoads = AF == ACT_FP4 ? 1 : kXBytes / (kSplitThreads * 16);
+  static constexpr int kXWaves = AF == ACT_FP4 ? 8 : kSplitWaves;
   static constexpr int kWLoads = kWBytes / (kSplitThreads * 16);  // 2
-  // + one scale dword per thread: waves 0-7 the weight scales (64 rows each),
-  // waves 8-11 the activation scales, waves 12-15 the same again (so every
-  // wave issues the same count)
-  static constexpr int kLoads = kXLoads + kWLoads + 1;
+  static constexpr int kXSLanes = kXSBytes / 4;                   // 256 or 128
+  static constexpr int kMfmaFmt = AF == ACT_FP8X2 ? 0 : (AF == ACT_FP6X2 ? 2 : 4);
   static_assert(kSplitStages * kBytes <= 160 * 1024, "LDS stages exceed 160 KB");
-  static_assert(kWSBytes == 8 * 256 && kXSBytes == 4 * 256, "scale loads per wave");
+  static_assert(kXLoads * kXWaves * 64 * 16 == kXBytes, "activation loads");
+  static_assert(kWSBytes == 8 * 256 && kXSLanes % 64 == 0, "scale loads per wave");
+  __device__ static int xswz(int row) { return kXPieces == 16 ? (row & 15) : ((row >> 1) & 3); }
 };
 
 typedef int glm_i32x8 __attribute__((ext_vector_type(8)));
 
-template <int NPROJ>
-__global__ __launch_bounds__(kSplitThreads) void grouped_f8f4_kernel(SplitArgs a) {
-  using S = SplitStage;
+template <int NPROJ, int AF>
+__global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs a) {
+  using S = SplitStage<AF>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int nft = a.feature_tiles;
   const int ntiles = *a.num_tiles;
@@ -556,16 +675,12 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f4_kernel(SplitArgs a
   const long long e = tile.x;
   const int pos0 = tile.y, rows = tile.z;
   const int K = a.K;
-  const int nchunks = K / S::kChunk;
+  const int nchunks = K / 128;
   constexpr int kHalf = kSplitTileW / 2;
   const int f0 = ftile * (kSplitTileW / NPROJ);
-  auto act_row = [&](int row) -> long long {
+  auto act_row = [&](int row) -> uint32_t {
     const int pos = pos0 + (row < rows ? row : 0);  // past the end: re-read row 0
-    return a.act_index != nullptr ? a.act_index[pos] : pos;
-  };
-  // staged weight row R -> (projection, feature row)
-  auto w_base = [&](int row, const uint8_t *const *arr) {
-    return NPROJ == 2 && row >= kHalf ? arr[1] : arr[0];
+    return (uint32_t)(a.act_index != nullptr ? a.act_index[pos] : pos);
   };
   auto w_feature = [&](int row) { return f0 + (NPROJ == 2 ? row % kHalf : row); };
 
@@ -574,12 +689,15 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f4_kernel(SplitArgs a
   // resources, per-lane offsets 32-bit; the chunk advances the uniform offset.
   const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.xhi, a.split_bytes);
   const uint32_t lo_off = (uint32_t)(a.xlo - a.xhi);
+  const uint32_t code_row = (uint32_t)act_code_row(K, AF);
   uint32_t xoff[S::kXLoads];
 #pragma unroll
   for (int j = 0; j < S::kXLoads; ++j) {
     const int slot = (j * kSplitWaves + wave) * 64 + lane;
-    const int row = slot / 16, piece = (slot % 16) ^ (row & 15);
-    xoff[j] = (piece < 8 ? 0u : lo_off) + (uint32_t)act_row(row) * (uint32_t)K + (piece & 7) * 16;
+    const int row = (slot / S::kXPieces) % kTileM;  // (ACT_FP4: waves 8-15 load nothing)
+    const int piece = (slot % S::kXPieces) ^ S::xswz(row);
+    xoff[j] = act_row(row) * code_row +
+              (S::kParts == 2 ? (piece < 8 ? 0u : lo_off) + (piece & 7) * 16 : piece * 16);
   }
   // weight load j covers staged rows [256 j, 256 j + 256): one projection
   const uint32_t wproj_bytes = (uint32_t)a.N * (uint32_t)(K / 2);
@@ -593,6 +711,9 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f4_kernel(SplitArgs a
     woff[j] = (uint32_t)w_feature(row) * (uint32_t)(K / 2) + piece * 16;
   }
   static_assert(S::kWLoads == 2 && kSplitWaves * 64 / 4 == kHalf, "one projection per load");
+  // one scale dword per thread: waves 0-7 the weight scales (64 rows each);
+  // waves 8-15 the activation scales, slot s = term * 128 + row, repeated
+  // once the slots run out (every wave issues the same count)
   __amdgpu_buffer_rsrc_t srs;
   uint32_t soff;
   int sdst;
@@ -604,18 +725,20 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f4_kernel(SplitArgs a
     soff = (uint32_t)w_feature(row) * (uint32_t)(K / 32);
     sdst = S::kWS + wv * 256;
   } else {
-    const int xj = wv & 3;  // hi rows 0-63, hi 64-127, lo 0-63, lo 64-127
+    const int s0 = ((wv - 8) * 64) % S::kXSLanes, s = s0 + lane;
     srs = xrs;
-    soff = (uint32_t)((xj < 2 ? a.xshi : a.xslo) - a.xhi) +
-           (uint32_t)act_row((xj & 1) * 64 + lane) * (uint32_t)(K / 32);
-    sdst = S::kXS + xj * 256;
+    soff = (uint32_t)((s >= kTileM ? a.xslo : a.xshi) - a.xhi) + act_row(s % kTileM) * (uint32_t)(K / 32);
+    sdst = S::kXS + s0 * 4;
   }
 
   auto issue = [&](int c, int stage) {
     uint8_t *base = smem + stage * S::kBytes;
+    if (wv < S::kXWaves) {
 #pragma unroll
-    for (int j = 0; j < S::kXLoads; ++j)
-      buf16_to_lds(xrs, base + S::kX + (j * kSplitWaves + wv) * 1024, xoff[j], c * 128);
+      for (int j = 0; j < S::kXLoads; ++j)
+        buf16_to_lds(xrs, base + S::kX + (j * kSplitWaves + wv) * 1024, xoff[j],
+                     c * S::kTermChunk);
+    }
 #pragma unroll
     for (int j = 0; j < S::kWLoads; ++j)
       buf16_to_lds(wrs[j], base + S::kW + (j * kSplitWaves + wv) * 1024, woff[j], c * 64);
@@ -635,15 +758,19 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f4_kernel(SplitArgs a
     for (int j = 0; j < 4; ++j) acc[i][j] = glm_f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Lane-dependent parts of the LDS operand addresses.  Every block starts at
-  // a multiple of 16 rows, so a lane's swizzle depends on r alone: activation
-  // row 16m + r, piece p sits at (16m + r) * 256 + 16 (p ^ r); weight row
-  // 16m + r, piece q at (16m + r) * 64 + 16 (q ^ ((r >> 1) & 3)).
-  const uint32_t xl_hi0 = r * 256 + 16 * (q ^ r), xl_hi1 = r * 256 + 16 * ((4 + q) ^ r);
-  const uint32_t xl_lo0 = r * 256 + 16 * ((8 + q) ^ r), xl_lo1 = r * 256 + 16 * ((12 + q) ^ r);
+  // a multiple of 16 rows, so a lane's swizzle depends on r alone: two-term
+  // activation row 16m + r, piece p at (16m + r) * 256 + 16 (p ^ r); ACT_FP4
+  // and weight row 16m + r, piece p at (16m + r) * 64 + 16 (p ^ ((r >> 1) & 3)).
+  uint32_t xl[2][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    xl[t][0] = r * S::kXRow + 16 * (S::kParts == 2 ? ((8 * t + q) ^ r) : (q ^ ((r >> 1) & 3)));
+    xl[t][1] = r * S::kXRow + 16 * ((8 * t + 4 + q) ^ r);
+  }
   const uint32_t wl = r * 64 + 16 * (q ^ ((r >> 1) & 3));
   const uint32_t sl = r * 4;
 
-  // MFMAs of one staged chunk: for each activation fragment (hi/lo x 4 token
+  // MFMAs of one staged chunk: for each activation fragment (term x 4 token
   // blocks) 4 MFMAs, one per weight-row block.
   auto compute = [&](int stage) {
     const uint8_t *base = smem + stage * S::kBytes;
@@ -656,17 +783,21 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f4_kernel(SplitArgs a
       wa[rt] = glm_i32x8{(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
       wsc[rt] = (int)(*reinterpret_cast<const uint32_t *>(base + S::kWS + w16 * 4 + sl) >> (8 * q));
     }
-    // activation fragment f = (part, ct) of this chunk: hi then lo, 4 token
-    // blocks each
+    // activation fragment f = (term f / 4, token block f % 4)
+    constexpr int kFrags = 4 * S::kParts;
     auto xfrag = [&](int f, glm_i32x8 &xb, int &xsc) {
-      const int part = f >> 2, ct = f & 3;
-      const uint8_t *xblk = base + S::kX + (wt * 64 + ct * 16) * 256;
-      const glm_u32x4 b0 = *reinterpret_cast<const glm_u32x4 *>(xblk + (part ? xl_lo0 : xl_hi0));
-      const glm_u32x4 b1 = *reinterpret_cast<const glm_u32x4 *>(xblk + (part ? xl_lo1 : xl_hi1));
-      xb = glm_i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3],
-                     (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+      const int t = f >> 2, ct = f & 3;
+      const uint8_t *xblk = base + S::kX + (wt * 64 + ct * 16) * S::kXRow;
+      const glm_u32x4 b0 = *reinterpret_cast<const glm_u32x4 *>(xblk + xl[t][0]);
+      if constexpr (S::kParts == 2) {
+        const glm_u32x4 b1 = *reinterpret_cast<const glm_u32x4 *>(xblk + xl[t][1]);
+        xb = glm_i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3],
+                       (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+      } else {
+        xb = glm_i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], 0, 0, 0, 0};
+      }
       xsc = (int)(*reinterpret_cast<const uint32_t *>(
-                      base + S::kXS + (part * kTileM + wt * 64 + ct * 16) * 4 + sl) >>
+                      base + S::kXS + (t * kTileM + wt * 64 + ct * 16) * 4 + sl) >>
                   (8 * q));
     };
     // Fragment f + 1 is read from LDS before fragment f's MFMAs issue, so
@@ -676,20 +807,20 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f4_kernel(SplitArgs a
     int xsc;
     xfrag(0, xb, xsc);
 #pragma unroll
-    for (int f = 0; f < 8; ++f) {
+    for (int f = 0; f < kFrags; ++f) {
       glm_i32x8 xn;
       int xscn = 0;
-      if (f + 1 < 8) xfrag(f + 1, xn, xscn);
+      if (f + 1 < kFrags) xfrag(f + 1, xn, xscn);
       // token blocks wholly past the tile's rows (the last, partial tile of
       // an expert) are skipped: their columns are never stored
       if (wt * 64 + (f & 3) * 16 < rows) {
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt)
           acc[rt][f & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              wa[rt], xb, acc[rt][f & 3], 4, 0, 0, wsc[rt], 0, xsc);
+              wa[rt], xb, acc[rt][f & 3], 4, S::kMfmaFmt, 0, wsc[rt], 0, xsc);
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (f + 1 < 8) {
+      if (f + 1 < kFrags) {
         xb = xn;
         xsc = xscn;
       }
@@ -709,7 +840,7 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f4_kernel(SplitArgs a
 
   // ---- epilogue: lane (r, q) of block (rt, ct) holds weight rows 4q..4q+3 of
   // the block for token column r
-  if constexpr (NPROJ == 2) {
+  if constexpr (NPROJ == 2 && AF == ACT_FP8X2) {
     if (a.out_split != nullptr) {
       // h's FP8 hi/lo split, exactly as act_split_kernel forms it from the
       // bf16 h: the wave's 32 features f0 + 32 wf + [0, 32) of a token are one
@@ -726,11 +857,11 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f4_kernel(SplitArgs a
         for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int m = 0; m < 4; ++m)
-            v[4 * i + m] = bf16_round(limited_swiglu(bf16_round(acc[i][ct][m]),
-                                                     bf16_round(acc[2 + i][ct][m]), a.limit));
+            v[4 * i + m] = bf16_round(limited_swiglu_fast(bf16_round(acc[i][ct][m]),
+                                                          bf16_round(acc[2 + i][ct][m]), a.limit));
         uint32_t ch[2], cl[2];
         int bh, bl;
-        split_group_part(v, q, ch, cl, &bh, &bl);
+        split_group_part(v, ch, cl, &bh, &bl);
         if (row < rows) {
           const size_t prow = (size_t)(pos0 + row);
           uint8_t *hi = a.out_split + prow * a.N + g0;
@@ -760,8 +891,8 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f4_kernel(SplitArgs a
         uint32_t o[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m)
-          o[m] = f32_to_bf16(limited_swiglu(bf16_round(acc[i][ct][m]),
-                                            bf16_round(acc[2 + i][ct][m]), a.limit));
+          o[m] = f32_to_bf16(limited_swiglu_fast(bf16_round(acc[i][ct][m]),
+                                                 bf16_round(acc[2 + i][ct][m]), a.limit));
         store_rows4(orow + f0 + wf * 32 + i * 16 + 4 * q, o);
       }
     } else {
@@ -819,56 +950,91 @@ size_t glm_act_split_bytes(long long rows, int K) { return SplitLayout(rows, K).
 
 // The block-scaled GEMMs read a split through one buffer resource with 32-bit
 // offsets: the whole split must stay below 4 GiB.
-bool glm_split_fits(long long rows, int K) {
-  return rows >= 0 && K > 0 && SplitLayout(rows, K).total <= 0xffffffffull;
+bool glm_split_fits(long long rows, int K, int af) {
+  return rows >= 0 && K > 0 && SplitLayout(rows, K, af).total <= 0xffffffffull;
 }
+bool glm_split_fits(long long rows, int K) { return glm_split_fits(rows, K, ACT_FP8X2); }
 
-// bf16 activations [rows][K] -> their hi/lo FP8 split (layout SplitLayout).
-int glm_act_split_launch(hipStream_t stream, const uint16_t *x, long long rows, int K,
-                         void *split) {
+// bf16 activations [rows][K] -> their split in format af (layout SplitLayout).
+static int act_split_launch_as(hipStream_t stream, const uint16_t *x, long long rows, int K,
+                               int af, void *split) {
   const long long groups = rows * (K / 32);
   if (groups <= 0) return GLM_OK;
-  const SplitLayout L(rows, K);
+  const SplitLayout L(rows, K, af);
   uint8_t *base = static_cast<uint8_t *>(split);
-  hipLaunchKernelGGL(act_split_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0,
-                     stream, x, groups, base, base + L.lo, base + L.shi, base + L.slo);
+  const dim3 grid((unsigned)((groups + 255) / 256));
+  if (af == ACT_FP8X2)
+    hipLaunchKernelGGL(act_split_kernel, grid, dim3(256), 0, stream, x, groups, base,
+                       base + L.lo, base + L.shi, base + L.slo);
+  else if (af == ACT_FP6X2)
+    hipLaunchKernelGGL(act_split_lowp_kernel<ACT_FP6X2>, grid, dim3(256), 0, stream, x, groups, K,
+                       base, base + L.lo, base + L.shi, base + L.slo);
+  else
+    hipLaunchKernelGGL(act_split_lowp_kernel<ACT_FP4>, grid, dim3(256), 0, stream, x, groups, K,
+                       base, base, base + L.shi, base + L.shi);
   GLM_LAUNCH_CHECK("act_split_kernel");
   return GLM_OK;
 }
 
-static int split_launch(hipStream_t stream, SplitArgs a, int nproj, int max_tiles) {
+int glm_act_split_launch(hipStream_t stream, const uint16_t *x, long long rows, int K,
+                         void *split) {
+  return act_split_launch_as(stream, x, rows, K, ACT_FP8X2, split);
+}
+
+template <int NPROJ, int AF>
+static void launch_f8f6f4(hipStream_t stream, dim3 grid, const SplitArgs &a) {
+  const size_t lds = kSplitStages * (size_t)SplitStage<AF>::kBytes;
+  hipLaunchKernelGGL((grouped_f8f6f4_kernel<NPROJ, AF>), grid, dim3(kSplitThreads), lds, stream,
+                     a);
+}
+
+static int split_launch(hipStream_t stream, SplitArgs a, int nproj, int max_tiles, int af) {
   a.feature_tiles = a.N / (nproj == 2 ? kSplitTileW / 2 : kSplitTileW);
+  // XCD x handles items [x * per, (x + 1) * per) with per <= ceil(max_items / 8),
+  // at linear ids x + 8k: the grid must reach 8 * ceil(max_items / 8)
   const long long max_items = (long long)max_tiles * a.feature_tiles;
   const dim3 grid((unsigned)(((max_items + kXcds - 1) / kXcds) * kXcds));
-  const size_t lds = kSplitStages * (size_t)SplitStage::kBytes;
-  if (nproj == 2)
-    hipLaunchKernelGGL(grouped_f8f4_kernel<2>, grid, dim3(kSplitThreads), lds, stream, a);
-  else
-    hipLaunchKernelGGL(grouped_f8f4_kernel<1>, grid, dim3(kSplitThreads), lds, stream, a);
-  GLM_LAUNCH_CHECK("grouped_f8f4_kernel");
+  if (nproj == 2) {
+    if (af == ACT_FP8X2)
+      launch_f8f6f4<2, ACT_FP8X2>(stream, grid, a);
+    else if (af == ACT_FP6X2)
+      launch_f8f6f4<2, ACT_FP6X2>(stream, grid, a);
+    else
+      launch_f8f6f4<2, ACT_FP4>(stream, grid, a);
+  } else {
+    if (af == ACT_FP8X2)
+      launch_f8f6f4<1, ACT_FP8X2>(stream, grid, a);
+    else if (af == ACT_FP6X2)
+      launch_f8f6f4<1, ACT_FP6X2>(stream, grid, a);
+    else
+      launch_f8f6f4<1, ACT_FP4>(stream, grid, a);
+  }
+  GLM_LAUNCH_CHECK("grouped_f8f6f4_kernel");
   return GLM_OK;
 }
 
-static void set_split(SplitArgs &a, const void *split, long long rows, int K) {
-  const SplitLayout L(rows, K);
+static void set_split(SplitArgs &a, const void *split, long long rows, int K, int af) {
+  const SplitLayout L(rows, K, af);
   const uint8_t *base = static_cast<const uint8_t *>(split);
   a.split_bytes = (uint32_t)L.total;
   a.xhi = base;
   a.xlo = base + L.lo;
   a.xshi = base + L.shi;
-  a.xslo = base + L.slo;
+  a.xslo = af == ACT_FP4 ? base + L.shi : base + L.slo;
 }
 
-// x_split: the split of the T token rows of x (d columns).
-int glm_grouped_gate_up_launch(hipStream_t stream, const void *x_split, int T,
-                               const int32_t *pair_token, const int4 *tiles,
-                               const int32_t *num_tiles, int max_tiles, int d, int I,
-                               const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
-                               const uint8_t *us, uint16_t *h, float limit, void *h_split,
-                               long long P) {
+// x_split: the split (format af) of the T token rows of x (d columns).
+// h_split (ACT_FP8X2 only): when set, the epilogue writes the split of h
+// [P][I] instead of h.
+static int grouped_gate_up_as(hipStream_t stream, const void *x_split, int T,
+                              const int32_t *pair_token, const int4 *tiles,
+                              const int32_t *num_tiles, int max_tiles, int d, int I,
+                              const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
+                              const uint8_t *us, uint16_t *h, float limit, void *h_split,
+                              long long P, int af) {
   SplitArgs a{};
-  set_split(a, x_split, T, d);
-  a.out_split = static_cast<uint8_t *>(h_split);  // when set: the split of h [P][I], not h
+  set_split(a, x_split, T, d, af);
+  a.out_split = static_cast<uint8_t *>(h_split);
   a.out_rows = P;
   a.act_index = pair_token;
   a.tiles = tiles;
@@ -883,15 +1049,25 @@ int glm_grouped_gate_up_launch(hipStream_t stream, const void *x_split, int T,
   a.K = d;
   a.out = h;
   a.limit = glm_limit_bf16(limit);
-  return split_launch(stream, a, 2, max_tiles);
+  return split_launch(stream, a, 2, max_tiles, af);
 }
 
-// h_split: the split of the P sorted rows of h (I columns).
-int glm_grouped_down_launch(hipStream_t stream, const void *h_split, long long P,
-                            const int4 *tiles, const int32_t *num_tiles, int max_tiles, int I,
-                            int d, const uint8_t *dw, const uint8_t *ds, uint16_t *y) {
+int glm_grouped_gate_up_launch(hipStream_t stream, const void *x_split, int T,
+                               const int32_t *pair_token, const int4 *tiles,
+                               const int32_t *num_tiles, int max_tiles, int d, int I,
+                               const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
+                               const uint8_t *us, uint16_t *h, float limit, void *h_split,
+                               long long P) {
+  return grouped_gate_up_as(stream, x_split, T, pair_token, tiles, num_tiles, max_tiles, d, I, gw,
+                            gs, uw, us, h, limit, h_split, P, ACT_FP8X2);
+}
+
+// h_split: the split (format af) of the P sorted rows of h (I columns).
+static int grouped_down_as(hipStream_t stream, const void *h_split, long long P,
+                           const int4 *tiles, const int32_t *num_tiles, int max_tiles, int I,
+                           int d, const uint8_t *dw, const uint8_t *ds, uint16_t *y, int af) {
   SplitArgs a{};
-  set_split(a, h_split, P, I);
+  set_split(a, h_split, P, I, af);
   a.act_index = nullptr;
   a.tiles = tiles;
   a.num_tiles = num_tiles;
@@ -902,7 +1078,14 @@ int glm_grouped_down_launch(hipStream_t stream, const void *h_split, long long P
   a.N = d;
   a.K = I;
   a.out = y;
-  return split_launch(stream, a, 1, max_tiles);
+  return split_launch(stream, a, 1, max_tiles, af);
+}
+
+int glm_grouped_down_launch(hipStream_t stream, const void *h_split, long long P,
+                            const int4 *tiles, const int32_t *num_tiles, int max_tiles, int I,
+                            int d, const uint8_t *dw, const uint8_t *ds, uint16_t *y) {
+  return grouped_down_as(stream, h_split, P, tiles, num_tiles, max_tiles, I, d, dw, ds, y,
+                         ACT_FP8X2);
 }
 
 // Dense bf16 SwiGLU MLP over T token rows (the shared expert at many tokens):
@@ -938,19 +1121,64 @@ int glm_grouped_dense_mlp_launch(hipStream_t stream, const uint16_t *x, int T, i
 
 bool glm_grouped_supported(int d, int I);
 
+static bool act_format_ok(int af) { return af == ACT_FP8X2 || af == ACT_FP6X2 || af == ACT_FP4; }
+
+extern "C" size_t glm_act_split_bytes_fmt(int rows, int K, int act_format) {
+  if (rows < 0 || K <= 0 || K % 32 != 0 || !act_format_ok(act_format)) return 0;
+  // the ACT_FP6X2 rows are stored in whole 128-element chunks
+  if (act_format == ACT_FP6X2 && K % 128 != 0) return 0;
+  return SplitLayout((long long)rows, K, act_format).total;
+}
+
 extern "C" size_t glm_act_split_bytes(int rows, int K) {
-  if (rows < 0 || K <= 0 || K % 32 != 0) return 0;
-  return glm_act_split_bytes((long long)rows, K);
+  return glm_act_split_bytes_fmt(rows, K, ACT_FP8X2);
+}
+
+extern "C" int glm_act_split(void *stream, const uint16_t *x, int rows, int K, int act_format,
+                             void *split) {
+  glm::clear_error();
+  GLM_REQUIRE(x && split, GLM_ERR_INVALID_ARGUMENT, "act_split: null pointer argument");
+  GLM_REQUIRE(act_format_ok(act_format), GLM_ERR_INVALID_ARGUMENT,
+              "act_split: unknown act_format %d", act_format);
+  GLM_REQUIRE(rows >= 0 && K > 0 && K % 32 == 0, GLM_ERR_INVALID_ARGUMENT,
+              "act_split: needs rows >= 0 and K %% 32 == 0 (rows=%d K=%d)", rows, K);
+  GLM_REQUIRE(act_format != ACT_FP6X2 || K % 128 == 0, GLM_ERR_UNSUPPORTED_SHAPE,
+              "act_split: the FP6 split needs K %% 128 == 0 (K=%d)", K);
+  GLM_REQUIRE(glm_aligned16({x, split}), GLM_ERR_INVALID_ARGUMENT,
+              "act_split: buffers must be 16-byte aligned");
+  return act_split_launch_as((hipStream_t)stream, x, rows, K, act_format, split);
 }
 
 extern "C" int glm_act_split_fp8(void *stream, const uint16_t *x, int rows, int K, void *split) {
+  return glm_act_split(stream, x, rows, K, ACT_FP8X2, split);
+}
+
+extern "C" int glm_expert_gate_up_grouped_fmt(void *stream, int act_format, const void *x_split,
+                                              int T, int d, int I, const uint8_t *gate_packed,
+                                              const uint8_t *gate_scales,
+                                              const uint8_t *up_packed, const uint8_t *up_scales,
+                                              const int32_t *pair_token, const int32_t *tiles,
+                                              const int32_t *num_tiles, int max_tiles,
+                                              float swiglu_limit, uint16_t *h) {
   glm::clear_error();
-  GLM_REQUIRE(x && split, GLM_ERR_INVALID_ARGUMENT, "act_split_fp8: null pointer argument");
-  GLM_REQUIRE(rows >= 0 && K > 0 && K % 32 == 0, GLM_ERR_INVALID_ARGUMENT,
-              "act_split_fp8: needs rows >= 0 and K %% 32 == 0 (rows=%d K=%d)", rows, K);
-  GLM_REQUIRE(glm_aligned16({x, split}), GLM_ERR_INVALID_ARGUMENT,
-              "act_split_fp8: buffers must be 16-byte aligned");
-  return glm_act_split_launch((hipStream_t)stream, x, rows, K, split);
+  GLM_REQUIRE(x_split && gate_packed && gate_scales && up_packed && up_scales && pair_token &&
+                  tiles && num_tiles && h,
+              GLM_ERR_INVALID_ARGUMENT, "expert_gate_up_grouped: null pointer argument");
+  GLM_REQUIRE(act_format_ok(act_format), GLM_ERR_INVALID_ARGUMENT,
+              "expert_gate_up_grouped: unknown act_format %d", act_format);
+  GLM_REQUIRE(max_tiles >= 0 && T >= 0, GLM_ERR_INVALID_ARGUMENT,
+              "expert_gate_up_grouped: max_tiles < 0 or T < 0");
+  GLM_REQUIRE(glm_grouped_supported(d, I), GLM_ERR_UNSUPPORTED_SHAPE,
+              "expert_gate_up_grouped: needs d %% 512 == 0 and I %% 256 == 0 (d=%d I=%d)", d, I);
+  GLM_REQUIRE(glm_aligned16({x_split, gate_packed, up_packed, tiles, h}),
+              GLM_ERR_INVALID_ARGUMENT, "expert_gate_up_grouped: buffers must be 16-byte aligned");
+  GLM_REQUIRE(glm_split_fits(T, d, act_format), GLM_ERR_UNSUPPORTED_SHAPE,
+              "expert_gate_up_grouped: the split of %d x %d activations exceeds 4 GiB", T, d);
+  if (max_tiles == 0 || T == 0) return GLM_OK;
+  return grouped_gate_up_as((hipStream_t)stream, x_split, T, pair_token,
+                            reinterpret_cast<const int4 *>(tiles), num_tiles, max_tiles, d, I,
+                            gate_packed, gate_scales, up_packed, up_scales, h, swiglu_limit,
+                            nullptr, 0, act_format);
 }
 
 extern "C" int glm_expert_gate_up_grouped(void *stream, const void *x_split, int T, int d, int I,
@@ -959,42 +1187,37 @@ extern "C" int glm_expert_gate_up_grouped(void *stream, const void *x_split, int
                                           const int32_t *pair_token, const int32_t *tiles,
                                           const int32_t *num_tiles, int max_tiles,
                                           float swiglu_limit, uint16_t *h) {
-  glm::clear_error();
-  GLM_REQUIRE(x_split && gate_packed && gate_scales && up_packed && up_scales && pair_token &&
-                  tiles && num_tiles && h,
-              GLM_ERR_INVALID_ARGUMENT, "expert_gate_up_grouped: null pointer argument");
-  GLM_REQUIRE(max_tiles >= 0 && T >= 0, GLM_ERR_INVALID_ARGUMENT,
-              "expert_gate_up_grouped: max_tiles < 0 or T < 0");
-  GLM_REQUIRE(glm_grouped_supported(d, I), GLM_ERR_UNSUPPORTED_SHAPE,
-              "expert_gate_up_grouped: needs d %% 512 == 0 and I %% 256 == 0 (d=%d I=%d)", d, I);
-  GLM_REQUIRE(glm_aligned16({x_split, gate_packed, up_packed, tiles, h}),
-              GLM_ERR_INVALID_ARGUMENT, "expert_gate_up_grouped: buffers must be 16-byte aligned");
-  GLM_REQUIRE(glm_split_fits(T, d), GLM_ERR_UNSUPPORTED_SHAPE,
-              "expert_gate_up_grouped: the split of %d x %d activations exceeds 4 GiB", T, d);
-  if (max_tiles == 0 || T == 0) return GLM_OK;
-  return glm_grouped_gate_up_launch((hipStream_t)stream, x_split, T, pair_token,
-                                    reinterpret_cast<const int4 *>(tiles), num_tiles, max_tiles,
-                                    d, I, gate_packed, gate_scales, up_packed, up_scales, h,
-                                    swiglu_limit, nullptr, 0);
+  return glm_expert_gate_up_grouped_fmt(stream, ACT_FP8X2, x_split, T, d, I, gate_packed,
+                                        gate_scales, up_packed, up_scales, pair_token, tiles,
+                                        num_tiles, max_tiles, swiglu_limit, h);
 }
 
-extern "C" int glm_expert_down_grouped(void *stream, const void *h_split, int P, int I, int d,
-                                       const uint8_t *down_packed, const uint8_t *down_scales,
-                                       const int32_t *tiles, const int32_t *num_tiles,
-                                       int max_tiles, uint16_t *y) {
+extern "C" int glm_expert_down_grouped_fmt(void *stream, int act_format, const void *h_split,
+                                           int P, int I, int d, const uint8_t *down_packed,
+                                           const uint8_t *down_scales, const int32_t *tiles,
+                                           const int32_t *num_tiles, int max_tiles, uint16_t *y) {
   glm::clear_error();
   GLM_REQUIRE(h_split && down_packed && down_scales && tiles && num_tiles && y,
               GLM_ERR_INVALID_ARGUMENT, "expert_down_grouped: null pointer argument");
+  GLM_REQUIRE(act_format_ok(act_format), GLM_ERR_INVALID_ARGUMENT,
+              "expert_down_grouped: unknown act_format %d", act_format);
   GLM_REQUIRE(max_tiles >= 0 && P >= 0, GLM_ERR_INVALID_ARGUMENT,
               "expert_down_grouped: max_tiles < 0 or P < 0");
   GLM_REQUIRE(glm_grouped_supported(d, I), GLM_ERR_UNSUPPORTED_SHAPE,
               "expert_down_grouped: needs d %% 512 == 0 and I %% 256 == 0 (d=%d I=%d)", d, I);
   GLM_REQUIRE(glm_aligned16({h_split, down_packed, tiles, y}), GLM_ERR_INVALID_ARGUMENT,
               "expert_down_grouped: buffers must be 16-byte aligned");
-  GLM_REQUIRE(glm_split_fits(P, I), GLM_ERR_UNSUPPORTED_SHAPE,
+  GLM_REQUIRE(glm_split_fits(P, I, act_format), GLM_ERR_UNSUPPORTED_SHAPE,
               "expert_down_grouped: the split of %d x %d activations exceeds 4 GiB", P, I);
   if (max_tiles == 0 || P == 0) return GLM_OK;
-  return glm_grouped_down_launch((hipStream_t)stream, h_split, P,
-                                 reinterpret_cast<const int4 *>(tiles), num_tiles, max_tiles, I,
-                                 d, down_packed, down_scales, y);
+  return grouped_down_as((hipStream_t)stream, h_split, P, reinterpret_cast<const int4 *>(tiles),
+                         num_tiles, max_tiles, I, d, down_packed, down_scales, y, act_format);
+}
+
+extern "C" int glm_expert_down_grouped(void *stream, const void *h_split, int P, int I, int d,
+                                       const uint8_t *down_packed, const uint8_t *down_scales,
+                                       const int32_t *tiles, const int32_t *num_tiles,
+                                       int max_tiles, uint16_t *y) {
+  return glm_expert_down_grouped_fmt(stream, ACT_FP8X2, h_split, P, I, d, down_packed,
+                                     down_scales, tiles, num_tiles, max_tiles, y);
 }

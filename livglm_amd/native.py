@@ -26,6 +26,10 @@ GLM_FMT_MXFP4 = 2
 GLM_MX_RULE_NEAREST = 0
 GLM_MX_RULE_OCP = 1
 
+GLM_ACT_FP8X2 = 0
+GLM_ACT_FP6X2 = 1
+GLM_ACT_FP4 = 2
+
 GLM_READ_DROP_CACHE = 1
 GLM_HC_BF16_STREAMS = 1
 GLM_NOALLOC_SCRATCH_BYTES = 64 << 20
@@ -54,6 +58,11 @@ SIGNATURES = {
     "glm_expert_gate_up_grouped": (_i, [_p, _p, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _i, _f,
                                         _p]),
     "glm_expert_down_grouped": (_i, [_p, _p, _i, _i, _i, _p, _p, _p, _p, _i, _p]),
+    "glm_act_split_bytes_fmt": (_sz, [_i, _i, _i]),
+    "glm_act_split": (_i, [_p, _p, _i, _i, _i, _p]),
+    "glm_expert_gate_up_grouped_fmt": (_i, [_p, _i, _p, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p,
+                                            _i, _f, _p]),
+    "glm_expert_down_grouped_fmt": (_i, [_p, _i, _p, _i, _i, _i, _p, _p, _p, _p, _i, _p]),
     "glm_moe_combine": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _p]),
     "glm_linear": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _p]),
     "glm_linear_f32": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _p]),

@@ -155,6 +155,29 @@ def test_prefill_entry_points_reject_bad_shapes(lib):
             1, 1, 2.5, fake, 2048, 768, fake, fake, fake, fake, 10.0, fake, fake, fake)
 
 
+def test_act_format_entry_points(lib):
+    import act_formats as A
+    fake = ctypes.c_void_p(0x1000)
+    # split sizes agree with the layout model; FP8X2 is the original split
+    for rows, K in [(1, 128), (7, 2048), (300, 768)]:
+        for fmt in (A.FP8X2, A.FP6X2, A.FP4):
+            assert lib.glm_act_split_bytes_fmt(rows, K, fmt) == A.split_bytes(rows, K, fmt)
+        assert lib.glm_act_split_bytes_fmt(rows, K, 0) == lib.glm_act_split_bytes(rows, K)
+    assert lib.glm_act_split_bytes_fmt(4, 96, native.GLM_ACT_FP6X2) == 0  # K % 128
+    assert lib.glm_act_split_bytes_fmt(4, 96, native.GLM_ACT_FP4) > 0
+    assert lib.glm_act_split_bytes_fmt(4, 128, 3) == 0
+    msg = _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_act_split", None, fake, 4, 128, 7, fake)
+    assert "act_format" in msg
+    _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_act_split", None, fake, 4, 96,
+            native.GLM_ACT_FP6X2, fake)
+    assert lib.glm_act_split(None, fake, 0, 128, native.GLM_ACT_FP4, fake) == native.GLM_OK
+    msg = _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_expert_gate_up_grouped_fmt", None, -1,
+                  fake, 8, 1024, 512, fake, fake, fake, fake, fake, fake, fake, 16, 10.0, fake)
+    assert "act_format" in msg
+    _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_expert_down_grouped_fmt", None,
+            native.GLM_ACT_FP6X2, fake, 64, 256, 768, fake, fake, fake, fake, 16, fake)
+
+
 def test_ffn_site_and_loader_entry_points_reject_bad_arguments(lib):
     fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
     assert lib.glm_hc_workspace_bytes(2, 4, 2048) == 32 * 2 * 25 * 4
