@@ -90,7 +90,10 @@ def parse_args():
     ap.add_argument("--load-threads", type=int, default=16,
                     help="bank_load: native read threads")
     ap.add_argument("--scalex", type=int, default=0,
-                    help="bank_load: 1 = ScaleX layer shards (coded scales, decoded on the GPU)")
+                    help="bank_load: 1 = ScaleX layer shards (coded scales, decoded on the GPU); "
+                         "few-token workloads (T <= 4): 1 = the routed scales kept ScaleX "
+                         "Mode-B coded in HBM with the checkpoint's statistics and decoded "
+                         "inside the kernels (glm_moe_forward_scalex)")
     # internal: the child runs of the counter passes
     ap.add_argument("--mode", default="full", choices=["full", "kernel", "copy"],
                     help=argparse.SUPPRESS)
@@ -172,6 +175,9 @@ class Setup:
                             b["linear.codes"].data_ptr(), b["linear.scales"].data_ptr())
                 del w
             self.banks.append(b)
+        self.scalex = None
+        if getattr(args, "scalex", 0) and T <= 4 and self.layers == 1 and not hc:
+            self.scalex = self._code_scales(args, np)
         self.trace = None
         if shape.routing == "markov":
             # per (step, layer) bias rows that keep each expert of the previous
@@ -194,6 +200,36 @@ class Setup:
         self.grouped = T > 64
         self.act_format = {"fp8x2": native.GLM_ACT_FP8X2, "fp6x2": native.GLM_ACT_FP6X2,
                            "fp4": native.GLM_ACT_FP4}[getattr(args, "act_format", "fp8x2")]
+
+    def _code_scales(self, args, np) -> dict:
+        """Replaces every bank's routed scales by ones with the real
+        checkpoint's statistics and adds their ScaleX Mode-B rows
+        (bank["scalex.rows"], one stride); returns the byte counts."""
+        from glm53flash.scale_codec import mode_b_bank
+        from livglm_amd.workloads import concentrated_scales
+        torch, E, d, I = self.torch, self.E, self.d, self.I
+        rng = np.random.default_rng(args.seed + 17)
+        coded = stride = 0
+        for b in self.banks:
+            g = concentrated_scales(rng, (E, I, d // 32))
+            dn = concentrated_scales(rng, (E, d, I // 32))
+            u = concentrated_scales(rng, (E, I, d // 32))
+            rows, st, c = mode_b_bank(g, dn, u)
+            stride = max(stride, st)
+            coded += c
+            b["gate_proj.weight_scale"] = torch.from_numpy(g).to(self.dev)
+            b["down_proj.weight_scale"] = torch.from_numpy(dn).to(self.dev)
+            b["up_proj.weight_scale"] = torch.from_numpy(u).to(self.dev)
+            b["scalex.rows"] = torch.from_numpy(rows).to(self.dev)
+        for b in self.banks:  # one stride for every bank
+            if b["scalex.rows"].shape[1] < stride:
+                pad = torch.zeros((E, stride), dtype=torch.uint8, device=self.dev)
+                pad[:, :b["scalex.rows"].shape[1]] = b["scalex.rows"]
+                b["scalex.rows"] = pad
+        raw = 3 * I * (d // 32)
+        return {"stride": stride, "coded_bytes_per_expert": coded / len(self.banks) / E,
+                "raw_scale_bytes_per_expert": raw,
+                "expert_bytes_decoded": 3 * I * d // 2 + raw}
 
     def bias(self, step: int, layer: int):
         """The router bias of one layer at one step."""
@@ -322,6 +358,18 @@ def measure(args, torch, np, workload: str, *, steps: int, warmup: int, traffic:
 
     def moe(x, layer: int, step: int) -> None:
         b = S.banks[layer]
+        if S.scalex is not None:
+            native.call(
+                "glm_moe_forward_scalex", S.stream, x.data_ptr(), T, d,
+                b["router_weight"].data_ptr(), S.bias(step, layer).data_ptr(), E, k,
+                shape.n_group, shape.topk_group, int(shape.norm_topk_prob),
+                shape.routed_scaling_factor, I, b["gate_proj.weight_packed"].data_ptr(),
+                b["up_proj.weight_packed"].data_ptr(), b["down_proj.weight_packed"].data_ptr(),
+                b["scalex.rows"].data_ptr(), S.scalex["stride"], Is, native.GLM_FMT_BF16,
+                b["shared.gate"].data_ptr(), None, b["shared.up"].data_ptr(), None,
+                b["shared.down"].data_ptr(), None, None, shape.swiglu_limit, ws.data_ptr(),
+                ws_bytes, out.data_ptr(), wts.data_ptr(), idx.data_ptr())
+            return
         native.call(
             "glm_moe_forward", S.stream, x.data_ptr(), T, d, b["router_weight"].data_ptr(),
             S.bias(step, layer).data_ptr(), E, k, shape.n_group, shape.topk_group,
@@ -470,6 +518,22 @@ def measure(args, torch, np, workload: str, *, steps: int, warmup: int, traffic:
         u = sum(unique_per_step) / len(unique_per_step)
         res["unique_experts_per_step"] = u
         res["layer_expert_gbps"] = u * shape.expert_bytes / (ms_per_step / 1e3) / 1e9
+        if S.scalex is not None:
+            # the same experts with their scales read as ScaleX Mode-B rows:
+            # a step moves each selected expert's codes and its coded row
+            sx = S.scalex
+            coded_expert = sx["expert_bytes_decoded"] - sx["raw_scale_bytes_per_expert"] + \
+                sx["coded_bytes_per_expert"]
+            res["scalex"] = {
+                "mode": "ScaleX Mode-B rows decoded inside select_gate_up / down_combine",
+                "row_stride": sx["stride"],
+                "coded_scale_bytes_per_expert": round(sx["coded_bytes_per_expert"]),
+                "raw_scale_bytes_per_expert": sx["raw_scale_bytes_per_expert"],
+                "expert_bytes_coded": round(coded_expert),
+                "expert_bytes_decoded": sx["expert_bytes_decoded"],
+                "expert_bytes_saved_frac": round(1 - coded_expert / sx["expert_bytes_decoded"], 4),
+                "coded_expert_gbps": round(u * coded_expert / (ms_per_step / 1e3) / 1e9, 1),
+            }
     if S.layers > 1:
         # bytes one decode step reads: every layer's k experts (Markov
         # routing at T=1 picks k distinct ones), shared expert, linear, router
@@ -590,6 +654,8 @@ def main() -> int:
         },
         "roofline": r["roofline"],
     }
+    if "scalex" in r:
+        line["scalex"] = r["scalex"]
     if "layer_expert_gbps" in r:
         # selected-expert bytes over the layer step's whole device time
         line["decode_expert_hbm_gbps"] = round(r["layer_expert_gbps"], 1)

@@ -372,6 +372,38 @@ int glm_moe_forward_noalloc(void *stream, const uint16_t *x, int T, int d,
                             const uint16_t *shared_in, float swiglu_limit, float *out,
                             float *weights_out, uint32_t *indices_out);
 
+/*
+ * glm_moe_forward with the routed experts' E8M0 scales kept ScaleX Mode-B
+ * coded in HBM (docs/scalex-mode-b.md:24-33; the reference's ScaleX QMV,
+ * native_expert_ssd.py:653-694): scalex_rows + e * scalex_stride holds expert
+ * e's Mode-B row (encode_mode_b_row, scale_codec.py:150-154: the Mode-A
+ * record of its gate | down | up scale bytes and the u16 tile directory) with
+ * the directory in front: the (raw + 511) / 512 + 1 u16 entries zero-padded
+ * to a multiple of 16 bytes, then the record (24-byte header, primary codes,
+ * exception positions and values).  The few-token kernels decode the scale rows of their
+ * tiles into LDS while the weights stream (the reference decodes 512-scale
+ * tiles into threadgroup memory inside its QMV); the outputs are
+ * bit-identical to glm_moe_forward on the decoded scales.  The gate/up/down
+ * scale pointers of glm_moe_forward are replaced by scalex_rows/stride; the
+ * other arguments are the same.  Limits: the few-token path (T <= 4,
+ * top_k <= 8, d / 512 in {2, 4, 6, 8}, I / 128 in {1, 2, 4, 6, 8, 16});
+ * rows 256-byte aligned, stride a positive multiple of 256.  The rows must be
+ * valid Mode-B rows (the host codec validates them; the kernels trust the
+ * header, the directory and the exception order).
+ */
+int glm_moe_forward_scalex(void *stream, const uint16_t *x, int T, int d,
+                           const float *router_weight, const float *router_bias, int E, int top_k,
+                           int n_group, int topk_group, int norm_topk_prob,
+                           float routed_scaling_factor, int I, const uint8_t *gate_packed,
+                           const uint8_t *up_packed, const uint8_t *down_packed,
+                           const uint8_t *scalex_rows, int64_t scalex_stride, int I_shared,
+                           int shared_fmt, const void *shared_gate,
+                           const uint8_t *shared_gate_scales, const void *shared_up,
+                           const uint8_t *shared_up_scales, const void *shared_down,
+                           const uint8_t *shared_down_scales, const uint16_t *shared_in,
+                           float swiglu_limit, void *workspace, size_t workspace_bytes, float *out,
+                           float *weights_out, uint32_t *indices_out);
+
 /* ------------------------------------------------------------ decoder FFN site */
 
 /* glm_hc_pre / glm_hc_post flag: the streams are bf16 in the model (passed

@@ -156,6 +156,39 @@ __device__ __forceinline__ void load_wave_weights(WaveWeights<FMT, NPROJ, CPW> &
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// load_wave_weights without the scale dwords: the caller fills ww.sd (for
+// example from scales decoded into LDS with wave_scales_from_lds).
+template <int FMT, int NPROJ, int CPW>
+__device__ __forceinline__ void load_wave_chunks(WaveWeights<FMT, NPROJ, CPW> &ww,
+                                                 const uint8_t *const wrow[NPROJ], int kbase,
+                                                 int q) {
+#pragma unroll
+  for (int c = 0; c < CPW; ++c)
+#pragma unroll
+    for (int p = 0; p < NPROJ; ++p)
+      ww.w[p][c] = load_chunk_at<FMT>(wrow[p], kbase + chunk_k<FMT, CPW>(c, q));
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// ww.sd from each projection's row of scale bytes in LDS (4-byte aligned):
+// the dwords load_wave_weights reads from global memory.
+template <int FMT, int NPROJ, int CPW>
+__device__ __forceinline__ void wave_scales_from_lds(WaveWeights<FMT, NPROJ, CPW> &ww,
+                                                     const uint8_t *const s_row[NPROJ],
+                                                     int kbase, int q) {
+#pragma unroll
+  for (int p = 0; p < NPROJ; ++p) {
+    const uint32_t *s = reinterpret_cast<const uint32_t *>(s_row[p] + (kbase >> 5));
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      if constexpr (paired_chunks<FMT, CPW>())
+        ww.sd[p][c] = s[(c >> 1) * 2 + (q >> 1)];
+      else
+        ww.sd[p][c] = s[c];
+    }
+  }
+}
+
 // B fragments of this lane's 32 activations starting at K = kl.
 // Activation fragments of one lane column.  `act` must point at a valid row:
 // a padding column reads any valid row instead of branching (an MFMA output

@@ -30,6 +30,7 @@
 // Every kernel boundary is a stream-ordered dependency; nothing synchronises
 // across blocks inside a kernel, and every reduction runs in one fixed order.
 #include "mfma_tile.h"
+#include "scalex_tile.h"
 #include "topk_select.h"
 
 int glm_router_select_launch(hipStream_t stream, const float *logits, const float *bias, int T,
@@ -527,6 +528,10 @@ struct PairArgs {
   float limit;
   int routed_blocks;
   int tpb;  // 16-row tiles of one pair per routed block (consecutive)
+  // ScaleX Mode-B scale rows (SX kernels; gs and us unused): expert e's row
+  // at sx + e * sx_stride
+  const uint8_t *sx;
+  long long sx_stride;
 };
 
 // LDS bytes of select_gate_up_kernel: the token row, then each of the four
@@ -536,7 +541,13 @@ __host__ __device__ constexpr size_t pair_gate_up_lds_bytes(int d, int EPL) {
   return (size_t)lds_row_stride(d) * 2 + (size_t)4 * (64 * EPL + 256 + 64) * 4;
 }
 
-template <int EPL, int CPW, int CPW_S>
+// LDS bytes of the decoded scale rows of an SX select_gate_up block: the
+// gate and the up rows of its tiles.
+__host__ __device__ constexpr size_t pair_gate_up_sx_bytes(int d, int tpb) {
+  return (size_t)2 * 16 * tpb * (d / 32);
+}
+
+template <int EPL, int CPW, int CPW_S, bool SX>
 __global__ __launch_bounds__(256) void select_gate_up_kernel(PairArgs a, SharedArgs sh) {
   extern __shared__ __attribute__((aligned(16))) uint16_t s_dyn[];
   __shared__ glm_f32x4 red[3 * 2 * 64];
@@ -578,11 +589,28 @@ __global__ __launch_bounds__(256) void select_gate_up_kernel(PairArgs a, SharedA
   const uint8_t *gw = a.gw + e * a.w_stride, *uw = a.uw + e * a.w_stride;
   const uint8_t *gs = a.gs + e * a.s_stride, *us = a.us + e * a.s_stride;
   WaveWeights<FMT_MXFP4, 2, CPW> ww;
+  // SX: the gate and the up scale rows of the block's tiles, decoded from the
+  // expert's Mode-B row into LDS by the whole block while the first tile's
+  // weights are in flight (gate scales at 16 r' G, up at (16 tpb + 16 r') G)
+  const int G = d / 32, nsx = 16 * a.tpb;
+  uint8_t *s_sc = reinterpret_cast<uint8_t *>(s_dyn) + pair_gate_up_lds_bytes(d, EPL);
   {
     const int row = tile0 * 16 + r;
     const uint8_t *wrow[2] = {gw + (size_t)row * (d / 2), uw + (size_t)row * (d / 2)};
-    const uint8_t *srow[2] = {gs + (size_t)row * (d / 32), us + (size_t)row * (d / 32)};
-    load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
+    if constexpr (SX) {
+      load_wave_chunks<FMT_MXFP4, 2, CPW>(ww, wrow, kbase, q);
+      const ScalexRow hx = scalex_row(a.sx + e * a.sx_stride, scalex_dir_bytes(3 * a.I * (a.d / 32)));
+      const uint32_t s0[2] = {(uint32_t)(tile0 * 16 * G), (uint32_t)((2 * a.I + tile0 * 16) * G)};
+      uint8_t *const dst[2] = {s_sc, s_sc + nsx * G};
+      scalex_decode<2>(hx, s0, (uint32_t)(nsx * G), dst, (int)threadIdx.x, 256,
+                       [] { __syncthreads(); });
+      __syncthreads();
+      const uint8_t *srow[2] = {s_sc + r * G, s_sc + (nsx + r) * G};
+      wave_scales_from_lds<FMT_MXFP4, 2, CPW>(ww, srow, kbase, q);
+    } else {
+      const uint8_t *srow[2] = {gs + (size_t)row * (d / 32), us + (size_t)row * (d / 32)};
+      load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
+    }
   }
   for (int ti = 0; ti < a.tpb; ++ti) {
     const int row0 = (tile0 + ti) * 16;
@@ -591,8 +619,15 @@ __global__ __launch_bounds__(256) void select_gate_up_kernel(PairArgs a, SharedA
     if (ti + 1 < a.tpb) {
       const int row = row0 + 16 + r;
       const uint8_t *wrow[2] = {gw + (size_t)row * (d / 2), uw + (size_t)row * (d / 2)};
-      const uint8_t *srow[2] = {gs + (size_t)row * (d / 32), us + (size_t)row * (d / 32)};
-      load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
+      if constexpr (SX) {
+        load_wave_chunks<FMT_MXFP4, 2, CPW>(ww, wrow, kbase, q);
+        const int rr = (ti + 1) * 16 + r;
+        const uint8_t *srow[2] = {s_sc + rr * G, s_sc + (nsx + rr) * G};
+        wave_scales_from_lds<FMT_MXFP4, 2, CPW>(ww, srow, kbase, q);
+      } else {
+        const uint8_t *srow[2] = {gs + (size_t)row * (d / 32), us + (size_t)row * (d / 32)};
+        load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
+      }
     }
     if (ksplit_reduce<2>(acc, red, wave, 4, lane) && r == 0) {
       uint32_t o[4];
@@ -633,6 +668,9 @@ struct PairDownArgs {
   float *hc_out;                            // [T][hc][d]
   int hc, hc_bf16;                          // hc_bf16: bf16 streams (GLM_HC_BF16_STREAMS)
   int tpb;  // 16-row tiles of d per block (consecutive)
+  // ScaleX Mode-B scale rows (SX kernels; ds unused)
+  const uint8_t *sx;
+  long long sx_stride;
 };
 
 constexpr int kPairMaxHc = 8;
@@ -641,7 +679,7 @@ constexpr int kPairMaxHc = 8;
 // the combine's order: out = sum_j f32(bf16(y_j)) * w_j (sequential j, no
 // contraction) + shared, where shared = bf16 of its partial sums added in
 // order.  Wave j (of max(k, 4)) owns expert j over the full K = I.
-template <int CPW_R>
+template <int CPW_R, bool SX>
 __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ __attribute__((aligned(16))) uint16_t s_h[];  // [k][lds_row_stride(I)]
@@ -674,11 +712,29 @@ __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
   }
   const uint8_t *dw = a.dw + e * a.w_stride, *ds = a.ds + e * a.s_stride;
   WaveWeights<FMT_MXFP4, 1, CPW_R> ww;
+  // SX: wave j decodes the down scale rows of its expert for the block's
+  // tiles into its own LDS area (after h), while the first tile's weights
+  // are in flight
+  const int Gi = I / 32, nsx = 16 * a.tpb;
+  uint8_t *s_sc = reinterpret_cast<uint8_t *>(s_h) + (size_t)k * lds_row_stride(I) * 2 +
+                  (size_t)j * nsx * Gi;
   if (j < k) {
     const int row = tile0 * 16 + r;
     const uint8_t *wrow[1] = {dw + (size_t)row * (I / 2)};
-    const uint8_t *srow[1] = {ds + (size_t)row * (I / 32)};
-    load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
+    if constexpr (SX) {
+      load_wave_chunks<FMT_MXFP4, 1, CPW_R>(ww, wrow, 0, q);
+      const ScalexRow hx = scalex_row(a.sx + e * a.sx_stride, scalex_dir_bytes(3 * a.I * (a.d / 32)));
+      // the down scales follow the gate's I x d/32 in the expert's stream
+      const uint32_t s0[1] = {(uint32_t)(I * (d / 32) + tile0 * 16 * Gi)};
+      uint8_t *const dst[1] = {s_sc};
+      scalex_decode<1>(hx, s0, (uint32_t)(nsx * Gi), dst, lane, 64, [] { wave_lds_sync(); });
+      wave_lds_sync();
+      const uint8_t *srow[1] = {s_sc + r * Gi};
+      wave_scales_from_lds<FMT_MXFP4, 1, CPW_R>(ww, srow, 0, q);
+    } else {
+      const uint8_t *srow[1] = {ds + (size_t)row * (I / 32)};
+      load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
+    }
   }
 #pragma unroll
   for (int u = 0; u < kHP; ++u) {
@@ -726,8 +782,14 @@ __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
       if (ti + 1 < a.tpb) {
         const int row = row0 + 16 + r;
         const uint8_t *wrow[1] = {dw + (size_t)row * (I / 2)};
-        const uint8_t *srow[1] = {ds + (size_t)row * (I / 32)};
-        load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
+        if constexpr (SX) {
+          load_wave_chunks<FMT_MXFP4, 1, CPW_R>(ww, wrow, 0, q);
+          const uint8_t *srow[1] = {s_sc + ((ti + 1) * 16 + r) * Gi};
+          wave_scales_from_lds<FMT_MXFP4, 1, CPW_R>(ww, srow, 0, q);
+        } else {
+          const uint8_t *srow[1] = {ds + (size_t)row * (I / 32)};
+          load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
+        }
       }
       if (r == 0) {
 #pragma unroll
@@ -987,14 +1049,23 @@ static int launch_select_gate_up(hipStream_t stream, const PairArgs &a, const Sh
                                  int cs) {
   const int d = a.d, E = a.E, T = a.T;
   const int epl = E <= 128 ? 2 : (E <= 256 ? 4 : 8);
-  const size_t lds2 = std::max(pair_gate_up_lds_bytes(d, epl), (size_t)T * cs * 128 * 2);
+  const bool sx = a.sx != nullptr;
+  const size_t lds2 =
+      std::max(pair_gate_up_lds_bytes(d, epl) + (sx ? pair_gate_up_sx_bytes(d, a.tpb) : 0),
+               (size_t)T * cs * 128 * 2);
   const dim3 g2(a.routed_blocks + sh.dn_blocks);
-#define GLM_PAIR_GU(EP, CS)                                                                    \
+#define GLM_PAIR_GU_D(EP, CS, SX)                                                              \
   switch (d / 512) {                                                                           \
-    case 2: hipLaunchKernelGGL((select_gate_up_kernel<EP, 2, CS>), g2, dim3(256), lds2, stream, a, sh); break; \
-    case 4: hipLaunchKernelGGL((select_gate_up_kernel<EP, 4, CS>), g2, dim3(256), lds2, stream, a, sh); break; \
-    case 6: hipLaunchKernelGGL((select_gate_up_kernel<EP, 6, CS>), g2, dim3(256), lds2, stream, a, sh); break; \
-    default: hipLaunchKernelGGL((select_gate_up_kernel<EP, 8, CS>), g2, dim3(256), lds2, stream, a, sh); break; \
+    case 2: hipLaunchKernelGGL((select_gate_up_kernel<EP, 2, CS, SX>), g2, dim3(256), lds2, stream, a, sh); break; \
+    case 4: hipLaunchKernelGGL((select_gate_up_kernel<EP, 4, CS, SX>), g2, dim3(256), lds2, stream, a, sh); break; \
+    case 6: hipLaunchKernelGGL((select_gate_up_kernel<EP, 6, CS, SX>), g2, dim3(256), lds2, stream, a, sh); break; \
+    default: hipLaunchKernelGGL((select_gate_up_kernel<EP, 8, CS, SX>), g2, dim3(256), lds2, stream, a, sh); break; \
+  }
+#define GLM_PAIR_GU(EP, CS)       \
+  if (sx) {                       \
+    GLM_PAIR_GU_D(EP, CS, true)   \
+  } else {                        \
+    GLM_PAIR_GU_D(EP, CS, false)  \
   }
 #define GLM_PAIR_GU_CS(EP) \
   if (cs == 1) {           \
@@ -1011,6 +1082,7 @@ static int launch_select_gate_up(hipStream_t stream, const PairArgs &a, const Sh
   }
 #undef GLM_PAIR_GU_CS
 #undef GLM_PAIR_GU
+#undef GLM_PAIR_GU_D
   GLM_LAUNCH_CHECK("select_gate_up_kernel");
   return GLM_OK;
 }
@@ -1032,7 +1104,7 @@ int glm_pair_path_launch(hipStream_t stream, const uint16_t *x, int T, int d, co
                          const uint16_t *sg, const uint16_t *su, const uint16_t *sd, int Is,
                          float *gp, float *up, uint16_t *hs, float *yp,
                          const uint16_t *shared_ready, uint16_t *h, float limit, float *out,
-                         const glm::HcFuse *hc) {
+                         const glm::HcFuse *hc, const uint8_t *sx, long long sx_stride) {
   RouteArgs ra{};
   ra.x = x;
   ra.w = w;
@@ -1070,6 +1142,8 @@ int glm_pair_path_launch(hipStream_t stream, const uint16_t *x, int T, int d, co
   a.limit = glm_limit_bf16(limit);
   a.tpb = pair_tiles_per_block(T * k, I);
   a.routed_blocks = T * k * (I / 16) / a.tpb;
+  a.sx = sx;
+  a.sx_stride = sx_stride;
   rc = launch_select_gate_up(stream, a, sh, sg ? glm_decode_shared_cpws(Is) : 1);
   if (rc) return rc;
 
@@ -1101,16 +1175,27 @@ int glm_pair_path_launch(hipStream_t stream, const uint16_t *x, int T, int d, co
   // geometry (d 4096) two, so the token's h rows and route load once per two tiles
   b.tpb = 1;
   while (b.tpb < 4 && T * (d / 16) / (2 * b.tpb) >= 256 && (d / 16) % (2 * b.tpb) == 0) b.tpb *= 2;
-  const size_t lds3 = (size_t)k * lds_row_stride(I) * 2;
+  b.sx = sx;
+  b.sx_stride = sx_stride;
+  // h rows, then (SX) every wave's decoded down scale rows
+  const size_t lds3 = (size_t)k * lds_row_stride(I) * 2 +
+                      (sx ? (size_t)k * 16 * b.tpb * (I / 32) : 0);
   const dim3 g3(T * (d / 16) / b.tpb), b3(64 * std::max(k, 4));
-  switch (I / 128) {
-    case 1: hipLaunchKernelGGL((down_combine_kernel<1>), g3, b3, lds3, stream, b); break;
-    case 2: hipLaunchKernelGGL((down_combine_kernel<2>), g3, b3, lds3, stream, b); break;
-    case 4: hipLaunchKernelGGL((down_combine_kernel<4>), g3, b3, lds3, stream, b); break;
-    case 6: hipLaunchKernelGGL((down_combine_kernel<6>), g3, b3, lds3, stream, b); break;
-    case 8: hipLaunchKernelGGL((down_combine_kernel<8>), g3, b3, lds3, stream, b); break;
-    default: hipLaunchKernelGGL((down_combine_kernel<16>), g3, b3, lds3, stream, b); break;
+#define GLM_PAIR_DN(SX)                                                                      \
+  switch (I / 128) {                                                                         \
+    case 1: hipLaunchKernelGGL((down_combine_kernel<1, SX>), g3, b3, lds3, stream, b); break; \
+    case 2: hipLaunchKernelGGL((down_combine_kernel<2, SX>), g3, b3, lds3, stream, b); break; \
+    case 4: hipLaunchKernelGGL((down_combine_kernel<4, SX>), g3, b3, lds3, stream, b); break; \
+    case 6: hipLaunchKernelGGL((down_combine_kernel<6, SX>), g3, b3, lds3, stream, b); break; \
+    case 8: hipLaunchKernelGGL((down_combine_kernel<8, SX>), g3, b3, lds3, stream, b); break; \
+    default: hipLaunchKernelGGL((down_combine_kernel<16, SX>), g3, b3, lds3, stream, b); break; \
   }
+  if (sx) {
+    GLM_PAIR_DN(true)
+  } else {
+    GLM_PAIR_DN(false)
+  }
+#undef GLM_PAIR_DN
   GLM_LAUNCH_CHECK("down_combine_kernel");
   return GLM_OK;
 }

@@ -80,7 +80,7 @@ int glm_pair_path_launch(hipStream_t stream, const uint16_t *x, int T, int d, co
                          const uint16_t *sg, const uint16_t *su, const uint16_t *sd, int Is,
                          float *gp, float *up, uint16_t *hs, float *yp,
                          const uint16_t *shared_ready, uint16_t *h, float limit, float *out,
-                         const glm::HcFuse *hc);
+                         const glm::HcFuse *hc, const uint8_t *sx, long long sx_stride);
 int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d, const float *w,
                             const float *bias, int E, int k, int n_group, int topk_group,
                             int norm, float scale, float *logits, float *weights,
@@ -259,7 +259,8 @@ static int moe_forward_core(void *stream_v, const uint16_t *x, int T, int d,
                             const uint16_t *shared_in, float swiglu_limit, void *workspace,
                             size_t workspace_bytes, float *out, float *weights_out,
                             uint32_t *indices_out, const glm::HcFuse *hc, bool *hc_done,
-                            bool noalloc);
+                            bool noalloc, const uint8_t *sx_rows = nullptr,
+                            long long sx_stride = 0);
 
 extern "C" int glm_moe_forward(void *stream_v, const uint16_t *x, int T, int d,
                                const float *router_weight, const float *router_bias, int E,
@@ -303,6 +304,40 @@ extern "C" int glm_moe_forward_noalloc(
                           shared_up_scales, shared_down, shared_down_scales, shared_in,
                           swiglu_limit, nullptr, 0, out, weights_out, indices_out, nullptr, &done,
                           true);
+}
+
+extern "C" int glm_moe_forward_scalex(
+    void *stream_v, const uint16_t *x, int T, int d, const float *router_weight,
+    const float *router_bias, int E, int top_k, int n_group, int topk_group, int norm_topk_prob,
+    float routed_scaling_factor, int I, const uint8_t *gate_packed, const uint8_t *up_packed,
+    const uint8_t *down_packed, const uint8_t *scalex_rows, int64_t scalex_stride, int I_shared,
+    int shared_fmt, const void *shared_gate, const uint8_t *shared_gate_scales,
+    const void *shared_up, const uint8_t *shared_up_scales, const void *shared_down,
+    const uint8_t *shared_down_scales, const uint16_t *shared_in, float swiglu_limit,
+    void *workspace, size_t workspace_bytes, float *out, float *weights_out,
+    uint32_t *indices_out) {
+  glm::clear_error();
+  GLM_REQUIRE(scalex_rows != nullptr, GLM_ERR_INVALID_ARGUMENT,
+              "moe_forward_scalex: null scalex_rows");
+  GLM_REQUIRE(scalex_stride > 0 && scalex_stride % 256 == 0 &&
+                  ((uintptr_t)scalex_rows & 255u) == 0,
+              GLM_ERR_INVALID_ARGUMENT,
+              "moe_forward_scalex: the rows must be 256-byte aligned with a stride that is a "
+              "positive multiple of 256 (stride %lld)",
+              (long long)scalex_stride);
+  GLM_REQUIRE(d % 128 == 0 && I % 128 == 0, GLM_ERR_UNSUPPORTED_SHAPE,
+              "moe_forward_scalex: d=%d and I=%d must be multiples of 128", d, I);
+  GLM_REQUIRE((long long)3 * I * (d / 32) < (1LL << 31), GLM_ERR_UNSUPPORTED_SHAPE,
+              "moe_forward_scalex: %lld scales per expert exceed 2^31",
+              (long long)3 * I * (d / 32));
+  bool done = false;
+  return moe_forward_core(stream_v, x, T, d, router_weight, router_bias, E, top_k, n_group,
+                          topk_group, norm_topk_prob, routed_scaling_factor, I, gate_packed,
+                          nullptr, up_packed, nullptr, down_packed, nullptr, I_shared, shared_fmt,
+                          shared_gate, shared_gate_scales, shared_up, shared_up_scales,
+                          shared_down, shared_down_scales, shared_in, swiglu_limit, workspace,
+                          workspace_bytes, out, weights_out, indices_out, nullptr, &done, false,
+                          scalex_rows, scalex_stride);
 }
 
 extern "C" int glm_moe_forward_hc(void *stream_v, const uint16_t *x, int T, int d,
@@ -355,10 +390,11 @@ static int moe_forward_core(void *stream_v, const uint16_t *x, int T, int d,
                             const uint16_t *shared_in, float swiglu_limit, void *workspace,
                             size_t workspace_bytes, float *out, float *weights_out,
                             uint32_t *indices_out, const glm::HcFuse *hc, bool *hc_done,
-                            bool noalloc) {
+                            bool noalloc, const uint8_t *sx_rows, long long sx_stride) {
   hipStream_t stream = (hipStream_t)stream_v;
-  GLM_REQUIRE(x && router_weight && router_bias && gate_packed && gate_scales && up_packed &&
-                  up_scales && down_packed && down_scales && (workspace || noalloc) && out,
+  GLM_REQUIRE(x && router_weight && router_bias && gate_packed && up_packed && down_packed &&
+                  (sx_rows || (gate_scales && up_scales && down_scales)) &&
+                  (workspace || noalloc) && out,
               GLM_ERR_INVALID_ARGUMENT, "moe_forward: null pointer argument");
   GLM_REQUIRE(T >= 0 && d > 0 && E > 0 && top_k > 0 && I > 0, GLM_ERR_INVALID_ARGUMENT,
               "moe_forward: invalid sizes T=%d d=%d E=%d k=%d I=%d", T, d, E, top_k, I);
@@ -408,6 +444,12 @@ static int moe_forward_core(void *stream_v, const uint16_t *x, int T, int d,
   const bool shared_bf16 = has_shared && shared_fmt == GLM_FMT_BF16;
   const uint16_t *shared_ready = shared_in;  // caller-computed shared output, if any
   const bool fuse_shared = shared_bf16 && !shared_in;
+  GLM_REQUIRE(!sx_rows || glm_pair_path_supported(T, d, E, top_k, I, fuse_shared ? Is : 0),
+              GLM_ERR_UNSUPPORTED_SHAPE,
+              "moe_forward_scalex: coded scales are decoded by the few-token kernels, which take "
+              "T <= 4, top_k <= 8, d / 512 in {2, 4, 6, 8} and I / 128 in {1, 2, 4, 6, 8, 16} "
+              "(T=%d d=%d k=%d I=%d)",
+              T, d, top_k, I);
   if (glm_pair_path_supported(T, d, E, top_k, I, fuse_shared ? Is : 0)) {
     // a few tokens: three token-major kernels, no dispatch
     if (has_shared && !shared_in && !shared_bf16) {
@@ -424,7 +466,7 @@ static int moe_forward_core(void *stream_v, const uint16_t *x, int T, int d,
         fuse_shared ? (const uint16_t *)shared_gate : nullptr,
         fuse_shared ? (const uint16_t *)shared_up : nullptr,
         fuse_shared ? (const uint16_t *)shared_down : nullptr, Is, w.gp, w.up, w.shared_h, w.yp,
-        shared_ready, w.h, swiglu_limit, out, hc);
+        shared_ready, w.h, swiglu_limit, out, hc, sx_rows, sx_stride);
     *hc_done = hc != nullptr;  // fused into the down + combine kernel
     return rc;
   }

@@ -75,6 +75,9 @@ SIGNATURES = {
     "glm_moe_forward": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _i, _f, _i,
                              _p, _p, _p, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p, _p, _p,
                              _f, _p, _sz, _p, _p, _p]),
+    "glm_moe_forward_scalex": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _i, _f, _i,
+                                    _p, _p, _p, _p, _i64, _i, _i, _p, _p, _p, _p, _p, _p,
+                                    _p, _f, _p, _sz, _p, _p, _p]),
     "glm_moe_forward_noalloc": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _i, _i, _i, _f, _i,
                                      _p, _p, _p, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p, _p,
                                      _p, _f, _p, _p, _p]),

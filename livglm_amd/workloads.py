@@ -106,6 +106,25 @@ def markov_bias_trace(E: int, k: int, layers: int, steps: int, rng: np.random.Ge
     return out
 
 
+def concentrated_scales(rng: np.random.Generator, shape, kind: str = "one_bit") -> np.ndarray:
+    """E8M0 scale bytes with the statistics of the real checkpoint's experts
+    (docs/scalex-mode-b.md:36-50: 12,067 of 12,096 experts code at one bit
+    with exceptions, 16.9 % of the raw bytes): two dominant exponents and
+    ~1 % others ("one_bit"); four dominant values ("two_bit"); or uniform
+    over 119..127 ("raw", which the codec stores as it is)."""
+    n = int(np.prod(shape))
+    if kind == "raw":
+        return rng.integers(SCALE_LO, SCALE_HI + 1, n, dtype=np.uint8).reshape(shape)
+    if kind == "one_bit":
+        v = np.where(rng.random(n) < 0.56, 121, 122).astype(np.uint8)
+        other = rng.random(n) < 0.01
+    else:
+        v = rng.choice(np.array([120, 121, 122, 123], np.uint8), n, p=[0.2, 0.35, 0.3, 0.15])
+        other = rng.random(n) < 0.002
+    v[other] = rng.integers(110, 128, int(other.sum()), dtype=np.uint8)
+    return v.reshape(shape)
+
+
 def make_layer(shape: MoEShape, seed: int, *, T: int | None = None) -> dict[str, np.ndarray]:
     """One layer's inputs and weights as numpy arrays (bf16 as uint16 bits)."""
     rng = np.random.default_rng(seed)

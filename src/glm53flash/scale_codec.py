@@ -165,3 +165,56 @@ def mode_b_indexed_nbytes(encoded_bytes: int, raw_bytes: int) -> int:
 def encode_mode_b_row(encoded: bytes) -> bytes:
     """A Mode-A record padded to even length plus its tile directory."""
     return bytes(encoded) + b"\0" * (len(encoded) & 1) + mode_b_tile_prefix(encoded)
+
+
+def mode_b_dir_bytes(raw_bytes: int) -> int:
+    """Bytes of the tile directory at the front of a resident row (u16 per
+    512-scale tile boundary, zero-padded to a multiple of 16)."""
+    tiles = (raw_bytes + MODE_B_TILE_SCALES - 1) // MODE_B_TILE_SCALES
+    return (2 * (tiles + 1) + 15) // 16 * 16
+
+
+def mode_b_slot(encoded) -> bytes:
+    """The resident form of a Mode-B row for ``glm_moe_forward_scalex``: the
+    same directory and record as ``encode_mode_b_row``, with the directory in
+    front (zero-padded to 16 bytes) so that the kernels find it and the
+    record's header at fixed offsets."""
+    info = validate_mode_a(encoded)
+    directory = mode_b_tile_prefix(encoded)
+    pad = mode_b_dir_bytes(info.raw_bytes) - len(directory)
+    return directory + b"\0" * pad + bytes(encoded)
+
+
+def mode_b_record(slot, raw_bytes: int) -> bytes:
+    """The Mode-A record inside a resident row (``mode_b_slot``, possibly
+    padded further): after the directory, its length from the header."""
+    start = mode_b_dir_bytes(raw_bytes)
+    head = bytes(slot[start:start + MODE_A_HEADER.size])
+    if len(head) < MODE_A_HEADER.size:
+        raise ScaleCodecError("a resident row shorter than its directory and a Mode-A header")
+    _, _, _, _, _, _, _, primary, exceptions = MODE_A_HEADER.unpack(head)
+    return bytes(slot[start:start + MODE_A_HEADER.size + primary + 5 * exceptions])
+
+
+def mode_b_bank(gate_scales, down_scales, up_scales, *, align: int = 256):
+    """The HBM form of a layer's coded scales for ``glm_moe_forward_scalex``:
+    expert e's resident Mode-B row (``mode_b_slot`` of the Mode-A record of
+    its gate | down | up scale bytes, the reference's record order) at
+    ``rows[e]``, every row padded to one stride, a multiple of ``align``.
+    Returns ``(rows uint8 [E, stride], stride, coded_bytes)`` where
+    ``coded_bytes`` sums the experts' own row lengths."""
+    g, dn, u = (np.ascontiguousarray(a, dtype=np.uint8) for a in (gate_scales, down_scales, up_scales))
+    if not (g.shape[0] == dn.shape[0] == u.shape[0]):
+        raise ScaleCodecError("gate, down and up scales disagree on the expert count")
+    E = g.shape[0]
+    rows = []
+    for e in range(E):
+        raw = g[e].tobytes() + dn[e].tobytes() + u[e].tobytes()
+        rows.append(mode_b_slot(encode_mode_a(raw)))
+    stride = max(len(r) for r in rows)
+    stride = (stride + align - 1) // align * align
+    out = np.zeros((E, stride), dtype=np.uint8)
+    for e, r in enumerate(rows):
+        out[e, :len(r)] = np.frombuffer(r, dtype=np.uint8)
+    return out, stride, sum(len(r) for r in rows)
+

@@ -197,3 +197,36 @@ def test_container_reader_checks(tmp_path):
     with pytest.raises(ScaleXError, match="prefix promises"):
         ScaleXLayer.read(bad)
     assert st.calcsize("<8sIIQ") == PREFIX.size == 24
+
+
+def test_mode_b_bank_rows_decode_to_the_scales():
+    # glm_moe_forward_scalex's bank: one Mode-B row per expert at a common
+    # 256-byte stride; the checkpoint-like mix codes at ~17 % of the raw bytes
+    from glm53flash import scale_codec
+    from livglm_amd.workloads import concentrated_scales
+    rng = np.random.default_rng(12)
+    E, I, d = 5, 256, 1024
+    kinds = ["one_bit", "two_bit", "raw", "one_bit", "one_bit"]
+    g = np.stack([concentrated_scales(rng, (I, d // 32), kd) for kd in kinds])
+    dn = np.stack([concentrated_scales(rng, (d, I // 32), kd) for kd in kinds])
+    u = np.stack([concentrated_scales(rng, (I, d // 32), kd) for kd in kinds])
+    rows, stride, coded = scale_codec.mode_b_bank(g, dn, u)
+    assert stride % 256 == 0 and rows.shape == (E, stride)
+    for e in range(E):
+        raw_n = g[e].size + dn[e].size + u[e].size
+        rec = scale_codec.mode_b_record(rows[e], raw_n)
+        assert scale_codec.decode_mode_a(rec) == g[e].tobytes() + dn[e].tobytes() + u[e].tobytes()
+        info = scale_codec.inspect_mode_a(rec)
+        # the directory of encode_mode_b_row, in front of the record
+        db = scale_codec.mode_b_dir_bytes(raw_n)
+        directory = scale_codec.mode_b_tile_prefix(rec)
+        row = bytes(rows[e])
+        assert db % 16 == 0 and row[:len(directory)] == directory and not any(row[len(directory):db])
+        assert row[db:db + len(rec)] == rec and not any(row[db + len(rec):])
+        assert scale_codec.encode_mode_b_row(rec).endswith(directory)
+        assert info.codec == {"one_bit": "one_bit", "two_bit": "two_bit", "raw": "raw"}[kinds[e]]
+    one = [e for e in range(E) if kinds[e] == "one_bit"]
+    raw = 3 * I * (d // 32)
+    for e in one:
+        info = scale_codec.inspect_mode_a(scale_codec.mode_b_record(rows[e], raw))
+        assert 0.14 < info.encoded_bytes / raw < 0.20
