@@ -251,6 +251,50 @@ __device__ __forceinline__ void mma_wave_weights_lds(const WaveWeights<FMT, NPRO
   }
 }
 
+// mma_wave_weights_lds for a wave that streams several tiles through the
+// same registers: right after chunk c's MFMAs the next tile's chunk c (from
+// wrow_next / srow_next, when `next`) is issued into the registers they
+// consumed, so the wave keeps about CPW chunks in flight across the tile
+// boundary instead of draining to zero before the next tile's loads.  With
+// paired chunks the scale dword of pair m serves chunks 2m and 2m + 1; the
+// next tile's dword goes out after chunk 2m + 1's MFMAs.  ww must have been
+// filled by load_wave_weights (or by this function for the previous tile).
+template <int FMT, int NPROJ, int CPW>
+__device__ __forceinline__ void mma_wave_weights_lds_roll(
+    WaveWeights<FMT, NPROJ, CPW> &ww, int kbase, int q, const uint16_t *s_row,
+    glm_f32x4 acc[NPROJ], bool next, const uint8_t *const wrow_next[NPROJ],
+    const uint8_t *const srow_next[NPROJ]) {
+  static_assert(FMT != FMT_BF16, "MX weights");
+  constexpr bool kPaired = paired_chunks<FMT, CPW>();
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    glm_bf16x8 xb[4];
+    load_act_frags_at(s_row + kbase + chunk_k<FMT, CPW>(c, q), 0, xb);
+#pragma unroll
+    for (int p = 0; p < NPROJ; ++p) {
+      glm_bf16x8 a[4];
+      const uint32_t sd = kPaired ? ww.sd[p][c & ~1] : ww.sd[p][c];
+      chunk_frags<FMT>(ww.w[p][c], scale_byte<FMT, CPW>(sd, c, q), a);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], xb[i], acc[p], 0, 0, 0);
+    }
+    if (next) {
+#pragma unroll
+      for (int p = 0; p < NPROJ; ++p) {
+        ww.w[p][c] = load_chunk_at<FMT>(wrow_next[p], kbase + chunk_k<FMT, CPW>(c, q));
+        const uint32_t *sn = reinterpret_cast<const uint32_t *>(srow_next[p] + (kbase >> 5));
+        if constexpr (kPaired) {
+          if (c & 1) ww.sd[p][c & ~1] = sn[(c >> 1) * 2 + (q >> 1)];
+        } else {
+          ww.sd[p][c] = sn[c];
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // LDS row stride (bf16 elements) for staged activation rows of length K: the
 // 16-byte pad spreads the rows of one MFMA B fragment over distinct banks.
 __host__ __device__ constexpr int lds_row_stride(int K) { return K + 8; }

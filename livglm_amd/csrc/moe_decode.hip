@@ -777,9 +777,18 @@ __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
     __syncthreads();  // h in LDS (first tile); s_p free again (later tiles)
     if (j < k) {
       glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
-      mma_wave_weights_lds<FMT_MXFP4, 1, CPW_R>(ww, 0, q, s_h + j * lds_row_stride(I),
-                                                acc);  // column 0 is stored
-      if (ti + 1 < a.tpb) {
+      if constexpr (!SX) {
+        // the next tile's chunks go out as this tile's MFMAs free their registers
+        const int row = row0 + 16 + r;
+        const uint8_t *wrow[1] = {dw + (size_t)row * (I / 2)};
+        const uint8_t *srow[1] = {ds + (size_t)row * (I / 32)};
+        mma_wave_weights_lds_roll<FMT_MXFP4, 1, CPW_R>(ww, 0, q, s_h + j * lds_row_stride(I), acc,
+                                                       ti + 1 < a.tpb, wrow, srow);
+      } else {
+        mma_wave_weights_lds<FMT_MXFP4, 1, CPW_R>(ww, 0, q, s_h + j * lds_row_stride(I),
+                                                  acc);  // column 0 is stored
+      }
+      if (SX && ti + 1 < a.tpb) {
         const int row = row0 + 16 + r;
         const uint8_t *wrow[1] = {dw + (size_t)row * (I / 2)};
         if constexpr (SX) {
