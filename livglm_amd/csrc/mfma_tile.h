@@ -11,6 +11,8 @@
 // chunks pair up as (c>>1)*256 + 64q + 32(c&1): the four lanes of a row then
 // read one whole 128-byte line per chunk pair (two 16-byte loads each) rather
 // than half a line per load, which the memory system serves faster.
+// bf16 weights (no groups) take K = k0 + 32i + 8q + s: load i of a row's four
+// lanes is then 64 contiguous bytes, and loads 2m, 2m + 1 complete line m.
 // Output lane (r, q) holds rows 4q..4q+3 of the tile for token column r.
 #pragma once
 
@@ -45,25 +47,32 @@ struct WChunk<FMT_BF16> {
   glm_u32x4 v[4];
 };
 
-// The 32 weights of this lane starting at K = kl.
+// The 32 MX weights of this lane starting at K = kl (one E8M0 group).
 template <int FMT>
 __device__ __forceinline__ WChunk<FMT> load_chunk_at(const uint8_t *wrow, int kl) {
+  static_assert(FMT != FMT_BF16, "MX weights");
   WChunk<FMT> w;
   if constexpr (FMT == FMT_MXFP4) {
     w.c = load_stream(wrow + (kl >> 1));
-  } else if constexpr (FMT == FMT_MXFP8) {
+  } else {
     w.c0 = load_stream(wrow + kl);
     w.c1 = load_stream(wrow + kl + 16);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) w.v[i] = load_stream(wrow + 2 * kl + 16 * i);
   }
   return w;
 }
 
+// Lane q's weights of the chunk at k0: MX, the group K [k0 + 32q, k0 + 32q +
+// 32); bf16, K = k0 + 32i + 8q + [0, 8) in v[i].
 template <int FMT>
 __device__ __forceinline__ WChunk<FMT> load_chunk(const uint8_t *wrow, int k0, int q) {
-  return load_chunk_at<FMT>(wrow, k0 + 32 * q);
+  if constexpr (FMT == FMT_BF16) {
+    WChunk<FMT> w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w.v[i] = load_stream(wrow + 2 * k0 + 64 * i + 16 * q);
+    return w;
+  } else {
+    return load_chunk_at<FMT>(wrow, k0 + 32 * q);
+  }
 }
 
 template <int FMT, int CPW>
@@ -200,11 +209,13 @@ __device__ __forceinline__ void load_act_frags_at(const uint16_t *act, int kl, g
   for (int i = 0; i < 4; ++i) xb[i] = src[i];
 }
 
+// B fragments against a bf16 weight chunk at k0 (load_chunk<FMT_BF16>):
+// xb[i] = K k0 + 32i + 8q + [0, 8).
 __device__ __forceinline__ void load_act_frags(const uint16_t *act, int k0, int q,
                                                glm_bf16x8 xb[4]) {
-  const glm_bf16x8 *src = reinterpret_cast<const glm_bf16x8 *>(act + k0 + 32 * q);
+  const glm_bf16x8 *src = reinterpret_cast<const glm_bf16x8 *>(act + k0 + 8 * q);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) xb[i] = src[i];
+  for (int i = 0; i < 4; ++i) xb[i] = src[4 * i];
 }
 
 // MFMAs of preloaded MX weights against one activation row per lane column.

@@ -243,24 +243,49 @@ __global__ __launch_bounds__(kRouteThreads) void route_logits_kernel(RouteArgs a
   }
   const int kq = d >> 2;
   const float *wrow = a.w + (size_t)e * d + wave * kq;
+  auto fma4 = [](float &acc, float4 wv, uint2 xv) {
+    float s = acc;
+    s = fmaf(bf16_to_f32(xv.x & 0xffffu), wv.x, s);
+    s = fmaf(bf16_to_f32(xv.x >> 16), wv.y, s);
+    s = fmaf(bf16_to_f32(xv.y & 0xffffu), wv.z, s);
+    s = fmaf(bf16_to_f32(xv.y >> 16), wv.w, s);
+    acc = s;
+  };
   for (int t0 = 0; t0 < T; t0 += TT) {
     float acc[TT];
 #pragma unroll
     for (int t = 0; t < TT; ++t) acc[t] = 0.0f;
-    for (int kk = lane * 4; kk < kq; kk += 256) {
+    // tokens past T re-read the last row (never stored): branch-free
+    // loads are all in flight at once
+    int kk0 = lane * 4;
+    if constexpr (TT <= 2) {
+      // the row's first four rounds of 256 (all of K up to d = 4096) are
+      // loaded together, so it arrives in one memory round trip; the sums
+      // still run in K order
+      constexpr int kRounds = 4;
+      float4 wv[kRounds];
+#pragma unroll
+      for (int u = 0; u < kRounds; ++u)
+        if (kk0 + 256 * u < kq) wv[u] = *reinterpret_cast<const float4 *>(wrow + kk0 + 256 * u);
+#pragma unroll
+      for (int u = 0; u < kRounds; ++u) {
+        const int kk = kk0 + 256 * u;
+        if (kk < kq) {
+#pragma unroll
+          for (int t = 0; t < TT; ++t) {
+            const int tt = min(t0 + t, T - 1);
+            fma4(acc[t], wv[u], *reinterpret_cast<const uint2 *>(a.x + (size_t)tt * d + wave * kq + kk));
+          }
+        }
+      }
+      kk0 += 256 * kRounds;
+    }
+    for (int kk = kk0; kk < kq; kk += 256) {
       const float4 wv = *reinterpret_cast<const float4 *>(wrow + kk);
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
-        // tokens past T re-read the last row (never stored): branch-free
-        // loads are all in flight at once
         const int tt = min(t0 + t, T - 1);
-        const uint2 xv = *reinterpret_cast<const uint2 *>(a.x + (size_t)tt * d + wave * kq + kk);
-        float s = acc[t];
-        s = fmaf(bf16_to_f32(xv.x & 0xffffu), wv.x, s);
-        s = fmaf(bf16_to_f32(xv.x >> 16), wv.y, s);
-        s = fmaf(bf16_to_f32(xv.y & 0xffffu), wv.z, s);
-        s = fmaf(bf16_to_f32(xv.y >> 16), wv.w, s);
-        acc[t] = s;
+        fma4(acc[t], wv, *reinterpret_cast<const uint2 *>(a.x + (size_t)tt * d + wave * kq + kk));
       }
     }
 #pragma unroll

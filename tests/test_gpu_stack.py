@@ -274,8 +274,12 @@ def test_stack42_full_size_properties():
             for j in np.nonzero(g_i != w_i)[0]:
                 assert abs(float(choice[0, g_i[j]]) - float(choice[0, w_i[j]])) < 1e-3, \
                     (st, layer, j)
+            # the weights sum to the scaling factor unless the chosen scores
+            # vanish against the normalisation's 1e-20 guard (moe.py:61), as
+            # deep in this synthetic stack where activations have grown
             w_sum = float(got_w[layer].sum(dtype=np.float64))
-            assert w_sum == 0.0 or abs(w_sum - s.routed_scaling_factor) < 1e-5, (st, layer)
+            want_sum = float(w_want[0].sum(dtype=np.float64))
+            assert abs(w_sum - want_sum) <= 1e-5 * max(1.0, want_sum), (st, layer, w_sum, want_sum)
             order_g, order_w = np.argsort(g_i), np.argsort(w_i)
             np.testing.assert_allclose(got_w[layer][0][order_g], w_want[0][order_w], rtol=1e-2,
                                        atol=1e-4, err_msg=str((st, layer)))
