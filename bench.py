@@ -791,6 +791,9 @@ def bank_load_bench(args, torch, np) -> int:
                     for key in BANK_KEYS:
                         tname = expert_tensor_name(b.layer, e, *key.split("."))
                         want = np.frombuffer(layout.tensor_bytes(tname), np.uint8)
+                        if key.endswith(".weight_packed"):  # the bank layout of the codes
+                            want = native.mxfp4_tile_host(
+                                want.reshape(b.tensors[key].shape[1:])).reshape(-1)
                         got = b.tensors[key][e].cpu().numpy().reshape(-1)
                         if not np.array_equal(got, want):
                             raise SystemExit(f"bank_load: layer {b.layer} {tname} differs")
@@ -805,6 +808,9 @@ def bank_load_bench(args, torch, np) -> int:
                 # every layer stores the same bank, expert records back to back
                 for seg in first.segments:
                     want = blob[:, seg.at:seg.at + seg.nbytes]
+                    if seg.key.endswith(".weight_packed"):  # the bank layout of the codes
+                        want = native.mxfp4_tile_host(
+                            want.reshape(b.tensors[seg.key].shape)).reshape(shape.E, -1)
                     got = b.tensors[seg.key].cpu().numpy().reshape(shape.E, -1)
                     if not np.array_equal(got, want):
                         raise SystemExit(f"bank_load: layer {b.layer} {seg.key} differs")
@@ -843,7 +849,10 @@ def bank_load_bench(args, torch, np) -> int:
             rel = e * shape.expert_bytes
             for key, bank_t in banks[0].tensors.items():
                 n_slot = bank_t.numel() // shape.E
-                segs.append((rel, bank_t.data_ptr() + e * n_slot, n_slot))
+                # packed codes land tile-major (the bank layout), as the loader writes them
+                tk = (2 * bank_t.shape[2] if key.endswith(".weight_packed")
+                      and native.mxfp4_is_tiled(bank_t.shape[1], 2 * bank_t.shape[2]) else 0)
+                segs.append((rel, bank_t.data_ptr() + e * n_slot, n_slot, tk))
                 rel += n_slot
         table = np.array(segs, dtype=np.int64)
         dtab = torch.empty(table.size, dtype=torch.int64, device="cuda")

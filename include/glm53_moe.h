@@ -7,10 +7,17 @@
  *     All work is enqueued on it; no entry point synchronises, allocates device
  *     memory or frees it.  The caller owns every buffer.
  *   - Pointers are device pointers to row-major arrays.  bf16 values travel as
- *     uint16_t bit patterns.  Expert banks use the reference checkpoint layout
- *     (weight_packed / weight_scale, expert_source.py:189-229), stacked over
- *     experts: gate/up packed [E][I][d/2] u8, gate/up scales [E][I][d/32] u8,
- *     down packed [E][d][I/2] u8, down scales [E][d][I/32] u8.
+ *     uint16_t bit patterns.  Expert banks hold the reference checkpoint's
+ *     tensors (weight_packed / weight_scale, expert_source.py:189-229),
+ *     stacked over experts: gate/up packed [E][I][d/2] u8, gate/up scales
+ *     [E][I][d/32] u8, down packed [E][d][I/2] u8, down scales [E][d][I/32]
+ *     u8.  The scales keep the checkpoint's row-major layout; each expert's
+ *     packed codes are in the BANK LAYOUT: a matrix of `rows` x K codes with
+ *     rows % 16 == 0 and K % 128 == 0 (every geometry the MFMA kernels take)
+ *     is tile-major -- the 16-row x 128-code block (t, c) is 1 KB at byte
+ *     (t K/128 + c) 1024, its 16-byte piece r + 16 q holding row 16 t + r,
+ *     codes 128 c + 32 q .. + 31 -- and any other matrix stays row-major.
+ *     glm_mxfp4_tile and glm_bank_scatter write it from checkpoint bytes.
  *   - Return value: GLM_OK (0) or a negative GLM_ERR_* code; the message is
  *     available from glm_last_error() on the calling thread.  No C++ exception
  *     crosses the ABI.
@@ -27,7 +34,7 @@
 extern "C" {
 #endif
 
-#define GLM_ABI_VERSION 1
+#define GLM_ABI_VERSION 2
 
 #define GLM_OK 0
 #define GLM_ERR_INVALID_ARGUMENT (-1) /* null pointer, negative size, bad enum */
@@ -507,9 +514,12 @@ int glm_file_read_ranges(const char *path, int n, const int64_t *offset, const i
 
 /*
  * Moves n segments out of a device staging buffer on `stream`: segments is a
- * HOST table int64 [n][3] of {source offset in staging, destination device
- * address, bytes}; it is validated against staging_bytes and copied to
- * device_table (device memory of at least 24 n bytes, owned by the caller and
+ * HOST table int64 [n][4] of {source offset in staging, destination device
+ * address, bytes, tile_k}; tile_k > 0 marks a whole row-major MXFP4 matrix of
+ * tile_k codes a row (bytes = rows * tile_k / 2, rows % 16 == 0, tile_k % 128
+ * == 0, a 16-byte aligned destination) that lands in the bank layout,
+ * tile_k == 0 a plain copy.  The table is validated against staging_bytes and copied to
+ * device_table (device memory of at least 32 n bytes, owned by the caller and
  * kept until the stream has run the copy).  Replaces the device side of
  * mx._expert_ssd_direct_load_into (native_expert_ssd.py:379-385), which wrote
  * one expert's six tensors into its slot (allocate_slots,
@@ -517,6 +527,21 @@ int glm_file_read_ranges(const char *path, int n, const int64_t *offset, const i
  */
 int glm_bank_scatter(void *stream, const uint8_t *staging, int64_t staging_bytes,
                      const int64_t *segments, int n, int64_t *device_table);
+
+/*
+ * Checkpoint MXFP4 codes -> the bank layout: `count` consecutive row-major
+ * matrices of rows x K codes (rows * K / 2 bytes each, K % 32 == 0) at src
+ * are written to dst, tile-major when rows % 16 == 0 and K % 128 == 0 (src
+ * and dst 16-byte aligned), else copied unchanged.  src and dst must not
+ * overlap.  No counterpart in the reference, whose MLX kernels read the
+ * checkpoint rows (native_expert_ssd.py:653-694): the tiles let one wave load
+ * of the expert kernels read 1 KB of contiguous memory.
+ */
+int glm_mxfp4_tile(void *stream, const uint8_t *src, uint8_t *dst, int64_t count, int rows,
+                   int K);
+
+/* 1 when the bank stores a rows x K MXFP4 matrix tile-major, else 0. */
+int glm_mxfp4_is_tiled(int rows, int K);
 
 /*
  * Decodes n ScaleX Mode-A scale records (scale_codec.py:35-91,151-201) that

@@ -29,20 +29,40 @@ constexpr int kScatterThreads = 256;
 constexpr long long kScatterBlockBytes = 64ll << 10;  // bytes per workgroup
 constexpr int kMaxSegmentsPerLaunch = 65535;          // grid.y
 
+constexpr int kScatterCols = 4;
+
 // Segment table row: {source offset in the staging buffer, destination
-// address, bytes}.  One workgroup copies kScatterBlockBytes of one segment:
-// 16-byte vector copies when source and destination are both 16-byte
-// aligned, byte copies otherwise.
+// address, bytes, tile_k}.  One workgroup copies kScatterBlockBytes of one
+// segment: tile_k > 0 marks a whole MXFP4 matrix with tile_k codes a row,
+// written tile-major in 16-byte pieces (the destination aligned, the source
+// wherever the checkpoint put it); otherwise 16-byte vector copies when
+// source and destination are both 16-byte aligned, byte copies else.
 __global__ __launch_bounds__(kScatterThreads) void bank_scatter_kernel(const uint8_t *staging,
                                                                        const int64_t *segments) {
-  const int64_t *row = segments + 3ll * blockIdx.y;
+  const int64_t *row = segments + (long long)kScatterCols * blockIdx.y;
   const long long src_off = row[0];
   uint8_t *dst = reinterpret_cast<uint8_t *>(row[1]);
   const long long bytes = row[2];
+  const long long tile_k = row[3];
   const long long begin = (long long)blockIdx.x * kScatterBlockBytes;
   if (begin >= bytes) return;
   const long long end = begin + kScatterBlockBytes < bytes ? begin + kScatterBlockBytes : bytes;
   const uint8_t *src = staging + src_off;
+  if (tile_k > 0) {
+    const long long ppr = tile_k / 32;  // 16-byte pieces a row
+    const bool aligned = (reinterpret_cast<uintptr_t>(src) & 15u) == 0;
+    for (long long i = begin + 16ll * threadIdx.x; i < end; i += 16ll * kScatterThreads) {
+      const long long piece = i >> 4;
+      uint8_t *d = dst + 16 * mxfp4_tile_piece(piece / ppr, piece % ppr, tile_k);
+      if (aligned) {
+        *reinterpret_cast<glm_u32x4 *>(d) = *reinterpret_cast<const glm_u32x4 *>(src + i);
+      } else {
+#pragma unroll
+        for (int b = 0; b < 16; ++b) d[b] = src[i + b];
+      }
+    }
+    return;
+  }
   long long tail = begin;
   if (((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15u) == 0) {
     const long long vend = begin + ((end - begin) & ~15ll);
@@ -51,6 +71,21 @@ __global__ __launch_bounds__(kScatterThreads) void bank_scatter_kernel(const uin
     tail = vend;
   }
   for (long long i = tail + threadIdx.x; i < end; i += kScatterThreads) dst[i] = src[i];
+}
+
+// count row-major MXFP4 matrices of per_matrix 16-byte pieces -> tile-major
+// (grid-stride over the source pieces; reads coalesced, writes whole pieces).
+__global__ __launch_bounds__(kScatterThreads) void mxfp4_tile_kernel(const uint8_t *src,
+                                                                     uint8_t *dst, long long pieces,
+                                                                     long long per_matrix, int K) {
+  const long long ppr = K / 32;
+  for (long long i = (long long)blockIdx.x * kScatterThreads + threadIdx.x; i < pieces;
+       i += (long long)gridDim.x * kScatterThreads) {
+    const long long m = i / per_matrix, rem = i - m * per_matrix;
+    const long long o = m * per_matrix + mxfp4_tile_piece(rem / ppr, rem % ppr, K);
+    *reinterpret_cast<glm_u32x4 *>(dst + 16 * o) =
+        *reinterpret_cast<const glm_u32x4 *>(src + 16 * i);
+  }
 }
 
 // ScaleX Mode-A records (scale_codec.py:35-91) decoded into raw E8M0 bytes.
@@ -266,26 +301,68 @@ extern "C" int glm_bank_scatter(void *stream, const uint8_t *staging, int64_t st
               "bank_scatter: null pointer");
   long long max_bytes = 0;
   for (int i = 0; i < n; ++i) {
-    const int64_t *row = segments + 3ll * i;
+    const int64_t *row = segments + (long long)glm::kScatterCols * i;
     GLM_REQUIRE(row[0] >= 0 && row[2] >= 0 && row[0] + row[2] <= staging_bytes,
                 GLM_ERR_INVALID_ARGUMENT,
                 "bank_scatter: segment %d [%lld, +%lld) is outside the %lld-byte staging buffer", i,
                 (long long)row[0], (long long)row[2], (long long)staging_bytes);
     GLM_REQUIRE(row[2] == 0 || row[1] != 0, GLM_ERR_INVALID_ARGUMENT,
                 "bank_scatter: segment %d has no destination", i);
+    if (row[3] != 0) {
+      const long long K = row[3], rows = K > 0 && K % 2 == 0 ? row[2] / (K / 2) : 0;
+      GLM_REQUIRE(K > 0 && rows * (K / 2) == row[2] && glm::mxfp4_tiled(rows, K) &&
+                      (row[1] & 15) == 0,
+                  GLM_ERR_INVALID_ARGUMENT,
+                  "bank_scatter: segment %d is not a tileable MXFP4 matrix (K %lld, %lld bytes: "
+                  "rows %% 16 == 0 and K %% 128 == 0, a 16-byte aligned destination)",
+                  i, K, (long long)row[2]);
+    }
     max_bytes = std::max<long long>(max_bytes, row[2]);
   }
   if (max_bytes == 0) return GLM_OK;
   const long long blocks = (max_bytes + kScatterBlockBytes - 1) / kScatterBlockBytes;
   GLM_REQUIRE(blocks <= 0x7fffffffll, GLM_ERR_UNSUPPORTED_SHAPE, "bank_scatter: segment too large");
-  GLM_HIP_CHECK(hipMemcpyAsync(device_table, segments, (size_t)n * 3 * sizeof(int64_t),
+  GLM_HIP_CHECK(hipMemcpyAsync(device_table, segments,
+                               (size_t)n * glm::kScatterCols * sizeof(int64_t),
                                hipMemcpyHostToDevice, (hipStream_t)stream));
   for (int first = 0; first < n; first += kMaxSegmentsPerLaunch) {
     const int count = std::min(kMaxSegmentsPerLaunch, n - first);
     hipLaunchKernelGGL(bank_scatter_kernel, dim3((unsigned)blocks, (unsigned)count),
                        dim3(kScatterThreads), 0, (hipStream_t)stream, staging,
-                       device_table + 3ll * first);
+                       device_table + (long long)glm::kScatterCols * first);
     GLM_LAUNCH_CHECK("bank_scatter_kernel");
   }
+  return GLM_OK;
+}
+
+extern "C" int glm_mxfp4_is_tiled(int rows, int K) {
+  return rows > 0 && K > 0 && glm::mxfp4_tiled(rows, K) ? 1 : 0;
+}
+
+extern "C" int glm_mxfp4_tile(void *stream, const uint8_t *src, uint8_t *dst, int64_t count,
+                              int rows, int K) {
+  glm::clear_error();
+  GLM_REQUIRE(count >= 0 && rows >= 1 && K >= 32 && K % 32 == 0, GLM_ERR_INVALID_ARGUMENT,
+              "mxfp4_tile: count %lld rows %d K %d (K a multiple of 32)", (long long)count, rows,
+              K);
+  if (count == 0) return GLM_OK;
+  GLM_REQUIRE(src && dst, GLM_ERR_INVALID_ARGUMENT, "mxfp4_tile: null pointer");
+  const long long bytes = count * (long long)rows * (K / 2);
+  const uintptr_t s0 = reinterpret_cast<uintptr_t>(src), d0 = reinterpret_cast<uintptr_t>(dst);
+  GLM_REQUIRE(d0 + bytes <= s0 || s0 + bytes <= d0, GLM_ERR_INVALID_ARGUMENT,
+              "mxfp4_tile: source and destination overlap");
+  if (!glm::mxfp4_tiled(rows, K)) {  // this geometry stays row-major
+    GLM_HIP_CHECK(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToDevice,
+                                 (hipStream_t)stream));
+    return GLM_OK;
+  }
+  GLM_REQUIRE(((s0 | d0) & 15) == 0, GLM_ERR_INVALID_ARGUMENT,
+              "mxfp4_tile: buffers must be 16-byte aligned");
+  const long long pieces = bytes / 16;
+  const long long blocks = std::min<long long>((pieces + glm::kScatterThreads - 1) /
+                                               glm::kScatterThreads, 65536);
+  hipLaunchKernelGGL(glm::mxfp4_tile_kernel, dim3((unsigned)blocks), dim3(glm::kScatterThreads), 0,
+                     (hipStream_t)stream, src, dst, pieces, (long long)rows * (K / 32), K);
+  GLM_LAUNCH_CHECK("mxfp4_tile_kernel");
   return GLM_OK;
 }

@@ -100,6 +100,21 @@ __device__ __forceinline__ float sigmoid_f32(float x) {
   return x < 0.0f ? y : 1.0f - y;
 }
 
+// The bank keeps an MXFP4 matrix of `rows` x K codes (K / 2 bytes a row in
+// the checkpoint) tile-major when rows % 16 == 0 and K % 128 == 0 -- every
+// geometry the MFMA kernels take; any other matrix stays row-major.  Tile
+// t (rows 16t..16t+15) and chunk c (codes 128c..128c+127) form the 1 KB
+// block at byte (t K/128 + c) * 1024, whose 16-byte piece l = r + 16 q holds
+// row 16t + r, codes 128c + 32q .. +31 (one E8M0 group): a wave's 64 lanes
+// read one block as 1 KB of contiguous memory.  Piece p (bytes 16p..16p+15)
+// of a row-major row goes to piece mxfp4_tile_piece(row, p, K).
+__host__ __device__ inline bool mxfp4_tiled(long long rows, long long K) {
+  return rows % 16 == 0 && K % 128 == 0;
+}
+__host__ __device__ inline long long mxfp4_tile_piece(long long row, long long p, long long K) {
+  return ((row >> 4) * (K / 128) + (p >> 2)) * 64 + (row & 15) + 16 * (p & 3);
+}
+
 // sigmoid with the hardware exp2 and reciprocal: within a few f32 ulp of
 // sigmoid_f32 (the bf16 rounding that follows absorbs that except within a
 // few ulp of a bf16 rounding tie), at a fraction of its instructions.

@@ -6,24 +6,20 @@
 //   gate/up: h[pos] = limited_swiglu(bf16(x[tok(pos)] . Wg_e^T), bf16(x[tok(pos)] . Wu_e^T))
 //   down:    y[pos] = bf16(h[pos] . Wd_e^T)
 // and, in dense mode (one "expert", rows = tokens), the bf16 shared expert
-// DenseMLP (layers.py:160-171) at many tokens.
+// DenseMLP (layers.py:160-171) at many tokens.  The routed MXFP4 experts run
+// on the block-scaled GEMMs further down; the bf16 kernel here serves the
+// dense shared expert.
 //
 // The dispatch cuts each expert's rows into tiles of kTileM rows.  A workgroup
 // computes one row tile against kTileW = 256 weight rows (gate/up: 128
 // features of each projection; down: 256 features) in a 4 x 2 arrangement of
 // eight waves: wave (wf, wt) owns 64 weight rows x 64 tokens, i.e. 4 x 4
 // accumulator tiles of v_mfma_f32_16x16x32_bf16 (two waves per SIMD, so one
-// wave's conversions and LDS reads overlap the other's MFMAs).  K advances in
-// chunks (128 for MXFP4 weights, 64 for bf16): the activation rows (bf16,
-// gathered through the dispatch for gate/up) and the weight rows of a chunk
-// are staged in LDS, double-buffered, and the next chunk's global loads are
-// issued before the current chunk's MFMAs.  MXFP4 weights are converted to
-// bf16 in registers with v_cvt_scalef32_pk_bf16_fp4 (exact for the
-// checkpoints' scales).
-//
-// K mapping.  MXFP4: MFMA i of a chunk, slot s of lane (r, q) is K = 32q + 8i +
-// s -- lane q's 16 staged bytes of a weight row are one whole E8M0 group, so
-// each lane needs one scale byte per chunk.  bf16: K = 32i + 8q + s (natural).
+// wave's LDS reads overlap the other's MFMAs).  K advances in chunks of 64:
+// the activation rows (bf16, gathered through the dispatch for gate/up) and
+// the weight rows of a chunk are staged in LDS, three stages deep, and the
+// next chunks' global loads are issued before the current chunk's MFMAs.
+// MFMA i, slot s of lane (r, q) is K = 32i + 8q + s.
 //
 // Workgroup -> (row tile, feature tile) is XCD-aware: workgroups are dealt to
 // the 8 XCDs round-robin by linear id, so XCD x takes the x-th contiguous
@@ -51,29 +47,24 @@ constexpr int kStages = 3;     // LDS ring: two chunks in flight while one is co
 // Direct global->LDS loads write one wave's 64 x 16 bytes contiguously, so a
 // lane's LDS slot is fixed by its lane id; each lane fetches the global piece
 // that belongs in its slot.
-template <int WFMT>
-struct GroupedLayout {
-  static constexpr int kChunk = WFMT == FMT_MXFP4 ? 128 : 64;  // K per stage
+struct Bf16Layout {
+  static constexpr int kChunk = 64;  // K per stage
   static constexpr int kXRowBytes = kChunk * 2;
-  static constexpr int kWRowBytes = WFMT == FMT_MXFP4 ? kChunk / 2 : kChunk * 2;
+  static constexpr int kWRowBytes = kChunk * 2;
   static constexpr int kXBytes = kTileM * kXRowBytes;
   static constexpr int kWBytes = kTileW * kWRowBytes;
-  static constexpr int kSBytes = WFMT == FMT_MXFP4 ? kTileW * 4 : 0;
-  static constexpr int kStageBytes = kXBytes + kWBytes + kSBytes;
+  static constexpr int kStageBytes = kXBytes + kWBytes;
   static constexpr int kXPerRow = kXRowBytes / 16;  // pieces per row
   static constexpr int kWPerRow = kWRowBytes / 16;
   static constexpr int kXLoads = kXBytes / (kThreads * 16);  // 16-byte loads per thread
   static constexpr int kWLoads = kWBytes / (kThreads * 16);
-  static constexpr int kSLoads = WFMT == FMT_MXFP4 ? 1 : 0;  // 4-byte loads per thread
-  static constexpr int kLoads = kXLoads + kWLoads + kSLoads;  // per chunk, per thread
+  static constexpr int kLoads = kXLoads + kWLoads;  // per chunk, per thread
   static_assert(kXBytes % (kThreads * 16) == 0 && kWBytes % (kThreads * 16) == 0, "staging");
   static_assert(kStages * kStageBytes <= 160 * 1024, "LDS ring exceeds 160 KB");
 
-  // 256-byte activation rows: 16 pieces, swizzle over the row's low 4 bits;
-  // 128-byte rows: 8 pieces, the low 3 bits.
-  __device__ static int xswz(int row) { return kXPerRow == 16 ? (row & 15) : (row & 7); }
-  // 64-byte MXFP4 weight rows pair up in 128 bytes: swizzle by row / 2.
-  __device__ static int wswz(int row) { return kWPerRow == 4 ? ((row >> 1) & 3) : (row & 7); }
+  // 128-byte rows of 8 pieces: swizzle over the row's low 3 bits
+  __device__ static int xswz(int row) { return row & 7; }
+  __device__ static int wswz(int row) { return row & 7; }
 };
 
 // s_waitcnt immediate that waits for the vector-memory counter to reach n
@@ -97,13 +88,10 @@ struct GroupedArgs {
   float limit;               // bf16-rounded SwiGLU limit (gate/up)
 };
 
-// Direct global->LDS loads: lane i's 16 (4) bytes land at lds + 16 i (4 i);
+// Direct global->LDS loads: lane i's 16 bytes land at lds + 16 i;
 // the LDS address is wave-uniform.
 __device__ __forceinline__ void load16_to_lds(const void *src, void *lds) {
   __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
-}
-__device__ __forceinline__ void load4_to_lds(const void *src, void *lds) {
-  __builtin_amdgcn_global_load_lds(src, lds, 4, 0, 0);
 }
 
 // Buffer-resource forms: a wave-uniform base and size in scalar registers,
@@ -132,9 +120,9 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int NPROJ, int WFMT>
-__global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a) {
-  using L = GroupedLayout<WFMT>;
+template <int NPROJ>
+__global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs a) {
+  using L = Bf16Layout;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int nft = a.feature_tiles;
   const int ntiles = a.dense_rows > 0 ? (a.dense_rows + kTileM - 1) / kTileM : *a.num_tiles;
@@ -159,7 +147,7 @@ __global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a
   const int nchunks = K / L::kChunk;
   // weight rows of this workgroup: NPROJ == 2 -> [gate f0..f0+127 | up f0..f0+127]
   const int f0 = ftile * (kTileW / NPROJ);
-  const int wrow_bytes = WFMT == FMT_MXFP4 ? K / 2 : K * 2;
+  const int wrow_bytes = K * 2;
 
   // ---- load assignment (fixed over the K loop).  Load j of wave w fills the
   // (j * kWaves + w)-th 1 KB block of the stage region.
@@ -185,15 +173,6 @@ __global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a
     const int frow = f0 + (NPROJ == 2 ? row % (kTileW / 2) : row);
     wsrc[j] = wbase + e * a.w_stride + (size_t)frow * wrow_bytes + piece * 16;
   }
-  const uint8_t *ssrc = nullptr;
-  if constexpr (WFMT == FMT_MXFP4) {
-    // 4 waves cover the 256 rows' scale dwords; waves 4..7 load the same
-    // bytes again so every wave issues the same number of loads per chunk
-    const int row = (wave & 3) * 64 + lane;
-    const uint8_t *sbase = NPROJ == 2 && row >= kTileW / 2 ? a.s[1] : a.s[0];
-    const int frow = f0 + (NPROJ == 2 ? row % (kTileW / 2) : row);
-    ssrc = sbase + e * a.s_stride + (size_t)frow * (K / 32);
-  }
 
   // Direct global->LDS loads of chunk c into ring stage `stage`.
   auto issue = [&](int c, int stage) {
@@ -204,8 +183,6 @@ __global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a
 #pragma unroll
     for (int j = 0; j < L::kWLoads; ++j)
       load16_to_lds(wsrc[j] + c * L::kWRowBytes, base + L::kXBytes + (j * kWaves + wave) * 1024);
-    if constexpr (WFMT == FMT_MXFP4)
-      load4_to_lds(ssrc + c * 4, base + L::kXBytes + L::kWBytes + (wave & 3) * 256);
   };
 
   glm_f32x4 acc[4][4];
@@ -219,42 +196,12 @@ __global__ __launch_bounds__(kThreads) void grouped_mx_gemm_kernel(GroupedArgs a
   auto wrow_of = [&](int rt) {
     return NPROJ == 2 ? (rt / 2) * (kTileW / 2) + wf * 32 + (rt % 2) * 16 : wf * 64 + rt * 16;
   };
-  // MFMAs of one staged chunk.  MXFP4: MFMA i, slot s of lane (r, q) is
-  // K = 32q + 8i + s (lane q's 16 weight bytes are one whole E8M0 group);
-  // bf16: K = 32i + 8q + s.
+  // MFMAs of one staged chunk: MFMA i, slot s of lane (r, q) is K = 32i + 8q + s.
   auto compute = [&](int stage) {
     const uint8_t *base = smem + stage * L::kStageBytes;
     const uint8_t *sx = base;
     const uint8_t *sw = base + L::kXBytes;
-    if constexpr (WFMT == FMT_MXFP4) {
-      const uint32_t *ss = reinterpret_cast<const uint32_t *>(sw + L::kWBytes);
-      glm_u32x4 raw[4];
-      float scale[4];
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt) {
-        const int wr = wrow_of(rt) + r;
-        raw[rt] = *reinterpret_cast<const glm_u32x4 *>(sw + wr * L::kWRowBytes +
-                                                       16 * (q ^ L::wswz(wr)));
-        scale[rt] = e8m0_to_f32((ss[wr] >> (8 * q)) & 0xffu);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        glm_bf16x8 xb[4];
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-          const int xr = wt * 64 + ct * 16 + r;
-          xb[ct] = *reinterpret_cast<const glm_bf16x8 *>(sx + xr * L::kXRowBytes +
-                                                         16 * ((4 * q + i) ^ L::xswz(xr)));
-        }
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
-          const glm_bf16x8 af = mxfp4_word_to_bf16x8(raw[rt][i], scale[rt]);
-#pragma unroll
-          for (int ct = 0; ct < 4; ++ct)
-            acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, xb[ct], acc[rt][ct], 0, 0, 0);
-        }
-      }
-    } else {
+    {
 #pragma unroll
       for (int i = 0; i < L::kChunk / 32; ++i) {
         glm_bf16x8 xb[4], af[4];
@@ -625,7 +572,8 @@ constexpr int kSplitStages = 2;  // double buffer: chunk c + 1 lands while c is 
 //                row R at p ^ (R & 15); ACT_FP4 [128 rows][64 B], piece p of
 //                row R at p ^ ((R >> 1) & 3)
 //   act. scales  [terms][128 rows] u32 (the chunk's 4 E8M0 bytes)
-//   weights      [512 rows][64 B], piece p of row R at p ^ ((R >> 1) & 3)
+//   weights      32 blocks of 16 rows x 64 B, each a tile-major block of the
+//                bank as loaded: row 16 b + r, group q at 1024 b + 16 (r + 16 q)
 //   w. scales    [512 rows] u32
 template <int AF>
 struct SplitStage {
@@ -699,16 +647,17 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
     xoff[j] = act_row(row) * code_row +
               (S::kParts == 2 ? (piece < 8 ? 0u : lo_off) + (piece & 7) * 16 : piece * 16);
   }
-  // weight load j covers staged rows [256 j, 256 j + 256): one projection
+  // weight load j of wave w stages rows 16 g .. 16 g + 15, g = 16 j + w (load
+  // j: one projection's 256 rows): the bank's tile-major block of those 16
+  // features and the chunk, 1 KB of contiguous memory (chunk c at c KB)
   const uint32_t wproj_bytes = (uint32_t)a.N * (uint32_t)(K / 2);
   __amdgpu_buffer_rsrc_t wrs[S::kWLoads];
   uint32_t woff[S::kWLoads];
 #pragma unroll
   for (int j = 0; j < S::kWLoads; ++j) {
-    const int slot = (j * kSplitWaves + wave) * 64 + lane;
-    const int row = slot / 4, piece = (slot % 4) ^ ((row >> 1) & 3);
+    const int g = j * kSplitWaves + wave;
     wrs[j] = make_rsrc(a.w[NPROJ == 2 ? j : 0] + e * a.w_stride, wproj_bytes);
-    woff[j] = (uint32_t)w_feature(row) * (uint32_t)(K / 2) + piece * 16;
+    woff[j] = (uint32_t)(w_feature(16 * g) / 16) * (uint32_t)(K / 128) * 1024u + 16u * lane;
   }
   static_assert(S::kWLoads == 2 && kSplitWaves * 64 / 4 == kHalf, "one projection per load");
   // one scale dword per thread: waves 0-7 the weight scales (64 rows each);
@@ -741,7 +690,7 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
     }
 #pragma unroll
     for (int j = 0; j < S::kWLoads; ++j)
-      buf16_to_lds(wrs[j], base + S::kW + (j * kSplitWaves + wv) * 1024, woff[j], c * 64);
+      buf16_to_lds(wrs[j], base + S::kW + (j * kSplitWaves + wv) * 1024, woff[j], c * 1024);
     buf4_to_lds(srs, base + sdst, soff, c * 4);
   };
 
@@ -760,14 +709,15 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
   // Lane-dependent parts of the LDS operand addresses.  Every block starts at
   // a multiple of 16 rows, so a lane's swizzle depends on r alone: two-term
   // activation row 16m + r, piece p at (16m + r) * 256 + 16 (p ^ r); ACT_FP4
-  // and weight row 16m + r, piece p at (16m + r) * 64 + 16 (p ^ ((r >> 1) & 3)).
+  // row 16m + r, piece p at (16m + r) * 64 + 16 (p ^ ((r >> 1) & 3)); weight
+  // row 16m + r, group q at 1024 m + 16 (r + 16 q).
   uint32_t xl[2][2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     xl[t][0] = r * S::kXRow + 16 * (S::kParts == 2 ? ((8 * t + q) ^ r) : (q ^ ((r >> 1) & 3)));
     xl[t][1] = r * S::kXRow + 16 * ((8 * t + 4 + q) ^ r);
   }
-  const uint32_t wl = r * 64 + 16 * (q ^ ((r >> 1) & 3));
+  const uint32_t wl = 16 * r + 256 * q;
   const uint32_t sl = r * 4;
 
   // MFMAs of one staged chunk: for each activation fragment (term x 4 token
@@ -919,30 +869,18 @@ bool glm_grouped_supported(int d, int I) {
   return d % 512 == 0 && I % 256 == 0;
 }
 
-static int grouped_launch(hipStream_t stream, GroupedArgs a, int nproj, int wfmt, int max_tiles) {
+static int grouped_launch(hipStream_t stream, GroupedArgs a, int nproj, int max_tiles) {
   a.feature_tiles = a.N / (nproj == 2 ? kTileW / 2 : kTileW);
   // XCD x handles items [x * per, (x + 1) * per) with per <= ceil(max_items / 8),
   // at linear ids x + 8k: the grid must reach 8 * ceil(max_items / 8)
   const long long max_items = (long long)max_tiles * a.feature_tiles;
   const dim3 grid((unsigned)(((max_items + kXcds - 1) / kXcds) * kXcds));
-  if (wfmt == FMT_MXFP4) {
-    const size_t lds = kStages * (size_t)GroupedLayout<FMT_MXFP4>::kStageBytes;
-    if (nproj == 2)
-      hipLaunchKernelGGL((grouped_mx_gemm_kernel<2, FMT_MXFP4>), grid, dim3(kThreads), lds,
-                         stream, a);
-    else
-      hipLaunchKernelGGL((grouped_mx_gemm_kernel<1, FMT_MXFP4>), grid, dim3(kThreads), lds,
-                         stream, a);
-  } else {
-    const size_t lds = kStages * (size_t)GroupedLayout<FMT_BF16>::kStageBytes;
-    if (nproj == 2)
-      hipLaunchKernelGGL((grouped_mx_gemm_kernel<2, FMT_BF16>), grid, dim3(kThreads), lds,
-                         stream, a);
-    else
-      hipLaunchKernelGGL((grouped_mx_gemm_kernel<1, FMT_BF16>), grid, dim3(kThreads), lds,
-                         stream, a);
-  }
-  GLM_LAUNCH_CHECK("grouped_mx_gemm_kernel");
+  const size_t lds = kStages * (size_t)Bf16Layout::kStageBytes;
+  if (nproj == 2)
+    hipLaunchKernelGGL((grouped_bf16_gemm_kernel<2>), grid, dim3(kThreads), lds, stream, a);
+  else
+    hipLaunchKernelGGL((grouped_bf16_gemm_kernel<1>), grid, dim3(kThreads), lds, stream, a);
+  GLM_LAUNCH_CHECK("grouped_bf16_gemm_kernel");
   return GLM_OK;
 }
 
@@ -1107,7 +1045,7 @@ int glm_grouped_dense_mlp_launch(hipStream_t stream, const uint16_t *x, int T, i
   a.K = d;
   a.out = h;
   a.limit = glm_limit_bf16(limit);
-  int rc = grouped_launch(stream, a, 2, FMT_BF16, tiles);
+  int rc = grouped_launch(stream, a, 2, tiles);
   if (rc) return rc;
   GroupedArgs b{};
   b.act = h;
@@ -1116,7 +1054,7 @@ int glm_grouped_dense_mlp_launch(hipStream_t stream, const uint16_t *x, int T, i
   b.N = d;
   b.K = I;
   b.out = out;
-  return grouped_launch(stream, b, 1, FMT_BF16, tiles);
+  return grouped_launch(stream, b, 1, tiles);
 }
 
 bool glm_grouped_supported(int d, int I);

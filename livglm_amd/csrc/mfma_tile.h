@@ -6,13 +6,18 @@
 // four bf16x8 MFMA A-fragments (values exact in bf16).  The B operand is one
 // activation row per token column r at the same K positions, so
 // v_mfma_f32_16x16x32_bf16 does the whole K reduction:
-//   MFMA i, slot s of lane (r, q)  <->  K = kbase + chunk_k(c, q) + 8i + s.
-// chunk_k is c*128 + 32q, except for MXFP4 with an even chunk count, where
-// chunks pair up as (c>>1)*256 + 64q + 32(c&1): the four lanes of a row then
-// read one whole 128-byte line per chunk pair (two 16-byte loads each) rather
-// than half a line per load, which the memory system serves faster.
-// bf16 weights (no groups) take K = k0 + 32i + 8q + s: load i of a row's four
-// lanes is then 64 contiguous bytes, and loads 2m, 2m + 1 complete line m.
+//   MFMA i, slot s of lane (r, q)  <->  K = kbase + 128c + 32q + 8i + s.
+// MXFP4 weights (the expert bank) are stored tile-major: the 16-row x 128-K
+// block (tile t, chunk c) of a matrix with K columns is 1 KB at byte
+// (t K/128 + c) * 1024, lane l's 16 bytes at 16 l being row 16t + r, group
+// 4c + q -- so a wave's load of one chunk reads 1 KB of contiguous memory,
+// which HBM streams ~15 % faster than the 16 row pieces of the row-major
+// checkpoint layout.  tile_lane_ptr gives a lane's position in the tile's
+// first block; chunk c of K follows c KB further.  E8M0 scales stay
+// row-major [rows][K/32].
+// bf16 weights (row-major, no groups) take K = k0 + 32i + 8q + s: load i of a
+// row's four lanes is then 64 contiguous bytes, and loads 2m, 2m + 1
+// complete line m.
 // Output lane (r, q) holds rows 4q..4q+3 of the tile for token column r.
 #pragma once
 
@@ -39,55 +44,36 @@ struct WChunk<FMT_MXFP4> {
   glm_u32x4 c;
 };
 template <>
-struct WChunk<FMT_MXFP8> {
-  glm_u32x4 c0, c1;
-};
-template <>
 struct WChunk<FMT_BF16> {
   glm_u32x4 v[4];
 };
 
-// The 32 MX weights of this lane starting at K = kl (one E8M0 group).
-template <int FMT>
-__device__ __forceinline__ WChunk<FMT> load_chunk_at(const uint8_t *wrow, int kl) {
-  static_assert(FMT != FMT_BF16, "MX weights");
-  WChunk<FMT> w;
-  if constexpr (FMT == FMT_MXFP4) {
-    w.c = load_stream(wrow + (kl >> 1));
-  } else {
-    w.c0 = load_stream(wrow + kl);
-    w.c1 = load_stream(wrow + kl + 16);
-  }
+// This lane's position in the first block of the 16-row tile starting at row
+// row0 (a multiple of 16) of a tile-major MXFP4 matrix with K columns.
+__device__ __forceinline__ const uint8_t *tile_lane_ptr(const uint8_t *w, int row0, int K,
+                                                        int lane) {
+  return w + (size_t)row0 * (K / 2) + 16 * lane;
+}
+
+// This lane's 32 MXFP4 weights of the chunk holding K = kl (a multiple of
+// 128 plus 32q): wtile is the lane's tile_lane_ptr.
+__device__ __forceinline__ WChunk<FMT_MXFP4> load_mxfp4_chunk(const uint8_t *wtile, int kl) {
+  WChunk<FMT_MXFP4> w;
+  w.c = load_stream(wtile + (size_t)(kl >> 7) * 1024);
   return w;
 }
 
-// Lane q's weights of the chunk at k0: MX, the group K [k0 + 32q, k0 + 32q +
-// 32); bf16, K = k0 + 32i + 8q + [0, 8) in v[i].
-template <int FMT>
-__device__ __forceinline__ WChunk<FMT> load_chunk(const uint8_t *wrow, int k0, int q) {
-  if constexpr (FMT == FMT_BF16) {
-    WChunk<FMT> w;
+// bf16 weights of lane q in the chunk at k0 (row-major row wrow): K = k0 +
+// 32i + 8q + [0, 8) in v[i].
+__device__ __forceinline__ WChunk<FMT_BF16> load_bf16_chunk(const uint8_t *wrow, int k0, int q) {
+  WChunk<FMT_BF16> w;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w.v[i] = load_stream(wrow + 2 * k0 + 64 * i + 16 * q);
-    return w;
-  } else {
-    return load_chunk_at<FMT>(wrow, k0 + 32 * q);
-  }
-}
-
-template <int FMT, int CPW>
-__host__ __device__ constexpr bool paired_chunks() {
-  return FMT == FMT_MXFP4 && CPW % 2 == 0;
+  for (int i = 0; i < 4; ++i) w.v[i] = load_stream(wrow + 2 * k0 + 64 * i + 16 * q);
+  return w;
 }
 
 // First K (relative to the wave's kbase) of lane q's 32 weights in chunk c.
-template <int FMT, int CPW>
-__device__ __forceinline__ int chunk_k(int c, int q) {
-  if constexpr (paired_chunks<FMT, CPW>())
-    return (c >> 1) * 256 + 64 * q + 32 * (c & 1);
-  else
-    return c * 128 + 32 * q;
-}
+__device__ __forceinline__ int chunk_k(int c, int q) { return c * 128 + 32 * q; }
 
 template <int FMT>
 __device__ __forceinline__ void chunk_frags(const WChunk<FMT> &w, uint32_t scale_byte,
@@ -96,12 +82,6 @@ __device__ __forceinline__ void chunk_frags(const WChunk<FMT> &w, uint32_t scale
     const float sc = e8m0_to_f32(scale_byte);
 #pragma unroll
     for (int i = 0; i < 4; ++i) a[i] = mxfp4_word_to_bf16x8(w.c[i], sc);
-  } else if constexpr (FMT == FMT_MXFP8) {
-    const float sc = e8m0_to_f32(scale_byte);
-    a[0] = mxfp8_words_to_bf16x8(w.c0[0], w.c0[1], sc);
-    a[1] = mxfp8_words_to_bf16x8(w.c0[2], w.c0[3], sc);
-    a[2] = mxfp8_words_to_bf16x8(w.c1[0], w.c1[1], sc);
-    a[3] = mxfp8_words_to_bf16x8(w.c1[2], w.c1[3], sc);
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i) a[i] = __builtin_bit_cast(glm_bf16x8, w.v[i]);
@@ -114,29 +94,24 @@ __host__ __device__ constexpr int bf16_batch(int cpw, int max_batch) {
   return 1;
 }
 
-// The MX weights of one wave (CPW chunks x NPROJ matrices): issued as one
+// The MXFP4 weights of one wave (CPW chunks x NPROJ matrices): issued as one
 // batch of 128-bit loads before anything that depends on the activations.
 template <int FMT, int NPROJ, int CPW>
 struct WaveWeights {
+  static_assert(FMT == FMT_MXFP4, "tile-major MXFP4 weights");
   WChunk<FMT> w[NPROJ][CPW];
-  uint32_t sd[NPROJ][CPW];  // scale dword holding lane q's group of chunk c (see scale_byte)
+  uint32_t sd[NPROJ][CPW];  // scale dword of chunk c: byte q is lane q's group
 };
 
-// Lane q's E8M0 byte of chunk c within the dword loaded for it.
-template <int FMT, int CPW>
-__device__ __forceinline__ uint32_t scale_byte(uint32_t sd, int c, int q) {
-  if constexpr (paired_chunks<FMT, CPW>())
-    return (sd >> (8 * (2 * (q & 1) + (c & 1)))) & 0xffu;
-  else
-    return (sd >> (8 * q)) & 0xffu;
-}
+// Lane q's E8M0 byte within the dword loaded for its chunk.
+__device__ __forceinline__ uint32_t scale_byte(uint32_t sd, int q) { return (sd >> (8 * q)) & 0xffu; }
 
+// wtile: each projection's tile_lane_ptr; srow: this lane's row of scales.
 template <int FMT, int NPROJ, int CPW>
 __device__ __forceinline__ void load_wave_weights(WaveWeights<FMT, NPROJ, CPW> &ww,
-                                                  const uint8_t *const wrow[NPROJ],
+                                                  const uint8_t *const wtile[NPROJ],
                                                   const uint8_t *const srow[NPROJ], int kbase,
                                                   int q) {
-  static_assert(FMT != FMT_BF16, "bf16 weights are streamed in batches by wave_mma");
   // Scales first, then the chunks in the order the MFMAs consume them: loads
   // complete in issue order, so chunk 0 can be converted while later chunks
   // are still in flight.
@@ -144,21 +119,12 @@ __device__ __forceinline__ void load_wave_weights(WaveWeights<FMT, NPROJ, CPW> &
   for (int p = 0; p < NPROJ; ++p) {
     const uint32_t *s = reinterpret_cast<const uint32_t *>(srow[p] + (kbase >> 5));
 #pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-      if constexpr (paired_chunks<FMT, CPW>()) {
-        // groups of chunk pair m: 8 bytes at m*8; lane q's two are bytes 2q, 2q+1
-        if ((c & 1) == 0) ww.sd[p][c] = s[(c >> 1) * 2 + (q >> 1)];
-        else ww.sd[p][c] = ww.sd[p][c - 1];
-      } else {
-        ww.sd[p][c] = s[c];
-      }
-    }
+    for (int c = 0; c < CPW; ++c) ww.sd[p][c] = s[c];
   }
 #pragma unroll
   for (int c = 0; c < CPW; ++c)
 #pragma unroll
-    for (int p = 0; p < NPROJ; ++p)
-      ww.w[p][c] = load_chunk_at<FMT>(wrow[p], kbase + chunk_k<FMT, CPW>(c, q));
+    for (int p = 0; p < NPROJ; ++p) ww.w[p][c] = load_mxfp4_chunk(wtile[p], kbase + chunk_k(c, q));
   // every load above is issued before anything that follows: the scheduler
   // would otherwise sink some of them behind the first MFMAs, which costs a
   // second memory round trip
@@ -169,13 +135,12 @@ __device__ __forceinline__ void load_wave_weights(WaveWeights<FMT, NPROJ, CPW> &
 // example from scales decoded into LDS with wave_scales_from_lds).
 template <int FMT, int NPROJ, int CPW>
 __device__ __forceinline__ void load_wave_chunks(WaveWeights<FMT, NPROJ, CPW> &ww,
-                                                 const uint8_t *const wrow[NPROJ], int kbase,
+                                                 const uint8_t *const wtile[NPROJ], int kbase,
                                                  int q) {
 #pragma unroll
   for (int c = 0; c < CPW; ++c)
 #pragma unroll
-    for (int p = 0; p < NPROJ; ++p)
-      ww.w[p][c] = load_chunk_at<FMT>(wrow[p], kbase + chunk_k<FMT, CPW>(c, q));
+    for (int p = 0; p < NPROJ; ++p) ww.w[p][c] = load_mxfp4_chunk(wtile[p], kbase + chunk_k(c, q));
   __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -189,12 +154,7 @@ __device__ __forceinline__ void wave_scales_from_lds(WaveWeights<FMT, NPROJ, CPW
   for (int p = 0; p < NPROJ; ++p) {
     const uint32_t *s = reinterpret_cast<const uint32_t *>(s_row[p] + (kbase >> 5));
 #pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-      if constexpr (paired_chunks<FMT, CPW>())
-        ww.sd[p][c] = s[(c >> 1) * 2 + (q >> 1)];
-      else
-        ww.sd[p][c] = s[c];
-    }
+    for (int c = 0; c < CPW; ++c) ww.sd[p][c] = s[c];
   }
 }
 
@@ -209,7 +169,7 @@ __device__ __forceinline__ void load_act_frags_at(const uint16_t *act, int kl, g
   for (int i = 0; i < 4; ++i) xb[i] = src[i];
 }
 
-// B fragments against a bf16 weight chunk at k0 (load_chunk<FMT_BF16>):
+// B fragments against a bf16 weight chunk at k0 (load_bf16_chunk):
 // xb[i] = K k0 + 32i + 8q + [0, 8).
 __device__ __forceinline__ void load_act_frags(const uint16_t *act, int k0, int q,
                                                glm_bf16x8 xb[4]) {
@@ -226,13 +186,13 @@ __device__ __forceinline__ void mma_wave_weights(const WaveWeights<FMT, NPROJ, C
   glm_bf16x8 xb[CPW][4];
 #pragma unroll
   for (int c = 0; c < CPW; ++c)
-    load_act_frags_at(act + kbase + chunk_k<FMT, CPW>(c, q), 0, xb[c]);
+    load_act_frags_at(act + kbase + chunk_k(c, q), 0, xb[c]);
 #pragma unroll
   for (int c = 0; c < CPW; ++c) {
 #pragma unroll
     for (int p = 0; p < NPROJ; ++p) {
       glm_bf16x8 a[4];
-      chunk_frags<FMT>(ww.w[p][c], scale_byte<FMT, CPW>(ww.sd[p][c], c, q), a);
+      chunk_frags<FMT>(ww.w[p][c], scale_byte(ww.sd[p][c], q), a);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], xb[c][i], acc[p], 0, 0, 0);
@@ -250,11 +210,11 @@ __device__ __forceinline__ void mma_wave_weights_lds(const WaveWeights<FMT, NPRO
 #pragma unroll
   for (int c = 0; c < CPW; ++c) {
     glm_bf16x8 xb[4];
-    load_act_frags_at(s_row + kbase + chunk_k<FMT, CPW>(c, q), 0, xb);
+    load_act_frags_at(s_row + kbase + chunk_k(c, q), 0, xb);
 #pragma unroll
     for (int p = 0; p < NPROJ; ++p) {
       glm_bf16x8 a[4];
-      chunk_frags<FMT>(ww.w[p][c], scale_byte<FMT, CPW>(ww.sd[p][c], c, q), a);
+      chunk_frags<FMT>(ww.w[p][c], scale_byte(ww.sd[p][c], q), a);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], xb[i], acc[p], 0, 0, 0);
@@ -263,29 +223,25 @@ __device__ __forceinline__ void mma_wave_weights_lds(const WaveWeights<FMT, NPRO
 }
 
 // mma_wave_weights_lds for a wave that streams several tiles through the
-// same registers: right after chunk c's MFMAs the next tile's chunk c (from
-// wrow_next / srow_next, when `next`) is issued into the registers they
-// consumed, so the wave keeps about CPW chunks in flight across the tile
-// boundary instead of draining to zero before the next tile's loads.  With
-// paired chunks the scale dword of pair m serves chunks 2m and 2m + 1; the
-// next tile's dword goes out after chunk 2m + 1's MFMAs.  ww must have been
-// filled by load_wave_weights (or by this function for the previous tile).
+// same registers: right after chunk c's MFMAs the next tile's chunk c and its
+// scale dword (from wtile_next / srow_next, when `next`) are issued into the
+// registers they consumed, so the wave keeps about CPW chunks in flight
+// across the tile boundary instead of draining to zero before the next
+// tile's loads.  ww must have been filled by load_wave_weights (or by this
+// function for the previous tile).
 template <int FMT, int NPROJ, int CPW>
 __device__ __forceinline__ void mma_wave_weights_lds_roll(
     WaveWeights<FMT, NPROJ, CPW> &ww, int kbase, int q, const uint16_t *s_row,
-    glm_f32x4 acc[NPROJ], bool next, const uint8_t *const wrow_next[NPROJ],
+    glm_f32x4 acc[NPROJ], bool next, const uint8_t *const wtile_next[NPROJ],
     const uint8_t *const srow_next[NPROJ]) {
-  static_assert(FMT != FMT_BF16, "MX weights");
-  constexpr bool kPaired = paired_chunks<FMT, CPW>();
 #pragma unroll
   for (int c = 0; c < CPW; ++c) {
     glm_bf16x8 xb[4];
-    load_act_frags_at(s_row + kbase + chunk_k<FMT, CPW>(c, q), 0, xb);
+    load_act_frags_at(s_row + kbase + chunk_k(c, q), 0, xb);
 #pragma unroll
     for (int p = 0; p < NPROJ; ++p) {
       glm_bf16x8 a[4];
-      const uint32_t sd = kPaired ? ww.sd[p][c & ~1] : ww.sd[p][c];
-      chunk_frags<FMT>(ww.w[p][c], scale_byte<FMT, CPW>(sd, c, q), a);
+      chunk_frags<FMT>(ww.w[p][c], scale_byte(ww.sd[p][c], q), a);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], xb[i], acc[p], 0, 0, 0);
@@ -293,13 +249,8 @@ __device__ __forceinline__ void mma_wave_weights_lds_roll(
     if (next) {
 #pragma unroll
       for (int p = 0; p < NPROJ; ++p) {
-        ww.w[p][c] = load_chunk_at<FMT>(wrow_next[p], kbase + chunk_k<FMT, CPW>(c, q));
-        const uint32_t *sn = reinterpret_cast<const uint32_t *>(srow_next[p] + (kbase >> 5));
-        if constexpr (kPaired) {
-          if (c & 1) ww.sd[p][c & ~1] = sn[(c >> 1) * 2 + (q >> 1)];
-        } else {
-          ww.sd[p][c] = sn[c];
-        }
+        ww.w[p][c] = load_mxfp4_chunk(wtile_next[p], kbase + chunk_k(c, q));
+        ww.sd[p][c] = reinterpret_cast<const uint32_t *>(srow_next[p] + (kbase >> 5))[c];
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -325,10 +276,11 @@ __device__ __forceinline__ void stage_rows(uint16_t *s_x, const uint16_t *src,
 }
 
 // Accumulates, over chunks [kbase/128, kbase/128 + CPW), the 16-row tile of
-// NPROJ weight matrices against one activation row per lane column.
-// wrow/srow: this lane's weight/scale row; act: this lane's activation row
-// (nullptr for a padding column).  Scales of the CPW chunks are CPW aligned
-// dwords at srow + kbase/32 (byte q of dword c is this lane's group).
+// NPROJ weight matrices against one activation row per lane column.  MXFP4:
+// wrow is each projection's tile_lane_ptr and srow this lane's scale row
+// (byte q of dword c at srow + kbase/32 is its group); bf16: wrow is this
+// lane's row.  act: this lane's activation row (a valid row for a padding
+// column).
 template <int FMT, int NPROJ, int CPW>
 __device__ __forceinline__ void wave_mma(const uint8_t *const wrow[NPROJ],
                                          const uint8_t *const srow[NPROJ], int kbase, int q,
@@ -347,7 +299,7 @@ __device__ __forceinline__ void wave_mma(const uint8_t *const wrow[NPROJ],
 #pragma unroll
       for (int c = 0; c < NB; ++c)
 #pragma unroll
-        for (int p = 0; p < NPROJ; ++p) w[p][c] = load_chunk<FMT>(wrow[p], kbase + (b0 + c) * 128, q);
+        for (int p = 0; p < NPROJ; ++p) w[p][c] = load_bf16_chunk(wrow[p], kbase + (b0 + c) * 128, q);
       glm_bf16x8 xb[NB][4];
 #pragma unroll
       for (int c = 0; c < NB; ++c) load_act_frags(act, kbase + (b0 + c) * 128, q, xb[c]);

@@ -170,7 +170,7 @@ __device__ void shared_down_tile(const SharedArgs &a, int b, uint16_t *s_h) {
     const uint8_t *wp = a.sd + ((size_t)(row0 + r) * a.Is + kbase) * 2;
     WChunk<FMT_BF16> w[CPW_S];
 #pragma unroll
-    for (int c = 0; c < CPW_S; ++c) w[c] = load_chunk<FMT_BF16>(wp, c * 128, q);
+    for (int c = 0; c < CPW_S; ++c) w[c] = load_bf16_chunk(wp, c * 128, q);
     for (int i0 = 0; i0 < a.T * KS; i0 += 512) {
       float gv[2][kMaxSkq], uv[2][kMaxSkq];
 #pragma unroll
@@ -444,15 +444,15 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(GateUpArgs a) {
   const int e = wk.x, base = wk.y, n = wk.z;
   if (e < 0 || n <= 0) return;
   const int kbase = wave * CPW * 128;
-  const uint8_t *wrow[2] = {a.gw + e * a.w_stride + (size_t)(row0 + r) * (d / 2),
-                            a.uw + e * a.w_stride + (size_t)(row0 + r) * (d / 2)};
+  const uint8_t *wtile[2] = {tile_lane_ptr(a.gw + e * a.w_stride, row0, d, lane),
+                             tile_lane_ptr(a.uw + e * a.w_stride, row0, d, lane)};
   const uint8_t *srow[2] = {a.gs + e * a.s_stride + (size_t)(row0 + r) * (d / 32),
                             a.us + e * a.s_stride + (size_t)(row0 + r) * (d / 32)};
   // the weight stream once for all token batches; lane column r reads its
   // token's row straight from global memory (L2-resident), in flight with
   // the weights
   WaveWeights<FMT_MXFP4, 2, CPW> ww;
-  load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
+  load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wtile, srow, kbase, q);
   for (int p0 = 0; p0 < n; p0 += 16) {
     const int rows = min(16, n - p0);
     // Opaque to the compiler per batch: the weights' conversion stays inside
@@ -503,10 +503,10 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DownArgs a) {
   const int row0 = (blockIdx.x % tiles) * 64 + wave * 16;
   const int e = wk.x, base = wk.y, n = wk.z;
   if (e < 0 || n <= 0) return;
-  const uint8_t *wrow[1] = {a.dw + e * a.w_stride + (size_t)(row0 + r) * (a.I / 2)};
+  const uint8_t *wtile[1] = {tile_lane_ptr(a.dw + e * a.w_stride, row0, a.I, lane)};
   const uint8_t *srow[1] = {a.ds + e * a.s_stride + (size_t)(row0 + r) * (a.I / 32)};
   WaveWeights<FMT_MXFP4, 1, CPW_R> ww;  // loaded once for all token batches
-  load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
+  load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wtile, srow, 0, q);
   for (int p0 = 0; p0 < n; p0 += kDownStageRows) {
     const int rows = min(kDownStageRows, n - p0);
     if constexpr (CPW_R > 8) {
@@ -621,9 +621,10 @@ __global__ __launch_bounds__(256) void select_gate_up_kernel(PairArgs a, SharedA
   uint8_t *s_sc = reinterpret_cast<uint8_t *>(s_dyn) + pair_gate_up_lds_bytes(d, EPL);
   {
     const int row = tile0 * 16 + r;
-    const uint8_t *wrow[2] = {gw + (size_t)row * (d / 2), uw + (size_t)row * (d / 2)};
+    const uint8_t *wtile[2] = {tile_lane_ptr(gw, tile0 * 16, d, lane),
+                               tile_lane_ptr(uw, tile0 * 16, d, lane)};
     if constexpr (SX) {
-      load_wave_chunks<FMT_MXFP4, 2, CPW>(ww, wrow, kbase, q);
+      load_wave_chunks<FMT_MXFP4, 2, CPW>(ww, wtile, kbase, q);
       const ScalexRow hx = scalex_row(a.sx + e * a.sx_stride, scalex_dir_bytes(3 * a.I * (a.d / 32)));
       const uint32_t s0[2] = {(uint32_t)(tile0 * 16 * G), (uint32_t)((2 * a.I + tile0 * 16) * G)};
       uint8_t *const dst[2] = {s_sc, s_sc + nsx * G};
@@ -634,7 +635,7 @@ __global__ __launch_bounds__(256) void select_gate_up_kernel(PairArgs a, SharedA
       wave_scales_from_lds<FMT_MXFP4, 2, CPW>(ww, srow, kbase, q);
     } else {
       const uint8_t *srow[2] = {gs + (size_t)row * (d / 32), us + (size_t)row * (d / 32)};
-      load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
+      load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wtile, srow, kbase, q);
     }
   }
   for (int ti = 0; ti < a.tpb; ++ti) {
@@ -643,15 +644,16 @@ __global__ __launch_bounds__(256) void select_gate_up_kernel(PairArgs a, SharedA
     mma_wave_weights_lds<FMT_MXFP4, 2, CPW>(ww, kbase, q, s_x, acc);  // column 0 is stored
     if (ti + 1 < a.tpb) {
       const int row = row0 + 16 + r;
-      const uint8_t *wrow[2] = {gw + (size_t)row * (d / 2), uw + (size_t)row * (d / 2)};
+      const uint8_t *wtile[2] = {tile_lane_ptr(gw, row0 + 16, d, lane),
+                                 tile_lane_ptr(uw, row0 + 16, d, lane)};
       if constexpr (SX) {
-        load_wave_chunks<FMT_MXFP4, 2, CPW>(ww, wrow, kbase, q);
+        load_wave_chunks<FMT_MXFP4, 2, CPW>(ww, wtile, kbase, q);
         const int rr = (ti + 1) * 16 + r;
         const uint8_t *srow[2] = {s_sc + rr * G, s_sc + (nsx + rr) * G};
         wave_scales_from_lds<FMT_MXFP4, 2, CPW>(ww, srow, kbase, q);
       } else {
         const uint8_t *srow[2] = {gs + (size_t)row * (d / 32), us + (size_t)row * (d / 32)};
-        load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wrow, srow, kbase, q);
+        load_wave_weights<FMT_MXFP4, 2, CPW>(ww, wtile, srow, kbase, q);
       }
     }
     if (ksplit_reduce<2>(acc, red, wave, 4, lane) && r == 0) {
@@ -699,6 +701,8 @@ struct PairDownArgs {
 };
 
 constexpr int kPairMaxHc = 8;
+constexpr int kPairMaxParts = 8;    // shared down partial sums (Is <= 2048)
+constexpr int kPairMaxCols = 64;    // output columns of a down_combine block (tpb <= 4)
 
 // Down projection of all k experts of one token on 16 rows of d, merged in
 // the combine's order: out = sum_j f32(bf16(y_j)) * w_j (sequential j, no
@@ -709,6 +713,9 @@ __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ __attribute__((aligned(16))) uint16_t s_h[];  // [k][lds_row_stride(I)]
   __shared__ float s_p[kPairMaxK][16];
+  __shared__ float s_shv[kPairMaxCols];              // shared contribution per column
+  __shared__ float s_rv[kPairMaxHc][kPairMaxCols];   // residual streams per column
+  __shared__ float s_hc[kPairMaxHc + kPairMaxHc * kPairMaxHc];
   const int lane = threadIdx.x & 63;
   const int j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, q = lane >> 4;
@@ -716,16 +723,43 @@ __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
   const int groups = d / 16 / a.tpb;  // blocks per token
   const int t = blockIdx.x / groups;
   const int tile0 = (blockIdx.x % groups) * a.tpb;
-  // Every load goes out before the first wait: the wave's route, the h rows
-  // (into registers; past the rows the index is clamped so that no load
-  // depends on the lane), then the weights of the first tile, whose
-  // addresses wait only for the route; the h rows reach LDS after that.
-  long long e = 0;
-  float wj = 0.0f;
-  if (j < k) {
-    e = a.indices[(size_t)t * k + j];
-    wj = a.weights[(size_t)t * k + j];
+  const int ncol = 16 * a.tpb;  // the block's output columns tile0 * 16 + [0, ncol)
+  const int hc = a.hc;
+  const bool has_shared = a.shared_parts != nullptr || a.shared != nullptr;
+  // The loads go out in this order, the same in every wave and on no
+  // branch, so that every wait covers exactly what it needs (a register whose
+  // load is pending cannot be merged at a branch join without a full wait):
+  // the epilogue's values of the block's columns, one column per lane (shared
+  // contribution, residual streams, the FFN site's gates; inputs that are
+  // absent read the output row instead, in bounds and unused), the route, the
+  // h rows, then the first tile's weights, whose addresses wait only for the
+  // route.  Waves past k mirror expert k - 1 and store nothing.
+  const int cl = tile0 * 16 + min(lane, ncol - 1);
+  const float *spb = a.shared_parts != nullptr ? a.shared_parts : a.out;
+  const int np = a.shared_parts != nullptr ? a.nparts : 1;
+  float sp[kPairMaxParts];
+#pragma unroll
+  for (int qq = 0; qq < kPairMaxParts; ++qq)
+    sp[qq] = spb[((size_t)min(qq, np - 1) * a.T + t) * d + cl];
+  const uint16_t *sbf = a.shared != nullptr ? a.shared : reinterpret_cast<const uint16_t *>(a.out);
+  const uint16_t sb = sbf[(size_t)t * d + cl];
+  const bool fuse_hc = a.hc_out != nullptr;
+  const int hcc = fuse_hc ? hc : 1;
+  const float *rvb = fuse_hc ? a.hc_res : a.out;
+  float rv[kPairMaxHc];
+#pragma unroll
+  for (int i = 0; i < kPairMaxHc; ++i) rv[i] = rvb[((size_t)t * hcc + min(i, hcc - 1)) * d + cl];
+  // gates: hc post values, then hc x hc comb values (<= 72: entries lane, lane + 64)
+  const float *postb = fuse_hc ? a.hc_post : a.out, *combb = fuse_hc ? a.hc_comb : a.out;
+  float gate[2];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int i = min(lane + 64 * g, hcc + hcc * hcc - 1);
+    gate[g] = i < hcc ? postb[(size_t)t * hcc + i] : combb[(size_t)t * hcc * hcc + i - hcc];
   }
+  const int jr = min(j, k - 1);
+  const long long e = a.indices[(size_t)t * k + jr];
+  const float wj = a.weights[(size_t)t * k + jr];
   const int per_row = I / 8, nh = k * per_row;  // 16-byte pieces of the k rows of h
   const uint16_t *hsrc = a.h + (size_t)t * k * I;
   constexpr int kHP = h_pieces(CPW_R);
@@ -742,24 +776,29 @@ __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
   // are in flight
   const int Gi = I / 32, nsx = 16 * a.tpb;
   uint8_t *s_sc = reinterpret_cast<uint8_t *>(s_h) + (size_t)k * lds_row_stride(I) * 2 +
-                  (size_t)j * nsx * Gi;
-  if (j < k) {
+                  (size_t)jr * nsx * Gi;
+  {
     const int row = tile0 * 16 + r;
-    const uint8_t *wrow[1] = {dw + (size_t)row * (I / 2)};
+    const uint8_t *wtile[1] = {tile_lane_ptr(dw, tile0 * 16, I, lane)};
     if constexpr (SX) {
-      load_wave_chunks<FMT_MXFP4, 1, CPW_R>(ww, wrow, 0, q);
-      const ScalexRow hx = scalex_row(a.sx + e * a.sx_stride, scalex_dir_bytes(3 * a.I * (a.d / 32)));
-      // the down scales follow the gate's I x d/32 in the expert's stream
-      const uint32_t s0[1] = {(uint32_t)(I * (d / 32) + tile0 * 16 * Gi)};
-      uint8_t *const dst[1] = {s_sc};
-      scalex_decode<1>(hx, s0, (uint32_t)(nsx * Gi), dst, lane, 64, [] { wave_lds_sync(); });
-      wave_lds_sync();
-      const uint8_t *srow[1] = {s_sc + r * Gi};
-      wave_scales_from_lds<FMT_MXFP4, 1, CPW_R>(ww, srow, 0, q);
+      load_wave_chunks<FMT_MXFP4, 1, CPW_R>(ww, wtile, 0, q);
     } else {
       const uint8_t *srow[1] = {ds + (size_t)row * (I / 32)};
-      load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
+      load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wtile, srow, 0, q);
     }
+  }
+  // the epilogue's values to LDS (the shared partial sums added in order)
+  if (j == 0 && lane < ncol) {
+    float v = sp[0];
+#pragma unroll
+    for (int qq = 1; qq < kPairMaxParts; ++qq) v = qq < np ? v + sp[qq] : v;
+    s_shv[lane] = a.shared_parts != nullptr ? bf16_round(v) : bf16_to_f32(sb);
+#pragma unroll
+    for (int i = 0; i < kPairMaxHc; ++i) s_rv[i][lane] = i < hc ? rv[i] : 0.0f;
+  } else if (j == 1 && fuse_hc) {
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+      if (lane + 64 * g < hc + hc * hc) s_hc[lane + 64 * g] = gate[g];
   }
 #pragma unroll
   for (int u = 0; u < kHP; ++u) {
@@ -767,74 +806,51 @@ __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
     if (i < nh)
       *reinterpret_cast<glm_u32x4 *>(s_h + (i / per_row) * lds_row_stride(I) + (i % per_row) * 8) = hv[u];
   }
-  // the FFN site's gates for this token
-  __shared__ float s_hc[kPairMaxHc + kPairMaxHc * kPairMaxHc];
-  const int hc = a.hc;
-  if (a.hc_out != nullptr) {
-    const int ns = hc + hc * hc;
-    if ((int)threadIdx.x >= 64 && (int)threadIdx.x < 64 + ns) {
-      const int i = threadIdx.x - 64;
-      s_hc[i] = i < hc ? a.hc_post[(size_t)t * hc + i] : a.hc_comb[(size_t)t * hc * hc + i - hc];
+  if constexpr (SX) {
+    if (j < k) {
+      const ScalexRow hx = scalex_row(a.sx + e * a.sx_stride, scalex_dir_bytes(3 * a.I * (a.d / 32)));
+      // the down scales follow the gate's I x d/32 in the expert's stream
+      const uint32_t s0[1] = {(uint32_t)(I * (d / 32) + tile0 * 16 * Gi)};
+      uint8_t *const dst[1] = {s_sc};
+      scalex_decode<1>(hx, s0, (uint32_t)(nsx * Gi), dst, lane, 64, [] { wave_lds_sync(); });
     }
+    wave_lds_sync();
+    const uint8_t *srow[1] = {s_sc + r * Gi};
+    wave_scales_from_lds<FMT_MXFP4, 1, CPW_R>(ww, srow, 0, q);
   }
   // the block's 16-row tiles in turn; the next tile's weights are issued as
   // soon as the MFMAs have consumed this tile's registers
   for (int ti = 0; ti < a.tpb; ++ti) {
     const int row0 = (tile0 + ti) * 16;
-    const int c = row0 + threadIdx.x;  // output column of threads < 16
-    // the shared expert's contribution and the residual streams of these outputs
-    float shared_v = 0.0f;
-    float rv[kPairMaxHc];
-    if (threadIdx.x < 16) {
-      if (a.hc_out != nullptr) {
-#pragma unroll
-        for (int i = 0; i < kPairMaxHc; ++i)
-          rv[i] = i < hc ? a.hc_res[((size_t)t * hc + i) * d + c] : 0.0f;
-      }
-      if (a.shared_parts != nullptr) {
-        float sp = a.shared_parts[(size_t)t * d + c];
-        for (int qq = 1; qq < a.nparts; ++qq) sp = sp + a.shared_parts[((size_t)qq * a.T + t) * d + c];
-        shared_v = bf16_round(sp);
-      } else if (a.shared != nullptr) {
-        shared_v = bf16_to_f32(a.shared[(size_t)t * d + c]);
+    __syncthreads();  // h and the epilogue's values in LDS (first tile); s_p free again (later tiles)
+    glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
+    if constexpr (!SX) {
+      const int row = row0 + 16 + r;
+      const uint8_t *wtile[1] = {tile_lane_ptr(dw, row0 + 16, I, lane)};
+      const uint8_t *srow[1] = {ds + (size_t)row * (I / 32)};
+      mma_wave_weights_lds_roll<FMT_MXFP4, 1, CPW_R>(ww, 0, q, s_h + jr * lds_row_stride(I), acc,
+                                                     ti + 1 < a.tpb, wtile, srow);
+    } else {
+      mma_wave_weights_lds<FMT_MXFP4, 1, CPW_R>(ww, 0, q, s_h + jr * lds_row_stride(I),
+                                                acc);  // column 0 is stored
+      if (ti + 1 < a.tpb) {
+        const uint8_t *wtile[1] = {tile_lane_ptr(dw, row0 + 16, I, lane)};
+        load_wave_chunks<FMT_MXFP4, 1, CPW_R>(ww, wtile, 0, q);
+        const uint8_t *srow[1] = {s_sc + ((ti + 1) * 16 + r) * Gi};
+        wave_scales_from_lds<FMT_MXFP4, 1, CPW_R>(ww, srow, 0, q);
       }
     }
-    __syncthreads();  // h in LDS (first tile); s_p free again (later tiles)
-    if (j < k) {
-      glm_f32x4 acc[1] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}};
-      if constexpr (!SX) {
-        // the next tile's chunks go out as this tile's MFMAs free their registers
-        const int row = row0 + 16 + r;
-        const uint8_t *wrow[1] = {dw + (size_t)row * (I / 2)};
-        const uint8_t *srow[1] = {ds + (size_t)row * (I / 32)};
-        mma_wave_weights_lds_roll<FMT_MXFP4, 1, CPW_R>(ww, 0, q, s_h + j * lds_row_stride(I), acc,
-                                                       ti + 1 < a.tpb, wrow, srow);
-      } else {
-        mma_wave_weights_lds<FMT_MXFP4, 1, CPW_R>(ww, 0, q, s_h + j * lds_row_stride(I),
-                                                  acc);  // column 0 is stored
-      }
-      if (SX && ti + 1 < a.tpb) {
-        const int row = row0 + 16 + r;
-        const uint8_t *wrow[1] = {dw + (size_t)row * (I / 2)};
-        if constexpr (SX) {
-          load_wave_chunks<FMT_MXFP4, 1, CPW_R>(ww, wrow, 0, q);
-          const uint8_t *srow[1] = {s_sc + ((ti + 1) * 16 + r) * Gi};
-          wave_scales_from_lds<FMT_MXFP4, 1, CPW_R>(ww, srow, 0, q);
-        } else {
-          const uint8_t *srow[1] = {ds + (size_t)row * (I / 32)};
-          load_wave_weights<FMT_MXFP4, 1, CPW_R>(ww, wrow, srow, 0, q);
-        }
-      }
-      if (r == 0) {
+    if (j < k && r == 0) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) s_p[j][4 * q + m] = bf16_round(acc[0][m]) * wj;
-      }
+      for (int m = 0; m < 4; ++m) s_p[j][4 * q + m] = bf16_round(acc[0][m]) * wj;
     }
     __syncthreads();
     if (threadIdx.x < 16) {
+      const int cc = ti * 16 + threadIdx.x;  // column row0 + threadIdx.x among the block's
+      const int c = row0 + threadIdx.x;
       float o = 0.0f;
       for (int jj = 0; jj < k; ++jj) o = o + s_p[jj][threadIdx.x];
-      if (a.shared_parts != nullptr || a.shared != nullptr) o = o + shared_v;
+      if (has_shared) o = o + s_shv[cc];
       a.out[(size_t)t * d + c] = o;
       if (a.hc_out != nullptr) {
         // hyper_residual (mhc.py:51-60): the placement and the mixing sum
@@ -849,7 +865,7 @@ __global__ __launch_bounds__(512) void down_combine_kernel(PairDownArgs a) {
             if (i < hc) {
               float w = s_hc[hc + i * hc + jj];
               if (a.hc_bf16) w = bf16_round(w);
-              m = m + w * rv[i];
+              m = m + w * s_rv[i][cc];
             }
           }
           if (a.hc_bf16) m = bf16_round(m);
@@ -1196,6 +1212,8 @@ int glm_pair_path_launch(hipStream_t stream, const uint16_t *x, int T, int d, co
   b.shared = sg ? nullptr : shared_ready;
   b.shared_parts = sg ? yp : nullptr;
   b.nparts = sg ? sh.skd : 0;
+  GLM_REQUIRE(b.nparts <= kPairMaxParts, GLM_ERR_UNSUPPORTED_SHAPE,
+              "few-token layer: %d shared down partial sums > %d", b.nparts, kPairMaxParts);
   b.out = out;
   if (hc != nullptr) {
     b.hc_res = hc->res;

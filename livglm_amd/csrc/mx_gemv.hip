@@ -17,6 +17,10 @@
 // reduction, so no cross-lane shuffles are needed; the K-split partials of a
 // workgroup are reduced through LDS in a fixed wave order, so results are
 // deterministic.  K index of MFMA i, slot s of lane (r, q) = c*128 + 32q + 8i + s.
+// Routed experts' MXFP4 weights are the bank's (tiled = 1): tile-major, the
+// 16-row x 128-K block of tile t and chunk c at byte (t K/128 + c) * 1024
+// with lane l's 16 bytes at 16 l, so a wave's load reads 1 KB of contiguous
+// memory; resident linears and the shared expert stay row-major.
 #include "glm_common.h"
 
 #include <algorithm>
@@ -38,6 +42,7 @@ struct GemvArgs {
   int dense_rows;            // dense mode: number of activation rows
   uint16_t *out;             // bf16 [pos][N]
   float limit;               // bf16-rounded swiglu limit (NPROJ == 2)
+  int tiled;                 // MXFP4 weights tile-major (the expert bank); N % 16 == K % 128 == 0
 };
 
 __host__ __device__ constexpr int row_bytes(int fmt, int K) {
@@ -72,6 +77,16 @@ __device__ __forceinline__ Raw<FMT_MXFP4> load_raw<FMT_MXFP4>(const uint8_t *wro
                                                               int q) {
   Raw<FMT_MXFP4> r;
   r.c = *reinterpret_cast<const glm_u32x4 *>(wrow + (k0 >> 1) + 16 * q);
+  r.s = srow[(k0 >> 5) + q];
+  return r;
+}
+
+// The chunk at k0 (a multiple of 128) of a tile-major MXFP4 matrix: wtile
+// is this lane's 16-byte piece in its tile's first block.
+__device__ __forceinline__ Raw<FMT_MXFP4> load_raw_tiled(const uint8_t *wtile,
+                                                         const uint8_t *srow, int k0, int q) {
+  Raw<FMT_MXFP4> r;
+  r.c = *reinterpret_cast<const glm_u32x4 *>(wtile + (size_t)(k0 >> 7) * 1024);
   r.s = srow[(k0 >> 5) + q];
   return r;
 }
@@ -126,8 +141,9 @@ __device__ __forceinline__ void to_frags<FMT_BF16>(const Raw<FMT_BF16> &r, glm_b
 
 constexpr int kMaxTiles = 4;  // token tiles of 16 held in registers per pass
 
-template <int FMT, int NPROJ, int CPW>
+template <int FMT, int NPROJ, int CPW, bool TILED>
 __global__ __launch_bounds__(512) void mx_gemv_kernel(const GemvArgs args) {
+  static_assert(!TILED || FMT == FMT_MXFP4, "tile-major weights are MXFP4");
   extern __shared__ glm_f32x4 red[];  // [ksplit][kMaxTiles][NPROJ][64]
   const int ksplit = blockDim.x >> 6;
   const int wave = threadIdx.x >> 6;
@@ -152,7 +168,8 @@ __global__ __launch_bounds__(512) void mx_gemv_kernel(const GemvArgs args) {
   const uint8_t *srow[NPROJ];
 #pragma unroll
   for (int p = 0; p < NPROJ; ++p) {
-    wrow[p] = args.w[p] + (long long)e * args.w_stride + (long long)(row0 + r) * rb;
+    wrow[p] = args.w[p] + (long long)e * args.w_stride +
+              (TILED ? (long long)row0 * rb + 16 * lane : (long long)(row0 + r) * rb);
     srow[p] = FMT == FMT_BF16 ? nullptr
                               : args.s[p] + (long long)e * args.s_stride +
                                     (long long)(row0 + r) * (K >> 5);
@@ -178,7 +195,12 @@ __global__ __launch_bounds__(512) void mx_gemv_kernel(const GemvArgs args) {
 #pragma unroll
     for (int c = 0; c < CPW; ++c)
 #pragma unroll
-      for (int p = 0; p < NPROJ; ++p) raw[p][c] = load_raw<FMT>(wrow[p], srow[p], kbase + c * 128, q);
+      for (int p = 0; p < NPROJ; ++p) {
+        if constexpr (TILED)
+          raw[p][c] = load_raw_tiled(wrow[p], srow[p], kbase + c * 128, q);
+        else
+          raw[p][c] = load_raw<FMT>(wrow[p], srow[p], kbase + c * 128, q);
+      }
     glm_bf16x8 b0[CPW][4];
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
@@ -453,10 +475,14 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const GemvArgs args) 
   if (row >= args.N) return;
   const int K = args.K;
   const int rb = row_bytes(FMT, K);
-  const uint8_t *wrow[NPROJ];
+  // tile-major MXFP4 (the bank's layout of a geometry the MFMA path has no
+  // K split for): element k of the row sits in piece mxfp4_tile_piece of the
+  // matrix
+  const bool tiled = FMT == FMT_MXFP4 && args.tiled;
+  const uint8_t *wmat[NPROJ];
   const uint8_t *srow[NPROJ];
   for (int p = 0; p < NPROJ; ++p) {
-    wrow[p] = args.w[p] + (long long)e * args.w_stride + (long long)row * rb;
+    wmat[p] = args.w[p] + (long long)e * args.w_stride;
     srow[p] = FMT == FMT_BF16 ? nullptr
                               : args.s[p] + (long long)e * args.s_stride + (long long)row * (K >> 5);
   }
@@ -466,7 +492,17 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const GemvArgs args) 
     float acc[NPROJ];
     for (int p = 0; p < NPROJ; ++p) {
       float a = 0.0f;
-      for (int k = 0; k < K; ++k) a = fmaf(bf16_to_f32(xr[k]), weight_at<FMT>(wrow[p], srow[p], k), a);
+      if (tiled) {
+        for (int k = 0; k < K; ++k) {
+          const uint8_t *piece = wmat[p] + 16 * mxfp4_tile_piece(row, k >> 5, K);
+          const uint32_t byte = piece[(k >> 1) & 15];
+          const float wk = e2m1_value((k & 1) ? (byte >> 4) : (byte & 15)) * e8m0_to_f32(srow[p][k >> 5]);
+          a = fmaf(bf16_to_f32(xr[k]), wk, a);
+        }
+      } else {
+        const uint8_t *wrow = wmat[p] + (long long)row * rb;
+        for (int k = 0; k < K; ++k) a = fmaf(bf16_to_f32(xr[k]), weight_at<FMT>(wrow, srow[p], k), a);
+      }
       acc[p] = a;
     }
     float v;
@@ -479,6 +515,8 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const GemvArgs args) 
 }  // namespace glm
 
 using glm::GemvArgs;
+
+extern "C" int glm_mxfp4_is_tiled(int rows, int K);
 
 // Picks the K split for the MFMA path: total chunks KC = K/128 = ksplit*cpw.
 static bool choose_split(int fmt, int nproj, int K, int *ksplit, int *cpw) {
@@ -504,26 +542,41 @@ static bool choose_split(int fmt, int nproj, int K, int *ksplit, int *cpw) {
   return false;
 }
 
+template <int FMT, int NPROJ, bool TILED>
+static void launch_mfma(hipStream_t stream, const GemvArgs &a, int grid_y, int ksplit, int cpw) {
+  dim3 grid(a.N / 16, grid_y);
+  dim3 block(64 * ksplit);
+  const size_t lds = ksplit > 1 ? (size_t)ksplit * glm::kMaxTiles * NPROJ * 64 * 16 : 0;
+  switch (cpw) {
+    case 1:
+      hipLaunchKernelGGL((glm::mx_gemv_kernel<FMT, NPROJ, 1, TILED>), grid, block, lds, stream, a);
+      break;
+    case 2:
+      hipLaunchKernelGGL((glm::mx_gemv_kernel<FMT, NPROJ, 2, TILED>), grid, block, lds, stream, a);
+      break;
+    case 3:
+      hipLaunchKernelGGL((glm::mx_gemv_kernel<FMT, NPROJ, 3, TILED>), grid, block, lds, stream, a);
+      break;
+    default:
+      hipLaunchKernelGGL((glm::mx_gemv_kernel<FMT, NPROJ, 4, TILED>), grid, block, lds, stream, a);
+      break;
+  }
+}
+
 template <int FMT, int NPROJ>
 static int launch_fmt(hipStream_t stream, const GemvArgs &a, int grid_y) {
   int ksplit = 0, cpw = 0;
-  if (a.N % 16 == 0 && choose_split(FMT, NPROJ, a.K, &ksplit, &cpw)) {
-    dim3 grid(a.N / 16, grid_y);
-    dim3 block(64 * ksplit);
-    const size_t lds = ksplit > 1 ? (size_t)ksplit * glm::kMaxTiles * NPROJ * 64 * 16 : 0;
-    switch (cpw) {
-      case 1:
-        hipLaunchKernelGGL((glm::mx_gemv_kernel<FMT, NPROJ, 1>), grid, block, lds, stream, a);
-        break;
-      case 2:
-        hipLaunchKernelGGL((glm::mx_gemv_kernel<FMT, NPROJ, 2>), grid, block, lds, stream, a);
-        break;
-      case 3:
-        hipLaunchKernelGGL((glm::mx_gemv_kernel<FMT, NPROJ, 3>), grid, block, lds, stream, a);
-        break;
-      default:
-        hipLaunchKernelGGL((glm::mx_gemv_kernel<FMT, NPROJ, 4>), grid, block, lds, stream, a);
-        break;
+  const bool mfma = a.N % 16 == 0 && choose_split(FMT, NPROJ, a.K, &ksplit, &cpw);
+  GLM_REQUIRE(!a.tiled || (FMT == GLM_FMT_MXFP4 && glm::mxfp4_tiled(a.N, a.K)),
+              GLM_ERR_UNSUPPORTED_SHAPE,
+              "gemv: tile-major weights need MXFP4, N %% 16 == 0 and K %% 128 == 0 (N=%d K=%d)",
+              a.N, a.K);
+  if (mfma) {
+    if constexpr (FMT == GLM_FMT_MXFP4) {
+      if (a.tiled) launch_mfma<FMT, NPROJ, true>(stream, a, grid_y, ksplit, cpw);
+      else launch_mfma<FMT, NPROJ, false>(stream, a, grid_y, ksplit, cpw);
+    } else {
+      launch_mfma<FMT, NPROJ, false>(stream, a, grid_y, ksplit, cpw);
     }
     GLM_LAUNCH_CHECK("mx_gemv_kernel");
     return GLM_OK;
@@ -587,6 +640,7 @@ int glm_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int 
   a.work = work;
   a.out = h;
   a.limit = glm_limit_bf16(limit);
+  a.tiled = glm_mxfp4_is_tiled(I, d);  // the bank's layout of this geometry
   const int slots = std::min(E, T * k);
   return glm_gemv_launch(stream, GLM_FMT_MXFP4, 2, a, slots);
 }
@@ -606,6 +660,7 @@ int glm_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, 
   a.K = I;
   a.work = work;
   a.out = y;
+  a.tiled = glm_mxfp4_is_tiled(d, I);
   const int slots = std::min(E, T * k);
   return glm_gemv_launch(stream, GLM_FMT_MXFP4, 1, a, slots);
 }

@@ -34,7 +34,7 @@ GLM_READ_DROP_CACHE = 1
 GLM_HC_BF16_STREAMS = 1
 GLM_NOALLOC_SCRATCH_BYTES = 64 << 20
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int
@@ -91,6 +91,8 @@ SIGNATURES = {
     "glm_rms_norm": (_i, [_p, _p, _i, _i, _p, _f, _p, _p]),
     "glm_file_read_ranges": (_i, [ctypes.c_char_p, _i, _p, _p, _p, _i, _i]),
     "glm_bank_scatter": (_i, [_p, _p, _i64, _p, _i, _p]),
+    "glm_mxfp4_tile": (_i, [_p, _p, _p, _i64, _i, _i]),
+    "glm_mxfp4_is_tiled": (_i, [_i, _i]),
     "glm_scalex_decode": (_i, [_p, _p, _i64, _p, _i, _p]),
 }
 
@@ -144,3 +146,49 @@ def check(name: str, code: int) -> None:
 def call(name: str, *args) -> None:
     """Invoke ``name`` with ``args`` and raise NativeError on a non-zero status."""
     check(name, getattr(load(), name)(*args))
+
+
+def mxfp4_is_tiled(rows: int, K: int) -> bool:
+    """Whether the expert bank stores a rows x K MXFP4 matrix tile-major."""
+    return bool(load().glm_mxfp4_is_tiled(rows, K))
+
+
+def mxfp4_tile(packed, stream=None, out=None):
+    """Checkpoint MXFP4 codes -> the expert bank's layout, on the GPU.
+
+    ``packed`` is a CUDA u8 tensor ``[..., rows, K/2]`` (a stack of row-major
+    matrices); returns ``out`` (allocated like ``packed`` when not given)
+    holding each matrix tile-major when ``rows % 16 == 0`` and ``K % 128 ==
+    0``, else copied (glm_mxfp4_tile)."""
+    import torch
+
+    if not packed.is_cuda or packed.dtype != torch.uint8:
+        raise ValueError("mxfp4_tile takes a CUDA uint8 tensor")
+    src = packed.contiguous()
+    rows, K = int(src.shape[-2]), int(src.shape[-1]) * 2
+    count = src.numel() // (rows * (K // 2)) if src.numel() else 0
+    dst = torch.empty_like(src) if out is None else out
+    if dst.shape != src.shape or dst.dtype != torch.uint8 or not dst.is_contiguous():
+        raise ValueError("mxfp4_tile: out must be a contiguous uint8 tensor shaped like packed")
+    s = torch.cuda.current_stream(src.device).cuda_stream if stream is None else stream
+    call("glm_mxfp4_tile", s, src.data_ptr(), dst.data_ptr(), count, rows, K)
+    return dst
+
+
+def mxfp4_tile_host(packed):
+    """The bank layout of checkpoint MXFP4 codes, on the host (numpy), for
+    checking what the GPU wrote: a stack ``[..., rows, K/2]`` of row-major
+    matrices, each tile-major when ``rows % 16 == 0`` and ``K % 128 == 0`` --
+    row 16t + r, bytes 64c + 16q .. +15 go to piece r + 16q of the 1 KB block
+    (t, c) -- else unchanged."""
+    import numpy as np
+
+    a = np.ascontiguousarray(packed, dtype=np.uint8)
+    rows, half = a.shape[-2], a.shape[-1]
+    if rows % 16 or (2 * half) % 128:
+        return a.copy()
+    lead = a.shape[:-2]
+    t = a.reshape(*lead, rows // 16, 16, half // 64, 4, 16)  # (t, r, c, q, byte)
+    n = len(lead)
+    t = t.transpose(*range(n), n, n + 2, n + 3, n + 1, n + 4)  # (t, c, q, r, byte)
+    return np.ascontiguousarray(t).reshape(a.shape)

@@ -103,8 +103,8 @@ class ExpertBankLoader:
             self._tables = []
             self._dtables = []
             self._events = [None] * self.nbuf
-        if not self._tables or self._tables[0].numel() < 3 * segments:
-            self._tables = [torch.empty(3 * max(segments, 64), dtype=torch.int64, device=device)
+        if not self._tables or self._tables[0].numel() < 4 * segments:
+            self._tables = [torch.empty(4 * max(segments, 64), dtype=torch.int64, device=device)
                             for _ in range(self.nbuf)]
         if not self._dtables or self._dtables[0].numel() < 13 * segments:
             self._dtables = [torch.empty(13 * max(segments, 64), dtype=torch.int64, device=device)
@@ -172,23 +172,28 @@ class ExpertBankLoader:
         if len(devices) != 1:
             raise ContractError("the banks of one load_many call must share a device")
         (device,) = devices
-        work = []  # (bank base pointers, slot bytes, chunk)
+        work = []  # (bank base pointers, slot bytes, chunk, tile_k per tensor)
         for bank, layer in zip(banks, layers):
             shapes = bank.shapes()
             slot_bytes = {name: int(np.prod(shape[1:])) for name, shape in shapes.items()}
             base = {name: bank.tensors[name].data_ptr() for name in shapes}
-            work.extend((base, slot_bytes, chunk) for chunk in self._chunks(layer))
-        self._buffers(device, max(sum(len(r.segments) for _, r in c) for _, _, c in work))
+            # packed codes land in the bank layout: tile-major where the
+            # geometry allows (glm_bank_scatter's tile_k = codes per row)
+            tile_k = {name: (2 * shape[2] if name.endswith(".weight_packed")
+                             and N.native.mxfp4_is_tiled(shape[1], 2 * shape[2]) else 0)
+                      for name, shape in shapes.items()}
+            work.extend((base, slot_bytes, chunk, tile_k) for chunk in self._chunks(layer))
+        self._buffers(device, max(sum(len(r.segments) for _, r in c) for _, _, c, _ in work))
         stream = torch.cuda.current_stream(device)
         t0 = time.perf_counter()
         total = reads_total = 0
-        for c, (base, slot_bytes, chunk) in enumerate(work):
+        for c, (base, slot_bytes, chunk, tile_k) in enumerate(work):
             slot = c % self.nbuf
             if self._events[slot] is not None:
                 self._events[slot].synchronize()  # the buffers of chunk c - nbuf are free again
             # merge records that follow each other in the file into one read
             reads: list[_Read] = []
-            segments: list[tuple[int, int, int]] = []
+            segments: list[tuple[int, int, int, int]] = []
             coded: list[tuple[int, object]] = []  # (staging offset, ScaleX record)
             staged = 0
             for x, rd in chunk:
@@ -202,8 +207,10 @@ class ExpertBankLoader:
                     reads.append(_Read(rd.shard, rd.offset, rd.nbytes, at))
                     staged = at + rd.nbytes
                 for seg in rd.segments:
+                    if tile_k[seg.key] and seg.nbytes != slot_bytes[seg.key]:
+                        raise AssertionError(f"{seg.key}: a tiled segment must be a whole matrix")
                     segments.append((at + seg.at, base[seg.key] + expert * slot_bytes[seg.key],
-                                     seg.nbytes))
+                                     seg.nbytes, tile_k[seg.key]))
                     total += seg.nbytes
                 if x.coded is not None:
                     # a ScaleX record: its coded scales open the read
@@ -223,7 +230,7 @@ class ExpertBankLoader:
             decode = self._decode_rows(host, coded, base, slot_bytes)
             dev = self._dev[slot]
             dev[:staged].copy_(host[:staged], non_blocking=True)
-            table = np.ascontiguousarray(np.array(segments, dtype=np.int64).reshape(-1, 3))
+            table = np.ascontiguousarray(np.array(segments, dtype=np.int64).reshape(-1, 4))
             N.call("glm_bank_scatter", stream.cuda_stream, dev.data_ptr(), staged,
                    table.ctypes.data, table.shape[0], self._tables[slot].data_ptr())
             if decode is not None:

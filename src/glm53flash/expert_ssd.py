@@ -154,7 +154,8 @@ class HBMExpertBank:
     def load_expert(self, expert: int, tensors: dict[str, torch.Tensor]) -> None:
         """Copies one expert's six checkpoint tensors into its slot.  Keys are
         the checkpoint names (``gate_proj.weight_packed``, ``...weight_scale``)
-        or the reference's MLX names (``gate_proj.weight``, ``...scales``)."""
+        or the reference's MLX names (``gate_proj.weight``, ``...scales``).
+        Packed codes land in the bank layout (``native.mxfp4_tile``)."""
         self._require_active()
         if not 0 <= expert < self.num_experts:
             raise ContractError(f"expert id {expert} is out of range")
@@ -168,11 +169,17 @@ class HBMExpertBank:
             if tuple(src.shape[:-1]) != shape[1:-1] or src.numel() != int(torch.Size(shape[1:]).numel()):
                 raise ContractError(f"{name} of expert {expert} has shape {tuple(src.shape)}, "
                                     f"expected {shape[1:]}")
-            self.tensors[name][expert].copy_(src.reshape(shape[1:]))
+            if part == "weight_packed":
+                N.native.mxfp4_tile(src.reshape(shape[1:]).to(self.device),
+                                  out=self.tensors[name][expert])
+            else:
+                self.tensors[name][expert].copy_(src.reshape(shape[1:]))
 
     def load_bank(self, tensors: dict[str, torch.Tensor]) -> None:
-        """Replaces the whole bank with stacked ``[E, ...]`` tensors (no copy
-        when they are already contiguous u8 on this device)."""
+        """Replaces the whole bank with stacked ``[E, ...]`` checkpoint
+        tensors: the packed codes are rewritten in the bank layout
+        (``native.mxfp4_tile``), the scales kept as they are (no copy when
+        already contiguous u8 on this device)."""
         self._require_active()
         for name, shape in self.shapes().items():
             src = self._as_bytes(tensors[name])
@@ -182,6 +189,8 @@ class HBMExpertBank:
                 src = src.reshape(shape)
             if src.device != self.device:
                 src = src.to(self.device)
+            if name.endswith(".weight_packed"):
+                src = N.native.mxfp4_tile(src)
             self.tensors[name] = src.contiguous()
 
     def projection(self, part: str) -> tuple[torch.Tensor, torch.Tensor]:

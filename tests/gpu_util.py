@@ -53,8 +53,19 @@ def p(t: torch.Tensor | None):
     return t.data_ptr()
 
 
-def upload_layer(layer: dict[str, np.ndarray]) -> dict[str, torch.Tensor]:
-    return {k: to_dev(v) for k, v in layer.items()}
+PACKED_KEYS = ("gate_proj.weight_packed", "up_proj.weight_packed", "down_proj.weight_packed")
+
+
+def upload_layer(layer: dict[str, np.ndarray], bank_layout: bool = True) -> dict[str, torch.Tensor]:
+    """The layer's arrays on the GPU; the experts' packed codes in the bank
+    layout (glm_mxfp4_tile) unless bank_layout is False (checkpoint bytes, as
+    the Python mirror's load_bank takes them)."""
+    dev = {k: to_dev(v) for k, v in layer.items()}
+    if bank_layout:
+        for k in PACKED_KEYS:
+            if k in dev:
+                dev[k] = native.mxfp4_tile(dev[k])
+    return dev
 
 
 def workspace(nbytes: int) -> torch.Tensor:

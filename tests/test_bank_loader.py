@@ -241,3 +241,32 @@ def test_loader_chunks_cover_each_record_once(tmp_path):
         assert offs == sorted(offs)
     # a chunk never holds less than the largest record
     assert ExpertBankLoader(plan, chunk_bytes=256).chunk_bytes >= RECORD
+
+
+def test_bank_layout_host_statement():
+    """native.mxfp4_tile_host, the host statement of the bank layout the GPU
+    writes (glm_mxfp4_tile, glm_bank_scatter): a permutation of each matrix's
+    bytes; in every 1 KB block (tile t, chunk c) the 16 bytes at 16 (r + 16 q)
+    are row 16 t + r, K codes 128 c + 32 q .. +31 -- the 32 codes of one E8M0
+    group, i.e. what lane (r, q) of a 16-row MFMA tile consumes; geometries
+    that do not tile stay as they are."""
+    from livglm_amd import native
+    rng = np.random.default_rng(5320)
+    for lead, rows, K in (((2,), 32, 256), ((), 48, 128), ((2, 3), 16, 384)):
+        a = rng.integers(0, 256, (*lead, rows, K // 2), dtype=np.uint8)
+        t = native.mxfp4_tile_host(a)
+        assert t.shape == a.shape
+        flat_a = a.reshape(-1, rows, K // 2)
+        flat_t = t.reshape(-1, rows * K // 2)
+        for m in range(flat_a.shape[0]):
+            assert np.array_equal(np.sort(flat_t[m]), np.sort(flat_a[m].reshape(-1)))
+            for blk in range((rows // 16) * (K // 128)):
+                tt, c = divmod(blk, K // 128)
+                for lane in range(64):
+                    r, q = lane % 16, lane // 16
+                    got = flat_t[m, blk * 1024 + 16 * lane: blk * 1024 + 16 * lane + 16]
+                    want = flat_a[m, 16 * tt + r, 64 * c + 16 * q: 64 * c + 16 * q + 16]
+                    assert np.array_equal(got, want), (m, tt, c, r, q)
+    for rows, K in ((20, 128), (16, 96), (32, 64)):
+        a = rng.integers(0, 256, (rows, K // 2), dtype=np.uint8)
+        assert np.array_equal(native.mxfp4_tile_host(a), a)

@@ -1,9 +1,10 @@
 """Checkpoint shards -> HBM bank on the GPU: every slot byte-exact, and the
 loaded bank computes what a bank filled from the same arrays computes.
 
-The expected bytes are the arrays the test wrote into the shards; the
-routed-expert output is checked against the oracle's routed experts
-(``expert_ssd.py:185-188``) within the bf16 gate.
+The expected bytes are the arrays the test wrote into the shards, the packed
+codes in the bank layout (``native.mxfp4_tile_host``: tile-major where the
+geometry allows); the routed-expert output is checked against the oracle's
+routed experts (``expert_ssd.py:185-188``) within the bf16 gate.
 """
 
 from __future__ import annotations
@@ -30,10 +31,11 @@ def _plan(root, E, d, I, layers):
 
 
 @pytest.mark.parametrize("misalign", [False, True])
-def test_loader_fills_every_slot_exactly(gu, tmp_path, misalign):
+@pytest.mark.parametrize("d,I", [(64, 32), (256, 128)])  # row-major codes; tile-major codes
+def test_loader_fills_every_slot_exactly(gu, tmp_path, misalign, d, I):
     from glm53flash.bank_loader import ExpertBankLoader
     from glm53flash.expert_ssd import HBMExpertBank
-    E, d, I, layers = 12, 64, 32, (3, 4)
+    E, layers = 12, (3, 4)
     record = 3 * I * d * 17 // 32
     print(f"bank loader: misalign={misalign} E={E} d={d} I={I}", flush=True)
     arrays = make_checkpoint(str(tmp_path), layers=layers, E=E, d=d, I=I, misalign=misalign,
@@ -56,6 +58,8 @@ def test_loader_fills_every_slot_exactly(gu, tmp_path, misalign):
             for part in PARTS:
                 got = gu.host(bank.tensors[f"{comp}.{part}"])
                 want = np.stack([arrays[(layer, e)][(comp, part)] for e in range(E)])
+                if part == "weight_packed":
+                    want = gu.native.mxfp4_tile_host(want)
                 assert got.shape == want.shape and np.array_equal(got, want), (layer, comp, part)
     loader.close()
 
@@ -106,18 +110,27 @@ def test_bank_scatter_segments_of_any_alignment(gu):
              (1000, 250_000, 0), (299_990, 260_000, 10), (12_345, 270_001, 65_537)]
     for s, o, n in cases:
         assert s + n <= staging_np.size and o + n <= dst_np.size
+    # tiled segments: whole MXFP4 matrices (rows x K codes) into the bank
+    # layout, from an aligned and from an odd staging offset
+    tiled = [(64_000, 340_000, 32, 256), (150_001, 360_000, 48, 128)]
+    for s, o, rows, K in tiled:
+        assert s + rows * K // 2 <= staging_np.size and o + rows * K // 2 <= dst_np.size
     base = dst.data_ptr()
-    table = np.array([(s, base + o, n) for s, o, n in cases], dtype=np.int64)
+    table = np.array([(s, base + o, n, 0) for s, o, n in cases]
+                     + [(s, base + o, rows * K // 2, K) for s, o, rows, K in tiled], dtype=np.int64)
     dtab = torch.empty(table.size, dtype=torch.int64, device="cuda")
-    print("bank scatter: 7 segments, odd offsets", flush=True)
+    print("bank scatter: 7 segments, odd offsets; 2 tiled", flush=True)
     gu.native.call("glm_bank_scatter", gu.stream(), staging.data_ptr(), staging_np.size,
-                   table.ctypes.data, len(cases), dtab.data_ptr())
+                   table.ctypes.data, table.shape[0], dtab.data_ptr())
     want = dst_np.copy()
     for s, o, n in cases:
         want[o:o + n] = staging_np[s:s + n]
+    for s, o, rows, K in tiled:
+        n = rows * K // 2
+        want[o:o + n] = gu.native.mxfp4_tile_host(staging_np[s:s + n].reshape(rows, K // 2)).reshape(-1)
     assert np.array_equal(gu.host(dst), want)
     # a segment reaching past the staging buffer is rejected before any launch
-    bad = np.array([(299_999, base, 2)], dtype=np.int64)
+    bad = np.array([(299_999, base, 2, 0)], dtype=np.int64)
     with pytest.raises(gu.native.NativeError, match="outside"):
         gu.native.call("glm_bank_scatter", gu.stream(), staging.data_ptr(), staging_np.size,
                        bad.ctypes.data, 1, dtab.data_ptr())
@@ -126,7 +139,8 @@ def test_bank_scatter_segments_of_any_alignment(gu):
 @pytest.mark.parametrize("scales", ["two_value", "uniform"])
 def test_scalex_layer_loads_the_same_bank(gu, tmp_path, scales):
     """A ScaleX layer shard (coded scales, decoded on the GPU while loading)
-    fills the bank with exactly the bytes of the native checkpoint.  "uniform"
+    fills the bank with exactly the bytes of the native checkpoint (the codes
+    in the bank layout).  "uniform"
     scales make the codec keep raw records; "two_value" ones code one bit per
     scale with exceptions."""
     from glm53flash.bank_loader import ExpertBankLoader
@@ -151,6 +165,8 @@ def test_scalex_layer_loads_the_same_bank(gu, tmp_path, scales):
             for part in PARTS:
                 got = gu.host(bank.tensors[f"{comp}.{part}"])
                 want = np.stack([arrays[(layer, e)][(comp, part)] for e in range(E)])
+                if part == "weight_packed":
+                    want = gu.native.mxfp4_tile_host(want)
                 assert np.array_equal(got, want), (layer, comp, part)
     loader.close()
 
@@ -176,5 +192,24 @@ def test_loader_at_the_real_record_size(gu, tmp_path):
         for part in PARTS:
             got = gu.host(bank.tensors[f"{comp}.{part}"])
             want = np.stack([arrays[(layer, e)][(comp, part)] for e in range(E)])
+            if part == "weight_packed":
+                want = gu.native.mxfp4_tile_host(want)
             assert np.array_equal(got, want), (comp, part)
     loader.close()
+
+
+@pytest.mark.parametrize("count,rows,K", [(3, 32, 256), (2, 48, 128), (1, 2048, 4096),
+                                         (2, 20, 128), (3, 16, 96), (0, 16, 128)])
+def test_mxfp4_tile_writes_the_bank_layout(gu, count, rows, K):
+    """glm_mxfp4_tile against the host statement of the layout: tile-major
+    where rows % 16 == 0 and K % 128 == 0, a copy otherwise."""
+    import torch
+    rng = np.random.default_rng(rows * 7 + K)
+    src_np = rng.integers(0, 256, (count, rows, K // 2), dtype=np.uint8)
+    print(f"mxfp4_tile: count={count} rows={rows} K={K}", flush=True)
+    src = gu.to_dev(src_np) if count else torch.empty((0, rows, K // 2), dtype=torch.uint8,
+                                                          device="cuda")
+    got = gu.native.mxfp4_tile(src)
+    torch.cuda.synchronize()
+    assert np.array_equal(gu.host(got), gu.native.mxfp4_tile_host(src_np))
+    assert gu.native.mxfp4_is_tiled(rows, K) == (rows % 16 == 0 and K % 128 == 0)

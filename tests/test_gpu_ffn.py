@@ -145,7 +145,7 @@ def _ffn(gu, shape, layer, h, hc, iters):
     site = MoEDecoderFFN(cfg, 3, lambda i: HBMExpertBank(
         layer=i, num_experts=shape.E, hidden_size=shape.d, intermediate_size=shape.I,
         swiglu_limit=shape.swiglu_limit, device="cuda"))
-    dl = gu.upload_layer(layer)
+    dl = gu.upload_layer(layer, bank_layout=False)  # load_bank takes checkpoint bytes
     moe = site.mlp
     moe.gate.weight = dl["router_weight"]
     moe.gate.e_score_correction_bias = dl["router_bias"]

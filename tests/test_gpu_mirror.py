@@ -39,7 +39,7 @@ def _moe(gu, shape, layer):
     moe = ExpertSSDMoE(cfg, 1, lambda i: HBMExpertBank(
         layer=i, num_experts=shape.E, hidden_size=shape.d, intermediate_size=shape.I,
         swiglu_limit=shape.swiglu_limit, device="cuda"))
-    dl = gu.upload_layer(layer)
+    dl = gu.upload_layer(layer, bank_layout=False)  # load_bank takes checkpoint bytes
     moe.gate.weight = dl["router_weight"]
     moe.gate.e_score_correction_bias = dl["router_bias"]
     moe.shared_experts.gate_proj.weight = dl["shared.gate"]

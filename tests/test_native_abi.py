@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.glm_abi_version() == native.ABI_VERSION == 1
+    assert lib.glm_abi_version() == native.ABI_VERSION == 2
 
 
 def test_workspace_size_is_host_only_and_monotone(lib):
@@ -197,11 +197,22 @@ def test_ffn_site_and_loader_entry_points_reject_bad_arguments(lib):
             fake, 0, fake)
     _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_rms_norm", None, fake, 2, 30, None, 1e-6,
             fake, None)
-    # a segment past the staging buffer, and a ScaleX record whose lengths disagree
-    seg = (ctypes.c_int64 * 3)(100, 0x2000, 200)
+    # a segment past the staging buffer, a tiled segment that is not a whole
+    # tileable matrix, and a ScaleX record whose lengths disagree
+    seg = (ctypes.c_int64 * 4)(100, 0x2000, 200, 0)
     msg = _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_bank_scatter", None, fake, 256,
                   ctypes.cast(seg, ctypes.c_void_p), 1, fake)
     assert "outside" in msg
+    for tile_k, nbytes in ((128, 64 * 8), (96, 48 * 16), (128, 64 * 16 + 16)):
+        seg = (ctypes.c_int64 * 4)(0, 0x2000, nbytes, tile_k)
+        msg = _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_bank_scatter", None, fake, 4096,
+                      ctypes.cast(seg, ctypes.c_void_p), 1, fake)
+        assert "tileable" in msg
+    # the tile transform: K not a multiple of 32, overlapping buffers
+    _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_mxfp4_tile", None, 0x1000, 0x2000, 1, 16, 48)
+    msg = _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_mxfp4_tile", None, 0x1000, 0x1200, 1, 16,
+                  128)
+    assert "overlap" in msg
     rec = (ctypes.c_int64 * 13)(0, 24 + 8 + 5, 64, 1, 0, 9, 1, 0x2000, 64, 0x3000, 0, 0x4000, 0)
     msg = _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_scalex_decode", None, fake, 4096,
                   ctypes.cast(rec, ctypes.c_void_p), 1, fake)
