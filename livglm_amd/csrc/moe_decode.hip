@@ -572,8 +572,11 @@ __host__ __device__ constexpr size_t pair_gate_up_sx_bytes(int d, int tpb) {
   return (size_t)2 * 16 * tpb * (d / 32);
 }
 
+// Four waves per SIMD (at most 128 registers, no spills): at the real expert
+// geometry the routed and the shared-down blocks of one launch are then all
+// resident at once.
 template <int EPL, int CPW, int CPW_S, bool SX>
-__global__ __launch_bounds__(256) void select_gate_up_kernel(PairArgs a, SharedArgs sh) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void select_gate_up_kernel(PairArgs a, SharedArgs sh) {
   extern __shared__ __attribute__((aligned(16))) uint16_t s_dyn[];
   __shared__ glm_f32x4 red[3 * 2 * 64];
   if ((int)blockIdx.x >= a.routed_blocks) {
@@ -594,10 +597,14 @@ __global__ __launch_bounds__(256) void select_gate_up_kernel(PairArgs a, SharedA
   // weight loads.  Wave 0 of one block per token publishes the route.
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   uint16_t *s_x = s_dyn;  // token t's row
+  // the wave's K range of the row goes to registers first and to LDS after
+  // the selection, whose logit and bias loads then share its round trip
+  constexpr int kRowPieces = (CPW * 16 + 63) / 64;
+  glm_u32x4 xrow[kRowPieces];
   {
     const glm_u32x4 *src = reinterpret_cast<const glm_u32x4 *>(a.x + (size_t)t * d + wv * CPW * 128);
-    glm_u32x4 *dst = reinterpret_cast<glm_u32x4 *>(s_x + wv * CPW * 128);
-    for (int i = lane; i < CPW * 16; i += 64) dst[i] = src[i];
+#pragma unroll
+    for (int u = 0; u < kRowPieces; ++u) xrow[u] = src[min(lane + 64 * u, CPW * 16 - 1)];
   }
   float *scratch = reinterpret_cast<float *>(s_dyn + lds_row_stride(d)) + wv * (64 * EPL + 256 + 64);
   int *s_selw = reinterpret_cast<int *>(scratch + 64 * EPL + 256);
@@ -605,6 +612,12 @@ __global__ __launch_bounds__(256) void select_gate_up_kernel(PairArgs a, SharedA
   select_token<EPL>(a.logits + (size_t)t * E, a.bias, E, k, a.n_group, a.topk_group, a.norm,
                     a.scale, publish ? a.weights + (size_t)t * k : nullptr,
                     publish ? a.indices + (size_t)t * k : nullptr, s_selw, scratch, lane);
+  {
+    glm_u32x4 *dst = reinterpret_cast<glm_u32x4 *>(s_x + wv * CPW * 128);
+#pragma unroll
+    for (int u = 0; u < kRowPieces; ++u)
+      if (lane + 64 * u < CPW * 16) dst[lane + 64 * u] = xrow[u];
+  }
   wave_lds_sync();  // the staged row and the choice, for this wave
   const long long e = s_selw[j];
   const int kbase = wv * CPW * 128;
@@ -1098,7 +1111,8 @@ int glm_fill_zero_launch(hipStream_t stream, void *p, size_t bytes) {
 static int launch_select_gate_up(hipStream_t stream, const PairArgs &a, const SharedArgs &sh,
                                  int cs) {
   const int d = a.d, E = a.E, T = a.T;
-  const int epl = E <= 128 ? 2 : (E <= 256 ? 4 : 8);
+  // experts per lane of the selecting wave: E <= 64 * epl
+  const int epl = E <= 128 ? 2 : (E <= 256 ? 4 : (E <= 320 ? 5 : 8));
   const bool sx = a.sx != nullptr;
   const size_t lds2 =
       std::max(pair_gate_up_lds_bytes(d, epl) + (sx ? pair_gate_up_sx_bytes(d, a.tpb) : 0),
@@ -1127,6 +1141,8 @@ static int launch_select_gate_up(hipStream_t stream, const PairArgs &a, const Sh
     GLM_PAIR_GU_CS(2)
   } else if (epl == 4) {
     GLM_PAIR_GU_CS(4)
+  } else if (epl == 5) {
+    GLM_PAIR_GU_CS(5)
   } else {
     GLM_PAIR_GU_CS(8)
   }
