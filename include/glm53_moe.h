@@ -146,9 +146,13 @@ int glm_expert_down(void *stream, const uint16_t *h, int T, int top_k, int I, in
 /*
  * Row tiles of the grouped GEMMs below, from a dispatch work list: every
  * active slot u (work[u] = {expert, first sorted position, rows, 0}) gives
- * ceil(rows / 128) tiles {expert, first position, rows <= 128, 0}, in slot
- * order.  tiles int4 [max_tiles] with max_tiles >= ceil(T*k / 128) + E;
- * num_tiles [1].  No reference counterpart: it feeds the prefill GEMMs below.
+ * nt = ceil(rows / 160) tiles {expert, first position, tile rows, 0}, in slot
+ * order: the slot's 16-row blocks B = ceil(rows / 16) are dealt out evenly,
+ * tile i starting at row 16 floor(i B / nt) of the slot, so every tile has at
+ * most 160 rows and all but the slot's last a multiple of 16.  tiles int4
+ * [max_tiles] with max_tiles >= ceil(T*k / 160) + E; num_tiles [1].  No
+ * reference counterpart: it feeds the prefill GEMMs below, which take tiles
+ * of at most 160 rows.
  */
 int glm_moe_tiles(void *stream, const int32_t *work, int E, int32_t *tiles, int32_t *num_tiles);
 

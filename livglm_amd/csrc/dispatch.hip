@@ -44,6 +44,21 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int *s_wave, int *tot
   return base + incl - v;
 }
 
+// Row tiles of the grouped GEMMs: an expert's c rows go to
+// nt = ceil(c / tile_rows) tiles (tile_rows a multiple of 16), its 16-row
+// blocks dealt out evenly, so every tile but the last is a whole number of
+// blocks and none exceeds tile_rows (ceil(c / 16) <= nt * tile_rows / 16).
+// Tile i is {first row within the expert, rows}.
+__device__ __forceinline__ int row_tiles(int c, int tile_rows) {
+  return (c + tile_rows - 1) / tile_rows;
+}
+__device__ __forceinline__ int2 row_tile(int c, int nt, int i) {
+  const long long blocks = (c + 15) / 16;
+  const int r0 = 16 * (int)(i * blocks / nt);
+  const int r1 = min(16 * (int)((i + 1) * blocks / nt), c);
+  return make_int2(r0, r1 - r0);
+}
+
 // Single workgroup; LDS: cnt[E] off[E] run[E] bits[E][32] + scan scratch.
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     const uint32_t *__restrict__ idx, int P, int k, int E, int32_t *__restrict__ counts,
@@ -74,8 +89,8 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
   __syncthreads();
 
   // offsets = exclusive scan of counts; active = compacted ids with count > 0;
-  // optionally the row tiles of the grouped GEMMs (tile_rows rows each, in
-  // expert order): {expert, first sorted position, rows, 0}.
+  // optionally the row tiles of the grouped GEMMs (row_tile, in expert
+  // order): {expert, first sorted position, rows, 0}.
   int carry = 0, carry_active = 0, carry_tiles = 0;
   for (int e0 = 0; e0 < E; e0 += kDispatchThreads) {
     const int e = e0 + tid;
@@ -84,7 +99,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     const int ex = block_exclusive_scan(c, s_scan, &tot);
     int tot_a = 0;
     const int ex_a = block_exclusive_scan(c > 0 ? 1 : 0, s_scan, &tot_a);
-    const int nt = tiles != nullptr ? (c + tile_rows - 1) / tile_rows : 0;
+    const int nt = tiles != nullptr ? row_tiles(c, tile_rows) : 0;
     int tot_t = 0;
     const int ex_t = block_exclusive_scan(nt, s_scan, &tot_t);
     if (e < E) {
@@ -95,9 +110,10 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
         active[carry_active + ex_a] = e;
         work[carry_active + ex_a] = make_int4(e, carry + ex, c, 0);
       }
-      for (int i = 0; i < nt; ++i)
-        tiles[carry_tiles + ex_t + i] =
-            make_int4(e, carry + ex + i * tile_rows, min(tile_rows, c - i * tile_rows), 0);
+      for (int i = 0; i < nt; ++i) {
+        const int2 t = row_tile(c, nt, i);
+        tiles[carry_tiles + ex_t + i] = make_int4(e, carry + ex + t.x, t.y, 0);
+      }
     }
     carry += tot;
     carry_active += tot_a;
@@ -220,7 +236,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_scan_kernel(
     const int ex = block_exclusive_scan(c_e, s_scan, &tot);
     int tot_a = 0;
     const int ex_a = block_exclusive_scan(c_e > 0 ? 1 : 0, s_scan, &tot_a);
-    const int nt = tiles != nullptr ? (c_e + tile_rows - 1) / tile_rows : 0;
+    const int nt = tiles != nullptr ? row_tiles(c_e, tile_rows) : 0;
     int tot_t = 0;
     const int ex_t = block_exclusive_scan(nt, s_scan, &tot_t);
     if (e < E) {
@@ -240,9 +256,10 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_scan_kernel(
         active[carry_active + ex_a] = e;
         work[carry_active + ex_a] = make_int4(e, off, c_e, 0);
       }
-      for (int i = 0; i < nt; ++i)
-        tiles[carry_tiles + ex_t + i] =
-            make_int4(e, off + i * tile_rows, min(tile_rows, c_e - i * tile_rows), 0);
+      for (int i = 0; i < nt; ++i) {
+        const int2 t = row_tile(c_e, nt, i);
+        tiles[carry_tiles + ex_t + i] = make_int4(e, off + t.x, t.y, 0);
+      }
     }
     carry += tot;
     carry_active += tot_a;
@@ -309,7 +326,7 @@ __global__ void dispatch_tokens_kernel(const int32_t *__restrict__ offsets, int 
 }
 
 // Row tiles of the grouped GEMMs from a work list (one workgroup): slot u of
-// {expert, first position, rows, 0} gives ceil(rows / tile_rows) tiles.
+// {expert, first position, rows, 0} gives row_tiles(rows, tile_rows) tiles.
 __global__ __launch_bounds__(kDispatchThreads) void tiles_from_work_kernel(
     const int4 *__restrict__ work, int E, int tile_rows, int4 *__restrict__ tiles,
     int32_t *__restrict__ num_tiles) {
@@ -320,11 +337,13 @@ __global__ __launch_bounds__(kDispatchThreads) void tiles_from_work_kernel(
     const int u = u0 + tid;
     const int4 wk = u < E ? work[u] : make_int4(-1, 0, 0, 0);
     const int n = wk.x >= 0 ? wk.z : 0;
-    const int nt = (n + tile_rows - 1) / tile_rows;
+    const int nt = row_tiles(n, tile_rows);
     int tot = 0;
     const int ex = block_exclusive_scan(nt, s_scan, &tot);
-    for (int i = 0; i < nt; ++i)
-      tiles[carry + ex + i] = make_int4(wk.x, wk.y + i * tile_rows, min(tile_rows, n - i * tile_rows), 0);
+    for (int i = 0; i < nt; ++i) {
+      const int2 t = row_tile(n, nt, i);
+      tiles[carry + ex + i] = make_int4(wk.x, wk.y + t.x, t.y, 0);
+    }
     carry += tot;
   }
   if (tid == 0) num_tiles[0] = carry;

@@ -10,14 +10,15 @@
 // on the block-scaled GEMMs further down; the bf16 kernel here serves the
 // dense shared expert.
 //
-// The dispatch cuts each expert's rows into tiles of kTileM rows.  A workgroup
-// computes one row tile against kTileW = 256 weight rows (gate/up: 128
-// features of each projection; down: 256 features) in a 4 x 2 arrangement of
-// eight waves: wave (wf, wt) owns 64 weight rows x 64 tokens, i.e. 4 x 4
-// accumulator tiles of v_mfma_f32_16x16x32_bf16 (two waves per SIMD, so one
-// wave's LDS reads overlap the other's MFMAs).  K advances in chunks of 64:
-// the activation rows (bf16, gathered through the dispatch for gate/up) and
-// the weight rows of a chunk are staged in LDS, three stages deep, and the
+// The dispatch cuts each routed expert's rows into row tiles of at most 160
+// rows (the block-scaled GEMMs below); the dense bf16 kernel cuts the tokens
+// into tiles of kTileM = 128 rows.  A workgroup of the bf16 kernel computes
+// one row tile against kTileW = 256 weight rows (gate/up: 128 features of each
+// projection; down: 256 features) in a 4 x 2 arrangement of eight waves: wave
+// (wf, wt) owns 64 weight rows x 64 tokens, i.e. 4 x 4 accumulator tiles of
+// v_mfma_f32_16x16x32_bf16 (two waves per SIMD, so one wave's LDS reads
+// overlap the other's MFMAs).  K advances in chunks of 64: the activation rows
+// and the weight rows of a chunk are staged in LDS, three stages deep, and the
 // next chunks' global loads are issued before the current chunk's MFMAs.
 // MFMA i, slot s of lane (r, q) is K = 32i + 8q + s.
 //
@@ -74,14 +75,9 @@ __host__ __device__ constexpr int vmcnt_imm(int n) {
 }
 
 struct GroupedArgs {
-  const uint16_t *act;       // gate/up: x [T][K]; down: h [P][K]
-  const int32_t *act_index;  // sorted position -> activation row (nullptr: the position)
-  const int4 *tiles;         // {expert, first sorted position, rows, 0}
-  const int32_t *num_tiles;
-  int dense_rows;            // > 0: dense mode, tiles of kTileM consecutive rows of expert 0
-  const uint8_t *w[2];       // stacked weights [E][N][row bytes] per projection
-  const uint8_t *s[2];       // stacked E8M0 scales [E][N][K/32] (MXFP4)
-  long long w_stride, s_stride;
+  const uint16_t *act;       // gate/up: x [T][K]; down: h [T][K]
+  int dense_rows;            // T: tiles of kTileM consecutive rows
+  const uint8_t *w[2];       // bf16 weights [N][K] per projection
   int N, K;                  // weight rows per expert and projection; reduction length
   int feature_tiles;         // workgroups along N per row tile
   uint16_t *out;             // bf16 [rows][N]
@@ -125,7 +121,7 @@ __global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs
   using L = Bf16Layout;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int nft = a.feature_tiles;
-  const int ntiles = a.dense_rows > 0 ? (a.dense_rows + kTileM - 1) / kTileM : *a.num_tiles;
+  const int ntiles = (a.dense_rows + kTileM - 1) / kTileM;
   const int items = ntiles * nft;
   const int lin = blockIdx.x;  // the grid is a multiple of kXcds covering every item
   const int per_xcd = (items + kXcds - 1) / kXcds;
@@ -137,12 +133,7 @@ __global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs
   const int lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int wf = wave & 3, wt = wave >> 2;
-  const int4 tile =
-      a.dense_rows > 0
-          ? make_int4(0, tile_id * kTileM, min(kTileM, a.dense_rows - tile_id * kTileM), 0)
-          : a.tiles[tile_id];
-  const long long e = tile.x;
-  const int pos0 = tile.y, rows = tile.z;
+  const int pos0 = tile_id * kTileM, rows = min(kTileM, a.dense_rows - pos0);
   const int K = a.K;
   const int nchunks = K / L::kChunk;
   // weight rows of this workgroup: NPROJ == 2 -> [gate f0..f0+127 | up f0..f0+127]
@@ -159,7 +150,7 @@ __global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs
     // rows past the tile's end re-read its first row: MFMA columns are
     // independent and those columns are never stored
     const int pos = pos0 + (row < rows ? row : 0);
-    const long long arow = a.act_index != nullptr ? a.act_index[pos] : pos;
+    const long long arow = pos;
     xsrc[j] = reinterpret_cast<const uint8_t *>(a.act + arow * K) + piece * 16;
   }
   const uint8_t *wsrc[L::kWLoads];
@@ -171,7 +162,7 @@ __global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs
     // becomes a vector memory load)
     const uint8_t *wbase = NPROJ == 2 && row >= kTileW / 2 ? a.w[1] : a.w[0];
     const int frow = f0 + (NPROJ == 2 ? row % (kTileW / 2) : row);
-    wsrc[j] = wbase + e * a.w_stride + (size_t)frow * wrow_bytes + piece * 16;
+    wsrc[j] = wbase + (size_t)frow * wrow_bytes + piece * 16;
   }
 
   // Direct global->LDS loads of chunk c into ring stage `stage`.
@@ -553,25 +544,31 @@ struct SplitArgs {
   long long out_rows;
 };
 
-// Workgroup tile of the block-scaled GEMMs: 128 token rows x 512 weight rows
-// (gate/up: 256 features of each projection), 16 waves as 8 (weight rows) x
-// 2 (tokens), each wave 64 weight rows x 64 tokens = 4 x 4 MFMA blocks.  The
-// two-term activations cost 2 bytes per element (hi + lo) against the
-// weights' half byte, so the tile is wide along the weights: per 128-K chunk
-// a workgroup stages 67 KB of operands for 2 x 128 x 512 x 128 MACs.  Four
-// waves per SIMD hide each other's LDS reads behind their MFMAs, and sixteen
-// waves keep enough direct-to-LDS loads in flight (eight waves cap them near
-// 3.7 TB/s on gfx950).
+// Workgroup tile of the block-scaled GEMMs: up to 160 token rows (a row tile
+// of the dispatch) x 512 weight rows (gate/up: 256 features of each
+// projection), 16 waves as 8 (weight rows) x 2 (tokens), each wave 64 weight
+// rows x 80 tokens = 4 x 5 MFMA blocks.  The two-term activations cost 2
+// bytes per element (hi + lo) against the weights' half byte, so the tile is
+// wide along the weights: per 128-K chunk a workgroup stages 75 KB of
+// operands for 2 x 160 x 512 x 128 MACs.  Four waves per SIMD hide each
+// other's LDS reads behind their MFMAs, and sixteen waves keep enough
+// direct-to-LDS loads in flight (eight waves cap them near 3.7 TB/s on
+// gfx950).  Row tiles of up to 160 rows give an expert of 129-320 rows two
+// tiles instead of three, the last of a few rows that would cost a full
+// tile's weight stream.
+constexpr int kSplitTileM = 160;
+constexpr int kSplitTokBlocks = kSplitTileM / 32;  // 16-row token blocks per token wave
 constexpr int kSplitTileW = 512;
 constexpr int kSplitThreads = 1024;
 constexpr int kSplitWaves = kSplitThreads / 64;
 constexpr int kSplitStages = 2;  // double buffer: chunk c + 1 lands while c is consumed
 
 // LDS stage (one 128-K chunk):
-//   activations  two-term formats [128 rows][hi 128 B | lo 128 B], piece p of
-//                row R at p ^ (R & 15); ACT_FP4 [128 rows][64 B], piece p of
+//   activations  two-term formats [160 rows][hi 128 B | lo 128 B], piece p of
+//                row R at p ^ (R & 15); ACT_FP4 [160 rows][64 B], piece p of
 //                row R at p ^ ((R >> 1) & 3)
-//   act. scales  [terms][128 rows] u32 (the chunk's 4 E8M0 bytes)
+//   act. scales  [terms][160 rows] u32 (the chunk's 4 E8M0 bytes), padded to
+//                a multiple of 64 slots
 //   weights      32 blocks of 16 rows x 64 B, each a tile-major block of the
 //                bank as loaded: row 16 b + r, group q at 1024 b + 16 (r + 16 q)
 //   w. scales    [512 rows] u32
@@ -581,21 +578,23 @@ struct SplitStage {
   static constexpr int kXRow = AF == ACT_FP4 ? 64 : 256;
   static constexpr int kXPieces = kXRow / 16;
   static constexpr int kTermChunk = AF == ACT_FP4 ? 64 : 128;  // stored bytes per row and chunk
-  static constexpr int kXBytes = kTileM * kXRow;
-  static constexpr int kXSBytes = kParts * kTileM * 4;
+  static constexpr int kXBytes = kSplitTileM * kXRow;
+  static constexpr int kXSRows = kParts * kSplitTileM;          // real scale slots
+  static constexpr int kXSLanes = (kXSRows + 63) / 64 * 64;      // 320 or 192
+  static constexpr int kXSBytes = kXSLanes * 4;
   static constexpr int kWBytes = kSplitTileW * 64;
   static constexpr int kWSBytes = kSplitTileW * 4;
   static constexpr int kX = 0, kXS = kXBytes, kW = kXS + kXSBytes, kWS = kW + kWBytes;
   static constexpr int kBytes = kWS + kWSBytes;
-  // 16-byte activation loads per thread (ACT_FP4: waves 0-7 load one each)
-  static constexpr int kXLoads = AF == ACT_FP4 ? 1 : kXBytes / (kSplitThreads * 16);
-  static constexpr int kXWaves = AF == ACT_FP4 ? 8 : kSplitWaves;
-  static constexpr int kWLoads = kWBytes / (kSplitThreads * 16);  // 2
-  static constexpr int kXSLanes = kXSBytes / 4;                   // 256 or 128
+  // 1 KB wave loads of the activations (40 or 10): load j of wave w is wave
+  // load 16 j + w, issued when it exists
+  static constexpr int kXSlots = kXBytes / 1024;
+  static constexpr int kXLoads = (kXSlots + kSplitWaves - 1) / kSplitWaves;  // 3 or 1
+  static constexpr int kWLoads = kWBytes / (kSplitThreads * 16);             // 2
   static constexpr int kMfmaFmt = AF == ACT_FP8X2 ? 0 : (AF == ACT_FP6X2 ? 2 : 4);
   static_assert(kSplitStages * kBytes <= 160 * 1024, "LDS stages exceed 160 KB");
-  static_assert(kXLoads * kXWaves * 64 * 16 == kXBytes, "activation loads");
-  static_assert(kWSBytes == 8 * 256 && kXSLanes % 64 == 0, "scale loads per wave");
+  static_assert(kXBytes % 1024 == 0, "activation loads");
+  static_assert(kWSBytes == 8 * 256 && kXSLanes <= 8 * 64, "scale loads per wave");
   __device__ static int xswz(int row) { return kXPieces == 16 ? (row & 15) : ((row >> 1) & 3); }
 };
 
@@ -642,7 +641,7 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
 #pragma unroll
   for (int j = 0; j < S::kXLoads; ++j) {
     const int slot = (j * kSplitWaves + wave) * 64 + lane;
-    const int row = (slot / S::kXPieces) % kTileM;  // (ACT_FP4: waves 8-15 load nothing)
+    const int row = (slot / S::kXPieces) % kSplitTileM;  // (loads past kXSlots: never issued)
     const int piece = (slot % S::kXPieces) ^ S::xswz(row);
     xoff[j] = act_row(row) * code_row +
               (S::kParts == 2 ? (piece < 8 ? 0u : lo_off) + (piece & 7) * 16 : piece * 16);
@@ -661,8 +660,9 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
   }
   static_assert(S::kWLoads == 2 && kSplitWaves * 64 / 4 == kHalf, "one projection per load");
   // one scale dword per thread: waves 0-7 the weight scales (64 rows each);
-  // waves 8-15 the activation scales, slot s = term * 128 + row, repeated
-  // once the slots run out (every wave issues the same count)
+  // waves 8-15 the activation scales, slot s = term * 160 + row, repeated
+  // once the slots run out (every wave issues the same count); the padding
+  // slots past the real ones load slot 0's scale
   __amdgpu_buffer_rsrc_t srs;
   uint32_t soff;
   int sdst;
@@ -674,20 +674,21 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
     soff = (uint32_t)w_feature(row) * (uint32_t)(K / 32);
     sdst = S::kWS + wv * 256;
   } else {
-    const int s0 = ((wv - 8) * 64) % S::kXSLanes, s = s0 + lane;
+    const int s0 = ((wv - 8) * 64) % S::kXSLanes;
+    const int s = s0 + lane < S::kXSRows ? s0 + lane : 0;
     srs = xrs;
-    soff = (uint32_t)((s >= kTileM ? a.xslo : a.xshi) - a.xhi) + act_row(s % kTileM) * (uint32_t)(K / 32);
+    soff = (uint32_t)((s >= kSplitTileM ? a.xslo : a.xshi) - a.xhi) +
+           act_row(s % kSplitTileM) * (uint32_t)(K / 32);
     sdst = S::kXS + s0 * 4;
   }
 
   auto issue = [&](int c, int stage) {
     uint8_t *base = smem + stage * S::kBytes;
-    if (wv < S::kXWaves) {
 #pragma unroll
-      for (int j = 0; j < S::kXLoads; ++j)
+    for (int j = 0; j < S::kXLoads; ++j)
+      if (j * kSplitWaves + wv < S::kXSlots)
         buf16_to_lds(xrs, base + S::kX + (j * kSplitWaves + wv) * 1024, xoff[j],
                      c * S::kTermChunk);
-    }
 #pragma unroll
     for (int j = 0; j < S::kWLoads; ++j)
       buf16_to_lds(wrs[j], base + S::kW + (j * kSplitWaves + wv) * 1024, woff[j], c * 1024);
@@ -700,11 +701,19 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
     return NPROJ == 2 ? (rt / 2) * kHalf + wf * 32 + (rt % 2) * 16 : wf * 64 + rt * 16;
   };
 
-  glm_f32x4 acc[4][4];
+  // the tile's 16-row token blocks are split evenly between the two token
+  // waves (wave 0 takes the odd one), so the four waves of a SIMD issue
+  // about as many MFMAs each; blocks past the tile's rows are skipped (their
+  // columns are never stored)
+  constexpr int kTB = kSplitTokBlocks;
+  const int half = 16 * ((((rows + 15) >> 4) + 1) >> 1);
+  const int tok0 = wt ? half : 0;     // the wave's first token row
+  const int tend = wt ? rows : half;  // and the end of its blocks (<= tok0 + 16 kTB)
+  glm_f32x4 acc[4][kTB];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = glm_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < kTB; ++j) acc[i][j] = glm_f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Lane-dependent parts of the LDS operand addresses.  Every block starts at
   // a multiple of 16 rows, so a lane's swizzle depends on r alone: two-term
@@ -720,7 +729,7 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
   const uint32_t wl = 16 * r + 256 * q;
   const uint32_t sl = r * 4;
 
-  // MFMAs of one staged chunk: for each activation fragment (term x 4 token
+  // MFMAs of one staged chunk: for each activation fragment (term x 5 token
   // blocks) 4 MFMAs, one per weight-row block.
   auto compute = [&](int stage) {
     const uint8_t *base = smem + stage * S::kBytes;
@@ -733,11 +742,11 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
       wa[rt] = glm_i32x8{(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
       wsc[rt] = (int)(*reinterpret_cast<const uint32_t *>(base + S::kWS + w16 * 4 + sl) >> (8 * q));
     }
-    // activation fragment f = (term f / 4, token block f % 4)
-    constexpr int kFrags = 4 * S::kParts;
+    // activation fragment f = (term f / kTB, token block f % kTB)
+    constexpr int kFrags = kTB * S::kParts;
     auto xfrag = [&](int f, glm_i32x8 &xb, int &xsc) {
-      const int t = f >> 2, ct = f & 3;
-      const uint8_t *xblk = base + S::kX + (wt * 64 + ct * 16) * S::kXRow;
+      const int t = f / kTB, ct = f % kTB;
+      const uint8_t *xblk = base + S::kX + (tok0 + ct * 16) * S::kXRow;
       const glm_u32x4 b0 = *reinterpret_cast<const glm_u32x4 *>(xblk + xl[t][0]);
       if constexpr (S::kParts == 2) {
         const glm_u32x4 b1 = *reinterpret_cast<const glm_u32x4 *>(xblk + xl[t][1]);
@@ -747,32 +756,19 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
         xb = glm_i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], 0, 0, 0, 0};
       }
       xsc = (int)(*reinterpret_cast<const uint32_t *>(
-                      base + S::kXS + (t * kTileM + wt * 64 + ct * 16) * 4 + sl) >>
+                      base + S::kXS + (t * kSplitTileM + tok0 + ct * 16) * 4 + sl) >>
                   (8 * q));
     };
-    // Fragment f + 1 is read from LDS before fragment f's MFMAs issue, so
-    // its latency hides behind them; one fragment ahead bounds the live
-    // registers.
-    glm_i32x8 xb;
-    int xsc;
-    xfrag(0, xb, xsc);
 #pragma unroll
     for (int f = 0; f < kFrags; ++f) {
-      glm_i32x8 xn;
-      int xscn = 0;
-      if (f + 1 < kFrags) xfrag(f + 1, xn, xscn);
-      // token blocks wholly past the tile's rows (the last, partial tile of
-      // an expert) are skipped: their columns are never stored
-      if (wt * 64 + (f & 3) * 16 < rows) {
+      if (tok0 + (f % kTB) * 16 < tend) {
+        glm_i32x8 xb;
+        int xsc;
+        xfrag(f, xb, xsc);
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt)
-          acc[rt][f & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              wa[rt], xb, acc[rt][f & 3], 4, S::kMfmaFmt, 0, wsc[rt], 0, xsc);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      if (f + 1 < kFrags) {
-        xb = xn;
-        xsc = xscn;
+          acc[rt][f % kTB] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              wa[rt], xb, acc[rt][f % kTB], 4, S::kMfmaFmt, 0, wsc[rt], 0, xsc);
       }
     }
   };
@@ -800,8 +796,9 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
       const SplitLayout L(a.out_rows, a.N);
       const int g0 = f0 + wf * 32;
 #pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        const int row = wt * 64 + ct * 16 + r;
+      for (int ct = 0; ct < kTB; ++ct) {
+        if (tok0 + ct * 16 >= tend) continue;
+        const int row = tok0 + ct * 16 + r;
         float v[8];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -831,9 +828,9 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
     }
   }
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    const int row = wt * 64 + ct * 16 + r;
-    if (row >= rows) continue;
+  for (int ct = 0; ct < kTB; ++ct) {
+    const int row = tok0 + ct * 16 + r;
+    if (tok0 + ct * 16 >= tend || row >= rows) continue;
     uint16_t *orow = a.out + (size_t)(pos0 + row) * a.N;
     if constexpr (NPROJ == 2) {
 #pragma unroll
@@ -861,7 +858,7 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
 
 using namespace glm;
 
-int glm_grouped_tile_rows() { return kTileM; }
+int glm_grouped_tile_rows() { return kSplitTileM; }
 
 // Whether the grouped GEMMs cover these shapes: gate/up K = d, N = I in
 // feature tiles of 128 per projection; down K = I, N = d in tiles of 256.

@@ -219,6 +219,14 @@ def test_router_nan_choice_ranks_as_minus_inf(gu, T, groups):
     _check_indices(got_l, idx, choice, 4)
 
 
+def _row_tiles(e, off, c):
+    """glm_moe_tiles' rule: ceil(c / 160) tiles, the 16-row blocks dealt out
+    evenly (tile i starts at block floor(i B / nt))."""
+    nt, blocks = -(-c // 160), -(-c // 16)
+    starts = [16 * (i * blocks // nt) for i in range(nt)] + [c]
+    return [(e, off + starts[i], min(starts[i + 1], c) - starts[i]) for i in range(nt)]
+
+
 def _work_list(counts, offsets, active, E):
     work = np.tile(np.array([-1, 0, 0, 0], np.int32), (E, 1))
     for u, e in enumerate(active):
@@ -387,10 +395,19 @@ def test_grouped_expert_gemms_parity(gu):
     tiles = torch.empty((max_tiles, 4), dtype=torch.int32, device="cuda")
     ntiles = torch.empty(1, dtype=torch.int32, device="cuda")
     gu.call("glm_moe_tiles", gu.stream(), gu.p(work), E, gu.p(tiles), gu.p(ntiles))
-    want_tiles = [(e, int(offsets[e]) + i, min(128, int(counts[e]) - i))
-                  for e in active for i in range(0, int(counts[e]), 128)]
+    want_tiles = [t for e in active for t in _row_tiles(e, int(offsets[e]), int(counts[e]))]
     assert int(gu.host(ntiles)[0]) == len(want_tiles)
-    assert [tuple(int(v) for v in t[:3]) for t in gu.host(tiles)[:len(want_tiles)]] == want_tiles
+    got_tiles = [tuple(int(v) for v in t[:3]) for t in gu.host(tiles)[:len(want_tiles)]]
+    assert got_tiles == want_tiles
+    # the tiles partition every expert's rows, at most 160 rows each, all but
+    # an expert's last a whole number of 16-row blocks, the fewest possible
+    for e in active:
+        mine = [t for t in got_tiles if t[0] == e]
+        assert len(mine) == -(-int(counts[e]) // 160)
+        assert mine[0][1] == int(offsets[e])
+        assert all(a[1] + a[2] == b[1] for a, b in zip(mine, mine[1:]))
+        assert mine[-1][1] + mine[-1][2] == int(offsets[e]) + int(counts[e])
+        assert all(0 < t[2] <= 160 for t in mine) and all(t[2] % 16 == 0 for t in mine[:-1])
     d_tok = gu.to_dev((perm // k).astype(np.int32))
     h = torch.empty((P, I), dtype=torch.bfloat16, device="cuda")
     y = torch.empty((P, d), dtype=torch.bfloat16, device="cuda")
