@@ -115,15 +115,6 @@ __host__ __device__ inline long long mxfp4_tile_piece(long long row, long long p
   return ((row >> 4) * (K / 128) + (p >> 2)) * 64 + (row & 15) + 16 * (p & 3);
 }
 
-// sigmoid with the hardware exp2 and reciprocal: within a few f32 ulp of
-// sigmoid_f32 (the bf16 rounding that follows absorbs that except within a
-// few ulp of a bf16 rounding tie), at a fraction of its instructions.
-__device__ __forceinline__ float sigmoid_fast(float x) {
-  const float e = __builtin_amdgcn_exp2f(fabsf(x) * 1.44269504088896341f);
-  const float y = __builtin_amdgcn_rcpf(1.0f + e);
-  return x < 0.0f ? y : 1.0f - y;
-}
-
 // limited_swiglu on one element with bf16 intermediates (expert_ssd.py:103-107):
 // g = min(g, L); u = clip(u, -L, L); h = bf16(bf16(g * bf16(sigmoid(g))) * u).
 __device__ __forceinline__ float limited_swiglu(float g, float u, float limit_bf16) {
@@ -136,17 +127,37 @@ __device__ __forceinline__ float limited_swiglu(float g, float u, float limit_bf
   return bf16_round(a * u);
 }
 
-// limited_swiglu with sigmoid_fast, for the epilogues of the many-token GEMMs
-// (64 of them per lane there, where the exact sigmoid's dependent chains do
-// not hide behind two waves per SIMD).
-__device__ __forceinline__ float limited_swiglu_fast(float g, float u, float limit_bf16) {
-  if (limit_bf16 > 0.0f) {
-    g = fminf(g, limit_bf16);
-    u = fminf(fmaxf(u, -limit_bf16), limit_bf16);
-  }
-  float s = bf16_round(sigmoid_fast(g));
-  float a = bf16_round(g * s);
-  return bf16_round(a * u);
+// Two f32 -> bf16 roundings (nearest even) in one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ void bf16_round2(float &a, float &b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  const uint32_t p = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+  a = __uint_as_float(p << 16);
+  b = __uint_as_float(p & 0xffff0000u);
+}
+
+// limited_swiglu on two elements with bf16 intermediates (expert_ssd.py:
+// 103-107), for the epilogues of the many-token GEMMs: g, u the bf16 gate and
+// up values; lim the bf16 limit, or +inf when there is none (NaN passes
+// through the clamps, as it does through the reference's).  The sigmoid is
+// 1 / (1 + 2^(-g log2 e)) on the hardware exp2 and reciprocal: within a few
+// f32 ulp of sigmoid_f32, which the bf16 rounding that follows absorbs except
+// within a few ulp of a bf16 rounding tie.  Each bf16 rounding of the pair
+// is one convert.
+__device__ __forceinline__ void limited_swiglu2_fast(float g0, float g1, float u0, float u1,
+                                                     float lim, float &h0, float &h1) {
+  g0 = g0 > lim ? lim : g0;
+  g1 = g1 > lim ? lim : g1;
+  u0 = u0 > lim ? lim : (u0 < -lim ? -lim : u0);
+  u1 = u1 > lim ? lim : (u1 < -lim ? -lim : u1);
+  float s0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g0 * -1.44269504088896341f));
+  float s1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g1 * -1.44269504088896341f));
+  bf16_round2(s0, s1);
+  float a0 = g0 * s0, a1 = g1 * s1;
+  bf16_round2(a0, a1);
+  h0 = a0 * u0;
+  h1 = a1 * u1;
+  bf16_round2(h0, h1);
 }
 
 // 8 packed E2M1 codes (one u32, low nibble first) -> 8 bf16 times `scale`,

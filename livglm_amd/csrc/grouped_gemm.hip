@@ -486,13 +486,23 @@ __global__ __launch_bounds__(256) void act_split_lowp_kernel(const uint16_t *x, 
 // lane's elements 16 i + 4 q + m at v[4 i + m].  Same arithmetic as
 // act_split_kernel: ch[i] / cl[i] are the hi / lo codes of elements
 // 16 i + 4 q .. + 3, bh / bl the group's scale bytes.
+// Maximum over the four lanes l, l ^ 16, l ^ 32, l ^ 48: gfx950's row swaps
+// (one VALU instruction each, no LDS round trip).
+__device__ __forceinline__ float quad_row_max(float v) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+  const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+}
+
 __device__ __forceinline__ void split_group_part(float v[8], uint32_t ch[2], uint32_t cl[2],
                                                  int *bh_out, int *bl_out) {
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
-  amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+  amax = quad_row_max(amax);
   const int bh = split_scale_byte(amax);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -509,8 +519,7 @@ __device__ __forceinline__ void split_group_part(float v[8], uint32_t ch[2], uin
   float ramax = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) ramax = fmaxf(ramax, fabsf(v[j]));
-  ramax = fmaxf(ramax, __shfl_xor(ramax, 16, 64));
-  ramax = fmaxf(ramax, __shfl_xor(ramax, 32, 64));
+  ramax = quad_row_max(ramax);
   const int bl = split_scale_byte(ramax);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -784,6 +793,16 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
     compute(c % kSplitStages);
   }
 
+  // SwiGLU of the gate/up sums m, m + 1 of one accumulator pair (gate block,
+  // up block), each projection rounded to bf16 first
+  const float lim = a.limit > 0.0f ? a.limit : __builtin_inff();
+  auto swiglu_pair = [&](const glm_f32x4 &g, const glm_f32x4 &u, int m, float &h0, float &h1) {
+    float g0 = g[m], g1 = g[m + 1], u0 = u[m], u1 = u[m + 1];
+    bf16_round2(g0, g1);
+    bf16_round2(u0, u1);
+    limited_swiglu2_fast(g0, g1, u0, u1, lim, h0, h1);
+  };
+
   // ---- epilogue: lane (r, q) of block (rt, ct) holds weight rows 4q..4q+3 of
   // the block for token column r
   if constexpr (NPROJ == 2 && AF == ACT_FP8X2) {
@@ -803,9 +822,8 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int m = 0; m < 4; ++m)
-            v[4 * i + m] = bf16_round(limited_swiglu_fast(bf16_round(acc[i][ct][m]),
-                                                          bf16_round(acc[2 + i][ct][m]), a.limit));
+          for (int m = 0; m < 4; m += 2)
+            swiglu_pair(acc[i][ct], acc[2 + i][ct], m, v[4 * i + m], v[4 * i + m + 1]);
         uint32_t ch[2], cl[2];
         int bh, bl;
         split_group_part(v, ch, cl, &bh, &bl);
@@ -835,11 +853,12 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
     if constexpr (NPROJ == 2) {
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
+        float h[4];
+        swiglu_pair(acc[i][ct], acc[2 + i][ct], 0, h[0], h[1]);
+        swiglu_pair(acc[i][ct], acc[2 + i][ct], 2, h[2], h[3]);
         uint32_t o[4];
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-          o[m] = f32_to_bf16(limited_swiglu_fast(bf16_round(acc[i][ct][m]),
-                                                 bf16_round(acc[2 + i][ct][m]), a.limit));
+        for (int m = 0; m < 4; ++m) o[m] = __float_as_uint(h[m]) >> 16;  // bf16-exact
         store_rows4(orow + f0 + wf * 32 + i * 16 + 4 * q, o);
       }
     } else {
