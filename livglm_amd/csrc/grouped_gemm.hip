@@ -28,6 +28,7 @@
 // row tile (which share its activation rows) and the row tiles of one expert
 // (which share its weights) then run side by side on one XCD and meet in its
 // L2.  Items past the real tile count (known only on the device) exit.
+#include "lds_stage.h"
 #include "mfma_tile.h"
 
 namespace glm {
@@ -68,12 +69,6 @@ struct Bf16Layout {
   __device__ static int wswz(int row) { return row & 7; }
 };
 
-// s_waitcnt immediate that waits for the vector-memory counter to reach n
-// (at most n of this wave's loads outstanding) and leaves the others alone.
-__host__ __device__ constexpr int vmcnt_imm(int n) {
-  return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
-}
-
 struct GroupedArgs {
   const uint16_t *act;       // gate/up: x [T][K]; down: h [T][K]
   int dense_rows;            // T: tiles of kTileM consecutive rows
@@ -88,32 +83,6 @@ struct GroupedArgs {
 // the LDS address is wave-uniform.
 __device__ __forceinline__ void load16_to_lds(const void *src, void *lds) {
   __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
-}
-
-// Buffer-resource forms: a wave-uniform base and size in scalar registers,
-// a 32-bit per-lane offset and a uniform per-chunk offset; reads past the
-// size return zeros.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
-                                           0x00020000);
-}
-__device__ __forceinline__ void buf16_to_lds(__amdgpu_buffer_rsrc_t rs, void *lds, uint32_t voff,
-                                             uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds, 16, voff, soff, 0, 0);
-}
-__device__ __forceinline__ void buf4_to_lds(__amdgpu_buffer_rsrc_t rs, void *lds, uint32_t voff,
-                                            uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds, 4, voff, soff, 0, 0);
-}
-
-// Workgroup barrier without a memory fence: the direct-to-LDS loads are
-// waited for explicitly (vmcnt) before it, and a fence here would make the
-// compiler wait for every load in flight, including the prefetched chunks.
-// The empty asm statements keep the compiler from moving LDS accesses across.
-__device__ __forceinline__ void ring_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
 }
 
 template <int NPROJ>

@@ -1,6 +1,7 @@
 // Router: logits GEMV + sigmoid/bias/group-mask/top-k/normalise.
 // Restates TopKRouter.__call__ (moe.py:36-63) for gfx950.
 #include "glm_common.h"
+#include "lds_stage.h"
 #include "topk_select.h"
 
 namespace glm {
@@ -153,9 +154,14 @@ __global__ __launch_bounds__(64 * KSPLIT) void router_gemm_kernel(
 // and f32 accumulation: the f32 dot product up to the summation order, at the
 // bf16 MFMA rate (a 32-wide K step is three bf16 MFMAs per tile instead of
 // eight f32 ones).
-// Workgroup = 64 tokens x 32 experts (4 x 2 tiles), 8 waves split K; each
-// wave keeps the next step's operands in flight, and the partial sums are
-// added in wave order through LDS, one tile per wave.
+// Workgroup = 64 tokens x 32 experts, eight waves, one 16 x 16 output tile
+// each over the whole of K.  K advances in chunks of 64: the chunk's 64 token
+// rows and 96 split-weight rows (3 parts x 32 experts) are staged in LDS by
+// direct-to-LDS wave loads of 8 rows x 128 B (whole cache lines), three stages
+// deep; piece p (16 bytes) of staged row R sits at p ^ (R & 7), so the MFMA
+// operand reads (16 rows x one piece column) spread over the banks.  (Loads
+// of 16 rows x 64 B straight into registers, one MFMA operand per lane, ran
+// at ~28 GB/s per CU: 23.2 against 16.6 us at T = 4096, E = 128, d = 2048.)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void router_weight_split_kernel(const float *__restrict__ w,
                                                                   long long n,
@@ -173,72 +179,94 @@ __global__ __launch_bounds__(256) void router_weight_split_kernel(const float *_
 }
 
 constexpr int kSplitRouterWaves = 8;
+constexpr int kRouterRows = 64 + 96;          // staged rows per chunk: tokens, then 3 x 32 weights
+constexpr int kRouterStageBytes = kRouterRows * 128;
+constexpr int kRouterStages = 3;
+constexpr int kRouterWaveLoads = kRouterRows / 8;  // 20 wave loads of 1 KB per chunk
+static_assert(kRouterWaveLoads <= 3 * kSplitRouterWaves, "three loads per wave and chunk");
+static_assert(kRouterStages == 3, "the ring's wait counts");
 
 __global__ __launch_bounds__(64 * kSplitRouterWaves) void router_gemm_bf16x3_kernel(
     const uint16_t *__restrict__ x, const uint16_t *__restrict__ ws, int T, int d, int E,
     float *__restrict__ logits) {
-  __shared__ glm_f32x4 red[kSplitRouterWaves][8][64];  // [wave][tile][lane], 64 KB
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // kRouterStages stages
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, q = lane >> 4;
   const int t0 = blockIdx.x * 64;
   const int e0 = blockIdx.y * 32;
-  const int kq = d / kSplitRouterWaves;  // this wave's K range, a multiple of 64
-  const int kb = wave * kq + 8 * q;
-  const size_t plane = (size_t)E * d;
-  const uint16_t *xr[4], *wr[2];
+  const int nchunks = d / 64;
+  // load j of wave w stages rows 8 g .. 8 g + 7, g = 8 j + w (j = 2: waves
+  // 4-7 repeat the loads of waves 0-3, so every wave issues three per chunk);
+  // lane l fetches piece (l & 7) ^ (row & 7) of row 8 g + (l >> 3)
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)((size_t)T * d * 2));
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(ws, (uint32_t)((size_t)3 * E * d * 2));
+  int gl[3];
+  uint32_t voff[3];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) xr[tt] = x + (size_t)min(t0 + 16 * tt + r, T - 1) * d + kb;
-#pragma unroll
-  for (int et = 0; et < 2; ++et) wr[et] = ws + (size_t)min(e0 + 16 * et + r, E - 1) * d + kb;
-  glm_f32x4 acc[4][2];
-#pragma unroll
-  for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-    for (int et = 0; et < 2; ++et) acc[tt][et] = glm_f32x4{0.f, 0.f, 0.f, 0.f};
-  // operands of a 32-wide K step: 4 token fragments, 2 x 3 weight fragments
-  auto load = [&](int k0, glm_bf16x8 xa[4], glm_bf16x8 wb[2][3]) {
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) xa[tt] = *reinterpret_cast<const glm_bf16x8 *>(xr[tt] + k0);
-#pragma unroll
-    for (int et = 0; et < 2; ++et)
-#pragma unroll
-      for (int p = 0; p < 3; ++p)
-        wb[et][p] = *reinterpret_cast<const glm_bf16x8 *>(wr[et] + p * plane + k0);
-  };
-  glm_bf16x8 xa[2][4], wb[2][2][3];
-  load(0, xa[0], wb[0]);
-  for (int k0 = 0; k0 < kq; k0 += 64) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int kn = k0 + 32 * (h + 1);
-      if (kn < kq) load(kn, xa[h ^ 1], wb[h ^ 1]);
-#pragma unroll
-      for (int p = 0; p < 3; ++p)
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-          for (int et = 0; et < 2; ++et)
-            acc[tt][et] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[h][tt], wb[h][et][p],
-                                                                  acc[tt][et], 0, 0, 0);
+  for (int j = 0; j < 3; ++j) {
+    const int g = j < 2 ? 8 * j + wave : 16 + (wave & 3);
+    gl[j] = g;
+    const int row = 8 * g + (lane >> 3), piece = (lane & 7) ^ (row & 7);
+    size_t src_row;
+    if (row < 64) {
+      src_row = (size_t)min(t0 + row, T - 1);
+    } else {
+      const int wr = row - 64, part = wr / 32;
+      src_row = (size_t)part * E + min(e0 + wr % 32, E - 1);
     }
+    voff[j] = (uint32_t)(src_row * d * 2) + 16u * piece;
   }
-  // wave w adds tile w of every wave in wave order
+  auto issue = [&](int c, int stage) {
+    uint8_t *base = smem + stage * kRouterStageBytes;
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt)
+    for (int j = 0; j < 3; ++j)
+      buf16_to_lds(j == 0 ? xrs : wrs, base + gl[j] * 1024, voff[j], c * 128);
+  };
+  // this wave's output tile: tokens 16 tt .. + 15, experts 16 et .. + 15
+  const int tt = wave >> 1, et = wave & 1;
+  glm_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int stage) {
+    const uint8_t *base = smem + stage * kRouterStageBytes;
 #pragma unroll
-    for (int et = 0; et < 2; ++et) red[wave][tt * 2 + et][lane] = acc[tt][et];
-  __syncthreads();
-  const int tile = wave, tt = tile >> 1, et = tile & 1;
-  glm_f32x4 sum = red[0][tile][lane];
+    for (int i = 0; i < 2; ++i) {
+      const int xr = 16 * tt + r;
+      const glm_bf16x8 xa =
+          *reinterpret_cast<const glm_bf16x8 *>(base + xr * 128 + 16 * ((4 * i + q) ^ (xr & 7)));
+      glm_bf16x8 wb[3];
 #pragma unroll
-  for (int w = 1; w < kSplitRouterWaves; ++w) sum += red[w][tile][lane];
+      for (int p = 0; p < 3; ++p) {
+        const int wr = 64 + 32 * p + 16 * et + r;
+        wb[p] = *reinterpret_cast<const glm_bf16x8 *>(base + wr * 128 +
+                                                      16 * ((4 * i + q) ^ (wr & 7)));
+      }
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, wb[p], acc, 0, 0, 0);
+    }
+  };
+  // ring: chunks c + 1 and c + 2 in flight while c is consumed (a deeper ring
+  // measured the same: the kernel is bound by the L2-to-LDS traffic of its
+  // tiles and the LDS operand reads, not by round trips); the barrier of
+  // iteration c also guarantees that every wave is done with chunk c - 1,
+  // whose stage the loads of chunk c + 2 overwrite
+  issue(0, 0);
+  if (nchunks > 1) issue(1, 1);
+  for (int c = 0; c < nchunks; ++c) {
+    if (c + 1 < nchunks)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(3));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    ring_barrier();
+    if (c + 2 < nchunks) issue(c + 2, (c + 2) % kRouterStages);
+    compute(c % kRouterStages);
+  }
   // lane (r, q) holds tokens 4q..4q+3 of the tile for expert e0 + 16 et + r
   const int e = e0 + 16 * et + r;
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     const int t = t0 + 16 * tt + 4 * q + m;
-    if (t < T && e < E) logits[(size_t)t * E + e] = sum[m];
+    if (t < T && e < E) logits[(size_t)t * E + e] = acc[m];
   }
 }
 
@@ -317,7 +345,8 @@ int glm_router_select_launch(hipStream_t stream, const float *logits, const floa
 // Whether the bf16-split router GEMM covers this call (it needs
 // glm_router_split_bytes of scratch for the split weights).
 bool glm_router_split_supported(int T, int d) {
-  return T >= 256 && d % (64 * glm::kSplitRouterWaves) == 0;
+  // (the staged loads address x through a 32-bit buffer range)
+  return T >= 256 && d % (64 * glm::kSplitRouterWaves) == 0 && (size_t)T * d * 2 < (1ull << 32);
 }
 
 size_t glm_router_split_bytes(int E, int d) { return (size_t)3 * E * d * 2; }
@@ -334,7 +363,8 @@ int glm_router_launch(hipStream_t stream, const uint16_t *x, int T, int d, const
                        stream, weight, n, wsplit);
     GLM_LAUNCH_CHECK("router_weight_split_kernel");
     const dim3 grid((T + 63) / 64, (E + 31) / 32);
-    hipLaunchKernelGGL(router_gemm_bf16x3_kernel, grid, dim3(64 * kSplitRouterWaves), 0, stream, x,
+    hipLaunchKernelGGL(router_gemm_bf16x3_kernel, grid, dim3(64 * kSplitRouterWaves),
+                       (size_t)kRouterStages * kRouterStageBytes, stream, x,
                        wsplit, T, d, E, logits);
   } else if (glm_router_gemm_supported(T, d)) {
     const int rc = glm_router_logits_launch(stream, x, T, d, weight, E, logits);
