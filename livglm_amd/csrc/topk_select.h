@@ -24,15 +24,18 @@ __device__ __forceinline__ int dpp_i32(int v) {
   return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, true);
 }
 
-// Maximum of an int over the wave: DPP within each row of 16 lanes (quad
-// swaps, then row rotations by 4 and 8), then the four row maxima in SALU.
+// Maximum of an int over the wave, left in every lane: DPP within each row
+// of 16 lanes (quad swaps, then row rotations by 4 and 8), then across the
+// rows through gfx950's row swaps -- all vector ALU, no scalar round trip.
 __device__ __forceinline__ int wave_max_i32(int v) {
   v = max(v, dpp_i32<0xB1>(v));   // quad_perm [1,0,3,2]
   v = max(v, dpp_i32<0x4E>(v));   // quad_perm [2,3,0,1]
   v = max(v, dpp_i32<0x124>(v));  // row_ror:4
   v = max(v, dpp_i32<0x128>(v));  // row_ror:8
-  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+  const auto s = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+  v = max((int)s[0], (int)s[1]);  // rows 0|1 and 2|3
+  const auto t = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+  return max((int)t[0], (int)t[1]);
 }
 
 // Signed-int key with the order of a non-NaN float (-0 must be folded to +0
@@ -110,7 +113,10 @@ __device__ void select_token(const float *logits_row, const float *bias, int E, 
     const float c = choice[i] != choice[i] ? -INFINITY : choice[i] + 0.0f;  // NaN -> -inf, -0 -> +0
     key[i] = lane + 64 * i < E ? order_key(c) : INT_MIN;
   }
-  // Branch-free rounds: lane k-1-r keeps round r's expert and score.
+  // Lane k-1-r keeps round r's expert and score.  The winner is almost always
+  // the only expert holding the maximum: one ballot names its lane, whose
+  // highest slot holding it is the slot.  On a tie the highest such slot over
+  // the wave wins, then the highest lane holding it there.
   int my_idx = 0;
   float my_w = 0.0f;
   for (int r = 0; r < k; ++r) {
@@ -118,26 +124,27 @@ __device__ void select_token(const float *logits_row, const float *bias, int E, 
 #pragma unroll
     for (int i = 1; i < EPL; ++i) m = max(m, key[i]);
     const int best = wave_max_i32(m);
-    unsigned long long bal = 0ull;
-    int slot = 0;
+    int slot_l = -1;  // this lane's highest slot holding the maximum
+    float sc_l = 0.0f;
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
-      const unsigned long long b = __ballot(key[i] == best);
-      if (b != 0ull) {  // wave-uniform: the highest matching slot wins
-        bal = b;
-        slot = i;
-      }
+      const bool hit = key[i] == best;
+      slot_l = hit ? i : slot_l;
+      sc_l = hit ? score[i] : sc_l;
     }
-    const int wl = 63 - __clzll((long long)bal);
-    float sc = score[0];
+    const unsigned long long bal = __ballot(slot_l >= 0);
+    int wl, slot;
+    if (__popcll(bal) == 1) {
+      wl = __ffsll((long long)bal) - 1;
+      slot = __builtin_amdgcn_readlane(slot_l, wl);
+    } else {
+      slot = wave_max_i32(slot_l);
+      wl = 63 - __clzll((long long)__ballot(slot_l == slot));
+    }
+    const float wsc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc_l), wl));
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      if (i == slot) {
-        sc = score[i];
-        if (lane == wl) key[i] = INT_MIN;
-      }
-    }
-    const float wsc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc), wl));
+    for (int i = 0; i < EPL; ++i)
+      if (lane == wl && i == slot) key[i] = INT_MIN;
     const bool mine = lane == k - 1 - r;
     my_idx = mine ? wl + 64 * slot : my_idx;
     my_w = mine ? wsc : my_w;
