@@ -573,6 +573,7 @@ struct SplitStage {
   static_assert(kSplitStages * kBytes <= 160 * 1024, "LDS stages exceed 160 KB");
   static_assert(kXBytes % 1024 == 0, "activation loads");
   static_assert(kWSBytes == 8 * 256 && kXSLanes <= 8 * 64, "scale loads per wave");
+  static_assert(kSplitWaves * 16 * 144 <= kBytes, "the down epilogue's staging fits a stage");
   __device__ static int xswz(int row) { return kXPieces == 16 ? (row & 15) : ((row >> 1) & 3); }
 };
 
@@ -814,12 +815,12 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
       return;
     }
   }
+  if constexpr (NPROJ == 2) {
 #pragma unroll
-  for (int ct = 0; ct < kTB; ++ct) {
-    const int row = tok0 + ct * 16 + r;
-    if (tok0 + ct * 16 >= tend || row >= rows) continue;
-    uint16_t *orow = a.out + (size_t)(pos0 + row) * a.N;
-    if constexpr (NPROJ == 2) {
+    for (int ct = 0; ct < kTB; ++ct) {
+      const int row = tok0 + ct * 16 + r;
+      if (tok0 + ct * 16 >= tend || row >= rows) continue;
+      uint16_t *orow = a.out + (size_t)(pos0 + row) * a.N;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         float h[4];
@@ -830,14 +831,40 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
         for (int m = 0; m < 4; ++m) o[m] = __float_as_uint(h[m]) >> 16;  // bf16-exact
         store_rows4(orow + f0 + wf * 32 + i * 16 + 4 * q, o);
       }
-    } else {
+    }
+  } else {
+    // y through LDS, so that every store writes whole 128-byte lines: per
+    // token block the wave's 16 rows x 64 features go to its own 16 x 144 B
+    // area of the stage no chunk occupies (the ring's last loads went to the
+    // other one), and come back as 16 contiguous bytes per lane, 8 lanes a
+    // row.  (Stored straight from the accumulators each instruction wrote
+    // 8 bytes into each of 16 rows.)
+    uint8_t *yst = smem + (nchunks % kSplitStages) * S::kBytes + wv * (16 * 144);
+    const int rr = lane >> 3, seg = lane & 7;
+#pragma unroll
+    for (int ct = 0; ct < kTB; ++ct) {
+      if (tok0 + ct * 16 >= tend) continue;
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt) {
         uint32_t o[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) o[m] = f32_to_bf16(acc[rt][ct][m]);
-        store_rows4(orow + f0 + wf * 64 + rt * 16 + 4 * q, o);
+        *reinterpret_cast<uint2 *>(yst + r * 144 + (rt * 16 + 4 * q) * 2) =
+            uint2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
       }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int row = tok0 + ct * 16 + 8 * h + rr;
+        const glm_u32x4 v = *reinterpret_cast<const glm_u32x4 *>(yst + (8 * h + rr) * 144 + 16 * seg);
+        if (row < rows)
+          *reinterpret_cast<glm_u32x4 *>(a.out + (size_t)(pos0 + row) * a.N + f0 + wf * 64 + 8 * seg) = v;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
 }
