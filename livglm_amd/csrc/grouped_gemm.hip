@@ -63,6 +63,7 @@ struct Bf16Layout {
   static constexpr int kLoads = kXLoads + kWLoads;  // per chunk, per thread
   static_assert(kXBytes % (kThreads * 16) == 0 && kWBytes % (kThreads * 16) == 0, "staging");
   static_assert(kStages * kStageBytes <= 160 * 1024, "LDS ring exceeds 160 KB");
+  static_assert(kWaves * 16 * 144 <= kStageBytes, "the down epilogue's staging fits a stage");
 
   // 128-byte rows of 8 pieces: swizzle over the row's low 3 bits
   __device__ static int xswz(int row) { return row & 7; }
@@ -204,29 +205,63 @@ __global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs
 
   // ---- epilogue: lane (r, q) of tile (rt, ct) holds features 4q..4q+3 of the
   // row tile for token column r
+  if constexpr (NPROJ == 2) {
+    // SwiGLU on pairs of elements (limited_swiglu2_fast: the hardware exp2 /
+    // reciprocal sigmoid, one packed convert per bf16 rounding of a pair)
+    const float lim = a.limit > 0.0f ? a.limit : __builtin_inff();
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    const int row = wt * 64 + ct * 16 + r;
-    if (row >= rows) continue;
-    uint16_t *orow = a.out + (size_t)(pos0 + row) * a.N;
-    if constexpr (NPROJ == 2) {
+    for (int ct = 0; ct < 4; ++ct) {
+      const int row = wt * 64 + ct * 16 + r;
+      if (row >= rows) continue;
+      uint16_t *orow = a.out + (size_t)(pos0 + row) * a.N;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
+        float h[4];
+#pragma unroll
+        for (int m = 0; m < 4; m += 2) {
+          float g0 = acc[i][ct][m], g1 = acc[i][ct][m + 1];
+          float u0 = acc[2 + i][ct][m], u1 = acc[2 + i][ct][m + 1];
+          bf16_round2(g0, g1);
+          bf16_round2(u0, u1);
+          limited_swiglu2_fast(g0, g1, u0, u1, lim, h[m], h[m + 1]);
+        }
         uint32_t o[4];
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-          o[m] = f32_to_bf16(limited_swiglu(bf16_round(acc[i][ct][m]),
-                                            bf16_round(acc[2 + i][ct][m]), a.limit));
+        for (int m = 0; m < 4; ++m) o[m] = __float_as_uint(h[m]) >> 16;  // bf16-exact
         store_rows4(orow + f0 + wf * 32 + i * 16 + 4 * q, o);
       }
-    } else {
+    }
+  } else {
+    // the output through LDS, so that every store writes whole 128-byte
+    // lines: per token block the wave's 16 rows x 64 features go to its own
+    // 16 x 144 B area of the stage no chunk occupies (the ring's last loads
+    // went to the other two) and come back 16 contiguous bytes per lane
+    uint8_t *yst = smem + (nchunks % kStages) * L::kStageBytes + wave * (16 * 144);
+    const int rr = lane >> 3, seg = lane & 7;
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      if (wt * 64 + ct * 16 >= rows) continue;
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt) {
         uint32_t o[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) o[m] = f32_to_bf16(acc[rt][ct][m]);
-        store_rows4(orow + f0 + wf * 64 + rt * 16 + 4 * q, o);
+        *reinterpret_cast<uint2 *>(yst + r * 144 + (rt * 16 + 4 * q) * 2) =
+            uint2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
       }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int row = wt * 64 + ct * 16 + 8 * h + rr;
+        const glm_u32x4 v = *reinterpret_cast<const glm_u32x4 *>(yst + (8 * h + rr) * 144 + 16 * seg);
+        if (row < rows)
+          *reinterpret_cast<glm_u32x4 *>(a.out + (size_t)(pos0 + row) * a.N + f0 + wf * 64 + 8 * seg) = v;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
 }
