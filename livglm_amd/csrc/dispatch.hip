@@ -175,7 +175,8 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
 
 // ---------------------------------------------------------------------------
 // Multi-workgroup dispatch for many pairs: the pairs are cut into chunks of
-// 1024 (one workgroup each).  (1) every chunk counts its experts; (2) one
+// 1024 (one workgroup each).  (1) every chunk counts its experts (done by the
+// scan's own workgroup when the chunk histograms fit its LDS); (2) one
 // workgroup turns the chunk counts into expert offsets and per-chunk bases
 // (bases[c][e] = offsets[e] + pairs of expert e in chunks < c), plus the work
 // list and row tiles; (3) every chunk ranks its pairs stably within the chunk
@@ -202,18 +203,51 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(
   if (tid == 0) row[E] = s_bad;
 }
 
+// FUSED: the same workgroup first counts the chunks itself, into LDS
+// histograms [nchunks][E] (dynamic LDS), reading the indices once; the chunk
+// bases then go to chunk_counts for the scatter as in the three-kernel form.
+template <bool FUSED>
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_scan_kernel(
-    int32_t *__restrict__ chunk_counts, int nchunks, int E, int32_t *__restrict__ counts,
-    int32_t *__restrict__ offsets, int32_t *__restrict__ active, int32_t *__restrict__ num_active,
-    int4 *__restrict__ work, int32_t *__restrict__ status, int tile_rows,
-    int4 *__restrict__ tiles, int32_t *__restrict__ num_tiles) {
+    const uint32_t *__restrict__ idx, int P, int32_t *__restrict__ chunk_counts, int nchunks,
+    int E, int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
+    int32_t *__restrict__ active, int32_t *__restrict__ num_active, int4 *__restrict__ work,
+    int32_t *__restrict__ status, int tile_rows, int4 *__restrict__ tiles,
+    int32_t *__restrict__ num_tiles) {
+  extern __shared__ int32_t hist[];  // FUSED: [nchunks][E]
   __shared__ int s_scan[kDispatchThreads / 64 + 1];
+  __shared__ int s_bad;
   const int tid = threadIdx.x;
-  // per expert: running sum over chunks (chunk_counts[c][e] becomes the
-  // exclusive base within the expert); bad flags OR-ed by thread 0
   int bad = 0;
-  if (tid == 0)
-    for (int c = 0; c < nchunks; ++c) bad |= chunk_counts[(size_t)c * (E + 1) + E];
+  if constexpr (FUSED) {
+    for (int i = tid; i < nchunks * E; i += kDispatchThreads) hist[i] = 0;
+    if (tid == 0) s_bad = 0;
+    __syncthreads();
+    // thread t takes pair t of every chunk, 16 chunks' loads at a time
+    for (int c0 = 0; c0 < nchunks; c0 += 16) {
+      uint32_t ev[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const long long p = (long long)(c0 + j) * kDispatchThreads + tid;
+        ev[j] = c0 + j < nchunks && p < P ? idx[p] : 0xffffffffu;
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const long long p = (long long)(c0 + j) * kDispatchThreads + tid;
+        if (c0 + j < nchunks && p < P) {
+          if (ev[j] < (uint32_t)E) atomicAdd(&hist[(c0 + j) * E + ev[j]], 1);
+          else s_bad = 1;
+        }
+      }
+    }
+    __syncthreads();
+    bad = s_bad;
+  } else {
+    // bad flags OR-ed by thread 0
+    if (tid == 0)
+      for (int c = 0; c < nchunks; ++c) bad |= chunk_counts[(size_t)c * (E + 1) + E];
+  }
+  // per expert: running sum over chunks (the count of chunk c becomes the
+  // exclusive base of chunk c within the expert)
   int carry = 0, carry_active = 0, carry_tiles = 0;
   for (int e0 = 0; e0 < E; e0 += kDispatchThreads) {
     const int e = e0 + tid;
@@ -224,10 +258,17 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_scan_kernel(
         int n[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j)
-          n[j] = c0 + j < nchunks ? chunk_counts[(size_t)(c0 + j) * (E + 1) + e] : 0;
+          n[j] = c0 + j >= nchunks ? 0
+                 : FUSED           ? hist[(c0 + j) * E + e]
+                                   : chunk_counts[(size_t)(c0 + j) * (E + 1) + e];
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-          if (c0 + j < nchunks) chunk_counts[(size_t)(c0 + j) * (E + 1) + e] = c_e;
+          if (c0 + j < nchunks) {
+            if (FUSED)
+              hist[(c0 + j) * E + e] = c_e;
+            else
+              chunk_counts[(size_t)(c0 + j) * (E + 1) + e] = c_e;
+          }
           c_e += n[j];
         }
       }
@@ -247,7 +288,9 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_scan_kernel(
         int v[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j)
-          v[j] = c0 + j < nchunks ? chunk_counts[(size_t)(c0 + j) * (E + 1) + e] : 0;
+          v[j] = c0 + j >= nchunks ? 0
+                 : FUSED           ? hist[(c0 + j) * E + e]
+                                   : chunk_counts[(size_t)(c0 + j) * (E + 1) + e];
 #pragma unroll
         for (int j = 0; j < 16; ++j)
           if (c0 + j < nchunks) chunk_counts[(size_t)(c0 + j) * (E + 1) + e] = v[j] + off;
@@ -398,13 +441,23 @@ int glm_dispatch_launch(hipStream_t stream, const uint32_t *indices, int T, int 
                   "dispatch: %d chunks x %d experts do not fit in pair_token", nchunks, E + 1);
       chunk_scratch = pair_token;
     }
-    hipLaunchKernelGGL(glm::dispatch_count_kernel, dim3(nchunks), dim3(glm::kDispatchThreads),
-                       (size_t)E * 4, stream, indices, P, E, chunk_scratch);
-    GLM_LAUNCH_CHECK("dispatch_count_kernel");
-    hipLaunchKernelGGL(glm::dispatch_scan_kernel, dim3(1), dim3(glm::kDispatchThreads), 0,
-                       stream, chunk_scratch, nchunks, E, counts, offsets, active, num_active,
-                       work, status, tile_rows, tiles, num_tiles);
-    GLM_LAUNCH_CHECK("dispatch_scan_kernel");
+    // the chunk histograms of one workgroup fit its LDS up to 64 KB (T*k
+    // pairs x E experts: 131,072 x 128): count and scan in one kernel
+    const size_t hist_bytes = (size_t)nchunks * E * 4;
+    if (hist_bytes <= 64 * 1024) {
+      hipLaunchKernelGGL(glm::dispatch_scan_kernel<true>, dim3(1), dim3(glm::kDispatchThreads),
+                         hist_bytes, stream, indices, P, chunk_scratch, nchunks, E, counts,
+                         offsets, active, num_active, work, status, tile_rows, tiles, num_tiles);
+      GLM_LAUNCH_CHECK("dispatch_scan_kernel");
+    } else {
+      hipLaunchKernelGGL(glm::dispatch_count_kernel, dim3(nchunks), dim3(glm::kDispatchThreads),
+                         (size_t)E * 4, stream, indices, P, E, chunk_scratch);
+      GLM_LAUNCH_CHECK("dispatch_count_kernel");
+      hipLaunchKernelGGL(glm::dispatch_scan_kernel<false>, dim3(1), dim3(glm::kDispatchThreads),
+                         0, stream, indices, P, chunk_scratch, nchunks, E, counts, offsets,
+                         active, num_active, work, status, tile_rows, tiles, num_tiles);
+      GLM_LAUNCH_CHECK("dispatch_scan_kernel");
+    }
     hipLaunchKernelGGL(glm::dispatch_scatter_kernel, dim3(nchunks), dim3(glm::kDispatchThreads),
                        (size_t)E * 32 * 4, stream, indices, P, k, E, chunk_scratch, perm, inv,
                        in_place ? nullptr : pair_token);

@@ -248,9 +248,13 @@ def _dispatch(gu, idx, E):
     return {n: gu.host(t) for n, t in bufs.items()}
 
 
+# (16384, 8, 288): the chunk histograms (128 x 288) exceed one workgroup's
+# 64 KB, so count and scan run as separate kernels; every other case above
+# 4096 pairs counts inside the scan's workgroup
 @pytest.mark.parametrize("T,k,E,kind", [
     (1, 2, 16, "distinct"), (2, 8, 128, "distinct"), (64, 8, 128, "skew"),
     (4096, 8, 128, "distinct"), (3000, 8, 288, "skew"), (5, 4, 8, "dups"), (1, 1, 1, "distinct"),
+    (16384, 8, 288, "dups"),
 ])
 def test_dispatch_bit_exact(gu, T, k, E, kind):
     rng = np.random.default_rng(T * 31 + k + E)
@@ -275,10 +279,11 @@ def test_dispatch_bit_exact(gu, T, k, E, kind):
     assert got["status"][0] == 0
 
 
-@pytest.mark.parametrize("T,k,E", [(2, 2, 4), (900, 8, 32)])
+@pytest.mark.parametrize("T,k,E", [(2, 2, 4), (900, 8, 32), (9000, 8, 448)])
 def test_dispatch_flags_out_of_range(gu, T, k, E):
-    # pairs with an index >= E are dropped on both the one-workgroup path and
-    # the chunk-parallel one (900 x 8 pairs): status 1, inv -1, the valid pairs
+    # pairs with an index >= E are dropped on the one-workgroup path, the
+    # chunk-parallel one with the counts in the scan's workgroup (900 x 8
+    # pairs) and with a separate count kernel (9000 x 8 x 448): status 1, inv -1, the valid pairs
     # sorted as if the others were absent, -1 past them in perm and pair_token
     rng = np.random.default_rng(E + T)
     idx = rng.integers(0, E, (T, k)).astype(np.int64)
