@@ -69,7 +69,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--workload", default="verify_t2",
                     help="decode_t1 | verify_t2 | batch_t64 | prefill_t4096 | stack42_t1 | "
-                         "bank_load")
+                         "bank_load | dispatch_t4096")
     ap.add_argument("--min-rotation-gb", type=float, default=4.0,
                     help="total size of the distinct layer banks the steps rotate over")
     ap.add_argument("--kernel-launches", type=int, default=128)
@@ -619,6 +619,8 @@ def main() -> int:
         return copy_probe(torch)
     if args.workload == "bank_load":
         return bank_load_bench(args, torch, np)
+    if args.workload == "dispatch_t4096":
+        return dispatch_bench(args, torch, np)
     if args.mode == "kernel":
         S = Setup(args, torch, np, args.workload, args.steps, args.warmup, args.min_rotation_gb)
         S.kernel_plans(args.kernel_launches)
@@ -909,6 +911,65 @@ def bank_load_bench(args, torch, np) -> int:
                          **host_cpu(), "kind": "port",
                          "sample": f"4 reads of one {n_read} B range of a shard in the page cache "
                                    "into pinned host memory (glm_file_read_ranges)"},
+    }
+    print(json.dumps(line))
+    return 0
+
+
+def dispatch_bench(args, torch, np) -> int:
+    """The public glm_moe_dispatch at T=4096, k=8, E=128 (32,768 pairs, random
+    distinct top-8 of every token): 10 calls, then args.steps back-to-back
+    calls timed with HIP events on the calling stream.  The CPU baseline is the
+    oracle's dispatch (stable argsort) on the same indices."""
+    from livglm_amd import native
+
+    T, k, E = 4096, 8, 128
+    P = T * k
+    rng = np.random.default_rng(args.seed)
+    idx_np = np.argsort(rng.random((T, E)), axis=1)[:, :k].astype(np.int32)
+    native.load()
+    dev = torch.device("cuda:0")
+    idx = torch.from_numpy(idx_np).to(dev)
+    i32 = dict(dtype=torch.int32, device=dev)
+    names = ("counts", "offsets", "perm", "inv", "pair_token", "active", "num_active", "work",
+             "status")
+    sizes = (E, E + 1, P, P, P, E, 1, 4 * E, 1)
+    b = {n: torch.empty(sz, **i32) for n, sz in zip(names, sizes)}
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def call():
+        native.call("glm_moe_dispatch", stream, idx.data_ptr(), T, k, E,
+                    *(b[n].data_ptr() for n in names))
+
+    for _ in range(10):
+        call()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        call()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / args.steps
+    # CPU baseline: the oracle's dispatch, timed on the same indices
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import moe_oracle as O
+    t0 = time.perf_counter()
+    reps = 0
+    while time.perf_counter() - t0 < max(0.2, args.cpu_seconds):
+        O.dispatch(idx_np, E)
+        reps += 1
+    cpu_us = (time.perf_counter() - t0) * 1e6 / reps
+    line = {
+        "metric": "glm_moe_dispatch time per call", "value": round(us, 3), "unit": "us",
+        "n_gpus": 1, "steps": args.steps, "warmup": 10, "ms_per_step": round(us / 1e3, 6),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "int32",
+        "data": "synthetic",
+        "config": {"workload": f"dispatch_t4096: glm_moe_dispatch T={T} k={k} E={E} "
+                               f"({P} pairs, distinct top-{k} per token)"},
+        "cpu_baseline": {"value": round(cpu_us, 1), "unit": "us", "cores": 1, **host_cpu(),
+                         "kind": "port", "sample": f"the oracle's dispatch on the same indices, "
+                                                   f"{reps} calls"},
     }
     print(json.dumps(line))
     return 0
