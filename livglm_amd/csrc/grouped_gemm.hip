@@ -634,7 +634,10 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
   const int wf = wv & 7, wt = wv >> 3;
   const int4 tile = a.tiles[tile_id];
   const long long e = tile.x;
-  const int pos0 = tile.y, rows = tile.z;
+  // (a tile list from glm_moe_tiles has at most kSplitTileM rows a tile; a
+  // longer tile from elsewhere is cut there, so no row past the staged ones
+  // is read or stored)
+  const int pos0 = tile.y, rows = min(tile.z, kSplitTileM);
   const int K = a.K;
   const int nchunks = K / 128;
   constexpr int kHalf = kSplitTileW / 2;
