@@ -340,66 +340,69 @@ __device__ __forceinline__ int fit_scale_byte(float amax, float mmax, int emax) 
 // E4M3FN: maximum 448 = 0.875 2^9
 __device__ __forceinline__ int split_scale_byte(float amax) { return fit_scale_byte(amax, 0.875f, 9); }
 
-// One thread per 32-element group: hi/lo E4M3FN codes and their scales.
+// Four lanes per 32-element group, eight elements each: hi/lo E4M3FN codes and
+// their scales.  A wave loads 1 KB of contiguous bf16 per instruction and
+// stores 512 contiguous bytes of codes; the group maxima are combined over the
+// lane quad with DPP.  (One lane per group loaded 64 B strides per instruction.)
+__device__ __forceinline__ float quad_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, true)));
+  return fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, true)));
+}
 __global__ __launch_bounds__(256) void act_split_kernel(const uint16_t *x, long long groups,
                                                         uint8_t *hi, uint8_t *lo, uint8_t *shi,
                                                         uint8_t *slo) {
-  const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (g >= groups) return;
-  const glm_u32x4 *src = reinterpret_cast<const glm_u32x4 *>(x + g * 32);
-  float v[32];
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long g = i >> 2;
+  const int part = (int)(i & 3);  // elements 8 part .. 8 part + 7 of the group
+  if (g >= groups) return;        // whole lane quads leave together
+  const glm_u32x4 w = *reinterpret_cast<const glm_u32x4 *>(x + g * 32 + 8 * part);
+  float v[8];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const glm_u32x4 w = src[j];
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      v[8 * j + 2 * h] = __uint_as_float(w[h] << 16);
-      v[8 * j + 2 * h + 1] = __uint_as_float(w[h] & 0xffff0000u);
-    }
+  for (int h = 0; h < 4; ++h) {
+    v[2 * h] = __uint_as_float(w[h] << 16);
+    v[2 * h + 1] = __uint_as_float(w[h] & 0xffff0000u);
   }
   float amax = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
-  const int bh = split_scale_byte(amax);
-  uint32_t ch[8];
+  for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+  const int bh = split_scale_byte(quad_max(amax));
+  uint32_t ch[2];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    int w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j], 127 - bh),
+  for (int j = 0; j < 2; ++j) {
+    int c = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j], 127 - bh),
                                             ldexpf(v[4 * j + 1], 127 - bh), 0, false);
-    w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j + 2], 127 - bh),
-                                        ldexpf(v[4 * j + 3], 127 - bh), w, true);
-    ch[j] = (uint32_t)w;
+    c = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j + 2], 127 - bh),
+                                        ldexpf(v[4 * j + 3], 127 - bh), c, true);
+    ch[j] = (uint32_t)c;
   }
   // residuals (exact in f32) and their own scale
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int c = (int)ch[j];
+    v[4 * j] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(c, 0), bh - 127);
+    v[4 * j + 1] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(c, 1), bh - 127);
+    v[4 * j + 2] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(c, 2), bh - 127);
+    v[4 * j + 3] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(c, 3), bh - 127);
+  }
   float ramax = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int w = (int)ch[j];
-    v[4 * j] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 0), bh - 127);
-    v[4 * j + 1] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 1), bh - 127);
-    v[4 * j + 2] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 2), bh - 127);
-    v[4 * j + 3] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 3), bh - 127);
-  }
+  for (int j = 0; j < 8; ++j) ramax = fmaxf(ramax, fabsf(v[j]));
+  const int bl = split_scale_byte(quad_max(ramax));
+  uint32_t cl[2];
 #pragma unroll
-  for (int j = 0; j < 32; ++j) ramax = fmaxf(ramax, fabsf(v[j]));
-  const int bl = split_scale_byte(ramax);
-  uint32_t cl[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    int w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j], 127 - bl),
+  for (int j = 0; j < 2; ++j) {
+    int c = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j], 127 - bl),
                                             ldexpf(v[4 * j + 1], 127 - bl), 0, false);
-    w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j + 2], 127 - bl),
-                                        ldexpf(v[4 * j + 3], 127 - bl), w, true);
-    cl[j] = (uint32_t)w;
+    c = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j + 2], 127 - bl),
+                                        ldexpf(v[4 * j + 3], 127 - bl), c, true);
+    cl[j] = (uint32_t)c;
   }
-  glm_u32x4 *dh = reinterpret_cast<glm_u32x4 *>(hi + g * 32);
-  glm_u32x4 *dl = reinterpret_cast<glm_u32x4 *>(lo + g * 32);
-  dh[0] = glm_u32x4{ch[0], ch[1], ch[2], ch[3]};
-  dh[1] = glm_u32x4{ch[4], ch[5], ch[6], ch[7]};
-  dl[0] = glm_u32x4{cl[0], cl[1], cl[2], cl[3]};
-  dl[1] = glm_u32x4{cl[4], cl[5], cl[6], cl[7]};
-  shi[g] = (uint8_t)bh;
-  slo[g] = (uint8_t)bl;
+  *reinterpret_cast<uint2 *>(hi + g * 32 + 8 * part) = uint2{ch[0], ch[1]};
+  *reinterpret_cast<uint2 *>(lo + g * 32 + 8 * part) = uint2{cl[0], cl[1]};
+  if (part == 0) {
+    shi[g] = (uint8_t)bh;
+    slo[g] = (uint8_t)bl;
+  }
 }
 
 // E2M3 / E2M1 code of v 2^(127 - b), round to nearest even, saturating at the
@@ -952,7 +955,8 @@ static int act_split_launch_as(hipStream_t stream, const uint16_t *x, long long 
   uint8_t *base = static_cast<uint8_t *>(split);
   const dim3 grid((unsigned)((groups + 255) / 256));
   if (af == ACT_FP8X2)
-    hipLaunchKernelGGL(act_split_kernel, grid, dim3(256), 0, stream, x, groups, base,
+    hipLaunchKernelGGL(act_split_kernel, dim3((unsigned)((4 * groups + 255) / 256)), dim3(256), 0,
+                       stream, x, groups, base,
                        base + L.lo, base + L.shi, base + L.slo);
   else if (af == ACT_FP6X2)
     hipLaunchKernelGGL(act_split_lowp_kernel<ACT_FP6X2>, grid, dim3(256), 0, stream, x, groups, K,
