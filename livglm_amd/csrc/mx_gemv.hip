@@ -431,6 +431,104 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(const LinearRowsArgs a
   }
 }
 
+// MXFP8 weights with the K columns interleaved over the lanes: in step j
+// lane l takes columns 256 j + 4 l .. + 3 of its wave's two rows (one dword
+// of codes and its scale byte per row) and of each token (16 bytes of f32 or
+// 8 of bf16 x).  Every load instruction of the wave then reads one contiguous
+// stretch (256 B of codes, 1 KB of f32 x); with 32-wide slices per lane each
+// 16-byte piece of a lane's x lies on its own 128-byte line, 64 lines per
+// instruction.  The same kernel serves bf16 and f32 x, so the two entry
+// points agree bit for bit.
+constexpr int kMx8Steps = 8;  // 256-column steps per pass (K = 2048: one pass)
+
+template <bool XF32>
+__device__ __forceinline__ void x_cols4(const void *x, size_t off, glm_bf16x2 &p0, glm_bf16x2 &p1) {
+  if constexpr (XF32) {
+    const glm_f32x4 v = *reinterpret_cast<const glm_f32x4 *>(static_cast<const float *>(x) + off);
+    p0[0] = (__bf16)v[0];
+    p0[1] = (__bf16)v[1];
+    p1[0] = (__bf16)v[2];
+    p1[1] = (__bf16)v[3];
+  } else {
+    typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+    const bf16x4 v = *reinterpret_cast<const bf16x4 *>(static_cast<const uint16_t *>(x) + off);
+    p0 = __builtin_shufflevector(v, v, 0, 1);
+    p1 = __builtin_shufflevector(v, v, 2, 3);
+  }
+}
+
+template <bool XF32>
+__global__ __launch_bounds__(256) void linear_mx8_kernel(const LinearRowsArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kRowsPerWave;
+  const int K = a.K, steps = K / 256;
+  float acc[kRowsPerWave][kLinearMaxT];
+#pragma unroll
+  for (int rr = 0; rr < kRowsPerWave; ++rr)
+#pragma unroll
+    for (int t = 0; t < kLinearMaxT; ++t) acc[rr][t] = 0.0f;
+  for (int j0 = 0; j0 < steps; j0 += kMx8Steps) {
+    // every load of the pass goes out before any use (steps past the end
+    // repeat the last one and are not added)
+    uint32_t code[kMx8Steps][kRowsPerWave], sb[kMx8Steps][kRowsPerWave];
+    glm_bf16x2 xp[kMx8Steps][2];
+#pragma unroll
+    for (int jj = 0; jj < kMx8Steps; ++jj) {
+      const int col = 256 * min(j0 + jj, steps - 1) + 4 * lane;
+#pragma unroll
+      for (int rr = 0; rr < kRowsPerWave; ++rr) {
+        code[jj][rr] = __builtin_nontemporal_load(
+            reinterpret_cast<const uint32_t *>(a.w + (size_t)(row0 + rr) * K + col));
+        sb[jj][rr] = a.s[(size_t)(row0 + rr) * (K / 32) + col / 32];
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < kMx8Steps; ++jj)
+      x_cols4<XF32>(a.x, 256 * min(j0 + jj, steps - 1) + 4 * lane, xp[jj][0], xp[jj][1]);
+    __builtin_amdgcn_sched_barrier(0);
+    glm_bf16x2 wp[kMx8Steps][kRowsPerWave][2];
+#pragma unroll
+    for (int jj = 0; jj < kMx8Steps; ++jj)
+#pragma unroll
+      for (int rr = 0; rr < kRowsPerWave; ++rr) {
+        const float sc = e8m0_to_f32(sb[jj][rr]);
+        wp[jj][rr][0] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(code[jj][rr], sc, false);
+        wp[jj][rr][1] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(code[jj][rr], sc, true);
+      }
+#pragma unroll
+    for (int t = 0; t < kLinearMaxT; ++t) {
+      if (t < a.T) {
+        if (t > 0) {
+#pragma unroll
+          for (int jj = 0; jj < kMx8Steps; ++jj)
+            x_cols4<XF32>(a.x, (size_t)t * K + 256 * min(j0 + jj, steps - 1) + 4 * lane,
+                          xp[jj][0], xp[jj][1]);
+        }
+#pragma unroll
+        for (int jj = 0; jj < kMx8Steps; ++jj) {
+          if (j0 + jj < steps) {
+#pragma unroll
+            for (int rr = 0; rr < kRowsPerWave; ++rr) {
+              acc[rr][t] = __builtin_amdgcn_fdot2_f32_bf16(wp[jj][rr][0], xp[jj][0], acc[rr][t], false);
+              acc[rr][t] = __builtin_amdgcn_fdot2_f32_bf16(wp[jj][rr][1], xp[jj][1], acc[rr][t], false);
+            }
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kLinearMaxT; ++t) {
+    if (t < a.T) {
+#pragma unroll
+      for (int rr = 0; rr < kRowsPerWave; ++rr) {
+        const float v = wave_sum(acc[rr][t]);
+        if (lane == 0) a.y[(size_t)t * a.N + row0 + rr] = (uint16_t)f32_to_bf16(v);
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Generic fallback for shapes the MFMA tiling does not cover (K % 128 or
 // N % 16 non-zero; e.g. the tiny test geometries).  One thread per output.
@@ -679,7 +777,12 @@ static int launch_linear_rows(hipStream_t stream, const void *x, int T, int in_d
   const dim3 grid(out_dims / (4 * glm::kRowsPerWave)), block(256);
   switch (fmt) {
     case GLM_FMT_MXFP4: hipLaunchKernelGGL((glm::linear_rows_kernel<GLM_FMT_MXFP4, XF32>), grid, block, 0, stream, a); break;
-    case GLM_FMT_MXFP8: hipLaunchKernelGGL((glm::linear_rows_kernel<GLM_FMT_MXFP8, XF32>), grid, block, 0, stream, a); break;
+    case GLM_FMT_MXFP8:
+      if (in_dims % 256 == 0)
+        hipLaunchKernelGGL((glm::linear_mx8_kernel<XF32>), grid, block, 0, stream, a);
+      else
+        hipLaunchKernelGGL((glm::linear_rows_kernel<GLM_FMT_MXFP8, XF32>), grid, block, 0, stream, a);
+      break;
     default: hipLaunchKernelGGL((glm::linear_rows_kernel<GLM_FMT_BF16, XF32>), grid, block, 0, stream, a); break;
   }
   GLM_LAUNCH_CHECK("linear_rows_kernel");
