@@ -114,12 +114,31 @@ __device__ __forceinline__ void load_wave_weights(WaveWeights<FMT, NPROJ, CPW> &
                                                   int q) {
   // Scales first, then the chunks in the order the MFMAs consume them: loads
   // complete in issue order, so chunk 0 can be converted while later chunks
-  // are still in flight.
+  // are still in flight.  A scale load touches the lines of 16 rows, so the
+  // CPW dwords of a row go out in as few loads as their alignment allows:
+  // every caller starts a wave at a multiple of CPW chunks of rows whose
+  // length is a multiple of CPW chunks, so they are 4 CPW-byte aligned.
 #pragma unroll
   for (int p = 0; p < NPROJ; ++p) {
     const uint32_t *s = reinterpret_cast<const uint32_t *>(srow[p] + (kbase >> 5));
+    if constexpr (CPW % 4 == 0) {
 #pragma unroll
-    for (int c = 0; c < CPW; ++c) ww.sd[p][c] = s[c];
+      for (int c = 0; c < CPW; c += 4) {
+        const glm_u32x4 v = *reinterpret_cast<const glm_u32x4 *>(s + c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ww.sd[p][c + i] = v[i];
+      }
+    } else if constexpr (CPW % 2 == 0) {
+#pragma unroll
+      for (int c = 0; c < CPW; c += 2) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(s + c);
+        ww.sd[p][c] = v.x;
+        ww.sd[p][c + 1] = v.y;
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < CPW; ++c) ww.sd[p][c] = s[c];
+    }
   }
 #pragma unroll
   for (int c = 0; c < CPW; ++c)
