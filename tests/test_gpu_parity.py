@@ -675,6 +675,33 @@ def test_linear_parity_and_f32_input(gu, fmt, T):
         assert rc == native.GLM_ERR_UNSUPPORTED_SHAPE
 
 
+@pytest.mark.parametrize("in_f", [1024, 2304, 4096])
+@pytest.mark.parametrize("T", [1, 4])
+def test_linear_mxfp8_column_steps(gu, in_f, T):
+    # the MXFP8 few-token linear walks K in passes of eight 256-column steps:
+    # K = 1024 fills half a pass, 2304 one pass and one step, 4096 two passes
+    torch = _torch()
+    rng = np.random.default_rng(5410 + in_f + T)
+    out_f = 512
+    w = O.f32_to_bf16_bits(rng.normal(0, 0.02, (out_f, in_f)).astype(np.float32))
+    c, sc = O.quantize_mx(w, 8, O.MX_RULE_NEAREST)
+    mat = O.dequant_mxfp8(c, sc)
+    codes, scales = gu.to_dev(c), gu.to_dev(sc)
+    x32 = (rng.normal(0, 1, (T, in_f)) * (1 + 2.0 ** -12)).astype(np.float32)
+    xb = O.f32_to_bf16_bits(x32)
+    want = O.linear_bf16(O.bf16_bits_to_f32(xb), mat)
+    y = torch.empty((T, out_f), dtype=torch.bfloat16, device="cuda")
+    gu.call("glm_linear", gu.stream(), gu.p(gu.to_dev(xb)), T, in_f, gu.p(codes), gu.p(scales),
+            native.GLM_FMT_MXFP8, out_f, gu.p(y))
+    got = O.bf16_bits_to_f32(gu.bf16_bits(y))
+    assert O.rel_l2(got, want) < REL_L2
+    assert np.mean(got == want) > 0.97
+    y32 = torch.empty_like(y)
+    gu.call("glm_linear_f32", gu.stream(), gu.p(torch.from_numpy(x32).cuda()), T, in_f,
+            gu.p(codes), gu.p(scales), native.GLM_FMT_MXFP8, out_f, gu.p(y32))
+    assert np.array_equal(gu.bf16_bits(y32), gu.bf16_bits(y))
+
+
 # --------------------------------------------------------------------------- whole layer
 
 
