@@ -738,7 +738,7 @@ def bank_load_bench(args, torch, np) -> int:
         payload = write_expert_checkpoint(root, shape, layers, args.seed,
                                           two_value_scales=bool(args.scalex))
         if args.scalex:
-            from glm53flash.scalex_layer import write_scalex_layer
+            from livglm_amd.workloads import write_scalex_layer
             for layer in layers:
                 shard = os.path.join(root, f"model-layer{layer:02d}.safetensors")
                 write_scalex_layer(shard, shard + ".sx", layer=layer, experts=shape.E)

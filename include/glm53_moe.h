@@ -209,6 +209,11 @@ int glm_act_split(void *stream, const uint16_t *x, int rows, int K, int act_form
  * expert_ssd.py:103-107,185-186).
  * x_split: glm_act_split_fp8 of x bf16 [T][d].  h bf16 [T*k][I] in sorted
  * order, token rows through pair_token (as glm_expert_gate_up).
+ * tiles int32 [max_tiles][4] {expert, first sorted row, rows, 0} as
+ * glm_moe_tiles writes them; the device-side *num_tiles is clamped to
+ * max_tiles and tiles with rows <= 0 or a negative expert or row are skipped,
+ * but expert ids must lie in the bank and rows inside h (the library is not
+ * given E or T*k here and cannot check them).
  * Limits: d % 512 == 0, I % 256 == 0.
  */
 int glm_expert_gate_up_grouped(void *stream, const void *x_split, int T, int d, int I,
@@ -323,9 +328,12 @@ int glm_moe_workspace_init(void *stream, void *workspace, size_t workspace_bytes
  * One whole routed-MoE layer on a bf16 [T][d] input.  Replaces
  * ExpertSSDMoE.__call__ / _call_impl (moe.py:96-201) with an HBM-resident
  * expert bank: router -> dispatch -> gate/up+SwiGLU -> down -> shared expert
- * -> weighted combine, all on `stream` with no host synchronisation.  For
- * decode sizes (T*k <= 512) it is five kernels: router logits, selection +
- * dispatch, routed (+ bf16 shared) gate/up, routed (+ shared) down, combine.
+ * -> weighted combine, all on `stream` with no host synchronisation.  Up to
+ * four tokens (top_k <= 8) it is three kernels: router logits (+ bf16 shared
+ * gate/up), top-k selection + routed gate/up (+ shared down), routed down +
+ * weighted combine.  Up to 64 tokens (T*k <= 512) it is the decode path:
+ * router logits, selection, dispatch (+ shared down), routed gate/up, routed
+ * down, combine.  Beyond that the dispatch and the grouped MFMA GEMMs.
  * shared_in (may be NULL): the shared expert's bf16 output [T][d] computed by
  * the caller -- e.g. with glm_dense_mlp on a second stream, overlapping the
  * routing -- in which case the shared weights are not read.
@@ -560,8 +568,10 @@ int glm_mxfp4_is_tiled(int rows, int K);
  * copy).  Exception positions must be ascending (the caller checks them; an
  * unordered list decodes wrongly but stays in bounds).  Replaces the per-call
  * Mode-B decode of the reference's ScaleX kernels (native_expert_ssd.py:
- * 653-694, docs/scalex-mode-b.md:29-33): here scales are decoded once, when
- * the layer is loaded into HBM.
+ * 653-694, docs/scalex-mode-b.md:29-33) for banks that keep plain scales:
+ * the loader decodes once, when the layer is loaded into HBM.  Banks that keep
+ * the Mode-B rows are decoded inside the few-token kernels on every call
+ * instead (glm_moe_forward_scalex).
  */
 int glm_scalex_decode(void *stream, const uint8_t *staging, int64_t staging_bytes,
                       const int64_t *records, int n, int64_t *device_table);

@@ -546,7 +546,8 @@ struct SplitArgs {
   uint32_t split_bytes;        // the split buffer starting at xhi (SplitLayout)
   const int32_t *act_index;    // sorted position -> activation row (nullptr: the position)
   const int4 *tiles;           // {expert, first sorted position, rows, 0}
-  const int32_t *num_tiles;
+  const int32_t *num_tiles;    // device-side count, read once and clamped to max_tiles
+  int max_tiles;               // entries of `tiles` (the grid is sized for them)
   const uint8_t *w[2];         // stacked MXFP4 weights [E][N][K/2] per projection
   const uint8_t *s[2];         // stacked E8M0 scales [E][N][K/32]
   long long w_stride, s_stride;
@@ -622,7 +623,9 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
   using S = SplitStage<AF>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int nft = a.feature_tiles;
-  const int ntiles = *a.num_tiles;
+  // a count above the list's length is clamped to it, so no entry past
+  // `tiles` is read and every item still has a workgroup in the grid
+  const int ntiles = max(0, min(*a.num_tiles, a.max_tiles));
   const int items = ntiles * nft;
   const int lin = blockIdx.x;
   const int per_xcd = (items + kXcds - 1) / kXcds;
@@ -630,12 +633,15 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
   const int item = (lin % kXcds) * per_xcd + k_on_xcd;
   if (k_on_xcd >= per_xcd || item >= items) return;
   const int tile_id = item / nft, ftile = item % nft;
+  const int4 tile = a.tiles[tile_id];
+  // an empty tile, or one with a negative expert or position, has no work
+  // (glm_moe_tiles writes none; the check keeps a caller's list in bounds)
+  if (tile.z <= 0 || tile.x < 0 || tile.y < 0) return;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform copy
   const int wf = wv & 7, wt = wv >> 3;
-  const int4 tile = a.tiles[tile_id];
   const long long e = tile.x;
   // (a tile list from glm_moe_tiles has at most kSplitTileM rows a tile; a
   // longer tile from elsewhere is cut there, so no row past the staged ones
@@ -982,6 +988,7 @@ static void launch_f8f6f4(hipStream_t stream, dim3 grid, const SplitArgs &a) {
 
 static int split_launch(hipStream_t stream, SplitArgs a, int nproj, int max_tiles, int af) {
   a.feature_tiles = a.N / (nproj == 2 ? kSplitTileW / 2 : kSplitTileW);
+  a.max_tiles = max_tiles;
   // XCD x handles items [x * per, (x + 1) * per) with per <= ceil(max_items / 8),
   // at linear ids x + 8k: the grid must reach 8 * ceil(max_items / 8)
   const long long max_items = (long long)max_tiles * a.feature_tiles;

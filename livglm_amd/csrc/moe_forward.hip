@@ -4,6 +4,7 @@
 #include <string>
 
 #include "glm_common.h"
+#include "scalex_tile.h"
 
 // ---------------------------------------------------------------- errors
 
@@ -330,6 +331,12 @@ extern "C" int glm_moe_forward_scalex(
   GLM_REQUIRE((long long)3 * I * (d / 32) < (1LL << 31), GLM_ERR_UNSUPPORTED_SHAPE,
               "moe_forward_scalex: %lld scales per expert exceed 2^31",
               (long long)3 * I * (d / 32));
+  // the kernels read each row's directory and record header at fixed offsets
+  const long long fixed = (long long)glm::scalex_dir_bytes((uint32_t)(3 * I * (d / 32))) + 24;
+  GLM_REQUIRE(scalex_stride >= fixed, GLM_ERR_INVALID_ARGUMENT,
+              "moe_forward_scalex: stride %lld is shorter than a row's directory and record "
+              "header (%lld bytes)",
+              (long long)scalex_stride, fixed);
   bool done = false;
   return moe_forward_core(stream_v, x, T, d, router_weight, router_bias, E, top_k, n_group,
                           topk_group, norm_topk_prob, routed_scaling_factor, I, gate_packed,

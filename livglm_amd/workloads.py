@@ -219,6 +219,96 @@ def write_expert_checkpoint(root: str, shape: MoEShape, layers, seed: int,
     return len(layers) * E * record
 
 
+def write_scalex_layer(source, destination, *, layer: int, experts: int):
+    """Test and benchmark fixture: writes the ScaleX container of a synthetic
+    safetensors shard that holds exactly the routed-expert tensors of
+    ``layer`` (experts 0 .. experts - 1) in the container format the package
+    reads (``glm53flash.scalex_layer``), then reads it back and verifies the
+    rebuild.  Every expert's coded scales must fit the Mode-B tile directory
+    (at most 65535 exceptions), or nothing is written; the file is written
+    beside ``destination`` and renamed onto it only once it verifies."""
+    import hashlib
+    import json
+    import os
+    from pathlib import Path
+
+    from glm53flash import scalex_layer as X
+    from glm53flash.checkpoint import read_safetensors_header
+    from glm53flash.scale_codec import (decode_mode_a, encode_mode_a, inspect_mode_a,
+                                        mode_b_tile_prefix)
+
+    src, dst = Path(source), Path(destination)
+    if X.is_scalex_file(src):
+        raise X.ScaleXError(f"{src} is already a ScaleX container")
+    if dst.exists():
+        raise X.ScaleXError(f"{dst} exists; not overwriting it")
+    base, header = read_safetensors_header(src)
+    names = {X.tensor_name(layer, e, c, p) for e in range(experts) for c in X.RECORD_ORDER
+             for p in ("weight_packed", "weight_scale")}
+    present = set(header) - {"__metadata__"}
+    if present != names:
+        extra, missing = sorted(present - names)[:3], sorted(names - present)[:3]
+        raise X.ScaleXError(f"{src}: not exactly layer {layer}'s {experts} experts "
+                            f"(extra {extra}, missing {missing})")
+    spans = X._payload_order(header)
+    if base + (spans[-1][1] if spans else 0) != src.stat().st_size:
+        raise X.ScaleXError(f"{src}: data area does not end at the end of the file")
+    with src.open("rb") as fh:
+        prefix = fh.read(base)
+
+        def read(n: str) -> bytes:
+            fh.seek(base + header[n]["data_offsets"][0])
+            return fh.read(X._header_size(header, n))
+
+        records, blobs = [], []
+        at = base
+        for e in range(experts):
+            scale_parts = [read(X.tensor_name(layer, e, c, "weight_scale")) for c in X.RECORD_ORDER]
+            weights = [read(X.tensor_name(layer, e, c, "weight_packed")) for c in X.RECORD_ORDER]
+            raw = b"".join(scale_parts)
+            coded = encode_mode_a(raw)
+            if decode_mode_a(coded) != raw:
+                raise X.ScaleXError(f"{src}: expert {e}'s scales do not survive coding")
+            mode_b_tile_prefix(coded)  # raises when the exceptions overflow the directory
+            records.append({
+                "expert": e, "stored_offset": at, "encoded_bytes": len(coded),
+                "decoded_bytes": len(raw), "codec": inspect_mode_a(coded).codec,
+                "scale_names": [X.tensor_name(layer, e, c, "weight_scale") for c in X.RECORD_ORDER],
+                "scale_nbytes": [len(p) for p in scale_parts],
+                "weight_names": [X.tensor_name(layer, e, c, "weight_packed")
+                                 for c in X.RECORD_ORDER],
+                "weight_nbytes": [len(w) for w in weights]})
+            blobs.append(coded + b"".join(weights))
+            at += len(blobs[-1])
+    digest = hashlib.sha256()
+    with src.open("rb") as fh:
+        while block := fh.read(16 << 20):
+            digest.update(block)
+    meta = {"format": X.FORMAT, "version": X.VERSION, "layer": int(layer),
+            "experts": int(experts), "scale_order": list(X.RECORD_ORDER),
+            "weight_order": list(X.RECORD_ORDER), "original_bytes": src.stat().st_size,
+            "original_sha256": digest.hexdigest(), "original_prefix_bytes": len(prefix),
+            "original_prefix_sha256": hashlib.sha256(prefix).hexdigest(), "records": records}
+    meta_raw = json.dumps(meta, sort_keys=True, separators=(",", ":")).encode()
+    tmp = dst.with_name(dst.name + f".partial{os.getpid()}")
+    try:
+        with tmp.open("xb") as out:
+            out.write(X.PREFIX.pack(X.MAGIC, X.VERSION, len(meta_raw), at))
+            out.write(meta_raw)
+            out.write(prefix)
+            for blob in blobs:
+                out.write(blob)
+        os.chmod(tmp, src.stat().st_mode)
+        X.ScaleXLayer.read(tmp).verify()
+        if dst.exists():
+            raise X.ScaleXError(f"{dst} exists; not overwriting it")
+        os.replace(tmp, dst)
+    finally:
+        if tmp.exists():
+            tmp.unlink()
+    return X.ScaleXLayer.read(dst)
+
+
 def make_hc(T: int, hc: int, d: int, seed: int, *, bf16_streams: bool = False):
     """Hyper-connection inputs of a decoder FFN site: streams f32 [T, hc, d]
     N(0, 1) (bf16-representable when ``bf16_streams``), fn f32

@@ -473,7 +473,7 @@ PINNING = {
     "e2m1_table": "OCP MX v1.0 closed form; every code checked",
     "unpack_e2m1_codes": "nibble order: MXFP4 round trip of N(0,s) weights gives cosine > 0.99 only "
                          "with low-nibble-first (reports/preflight.json:22-155 scale)",
-    "e4m3fn_table": "reference KAT tests/test_fp8.py:31-35 + NaN codes test_fp8.py:55-59",
+    "e4m3fn_table": "reference KAT tests/test_fp8.py:8-12 + NaN codes test_fp8.py:32-36",
     "e8m0_to_f32": "closed form 2**(e-127), all 256 bytes",
     "dequant_mxfp4/8": "closed forms above; group broadcast checked on one-hot scales",
     "mx_scale_exponent": "brute force against math.log2 on random and boundary values",

@@ -31,7 +31,6 @@ from dataclasses import dataclass
 import hashlib
 import json
 import math
-import os
 from pathlib import Path
 import re
 import struct
@@ -39,7 +38,7 @@ from typing import Any, Iterator
 
 from .checkpoint import ELEMENT_BYTES, read_safetensors_header
 from .contract import ContractError
-from .scale_codec import MODE_A_HEADER, decode_mode_a, encode_mode_a, inspect_mode_a
+from .scale_codec import MODE_A_HEADER, decode_mode_a, inspect_mode_a
 
 FORMAT = "livglm_scalex_layer_v1"
 MAGIC = b"LVGLMSX1"
@@ -319,71 +318,3 @@ class ScaleXLayer:
         if h.hexdigest() != self.original_sha256:
             raise ScaleXError(f"{self.path}: rebuilt original does not match original_sha256")
         return self.original_sha256
-
-
-def write_scalex_layer(source, destination, *, layer: int, experts: int) -> ScaleXLayer:
-    """Writes the ScaleX container of a safetensors shard that holds exactly the
-    routed-expert tensors of ``layer`` (experts 0 .. experts - 1), then reads it
-    back and verifies the rebuild."""
-    src, dst = Path(source), Path(destination)
-    if is_scalex_file(src):
-        raise ScaleXError(f"{src} is already a ScaleX container")
-    if dst.exists():
-        raise ScaleXError(f"{dst} exists; not overwriting it")
-    base, header = read_safetensors_header(src)
-    names = {tensor_name(layer, e, c, p) for e in range(experts) for c in RECORD_ORDER
-             for p in ("weight_packed", "weight_scale")}
-    present = set(header) - {"__metadata__"}
-    if present != names:
-        extra, missing = sorted(present - names)[:3], sorted(names - present)[:3]
-        raise ScaleXError(f"{src}: not exactly layer {layer}'s {experts} experts "
-                          f"(extra {extra}, missing {missing})")
-    spans = _payload_order(header)
-    if base + (spans[-1][1] if spans else 0) != src.stat().st_size:
-        raise ScaleXError(f"{src}: data area does not end at the end of the file")
-    with src.open("rb") as fh:
-        prefix = fh.read(base)
-
-        def read(n: str) -> bytes:
-            size = _header_size(header, n)
-            fh.seek(base + header[n]["data_offsets"][0])
-            return fh.read(size)
-
-        records, blobs = [], []
-        at = base
-        for e in range(experts):
-            scale_parts = [read(tensor_name(layer, e, c, "weight_scale")) for c in RECORD_ORDER]
-            weights = [read(tensor_name(layer, e, c, "weight_packed")) for c in RECORD_ORDER]
-            raw = b"".join(scale_parts)
-            coded = encode_mode_a(raw)
-            if decode_mode_a(coded) != raw:
-                raise ScaleXError(f"{src}: expert {e}'s scales do not survive coding")
-            records.append({
-                "expert": e, "stored_offset": at, "encoded_bytes": len(coded),
-                "decoded_bytes": len(raw), "codec": inspect_mode_a(coded).codec,
-                "scale_names": [tensor_name(layer, e, c, "weight_scale") for c in RECORD_ORDER],
-                "scale_nbytes": [len(p) for p in scale_parts],
-                "weight_names": [tensor_name(layer, e, c, "weight_packed") for c in RECORD_ORDER],
-                "weight_nbytes": [len(w) for w in weights]})
-            blobs.append(coded + b"".join(weights))
-            at += len(blobs[-1])
-    digest = hashlib.sha256()
-    with src.open("rb") as fh:
-        while block := fh.read(16 << 20):
-            digest.update(block)
-    meta = {"format": FORMAT, "version": VERSION, "layer": int(layer), "experts": int(experts),
-            "scale_order": list(RECORD_ORDER), "weight_order": list(RECORD_ORDER),
-            "original_bytes": src.stat().st_size, "original_sha256": digest.hexdigest(),
-            "original_prefix_bytes": len(prefix),
-            "original_prefix_sha256": hashlib.sha256(prefix).hexdigest(), "records": records}
-    meta_raw = json.dumps(meta, sort_keys=True, separators=(",", ":")).encode()
-    with dst.open("xb") as out:
-        out.write(PREFIX.pack(MAGIC, VERSION, len(meta_raw), at))
-        out.write(meta_raw)
-        out.write(prefix)
-        for blob in blobs:
-            out.write(blob)
-    os.chmod(dst, src.stat().st_mode)
-    written = ScaleXLayer.read(dst)
-    written.verify()
-    return written

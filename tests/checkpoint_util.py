@@ -107,7 +107,7 @@ def make_checkpoint(root: str, *, layers=(3, 4), E: int = 12, d: int = 64, I: in
         json.dump({"text_config": {"hidden_size": d, "moe_intermediate_size": I,
                                    "n_routed_experts": E}}, f)
     if scalex:
-        from glm53flash.scalex_layer import write_scalex_layer
+        from livglm_amd.workloads import write_scalex_layer
         assert shards_per_layer == 1 and not extras and not misalign
         for layer in layers:
             shard = os.path.join(root, f"model-layer{layer}-00.safetensors")

@@ -69,7 +69,8 @@ def upload_layer(layer: dict[str, np.ndarray], bank_layout: bool = True) -> dict
 
 
 def workspace(nbytes: int) -> torch.Tensor:
-    """A layer workspace, initialised through the C ABI (hand-off counters at zero)."""
+    """A layer workspace, zero-filled through the C ABI (glm_moe_forward does
+    not need it cleared; a defined initial state keeps failures reproducible)."""
     ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     call("glm_moe_workspace_init", stream(), p(ws), nbytes)
     return ws

@@ -1,10 +1,14 @@
 """GPU checks of glm_moe_forward_scalex: the few-token layer reading its
 routed experts' E8M0 scales as ScaleX Mode-B rows and decoding them inside
-the kernels must give, bit for bit, what glm_moe_forward gives on the decoded
-scales (the coding is lossless: docs/scalex-mode-b.md:8-20).  Banks mix the
-codec's three forms (one bit with exceptions, two bits, raw), and planted
-exceptions sit on 512-scale tile edges, on the first and last scale and at
-the borders of the gate, down and up segments."""
+the kernels (the reference decodes 512-scale tiles in threadgroup memory
+inside its QMV, src/glm53flash/native_expert_ssd.py:653-694) must match the
+oracle's layer on the decoded scales -- indices exact on clear-margin rows,
+weights to f32 rounding, outputs within rel-L2 2e-3 -- and must give, bit for
+bit, what glm_moe_forward gives on the decoded scales (the coding is
+lossless: docs/scalex-mode-b.md:8-20).  Banks mix the codec's three forms
+(one bit with exceptions, two bits, raw), and planted exceptions sit on
+512-scale tile edges, on the first and last scale and at the borders of the
+gate, down and up segments."""
 
 from __future__ import annotations
 
@@ -13,9 +17,13 @@ import pytest
 
 from glm53flash import scale_codec as C
 from livglm_amd import native
+from oracle import moe_oracle as O
 from livglm_amd.workloads import BANK_KEYS, MoEShape, concentrated_scales, make_layer
 
 pytestmark = pytest.mark.gpu
+
+REL_L2 = 2e-3  # bf16 layer-output tolerance against the oracle
+MARGIN = 1e-5  # choice-score gap below which top-k order may flip
 
 
 def _torch():
@@ -80,6 +88,20 @@ def _forward(gu, dl, shape, T, scalex=None):
     return gu.host(out), gu.host(w), gu.host(idx)
 
 
+def _oracle(layer, shape):
+    x = O.bf16_bits_to_f32(layer["x"])
+    sw = None
+    if shape.I_shared:
+        sw = tuple(O.bf16_bits_to_f32(layer[key])
+                   for key in ("shared.gate", "shared.up", "shared.down"))
+    return O.moe_layer(x, layer["router_weight"], layer["router_bias"],
+                       O.Bank(*(layer[key] for key in BANK_KEYS)), sw, top_k=shape.k,
+                       n_group=shape.n_group, topk_group=shape.topk_group,
+                       norm_topk_prob=shape.norm_topk_prob,
+                       routed_scaling_factor=shape.routed_scaling_factor,
+                       swiglu_limit=shape.swiglu_limit, return_intermediates=True)
+
+
 CASES = [
     # (T, d, E, k, I, I_shared, kinds)
     (2, 2048, 128, 8, 768, 768, ("one_bit",)),
@@ -92,7 +114,7 @@ CASES = [
 
 
 @pytest.mark.parametrize("case", CASES, ids=lambda c: f"T{c[0]}-d{c[1]}-E{c[2]}-I{c[4]}")
-def test_scalex_forward_is_bit_identical_to_decoded_scales(gu, case):
+def test_scalex_forward_matches_oracle_and_decoded_scales(gu, case):
     T, d, E, k, I, Is, kinds = case
     shape = MoEShape("scalex", T, d, E, k, I, Is)
     layer = make_layer(shape, 2100 + d + E)
@@ -113,6 +135,16 @@ def test_scalex_forward_is_bit_identical_to_decoded_scales(gu, case):
     for g, w_ in zip(got, want):
         assert np.array_equal(g.view(np.uint32) if g.dtype == np.float32 else g,
                               w_.view(np.uint32) if w_.dtype == np.float32 else w_)
+    # the in-kernel decode against the oracle's layer on the decoded scales
+    ref, inter = _oracle(layer, shape)
+    out, w, idx = got
+    idx = idx.astype(np.uint32)
+    sure = O.topk_margin(inter["choice"], k) > MARGIN
+    assert not np.any(np.any(idx != inter["indices"], axis=1) & sure)
+    same = np.all(idx == inter["indices"], axis=1)
+    assert same.sum() >= T - 1
+    np.testing.assert_allclose(w[same], inter["weights"][same], rtol=2e-6, atol=1e-7)
+    assert O.rel_l2(out[same], ref[same]) < REL_L2
 
 
 def test_scalex_forward_rejects_what_it_cannot_take(gu):

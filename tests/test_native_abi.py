@@ -224,6 +224,51 @@ def test_ffn_site_and_loader_entry_points_reject_bad_arguments(lib):
     assert "cover" in msg
 
 
+def _grouped_items(grid, nft, num_tiles, max_tiles, xcds=8):
+    """The block-scaled grouped kernels' workgroup -> (tile, feature tile)
+    mapping (grouped_f8f6f4_kernel), restated: the device-side count clamped
+    to max_tiles, XCD x taking the x-th contiguous share of the items."""
+    ntiles = max(0, min(num_tiles, max_tiles))
+    items = ntiles * nft
+    per = (items + xcds - 1) // xcds
+    out = []
+    for lin in range(grid):
+        k_on, item = lin // xcds, (lin % xcds) * per + lin // xcds
+        if k_on >= per or item >= items:
+            continue
+        out.append((item // nft, item % nft))
+    return out
+
+
+@pytest.mark.parametrize("max_tiles,nft", [(1, 6), (7, 3), (256, 6), (300, 4)])
+def test_grouped_item_mapping_stays_in_the_tile_list(max_tiles, nft):
+    # the launcher sizes the grid from max_tiles; whatever count the device
+    # holds, every item runs once and no tile past the list is read
+    grid = (max_tiles * nft + 7) // 8 * 8
+    for num_tiles in (0, 1, max_tiles // 2, max_tiles, max_tiles + 1, 10 * max_tiles + 3, -5):
+        got = _grouped_items(grid, nft, num_tiles, max_tiles)
+        n = max(0, min(num_tiles, max_tiles))
+        assert sorted(got) == [(t, f) for t in range(n) for f in range(nft)]
+        assert all(t < max_tiles for t, _ in got)
+
+
+def test_scalex_forward_rejects_short_stride_on_host(lib):
+    # a stride shorter than a row's directory + record header would make each
+    # expert's header reads land in the next row: refused before any launch
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    rows = ctypes.c_void_p(0x10000)  # 256-byte aligned
+    fixed = 24 + ((2 * ((3 * 768 * 64 + 511) // 512 + 1)) + 15) // 16 * 16  # 616 at d 2048, I 768
+    for stride, ok in ((256, False), (512, False), (768, True)):
+        assert (stride >= fixed) == ok
+        if ok:
+            continue
+        msg = _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_moe_forward_scalex", None, fake, 2,
+                      2048, fake, fake, 128, 8, 1, 1, 1, 2.5, 768, fake, fake, fake, rows, stride,
+                      0, native.GLM_FMT_BF16, None, None, None, None, None, None, None, 10.0,
+                      fake, 1 << 30, fake, None, None)
+        assert "directory" in msg
+
+
 def test_split_beyond_32_bit_offsets_is_rejected_on_host(lib):
     # the grouped GEMMs address an activation split through 32-bit offsets: a
     # split above 4 GiB is refused instead of read as zeros past the limit

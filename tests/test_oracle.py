@@ -38,11 +38,11 @@ def test_e2m1_table_matches_bit_fields():
 
 
 def test_e4m3fn_reference_known_answers():
-    # tests/test_fp8.py:31-35 of the reference
+    # tests/test_fp8.py:8-12 of the reference
     raw = np.array([0x00, 0x01, 0x38, 0x3C, 0x7E, 0xB8], dtype=np.uint8)
     expected = np.array([0.0, 2**-9, 1.0, 1.5, 448.0, -1.0], np.float32)
     np.testing.assert_array_equal(O.e4m3fn_table()[raw], expected)
-    # tests/test_fp8.py:55-59: 0x7F is the non-finite code
+    # tests/test_fp8.py:32-36: 0x7F is the non-finite code
     assert math.isnan(O.e4m3fn_table()[0x7F]) and math.isnan(O.e4m3fn_table()[0xFF])
     finite = O.e4m3fn_table()[np.arange(256) % 128 != 0x7F]
     assert np.all(np.isfinite(finite))

@@ -150,11 +150,43 @@ def test_container_round_trip_and_plan(tmp_path):
                           experts=E, layers=layers)
 
 
+def test_fixture_writer_refuses_directory_overflow_and_leaves_no_file(tmp_path, monkeypatch):
+    """An expert whose exceptions overflow the u16 Mode-B directory is refused
+    before anything is written, and a failed write leaves neither the
+    destination nor a partial file behind."""
+    from glm53flash import scale_codec
+    from livglm_amd.workloads import write_scalex_layer
+    E, d, I = 2, 64, 64
+    root = tmp_path / "ck"
+    make_checkpoint(str(root), layers=(3,), E=E, d=d, I=I, extras=False, shuffle=False)
+    src = root / "model-layer3-00.safetensors"
+
+    def overflow(encoded):
+        raise scale_codec.ScaleCodecError("70000 exceptions overflow the u16 tile directory")
+
+    monkeypatch.setattr(scale_codec, "mode_b_tile_prefix", overflow)
+    with pytest.raises(scale_codec.ScaleCodecError, match="overflow"):
+        write_scalex_layer(src, tmp_path / "x.sx", layer=3, experts=E)
+    monkeypatch.undo()
+    assert sorted(p.name for p in tmp_path.iterdir()) == ["ck"]
+    # a verification failure after the bytes are written removes the partial file
+    from glm53flash import scalex_layer as X
+
+    def bad_verify(self):
+        raise X.ScaleXError("rebuilt original does not match original_sha256")
+
+    monkeypatch.setattr(X.ScaleXLayer, "verify", bad_verify)
+    with pytest.raises(X.ScaleXError, match="does not match"):
+        write_scalex_layer(src, tmp_path / "y.sx", layer=3, experts=E)
+    assert sorted(p.name for p in tmp_path.iterdir()) == ["ck"]
+
+
 def test_container_reader_checks(tmp_path):
     """Metadata that disagrees with the stored data is refused with a reason."""
     import json
     import struct as st
-    from glm53flash.scalex_layer import PREFIX, write_scalex_layer
+    from glm53flash.scalex_layer import PREFIX
+    from livglm_amd.workloads import write_scalex_layer
     E, d, I = 3, 64, 64
     root = tmp_path / "ck"
     make_checkpoint(str(root), layers=(3,), E=E, d=d, I=I, extras=False, shuffle=False)
