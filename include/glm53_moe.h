@@ -183,21 +183,27 @@ int glm_act_split_fp8(void *stream, const uint16_t *x, int rows, int K, void *sp
  *                  ~3e-4 relative error on Gaussian rows; two MFMAs at the
  *                  FP6 rate (twice FP8's);
  *   GLM_ACT_FP4    one E2M1 term: ~12 % relative error; one MFMA at the FP4
- *                  rate.
+ *                  rate;
+ *   GLM_ACT_FP8FP6 hi E4M3FN + lo E2M3 of the exact residual: exact for
+ *                  elements at most two binades below their group maximum's,
+ *                  error at most max / 840 (~3e-4 relative on Gaussian rows,
+ *                  as FP6X2); the hi MFMA at the FP8 rate, the lo at FP6's.
  * Split layout (glm_act_split_bytes_fmt(rows, K, fmt) bytes, regions 256-byte
  * aligned): hi codes, lo codes, hi scales [rows][K/32], lo scales (FP4: codes,
  * scales).  Code rows: FP8X2 [K] one byte per element; FP4 [K/2], two codes
- * per byte, low nibble first; FP6X2 [K] in 128-byte chunks per 128 elements,
+ * per byte, low nibble first; FP6X2 (both terms) and FP8FP6 (the lo term; hi
+ * as FP8X2) [K] in 128-byte chunks per 128 elements,
  * group g's 32 codes packed 6 bits each, low bits first, bytes 0..15 at 16 g
  * and bytes 16..23 at 64 + 16 g (the rest zero).
  * No reference counterpart (the reference multiplies bf16 activations): the
  * lower-precision forms are speed/accuracy variants of the grouped GEMMs.
- * Limits: K % 32 == 0 (FP6X2: K % 128 == 0); glm_act_split_bytes_fmt returns
+ * Limits: K % 32 == 0 (FP6X2, FP8FP6: K % 128 == 0); glm_act_split_bytes_fmt returns
  * 0 outside them.
  */
 #define GLM_ACT_FP8X2 0
 #define GLM_ACT_FP6X2 1
 #define GLM_ACT_FP4 2
+#define GLM_ACT_FP8FP6 3
 size_t glm_act_split_bytes_fmt(int rows, int K, int act_format);
 int glm_act_split(void *stream, const uint16_t *x, int rows, int K, int act_format, void *split);
 

@@ -280,6 +280,9 @@ __global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs
 //   ACT_FP6X2  the same two-term form with E2M3 codes: ~3e-4 relative error
 //              on Gaussian rows, two MFMAs at the FP6 rate (twice FP8's).
 //   ACT_FP4    one E2M1 term: ~12 % relative error, one MFMA at the FP4 rate.
+//   ACT_FP8FP6 hi E4M3FN (FP8 rate) + lo E2M3 (FP6 rate): exact for elements
+//              at most two binades below their group maximum's; lo's
+//              two-bit exponent bounds the error by max / 840, as ACT_FP6X2's.
 // Each term's scale is the smallest power of two that keeps the group's
 // largest magnitude within the element format's maximum (448, 7.5, 6); lo
 // encodes the exact f32 residual x - hi.  The MFMAs accumulate in f32: no
@@ -298,7 +301,7 @@ __global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs
 // ---------------------------------------------------------------------------
 
 // Activation formats of the block-scaled GEMMs (the C ABI's act_format).
-constexpr int ACT_FP8X2 = 0, ACT_FP6X2 = 1, ACT_FP4 = 2;
+constexpr int ACT_FP8X2 = 0, ACT_FP6X2 = 1, ACT_FP4 = 2, ACT_FP8FP6 = 3;
 
 __host__ __device__ constexpr int act_terms(int af) { return af == ACT_FP4 ? 1 : 2; }
 // Stored code bytes of one term per activation row of K elements.
@@ -439,6 +442,60 @@ __device__ __forceinline__ void lowp_term(float v[32], int b, uint32_t out[6]) {
     out[pos >> 5] |= c << (pos & 31);
     if ((pos & 31) + w > 32) out[(pos >> 5) + 1] |= c >> (32 - (pos & 31));
   }
+}
+
+// One thread per 32-element group: the ACT_FP8FP6 split -- hi E4M3FN codes
+// and scale exactly as act_split_kernel forms them, lo the E2M3 code of the
+// exact residual in the ACT_FP6X2 layout.
+__global__ __launch_bounds__(256) void act_split_fp8fp6_kernel(const uint16_t *x, long long groups,
+                                                               int K, uint8_t *hi, uint8_t *lo,
+                                                               uint8_t *shi, uint8_t *slo) {
+  const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= groups) return;
+  const glm_u32x4 *src = reinterpret_cast<const glm_u32x4 *>(x + g * 32);
+  float v[32];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const glm_u32x4 w = src[j];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      v[8 * j + 2 * h] = __uint_as_float(w[h] << 16);
+      v[8 * j + 2 * h + 1] = __uint_as_float(w[h] & 0xffff0000u);
+    }
+  }
+  const long long row = g / (K / 32);
+  const int grp = (int)(g % (K / 32));
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+  const int bh = split_scale_byte(amax);
+  uint32_t ch[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    int c = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j], 127 - bh),
+                                            ldexpf(v[4 * j + 1], 127 - bh), 0, false);
+    c = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j + 2], 127 - bh),
+                                        ldexpf(v[4 * j + 3], 127 - bh), c, true);
+    ch[j] = (uint32_t)c;
+    v[4 * j] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(c, 0), bh - 127);
+    v[4 * j + 1] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(c, 1), bh - 127);
+    v[4 * j + 2] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(c, 2), bh - 127);
+    v[4 * j + 3] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(c, 3), bh - 127);
+  }
+  float ramax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) ramax = fmaxf(ramax, fabsf(v[j]));
+  const int bl = fit_scale_byte(ramax, 0.9375f, 3);  // E2M3: 7.5 = 0.9375 2^3
+  uint32_t cl[6];
+  lowp_term<ACT_FP6X2>(v, bl, cl);
+  uint8_t *dh = hi + row * K + 32 * grp;
+  *reinterpret_cast<glm_u32x4 *>(dh) = glm_u32x4{ch[0], ch[1], ch[2], ch[3]};
+  *reinterpret_cast<glm_u32x4 *>(dh + 16) = glm_u32x4{ch[4], ch[5], ch[6], ch[7]};
+  uint8_t *dl = lo + row * K + 128 * (grp >> 2) + 16 * (grp & 3);
+  *reinterpret_cast<glm_u32x4 *>(dl) = glm_u32x4{cl[0], cl[1], cl[2], cl[3]};
+  *reinterpret_cast<glm_u32x4 *>(dl + 64) = glm_u32x4{cl[4], cl[5], 0u, 0u};
+  shi[g] = (uint8_t)bh;
+  slo[g] = (uint8_t)bl;
 }
 
 // One thread per 32-element group: the ACT_FP6X2 (hi, lo) or ACT_FP4 split.
@@ -608,7 +665,9 @@ struct SplitStage {
   static constexpr int kXSlots = kXBytes / 1024;
   static constexpr int kXLoads = (kXSlots + kSplitWaves - 1) / kSplitWaves;  // 3 or 1
   static constexpr int kWLoads = kWBytes / (kSplitThreads * 16);             // 2
-  static constexpr int kMfmaFmt = AF == ACT_FP8X2 ? 0 : (AF == ACT_FP6X2 ? 2 : 4);
+  // the MFMA's B format of the hi and the lo term (0 E4M3, 2 E2M3, 4 E2M1)
+  static constexpr int kMfmaFmt = AF == ACT_FP8X2 || AF == ACT_FP8FP6 ? 0 : (AF == ACT_FP6X2 ? 2 : 4);
+  static constexpr int kMfmaFmtLo = AF == ACT_FP8FP6 ? 2 : kMfmaFmt;
   static_assert(kSplitStages * kBytes <= 160 * 1024, "LDS stages exceed 160 KB");
   static_assert(kXBytes % 1024 == 0, "activation loads");
   static_assert(kWSBytes == 8 * 256 && kXSLanes <= 8 * 64, "scale loads per wave");
@@ -792,9 +851,14 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
         int xsc;
         xfrag(f, xb, xsc);
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt)
-          acc[rt][f % kTB] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              wa[rt], xb, acc[rt][f % kTB], 4, S::kMfmaFmt, 0, wsc[rt], 0, xsc);
+        for (int rt = 0; rt < 4; ++rt) {
+          if (f < kTB)
+            acc[rt][f % kTB] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                wa[rt], xb, acc[rt][f % kTB], 4, S::kMfmaFmt, 0, wsc[rt], 0, xsc);
+          else
+            acc[rt][f % kTB] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                wa[rt], xb, acc[rt][f % kTB], 4, S::kMfmaFmtLo, 0, wsc[rt], 0, xsc);
+        }
       }
     }
   };
@@ -964,6 +1028,9 @@ static int act_split_launch_as(hipStream_t stream, const uint16_t *x, long long 
     hipLaunchKernelGGL(act_split_kernel, dim3((unsigned)((4 * groups + 255) / 256)), dim3(256), 0,
                        stream, x, groups, base,
                        base + L.lo, base + L.shi, base + L.slo);
+  else if (af == ACT_FP8FP6)
+    hipLaunchKernelGGL(act_split_fp8fp6_kernel, grid, dim3(256), 0, stream, x, groups, K, base,
+                       base + L.lo, base + L.shi, base + L.slo);
   else if (af == ACT_FP6X2)
     hipLaunchKernelGGL(act_split_lowp_kernel<ACT_FP6X2>, grid, dim3(256), 0, stream, x, groups, K,
                        base, base + L.lo, base + L.shi, base + L.slo);
@@ -998,6 +1065,8 @@ static int split_launch(hipStream_t stream, SplitArgs a, int nproj, int max_tile
       launch_f8f6f4<2, ACT_FP8X2>(stream, grid, a);
     else if (af == ACT_FP6X2)
       launch_f8f6f4<2, ACT_FP6X2>(stream, grid, a);
+    else if (af == ACT_FP8FP6)
+      launch_f8f6f4<2, ACT_FP8FP6>(stream, grid, a);
     else
       launch_f8f6f4<2, ACT_FP4>(stream, grid, a);
   } else {
@@ -1005,6 +1074,8 @@ static int split_launch(hipStream_t stream, SplitArgs a, int nproj, int max_tile
       launch_f8f6f4<1, ACT_FP8X2>(stream, grid, a);
     else if (af == ACT_FP6X2)
       launch_f8f6f4<1, ACT_FP6X2>(stream, grid, a);
+    else if (af == ACT_FP8FP6)
+      launch_f8f6f4<1, ACT_FP8FP6>(stream, grid, a);
     else
       launch_f8f6f4<1, ACT_FP4>(stream, grid, a);
   }
@@ -1120,12 +1191,14 @@ int glm_grouped_dense_mlp_launch(hipStream_t stream, const uint16_t *x, int T, i
 
 bool glm_grouped_supported(int d, int I);
 
-static bool act_format_ok(int af) { return af == ACT_FP8X2 || af == ACT_FP6X2 || af == ACT_FP4; }
+static bool act_format_ok(int af) {
+  return af == ACT_FP8X2 || af == ACT_FP6X2 || af == ACT_FP4 || af == ACT_FP8FP6;
+}
 
 extern "C" size_t glm_act_split_bytes_fmt(int rows, int K, int act_format) {
   if (rows < 0 || K <= 0 || K % 32 != 0 || !act_format_ok(act_format)) return 0;
-  // the ACT_FP6X2 rows are stored in whole 128-element chunks
-  if (act_format == ACT_FP6X2 && K % 128 != 0) return 0;
+  // E2M3 rows are stored in whole 128-element chunks
+  if ((act_format == ACT_FP6X2 || act_format == ACT_FP8FP6) && K % 128 != 0) return 0;
   return SplitLayout((long long)rows, K, act_format).total;
 }
 
@@ -1141,8 +1214,8 @@ extern "C" int glm_act_split(void *stream, const uint16_t *x, int rows, int K, i
               "act_split: unknown act_format %d", act_format);
   GLM_REQUIRE(rows >= 0 && K > 0 && K % 32 == 0, GLM_ERR_INVALID_ARGUMENT,
               "act_split: needs rows >= 0 and K %% 32 == 0 (rows=%d K=%d)", rows, K);
-  GLM_REQUIRE(act_format != ACT_FP6X2 || K % 128 == 0, GLM_ERR_UNSUPPORTED_SHAPE,
-              "act_split: the FP6 split needs K %% 128 == 0 (K=%d)", K);
+  GLM_REQUIRE((act_format != ACT_FP6X2 && act_format != ACT_FP8FP6) || K % 128 == 0,
+              GLM_ERR_UNSUPPORTED_SHAPE, "act_split: an E2M3 term needs K %% 128 == 0 (K=%d)", K);
   GLM_REQUIRE(glm_aligned16({x, split}), GLM_ERR_INVALID_ARGUMENT,
               "act_split: buffers must be 16-byte aligned");
   return act_split_launch_as((hipStream_t)stream, x, rows, K, act_format, split);

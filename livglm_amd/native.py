@@ -29,6 +29,7 @@ GLM_MX_RULE_OCP = 1
 GLM_ACT_FP8X2 = 0
 GLM_ACT_FP6X2 = 1
 GLM_ACT_FP4 = 2
+GLM_ACT_FP8FP6 = 3
 
 GLM_READ_DROP_CACHE = 1
 GLM_HC_BF16_STREAMS = 1

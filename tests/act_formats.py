@@ -6,7 +6,9 @@ scales, round to nearest even):
 
 * ``FP8X2``: two E4M3FN terms, hi + lo (exact for normal-range groups);
 * ``FP6X2``: two E2M3 terms, hi + lo;
-* ``FP4``:   one E2M1 term.
+* ``FP4``:   one E2M1 term;
+* ``FP8FP6``: hi E4M3FN + lo E2M3 (exact for elements at most two binades
+  below their group maximum's, the lo MFMA at the FP6 rate).
 
 Each term's scale is the smallest power of two that keeps the group's largest
 magnitude within the element format's maximum (448, 7.5, 6); lo encodes the
@@ -21,9 +23,9 @@ import numpy as np
 
 from oracle import moe_oracle as O
 
-FP8X2, FP6X2, FP4 = 0, 1, 2
-NAMES = {FP8X2: "fp8x2", FP6X2: "fp6x2", FP4: "fp4"}
-TERMS = {FP8X2: 2, FP6X2: 2, FP4: 1}
+FP8X2, FP6X2, FP4, FP8FP6 = 0, 1, 2, 3
+NAMES = {FP8X2: "fp8x2", FP6X2: "fp6x2", FP4: "fp4", FP8FP6: "fp8fp6"}
+TERMS = {FP8X2: 2, FP6X2: 2, FP4: 1, FP8FP6: 2}
 
 
 def e2m3_magnitudes() -> np.ndarray:
@@ -72,7 +74,9 @@ _ELEM = {
     "e2m3": (7.5 / 8.0, 3, e2m3_encode, e2m3_decode),
     "e2m1": (6.0 / 8.0, 3, O.e2m1_encode, e2m1_decode),
 }
-_TERM_ELEM = {FP8X2: "e4m3", FP6X2: "e2m3", FP4: "e2m1"}
+# element format of each term
+_TERM_ELEM = {FP8X2: ("e4m3", "e4m3"), FP6X2: ("e2m3", "e2m3"), FP4: ("e2m1",),
+              FP8FP6: ("e4m3", "e2m3")}
 
 
 def scale_byte(amax, elem: str) -> np.ndarray:
@@ -87,12 +91,11 @@ def scale_byte(amax, elem: str) -> np.ndarray:
 def split(xb, K: int, fmt: int):
     """bf16 bit patterns [rows, K] -> list of (codes [rows, K] u8, scales
     [rows, K / 32] u8), one per term."""
-    elem = _TERM_ELEM[fmt]
-    _, _, enc, dec = _ELEM[elem]
     x = O.bf16_bits_to_f32(xb).astype(np.float32).reshape(-1, K // 32, 32)
     terms = []
     r = x
-    for _ in range(TERMS[fmt]):
+    for elem in _TERM_ELEM[fmt]:
+        _, _, enc, dec = _ELEM[elem]
         b = scale_byte(np.abs(r).max(axis=2), elem)
         codes = enc(np.ldexp(r.astype(np.float64), (127 - b)[..., None]).astype(np.float32))
         back = dec(codes) * np.ldexp(1.0, b - 127)[..., None]
@@ -103,10 +106,9 @@ def split(xb, K: int, fmt: int):
 
 def dequant(terms, K: int, fmt: int) -> np.ndarray:
     """Sum of the terms' values, float64 [rows, K]."""
-    dec = _ELEM[_TERM_ELEM[fmt]][3]
     out = 0.0
-    for codes, scales in terms:
-        v = dec(codes).reshape(-1, K // 32, 32) * np.ldexp(
+    for elem, (codes, scales) in zip(_TERM_ELEM[fmt], terms):
+        v = _ELEM[elem][3](codes).reshape(-1, K // 32, 32) * np.ldexp(
             1.0, scales.astype(np.int64) - 127)[..., None]
         out = out + v.reshape(-1, K)
     return out
@@ -124,17 +126,17 @@ def split_bytes(rows: int, K: int, fmt: int) -> int:
     return TERMS[fmt] * (_round256(rows * code_row_bytes(K, fmt)) + _round256(rows * K // 32))
 
 
-def _pack_codes(codes, K: int, fmt: int) -> np.ndarray:
+def _pack_codes(codes, K: int, elem: str) -> np.ndarray:
     """One term's codes [rows, K] -> its stored rows [rows, code_row_bytes].
 
-    FP8X2: one byte per element.  FP4: two codes per byte, low nibble first
-    (the MXFP4 weight layout).  FP6X2: per 128-element chunk 128 bytes; the
+    E4M3: one byte per element.  E2M1: two codes per byte, low nibble first
+    (the MXFP4 weight layout).  E2M3: per 128-element chunk 128 bytes; the
     32 codes of group g are packed 6 bits each, low bits first, into 24 bytes,
     bytes 0-15 at 16 g and bytes 16-23 at 64 + 16 g (the other 8 bytes zero)."""
     rows = codes.shape[0]
-    if fmt == FP8X2:
+    if elem == "e4m3":
         return codes.astype(np.uint8)
-    if fmt == FP4:
+    if elem == "e2m1":
         c = codes.reshape(rows, K // 2, 2).astype(np.uint8)
         return (c[..., 0] | (c[..., 1] << 4)).astype(np.uint8)
     g = codes.reshape(rows, K // 32, 32).astype(np.uint64)
@@ -158,8 +160,8 @@ def pack(terms, rows: int, K: int, fmt: int) -> np.ndarray:
     cb, sb = _round256(rows * code_row_bytes(K, fmt)), _round256(rows * K // 32)
     out = np.zeros(split_bytes(rows, K, fmt), dtype=np.uint8)
     nt = len(terms)
-    for i, (codes, scales) in enumerate(terms):
-        out[i * cb:i * cb + rows * code_row_bytes(K, fmt)] = _pack_codes(codes, K, fmt).ravel()
+    for i, (elem, (codes, scales)) in enumerate(zip(_TERM_ELEM[fmt], terms)):
+        out[i * cb:i * cb + rows * code_row_bytes(K, fmt)] = _pack_codes(codes, K, elem).ravel()
         o = nt * cb + i * sb
         out[o:o + rows * K // 32] = scales.ravel()
     return out

@@ -58,12 +58,33 @@ def test_split_error_bounds():
     xb = _groups(rng, rows, K)
     x = O.bf16_bits_to_f32(xb).astype(np.float64)
     amax = np.abs(x.reshape(rows, -1, 32)).max(axis=2)
-    for fmt, bound in [(A.FP8X2, 2.0 ** -22), (A.FP6X2, 2.0 ** -6), (A.FP4, 2.0 ** -2)]:
+    for fmt, bound in [(A.FP8X2, 2.0 ** -22), (A.FP6X2, 2.0 ** -6), (A.FP4, 2.0 ** -2),
+                       (A.FP8FP6, 1.0 / 840)]:
         err = np.abs(A.dequant(A.split(xb, K, fmt), K, fmt) - x).reshape(rows, -1, 32).max(axis=2)
         assert np.all(err <= bound * amax), (A.NAMES[fmt], float((err / amax).max()))
     # one term cannot do better than its element's half quantum at the top
     e1 = np.abs(A.dequant(A.split(xb, K, A.FP4), K, A.FP4) - x).reshape(rows, -1, 32).max(axis=2)
     assert np.mean(e1 > 2.0 ** -6 * amax) > 0.9
+
+
+def test_fp8fp6_exact_near_the_group_maximum():
+    # hi E4M3 keeps 4 significant bits, lo E2M3 the next 4 wherever the lo
+    # scale reaches: every element at most two binades below its group
+    # maximum's comes back exactly (a bf16 element has 8 bits); below that
+    # lo's two-bit exponent runs out and the error stays under max / 840
+    rng = np.random.default_rng(6)
+    rows, K = 128, 512
+    xb = _groups(rng, rows, K)
+    x = O.bf16_bits_to_f32(xb).astype(np.float64).reshape(rows, -1, 32)
+    d = A.dequant(A.split(xb, K, A.FP8FP6), K, A.FP8FP6).reshape(rows, -1, 32)
+    amax = np.abs(x).max(axis=2, keepdims=True)
+    _, emax = np.frexp(amax)
+    _, e = np.frexp(np.where(x != 0, np.abs(x), amax))
+    near = (emax - e <= 2) & (x != 0)
+    assert near.mean() > 0.5 and np.array_equal(d[near], x[near])
+    # the hi term alone is the FP8X2 split's hi term, byte for byte
+    hi8, hi86 = A.split(xb, K, A.FP8X2)[0], A.split(xb, K, A.FP8FP6)[0]
+    assert np.array_equal(hi8[0], hi86[0]) and np.array_equal(hi8[1], hi86[1])
 
 
 def test_fp6_packing_against_bit_unpacking():

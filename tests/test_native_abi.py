@@ -160,12 +160,13 @@ def test_act_format_entry_points(lib):
     fake = ctypes.c_void_p(0x1000)
     # split sizes agree with the layout model; FP8X2 is the original split
     for rows, K in [(1, 128), (7, 2048), (300, 768)]:
-        for fmt in (A.FP8X2, A.FP6X2, A.FP4):
+        for fmt in (A.FP8X2, A.FP6X2, A.FP4, A.FP8FP6):
             assert lib.glm_act_split_bytes_fmt(rows, K, fmt) == A.split_bytes(rows, K, fmt)
         assert lib.glm_act_split_bytes_fmt(rows, K, 0) == lib.glm_act_split_bytes(rows, K)
     assert lib.glm_act_split_bytes_fmt(4, 96, native.GLM_ACT_FP6X2) == 0  # K % 128
+    assert lib.glm_act_split_bytes_fmt(4, 96, native.GLM_ACT_FP8FP6) == 0
     assert lib.glm_act_split_bytes_fmt(4, 96, native.GLM_ACT_FP4) > 0
-    assert lib.glm_act_split_bytes_fmt(4, 128, 3) == 0
+    assert lib.glm_act_split_bytes_fmt(4, 128, 4) == 0
     msg = _expect(native.GLM_ERR_INVALID_ARGUMENT, "glm_act_split", None, fake, 4, 128, 7, fake)
     assert "act_format" in msg
     _expect(native.GLM_ERR_UNSUPPORTED_SHAPE, "glm_act_split", None, fake, 4, 96,
