@@ -23,8 +23,13 @@ I=768) it carries the metric's three parts:
     with the MFMA operations the rocprofv3 MOPS counters report beside it;
   * ``stack``: the 42-layer decode stack (MXFP8 resident linear + MoE layer per
     layer, one token per step, Markov routing) per step;
+  * ``decode_t1`` and ``batch_t64``: the other decode configurations (one token
+    of the small layer; 64 tokens with Zipf-skewed routing), each with its
+    dominant kernel against the HBM roofline, the layer-level selected-expert
+    GB/s and its own CPU baseline;
 and the CPU baseline (the C restatement in oracle/, OpenMP, on this host) on a
-bounded sample of the default workload.
+bounded sample of the default workload, with the single-threaded numpy
+oracle's rate beside it.
 """
 
 from __future__ import annotations
@@ -51,15 +56,15 @@ METRIC = "MoE layer tokens/s; decode expert HBM GB/s; MXFP4 MFMA util at T=4096"
 HBM_PEAK_GBPS = 8000.0
 MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "fp8": 5000.0, "fp4": 10100.0}  # MI355X dense
 COPY_BYTES = 256 << 20  # counter calibration: one device copy of this size
-ACT_NAMES = {0: "fp8x2", 1: "fp6x2", 2: "fp4"}
+ACT_NAMES = {0: "fp8x2", 1: "fp6x2", 2: "fp4", 3: "fp8fp6"}
 
 
 def design_ceiling(act_format: int) -> float:
     """Algorithmic TFLOP/s the grouped GEMM's MFMAs allow in an activation
     format: FP8 x FP4 twice per product (hi, lo) at the FP8 rate, FP6 x FP4
-    twice at the FP6 rate, FP4 x FP4 once."""
-    return {0: MFMA_PEAK_TFLOPS["fp8"] / 2, 1: MFMA_PEAK_TFLOPS["fp4"] / 2,
-            2: MFMA_PEAK_TFLOPS["fp4"]}[act_format]
+    twice at the FP6 rate, FP4 x FP4 once, FP8 x FP4 (hi) + FP6 x FP4 (lo)."""
+    fp8, fp4 = MFMA_PEAK_TFLOPS["fp8"], MFMA_PEAK_TFLOPS["fp4"]
+    return {0: fp8 / 2, 1: fp4 / 2, 2: fp4, 3: 1.0 / (1.0 / fp8 + 1.0 / fp4)}[act_format]
 
 
 def parse_args():
@@ -81,9 +86,10 @@ def parse_args():
     ap.add_argument("--traffic", type=int, default=1,
                     help="1: measure the dominant kernel's HBM traffic with rocprofv3 counters")
     ap.add_argument("--seed", type=int, default=5301)
-    ap.add_argument("--act-format", default="fp8x2", choices=["fp8x2", "fp6x2", "fp4"],
+    ap.add_argument("--act-format", default="fp8x2",
+                    choices=["fp8x2", "fp6x2", "fp4", "fp8fp6"],
                     help="prefill: activation format of the timed grouped gate/up GEMM "
-                         "(fp8x2: the exact split the layer uses; fp6x2, fp4: the "
+                         "(fp8x2: the exact split the layer uses; fp6x2, fp4, fp8fp6: the "
                          "lower-precision variants)")
     ap.add_argument("--load-layers", type=int, default=8,
                     help="bank_load: layers of the synthetic checkpoint (320 MB each)")
@@ -199,7 +205,8 @@ class Setup:
         self.few_token = T <= 4 and k <= 8 and self.decode_kernels
         self.grouped = T > 64
         self.act_format = {"fp8x2": native.GLM_ACT_FP8X2, "fp6x2": native.GLM_ACT_FP6X2,
-                           "fp4": native.GLM_ACT_FP4}[getattr(args, "act_format", "fp8x2")]
+                           "fp4": native.GLM_ACT_FP4, "fp8fp6": native.GLM_ACT_FP8FP6}[
+                               getattr(args, "act_format", "fp8x2")]
 
     def _code_scales(self, args, np) -> dict:
         """Replaces every bank's routed scales by ones with the real
@@ -601,6 +608,21 @@ def prefill_leg(r: dict, counters: dict | None) -> dict:
     return leg
 
 
+def decode_leg(r: dict) -> dict:
+    """A decode configuration's figures: the layer's tokens/s, the dominant
+    routed gate/up kernel against the HBM roofline (HIP events over a graph
+    of its launches), the selected experts' bytes over the layer step's device
+    time, and the C restatement on this host's cores."""
+    leg = {"workload": describe(r), "tokens_per_s": round(r["tokens_per_s"], 1),
+           "ms_per_step": round(r["ms_per_step"], 5), "roofline": r["roofline"]}
+    if "layer_expert_gbps" in r:
+        leg["decode_expert_hbm_gbps"] = round(r["layer_expert_gbps"], 1)
+        leg["decode_expert_hbm_frac"] = round(r["layer_expert_gbps"] / HBM_PEAK_GBPS, 4)
+        leg["decode_unique_experts_per_step"] = round(r["unique_experts_per_step"], 2)
+    leg["cpu_baseline"] = r["cpu"]
+    return leg
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -682,7 +704,19 @@ def main() -> int:
                      traffic=False, cpu_seconds=0.0, kernel_launches=64, min_rotation_gb=0.0)
         line["stack"] = {"workload": describe(st), "tokens_per_s": round(st["tokens_per_s"], 1),
                          "ms_per_step": round(st["ms_per_step"], 5), **st["stack"]}
+        # the other decode configurations: one token of the small layer (banks
+        # of 16 MB rotating over >= 1 GB, four times the memory-side cache) and
+        # 64 tokens with Zipf-skewed routing (as many banks as the default
+        # workload's rotation), each on its own banks
+        cpu_leg = min(3.0, args.cpu_seconds)
+        for name, rot in (("decode_t1", 1.0), ("batch_t64", args.min_rotation_gb)):
+            line[name] = decode_leg(measure(
+                args, torch, np, name, steps=args.steps, warmup=args.warmup, traffic=False,
+                cpu_seconds=cpu_leg, kernel_launches=64, min_rotation_gb=rot))
     line["cpu_baseline"] = r["cpu"]
+    if legs and args.cpu_seconds > 0:
+        line["cpu_baseline"]["numpy_1thread"] = cpu_baseline_numpy(
+            r["shape"], args.seed, min(3.0, args.cpu_seconds))
     print(json.dumps(line))
     return 0
 
@@ -1086,6 +1120,40 @@ def host_cpu() -> dict:
     except OSError:
         pass
     return {"nproc": os.cpu_count(), "cpu_model": model}
+
+
+def cpu_baseline_numpy(shape, seed: int, budget_s: float) -> dict:
+    """The numpy oracle (oracle/moe_oracle.py, f64 products) on one thread:
+    layer steps of ``shape`` on one seeded layer, as many as fit in
+    ``budget_s`` (at least one)."""
+    from threadpoolctl import threadpool_limits
+
+    from livglm_amd.workloads import make_layer
+    from oracle import moe_oracle as O
+
+    layer = make_layer(shape, seed)
+    bank = O.Bank(*(layer[key] for key in ("gate_proj.weight_packed", "gate_proj.weight_scale",
+                                           "up_proj.weight_packed", "up_proj.weight_scale",
+                                           "down_proj.weight_packed", "down_proj.weight_scale")))
+    sw = tuple(O.bf16_bits_to_f32(layer[k]) for k in ("shared.gate", "shared.up", "shared.down"))
+    x = O.bf16_bits_to_f32(layer["x"])
+    steps = 0
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        while True:
+            O.moe_layer(x, layer["router_weight"], layer["router_bias"], bank, sw,
+                        top_k=shape.k, n_group=shape.n_group, topk_group=shape.topk_group,
+                        norm_topk_prob=shape.norm_topk_prob,
+                        routed_scaling_factor=shape.routed_scaling_factor,
+                        swiglu_limit=shape.swiglu_limit)
+            steps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                break
+    return {"value": round(shape.T * steps / el, 3), "unit": "tokens/s", "cores": 1,
+            "kind": "port",
+            "sample": f"{steps} layer steps of {shape.name} (T={shape.T}) in {el:.2f} s; "
+                      "numpy oracle (f64 products, one BLAS thread), not MLX"}
 
 
 def cpu_baseline(shape, bank, xs, budget_s: float, bias=None, streams=None):
