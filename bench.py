@@ -180,6 +180,9 @@ class Setup:
                             native.GLM_FMT_MXFP8, native.GLM_MX_RULE_NEAREST,
                             b["linear.codes"].data_ptr(), b["linear.scales"].data_ptr())
                 del w
+                # the RMSNorm in front of it (bf16-representable weights around 1)
+                b["linear.norm"] = (1.0 + 0.1 * torch.randn(d, device=dev, generator=gen)).to(
+                    torch.bfloat16).to(torch.float32)
             self.banks.append(b)
         self.scalex = None
         if getattr(args, "scalex", 0) and T <= 4 and self.layers == 1 and not hc:
@@ -423,16 +426,22 @@ def measure(args, torch, np, workload: str, *, steps: int, warmup: int, traffic:
 
     def stack_step(s: int) -> None:
         """One decode step through the layer stack: per layer the resident
-        MXFP8 linear, then the MoE layer on its output; the f32 MoE output,
-        rounded to bf16, is the next layer's input (a stand-in for the
-        decoder's residual and norm, which are not part of this path).  The
-        rounding happens as glm_linear_f32 reads it."""
+        MXFP8 linear, then the MoE layer on its output.  The next layer reads
+        the f32 MoE output through an RMSNorm fused into its linear (the
+        decoder's norm in front of each block; the residual stream is not part
+        of this path)."""
         x = S.xs[s % S.n_inputs]
         for layer in range(S.layers):
             b = S.banks[layer]
-            fn, src = ("glm_linear", x) if layer == 0 else ("glm_linear_f32", out)
-            native.call(fn, S.stream, src.data_ptr(), T, d, b["linear.codes"].data_ptr(),
-                        b["linear.scales"].data_ptr(), native.GLM_FMT_MXFP8, d, act.data_ptr())
+            if layer == 0:
+                native.call("glm_linear", S.stream, x.data_ptr(), T, d,
+                            b["linear.codes"].data_ptr(), b["linear.scales"].data_ptr(),
+                            native.GLM_FMT_MXFP8, d, act.data_ptr())
+            else:
+                native.call("glm_rms_norm_linear", S.stream, out.data_ptr(), T, d,
+                            b["linear.norm"].data_ptr(), 1e-6, b["linear.codes"].data_ptr(),
+                            b["linear.scales"].data_ptr(), native.GLM_FMT_MXFP8, d,
+                            act.data_ptr())
             moe(act, layer, s)
 
     def capture(fn, first: int, count: int):
@@ -545,7 +554,7 @@ def measure(args, torch, np, workload: str, *, steps: int, warmup: int, traffic:
         # bytes one decode step reads: every layer's k experts (Markov
         # routing at T=1 picks k distinct ones), shared expert, linear, router
         expert = S.layers * k * shape.expert_bytes
-        other = S.layers * (3 * Is * d * 2 + d * d + d * d // 32 + E * d * 4)
+        other = S.layers * (3 * Is * d * 2 + d * d + d * d // 32 + d * 4 + E * d * 4)
         sec = ms_per_step / 1e3
         res["stack"] = {"layers": S.layers,
                         "us_per_layer": round(ms_per_step * 1e3 / S.layers, 3),
@@ -568,9 +577,9 @@ def describe(r: dict) -> str:
                 f"top-{sh.k} I={sh.I} (MXFP4 group-32 experts, bf16 shared expert "
                 f"I={sh.I_shared}) + hyper_residual")
     if r["layers"] > 1:
-        return (f"{sh.name}: {r['layers']} layers x (MXFP8 {sh.d}x{sh.d} resident linear + "
-                f"MoE layer T={T} d={sh.d} E={sh.E} top-{sh.k} I={sh.I}, MXFP4 group-32 experts, "
-                f"bf16 shared expert I={sh.I_shared}), Markov routing keeping 70% of the "
+        return (f"{sh.name}: {r['layers']} layers x (RMSNorm + MXFP8 {sh.d}x{sh.d} resident "
+                f"linear + MoE layer T={T} d={sh.d} E={sh.E} top-{sh.k} I={sh.I}, MXFP4 group-32 "
+                f"experts, bf16 shared expert I={sh.I_shared}), Markov routing keeping 70% of the "
                 f"previous step's experts, one token per step")
     return (f"{sh.name}: MoE layer T={T} d={sh.d} E={sh.E} top-{sh.k} I={sh.I} "
             f"(MXFP4 group-32 experts, bf16 shared expert I={sh.I_shared})")
@@ -1180,15 +1189,19 @@ def cpu_baseline(shape, bank, xs, budget_s: float, bias=None, streams=None):
     xs_h = xs.view(torch.int16).cpu().numpy().view(np.uint16)
     stack = shape.layers > 1
     site = shape.hc > 0
-    if site:
+    if site or stack:
         from oracle import mhc_oracle as H
         from oracle import moe_oracle as O
+    if site:
         st_h = streams.cpu().numpy()
+    y = None
     steps = 0
     t0 = time.perf_counter()
     while True:
         x = xs_h[steps % xs_h.shape[0]]
         if stack:
+            if y is not None:  # the previous layer step's output through the norm
+                x = O.f32_to_bf16_bits(H.rms_norm(y, host["linear.norm"], 1e-6))
             x = cpu_oracle.linear_mxfp8(x, host["linear.codes"], host["linear.scales"])
         if site:
             st = st_h[steps % st_h.shape[0]]
@@ -1211,8 +1224,8 @@ def cpu_baseline(shape, bank, xs, budget_s: float, bias=None, streams=None):
             "cores": cpu_oracle.threads(),
             **host_cpu(),
             "kind": "port",
-            "sample": f"{steps} single-layer steps (MXFP8 {shape.d}x{shape.d} linear + MoE layer, "
-                      f"T={shape.T}) on one resident layer in {el:.2f} s; tokens/s = 1 / "
+            "sample": f"{steps} single-layer steps (RMSNorm + MXFP8 {shape.d}x{shape.d} linear + "
+                      f"MoE layer, T={shape.T}) on one resident layer in {el:.2f} s; tokens/s = 1 / "
                       f"({shape.layers} x mean layer time); C restatement (not MLX), OpenMP",
         }
     return {

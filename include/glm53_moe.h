@@ -286,6 +286,22 @@ int glm_linear_f32(void *stream, const float *x, int T, int in_dims, const void 
                    const uint8_t *scales, int fmt, int out_dims, uint16_t *y);
 
 /*
+ * RMSNorm of f32 rows followed by the MXFP8 resident linear: RMSNorm
+ * (layers.py:119-131; unweighted when norm_weight is NULL, layers.py:134-140),
+ * x * (1 / sqrt(mean(x^2) + eps)) * w, rounded to bf16, then
+ * DeferredLinear.__call__ (layers.py:56-70) on it -- the decoder's norm in
+ * front of a resident projection, fused so that the normalised row is never
+ * written out.  Equal to glm_rms_norm (bf16 output) + glm_linear up to the
+ * order of the f32 sum of squares.
+ * x f32 [T][in]; norm_weight f32 [in] or NULL; weight/scales MXFP8
+ * (GLM_FMT_MXFP8 only); y bf16 [T][out].
+ * Limits: T <= 4, in % 256 == 0, out % 8 == 0.
+ */
+int glm_rms_norm_linear(void *stream, const float *x, int T, int in_dims,
+                        const float *norm_weight, float eps, const void *weight,
+                        const uint8_t *scales, int fmt, int out_dims, uint16_t *y);
+
+/*
  * Dense SwiGLU MLP (the shared expert).  Replaces DenseMLP.__call__
  * (layers.py:160-171): out = down(limited_swiglu(gate(x), up(x))).
  * All three weights share `fmt`.  h is caller scratch bf16 [T][I].
@@ -362,6 +378,7 @@ int glm_moe_forward(void *stream, const uint16_t *x, int T, int d, const float *
                     const uint16_t *shared_in, float swiglu_limit, void *workspace,
                     size_t workspace_bytes, float *out, float *weights_out,
                     uint32_t *indices_out);
+
 
 /* Size of the device array behind glm_moe_forward_noalloc (per device). */
 #define GLM_NOALLOC_SCRATCH_BYTES (64u << 20)

@@ -313,6 +313,10 @@ struct LinearRowsArgs {
   int T, K, N;
   const uint8_t *w, *s;
   uint16_t *y;
+  // linear_mx8_kernel<true, true>: RMSNorm of the f32 rows first (weight f32
+  // [K] or nullptr)
+  const float *norm_w;
+  float eps;
 };
 
 __device__ __forceinline__ glm_bf16x2 bf16_pair(const glm_bf16x8 &v, int p) {
@@ -457,8 +461,14 @@ __device__ __forceinline__ void x_cols4(const void *x, size_t off, glm_bf16x2 &p
   }
 }
 
-template <bool XF32>
+// NORM (f32 x only): every x row is replaced by its RMSNorm, x * (1 /
+// sqrt(mean(x^2) + eps)) * w (the product rounded after each factor, as
+// rms_norm_kernel), before the rounding to bf16.  The wave's loads of a pass
+// cover the whole row when K <= 256 kMx8Steps, so the sum of squares comes
+// from them; longer rows take one pre-pass over the row.
+template <bool XF32, bool NORM = false>
 __global__ __launch_bounds__(256) void linear_mx8_kernel(const LinearRowsArgs a) {
+  static_assert(XF32 || !NORM, "the fused RMSNorm reads f32 rows");
   const int lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kRowsPerWave;
   const int K = a.K, steps = K / 256;
@@ -467,6 +477,27 @@ __global__ __launch_bounds__(256) void linear_mx8_kernel(const LinearRowsArgs a)
   for (int rr = 0; rr < kRowsPerWave; ++rr)
 #pragma unroll
     for (int t = 0; t < kLinearMaxT; ++t) acc[rr][t] = 0.0f;
+  const bool one_pass = steps <= kMx8Steps;
+  float inv[kLinearMaxT];
+  auto norm_inv = [&](float ss) {
+    return 1.0f / sqrtf(wave_sum(ss) / (float)K + a.eps);
+  };
+  if constexpr (NORM) {
+    if (!one_pass) {
+#pragma unroll
+      for (int t = 0; t < kLinearMaxT; ++t) {
+        float ss = 0.0f;
+        if (t < a.T) {
+          for (int c = 4 * lane; c < K; c += 256) {
+            const glm_f32x4 v = *reinterpret_cast<const glm_f32x4 *>(
+                static_cast<const float *>(a.x) + (size_t)t * K + c);
+            ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+          }
+          inv[t] = norm_inv(ss);
+        }
+      }
+    }
+  }
   for (int j0 = 0; j0 < steps; j0 += kMx8Steps) {
     // every load of the pass goes out before any use (steps past the end
     // repeat the last one and are not added)
@@ -482,9 +513,49 @@ __global__ __launch_bounds__(256) void linear_mx8_kernel(const LinearRowsArgs a)
         sb[jj][rr] = a.s[(size_t)(row0 + rr) * (K / 32) + col / 32];
       }
     }
+    glm_f32x4 xf[kMx8Steps], nw[kMx8Steps];
+    if constexpr (NORM) {
 #pragma unroll
-    for (int jj = 0; jj < kMx8Steps; ++jj)
-      x_cols4<XF32>(a.x, 256 * min(j0 + jj, steps - 1) + 4 * lane, xp[jj][0], xp[jj][1]);
+      for (int jj = 0; jj < kMx8Steps; ++jj) {
+        const int col = 256 * min(j0 + jj, steps - 1) + 4 * lane;
+        xf[jj] = *reinterpret_cast<const glm_f32x4 *>(static_cast<const float *>(a.x) + col);
+        nw[jj] = a.norm_w != nullptr ? *reinterpret_cast<const glm_f32x4 *>(a.norm_w + col)
+                                     : glm_f32x4{1.f, 1.f, 1.f, 1.f};
+      }
+    } else {
+#pragma unroll
+      for (int jj = 0; jj < kMx8Steps; ++jj)
+        x_cols4<XF32>(a.x, 256 * min(j0 + jj, steps - 1) + 4 * lane, xp[jj][0], xp[jj][1]);
+    }
+    // token t's normalised columns of this pass as bf16 pairs (the sum of
+    // squares from the pass's own values when it covers the row; steps past
+    // the end repeat the last one and are left out of it)
+    auto norm_cols = [&](int t) {
+      if constexpr (NORM) {
+        if (one_pass) {
+          float ss = 0.0f;
+#pragma unroll
+          for (int jj = 0; jj < kMx8Steps; ++jj)
+            if (j0 + jj < steps)
+              ss += xf[jj][0] * xf[jj][0] + xf[jj][1] * xf[jj][1] + xf[jj][2] * xf[jj][2] +
+                    xf[jj][3] * xf[jj][3];
+          inv[t] = norm_inv(ss);
+        }
+#pragma unroll
+        for (int jj = 0; jj < kMx8Steps; ++jj) {
+          float v[4];
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            v[m] = xf[jj][m] * inv[t];
+            if (a.norm_w != nullptr) v[m] *= nw[jj][m];
+          }
+          xp[jj][0][0] = (__bf16)v[0];
+          xp[jj][0][1] = (__bf16)v[1];
+          xp[jj][1][0] = (__bf16)v[2];
+          xp[jj][1][1] = (__bf16)v[3];
+        }
+      }
+    };
     __builtin_amdgcn_sched_barrier(0);
     glm_bf16x2 wp[kMx8Steps][kRowsPerWave][2];
 #pragma unroll
@@ -500,10 +571,15 @@ __global__ __launch_bounds__(256) void linear_mx8_kernel(const LinearRowsArgs a)
       if (t < a.T) {
         if (t > 0) {
 #pragma unroll
-          for (int jj = 0; jj < kMx8Steps; ++jj)
-            x_cols4<XF32>(a.x, (size_t)t * K + 256 * min(j0 + jj, steps - 1) + 4 * lane,
-                          xp[jj][0], xp[jj][1]);
+          for (int jj = 0; jj < kMx8Steps; ++jj) {
+            const size_t off = (size_t)t * K + 256 * min(j0 + jj, steps - 1) + 4 * lane;
+            if constexpr (NORM)
+              xf[jj] = *reinterpret_cast<const glm_f32x4 *>(static_cast<const float *>(a.x) + off);
+            else
+              x_cols4<XF32>(a.x, off, xp[jj][0], xp[jj][1]);
+          }
         }
+        norm_cols(t);
 #pragma unroll
         for (int jj = 0; jj < kMx8Steps; ++jj) {
           if (j0 + jj < steps) {
@@ -773,7 +849,8 @@ template <bool XF32>
 static int launch_linear_rows(hipStream_t stream, const void *x, int T, int in_dims,
                               const void *weight, const uint8_t *scales, int fmt, int out_dims,
                               uint16_t *y) {
-  const glm::LinearRowsArgs a{x, T, in_dims, out_dims, static_cast<const uint8_t *>(weight), scales, y};
+  const glm::LinearRowsArgs a{x, T, in_dims, out_dims, static_cast<const uint8_t *>(weight), scales,
+                              y, nullptr, 0.0f};
   const dim3 grid(out_dims / (4 * glm::kRowsPerWave)), block(256);
   switch (fmt) {
     case GLM_FMT_MXFP4: hipLaunchKernelGGL((glm::linear_rows_kernel<GLM_FMT_MXFP4, XF32>), grid, block, 0, stream, a); break;
@@ -912,6 +989,34 @@ extern "C" int glm_linear_f32(void *stream, const float *x, int T, int in_dims, 
               glm::kLinearMaxT, 4 * glm::kRowsPerWave);
   return launch_linear_rows<true>((hipStream_t)stream, x, T, in_dims, weight, scales, fmt,
                                   out_dims, y);
+}
+
+extern "C" int glm_rms_norm_linear(void *stream, const float *x, int T, int in_dims,
+                                   const float *norm_weight, float eps, const void *weight,
+                                   const uint8_t *scales, int fmt, int out_dims, uint16_t *y) {
+  glm::clear_error();
+  GLM_REQUIRE(x && weight && scales && y, GLM_ERR_INVALID_ARGUMENT,
+              "rms_norm_linear: null pointer argument");
+  GLM_REQUIRE(T >= 0 && eps >= 0.0f, GLM_ERR_INVALID_ARGUMENT,
+              "rms_norm_linear: negative T or eps");
+  GLM_REQUIRE(fmt == GLM_FMT_MXFP8, GLM_ERR_UNSUPPORTED_SHAPE,
+              "rms_norm_linear: the fused norm takes MXFP8 weights (fmt %d)", fmt);
+  int rc = check_mx_geometry("rms_norm_linear", fmt, in_dims, out_dims);
+  if (rc) return rc;
+  GLM_REQUIRE(glm_aligned16({x, weight, y, norm_weight}), GLM_ERR_INVALID_ARGUMENT,
+              "rms_norm_linear: buffers must be 16-byte aligned");
+  if (T == 0) return GLM_OK;
+  GLM_REQUIRE(linear_rows_supported(T, in_dims, out_dims) && in_dims % 256 == 0,
+              GLM_ERR_UNSUPPORTED_SHAPE,
+              "rms_norm_linear: T=%d in=%d out=%d unsupported (T <= %d, in a multiple of 256, "
+              "out a multiple of %d)",
+              T, in_dims, out_dims, glm::kLinearMaxT, 4 * glm::kRowsPerWave);
+  const glm::LinearRowsArgs a{x, T, in_dims, out_dims, static_cast<const uint8_t *>(weight),
+                              scales, y, norm_weight, eps};
+  hipLaunchKernelGGL((glm::linear_mx8_kernel<true, true>), dim3(out_dims / (4 * glm::kRowsPerWave)),
+                     dim3(256), 0, (hipStream_t)stream, a);
+  GLM_LAUNCH_CHECK("linear_mx8_kernel");
+  return GLM_OK;
 }
 
 extern "C" int glm_dense_mlp(void *stream, const uint16_t *x, int T, int d, int I, int fmt,

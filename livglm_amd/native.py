@@ -67,6 +67,7 @@ SIGNATURES = {
     "glm_moe_combine": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _p]),
     "glm_linear": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _p]),
     "glm_linear_f32": (_i, [_p, _p, _i, _i, _p, _p, _i, _i, _p]),
+    "glm_rms_norm_linear": (_i, [_p, _p, _i, _i, _p, _f, _p, _p, _i, _i, _p]),
     "glm_dense_mlp": (_i, [_p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _f, _p, _p]),
     "glm_mx_quantize": (_i, [_p, _p, _i, _i, _i, _i, _p, _p]),
     "glm_mx_dequantize": (_i, [_p, _p, _p, _i, _i, _i, _p]),

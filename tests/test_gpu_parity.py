@@ -675,6 +675,42 @@ def test_linear_parity_and_f32_input(gu, fmt, T):
         assert rc == native.GLM_ERR_UNSUPPORTED_SHAPE
 
 
+@pytest.mark.parametrize("in_f", [1024, 2048, 4096])
+@pytest.mark.parametrize("T", [1, 4])
+@pytest.mark.parametrize("weighted", [True, False])
+def test_rms_norm_linear_parity(gu, in_f, T, weighted):
+    # the fused RMSNorm + MXFP8 linear against the oracle's norm (mhc_oracle.rms_norm,
+    # layers.py:119-140) rounded to bf16 and its linear; K = 1024 and 2048 take the
+    # norm from the pass's own loads, 4096 from a pre-pass over the row; and against
+    # glm_rms_norm + glm_linear (the same arithmetic up to the sum-of-squares order)
+    from oracle import mhc_oracle as H
+    torch = _torch()
+    rng = np.random.default_rng(5510 + in_f + T + weighted)
+    out_f, eps = 512, 1e-6
+    w = O.f32_to_bf16_bits(rng.normal(0, 0.02, (out_f, in_f)).astype(np.float32))
+    c, sc = O.quantize_mx(w, 8, O.MX_RULE_NEAREST)
+    mat = O.dequant_mxfp8(c, sc)
+    codes, scales = gu.to_dev(c), gu.to_dev(sc)
+    x32 = (rng.normal(0, 1, (T, in_f)) * rng.uniform(0.1, 300.0, (T, 1))).astype(np.float32)
+    nw = rng.normal(1.0, 0.1, in_f).astype(np.float32) if weighted else None
+    xn = O.f32_to_bf16_bits(H.rms_norm(x32, nw, eps))
+    want = O.linear_bf16(O.bf16_bits_to_f32(xn), mat)
+    y = torch.empty((T, out_f), dtype=torch.bfloat16, device="cuda")
+    x_dev = torch.from_numpy(x32).cuda()
+    nw_dev = torch.from_numpy(nw).cuda() if weighted else None
+    gu.call("glm_rms_norm_linear", gu.stream(), gu.p(x_dev), T, in_f, gu.p(nw_dev), eps,
+            gu.p(codes), gu.p(scales), native.GLM_FMT_MXFP8, out_f, gu.p(y))
+    got = O.bf16_bits_to_f32(gu.bf16_bits(y))
+    assert O.rel_l2(got, want) < REL_L2
+    assert np.mean(got == want) > 0.97
+    xb = torch.empty((T, in_f), dtype=torch.bfloat16, device="cuda")
+    gu.call("glm_rms_norm", gu.stream(), gu.p(x_dev), T, in_f, gu.p(nw_dev), eps, None, gu.p(xb))
+    y2 = torch.empty_like(y)
+    gu.call("glm_linear", gu.stream(), gu.p(xb), T, in_f, gu.p(codes), gu.p(scales),
+            native.GLM_FMT_MXFP8, out_f, gu.p(y2))
+    assert np.mean(gu.bf16_bits(y) == gu.bf16_bits(y2)) > 0.99
+
+
 @pytest.mark.parametrize("in_f", [1024, 2304, 4096])
 @pytest.mark.parametrize("T", [1, 4])
 def test_linear_mxfp8_column_steps(gu, in_f, T):
