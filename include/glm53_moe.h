@@ -390,7 +390,9 @@ int glm_moe_forward(void *stream, const uint16_t *x, int T, int d, const float *
  * The layer's workspace is a file-scope device array of
  * GLM_NOALLOC_SCRATCH_BYTES inside the library: every device that loads the
  * library holds its own copy until the process ends, and its address is
- * looked up once per device, on the first call with that device current.
+ * looked up once per device, on the first call with that device current
+ * (that call may itself be made under HIP graph capture; replays of a
+ * captured call equal glm_moe_forward's result).
  * Sizes whose workspace (glm_moe_workspace_bytes) exceeds the array are
  * rejected with GLM_ERR_WORKSPACE before any device work; decode sizes fit
  * (T = 64 at d 2048, E 128, k 8, I 768, I_shared 768 needs 8.7 MiB; T = 64 at

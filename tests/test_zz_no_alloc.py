@@ -1,12 +1,19 @@
 """glm_moe_forward_noalloc: the MoE layer with its workspace in the library's
 static device array.  Through the C ABI, two calls in a row (the second with
 a smaller input, so it runs on what the first left in the array) must equal
-glm_moe_forward with a fresh caller workspace bit for bit; sizes beyond the
-array are rejected on the host before any device work."""
+glm_moe_forward with a fresh caller workspace bit for bit; so must the
+replays of a HIP graph that captured the call, both after eager calls and
+when the capture holds the entry point's first call in a fresh process (the
+array's address is looked up then); sizes beyond the array are rejected on
+the host before any device work."""
 
 from __future__ import annotations
 
 import ctypes
+import json
+import os
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -74,6 +81,95 @@ def test_noalloc_equals_moe_forward_on_consecutive_calls(seq):
                                       err_msg=shape.name)
         np.testing.assert_array_equal(o_n.view(np.uint32), o_f.view(np.uint32),
                                       err_msg=shape.name)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["verify_t2", "batch_t64"])
+def test_noalloc_graph_replays_equal_moe_forward(name):
+    # captured after eager calls; each replay (other eager work in between,
+    # the outputs cleared) must give glm_moe_forward's result bit for bit
+    import torch
+
+    import gpu_util as gu
+    shape = SHAPES[name]
+    native.load()
+    _both(shape, 8850)  # eager calls first
+    layer = make_layer(shape, 8851)
+    dl = gu.upload_layer(layer)
+    T, d, k = shape.T, shape.d, shape.k
+    ws_bytes = native.load().glm_moe_workspace_bytes(T, d, shape.E, k, shape.I, shape.I_shared)
+    ws = gu.workspace(ws_bytes)
+    ref = [torch.empty((T, d), dtype=torch.float32, device="cuda"),
+           torch.empty((T, k), dtype=torch.float32, device="cuda"),
+           torch.empty((T, k), dtype=torch.int32, device="cuda")]
+    gu.call("glm_moe_forward", *_args(dl, shape, T, *ref, ws, ws_bytes))
+    want = [gu.host(t).view(np.uint32) for t in ref]
+    outs = [torch.empty_like(t) for t in ref]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        native.call("glm_moe_forward_noalloc", *_args(dl, shape, T, *outs))
+    for rep in range(3):
+        _both(SHAPES["verify_t2"], 8860 + rep)  # other eager work on the same array
+        for t in outs:
+            t.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for got, exp in zip(outs, want):
+            np.testing.assert_array_equal(gu.host(got).view(np.uint32), exp, err_msg=str(rep))
+
+
+FIRST_CALL_IN_CAPTURE = r"""
+import json, sys
+import numpy as np
+import torch
+import gpu_util as gu
+from livglm_amd import native
+from livglm_amd.workloads import SHAPES, make_layer
+from test_zz_no_alloc import _args
+shape = SHAPES["verify_t2"]
+lib = native.load()
+dl = gu.upload_layer(make_layer(shape, 8900))
+T, d, k = shape.T, shape.d, shape.k
+outs = [torch.empty((T, d), dtype=torch.float32, device="cuda"),
+        torch.empty((T, k), dtype=torch.float32, device="cuda"),
+        torch.empty((T, k), dtype=torch.int32, device="cuda")]
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):
+    rc = lib.glm_moe_forward_noalloc(*_args(dl, shape, T, *outs))
+res = {"rc": rc, "error": lib.glm_last_error().decode()}
+if rc == 0:
+    same = True
+    ws_bytes = lib.glm_moe_workspace_bytes(T, d, shape.E, k, shape.I, shape.I_shared)
+    ws = gu.workspace(ws_bytes)
+    ref = [torch.empty_like(t) for t in outs]
+    gu.call("glm_moe_forward", *_args(dl, shape, T, *ref, ws, ws_bytes))
+    for rep in range(2):
+        for t in outs:
+            t.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        same = same and all(np.array_equal(gu.host(a).view(np.uint32), gu.host(b).view(np.uint32))
+                            for a, b in zip(outs, ref))
+    res["equal"] = bool(same)
+print(json.dumps(res))
+"""
+
+
+@pytest.mark.gpu
+def test_noalloc_first_call_inside_graph_capture():
+    # a fresh process whose first glm_moe_forward_noalloc call (the one that
+    # looks up the array's address on the device) is made under capture
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, PYTHONPATH=os.pathsep.join(
+        [root, os.path.join(root, "src"), os.path.join(root, "tests")]))
+    proc = subprocess.run([sys.executable, "-c", FIRST_CALL_IN_CAPTURE], cwd=root, env=env,
+                          capture_output=True, text=True, timeout=110)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    res = json.loads(proc.stdout.strip().splitlines()[-1])
+    assert res["rc"] == native.GLM_OK, res
+    assert res["equal"], res
 
 
 def test_noalloc_rejects_sizes_beyond_the_array_on_host():
