@@ -680,16 +680,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void s
 }
 
 // 16-row tiles per routed block of select_gate_up_kernel: one while the grid
-// is small (8 pairs x 48 tiles at one token); with more tiles each block
-// streams several consecutive tiles of its pair, up to four, so the token
-// row + selection before the first weight load is paid once per block, not
-// once per tile (two at 16 pairs x 48 tiles: 20.95 against 21.15 us per
-// two-token layer step; four at the real expert geometry, 16 pairs x 128
-// tiles, where eight measured 60.9 against 59.6 us).
+// is small (up to 16 pairs x 48 tiles, one or two tokens at I 768); with
+// more tiles each block streams several consecutive tiles of its pair, up to
+// four, so the token row + selection before the first weight load is paid
+// once per block, not once per tile (four at the real expert geometry, 16
+// pairs x 128 tiles, where eight measured 60.9 against 59.6 us).  Two tiles
+// at 16 pairs x 48 tiles measured within the run-to-run spread of one
+// (20.91 against 20.99 us per step, interleaved on one box) and made the
+// kernel itself 4 % slower.
 static int pair_tiles_per_block(int pairs, int I) {
   const int tiles = I / 16;
   int tpb = 1;
-  while (tpb < 4 && (long long)pairs * tiles / tpb > 384 && tiles % (2 * tpb) == 0) tpb *= 2;
+  while (tpb < 4 && (long long)pairs * tiles / tpb > 768 && tiles % (2 * tpb) == 0) tpb *= 2;
   return tpb;
 }
 

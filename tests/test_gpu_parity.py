@@ -763,6 +763,8 @@ SMALL_LAYERS = [
     (3, 1024, 256, 8, 512, 128, (8, 4)),
     (4, 3072, 32, 4, 768, 0, (4, 2)),
     (2, 4096, 16, 3, 1024, 512, (1, 1)),
+    # two 16-row tiles per routed block (32 pairs x 48 tiles)
+    (4, 2048, 64, 8, 768, 768, (1, 1)),
     (4, 2048, 448, 8, 128, 256, (1, 1)),
     (5, 1024, 64, 6, 256, 256, (1, 1)),
     (9, 2048, 96, 5, 384, 0, (3, 2)),
