@@ -56,8 +56,9 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t *__re
 // products of f32(x) and W and accumulates them in f32 (only the summation
 // order differs from a sequential dot product: each wave keeps the even and
 // the odd K positions of a step in separate accumulators, added at the end).
-// Workgroup = 16 tokens x 32
-// experts (two 16 x 16 tiles); its KSPLIT waves split K into equal ranges
+// Workgroup = 16 tokens x 16 ET
+// experts (ET 16 x 16 tiles: two for many tokens, one for fewer, where it
+// doubles a small grid); its KSPLIT waves split K into equal ranges
 // (4 for many tokens, 16 for fewer, where the grid is small), so several
 // waves share each SIMD and hide each other's L2 latency, and the partial
 // sums are added in wave order through LDS.  MFMA i of a 32-wide K step takes
@@ -65,15 +66,16 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t *__re
 // (16 B of bf16) and 8 consecutive W (32 B) per step.  Rows past T or E are
 // clamped for the loads and never stored.
 // ---------------------------------------------------------------------------
-template <int KSPLIT, int PD>
+template <int KSPLIT, int PD, int ET = 2>
 __global__ __launch_bounds__(64 * KSPLIT) void router_gemm_kernel(
     const uint16_t *__restrict__ x, const float *__restrict__ w, int T, int d, int E,
     float *__restrict__ logits) {
   __shared__ glm_f32x4 red[KSPLIT - 1][2][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
+  static_assert(ET == 1 || ET == 2, "one or two expert tiles");
   const int t0 = blockIdx.x * 16;
-  const int e0 = blockIdx.y * 32;
+  const int e0 = blockIdx.y * 16 * ET;
   const int kq = d / KSPLIT;  // this wave's K range [wave * kq, (wave + 1) * kq), a multiple of 32 * PD
   const int kb = wave * kq;
   const uint16_t *xr = x + (size_t)min(t0 + r, T - 1) * d + kb + 8 * q;
@@ -116,9 +118,11 @@ __global__ __launch_bounds__(64 * KSPLIT) void router_gemm_kernel(
 #pragma unroll
       for (int m = 0; m < 8; m += 2) {
         acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[m], w0[m], acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[m], w1[m], acc1, 0, 0, 0);
+        if constexpr (ET == 2)
+          acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[m], w1[m], acc1, 0, 0, 0);
         acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[m + 1], w0[m + 1], acc2, 0, 0, 0);
-        acc3 = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[m + 1], w1[m + 1], acc3, 0, 0, 0);
+        if constexpr (ET == 2)
+          acc3 = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[m + 1], w1[m + 1], acc3, 0, 0, 0);
       }
     }
   }
@@ -141,7 +145,7 @@ __global__ __launch_bounds__(64 * KSPLIT) void router_gemm_kernel(
     const int t = t0 + 4 * q + m;
     if (t >= T) continue;
     if (e0 + r < E) logits[(size_t)t * E + e0 + r] = acc0[m];
-    if (e0 + 16 + r < E) logits[(size_t)t * E + e0 + 16 + r] = acc1[m];
+    if (ET == 2 && e0 + 16 + r < E) logits[(size_t)t * E + e0 + 16 + r] = acc1[m];
   }
 }
 
@@ -307,7 +311,11 @@ int glm_router_logits_launch(hipStream_t stream, const uint16_t *x, int T, int d
   }
   dim3 grid((T + 15) / 16, (E + 31) / 32);
   // prefetch depth: 32-wide K steps in flight per wave, where its K range allows
-  if (T >= 256 && d % (32 * 4) == 0) {
+  constexpr bool kOneTile = true;  // fewer than 256 tokens: one 16-expert tile per workgroup
+  if (T < 256 && d % (32 * 16 * 2) == 0 && kOneTile) {
+    grid.y = (E + 15) / 16;
+    hipLaunchKernelGGL((router_gemm_kernel<16, 2, 1>), grid, dim3(1024), 0, stream, x, weight, T, d, E, logits);
+  } else if (T >= 256 && d % (32 * 4) == 0) {
     if (d % (32 * 4 * 4) == 0)
       hipLaunchKernelGGL((router_gemm_kernel<4, 4>), grid, dim3(256), 0, stream, x, weight, T, d, E, logits);
     else
