@@ -302,6 +302,29 @@ __global__ __launch_bounds__(kRouteThreads) void route_logits_kernel(RouteArgs a
   }
 }
 
+// Logits already on the MFMA router: the per-token selection (one wave per
+// token, four tokens per block: blocks [0, sel)) rides beside the shared
+// expert's gate/up tiles (the blocks after them), which need only x.
+template <int CPW, int EPL>
+__global__ __launch_bounds__(kRouteThreads) void select_shared_kernel(RouteArgs a, SharedArgs sh) {
+  constexpr int kSelWords = 4 * (64 * EPL + 256) + 4 * 64;
+  constexpr int kRedWords = 3 * 2 * 64 * 4;
+  __shared__ __align__(16) float lds[kSelWords > kRedWords ? kSelWords : kRedWords];
+  const int sel_blocks = (a.T + 3) / 4;
+  if ((int)blockIdx.x >= sel_blocks) {
+    shared_gate_up_tile<CPW>(sh, blockIdx.x - sel_blocks, reinterpret_cast<glm_f32x4 *>(lds));
+    return;
+  }
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= a.T) return;  // wave-uniform; the selection synchronises one wave only
+  int *sel = reinterpret_cast<int *>(lds + 4 * (64 * EPL + 256)) + wave * 64;
+  select_token<EPL>(a.logits + (size_t)t * a.E, a.bias, a.E, a.k, a.n_group, a.topk_group,
+                    a.norm, a.scale, a.weights + (size_t)t * a.k, a.indices + (size_t)t * a.k, sel,
+                    lds + wave * (64 * EPL + 256), lane);
+}
+
 // One block: selection for every token, then the dispatch of its P pairs.
 template <int EPL, int CPW_S>
 __global__ __launch_bounds__(kRouteThreads) void select_dispatch_kernel(RouteArgs a,
@@ -1005,22 +1028,42 @@ int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d,
               perm,   inv,    pair_token, active, num_active, status, work, 0, 0};
   const SharedArgs sh = make_shared_args(x, T, d, sg, su, sd, Is, gp, up, hs, yp, limit);
   int rc;
-  if (glm_router_gemm_supported(T, d)) {  // many tokens: the logits on MFMA in their own kernel
+  const int epl = (E + 63) / 64;
+  const int e8 = epl <= 1 ? 1 : (epl <= 2 ? 2 : (epl <= 4 ? 4 : 8));
+  if (glm_router_gemm_supported(T, d)) {
+    // many tokens: the logits on MFMA in their own kernel, then the selection
+    // (one wave per token) beside the shared gate/up tiles
     rc = glm_router_logits_launch(stream, x, T, d, w, E, logits);
     if (rc) return rc;
     a.logits_done = 1;
-  }
-  rc = launch_route_logits(stream, a, sh);
-  if (rc) return rc;
-  // beyond a few tokens per wave the selection runs one wave per token first
-  if (T > 8) {
-    rc = glm_router_select_launch(stream, logits, bias, T, E, k, n_group, topk_group, norm, scale,
-                                  weights, indices);
-    if (rc) return rc;
     a.presel = 1;
+    const dim3 g((T + 3) / 4 + sh.gu_blocks);
+#define GLM_SS(C)                                                                              \
+  switch (e8) {                                                                                \
+    case 1: hipLaunchKernelGGL((select_shared_kernel<C, 1>), g, dim3(kRouteThreads), 0, stream, a, sh); break; \
+    case 2: hipLaunchKernelGGL((select_shared_kernel<C, 2>), g, dim3(kRouteThreads), 0, stream, a, sh); break; \
+    case 4: hipLaunchKernelGGL((select_shared_kernel<C, 4>), g, dim3(kRouteThreads), 0, stream, a, sh); break; \
+    default: hipLaunchKernelGGL((select_shared_kernel<C, 8>), g, dim3(kRouteThreads), 0, stream, a, sh); break; \
   }
-  const int epl = (E + 63) / 64;
-  const int e8 = epl <= 1 ? 1 : (epl <= 2 ? 2 : (epl <= 4 ? 4 : 8));
+    switch (d / 512) {
+      case 2: GLM_SS(2) break;
+      case 4: GLM_SS(4) break;
+      case 6: GLM_SS(6) break;
+      default: GLM_SS(8) break;
+    }
+#undef GLM_SS
+    GLM_LAUNCH_CHECK("select_shared_kernel");
+  } else {
+    rc = launch_route_logits(stream, a, sh);
+    if (rc) return rc;
+    // beyond a few tokens per wave the selection runs one wave per token first
+    if (T > 8) {
+      rc = glm_router_select_launch(stream, logits, bias, T, E, k, n_group, topk_group, norm,
+                                    scale, weights, indices);
+      if (rc) return rc;
+      a.presel = 1;
+    }
+  }
   const int cs = sg ? glm_decode_shared_cpws(Is) : 1;
   const size_t lds = std::max(glm_select_dispatch_lds_bytes(e8), (size_t)T * cs * 128 * 2);
   const dim3 g2(1 + sh.dn_blocks);
