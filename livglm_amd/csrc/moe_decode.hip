@@ -345,11 +345,26 @@ __global__ __launch_bounds__(kRouteThreads) void select_dispatch_kernel(RouteArg
   uint32_t *bits = (uint32_t *)(s_active + kFusedMaxE);  // [E][16]
   float *wave_scratch = (float *)(bits + kFusedMaxE * 16) + wave * (64 * EPL + 256);
 
+  // many tokens: the selection ran one wave per token in an earlier kernel;
+  // its indices (P <= 512: two per thread) are loaded before the LDS is
+  // cleared, so the memory round trip overlaps the clearing
+  constexpr int kPairsPerThread = kMaxFusedPairs / kRouteThreads;
+  int pre[kPairsPerThread];
+  if (a.presel) {
+#pragma unroll
+    for (int u = 0; u < kPairsPerThread; ++u) {
+      const int p = threadIdx.x + kRouteThreads * u;
+      pre[u] = p < P ? (int)a.indices[p] : 0;
+    }
+  }
   for (int i = threadIdx.x; i < E; i += kRouteThreads) cnt[i] = 0;
   for (int i = threadIdx.x; i < E * 16; i += kRouteThreads) bits[i] = 0;
   if (a.presel) {
-    // many tokens: the selection ran one wave per token in its own kernel
-    for (int p = threadIdx.x; p < P; p += kRouteThreads) s_idx[p] = (int)a.indices[p];
+#pragma unroll
+    for (int u = 0; u < kPairsPerThread; ++u) {
+      const int p = threadIdx.x + kRouteThreads * u;
+      if (p < P) s_idx[p] = pre[u];
+    }
   } else {
     // top-k per token (wave w: tokens w, w+4, ...)
     for (int t = wave; t < T; t += 4)
@@ -402,15 +417,23 @@ __global__ __launch_bounds__(kRouteThreads) void select_dispatch_kernel(RouteArg
   // The work slots go busiest expert first (ties by expert id): the routed
   // kernels' workgroups run in slot order, and a popular expert's tiles, which
   // loop over several token batches, would otherwise start last and set the
-  // launch's tail.  `active` stays ascending.
+  // launch's tail.  `active` stays ascending.  Slot of active expert u = the
+  // number of keys above its own, key(v) = count(v) * 1024 + 1023 - v (all
+  // distinct; the pad keys up to a multiple of 4 are -1, below every key).
+  int *key = reinterpret_cast<int *>(bits + kFusedMaxE * 16);  // [E] (selection scratch)
+  const int nkey = (tot_act + 3) & ~3;
+  for (int u = threadIdx.x; u < nkey; u += kRouteThreads)
+    key[u] = u < tot_act ? cnt[s_active[u]] * 1024 + 1023 - u : -1;
+  __syncthreads();
   for (int u = threadIdx.x; u < E; u += kRouteThreads) {
     if (u < tot_act) {
       const int ee = s_active[u];
       const int c = cnt[ee];
+      const int ku = key[u];
       int slot = 0;
-      for (int v = 0; v < tot_act; ++v) {
-        const int cv = cnt[s_active[v]];
-        slot += (cv > c || (cv == c && v < u)) ? 1 : 0;
+      for (int v = 0; v < nkey; v += 4) {
+        const int4 kv = *reinterpret_cast<const int4 *>(key + v);
+        slot += (kv.x > ku) + (kv.y > ku) + (kv.z > ku) + (kv.w > ku);
       }
       a.active[u] = ee;
       a.work[slot] = make_int4(ee, off[ee], c, 0);
