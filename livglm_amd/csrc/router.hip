@@ -309,10 +309,11 @@ int glm_router_logits_launch(hipStream_t stream, const uint16_t *x, int T, int d
     glm::set_error("router logits: unsupported T=%d d=%d", T, d);
     return GLM_ERR_UNSUPPORTED_SHAPE;
   }
+  // template arguments: K split (waves), 32-wide K steps in flight per wave,
+  // 16-expert tiles per workgroup
   dim3 grid((T + 15) / 16, (E + 31) / 32);
-  // prefetch depth: 32-wide K steps in flight per wave, where its K range allows
-  constexpr bool kOneTile = true;  // fewer than 256 tokens: one 16-expert tile per workgroup
-  if (T < 256 && d % (32 * 16 * 2) == 0 && kOneTile) {
+  if (T < 256 && d % (32 * 16 * 2) == 0) {
+    // fewer than 256 tokens: one 16-expert tile per workgroup, twice the grid
     grid.y = (E + 15) / 16;
     hipLaunchKernelGGL((router_gemm_kernel<16, 2, 1>), grid, dim3(1024), 0, stream, x, weight, T, d, E, logits);
   } else if (T >= 256 && d % (32 * 4) == 0) {
