@@ -472,21 +472,28 @@ struct GateUpArgs {
   int I, d;
   uint16_t *h;  // [P][I]
   float limit;
+  int shared_blocks;  // leading blocks that are the shared expert's gate/up tiles
 };
 
 // Routed gate/up: block b = (work slot b / (I/16), 16-row tile); 4 waves split
 // d.  The weights are loaded once; the expert's tokens go through in batches
 // of 16 (the MFMA's columns), each lane column reading its token's row from
-// global memory.
+// global memory.  With the shared expert riding along, the first
+// a.shared_blocks blocks are its full-K gate/up tiles (shared_gate_up_tile).
 template <int CPW>
-__global__ __launch_bounds__(256) void decode_gate_up_kernel(GateUpArgs a) {
+__global__ __launch_bounds__(256) void decode_gate_up_kernel(GateUpArgs a, SharedArgs sh) {
   __shared__ glm_f32x4 red[3 * 2 * 64];
+  if ((int)blockIdx.x < a.shared_blocks) {
+    shared_gate_up_tile<CPW>(sh, blockIdx.x, red);
+    return;
+  }
+  const int blk = (int)blockIdx.x - a.shared_blocks;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int d = a.d;
   const int tiles = a.I / 16;
-  const int4 wk = a.work[blockIdx.x / tiles];
-  const int row0 = (blockIdx.x % tiles) * 16;
+  const int4 wk = a.work[blk / tiles];
+  const int row0 = (blk % tiles) * 16;
   const int e = wk.x, base = wk.y, n = wk.z;
   if (e < 0 || n <= 0) return;
   const int kbase = wave * CPW * 128;
@@ -532,21 +539,29 @@ struct DownArgs {
   long long w_stride, s_stride;
   int I, d;
   uint16_t *y;  // [P][d]
+  int shared_blocks;  // leading blocks that are the shared expert's down tiles
 };
 
 // Routed down: block b = (work slot b / (d/64), 64-row tile); each wave owns
 // 16 output rows over the full K = I.  The weights are loaded once; the
 // slot's h rows go through in batches of 16, staged in LDS (all four waves
-// read every row).
-template <int CPW_R>
-__global__ __launch_bounds__(256) void decode_down_kernel(DownArgs a) {
+// read every row).  With the shared expert riding along, the first
+// a.shared_blocks blocks are its down tiles over the full-K gate/up tiles'
+// bf16 activations (shared_down_tile; no LDS).
+template <int CPW_R, int CPW_S>
+__global__ __launch_bounds__(256) void decode_down_kernel(DownArgs a, SharedArgs sh) {
   extern __shared__ __attribute__((aligned(16))) uint16_t s_x[];  // [16][lds_row_stride(I)]
+  if ((int)blockIdx.x < a.shared_blocks) {
+    shared_down_tile<CPW_S>(sh, blockIdx.x, s_x);
+    return;
+  }
+  const int blk = (int)blockIdx.x - a.shared_blocks;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int d = a.d;
   const int tiles = d / 64;
-  const int4 wk = a.work[blockIdx.x / tiles];
-  const int row0 = (blockIdx.x % tiles) * 64 + wave * 16;
+  const int4 wk = a.work[blk / tiles];
+  const int row0 = (blk % tiles) * 64 + wave * 16;
   const int e = wk.x, base = wk.y, n = wk.z;
   if (e < 0 || n <= 0) return;
   const uint8_t *wtile[1] = {tile_lane_ptr(a.dw + e * a.w_stride, row0, a.I, lane)};
@@ -1104,10 +1119,32 @@ int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d,
   return GLM_OK;
 }
 
+// From 16 to 32 tokens (the router on MFMA, full-K shared tiles in one or
+// two token groups) the decode path runs the bf16 shared expert's tiles
+// inside the routed expert kernels rather than beside the selection and the
+// dispatch, which they would otherwise outlast (d 2048, E 128, k 8, I 768:
+// 62.5 -> 58.8 us per layer step at 16 tokens, 76.9 -> 74.4 at 32).  At 64
+// tokens the four token groups re-read each shared tile four times inside
+// the routed stream, which costs more than it saves (92.5 -> 94.0), so there
+// the tiles stay beside the selection and the dispatch.
+bool glm_decode_shared_in_experts(int T, int d) {
+  return glm_router_gemm_supported(T, d) && glm_decode_shared_skq(T, d) == 1 && T <= 32;
+}
+
+// Routed gate/up of the decode path; with sg (and su, Is, hs) the shared
+// expert's full-K gate/up tiles run as the launch's first blocks and write
+// its bf16 activations hs [T][Is] (T > 8 only).
 int glm_decode_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int E,
                               int k, const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
                               const uint8_t *us, const int32_t *pair_token, const int4 *work,
-                              uint16_t *h, float limit) {
+                              uint16_t *h, float limit, const uint16_t *sg, const uint16_t *su,
+                              int Is, uint16_t *hs) {
+  const SharedArgs sh = make_shared_args(x, T, d, sg, su, nullptr, Is, nullptr, nullptr, hs,
+                                         nullptr, limit);
+  if (sg != nullptr && sh.skq != 1) {
+    glm::set_error("decode gate/up: the shared tiles ride along only from 9 tokens on (T=%d)", T);
+    return GLM_ERR_UNSUPPORTED_SHAPE;
+  }
   GateUpArgs a{};
   a.x = x;
   a.pair_token = pair_token;
@@ -1123,22 +1160,34 @@ int glm_decode_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int 
   a.d = d;
   a.h = h;
   a.limit = glm_limit_bf16(limit);
+  a.shared_blocks = sh.gu_blocks;
   const size_t lds = 0;
-  const int blocks = a.slots * (I / 16);
+  const int blocks = a.shared_blocks + a.slots * (I / 16);
   switch (d / 512) {
-    case 2: hipLaunchKernelGGL(decode_gate_up_kernel<2>, dim3(blocks), dim3(256), lds, stream, a); break;
-    case 4: hipLaunchKernelGGL(decode_gate_up_kernel<4>, dim3(blocks), dim3(256), lds, stream, a); break;
-    case 6: hipLaunchKernelGGL(decode_gate_up_kernel<6>, dim3(blocks), dim3(256), lds, stream, a); break;
-    case 8: hipLaunchKernelGGL(decode_gate_up_kernel<8>, dim3(blocks), dim3(256), lds, stream, a); break;
+    case 2: hipLaunchKernelGGL(decode_gate_up_kernel<2>, dim3(blocks), dim3(256), lds, stream, a, sh); break;
+    case 4: hipLaunchKernelGGL(decode_gate_up_kernel<4>, dim3(blocks), dim3(256), lds, stream, a, sh); break;
+    case 6: hipLaunchKernelGGL(decode_gate_up_kernel<6>, dim3(blocks), dim3(256), lds, stream, a, sh); break;
+    case 8: hipLaunchKernelGGL(decode_gate_up_kernel<8>, dim3(blocks), dim3(256), lds, stream, a, sh); break;
     default: glm::set_error("decode gate/up: unsupported d=%d", d); return GLM_ERR_UNSUPPORTED_SHAPE;
   }
   GLM_LAUNCH_CHECK("decode_gate_up_kernel");
   return GLM_OK;
 }
 
+// Routed down of the decode path; with sd (and Is, hs, yp) the shared
+// expert's down tiles over hs run as the launch's first blocks and write
+// their f32 K-range partial sums yp [skd][T][d] (T > 8 only).
 int glm_decode_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, int d,
                            int E, const uint8_t *dw, const uint8_t *ds, const int4 *work,
-                           uint16_t *y) {
+                           uint16_t *y, const uint16_t *sd, int Is, uint16_t *hs, float *yp) {
+  // (sd stands in for the gate/up pointers: it only marks the shared expert present)
+  const SharedArgs sh = make_shared_args(nullptr, T, d, sd, sd, sd, Is, nullptr, nullptr, hs, yp,
+                                         0.0f);
+  if (sd != nullptr && sh.skq != 1) {
+    glm::set_error("decode down: the shared tiles ride along only from 9 tokens on (T=%d)", T);
+    return GLM_ERR_UNSUPPORTED_SHAPE;
+  }
+  const int cs = sd != nullptr ? glm_decode_shared_cpws(Is) : 1;
   DownArgs a{};
   a.h = h;
   a.work = work;
@@ -1150,17 +1199,24 @@ int glm_decode_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, 
   a.I = I;
   a.d = d;
   a.y = y;
+  a.shared_blocks = sh.dn_blocks;
   const size_t lds = (size_t)std::min(T * k, kDownStageRows) * lds_row_stride(I) * 2;
-  const int blocks = a.slots * (d / 64);
+  const int blocks = a.shared_blocks + a.slots * (d / 64);
+#define GLM_DOWN(CR)                                                                            \
+  if (cs == 1)                                                                                  \
+    hipLaunchKernelGGL((decode_down_kernel<CR, 1>), dim3(blocks), dim3(256), lds, stream, a, sh); \
+  else                                                                                          \
+    hipLaunchKernelGGL((decode_down_kernel<CR, 2>), dim3(blocks), dim3(256), lds, stream, a, sh)
   switch (I / 128) {
-    case 1: hipLaunchKernelGGL(decode_down_kernel<1>, dim3(blocks), dim3(256), lds, stream, a); break;
-    case 2: hipLaunchKernelGGL(decode_down_kernel<2>, dim3(blocks), dim3(256), lds, stream, a); break;
-    case 4: hipLaunchKernelGGL(decode_down_kernel<4>, dim3(blocks), dim3(256), lds, stream, a); break;
-    case 6: hipLaunchKernelGGL(decode_down_kernel<6>, dim3(blocks), dim3(256), lds, stream, a); break;
-    case 8: hipLaunchKernelGGL(decode_down_kernel<8>, dim3(blocks), dim3(256), lds, stream, a); break;
-    case 16: hipLaunchKernelGGL(decode_down_kernel<16>, dim3(blocks), dim3(256), lds, stream, a); break;
+    case 1: GLM_DOWN(1); break;
+    case 2: GLM_DOWN(2); break;
+    case 4: GLM_DOWN(4); break;
+    case 6: GLM_DOWN(6); break;
+    case 8: GLM_DOWN(8); break;
+    case 16: GLM_DOWN(16); break;
     default: glm::set_error("decode down: unsupported I=%d", I); return GLM_ERR_UNSUPPORTED_SHAPE;
   }
+#undef GLM_DOWN
   GLM_LAUNCH_CHECK("decode_down_kernel");
   return GLM_OK;
 }

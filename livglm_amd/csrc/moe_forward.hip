@@ -93,10 +93,12 @@ int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d,
 int glm_decode_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int E,
                               int k, const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
                               const uint8_t *us, const int32_t *pair_token, const int4 *work,
-                              uint16_t *h, float limit);
+                              uint16_t *h, float limit, const uint16_t *sg, const uint16_t *su,
+                              int Is, uint16_t *hs);
 int glm_decode_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, int d,
                            int E, const uint8_t *dw, const uint8_t *ds, const int4 *work,
-                           uint16_t *y);
+                           uint16_t *y, const uint16_t *sd, int Is, uint16_t *hs, float *yp);
+bool glm_decode_shared_in_experts(int T, int d);
 int glm_combine_parts_launch(hipStream_t stream, const uint16_t *y, const int32_t *inv,
                              const float *w, const uint16_t *shared, const float *shared_parts,
                              int nparts, int T, int k, int d, float *out);
@@ -478,22 +480,27 @@ static int moe_forward_core(void *stream_v, const uint16_t *x, int T, int d,
     return rc;
   }
   if (glm_decode_path_supported(T, d, E, top_k, I, fuse_shared ? Is : 0)) {
-    // decode: five short kernels, no host synchronisation; the bf16 shared
-    // expert rides in the two routing kernels
+    // decode: six short kernels, no host synchronisation; the bf16 shared
+    // expert rides in the two routing kernels, or from 16 tokens on (router
+    // logits on MFMA) in the two routed expert kernels
+    const bool in_experts = fuse_shared && glm_decode_shared_in_experts(T, d);
+    const bool in_route = fuse_shared && !in_experts;
+    const uint16_t *sg = (const uint16_t *)shared_gate, *su = (const uint16_t *)shared_up,
+                   *sd = (const uint16_t *)shared_down;
     rc = glm_route_decode_launch(
         stream, x, T, d, router_weight, router_bias, E, top_k, n_group, topk_group,
         norm_topk_prob, routed_scaling_factor, w.logits, wts, idx, w.counts, w.offsets, w.perm,
-        w.inv, w.pair_token, w.active, w.num_active, w.status, w.work,
-        fuse_shared ? (const uint16_t *)shared_gate : nullptr,
-        fuse_shared ? (const uint16_t *)shared_up : nullptr,
-        fuse_shared ? (const uint16_t *)shared_down : nullptr, Is, w.gp, w.up, w.shared_h, w.yp,
+        w.inv, w.pair_token, w.active, w.num_active, w.status, w.work, in_route ? sg : nullptr,
+        in_route ? su : nullptr, in_route ? sd : nullptr, Is, w.gp, w.up, w.shared_h, w.yp,
         swiglu_limit);
     if (rc) return rc;
     rc = glm_decode_gate_up_launch(stream, x, T, d, I, E, top_k, gate_packed, gate_scales,
-                                   up_packed, up_scales, w.pair_token, w.work, w.h, swiglu_limit);
+                                   up_packed, up_scales, w.pair_token, w.work, w.h, swiglu_limit,
+                                   in_experts ? sg : nullptr, in_experts ? su : nullptr, Is,
+                                   w.shared_h);
     if (rc) return rc;
     rc = glm_decode_down_launch(stream, w.h, T, top_k, I, d, E, down_packed, down_scales, w.work,
-                                w.y);
+                                w.y, in_experts ? sd : nullptr, Is, w.shared_h, w.yp);
     if (rc) return rc;
     if (fuse_shared)
       return glm_combine_parts_launch(stream, w.y, w.inv, wts, nullptr, w.yp,

@@ -787,10 +787,11 @@ static int check_fmt(int fmt) {
 int glm_decode_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int E,
                               int k, const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
                               const uint8_t *us, const int32_t *pair_token, const int4 *work,
-                              uint16_t *h, float limit);
+                              uint16_t *h, float limit, const uint16_t *sg, const uint16_t *su,
+                              int Is, uint16_t *hs);
 int glm_decode_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, int d,
                            int E, const uint8_t *dw, const uint8_t *ds, const int4 *work,
-                           uint16_t *y);
+                           uint16_t *y, const uint16_t *sd, int Is, uint16_t *hs, float *yp);
 bool glm_decode_gate_up_supported(int d, int I);
 bool glm_decode_down_supported(int I, int d);
 
@@ -799,7 +800,7 @@ int glm_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int 
                        const int32_t *pair_token, const int4 *work, float limit, uint16_t *h) {
   if (glm_decode_gate_up_supported(d, I))
     return glm_decode_gate_up_launch(stream, x, T, d, I, E, k, gw, gs, uw, us, pair_token, work,
-                                     h, limit);
+                                     h, limit, nullptr, nullptr, 0, nullptr);
   GemvArgs a{};
   a.act = x;
   a.act_index = pair_token;
@@ -822,7 +823,8 @@ int glm_gate_up_launch(hipStream_t stream, const uint16_t *x, int T, int d, int 
 int glm_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, int d, int E,
                     const uint8_t *dw, const uint8_t *ds, const int4 *work, uint16_t *y) {
   if (glm_decode_down_supported(I, d))
-    return glm_decode_down_launch(stream, h, T, k, I, d, E, dw, ds, work, y);
+    return glm_decode_down_launch(stream, h, T, k, I, d, E, dw, ds, work, y, nullptr, 0, nullptr,
+                                  nullptr);
   GemvArgs a{};
   a.act = h;
   a.act_index = nullptr;

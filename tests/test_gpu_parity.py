@@ -776,6 +776,11 @@ SMALL_LAYERS = [
     (700, 1024, 32, 8, 256, 0, (1, 1)),
     # the decode path beyond 16 tokens (MFMA router, per-token selection, token groups)
     (40, 1024, 64, 8, 512, 512, (1, 1)),
+    # 16-32 tokens: the shared expert's tiles in the routed expert kernels (two
+    # chunks per shared down K range; one chunk at I_shared 128, two token groups)
+    (16, 2048, 64, 8, 768, 768, (1, 1)),
+    (24, 1024, 32, 4, 256, 128, (2, 1)),
+    (32, 4096, 24, 8, 2048, 1024, (1, 1)),
     # k = 64, every expert of E = 64 chosen by every token (the top-k upper bound)
     (3, 256, 64, 64, 64, 64, (1, 1)),
     # the real expert geometry with few experts (d = 4096, I = 2048, I_shared 1024)
