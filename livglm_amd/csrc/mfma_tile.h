@@ -64,11 +64,21 @@ __device__ __forceinline__ WChunk<FMT_MXFP4> load_mxfp4_chunk(const uint8_t *wti
 }
 
 // bf16 weights of lane q in the chunk at k0 (row-major row wrow): K = k0 +
-// 32i + 8q + [0, 8) in v[i].
+// 32i + 8q + [0, 8) in v[i].  NT: non-temporal loads (the full-K shared
+// tiles of many tokens, whose token groups re-read a tile); otherwise plain
+// loads, which the K-split tiles of a few tokens (each weight read once)
+// take slightly faster: 20.8 -> 20.5-20.6 us per layer step at two tokens
+// (d 2048, I_shared 768; three interleaved runs, one token within the
+// spread), where plain loads in the full-K tiles measured 92.7 -> 93.3 us at
+// 64 tokens.
+template <bool NT = true>
 __device__ __forceinline__ WChunk<FMT_BF16> load_bf16_chunk(const uint8_t *wrow, int k0, int q) {
   WChunk<FMT_BF16> w;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) w.v[i] = load_stream(wrow + 2 * k0 + 64 * i + 16 * q);
+  for (int i = 0; i < 4; ++i) {
+    const uint8_t *p = wrow + 2 * k0 + 64 * i + 16 * q;
+    w.v[i] = NT ? load_stream(p) : *reinterpret_cast<const glm_u32x4 *>(p);
+  }
   return w;
 }
 
@@ -299,8 +309,8 @@ __device__ __forceinline__ void stage_rows(uint16_t *s_x, const uint16_t *src,
 // wrow is each projection's tile_lane_ptr and srow this lane's scale row
 // (byte q of dword c at srow + kbase/32 is its group); bf16: wrow is this
 // lane's row.  act: this lane's activation row (a valid row for a padding
-// column).
-template <int FMT, int NPROJ, int CPW>
+// column).  NT: bf16 weights with non-temporal loads (load_bf16_chunk).
+template <int FMT, int NPROJ, int CPW, bool NT = true>
 __device__ __forceinline__ void wave_mma(const uint8_t *const wrow[NPROJ],
                                          const uint8_t *const srow[NPROJ], int kbase, int q,
                                          const uint16_t *act, glm_f32x4 acc[NPROJ]) {
@@ -318,7 +328,7 @@ __device__ __forceinline__ void wave_mma(const uint8_t *const wrow[NPROJ],
 #pragma unroll
       for (int c = 0; c < NB; ++c)
 #pragma unroll
-        for (int p = 0; p < NPROJ; ++p) w[p][c] = load_bf16_chunk(wrow[p], kbase + (b0 + c) * 128, q);
+        for (int p = 0; p < NPROJ; ++p) w[p][c] = load_bf16_chunk<NT>(wrow[p], kbase + (b0 + c) * 128, q);
       glm_bf16x8 xb[NB][4];
 #pragma unroll
       for (int c = 0; c < NB; ++c) load_act_frags(act, kbase + (b0 + c) * 128, q, xb[c]);

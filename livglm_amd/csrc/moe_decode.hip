@@ -119,7 +119,7 @@ __device__ void shared_gate_up_tile(const SharedArgs &a, int b, glm_f32x4 *red) 
       const int t = p0 + r;
       const uint16_t *act = a.x + (size_t)min(t, a.T - 1) * d;  // padding: any valid row
       glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
-      wave_mma<FMT_BF16, 2, 1>(wrow, srow, kbase, q, act, acc);
+      wave_mma<FMT_BF16, 2, 1, false>(wrow, srow, kbase, q, act, acc);
       if (ksplit_reduce<2>(acc, red, wave, 4, lane) && t < a.T) {
         const size_t o = ((size_t)kq * a.T + t) * a.Is + row0 + 4 * q;
         *reinterpret_cast<glm_f32x4 *>(a.gp + o) = acc[0];
@@ -170,7 +170,7 @@ __device__ void shared_down_tile(const SharedArgs &a, int b, uint16_t *s_h) {
     const uint8_t *wp = a.sd + ((size_t)(row0 + r) * a.Is + kbase) * 2;
     WChunk<FMT_BF16> w[CPW_S];
 #pragma unroll
-    for (int c = 0; c < CPW_S; ++c) w[c] = load_bf16_chunk(wp, c * 128, q);
+    for (int c = 0; c < CPW_S; ++c) w[c] = load_bf16_chunk<false>(wp, c * 128, q);
     for (int i0 = 0; i0 < a.T * KS; i0 += 512) {
       float gv[2][kMaxSkq], uv[2][kMaxSkq];
 #pragma unroll
