@@ -980,6 +980,427 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
   }
 }
 
+// ---------------------------------------------------------------------------
+// Eight-wave form of the block-scaled GEMMs: the same workgroup tile (up to
+// 160 dispatch rows x 512 weight rows), LDS stage and direct-to-LDS loads as
+// grouped_f8f6f4_kernel, computed by 8 waves of up to 256 registers (two per
+// SIMD) as 4 (weight rows) x 2 (tokens): each wave owns 128 weight rows x up
+// to 80 tokens = 8 x 5 MFMA blocks.  Every activation fragment read from LDS
+// then feeds 8 MFMAs instead of 4 (229 KB of operand reads per chunk and
+// workgroup instead of 393 KB), and the registers leave room to read
+// fragment f + 1 while the MFMAs of fragment f run.  The body is
+// instantiated per count NB of the wave's 16-row token blocks (0..5), so every
+// fragment and accumulator index is static.
+// ---------------------------------------------------------------------------
+constexpr int kW8Threads = 512;
+constexpr int kW8Waves = kW8Threads / 64;
+constexpr int kW8YRow = 272;  // bytes per row of the down epilogue's staging (256 + 16)
+
+// LDS of the eight-wave form: the two stages' parts side by side (all
+// activation codes, then all weight codes, weight scales, activation scales),
+// so that every operand read is a per-lane base register plus an immediate
+// offset below 64 KB.
+template <int AF>
+struct W8Layout {
+  using S = SplitStage<AF>;
+  static constexpr int kX = 0;
+  static constexpr int kW = kX + kSplitStages * S::kXBytes;
+  static constexpr int kWS = kW + kSplitStages * S::kWBytes;
+  static constexpr int kXS = kWS + kSplitStages * S::kWSBytes;
+  // the row table: one u32 per row any activation load can name (rows past
+  // the tile's hold row 0's offset)
+  static constexpr int kTabRows =
+      (S::kXSlots + kW8Waves - 1) / kW8Waves * kW8Waves * (64 / S::kXPieces);
+  static constexpr int kRows = kXS + kSplitStages * S::kXSBytes;  // u32 [kTabRows]
+  static constexpr int kBytes = kRows + kTabRows * 4;
+  static_assert(kRows == kSplitStages * S::kBytes, "the stages as in the stage layout");
+  static_assert(kBytes <= 160 * 1024, "LDS exceeds 160 KB");
+  static_assert((kSplitStages - 1) * S::kXBytes + (kSplitTileM / 2) * S::kXRow < 65536 &&
+                    (kSplitStages - 1) * S::kWBytes + S::kWBytes - 1024 < 65536,
+                "operand offsets fit the 16-bit LDS immediate");
+  static_assert(kW8Waves * 16 * kW8YRow <= kBytes, "the down epilogue's staging fits");
+};
+
+template <int N>
+struct W8Stage {
+  static constexpr int value = N;
+};
+
+// N dwords from LDS at base + j * STEP (j < N, at most 5) into v; the caller
+// waits for them (lgkmcnt) before use.
+template <int N, int STEP>
+__device__ __forceinline__ void lds_rows(uint32_t *v, uint32_t base) {
+  static_assert(N >= 1 && N <= 5 && (N - 1) * STEP < 65536, "row table reads");
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v[0]) : "v"(base) : "memory");
+  if constexpr (N > 1) asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v[1]) : "v"(base), "i"(STEP) : "memory");
+  if constexpr (N > 2) asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v[2]) : "v"(base), "i"(2 * STEP) : "memory");
+  if constexpr (N > 3) asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v[3]) : "v"(base), "i"(3 * STEP) : "memory");
+  if constexpr (N > 4) asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v[4]) : "v"(base), "i"(4 * STEP) : "memory");
+}
+
+template <int NPROJ, int AF, int NB>
+__device__ __forceinline__ void w8_body(const SplitArgs &a, long long e, int pos0, int rows,
+                                        int ftile, int tok0) {
+  using S = SplitStage<AF>;
+  using L = W8Layout<AF>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int r = lane & 15, q = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wf = wv & 3;
+  const int K = a.K;
+  const int nchunks = K / 128;
+  constexpr int kHalf = kSplitTileW / 2;
+  const int f0 = ftile * (kSplitTileW / NPROJ);
+  auto act_row = [&](int row) -> uint32_t {
+    const int pos = pos0 + (row < rows ? row : 0);  // past the end: re-read row 0
+    return (uint32_t)(a.act_index != nullptr ? a.act_index[pos] : pos);
+  };
+
+  // ---- load assignment (fixed over the K loop), as grouped_f8f6f4_kernel's
+  // with 8 waves: activation wave load j * 8 + w; weight block g = j * 8 + w
+  // (loads 0-1 the first projection's 256 rows, 2-3 the second's); weight
+  // scale rows 64 w .. 64 w + 63; activation scale slots 64 w .. 64 w + 63.
+  // Only the activation rows are per lane; the weight offsets are a lane
+  // term plus a uniform one.
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.xhi, a.split_bytes);
+  const uint32_t lo_off = (uint32_t)(a.xlo - a.xhi);
+  const uint32_t code_row = (uint32_t)act_code_row(K, AF);
+  // Activation wave load j of wave w covers rows R_j = (8 j + w) 64 / kXPieces
+  // + lane / kXPieces; the lane's piece is the same for every j (the row's
+  // swizzle bits do not depend on j), so a load's offset is the code-row
+  // offset of R_j, from a table of the tile's rows in LDS, plus one per-lane
+  // piece offset.
+  constexpr int kXL = (S::kXSlots + kW8Waves - 1) / kW8Waves;  // 5 or 2
+  constexpr int kRowsPerLoad = 64 / S::kXPieces;
+  uint32_t xpiece;
+  {
+    const int row = (wv * 64 + lane) / S::kXPieces;
+    const int piece = (lane % S::kXPieces) ^ S::xswz(row);
+    xpiece = S::kParts == 2 ? (piece < 8 ? 0u : lo_off) + (piece & 7) * 16 : piece * 16;
+  }
+  const uint32_t xtab = (uint32_t)(L::kRows + 4 * (wv * kRowsPerLoad + lane / S::kXPieces));
+  static_assert(L::kTabRows == kXL * kW8Waves * kRowsPerLoad && L::kTabRows >= kSplitTileM,
+                "the row table covers every load");
+  for (int i = threadIdx.x; i < L::kTabRows; i += kW8Threads)
+    reinterpret_cast<uint32_t *>(smem + L::kRows)[i] = act_row(i) * code_row;
+  constexpr int kWL = S::kWBytes / (kW8Threads * 16);
+  static_assert(kWL == 4, "two weight loads per projection");
+  const uint32_t wproj_bytes = (uint32_t)a.N * (uint32_t)(K / 2);
+  const __amdgpu_buffer_rsrc_t wrs0 = make_rsrc(a.w[0] + e * a.w_stride, wproj_bytes);
+  const __amdgpu_buffer_rsrc_t wrs1 = make_rsrc(a.w[NPROJ == 2 ? 1 : 0] + e * a.w_stride,
+                                                wproj_bytes);
+  const uint32_t wlane = 16u * lane;
+  uint32_t wuni[kWL];  // the block's first feature / 16 x the bytes of a block row
+#pragma unroll
+  for (int j = 0; j < kWL; ++j) {
+    const int g = j * kW8Waves + wv;
+    const int feat = f0 + (NPROJ == 2 ? (16 * g) % kHalf : 16 * g);
+    wuni[j] = (uint32_t)(feat / 16) * (uint32_t)(K / 128) * 1024u;
+  }
+  const __amdgpu_buffer_rsrc_t wsrs =
+      make_rsrc(a.s[NPROJ == 2 && wv >= 4 ? 1 : 0] + e * a.s_stride,
+                (uint32_t)a.N * (uint32_t)(K / 32));
+  const uint32_t wslane = (uint32_t)lane * (uint32_t)(K / 32);
+  const uint32_t wsuni =
+      (uint32_t)(f0 + (NPROJ == 2 ? (wv * 64) % kHalf : wv * 64)) * (uint32_t)(K / 32);
+  // every wave loads 64 scale slots (wave w: slots 64 w mod the padded
+  // count, so waves past the last slot repeat earlier ones with the same
+  // bytes); padding slots load slot 0's scale
+  const int xs0 = (wv * 64) % S::kXSLanes;
+  uint32_t xsoff;
+  {
+    const int s = xs0 + lane < S::kXSRows ? xs0 + lane : 0;
+    xsoff = (uint32_t)((s >= kSplitTileM ? a.xslo : a.xshi) - a.xhi) +
+            act_row(s % kSplitTileM) * (uint32_t)(K / 32);
+  }
+
+  auto issue = [&](auto st, int c) {
+    constexpr int ST = decltype(st)::value;
+    // the table reads as explicit instructions (one base register, immediate
+    // offsets; a compiler-generated read would keep one address register per
+    // load live across the loop), waited for after the weight loads
+    uint32_t xrow[kXL];
+    lds_rows<kXL, 4 * kW8Waves * kRowsPerLoad>(xrow, xtab);
+#pragma unroll
+    for (int j = 0; j < kWL; ++j)
+      buf16_to_lds(j < 2 ? wrs0 : wrs1, smem + L::kW + ST * S::kWBytes + (j * kW8Waves + wv) * 1024,
+                   wlane, wuni[j] + c * 1024);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int j = 0; j < kXL; ++j)
+      if (S::kXSlots % kW8Waves == 0 || j * kW8Waves + wv < S::kXSlots)
+        buf16_to_lds(xrs, smem + L::kX + ST * S::kXBytes + (j * kW8Waves + wv) * 1024,
+                     xrow[j] + xpiece, c * S::kTermChunk);
+    buf4_to_lds(wsrs, smem + L::kWS + ST * S::kWSBytes + wv * 256, wslane, wsuni + c * 4);
+    buf4_to_lds(xrs, smem + L::kXS + ST * S::kXSBytes + xs0 * 4, xsoff, c * 4);
+  };
+
+  // the wave's weight blocks (16 rows each, index into the stage's 32):
+  // gate/up: 4 gate blocks (features 64 wf .. 64 wf + 63), then the 4 up
+  // blocks of the same features; down: 8 consecutive blocks
+  auto wblk = [&](int b) {
+    return NPROJ == 2 ? (b < 4 ? 4 * wf + b : 16 + 4 * wf + b - 4) : 8 * wf + b;
+  };
+
+  glm_f32x4 acc[8][NB > 0 ? NB : 1];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < (NB > 0 ? NB : 1); ++j) acc[i][j] = glm_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Per-lane LDS bases.  Activation row tok0 + 16 ct + r, piece p at
+  // row * kXRow + 16 (p ^ swizzle(r)): the term-t, half-h piece of the
+  // two-term formats, p = 8 t + 4 h + q, lies at xl ^ 64 (2 t + h) (the row
+  // part is a multiple of 256); ACT_FP4's piece q at xl.  Weight block b,
+  // group q of row r at 1024 b + 16 lane; scale bytes at 4 row + q.
+  static_assert((L::kX % 256 == 0 && S::kXRow % 256 == 0) || S::kParts == 1, "xor addressing");
+  const uint32_t xl = (uint32_t)(L::kX + (tok0 + r) * S::kXRow +
+                                 16 * (S::kParts == 2 ? (q ^ r) : (q ^ ((r >> 1) & 3))));
+  const uint32_t wl = (uint32_t)L::kW + wlane;
+  const uint32_t wsl = (uint32_t)(L::kWS + 4 * r + q);
+  const uint32_t xsl = (uint32_t)(L::kXS + 4 * (tok0 + r) + q);
+
+  // MFMAs of one staged chunk: the activation fragment f + 1 (term f / NB,
+  // token block f % NB) is read while the 8 MFMAs of fragment f run.  The
+  // weight scale bytes are packed four to a register; the MFMA's byte select
+  // picks one.
+  auto compute = [&](auto st) {
+    constexpr int ST = decltype(st)::value;
+    if constexpr (NB > 0) {
+      constexpr int kFrags = NB * S::kParts;
+      glm_i32x8 xb[2];
+      int xsc[2];
+      auto xfrag = [&](int f, glm_i32x8 &xbv, int &xs) {
+        const int t = f / NB, ct = f % NB;
+        constexpr int kXo = ST * S::kXBytes;
+        const int co = kXo + ct * 16 * S::kXRow;
+        const glm_u32x4 b0 = *reinterpret_cast<const glm_u32x4 *>(smem + (xl ^ (128u * t)) + co);
+        if constexpr (S::kParts == 2) {
+          const glm_u32x4 b1 =
+              *reinterpret_cast<const glm_u32x4 *>(smem + (xl ^ (128u * t + 64u)) + co);
+          xbv = glm_i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3],
+                          (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+        } else {
+          xbv = glm_i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], 0, 0, 0, 0};
+        }
+        xs = smem[xsl + ST * S::kXSBytes + 4 * (t * kSplitTileM + ct * 16)];
+      };
+      xfrag(0, xb[0], xsc[0]);
+      glm_i32x8 wa[8];
+      int wsp[2];
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+        uint32_t sb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int blk = wblk(4 * hb + i);
+          const glm_u32x4 v =
+              *reinterpret_cast<const glm_u32x4 *>(smem + wl + ST * S::kWBytes + blk * 1024);
+          wa[4 * hb + i] = glm_i32x8{(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
+          sb[i] = smem[wsl + ST * S::kWSBytes + blk * 64];
+        }
+        wsp[hb] = (int)(sb[0] | (sb[1] << 8) | (sb[2] << 16) | (sb[3] << 24));
+      }
+#pragma unroll
+      for (int f = 0; f < kFrags; ++f) {
+        if (f + 1 < kFrags) xfrag(f + 1, xb[(f + 1) & 1], xsc[(f + 1) & 1]);
+        const int ct = f % NB;
+        const glm_i32x8 &xv = xb[f & 1];
+        const int xs = xsc[f & 1];
+        // weight block B (its scale byte B % 4 of wsp[B / 4]); the byte
+        // select must be a constant, hence one instantiation per block
+        auto mf = [&](auto bt) {
+          constexpr int B = decltype(bt)::value;
+          if (f < NB)
+            acc[B][ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                wa[B], xv, acc[B][ct], 4, S::kMfmaFmt, B & 3, wsp[B >> 2], 0, xs);
+          else
+            acc[B][ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                wa[B], xv, acc[B][ct], 4, S::kMfmaFmtLo, B & 3, wsp[B >> 2], 0, xs);
+        };
+        mf(W8Stage<0>{});
+        mf(W8Stage<1>{});
+        mf(W8Stage<2>{});
+        mf(W8Stage<3>{});
+        mf(W8Stage<4>{});
+        mf(W8Stage<5>{});
+        mf(W8Stage<6>{});
+        mf(W8Stage<7>{});
+      }
+      // the schedule: the chunk's first fragment, weights and scales, then per
+      // fragment the next fragment's three reads ahead of its 8 MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 3 + 16, 0);
+#pragma unroll
+      for (int f = 0; f < kFrags; ++f) {
+        if (f + 1 < kFrags) __builtin_amdgcn_sched_group_barrier(0x100, S::kParts + 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+      }
+    }
+  };
+
+  // Double buffer, unrolled by two so that each stage's offsets are
+  // immediates: the loads of chunk c + 1 are issued after the barrier that
+  // follows every wave's chunk c - 1 (whose stage they overwrite) and land
+  // while chunk c is consumed.
+  auto step = [&](auto st, int c) {
+    constexpr int ST = decltype(st)::value;
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    ring_barrier();
+    if (c + 1 < nchunks) issue(W8Stage<1 - ST>{}, c + 1);
+    compute(st);
+  };
+  ring_barrier();  // the row table
+  issue(W8Stage<0>{}, 0);
+  for (int c = 0; c < nchunks; c += 2) {
+    step(W8Stage<0>{}, c);
+    if (c + 1 < nchunks) step(W8Stage<1>{}, c + 1);
+  }
+  // the down epilogue stages y in LDS that other waves may still read:
+  // every wave (also one without token blocks) passes this barrier first
+  if constexpr (NPROJ == 1) ring_barrier();
+  if constexpr (NB == 0) return;
+
+  const float lim = a.limit > 0.0f ? a.limit : __builtin_inff();
+  auto swiglu_pair = [&](const glm_f32x4 &g, const glm_f32x4 &u, int m, float &h0, float &h1) {
+    float g0 = g[m], g1 = g[m + 1], u0 = u[m], u1 = u[m + 1];
+    bf16_round2(g0, g1);
+    bf16_round2(u0, u1);
+    limited_swiglu2_fast(g0, g1, u0, u1, lim, h0, h1);
+  };
+
+  // ---- epilogue: lane (r, q) of block (b, ct) holds weight rows 4q..4q+3 of
+  // the block for token column r
+  if constexpr (NPROJ == 2 && AF == ACT_FP8X2) {
+    if (a.out_split != nullptr) {
+      // h's FP8 hi/lo split (as act_split_kernel forms it from the bf16 h):
+      // the wave's 64 features are two scale groups, group gi held 8 per lane
+      // by the lanes (r, q = 0..3) in gate/up blocks 2 gi, 2 gi + 1
+      const SplitLayout SL(a.out_rows, a.N);
+#pragma unroll
+      for (int ct = 0; ct < NB; ++ct) {
+        const int row = tok0 + ct * 16 + r;
+#pragma unroll
+        for (int gi = 0; gi < 2; ++gi) {
+          float v[8];
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int m = 0; m < 4; m += 2)
+              swiglu_pair(acc[2 * gi + i][ct], acc[4 + 2 * gi + i][ct], m, v[4 * i + m],
+                          v[4 * i + m + 1]);
+          uint32_t ch[2], cl[2];
+          int bh, bl;
+          split_group_part(v, ch, cl, &bh, &bl);
+          if (row < rows) {
+            const int g0 = f0 + wf * 64 + gi * 32;
+            const size_t prow = (size_t)(pos0 + row);
+            uint8_t *hi = a.out_split + prow * a.N + g0;
+            uint8_t *lo = a.out_split + SL.lo + prow * a.N + g0;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+              *reinterpret_cast<uint32_t *>(hi + i * 16 + 4 * q) = ch[i];
+              *reinterpret_cast<uint32_t *>(lo + i * 16 + 4 * q) = cl[i];
+            }
+            if (q == 0) {
+              a.out_split[SL.shi + prow * (a.N / 32) + g0 / 32] = (uint8_t)bh;
+              a.out_split[SL.slo + prow * (a.N / 32) + g0 / 32] = (uint8_t)bl;
+            }
+          }
+        }
+      }
+      return;
+    }
+  }
+  if constexpr (NPROJ == 2) {
+#pragma unroll
+    for (int ct = 0; ct < NB; ++ct) {
+      const int row = tok0 + ct * 16 + r;
+      if (row >= rows) continue;
+      uint16_t *orow = a.out + (size_t)(pos0 + row) * a.N;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float h[4];
+        swiglu_pair(acc[i][ct], acc[4 + i][ct], 0, h[0], h[1]);
+        swiglu_pair(acc[i][ct], acc[4 + i][ct], 2, h[2], h[3]);
+        uint32_t o[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) o[m] = __float_as_uint(h[m]) >> 16;  // bf16-exact
+        store_rows4(orow + f0 + wf * 64 + i * 16 + 4 * q, o);
+      }
+    }
+  } else {
+    // y through LDS so that every store writes whole 128-byte lines: per
+    // token block the wave's 16 rows x 128 features go to its own 16 x 272 B
+    // area and come back as 16 contiguous bytes per lane, 16 lanes a row
+    uint8_t *yst = smem + wv * (16 * kW8YRow);
+    const int rr = lane >> 4, seg = lane & 15;
+#pragma unroll
+    for (int ct = 0; ct < NB; ++ct) {
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        uint32_t o[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) o[m] = f32_to_bf16(acc[b][ct][m]);
+        *reinterpret_cast<uint2 *>(yst + r * kW8YRow + (b * 16 + 4 * q) * 2) =
+            uint2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const int row = tok0 + ct * 16 + 4 * h + rr;
+        const glm_u32x4 v =
+            *reinterpret_cast<const glm_u32x4 *>(yst + (4 * h + rr) * kW8YRow + 16 * seg);
+        if (row < rows)
+          *reinterpret_cast<glm_u32x4 *>(a.out + (size_t)(pos0 + row) * a.N + f0 + wf * 128 +
+                                         8 * seg) = v;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  }
+}
+
+template <int NPROJ, int AF>
+__global__ __launch_bounds__(kW8Threads) void grouped_f8f6f4_w8_kernel(SplitArgs a) {
+  const int nft = a.feature_tiles;
+  // a count above the list's length is clamped to it, so no entry past
+  // `tiles` is read and every item still has a workgroup in the grid
+  const int ntiles = max(0, min(*a.num_tiles, a.max_tiles));
+  const int items = ntiles * nft;
+  const int lin = blockIdx.x;
+  const int per_xcd = (items + kXcds - 1) / kXcds;
+  const int k_on_xcd = lin / kXcds;
+  const int item = (lin % kXcds) * per_xcd + k_on_xcd;
+  if (k_on_xcd >= per_xcd || item >= items) return;
+  const int tile_id = item / nft, ftile = item % nft;
+  const int4 tile = a.tiles[tile_id];
+  // an empty tile, or one with a negative expert or position, has no work
+  // (glm_moe_tiles writes none; the check keeps a caller's list in bounds)
+  if (tile.z <= 0 || tile.x < 0 || tile.y < 0) return;
+  // (a longer tile than kSplitTileM rows from elsewhere is cut there)
+  const int rows = min(tile.z, kSplitTileM);
+  // the tile's 16-row token blocks split between the two token waves (wave
+  // row 0 takes the odd one); blocks past the tile's rows are not computed
+  const int nblk = (rows + 15) >> 4;
+  const int half = 16 * ((nblk + 1) >> 1);
+  const int wt = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) >> 2;
+  const int tok0 = wt ? half : 0;
+  const int nb = wt ? nblk - (half >> 4) : (half >> 4);
+  switch (nb) {
+    case 5: w8_body<NPROJ, AF, 5>(a, tile.x, tile.y, rows, ftile, tok0); break;
+    case 4: w8_body<NPROJ, AF, 4>(a, tile.x, tile.y, rows, ftile, tok0); break;
+    case 3: w8_body<NPROJ, AF, 3>(a, tile.x, tile.y, rows, ftile, tok0); break;
+    case 2: w8_body<NPROJ, AF, 2>(a, tile.x, tile.y, rows, ftile, tok0); break;
+    case 1: w8_body<NPROJ, AF, 1>(a, tile.x, tile.y, rows, ftile, tok0); break;
+    default: w8_body<NPROJ, AF, 0>(a, tile.x, tile.y, rows, ftile, tok0); break;
+  }
+}
+
 }  // namespace glm
 
 using namespace glm;
@@ -1046,11 +1467,20 @@ int glm_act_split_launch(hipStream_t stream, const uint16_t *x, long long rows, 
   return act_split_launch_as(stream, x, rows, K, ACT_FP8X2, split);
 }
 
+// The eight-wave form runs the gate/up GEMMs (T = 4096: 186.8 against 198.4 us
+// and 197 against 210 us, interleaved, on two boxes); the down GEMMs stay on
+// sixteen waves, which the eight-wave form did not beat (122 against 121 us).
+constexpr int kSplitWavesGateUp = 8, kSplitWavesDown = 16;
+
 template <int NPROJ, int AF>
 static void launch_f8f6f4(hipStream_t stream, dim3 grid, const SplitArgs &a) {
-  const size_t lds = kSplitStages * (size_t)SplitStage<AF>::kBytes;
-  hipLaunchKernelGGL((grouped_f8f6f4_kernel<NPROJ, AF>), grid, dim3(kSplitThreads), lds, stream,
-                     a);
+  constexpr int waves = NPROJ == 2 ? kSplitWavesGateUp : kSplitWavesDown;
+  if constexpr (waves == 8)
+    hipLaunchKernelGGL((grouped_f8f6f4_w8_kernel<NPROJ, AF>), grid, dim3(kW8Threads),
+                       (size_t)W8Layout<AF>::kBytes, stream, a);
+  else
+    hipLaunchKernelGGL((grouped_f8f6f4_kernel<NPROJ, AF>), grid, dim3(kSplitThreads),
+                       kSplitStages * (size_t)SplitStage<AF>::kBytes, stream, a);
 }
 
 static int split_launch(hipStream_t stream, SplitArgs a, int nproj, int max_tiles, int af) {
