@@ -175,179 +175,144 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
 
 // ---------------------------------------------------------------------------
 // Multi-workgroup dispatch for many pairs: the pairs are cut into chunks of
-// 1024 (one workgroup each).  (1) every chunk counts its experts (done by the
-// scan's own workgroup when the chunk histograms fit its LDS); (2) one
-// workgroup turns the chunk counts into expert offsets and per-chunk bases
-// (bases[c][e] = offsets[e] + pairs of expert e in chunks < c), plus the work
-// list and row tiles; (3) every chunk ranks its pairs stably within the chunk
-// (bitmap popcount, as above) and scatters them to bases[c][e] + rank.  The
-// result is identical to the single-workgroup dispatch.
+// 1024 (one workgroup each), in two kernels that run on every chunk at once.
+// (1) dispatch_rank_kernel: every chunk ranks its pairs stably within the
+// chunk -- lanes of a wave with the same expert are found with one ballot per
+// bit of the expert id, a pair's rank is the number of such lanes below it
+// plus the same expert's pairs in the chunk's earlier waves (per-wave counts
+// in LDS) -- and writes its expert counts.  (2) dispatch_place_kernel: every
+// chunk sums the chunk counts itself (expert totals and the counts of the
+// chunks before it), scans the totals into expert offsets and places its
+// pairs at offset + earlier chunks + rank; chunk 0 also writes the offsets,
+// counts, work list and row tiles.  The result is identical to the
+// single-workgroup dispatch.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(
-    const uint32_t *__restrict__ idx, int P, int E, int32_t *__restrict__ chunk_counts) {
-  extern __shared__ uint32_t cnt[];  // [E]
+constexpr int kDispatchWaves = kDispatchThreads / 64;
+
+// LDS: per-wave expert counts [kDispatchWaves][E] (E <= 448).
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_rank_kernel(
+    const uint32_t *__restrict__ idx, int P, int E, int32_t *__restrict__ chunk_counts,
+    int32_t *__restrict__ local_rank) {
+  extern __shared__ int32_t wcnt[];  // [kDispatchWaves][E]
   __shared__ int s_bad;
-  const int tid = threadIdx.x;
-  for (int e = tid; e < E; e += kDispatchThreads) cnt[e] = 0;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < kDispatchWaves * E; i += kDispatchThreads) wcnt[i] = 0;
   if (tid == 0) s_bad = 0;
-  __syncthreads();
   const int p = blockIdx.x * kDispatchThreads + tid;
+  const uint32_t e = p < P ? idx[p] : (uint32_t)E;
+  // key E stands for "no pair" (past the end, or an index >= E, which is dropped)
+  const uint32_t key = e < (uint32_t)E ? e : (uint32_t)E;
+  __syncthreads();
+  if (p < P && e >= (uint32_t)E) s_bad = 1;
+  // the lanes holding this lane's key: one ballot per bit of the key
+  const int nbits = 32 - __clz(E);
+  uint64_t same = ~0ull;
+  for (int bit = 0; bit < nbits; ++bit) {
+    const uint64_t m = __ballot((key >> bit) & 1u);
+    same &= ((key >> bit) & 1u) ? m : ~m;
+  }
+  const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
+  if (key < (uint32_t)E && below == 0) wcnt[wave * E + key] = __popcll(same);
+  __syncthreads();
+  // per expert: exclusive prefix over the waves; the chunk's count
+  for (int x = tid; x < E; x += kDispatchThreads) {
+    int run = 0;
+#pragma unroll
+    for (int w = 0; w < kDispatchWaves; ++w) {
+      const int c = wcnt[w * E + x];
+      wcnt[w * E + x] = run;
+      run += c;
+    }
+    chunk_counts[(size_t)blockIdx.x * (E + 1) + x] = run;
+  }
+  __syncthreads();
+  if (tid == 0) chunk_counts[(size_t)blockIdx.x * (E + 1) + E] = s_bad;
+  if (p < P) local_rank[p] = key < (uint32_t)E ? wcnt[wave * E + key] + below : -1;
+}
+
+// rank_inv: in, the chunk-local ranks of dispatch_rank_kernel; out, inv.
+// pair_token may be null (then the caller fills it from perm).
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_place_kernel(
+    const uint32_t *__restrict__ idx, int P, int k, int E,
+    const int32_t *__restrict__ chunk_counts, int nchunks, int32_t *__restrict__ rank_inv,
+    int32_t *__restrict__ perm, int32_t *__restrict__ pair_token, int32_t *__restrict__ counts,
+    int32_t *__restrict__ offsets, int32_t *__restrict__ active, int32_t *__restrict__ num_active,
+    int4 *__restrict__ work, int32_t *__restrict__ status, int tile_rows,
+    int4 *__restrict__ tiles, int32_t *__restrict__ num_tiles) {
+  __shared__ int32_t base[448];
+  __shared__ int s_scan[kDispatchThreads / 64 + 1];
+  const int tid = threadIdx.x;
+  const int chunk = blockIdx.x;
+  // expert tid: its total over all chunks and its pairs in the chunks before
+  // this one (16 chunks' loads issued together)
+  int total = 0, before = 0;
+  if (tid < E) {
+    for (int c0 = 0; c0 < nchunks; c0 += 16) {
+      int n[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        n[j] = c0 + j < nchunks ? chunk_counts[(size_t)(c0 + j) * (E + 1) + tid] : 0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        total += n[j];
+        before += c0 + j < chunk ? n[j] : 0;
+      }
+    }
+  }
+  int all = 0;
+  const int off = block_exclusive_scan(tid < E ? total : 0, s_scan, &all);
+  if (tid < E) base[tid] = off + before;
+  __syncthreads();
+  const int p = chunk * kDispatchThreads + tid;
   if (p < P) {
     const uint32_t e = idx[p];
-    if (e < (uint32_t)E) atomicAdd(&cnt[e], 1u);
-    else s_bad = 1;
-  }
-  __syncthreads();
-  int32_t *row = chunk_counts + (size_t)blockIdx.x * (E + 1);
-  for (int e = tid; e < E; e += kDispatchThreads) row[e] = (int)cnt[e];
-  if (tid == 0) row[E] = s_bad;
-}
-
-// FUSED: the same workgroup first counts the chunks itself, into LDS
-// histograms [nchunks][E] (dynamic LDS), reading the indices once; the chunk
-// bases then go to chunk_counts for the scatter as in the three-kernel form.
-template <bool FUSED>
-__global__ __launch_bounds__(kDispatchThreads) void dispatch_scan_kernel(
-    const uint32_t *__restrict__ idx, int P, int32_t *__restrict__ chunk_counts, int nchunks,
-    int E, int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
-    int32_t *__restrict__ active, int32_t *__restrict__ num_active, int4 *__restrict__ work,
-    int32_t *__restrict__ status, int tile_rows, int4 *__restrict__ tiles,
-    int32_t *__restrict__ num_tiles) {
-  extern __shared__ int32_t hist[];  // FUSED: [nchunks][E]
-  __shared__ int s_scan[kDispatchThreads / 64 + 1];
-  __shared__ int s_bad;
-  const int tid = threadIdx.x;
-  int bad = 0;
-  if constexpr (FUSED) {
-    for (int i = tid; i < nchunks * E; i += kDispatchThreads) hist[i] = 0;
-    if (tid == 0) s_bad = 0;
-    __syncthreads();
-    // thread t takes pair t of every chunk, 16 chunks' loads at a time
-    for (int c0 = 0; c0 < nchunks; c0 += 16) {
-      uint32_t ev[16];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const long long p = (long long)(c0 + j) * kDispatchThreads + tid;
-        ev[j] = c0 + j < nchunks && p < P ? idx[p] : 0xffffffffu;
-      }
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const long long p = (long long)(c0 + j) * kDispatchThreads + tid;
-        if (c0 + j < nchunks && p < P) {
-          if (ev[j] < (uint32_t)E) atomicAdd(&hist[(c0 + j) * E + ev[j]], 1);
-          else s_bad = 1;
-        }
-      }
-    }
-    __syncthreads();
-    bad = s_bad;
-  } else {
-    // bad flags OR-ed by thread 0
-    if (tid == 0)
-      for (int c = 0; c < nchunks; ++c) bad |= chunk_counts[(size_t)c * (E + 1) + E];
-  }
-  // per expert: running sum over chunks (the count of chunk c becomes the
-  // exclusive base of chunk c within the expert)
-  int carry = 0, carry_active = 0, carry_tiles = 0;
-  for (int e0 = 0; e0 < E; e0 += kDispatchThreads) {
-    const int e = e0 + tid;
-    int c_e = 0;
-    if (e < E) {
-      // 16 chunks at a time: their loads are issued together before any store
-      for (int c0 = 0; c0 < nchunks; c0 += 16) {
-        int n[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          n[j] = c0 + j >= nchunks ? 0
-                 : FUSED           ? hist[(c0 + j) * E + e]
-                                   : chunk_counts[(size_t)(c0 + j) * (E + 1) + e];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          if (c0 + j < nchunks) {
-            if (FUSED)
-              hist[(c0 + j) * E + e] = c_e;
-            else
-              chunk_counts[(size_t)(c0 + j) * (E + 1) + e] = c_e;
-          }
-          c_e += n[j];
-        }
-      }
-    }
-    int tot = 0;
-    const int ex = block_exclusive_scan(c_e, s_scan, &tot);
-    int tot_a = 0;
-    const int ex_a = block_exclusive_scan(c_e > 0 ? 1 : 0, s_scan, &tot_a);
-    const int nt = tiles != nullptr ? row_tiles(c_e, tile_rows) : 0;
-    int tot_t = 0;
-    const int ex_t = block_exclusive_scan(nt, s_scan, &tot_t);
-    if (e < E) {
-      const int off = carry + ex;
-      offsets[e] = off;
-      counts[e] = c_e;
-      for (int c0 = 0; c0 < nchunks; c0 += 16) {
-        int v[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          v[j] = c0 + j >= nchunks ? 0
-                 : FUSED           ? hist[(c0 + j) * E + e]
-                                   : chunk_counts[(size_t)(c0 + j) * (E + 1) + e];
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          if (c0 + j < nchunks) chunk_counts[(size_t)(c0 + j) * (E + 1) + e] = v[j] + off;
-      }
-      if (c_e > 0) {
-        active[carry_active + ex_a] = e;
-        work[carry_active + ex_a] = make_int4(e, off, c_e, 0);
-      }
-      for (int i = 0; i < nt; ++i) {
-        const int2 t = row_tile(c_e, nt, i);
-        tiles[carry_tiles + ex_t + i] = make_int4(e, off + t.x, t.y, 0);
-      }
-    }
-    carry += tot;
-    carry_active += tot_a;
-    carry_tiles += tot_t;
-  }
-  if (tid == 0) {
-    offsets[E] = carry;
-    num_active[0] = carry_active;
-    status[0] = bad;
-    if (num_tiles != nullptr) num_tiles[0] = carry_tiles;
-  }
-  for (int e = carry_active + tid; e < E; e += kDispatchThreads) {
-    active[e] = -1;
-    work[e] = make_int4(-1, 0, 0, 0);
-  }
-}
-
-__global__ __launch_bounds__(kDispatchThreads) void dispatch_scatter_kernel(
-    const uint32_t *__restrict__ idx, int P, int k, int E,
-    const int32_t *__restrict__ chunk_bases, int32_t *__restrict__ perm,
-    int32_t *__restrict__ inv, int32_t *__restrict__ pair_token) {
-  extern __shared__ uint32_t bits[];  // [E][32]
-  const int tid = threadIdx.x;
-  for (int w = tid; w < E * 32; w += kDispatchThreads) bits[w] = 0;
-  __syncthreads();
-  const int p = blockIdx.x * kDispatchThreads + tid;
-  uint32_t e = 0xffffffffu;
-  if (p < P) {
-    e = idx[p];
-    if (e < (uint32_t)E) atomicOr(&bits[e * 32 + (tid >> 5)], 1u << (tid & 31));
-  }
-  __syncthreads();
-  if (p < P) {
-    if (e < (uint32_t)E) {
-      const uint32_t *row = bits + e * 32;
-      int r = chunk_bases[(size_t)blockIdx.x * (E + 1) + e];
-      const int word = tid >> 5;
-      for (int w = 0; w < word; ++w) r += __popc(row[w]);
-      r += __popc(row[word] & ((1u << (tid & 31)) - 1u));
-      perm[r] = p;
-      inv[p] = r;
-      if (pair_token != nullptr) pair_token[r] = p / k;
+    const int r = rank_inv[p];
+    if (e < (uint32_t)E && r >= 0) {
+      const int pos = base[e] + r;
+      perm[pos] = p;
+      rank_inv[p] = pos;
+      if (pair_token != nullptr) pair_token[pos] = p / k;
     } else {
-      inv[p] = -1;
+      rank_inv[p] = -1;
     }
+  }
+  if (chunk != 0) return;
+  // chunk 0: offsets, counts, the work list of active experts, row tiles
+  int tot_a = 0;
+  const int ex_a = block_exclusive_scan(tid < E && total > 0 ? 1 : 0, s_scan, &tot_a);
+  const int nt = tiles != nullptr && tid < E ? row_tiles(total, tile_rows) : 0;
+  int tot_t = 0;
+  const int ex_t = block_exclusive_scan(nt, s_scan, &tot_t);
+  if (tid < E) {
+    offsets[tid] = off;
+    counts[tid] = total;
+    if (total > 0) {
+      active[ex_a] = tid;
+      work[ex_a] = make_int4(tid, off, total, 0);
+    }
+    for (int i = 0; i < nt; ++i) {
+      const int2 t = row_tile(total, nt, i);
+      tiles[ex_t + i] = make_int4(tid, off + t.x, t.y, 0);
+    }
+  }
+  for (int x = tot_a + tid; x < E; x += kDispatchThreads) {
+    active[x] = -1;
+    work[x] = make_int4(-1, 0, 0, 0);
+  }
+  // positions past the valid pairs (dropped indices >= E) hold -1
+  for (int pos = all + tid; pos < P; pos += kDispatchThreads) {
+    perm[pos] = -1;
+    if (pair_token != nullptr) pair_token[pos] = -1;
+  }
+  int bad = 0;
+  for (int c = tid; c < nchunks; c += kDispatchThreads) bad |= chunk_counts[(size_t)c * (E + 1) + E];
+  bad = __syncthreads_or(bad);
+  if (tid == 0) {
+    offsets[E] = all;
+    num_active[0] = tot_a;
+    status[0] = bad ? 1 : 0;
+    if (num_tiles != nullptr) num_tiles[0] = tot_t;
   }
 }
 
@@ -441,27 +406,16 @@ int glm_dispatch_launch(hipStream_t stream, const uint32_t *indices, int T, int 
                   "dispatch: %d chunks x %d experts do not fit in pair_token", nchunks, E + 1);
       chunk_scratch = pair_token;
     }
-    // the chunk histograms of one workgroup fit its LDS up to 64 KB (T*k
-    // pairs x E experts: 131,072 x 128): count and scan in one kernel
-    const size_t hist_bytes = (size_t)nchunks * E * 4;
-    if (hist_bytes <= 64 * 1024) {
-      hipLaunchKernelGGL(glm::dispatch_scan_kernel<true>, dim3(1), dim3(glm::kDispatchThreads),
-                         hist_bytes, stream, indices, P, chunk_scratch, nchunks, E, counts,
-                         offsets, active, num_active, work, status, tile_rows, tiles, num_tiles);
-      GLM_LAUNCH_CHECK("dispatch_scan_kernel");
-    } else {
-      hipLaunchKernelGGL(glm::dispatch_count_kernel, dim3(nchunks), dim3(glm::kDispatchThreads),
-                         (size_t)E * 4, stream, indices, P, E, chunk_scratch);
-      GLM_LAUNCH_CHECK("dispatch_count_kernel");
-      hipLaunchKernelGGL(glm::dispatch_scan_kernel<false>, dim3(1), dim3(glm::kDispatchThreads),
-                         0, stream, indices, P, chunk_scratch, nchunks, E, counts, offsets,
-                         active, num_active, work, status, tile_rows, tiles, num_tiles);
-      GLM_LAUNCH_CHECK("dispatch_scan_kernel");
-    }
-    hipLaunchKernelGGL(glm::dispatch_scatter_kernel, dim3(nchunks), dim3(glm::kDispatchThreads),
-                       (size_t)E * 32 * 4, stream, indices, P, k, E, chunk_scratch, perm, inv,
-                       in_place ? nullptr : pair_token);
-    GLM_LAUNCH_CHECK("dispatch_scatter_kernel");
+    // the chunk-local ranks go through inv, which the second kernel overwrites
+    hipLaunchKernelGGL(glm::dispatch_rank_kernel, dim3(nchunks), dim3(glm::kDispatchThreads),
+                       (size_t)glm::kDispatchWaves * E * 4, stream, indices, P, E, chunk_scratch,
+                       inv);
+    GLM_LAUNCH_CHECK("dispatch_rank_kernel");
+    hipLaunchKernelGGL(glm::dispatch_place_kernel, dim3(nchunks), dim3(glm::kDispatchThreads), 0,
+                       stream, indices, P, k, E, chunk_scratch, nchunks, inv, perm,
+                       in_place ? nullptr : pair_token, counts, offsets, active, num_active, work,
+                       status, tile_rows, tiles, num_tiles);
+    GLM_LAUNCH_CHECK("dispatch_place_kernel");
     if (in_place) {
       const int blocks = std::min((P + 255) / 256, 1024);
       hipLaunchKernelGGL(glm::dispatch_tokens_kernel, dim3(blocks), dim3(256), 0, stream, offsets,

@@ -159,13 +159,14 @@ __global__ __launch_bounds__(64 * KSPLIT) void router_gemm_kernel(
 // bf16 MFMA rate (a 32-wide K step is three bf16 MFMAs per tile instead of
 // eight f32 ones).
 // Workgroup = 64 tokens x 32 experts, eight waves, one 16 x 16 output tile
-// each over the whole of K.  K advances in chunks of 64: the chunk's 64 token
+// each over the whole of K.  K advances in chunks of 128: the chunk's 64 token
 // rows and 96 split-weight rows (3 parts x 32 experts) are staged in LDS by
-// direct-to-LDS wave loads of 8 rows x 128 B (whole cache lines), three stages
-// deep; piece p (16 bytes) of staged row R sits at p ^ (R & 7), so the MFMA
-// operand reads (16 rows x one piece column) spread over the banks.  (Loads
-// of 16 rows x 64 B straight into registers, one MFMA operand per lane, ran
-// at ~28 GB/s per CU: 23.2 against 16.6 us at T = 4096, E = 128, d = 2048.)
+// direct-to-LDS wave loads of 4 rows x 256 B (whole cache lines), three stages
+// deep; piece p (16 bytes) of staged row R sits at p ^ (R & 15), so the MFMA
+// operand reads (16 rows x one piece column) spread over the banks.  (Chunks
+// of 64 ran a workgroup barrier per 6 MFMAs of a wave: 16.3 us at T = 4096,
+// E = 128, d = 2048.  Loads of 16 rows x 64 B straight into registers, one
+// MFMA operand per lane, ran at ~28 GB/s per CU: 23.2 us.)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void router_weight_split_kernel(const float *__restrict__ w,
                                                                   long long n,
@@ -183,12 +184,18 @@ __global__ __launch_bounds__(256) void router_weight_split_kernel(const float *_
 }
 
 constexpr int kSplitRouterWaves = 8;
-constexpr int kRouterRows = 64 + 96;          // staged rows per chunk: tokens, then 3 x 32 weights
-constexpr int kRouterStageBytes = kRouterRows * 128;
+constexpr int kRouterChunk = 128;               // K per stage
+constexpr int kRouterRowBytes = kRouterChunk * 2;
+constexpr int kRouterRows = 64 + 96;            // staged rows per chunk: tokens, then 3 x 32 weights
+constexpr int kRouterStageBytes = kRouterRows * kRouterRowBytes;
 constexpr int kRouterStages = 3;
-constexpr int kRouterWaveLoads = kRouterRows / 8;  // 20 wave loads of 1 KB per chunk
-static_assert(kRouterWaveLoads <= 3 * kSplitRouterWaves, "three loads per wave and chunk");
+constexpr int kRouterRowsPerLoad = 1024 / kRouterRowBytes;            // 4
+constexpr int kRouterWaveLoads = kRouterRows / kRouterRowsPerLoad;    // 40 wave loads of 1 KB
+constexpr int kRouterLoads = kRouterWaveLoads / kSplitRouterWaves;    // 5 per wave
+static_assert(kRouterLoads * kSplitRouterWaves == kRouterWaveLoads, "loads split evenly");
+static_assert(64 % kRouterRowsPerLoad == 0, "a load stages token rows or weight rows");
 static_assert(kRouterStages == 3, "the ring's wait counts");
+static_assert(kRouterStages * kRouterStageBytes <= 160 * 1024, "LDS ring exceeds 160 KB");
 
 __global__ __launch_bounds__(64 * kSplitRouterWaves) void router_gemm_bf16x3_kernel(
     const uint16_t *__restrict__ x, const uint16_t *__restrict__ ws, int T, int d, int E,
@@ -199,19 +206,16 @@ __global__ __launch_bounds__(64 * kSplitRouterWaves) void router_gemm_bf16x3_ker
   const int r = lane & 15, q = lane >> 4;
   const int t0 = blockIdx.x * 64;
   const int e0 = blockIdx.y * 32;
-  const int nchunks = d / 64;
-  // load j of wave w stages rows 8 g .. 8 g + 7, g = 8 j + w (j = 2: waves
-  // 4-7 repeat the loads of waves 0-3, so every wave issues three per chunk);
-  // lane l fetches piece (l & 7) ^ (row & 7) of row 8 g + (l >> 3)
+  const int nchunks = d / kRouterChunk;
+  // load j of wave w stages rows 4 g .. 4 g + 3, g = 8 j + w; lane l fetches
+  // piece (l & 15) ^ (row & 15) of row 4 g + (l >> 4)
   const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)((size_t)T * d * 2));
   const __amdgpu_buffer_rsrc_t wrs = make_rsrc(ws, (uint32_t)((size_t)3 * E * d * 2));
-  int gl[3];
-  uint32_t voff[3];
+  uint32_t voff[kRouterLoads];
 #pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    const int g = j < 2 ? 8 * j + wave : 16 + (wave & 3);
-    gl[j] = g;
-    const int row = 8 * g + (lane >> 3), piece = (lane & 7) ^ (row & 7);
+  for (int j = 0; j < kRouterLoads; ++j) {
+    const int g = kSplitRouterWaves * j + wave;
+    const int row = kRouterRowsPerLoad * g + (lane >> 4), piece = (lane & 15) ^ (row & 15);
     size_t src_row;
     if (row < 64) {
       src_row = (size_t)min(t0 + row, T - 1);
@@ -224,8 +228,11 @@ __global__ __launch_bounds__(64 * kSplitRouterWaves) void router_gemm_bf16x3_ker
   auto issue = [&](int c, int stage) {
     uint8_t *base = smem + stage * kRouterStageBytes;
 #pragma unroll
-    for (int j = 0; j < 3; ++j)
-      buf16_to_lds(j == 0 ? xrs : wrs, base + gl[j] * 1024, voff[j], c * 128);
+    for (int j = 0; j < kRouterLoads; ++j) {
+      const int g = kSplitRouterWaves * j + wave;  // token rows: g < 16
+      buf16_to_lds(g < 64 / kRouterRowsPerLoad ? xrs : wrs, base + g * 1024, voff[j],
+                   c * kRouterRowBytes);
+    }
   };
   // this wave's output tile: tokens 16 tt .. + 15, experts 16 et .. + 15
   const int tt = wave >> 1, et = wave & 1;
@@ -233,32 +240,30 @@ __global__ __launch_bounds__(64 * kSplitRouterWaves) void router_gemm_bf16x3_ker
   auto compute = [&](int stage) {
     const uint8_t *base = smem + stage * kRouterStageBytes;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kRouterChunk / 32; ++i) {
       const int xr = 16 * tt + r;
-      const glm_bf16x8 xa =
-          *reinterpret_cast<const glm_bf16x8 *>(base + xr * 128 + 16 * ((4 * i + q) ^ (xr & 7)));
+      const glm_bf16x8 xa = *reinterpret_cast<const glm_bf16x8 *>(
+          base + xr * kRouterRowBytes + 16 * ((4 * i + q) ^ (xr & 15)));
       glm_bf16x8 wb[3];
 #pragma unroll
       for (int p = 0; p < 3; ++p) {
         const int wr = 64 + 32 * p + 16 * et + r;
-        wb[p] = *reinterpret_cast<const glm_bf16x8 *>(base + wr * 128 +
-                                                      16 * ((4 * i + q) ^ (wr & 7)));
+        wb[p] = *reinterpret_cast<const glm_bf16x8 *>(base + wr * kRouterRowBytes +
+                                                      16 * ((4 * i + q) ^ (wr & 15)));
       }
 #pragma unroll
       for (int p = 0; p < 3; ++p)
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, wb[p], acc, 0, 0, 0);
     }
   };
-  // ring: chunks c + 1 and c + 2 in flight while c is consumed (a deeper ring
-  // measured the same: the kernel is bound by the L2-to-LDS traffic of its
-  // tiles and the LDS operand reads, not by round trips); the barrier of
-  // iteration c also guarantees that every wave is done with chunk c - 1,
+  // ring: chunks c + 1 and c + 2 in flight while c is consumed; the barrier
+  // of iteration c also guarantees that every wave is done with chunk c - 1,
   // whose stage the loads of chunk c + 2 overwrite
   issue(0, 0);
   if (nchunks > 1) issue(1, 1);
   for (int c = 0; c < nchunks; ++c) {
     if (c + 1 < nchunks)
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(3));
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRouterLoads));
     else
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     ring_barrier();
