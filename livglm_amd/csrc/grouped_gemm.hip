@@ -17,7 +17,9 @@
 // projection; down: 256 features) in a 4 x 2 arrangement of eight waves: wave
 // (wf, wt) owns 64 weight rows x 64 tokens, i.e. 4 x 4 accumulator tiles of
 // v_mfma_f32_16x16x32_bf16 (two waves per SIMD, so one wave's LDS reads
-// overlap the other's MFMAs).  K advances in chunks of 64: the activation rows
+// overlap the other's MFMAs).  Gate/up grids that would stay below one
+// workgroup per CU take 192-row tiles instead (2 x 4 waves of 96 rows x 32
+// tokens).  K advances in chunks of 64: the activation rows
 // and the weight rows of a chunk are staged in LDS, three stages deep, and the
 // next chunks' global loads are issued before the current chunk's MFMAs.
 // MFMA i, slot s of lane (r, q) is K = 32i + 8q + s.
@@ -38,6 +40,7 @@ constexpr int kTileW = 256;    // weight rows per workgroup
 constexpr int kThreads = 512;  // 8 waves: 4 along the weight rows x 2 along the tokens
 constexpr int kWaves = kThreads / 64;
 constexpr int kXcds = 8;
+constexpr int kNumCUs = 256;  // MI355X
 constexpr int kStages = 3;     // LDS ring: two chunks in flight while one is consumed
 
 // One K chunk of a workgroup's operands in LDS, unpadded and XOR-swizzled in
@@ -49,12 +52,13 @@ constexpr int kStages = 3;     // LDS ring: two chunks in flight while one is co
 // Direct global->LDS loads write one wave's 64 x 16 bytes contiguously, so a
 // lane's LDS slot is fixed by its lane id; each lane fetches the global piece
 // that belongs in its slot.
+template <int TW>
 struct Bf16Layout {
   static constexpr int kChunk = 64;  // K per stage
   static constexpr int kXRowBytes = kChunk * 2;
   static constexpr int kWRowBytes = kChunk * 2;
   static constexpr int kXBytes = kTileM * kXRowBytes;
-  static constexpr int kWBytes = kTileW * kWRowBytes;
+  static constexpr int kWBytes = TW * kWRowBytes;
   static constexpr int kStageBytes = kXBytes + kWBytes;
   static constexpr int kXPerRow = kXRowBytes / 16;  // pieces per row
   static constexpr int kWPerRow = kWRowBytes / 16;
@@ -86,9 +90,25 @@ __device__ __forceinline__ void load16_to_lds(const void *src, void *lds) {
   __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
 }
 
-template <int NPROJ>
+// Wave arrangement of a TW-row weight tile: WF waves along the weight rows x
+// WT along the tokens, each wave BR x BT MFMA blocks of 16 x 16.  TW = 256:
+// 4 x 2 waves of 64 rows x 64 tokens; TW = 192 (gate/up: 96 features of each
+// projection, for grids that 256-row tiles leave below one workgroup per CU):
+// 2 x 4 waves of 96 rows x 32 tokens.
+template <int TW>
+struct Bf16Waves {
+  static constexpr int WF = TW == 256 ? 4 : 2;
+  static constexpr int WT = kWaves / WF;
+  static constexpr int BR = TW / (16 * WF);
+  static constexpr int BT = kTileM / (16 * WT);
+  static_assert(WF * BR * 16 == TW && WT * BT * 16 == kTileM, "wave tiles cover the tile");
+};
+
+template <int NPROJ, int TW>
 __global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs a) {
-  using L = Bf16Layout;
+  using L = Bf16Layout<TW>;
+  using WV = Bf16Waves<TW>;
+  static_assert(NPROJ == 2 || TW == 256, "192-row tiles pair gate and up");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int nft = a.feature_tiles;
   const int ntiles = (a.dense_rows + kTileM - 1) / kTileM;
@@ -102,12 +122,12 @@ __global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int wf = wave & 3, wt = wave >> 2;
+  const int wf = wave % WV::WF, wt = wave / WV::WF;
   const int pos0 = tile_id * kTileM, rows = min(kTileM, a.dense_rows - pos0);
   const int K = a.K;
   const int nchunks = K / L::kChunk;
-  // weight rows of this workgroup: NPROJ == 2 -> [gate f0..f0+127 | up f0..f0+127]
-  const int f0 = ftile * (kTileW / NPROJ);
+  // weight rows of this workgroup: NPROJ == 2 -> [gate f0..f0+TW/2 | up f0..f0+TW/2]
+  const int f0 = ftile * (TW / NPROJ);
   const int wrow_bytes = K * 2;
 
   // ---- load assignment (fixed over the K loop).  Load j of wave w fills the
@@ -130,8 +150,8 @@ __global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs
     const int row = slot / L::kWPerRow, piece = (slot % L::kWPerRow) ^ L::wswz(row);
     // (a select, not a.w[p]: a lane-varying index into the kernel arguments
     // becomes a vector memory load)
-    const uint8_t *wbase = NPROJ == 2 && row >= kTileW / 2 ? a.w[1] : a.w[0];
-    const int frow = f0 + (NPROJ == 2 ? row % (kTileW / 2) : row);
+    const uint8_t *wbase = NPROJ == 2 && row >= TW / 2 ? a.w[1] : a.w[0];
+    const int frow = f0 + (NPROJ == 2 ? row % (TW / 2) : row);
     wsrc[j] = wbase + (size_t)frow * wrow_bytes + piece * 16;
   }
 
@@ -146,16 +166,17 @@ __global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs
       load16_to_lds(wsrc[j] + c * L::kWRowBytes, base + L::kXBytes + (j * kWaves + wave) * 1024);
   };
 
-  glm_f32x4 acc[4][4];
+  constexpr int BR = WV::BR, BT = WV::BT, HB = BR / 2;
+  glm_f32x4 acc[BR][BT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < BR; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = glm_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < BT; ++j) acc[i][j] = glm_f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // this wave's 4 weight-row tiles within the 256 staged rows (gate/up: two
+  // this wave's BR weight-row tiles within the TW staged rows (gate/up: HB
   // gate tiles, then the up tiles of the same features)
   auto wrow_of = [&](int rt) {
-    return NPROJ == 2 ? (rt / 2) * (kTileW / 2) + wf * 32 + (rt % 2) * 16 : wf * 64 + rt * 16;
+    return NPROJ == 2 ? (rt / HB) * (TW / 2) + wf * HB * 16 + (rt % HB) * 16 : wf * BR * 16 + rt * 16;
   };
   // MFMAs of one staged chunk: MFMA i, slot s of lane (r, q) is K = 32i + 8q + s.
   auto compute = [&](int stage) {
@@ -165,23 +186,23 @@ __global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs
     {
 #pragma unroll
       for (int i = 0; i < L::kChunk / 32; ++i) {
-        glm_bf16x8 xb[4], af[4];
+        glm_bf16x8 xb[BT], af[BR];
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-          const int xr = wt * 64 + ct * 16 + r;
+        for (int ct = 0; ct < BT; ++ct) {
+          const int xr = wt * BT * 16 + ct * 16 + r;
           xb[ct] = *reinterpret_cast<const glm_bf16x8 *>(sx + xr * L::kXRowBytes +
                                                          16 * ((4 * i + q) ^ L::xswz(xr)));
         }
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
+        for (int rt = 0; rt < BR; ++rt) {
           const int wr = wrow_of(rt) + r;
           af[rt] = *reinterpret_cast<const glm_bf16x8 *>(sw + wr * L::kWRowBytes +
                                                          16 * ((4 * i + q) ^ L::wswz(wr)));
         }
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt)
+        for (int rt = 0; rt < BR; ++rt)
 #pragma unroll
-          for (int ct = 0; ct < 4; ++ct)
+          for (int ct = 0; ct < BT; ++ct)
             acc[rt][ct] =
                 __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[rt], xb[ct], acc[rt][ct], 0, 0, 0);
       }
@@ -210,17 +231,17 @@ __global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs
     // reciprocal sigmoid, one packed convert per bf16 rounding of a pair)
     const float lim = a.limit > 0.0f ? a.limit : __builtin_inff();
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      const int row = wt * 64 + ct * 16 + r;
+    for (int ct = 0; ct < BT; ++ct) {
+      const int row = wt * BT * 16 + ct * 16 + r;
       if (row >= rows) continue;
       uint16_t *orow = a.out + (size_t)(pos0 + row) * a.N;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < HB; ++i) {
         float h[4];
 #pragma unroll
         for (int m = 0; m < 4; m += 2) {
           float g0 = acc[i][ct][m], g1 = acc[i][ct][m + 1];
-          float u0 = acc[2 + i][ct][m], u1 = acc[2 + i][ct][m + 1];
+          float u0 = acc[HB + i][ct][m], u1 = acc[HB + i][ct][m + 1];
           bf16_round2(g0, g1);
           bf16_round2(u0, u1);
           limited_swiglu2_fast(g0, g1, u0, u1, lim, h[m], h[m + 1]);
@@ -228,7 +249,7 @@ __global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs
         uint32_t o[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) o[m] = __float_as_uint(h[m]) >> 16;  // bf16-exact
-        store_rows4(orow + f0 + wf * 32 + i * 16 + 4 * q, o);
+        store_rows4(orow + f0 + wf * HB * 16 + i * 16 + 4 * q, o);
       }
     }
   } else {
@@ -1414,16 +1435,24 @@ bool glm_grouped_supported(int d, int I) {
 }
 
 static int grouped_launch(hipStream_t stream, GroupedArgs a, int nproj, int max_tiles) {
-  a.feature_tiles = a.N / (nproj == 2 ? kTileW / 2 : kTileW);
+  // gate/up: 192-row tiles (96 features of each projection) when 256-row
+  // tiles would leave the grid below one workgroup per CU
+  const bool narrow = nproj == 2 && a.N % 96 == 0 &&
+                      (long long)max_tiles * (a.N / (kTileW / 2)) < kNumCUs;
+  a.feature_tiles = nproj == 2 ? a.N / (narrow ? 96 : kTileW / 2) : a.N / kTileW;
   // XCD x handles items [x * per, (x + 1) * per) with per <= ceil(max_items / 8),
   // at linear ids x + 8k: the grid must reach 8 * ceil(max_items / 8)
   const long long max_items = (long long)max_tiles * a.feature_tiles;
   const dim3 grid((unsigned)(((max_items + kXcds - 1) / kXcds) * kXcds));
-  const size_t lds = kStages * (size_t)Bf16Layout::kStageBytes;
-  if (nproj == 2)
-    hipLaunchKernelGGL((grouped_bf16_gemm_kernel<2>), grid, dim3(kThreads), lds, stream, a);
+  if (nproj == 2 && narrow)
+    hipLaunchKernelGGL((grouped_bf16_gemm_kernel<2, 192>), grid, dim3(kThreads),
+                       kStages * (size_t)Bf16Layout<192>::kStageBytes, stream, a);
+  else if (nproj == 2)
+    hipLaunchKernelGGL((grouped_bf16_gemm_kernel<2, 256>), grid, dim3(kThreads),
+                       kStages * (size_t)Bf16Layout<256>::kStageBytes, stream, a);
   else
-    hipLaunchKernelGGL((grouped_bf16_gemm_kernel<1>), grid, dim3(kThreads), lds, stream, a);
+    hipLaunchKernelGGL((grouped_bf16_gemm_kernel<1, 256>), grid, dim3(kThreads),
+                       kStages * (size_t)Bf16Layout<256>::kStageBytes, stream, a);
   GLM_LAUNCH_CHECK("grouped_bf16_gemm_kernel");
   return GLM_OK;
 }
