@@ -328,7 +328,7 @@ class Setup:
         """The dominant kernel's instantiation, as rocprofv3 names it."""
         d, E = self.d, self.E
         if self.grouped:
-            return f"grouped_f8f6f4_kernel<2, {self.act_format}>"
+            return f"grouped_f8f6f4_w8_kernel<2, {self.act_format}>"
         if self.few_token:
             epl = 2 if E <= 128 else (4 if E <= 256 else (5 if E <= 320 else 8))
             return f"select_gate_up_kernel<{epl}, {d // 512}, 1, false>"
