@@ -85,6 +85,21 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
 
 __device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// Element i of the router weights w [n] split into three bf16 parts
+// (w = p0 + p1 + p2: p0 = bf16(w), p1 = bf16(w - p0), p2 = bf16(w - p0 - p1)),
+// stored at ws[i], ws[n + i], ws[2 n + i].
+__device__ __forceinline__ void bf16x3_split_one(const float *__restrict__ w, long long n,
+                                                 uint16_t *__restrict__ ws, long long i) {
+  const float v = w[i];
+  const uint32_t b0 = f32_to_bf16(v);
+  const float r1 = v - bf16_to_f32(b0);
+  const uint32_t b1 = f32_to_bf16(r1);
+  const float r2 = r1 - bf16_to_f32(b1);
+  ws[i] = (uint16_t)b0;
+  ws[n + i] = (uint16_t)b1;
+  ws[2 * n + i] = (uint16_t)f32_to_bf16(r2);
+}
+
 // E8M0 byte -> f32 scale 2^(e-127) (byte 255 = NaN).
 __device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
   // branch-free: two selects on the shifted exponent

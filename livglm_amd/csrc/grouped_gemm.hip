@@ -372,10 +372,9 @@ __device__ __forceinline__ float quad_max(float v) {
   v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, true)));
   return fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, true)));
 }
-__global__ __launch_bounds__(256) void act_split_kernel(const uint16_t *x, long long groups,
-                                                        uint8_t *hi, uint8_t *lo, uint8_t *shi,
-                                                        uint8_t *slo) {
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void act_split_one(const uint16_t *x, long long groups, long long i,
+                                              uint8_t *hi, uint8_t *lo, uint8_t *shi,
+                                              uint8_t *slo) {
   const long long g = i >> 2;
   const int part = (int)(i & 3);  // elements 8 part .. 8 part + 7 of the group
   if (g >= groups) return;        // whole lane quads leave together
@@ -427,6 +426,29 @@ __global__ __launch_bounds__(256) void act_split_kernel(const uint16_t *x, long 
     shi[g] = (uint8_t)bh;
     slo[g] = (uint8_t)bl;
   }
+}
+
+__global__ __launch_bounds__(256) void act_split_kernel(const uint16_t *x, long long groups,
+                                                        uint8_t *hi, uint8_t *lo, uint8_t *shi,
+                                                        uint8_t *slo) {
+  act_split_one(x, groups, (long long)blockIdx.x * blockDim.x + threadIdx.x, hi, lo, shi, slo);
+}
+
+// The prefill layer's two splits in one launch: blocks [0, wblocks) split the
+// router weights into three bf16 parts (as router_weight_split_kernel), the
+// rest form x's FP8 hi/lo split (as act_split_kernel).
+__global__ __launch_bounds__(256) void prefill_split_kernel(const float *rw, long long nw,
+                                                            uint16_t *ws, int wblocks,
+                                                            const uint16_t *x, long long groups,
+                                                            uint8_t *hi, uint8_t *lo,
+                                                            uint8_t *shi, uint8_t *slo) {
+  if ((int)blockIdx.x < wblocks) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < nw) bf16x3_split_one(rw, nw, ws, i);
+    return;
+  }
+  act_split_one(x, groups, (long long)(blockIdx.x - wblocks) * blockDim.x + threadIdx.x, hi, lo,
+                shi, slo);
 }
 
 // E2M3 / E2M1 code of v 2^(127 - b), round to nearest even, saturating at the
@@ -1488,6 +1510,22 @@ static int act_split_launch_as(hipStream_t stream, const uint16_t *x, long long 
     hipLaunchKernelGGL(act_split_lowp_kernel<ACT_FP4>, grid, dim3(256), 0, stream, x, groups, K,
                        base, base, base + L.shi, base + L.shi);
   GLM_LAUNCH_CHECK("act_split_kernel");
+  return GLM_OK;
+}
+
+// Router weights [E][d] f32 -> their three bf16 parts (wsplit), and x [T][d]
+// -> its FP8 hi/lo split, in one launch.
+int glm_prefill_split_launch(hipStream_t stream, const float *router_weight, int E, int d,
+                             uint16_t *wsplit, const uint16_t *x, int T, void *x_split) {
+  const long long nw = (long long)E * d, groups = (long long)T * (d / 32);
+  const SplitLayout L(T, d, ACT_FP8X2);
+  uint8_t *base = static_cast<uint8_t *>(x_split);
+  const int wblocks = (int)((nw + 255) / 256);
+  const long long xblocks = (4 * groups + 255) / 256;
+  hipLaunchKernelGGL(prefill_split_kernel, dim3((unsigned)(wblocks + xblocks)), dim3(256), 0,
+                     stream, router_weight, nw, wsplit, wblocks, x, groups, base, base + L.lo,
+                     base + L.shi, base + L.slo);
+  GLM_LAUNCH_CHECK("prefill_split_kernel");
   return GLM_OK;
 }
 

@@ -37,8 +37,10 @@ int glm_router_validate(const void *x, int T, int d, const void *weight, const v
 int glm_router_launch(hipStream_t stream, const uint16_t *x, int T, int d, const float *weight,
                       const float *bias, int E, int k, int n_group, int topk_group, int norm,
                       float scale, float *logits, float *weights, uint32_t *indices,
-                      uint16_t *wsplit);
+                      uint16_t *wsplit, bool wsplit_ready);
 bool glm_router_split_supported(int T, int d);
+int glm_prefill_split_launch(hipStream_t stream, const float *router_weight, int E, int d,
+                             uint16_t *wsplit, const uint16_t *x, int T, void *x_split);
 size_t glm_router_split_bytes(int E, int d);
 int glm_dispatch_launch(hipStream_t stream, const uint32_t *indices, int T, int k, int E,
                         int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
@@ -514,10 +516,6 @@ static int moe_forward_core(void *stream_v, const uint16_t *x, int T, int d,
     }
     return glm_combine_launch(stream, w.y, w.inv, wts, shared_ready, T, top_k, d, out);
   }
-  rc = glm_router_launch(stream, x, T, d, router_weight, router_bias, E, top_k, n_group,
-                         topk_group, norm_topk_prob, routed_scaling_factor, w.logits, wts, idx,
-                         w.router_split);
-  if (rc) return rc;
   // general path: dispatch, then the grouped MFMA GEMMs over 128-row tiles
   // for more than 64 tokens when the shape allows, else the tiled GEMV
   // kernels over the work list (a few tokens in a 128-row tile would be
@@ -526,14 +524,27 @@ static int moe_forward_core(void *stream_v, const uint16_t *x, int T, int d,
   // beyond 4 GiB of split the layer stays on the GEMV kernels)
   const bool grouped = glm_grouped_supported(d, I) && T > 64 && glm_split_fits(T, d) &&
                        glm_split_fits((long long)T * top_k, I);
+  // with the bf16 router GEMM, x's FP8 split rides in the router weights'
+  // split launch (one kernel, two block ranges)
+  const bool split_early = grouped && w.router_split != nullptr && glm_router_split_supported(T, d);
+  if (split_early) {
+    rc = glm_prefill_split_launch(stream, router_weight, E, d, w.router_split, x, T, w.x_split);
+    if (rc) return rc;
+  }
+  rc = glm_router_launch(stream, x, T, d, router_weight, router_bias, E, top_k, n_group,
+                         topk_group, norm_topk_prob, routed_scaling_factor, w.logits, wts, idx,
+                         w.router_split, split_early);
+  if (rc) return rc;
   rc = glm_dispatch_launch(stream, idx, T, top_k, E, w.counts, w.offsets, w.perm, w.inv,
                            w.pair_token, w.active, w.num_active, w.work, w.status,
                            grouped ? glm_grouped_tile_rows() : 0, grouped ? w.tiles : nullptr,
                            grouped ? w.num_tiles : nullptr, w.chunk_counts);
   if (rc) return rc;
   if (grouped) {
-    rc = glm_act_split_launch(stream, x, T, d, w.x_split);
-    if (rc) return rc;
+    if (!split_early) {
+      rc = glm_act_split_launch(stream, x, T, d, w.x_split);
+      if (rc) return rc;
+    }
     rc = glm_grouped_gate_up_launch(stream, w.x_split, T, w.pair_token, w.tiles, w.num_tiles,
                                     w.max_tiles, d, I, gate_packed, gate_scales, up_packed,
                                     up_scales, w.h, swiglu_limit, w.h_split, (long long)T * top_k);

@@ -172,15 +172,7 @@ __global__ __launch_bounds__(256) void router_weight_split_kernel(const float *_
                                                                   long long n,
                                                                   uint16_t *__restrict__ ws) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const float v = w[i];
-  const uint32_t b0 = f32_to_bf16(v);
-  const float r1 = v - bf16_to_f32(b0);
-  const uint32_t b1 = f32_to_bf16(r1);
-  const float r2 = r1 - bf16_to_f32(b1);
-  ws[i] = (uint16_t)b0;
-  ws[n + i] = (uint16_t)b1;
-  ws[2 * n + i] = (uint16_t)f32_to_bf16(r2);
+  if (i < n) bf16x3_split_one(w, n, ws, i);
 }
 
 constexpr int kSplitRouterWaves = 8;
@@ -368,14 +360,16 @@ size_t glm_router_split_bytes(int E, int d) { return (size_t)3 * E * d * 2; }
 int glm_router_launch(hipStream_t stream, const uint16_t *x, int T, int d, const float *weight,
                       const float *bias, int E, int k, int n_group, int topk_group, int norm,
                       float scale, float *logits, float *weights, uint32_t *indices,
-                      uint16_t *wsplit) {
+                      uint16_t *wsplit, bool wsplit_ready) {
   using namespace glm;
   if (T == 0) return GLM_OK;
   if (wsplit != nullptr && glm_router_split_supported(T, d)) {
     const long long n = (long long)E * d;
-    hipLaunchKernelGGL(router_weight_split_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                       stream, weight, n, wsplit);
-    GLM_LAUNCH_CHECK("router_weight_split_kernel");
+    if (!wsplit_ready) {
+      hipLaunchKernelGGL(router_weight_split_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256),
+                         0, stream, weight, n, wsplit);
+      GLM_LAUNCH_CHECK("router_weight_split_kernel");
+    }
     const dim3 grid((T + 63) / 64, (E + 31) / 32);
     hipLaunchKernelGGL(router_gemm_bf16x3_kernel, grid, dim3(64 * kSplitRouterWaves),
                        (size_t)kRouterStages * kRouterStageBytes, stream, x,
@@ -430,5 +424,5 @@ extern "C" int glm_router_topk(void *stream, const uint16_t *x, int T, int d, co
               "router: logits buffer is required by this entry point");
   return glm_router_launch((hipStream_t)stream, x, T, d, weight, bias, E, top_k, n_group,
                            topk_group, norm_topk_prob, routed_scaling_factor, logits, weights,
-                           indices, nullptr);
+                           indices, nullptr, false);
 }
