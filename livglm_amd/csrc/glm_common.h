@@ -154,17 +154,18 @@ __device__ __forceinline__ void bf16_round2(float &a, float &b) {
 // limited_swiglu on two elements with bf16 intermediates (expert_ssd.py:
 // 103-107), for the epilogues of the many-token GEMMs: g, u the bf16 gate and
 // up values; lim the bf16 limit, or +inf when there is none (NaN passes
-// through the clamps, as it does through the reference's).  The sigmoid is
+// through the clamps, IEEE minimum / maximum, as it does through the
+// reference's).  The sigmoid is
 // 1 / (1 + 2^(-g log2 e)) on the hardware exp2 and reciprocal: within a few
 // f32 ulp of sigmoid_f32, which the bf16 rounding that follows absorbs except
 // within a few ulp of a bf16 rounding tie.  Each bf16 rounding of the pair
 // is one convert.
 __device__ __forceinline__ void limited_swiglu2_fast(float g0, float g1, float u0, float u1,
                                                      float lim, float &h0, float &h1) {
-  g0 = g0 > lim ? lim : g0;
-  g1 = g1 > lim ? lim : g1;
-  u0 = u0 > lim ? lim : (u0 < -lim ? -lim : u0);
-  u1 = u1 > lim ? lim : (u1 < -lim ? -lim : u1);
+  g0 = __builtin_elementwise_minimum(g0, lim);
+  g1 = __builtin_elementwise_minimum(g1, lim);
+  u0 = __builtin_elementwise_maximum(__builtin_elementwise_minimum(u0, lim), -lim);
+  u1 = __builtin_elementwise_maximum(__builtin_elementwise_minimum(u1, lim), -lim);
   float s0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g0 * -1.44269504088896341f));
   float s1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g1 * -1.44269504088896341f));
   bf16_round2(s0, s1);

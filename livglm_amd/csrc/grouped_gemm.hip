@@ -606,35 +606,39 @@ __device__ __forceinline__ float quad_row_max(float v) {
 
 __device__ __forceinline__ void split_group_part(float v[8], uint32_t ch[2], uint32_t cl[2],
                                                  int *bh_out, int *bl_out) {
+  // The scaled converts divide by (down) and multiply by (up) the f32 scale
+  // operand, of which only the exponent field counts: the E8M0 byte b shifted
+  // into that field stands for 2^(b - 127), also for b = 0.  The same codes
+  // and residuals as ldexp by 127 - b and the unscaled converts (checked on
+  // the device for every byte class, FP8 subnormals and ties).
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
   amax = quad_row_max(amax);
   const int bh = split_scale_byte(amax);
+  const float sh = __uint_as_float((uint32_t)bh << 23);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    int w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i], 127 - bh), ldexpf(v[4 * i + 1], 127 - bh),
-                                            0, false);
-    w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i + 2], 127 - bh),
-                                        ldexpf(v[4 * i + 3], 127 - bh), w, true);
-    ch[i] = (uint32_t)w;
-    v[4 * i] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 0), bh - 127);
-    v[4 * i + 1] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 1), bh - 127);
-    v[4 * i + 2] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 2), bh - 127);
-    v[4 * i + 3] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 3), bh - 127);
+    s16x2 w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(s16x2{0, 0}, v[4 * i], v[4 * i + 1], sh, false);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, v[4 * i + 2], v[4 * i + 3], sh, true);
+    ch[i] = __builtin_bit_cast(uint32_t, w);
+    v[4 * i] -= __builtin_amdgcn_cvt_scalef32_f32_fp8(ch[i], sh, 0);
+    v[4 * i + 1] -= __builtin_amdgcn_cvt_scalef32_f32_fp8(ch[i], sh, 1);
+    v[4 * i + 2] -= __builtin_amdgcn_cvt_scalef32_f32_fp8(ch[i], sh, 2);
+    v[4 * i + 3] -= __builtin_amdgcn_cvt_scalef32_f32_fp8(ch[i], sh, 3);
   }
   float ramax = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) ramax = fmaxf(ramax, fabsf(v[j]));
   ramax = quad_row_max(ramax);
   const int bl = split_scale_byte(ramax);
+  const float sl = __uint_as_float((uint32_t)bl << 23);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    int w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i], 127 - bl), ldexpf(v[4 * i + 1], 127 - bl),
-                                            0, false);
-    w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i + 2], 127 - bl),
-                                        ldexpf(v[4 * i + 3], 127 - bl), w, true);
-    cl[i] = (uint32_t)w;
+    s16x2 w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(s16x2{0, 0}, v[4 * i], v[4 * i + 1], sl, false);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, v[4 * i + 2], v[4 * i + 3], sl, true);
+    cl[i] = __builtin_bit_cast(uint32_t, w);
   }
   *bh_out = bh;
   *bl_out = bl;
