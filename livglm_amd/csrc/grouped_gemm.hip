@@ -372,6 +372,47 @@ __device__ __forceinline__ float quad_max(float v) {
   v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, true)));
   return fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, true)));
 }
+// The FP8 hi/lo split of one 32-element scale group held 8 per lane by four
+// lanes: v holds this lane's elements (hi and lo codes of v[4 j .. 4 j + 3] go
+// to ch[j] / cl[j]); gmax(a) is the maximum of a over the group's four lanes.
+// The scaled converts divide by (down) and multiply by (up) the f32 scale
+// operand, of which only the exponent field counts: the E8M0 byte b shifted
+// into that field stands for 2^(b - 127), also for b = 0.  Codes and residuals
+// are those of ldexp by 127 - b and the unscaled converts (checked on the
+// device for every byte class, FP8 subnormals and ties).
+template <typename GroupMax>
+__device__ __forceinline__ void fp8_split_lane8(float v[8], GroupMax gmax, uint32_t ch[2],
+                                                uint32_t cl[2], int &bh, int &bl) {
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+  bh = split_scale_byte(gmax(amax));
+  const float sh = __uint_as_float((uint32_t)bh << 23);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    s16x2 w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(s16x2{0, 0}, v[4 * j], v[4 * j + 1], sh, false);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, v[4 * j + 2], v[4 * j + 3], sh, true);
+    ch[j] = __builtin_bit_cast(uint32_t, w);
+    // residuals, exact in f32
+    v[4 * j] -= __builtin_amdgcn_cvt_scalef32_f32_fp8(ch[j], sh, 0);
+    v[4 * j + 1] -= __builtin_amdgcn_cvt_scalef32_f32_fp8(ch[j], sh, 1);
+    v[4 * j + 2] -= __builtin_amdgcn_cvt_scalef32_f32_fp8(ch[j], sh, 2);
+    v[4 * j + 3] -= __builtin_amdgcn_cvt_scalef32_f32_fp8(ch[j], sh, 3);
+  }
+  float ramax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ramax = fmaxf(ramax, fabsf(v[j]));
+  bl = split_scale_byte(gmax(ramax));
+  const float sl = __uint_as_float((uint32_t)bl << 23);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    s16x2 w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(s16x2{0, 0}, v[4 * j], v[4 * j + 1], sl, false);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, v[4 * j + 2], v[4 * j + 3], sl, true);
+    cl[j] = __builtin_bit_cast(uint32_t, w);
+  }
+}
+
 __device__ __forceinline__ void act_split_one(const uint16_t *x, long long groups, long long i,
                                               uint8_t *hi, uint8_t *lo, uint8_t *shi,
                                               uint8_t *slo) {
@@ -385,41 +426,9 @@ __device__ __forceinline__ void act_split_one(const uint16_t *x, long long group
     v[2 * h] = __uint_as_float(w[h] << 16);
     v[2 * h + 1] = __uint_as_float(w[h] & 0xffff0000u);
   }
-  float amax = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
-  const int bh = split_scale_byte(quad_max(amax));
-  uint32_t ch[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    int c = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j], 127 - bh),
-                                            ldexpf(v[4 * j + 1], 127 - bh), 0, false);
-    c = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j + 2], 127 - bh),
-                                        ldexpf(v[4 * j + 3], 127 - bh), c, true);
-    ch[j] = (uint32_t)c;
-  }
-  // residuals (exact in f32) and their own scale
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int c = (int)ch[j];
-    v[4 * j] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(c, 0), bh - 127);
-    v[4 * j + 1] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(c, 1), bh - 127);
-    v[4 * j + 2] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(c, 2), bh - 127);
-    v[4 * j + 3] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(c, 3), bh - 127);
-  }
-  float ramax = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) ramax = fmaxf(ramax, fabsf(v[j]));
-  const int bl = split_scale_byte(quad_max(ramax));
-  uint32_t cl[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    int c = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j], 127 - bl),
-                                            ldexpf(v[4 * j + 1], 127 - bl), 0, false);
-    c = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * j + 2], 127 - bl),
-                                        ldexpf(v[4 * j + 3], 127 - bl), c, true);
-    cl[j] = (uint32_t)c;
-  }
+  uint32_t ch[2], cl[2];
+  int bh, bl;
+  fp8_split_lane8(v, [](float m) { return quad_max(m); }, ch, cl, bh, bl);
   *reinterpret_cast<uint2 *>(hi + g * 32 + 8 * part) = uint2{ch[0], ch[1]};
   *reinterpret_cast<uint2 *>(lo + g * 32 + 8 * part) = uint2{cl[0], cl[1]};
   if (part == 0) {
@@ -588,11 +597,6 @@ __global__ __launch_bounds__(256) void act_split_lowp_kernel(const uint16_t *x, 
   }
 }
 
-// The split of one 32-element scale group held 8 per lane by the four lanes
-// q = 0..3 of a lane row (lanes r, r + 16, r + 32, r + 48); v holds this
-// lane's elements 16 i + 4 q + m at v[4 i + m].  Same arithmetic as
-// act_split_kernel: ch[i] / cl[i] are the hi / lo codes of elements
-// 16 i + 4 q .. + 3, bh / bl the group's scale bytes.
 // Maximum over the four lanes l, l ^ 16, l ^ 32, l ^ 48: gfx950's row swaps
 // (one VALU instruction each, no LDS round trip).
 __device__ __forceinline__ float quad_row_max(float v) {
@@ -604,44 +608,14 @@ __device__ __forceinline__ float quad_row_max(float v) {
   return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
 }
 
+// The split of one 32-element scale group held 8 per lane by the four lanes
+// q = 0..3 of a lane row (lanes r, r + 16, r + 32, r + 48); v holds this
+// lane's elements 16 i + 4 q + m at v[4 i + m].  The arithmetic of
+// act_split_kernel: ch[i] / cl[i] are the hi / lo codes of elements
+// 16 i + 4 q .. + 3, bh / bl the group's scale bytes.
 __device__ __forceinline__ void split_group_part(float v[8], uint32_t ch[2], uint32_t cl[2],
                                                  int *bh_out, int *bl_out) {
-  // The scaled converts divide by (down) and multiply by (up) the f32 scale
-  // operand, of which only the exponent field counts: the E8M0 byte b shifted
-  // into that field stands for 2^(b - 127), also for b = 0.  The same codes
-  // and residuals as ldexp by 127 - b and the unscaled converts (checked on
-  // the device for every byte class, FP8 subnormals and ties).
-  typedef short s16x2 __attribute__((ext_vector_type(2)));
-  float amax = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
-  amax = quad_row_max(amax);
-  const int bh = split_scale_byte(amax);
-  const float sh = __uint_as_float((uint32_t)bh << 23);
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    s16x2 w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(s16x2{0, 0}, v[4 * i], v[4 * i + 1], sh, false);
-    w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, v[4 * i + 2], v[4 * i + 3], sh, true);
-    ch[i] = __builtin_bit_cast(uint32_t, w);
-    v[4 * i] -= __builtin_amdgcn_cvt_scalef32_f32_fp8(ch[i], sh, 0);
-    v[4 * i + 1] -= __builtin_amdgcn_cvt_scalef32_f32_fp8(ch[i], sh, 1);
-    v[4 * i + 2] -= __builtin_amdgcn_cvt_scalef32_f32_fp8(ch[i], sh, 2);
-    v[4 * i + 3] -= __builtin_amdgcn_cvt_scalef32_f32_fp8(ch[i], sh, 3);
-  }
-  float ramax = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) ramax = fmaxf(ramax, fabsf(v[j]));
-  ramax = quad_row_max(ramax);
-  const int bl = split_scale_byte(ramax);
-  const float sl = __uint_as_float((uint32_t)bl << 23);
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    s16x2 w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(s16x2{0, 0}, v[4 * i], v[4 * i + 1], sl, false);
-    w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, v[4 * i + 2], v[4 * i + 3], sl, true);
-    cl[i] = __builtin_bit_cast(uint32_t, w);
-  }
-  *bh_out = bh;
-  *bl_out = bl;
+  fp8_split_lane8(v, [](float m) { return quad_row_max(m); }, ch, cl, *bh_out, *bl_out);
 }
 
 struct SplitArgs {

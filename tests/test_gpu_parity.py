@@ -548,6 +548,33 @@ def test_act_split_fp8_exact(gu):
     assert np.array_equal(recon.reshape(rows, K), O.bf16_bits_to_f32(xb).astype(np.float64))
 
 
+def test_act_split_fp8_extreme_scales(gu):
+    # the split at the ends of the E8M0 range: groups of bf16 denormals and
+    # near-denormals (scale byte 0), groups near the bf16 maximum (byte ~245),
+    # and groups with one large element over small ones (the lo term's scale
+    # far below hi's); codes and scales bit-exact against the numpy model
+    rng = np.random.default_rng(31)
+    rows, K = 64, 256
+    g = K // 32
+    x = rng.normal(0, 1, (rows, g, 32))
+    binade = np.empty((rows, g, 1), dtype=np.int64)
+    binade[:16] = rng.integers(-140, -118, (16, g, 1))   # tiny: scale byte 0 .. a few
+    binade[16:32] = rng.integers(110, 125, (16, g, 1))   # huge: scale byte ~234 .. 245
+    binade[32:] = rng.integers(-20, 20, (rows - 32, g, 1))
+    x = x * np.ldexp(1.0, binade)
+    x[32:48, :, 0] *= np.ldexp(1.0, 40)                  # one element 2^40 above the rest
+    x[48:, :, 5] = np.ldexp(1.0, rng.integers(-30, 30, (rows - 48, g)))
+    xb = O.f32_to_bf16_bits(x.reshape(rows, K).astype(np.float32))
+    lib = native.load()
+    buf = gu.workspace(lib.glm_act_split_bytes(rows, K))
+    gu.call("glm_act_split_fp8", gu.stream(), gu.p(gu.to_dev(xb)), rows, K, gu.p(buf))
+    hi, lo, shi, slo = _split_parts(buf, rows, K)
+    w_hi, w_lo, w_shi, w_slo = _split_model(xb, K)
+    assert (w_shi == 0).any() and w_shi.max() >= 240  # both ends of the range are reached
+    assert np.array_equal(shi, w_shi.reshape(rows, -1)) and np.array_equal(slo, w_slo.reshape(rows, -1))
+    assert np.array_equal(hi, w_hi) and np.array_equal(lo, w_lo)
+
+
 def test_routed_experts_generic_shapes(gu):
     # tiny geometry of the reference's tests (tests/helpers.py: d=32, I=32) and
     # one more that is not a multiple of the 128-wide MFMA chunk
