@@ -89,9 +89,11 @@ int glm_router_topk(void *stream, const uint16_t *x, int T, int d, const float *
  * u >= num_active hold {-1, 0, 0, 0}); status [1] (0, or 1 if an index >= E
  * was seen -- such pairs are dropped, inv = -1, and the sorted positions past
  * offsets[E] hold -1 in perm and pair_token).  Up to 4096 pairs one
- * workgroup sorts them; beyond, a chunk-parallel count / scan / scatter over
- * 1024-pair chunks (pair_token serves as its scratch until it is filled last;
- * the result is the same).
+ * workgroup sorts them; beyond, two chunk-parallel launches over 1024-pair
+ * chunks: each chunk ranks its pairs per expert and counts them, then each
+ * chunk sums the counts of the chunks before it and places its pairs
+ * (pair_token holds the chunk counts until it is filled last; the result is
+ * the same).
  * Limits: E <= 448 (one workgroup's LDS holds the per-expert bitmaps).
  */
 int glm_moe_dispatch(void *stream, const uint32_t *indices, int T, int top_k, int E,
