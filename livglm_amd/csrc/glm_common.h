@@ -132,10 +132,12 @@ __host__ __device__ inline long long mxfp4_tile_piece(long long row, long long p
 
 // limited_swiglu on one element with bf16 intermediates (expert_ssd.py:103-107):
 // g = min(g, L); u = clip(u, -L, L); h = bf16(bf16(g * bf16(sigmoid(g))) * u).
+// The clamps are IEEE minimum / maximum, so a NaN g or u passes through them,
+// as through mx.minimum / mx.clip.
 __device__ __forceinline__ float limited_swiglu(float g, float u, float limit_bf16) {
   if (limit_bf16 > 0.0f) {
-    g = fminf(g, limit_bf16);
-    u = fminf(fmaxf(u, -limit_bf16), limit_bf16);
+    g = __builtin_elementwise_minimum(g, limit_bf16);
+    u = __builtin_elementwise_maximum(__builtin_elementwise_minimum(u, limit_bf16), -limit_bf16);
   }
   float s = bf16_round(sigmoid_f32(g));
   float a = bf16_round(g * s);

@@ -49,9 +49,11 @@ static inline float sigmoid_f32(float x) {
   return x < 0.0f ? y : 1.0f - y;
 }
 
+/* limited_swiglu (expert_ssd.py:103-107); a NaN g or u passes through the
+ * clamps, as through mx.minimum / mx.clip and numpy's minimum / clip. */
 static inline float swiglu(float g, float u, float L) {
   if (L > 0.0f) {
-    g = g < L ? g : L;
+    g = g > L ? L : g;
     u = u < -L ? -L : (u > L ? L : u);
   }
   float s = bf16_round(sigmoid_f32(g));

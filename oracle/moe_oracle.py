@@ -272,8 +272,9 @@ def limited_swiglu_bf16(gate, up, limit: float) -> np.ndarray:
         g = np.minimum(g, L)
         u = np.clip(u, -L, L)
     s = bf16_round(sigmoid_f32(g))
-    a = bf16_round(g * s)
-    return bf16_round(a * u)
+    with np.errstate(invalid="ignore", over="ignore"):  # -inf * 0 is NaN, as in MLX
+        a = bf16_round(g * s)
+        return bf16_round(a * u)
 
 
 def _dot_f32(a, b) -> np.ndarray:

@@ -624,6 +624,51 @@ def test_limited_swiglu_general(gu):
         assert np.max(np.abs(got.astype(np.int32) - want.astype(np.int32))) <= 1
 
 
+def test_limited_swiglu_nan_and_infinities(gu):
+    # NaN in the gate or the up value passes the clamps (mx.minimum / mx.clip),
+    # +-inf is clamped to the limit, a gate of -inf without a limit gives NaN
+    vals = np.float32([np.nan, np.inf, -np.inf, 0.0, -0.0, 1.0, -3.0, 12.0, -12.0])
+    g, u = (a.ravel() for a in np.meshgrid(vals, vals, indexing="ij"))
+    gb, ub = O.f32_to_bf16_bits(g), O.f32_to_bf16_bits(u)
+    for limit in (10.0, 0.0):
+        want = O.f32_to_bf16_bits(O.limited_swiglu_bf16(O.bf16_bits_to_f32(gb),
+                                                        O.bf16_bits_to_f32(ub), limit))
+        got = _swiglu_gpu(gu, gb, ub, limit)
+        gf, wf = O.bf16_bits_to_f32(got), O.bf16_bits_to_f32(want)
+        assert np.array_equal(np.isnan(gf), np.isnan(wf))
+        np.testing.assert_array_equal(got[~np.isnan(wf)], want[~np.isnan(wf)])
+
+
+@pytest.mark.parametrize("T,d,E,k,I,Is", [(2, 2048, 128, 8, 768, 768), (40, 1024, 64, 8, 512, 512),
+                                          (200, 2048, 64, 8, 768, 0)])
+def test_moe_layer_nan_gate_scale(gu, T, d, E, k, I, Is):
+    # one routed expert's gate row with a NaN scale byte (E8M0 255): its gate
+    # value is NaN beside a finite up value, the NaN passes the SwiGLU clamp and
+    # every output of the tokens routed to that expert is NaN -- on the
+    # few-token, decode and grouped paths, as in the oracle
+    shape = MoEShape("nan_scale", T, d, E, k, I, Is)
+    layer = make_layer(shape, 6100 + T)
+    _, _, i0, _ = O.router(O.bf16_bits_to_f32(layer["x"]), layer["router_weight"],
+                           layer["router_bias"], top_k=k, n_group=1, topk_group=1,
+                           norm_topk_prob=True, routed_scaling_factor=shape.routed_scaling_factor)
+    # token 0's expert shared by the fewest tokens, so that some rows stay finite
+    e = int(min(i0[0], key=lambda c: (i0 == c).any(axis=1).sum()))
+    layer["gate_proj.weight_scale"][e, 5, 1] = 255
+    want, inter = _oracle_layer(layer, shape, shared=Is > 0)
+    hit = (inter["indices"] == e).any(axis=1)
+    assert hit.any() and not hit.all()
+    assert np.array_equal(np.isnan(want).all(axis=1), hit) and not np.isnan(want[~hit]).any()
+    out, w, idx = gu.run_layer(gu.upload_layer(layer), shape, shared=Is > 0)
+    got_idx = gu.host(idx).astype(np.uint32)
+    _check_indices(got_idx, inter["indices"], inter["choice"], k)
+    same = np.all(got_idx == inter["indices"], axis=1)
+    assert same[0] and same.sum() >= T - 1
+    got = gu.host(out)
+    assert np.array_equal(np.isnan(got[same]), np.isnan(want[same]))
+    ok = same & ~hit
+    assert O.rel_l2(got[ok], want[ok]) < REL_L2
+
+
 def test_combine_bit_exact(gu):
     torch = _torch()
     rng = np.random.default_rng(3)

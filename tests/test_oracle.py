@@ -242,6 +242,26 @@ def test_limited_swiglu_known_values():
     assert h2[0] == 20.0
 
 
+def test_limited_swiglu_nan_and_infinities():
+    # expert_ssd.py:103-107 clamps with mx.minimum / mx.clip, whose float forms
+    # return a NaN operand (MLX's Minimum / Maximum), and nn.silu is x * sigmoid(x):
+    # NaN in either input gives NaN, +inf is clamped to the limit, a gate of
+    # -inf gives -inf * 0 = NaN
+    L = 10.0
+    g = np.array([np.nan, 1.0, np.inf, -np.inf, 1.0, 2.0], np.float32)
+    u = np.array([1.0, np.nan, 1.0, 1.0, np.inf, -np.inf], np.float32)
+    h = O.limited_swiglu_bf16(g, u, L)
+    assert np.isnan(h[:2]).all() and np.isnan(h[3])
+    assert h[2] == O.limited_swiglu_bf16(np.float32([L]), np.float32([1.0]), L)[0] == 10.0
+    s1 = O.bf16_round(O.sigmoid_f32(np.float32(1.0)))
+    assert h[4] == O.bf16_round(O.bf16_round(np.float32(1.0) * s1) * np.float32(L))
+    s2 = O.bf16_round(O.sigmoid_f32(np.float32(2.0)))
+    assert h[5] == O.bf16_round(O.bf16_round(np.float32(2.0) * s2) * np.float32(-L))
+    # no limit: nothing is clamped
+    h0 = O.limited_swiglu_bf16(np.float32([np.inf, np.nan]), np.float32([1.0, 1.0]), 0.0)
+    assert h0[0] == np.inf and np.isnan(h0[1])
+
+
 # --------------------------------------------------------------------------- router
 
 
@@ -530,6 +550,38 @@ def test_c_restatement_router_nan_choice(cpu_twin):
                              norm_topk_prob=True, routed_scaling_factor=2.5)
     assert not (want == 6).any()
     np.testing.assert_array_equal(idx, want)
+
+
+def test_c_restatement_nan_gate_scale(cpu_twin):
+    # one routed expert's gate row with a NaN scale byte (E8M0 255): its gate
+    # value is NaN while its up value is finite; the NaN passes the SwiGLU
+    # clamp (as through mx.minimum) and every output of the tokens routed to
+    # that expert is NaN, in the C twin as in the numpy oracle
+    from livglm_amd.workloads import MoEShape
+    rng = np.random.default_rng(35)
+    shape = MoEShape("tiny", T=6, d=128, E=16, k=4, I=64, I_shared=0)
+    bank = _tiny_bank(rng, shape.E, shape.d, shape.I)
+    x = O.f32_to_bf16_bits(rng.normal(0, 1, (shape.T, shape.d)).astype(np.float32))
+    W = rng.normal(0, 0.02, (shape.E, shape.d)).astype(np.float32)
+    b = np.zeros(shape.E, np.float32)
+    _, _, idx0, _ = O.router(O.bf16_bits_to_f32(x), W, b, top_k=shape.k, n_group=1,
+                             topk_group=1, norm_topk_prob=True, routed_scaling_factor=2.5)
+    e = int(idx0[0, 0])
+    bank.gate_s[e, 3, 0] = 255
+    layer = {"x": x, "router_weight": W, "router_bias": b}
+    layer.update(zip(("gate_proj.weight_packed", "gate_proj.weight_scale", "up_proj.weight_packed",
+                      "up_proj.weight_scale", "down_proj.weight_packed", "down_proj.weight_scale"),
+                     (bank.gate_w, bank.gate_s, bank.up_w, bank.up_s, bank.down_w,
+                      bank.down_s)))
+    out, _, idx = cpu_twin.moe_layer(layer, shape, shared=False)
+    want = O.moe_layer(O.bf16_bits_to_f32(x), W, b, bank, None, top_k=shape.k, n_group=1,
+                       topk_group=1, norm_topk_prob=True, routed_scaling_factor=2.5,
+                       swiglu_limit=10.0)
+    hit = (idx0 == e).any(axis=1)
+    assert hit.any() and not hit.all()
+    assert np.array_equal(np.isnan(want), np.repeat(hit[:, None], shape.d, axis=1))
+    assert np.array_equal(np.isnan(out), np.isnan(want))
+    assert O.rel_l2(out[~hit], want[~hit]) < 1e-5
 
 
 def test_c_restatement_mxfp8_linear(cpu_twin):
