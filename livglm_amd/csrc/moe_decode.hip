@@ -31,6 +31,7 @@
 // across blocks inside a kernel, and every reduction runs in one fixed order.
 #include "mfma_tile.h"
 #include "scalex_tile.h"
+#include "router_mfma.h"
 #include "topk_select.h"
 
 int glm_router_select_launch(hipStream_t stream, const float *logits, const float *bias, int T,
@@ -146,6 +147,53 @@ __device__ void shared_gate_up_tile(const SharedArgs &a, int b, glm_f32x4 *red) 
       }
     }
   }
+}
+
+// The same full-K tile (16 rows, one group of 16 tokens) computed by 16 waves
+// that split K, CPW 128-wide chunks each: the workgroups that run beside the
+// router's tiles in router_shared_kernel, where a wave's whole K range goes
+// out in one round trip.
+constexpr int kRouterShWaves = 16;
+
+template <int CPW>
+__device__ void shared_gate_up_tile16(const SharedArgs &a, int b, glm_f32x4 *red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int d = a.d;
+  const int tiles = a.Is / 16;
+  const int row0 = (b % tiles) * 16;
+  const int t = (b / tiles) * 16 + r;
+  const int kbase = wave * CPW * 128;
+  const uint8_t *wrow[2] = {a.sg + (size_t)(row0 + r) * d * 2, a.su + (size_t)(row0 + r) * d * 2};
+  const uint8_t *srow[2] = {nullptr, nullptr};
+  const uint16_t *act = a.x + (size_t)min(t, a.T - 1) * d;  // padding: any valid row
+  glm_f32x4 acc[2] = {glm_f32x4{0.f, 0.f, 0.f, 0.f}, glm_f32x4{0.f, 0.f, 0.f, 0.f}};
+  wave_mma<FMT_BF16, 2, CPW>(wrow, srow, kbase, q, act, acc);
+  if (ksplit_reduce<2>(acc, red, wave, kRouterShWaves, lane) && t < a.T) {
+    uint32_t o[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      o[m] = f32_to_bf16(limited_swiglu(bf16_round(acc[0][m]), bf16_round(acc[1][m]), a.limit));
+    store_rows4(a.hs + (size_t)t * a.Is + row0 + 4 * q, o);
+  }
+}
+
+// Router logits on f32 MFMA (router_gemm_tile, 16-expert tiles, blocks
+// [0, router_blocks), token tile fastest) with the shared expert's full-K
+// gate/up tiles as the workgroups after them: both need only x, and the
+// router's small grid leaves most CUs free.
+template <int CPW>
+__global__ __launch_bounds__(64 * kRouterShWaves) void router_shared_kernel(
+    const uint16_t *x, const float *w, int T, int d, int E, float *logits, int token_tiles,
+    int router_blocks, SharedArgs sh) {
+  __shared__ glm_f32x4 red[kRouterShWaves - 1][2][64];
+  const int b = blockIdx.x;
+  if (b < router_blocks) {
+    router_gemm_tile<kRouterShWaves, 2, 1>(x, w, T, d, E, logits, b % token_tiles,
+                                           b / token_tiles, red);
+    return;
+  }
+  shared_gate_up_tile16<CPW>(sh, b - router_blocks, &red[0][0][0]);
 }
 
 template <int CPW_S>
@@ -1069,19 +1117,36 @@ int glm_route_decode_launch(hipStream_t stream, const uint16_t *x, int T, int d,
   const int epl = (E + 63) / 64;
   const int e8 = epl <= 1 ? 1 : (epl <= 2 ? 2 : (epl <= 4 ? 4 : 8));
   if (glm_router_gemm_supported(T, d)) {
-    // many tokens: the logits on MFMA in their own kernel, then the selection
-    // (one wave per token) beside the shared gate/up tiles
-    rc = glm_router_logits_launch(stream, x, T, d, w, E, logits);
-    if (rc) return rc;
+    // many tokens: the logits on MFMA, then the selection (one wave per
+    // token).  Below 256 tokens with d % 2048 == 0 the shared expert's full-K
+    // gate/up tiles run as extra workgroups of the router's launch (router_shared_kernel),
+    // otherwise beside the selection.
+    SharedArgs sh_sel = sh;
+    if (sh.gu_blocks > 0 && sh.skq == 1 && T < 256 && d % 2048 == 0 && d / 2048 <= 2) {
+      const int token_tiles = (T + 15) / 16;
+      const int router_blocks = token_tiles * ((E + 15) / 16);
+      const dim3 g0(router_blocks + sh.gu_blocks);
+      if (d / 2048 == 1)
+        hipLaunchKernelGGL((router_shared_kernel<1>), g0, dim3(64 * kRouterShWaves), 0, stream, x,
+                           w, T, d, E, logits, token_tiles, router_blocks, sh);
+      else
+        hipLaunchKernelGGL((router_shared_kernel<2>), g0, dim3(64 * kRouterShWaves), 0, stream, x,
+                           w, T, d, E, logits, token_tiles, router_blocks, sh);
+      GLM_LAUNCH_CHECK("router_shared_kernel");
+      sh_sel.gu_blocks = 0;
+    } else {
+      rc = glm_router_logits_launch(stream, x, T, d, w, E, logits);
+      if (rc) return rc;
+    }
     a.logits_done = 1;
     a.presel = 1;
-    const dim3 g((T + 3) / 4 + sh.gu_blocks);
+    const dim3 g((T + 3) / 4 + sh_sel.gu_blocks);
 #define GLM_SS(C)                                                                              \
   switch (e8) {                                                                                \
-    case 1: hipLaunchKernelGGL((select_shared_kernel<C, 1>), g, dim3(kRouteThreads), 0, stream, a, sh); break; \
-    case 2: hipLaunchKernelGGL((select_shared_kernel<C, 2>), g, dim3(kRouteThreads), 0, stream, a, sh); break; \
-    case 4: hipLaunchKernelGGL((select_shared_kernel<C, 4>), g, dim3(kRouteThreads), 0, stream, a, sh); break; \
-    default: hipLaunchKernelGGL((select_shared_kernel<C, 8>), g, dim3(kRouteThreads), 0, stream, a, sh); break; \
+    case 1: hipLaunchKernelGGL((select_shared_kernel<C, 1>), g, dim3(kRouteThreads), 0, stream, a, sh_sel); break; \
+    case 2: hipLaunchKernelGGL((select_shared_kernel<C, 2>), g, dim3(kRouteThreads), 0, stream, a, sh_sel); break; \
+    case 4: hipLaunchKernelGGL((select_shared_kernel<C, 4>), g, dim3(kRouteThreads), 0, stream, a, sh_sel); break; \
+    default: hipLaunchKernelGGL((select_shared_kernel<C, 8>), g, dim3(kRouteThreads), 0, stream, a, sh_sel); break; \
   }
     switch (d / 512) {
       case 2: GLM_SS(2) break;
