@@ -104,8 +104,10 @@ struct Bf16Waves {
   static_assert(WF * BR * 16 == TW && WT * BT * 16 == kTileM, "wave tiles cover the tile");
 };
 
+// One workgroup's work item of the bf16 GEMM; lin is its index in the
+// launch's range of these workgroups (a multiple of kXcds covering every item).
 template <int NPROJ, int TW>
-__global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs a) {
+__device__ __forceinline__ void bf16_gemm_item(const GroupedArgs &a, int lin) {
   using L = Bf16Layout<TW>;
   using WV = Bf16Waves<TW>;
   static_assert(NPROJ == 2 || TW == 256, "192-row tiles pair gate and up");
@@ -113,7 +115,6 @@ __global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs
   const int nft = a.feature_tiles;
   const int ntiles = (a.dense_rows + kTileM - 1) / kTileM;
   const int items = ntiles * nft;
-  const int lin = blockIdx.x;  // the grid is a multiple of kXcds covering every item
   const int per_xcd = (items + kXcds - 1) / kXcds;
   const int k_on_xcd = lin / kXcds;
   const int item = (lin % kXcds) * per_xcd + k_on_xcd;
@@ -285,6 +286,11 @@ __global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
+}
+
+template <int NPROJ, int TW>
+__global__ __launch_bounds__(kThreads) void grouped_bf16_gemm_kernel(GroupedArgs a) {
+  bf16_gemm_item<NPROJ, TW>(a, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1386,14 +1392,14 @@ __device__ __forceinline__ void w8_body(const SplitArgs &a, long long e, int pos
   }
 }
 
+// One workgroup's work item of the eight-wave form; lin as in bf16_gemm_item.
 template <int NPROJ, int AF>
-__global__ __launch_bounds__(kW8Threads) void grouped_f8f6f4_w8_kernel(SplitArgs a) {
+__device__ __forceinline__ void w8_item(const SplitArgs &a, int lin) {
   const int nft = a.feature_tiles;
   // a count above the list's length is clamped to it, so no entry past
   // `tiles` is read and every item still has a workgroup in the grid
   const int ntiles = max(0, min(*a.num_tiles, a.max_tiles));
   const int items = ntiles * nft;
-  const int lin = blockIdx.x;
   const int per_xcd = (items + kXcds - 1) / kXcds;
   const int k_on_xcd = lin / kXcds;
   const int item = (lin % kXcds) * per_xcd + k_on_xcd;
@@ -1420,6 +1426,25 @@ __global__ __launch_bounds__(kW8Threads) void grouped_f8f6f4_w8_kernel(SplitArgs
     case 1: w8_body<NPROJ, AF, 1>(a, tile.x, tile.y, rows, ftile, tok0); break;
     default: w8_body<NPROJ, AF, 0>(a, tile.x, tile.y, rows, ftile, tok0); break;
   }
+}
+
+template <int NPROJ, int AF>
+__global__ __launch_bounds__(kW8Threads) void grouped_f8f6f4_w8_kernel(SplitArgs a) {
+  w8_item<NPROJ, AF>(a, blockIdx.x);
+}
+
+// The routed gate/up (work items of the eight-wave form, workgroups
+// [0, routed_blocks)) and the bf16 shared expert's dense gate/up (TW-row
+// tiles, the workgroups after them) in one launch: the two need only x, and
+// the shared tiles fill the CUs that the routed items' last round leaves idle.
+template <int TW>
+__global__ __launch_bounds__(kW8Threads) void gate_up_with_shared_kernel(SplitArgs a, GroupedArgs s,
+                                                                        int routed_blocks) {
+  static_assert(kW8Threads == kThreads, "one workgroup size for both ranges");
+  if ((int)blockIdx.x < routed_blocks)
+    w8_item<2, ACT_FP8X2>(a, blockIdx.x);
+  else
+    bf16_gemm_item<2, TW>(s, blockIdx.x - routed_blocks);
 }
 
 }  // namespace glm
@@ -1635,6 +1660,81 @@ int glm_grouped_down_launch(hipStream_t stream, const void *h_split, long long P
 
 // Dense bf16 SwiGLU MLP over T token rows (the shared expert at many tokens):
 // h = limited_swiglu(bf16(x Wg^T), bf16(x Wu^T)); out = bf16(h Wd^T).
+// The layer's routed gate/up (FP8 split of x; the epilogue writes h's split)
+// and the bf16 shared expert's gate/up (x [T][d] -> shared_h [T][Is], dense
+// mode) in one launch, gate_up_with_shared_kernel: the routed workgroups as
+// split_launch grids them, then the shared ones as grouped_launch does (192- or
+// 256-row weight tiles).  The shared down follows with glm_grouped_dense_down_launch.
+int glm_grouped_gate_up_shared_launch(hipStream_t stream, const void *x_split, int T,
+                                      const int32_t *pair_token, const int4 *tiles,
+                                      const int32_t *num_tiles, int max_tiles, int d, int I,
+                                      const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
+                                      const uint8_t *us, uint16_t *h, float limit, void *h_split,
+                                      long long P, const uint16_t *x, int Is, const uint16_t *sgw,
+                                      const uint16_t *suw, uint16_t *shared_h) {
+  SplitArgs a{};
+  set_split(a, x_split, T, d, ACT_FP8X2);
+  a.out_split = static_cast<uint8_t *>(h_split);
+  a.out_rows = P;
+  a.act_index = pair_token;
+  a.tiles = tiles;
+  a.num_tiles = num_tiles;
+  a.max_tiles = max_tiles;
+  a.w[0] = gw;
+  a.w[1] = uw;
+  a.s[0] = gs;
+  a.s[1] = us;
+  a.w_stride = (long long)I * (d / 2);
+  a.s_stride = (long long)I * (d / 32);
+  a.N = I;
+  a.K = d;
+  a.out = h;
+  a.limit = glm_limit_bf16(limit);
+  a.feature_tiles = a.N / (kSplitTileW / 2);
+  const long long r_items = (long long)max_tiles * a.feature_tiles;
+  const long long routed_blocks = (r_items + kXcds - 1) / kXcds * kXcds;
+  GroupedArgs sh{};
+  sh.act = x;
+  sh.dense_rows = T;
+  sh.w[0] = reinterpret_cast<const uint8_t *>(sgw);
+  sh.w[1] = reinterpret_cast<const uint8_t *>(suw);
+  sh.N = Is;
+  sh.K = d;
+  sh.out = shared_h;
+  sh.limit = glm_limit_bf16(limit);
+  const int stiles = (T + kTileM - 1) / kTileM;
+  const bool narrow = Is % 96 == 0 && (long long)stiles * (Is / (kTileW / 2)) < kNumCUs;
+  sh.feature_tiles = Is / (narrow ? 96 : kTileW / 2);
+  const long long s_items = (long long)stiles * sh.feature_tiles;
+  const long long shared_blocks = (s_items + kXcds - 1) / kXcds * kXcds;
+  const dim3 grid((unsigned)(routed_blocks + shared_blocks));
+  constexpr size_t kW8 = W8Layout<ACT_FP8X2>::kBytes;
+  if (narrow) {
+    constexpr size_t kB = kStages * (size_t)Bf16Layout<192>::kStageBytes;
+    hipLaunchKernelGGL((gate_up_with_shared_kernel<192>), grid, dim3(kW8Threads), kW8 > kB ? kW8 : kB,
+                       stream, a, sh, (int)routed_blocks);
+  } else {
+    constexpr size_t kB = kStages * (size_t)Bf16Layout<256>::kStageBytes;
+    hipLaunchKernelGGL((gate_up_with_shared_kernel<256>), grid, dim3(kW8Threads), kW8 > kB ? kW8 : kB,
+                       stream, a, sh, (int)routed_blocks);
+  }
+  GLM_LAUNCH_CHECK("gate_up_with_shared_kernel");
+  return GLM_OK;
+}
+
+// The bf16 shared expert's down GEMM alone (dense mode): h [T][Is] -> out [T][d].
+int glm_grouped_dense_down_launch(hipStream_t stream, const uint16_t *h, int T, int Is, int d,
+                                  const uint16_t *dw, uint16_t *out) {
+  GroupedArgs b{};
+  b.act = h;
+  b.dense_rows = T;
+  b.w[0] = b.w[1] = reinterpret_cast<const uint8_t *>(dw);
+  b.N = d;
+  b.K = Is;
+  b.out = out;
+  return grouped_launch(stream, b, 1, (T + kTileM - 1) / kTileM);
+}
+
 bool glm_grouped_dense_mlp_supported(int T, int d, int I, int fmt) {
   return fmt == FMT_BF16 && T >= 256 && d % 256 == 0 && I % 128 == 0;
 }

@@ -71,6 +71,16 @@ int glm_down_launch(hipStream_t stream, const uint16_t *h, int T, int k, int I, 
 int glm_mlp_launch(hipStream_t stream, const uint16_t *x, int T, int d, int I, int fmt,
                    const void *gw, const uint8_t *gs, const void *uw, const uint8_t *us,
                    const void *dw, const uint8_t *ds, float limit, uint16_t *h, uint16_t *out);
+bool glm_grouped_dense_mlp_supported(int T, int d, int I, int fmt);
+int glm_grouped_gate_up_shared_launch(hipStream_t stream, const void *x_split, int T,
+                                      const int32_t *pair_token, const int4 *tiles,
+                                      const int32_t *num_tiles, int max_tiles, int d, int I,
+                                      const uint8_t *gw, const uint8_t *gs, const uint8_t *uw,
+                                      const uint8_t *us, uint16_t *h, float limit, void *h_split,
+                                      long long P, const uint16_t *x, int Is, const uint16_t *sgw,
+                                      const uint16_t *suw, uint16_t *shared_h);
+int glm_grouped_dense_down_launch(hipStream_t stream, const uint16_t *h, int T, int Is, int d,
+                                  const uint16_t *dw, uint16_t *out);
 int glm_combine_launch(hipStream_t stream, const uint16_t *y, const int32_t *inv, const float *w,
                        const uint16_t *shared, int T, int k, int d, float *out);
 bool glm_decode_path_supported(int T, int d, int E, int k, int I, int Is);
@@ -540,14 +550,26 @@ static int moe_forward_core(void *stream_v, const uint16_t *x, int T, int d,
                            grouped ? glm_grouped_tile_rows() : 0, grouped ? w.tiles : nullptr,
                            grouped ? w.num_tiles : nullptr, w.chunk_counts);
   if (rc) return rc;
+  bool shared_fused = false;
   if (grouped) {
     if (!split_early) {
       rc = glm_act_split_launch(stream, x, T, d, w.x_split);
       if (rc) return rc;
     }
-    rc = glm_grouped_gate_up_launch(stream, w.x_split, T, w.pair_token, w.tiles, w.num_tiles,
-                                    w.max_tiles, d, I, gate_packed, gate_scales, up_packed,
-                                    up_scales, w.h, swiglu_limit, w.h_split, (long long)T * top_k);
+    // a bf16 shared expert on the dense GEMMs: its gate/up tiles ride in the
+    // routed gate/up launch (after the routed work items)
+    shared_fused = has_shared && !shared_in &&
+                   glm_grouped_dense_mlp_supported(T, d, I_shared, shared_fmt);
+    if (shared_fused)
+      rc = glm_grouped_gate_up_shared_launch(
+          stream, w.x_split, T, w.pair_token, w.tiles, w.num_tiles, w.max_tiles, d, I,
+          gate_packed, gate_scales, up_packed, up_scales, w.h, swiglu_limit, w.h_split,
+          (long long)T * top_k, x, I_shared, static_cast<const uint16_t *>(shared_gate),
+          static_cast<const uint16_t *>(shared_up), w.shared_h);
+    else
+      rc = glm_grouped_gate_up_launch(stream, w.x_split, T, w.pair_token, w.tiles, w.num_tiles,
+                                      w.max_tiles, d, I, gate_packed, gate_scales, up_packed,
+                                      up_scales, w.h, swiglu_limit, w.h_split, (long long)T * top_k);
     if (rc) return rc;  // the gate/up epilogue writes h's FP8 split for the down GEMM
     rc = glm_grouped_down_launch(stream, w.h_split, (long long)T * top_k, w.tiles, w.num_tiles,
                                  w.max_tiles, I, d, down_packed, down_scales, w.y);
@@ -559,9 +581,13 @@ static int moe_forward_core(void *stream_v, const uint16_t *x, int T, int d,
   }
   if (rc) return rc;
   if (has_shared && !shared_in) {
-    rc = glm_mlp_launch(stream, x, T, d, I_shared, shared_fmt, shared_gate, shared_gate_scales,
-                        shared_up, shared_up_scales, shared_down, shared_down_scales,
-                        swiglu_limit, w.shared_h, w.shared_out);
+    if (shared_fused)
+      rc = glm_grouped_dense_down_launch(stream, w.shared_h, T, I_shared, d,
+                                         static_cast<const uint16_t *>(shared_down), w.shared_out);
+    else
+      rc = glm_mlp_launch(stream, x, T, d, I_shared, shared_fmt, shared_gate, shared_gate_scales,
+                          shared_up, shared_up_scales, shared_down, shared_down_scales,
+                          swiglu_limit, w.shared_h, w.shared_out);
     if (rc) return rc;
     shared_ready = w.shared_out;
   }
