@@ -848,6 +848,9 @@ SMALL_LAYERS = [
     (700, 1024, 32, 8, 256, 0, (1, 1)),
     # the decode path beyond 16 tokens (MFMA router, per-token selection, token groups)
     (40, 1024, 64, 8, 512, 512, (1, 1)),
+    # 33-64 tokens at d % 2048 == 0: the shared gate/up tiles in the router's
+    # launch (a partial last token tile and token group)
+    (50, 2048, 64, 8, 768, 768, (1, 1)),
     # 16-32 tokens: the shared expert's tiles in the routed expert kernels (two
     # chunks per shared down K range; one chunk at I_shared 128, two token groups)
     (16, 2048, 64, 8, 768, 768, (1, 1)),
