@@ -1015,7 +1015,9 @@ __global__ __launch_bounds__(kSplitThreads) void grouped_f8f6f4_kernel(SplitArgs
 // to 80 tokens = 8 x 5 MFMA blocks.  Every activation fragment read from LDS
 // then feeds 8 MFMAs instead of 4 (229 KB of operand reads per chunk and
 // workgroup instead of 393 KB), and the registers leave room to read
-// fragment f + 1 while the MFMAs of fragment f run.  The body is
+// fragment f + 1 while the MFMAs of fragment f run; with the exact FP8 split
+// the next chunk's weights and first fragment are read behind the last
+// MFMAs of the chunk before, after the barrier that releases them.  The body is
 // instantiated per count NB of the wave's 16-row token blocks (0..5), so every
 // fragment and accumulator index is static.
 // ---------------------------------------------------------------------------
@@ -1053,16 +1055,32 @@ struct W8Stage {
   static constexpr int value = N;
 };
 
-// N dwords from LDS at base + j * STEP (j < N, at most 5) into v; the caller
-// waits for them (lgkmcnt) before use.
+// N dwords from LDS at base + j * STEP (j < N, 2 or 5) into v, then a wait
+// for every LDS access of the wave in flight (lgkmcnt(0)), in one asm
+// statement: the compiler sees v defined only once the reads have landed, so
+// it never copies or spills a register that the LDS has yet to write.
 template <int N, int STEP>
 __device__ __forceinline__ void lds_rows(uint32_t *v, uint32_t base) {
-  static_assert(N >= 1 && N <= 5 && (N - 1) * STEP < 65536, "row table reads");
-  asm volatile("ds_read_b32 %0, %1" : "=v"(v[0]) : "v"(base) : "memory");
-  if constexpr (N > 1) asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v[1]) : "v"(base), "i"(STEP) : "memory");
-  if constexpr (N > 2) asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v[2]) : "v"(base), "i"(2 * STEP) : "memory");
-  if constexpr (N > 3) asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v[3]) : "v"(base), "i"(3 * STEP) : "memory");
-  if constexpr (N > 4) asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v[4]) : "v"(base), "i"(4 * STEP) : "memory");
+  static_assert((N == 2 || N == 5) && (N - 1) * STEP < 65536, "row table reads");
+  if constexpr (N == 2)
+    asm volatile(
+        "ds_read_b32 %0, %2\n\t"
+        "ds_read_b32 %1, %2 offset:%3\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1])
+        : "v"(base), "i"(STEP)
+        : "memory");
+  else
+    asm volatile(
+        "ds_read_b32 %0, %5\n\t"
+        "ds_read_b32 %1, %5 offset:%6\n\t"
+        "ds_read_b32 %2, %5 offset:%7\n\t"
+        "ds_read_b32 %3, %5 offset:%8\n\t"
+        "ds_read_b32 %4, %5 offset:%9\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4])
+        : "v"(base), "i"(STEP), "i"(2 * STEP), "i"(3 * STEP), "i"(4 * STEP)
+        : "memory");
 }
 
 template <int NPROJ, int AF, int NB>
@@ -1143,18 +1161,17 @@ __device__ __forceinline__ void w8_body(const SplitArgs &a, long long e, int pos
             act_row(s % kSplitTileM) * (uint32_t)(K / 32);
   }
 
-  auto issue = [&](auto st, int c) {
+  // The loads of chunk c into stage ST.  The activation rows' offsets come
+  // from the row table in LDS, read as explicit instructions (one base
+  // register, immediate offsets; a compiler-generated read keeps one address
+  // register per load live across the loop).
+  auto table_rows = [&](uint32_t *xrow) { lds_rows<kXL, 4 * kW8Waves * kRowsPerLoad>(xrow, xtab); };
+  auto issue_loads = [&](auto st, int c, const uint32_t *xrow) {
     constexpr int ST = decltype(st)::value;
-    // the table reads as explicit instructions (one base register, immediate
-    // offsets; a compiler-generated read would keep one address register per
-    // load live across the loop), waited for after the weight loads
-    uint32_t xrow[kXL];
-    lds_rows<kXL, 4 * kW8Waves * kRowsPerLoad>(xrow, xtab);
 #pragma unroll
     for (int j = 0; j < kWL; ++j)
       buf16_to_lds(j < 2 ? wrs0 : wrs1, smem + L::kW + ST * S::kWBytes + (j * kW8Waves + wv) * 1024,
                    wlane, wuni[j] + c * 1024);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
     for (int j = 0; j < kXL; ++j)
       if (S::kXSlots % kW8Waves == 0 || j * kW8Waves + wv < S::kXSlots)
@@ -1164,12 +1181,6 @@ __device__ __forceinline__ void w8_body(const SplitArgs &a, long long e, int pos
     buf4_to_lds(xrs, smem + L::kXS + ST * S::kXSBytes + xs0 * 4, xsoff, c * 4);
   };
 
-  // the wave's weight blocks (16 rows each, index into the stage's 32):
-  // gate/up: 4 gate blocks (features 64 wf .. 64 wf + 63), then the 4 up
-  // blocks of the same features; down: 8 consecutive blocks
-  auto wblk = [&](int b) {
-    return NPROJ == 2 ? (b < 4 ? 4 * wf + b : 16 + 4 * wf + b - 4) : 8 * wf + b;
-  };
 
   glm_f32x4 acc[8][NB > 0 ? NB : 1];
 #pragma unroll
@@ -1189,100 +1200,227 @@ __device__ __forceinline__ void w8_body(const SplitArgs &a, long long e, int pos
   const uint32_t wsl = (uint32_t)(L::kWS + 4 * r + q);
   const uint32_t xsl = (uint32_t)(L::kXS + 4 * (tok0 + r) + q);
 
-  // MFMAs of one staged chunk: the activation fragment f + 1 (term f / NB,
-  // token block f % NB) is read while the 8 MFMAs of fragment f run.  The
-  // weight scale bytes are packed four to a register; the MFMA's byte select
-  // picks one.
-  auto compute = [&](auto st) {
+  // Operand registers carried from one chunk to the next: the chunk's eight
+  // weight blocks (their scale bytes packed four to a register; the MFMA's
+  // byte select picks one) and two activation fragments, the one whose MFMAs
+  // run and the next.  Fragment f of a chunk is term f / NB, token block
+  // f % NB, held in xb[(f + P) & 1] for the chunk's parity P.
+  constexpr int kFrags = NB * S::kParts;
+  glm_i32x8 xb[2];
+  int xsc[2];
+  glm_i32x8 wa[8];
+  int wsp[2];
+  auto xfrag = [&](auto st, int f, glm_i32x8 &xbv, int &xs) {
     constexpr int ST = decltype(st)::value;
-    if constexpr (NB > 0) {
-      constexpr int kFrags = NB * S::kParts;
-      glm_i32x8 xb[2];
-      int xsc[2];
-      auto xfrag = [&](int f, glm_i32x8 &xbv, int &xs) {
-        const int t = f / NB, ct = f % NB;
-        constexpr int kXo = ST * S::kXBytes;
-        const int co = kXo + ct * 16 * S::kXRow;
-        const glm_u32x4 b0 = *reinterpret_cast<const glm_u32x4 *>(smem + (xl ^ (128u * t)) + co);
-        if constexpr (S::kParts == 2) {
-          const glm_u32x4 b1 =
-              *reinterpret_cast<const glm_u32x4 *>(smem + (xl ^ (128u * t + 64u)) + co);
-          xbv = glm_i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3],
-                          (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
-        } else {
-          xbv = glm_i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], 0, 0, 0, 0};
-        }
-        xs = smem[xsl + ST * S::kXSBytes + 4 * (t * kSplitTileM + ct * 16)];
-      };
-      xfrag(0, xb[0], xsc[0]);
-      glm_i32x8 wa[8];
-      int wsp[2];
+    const int t = f / NB, ct = f % NB;
+    constexpr int kXo = ST * S::kXBytes;
+    const int co = kXo + ct * 16 * S::kXRow;
+    const glm_u32x4 b0 = *reinterpret_cast<const glm_u32x4 *>(smem + (xl ^ (128u * t)) + co);
+    if constexpr (S::kParts == 2) {
+      const glm_u32x4 b1 = *reinterpret_cast<const glm_u32x4 *>(smem + (xl ^ (128u * t + 64u)) + co);
+      xbv = glm_i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3],
+                      (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+    } else {
+      xbv = glm_i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], 0, 0, 0, 0};
+    }
+    xs = smem[xsl + ST * S::kXSBytes + 4 * (t * kSplitTileM + ct * 16)];
+  };
+  // Weight block i of the wave (codes into w) and its scale byte.  The
+  // wave's eight blocks (16 rows each) index the stage's 32 as
+  // kWfBlocks * wf + boff(i): gate/up 4 gate blocks (features 64 wf ..
+  // 64 wf + 63), then the 4 up blocks of the same features; down 8
+  // consecutive blocks.  Each is read at one per-lane base plus an immediate
+  // offset.
+  constexpr int kWfBlocks = NPROJ == 2 ? 4 : 8;
+  auto boff = [](int i) { return NPROJ == 2 && i >= 4 ? i + 12 : i; };
+  const uint8_t *wbase = smem + wl + (uint32_t)(kWfBlocks * 1024) * (uint32_t)wf;
+  const uint8_t *wsbase = smem + wsl + (uint32_t)(kWfBlocks * 64) * (uint32_t)wf;
+  auto wread = [&](auto st, int i, glm_i32x8 &w) -> uint32_t {
+    constexpr int ST = decltype(st)::value;
+    const glm_u32x4 v =
+        *reinterpret_cast<const glm_u32x4 *>(wbase + ST * S::kWBytes + boff(i) * 1024);
+    w = glm_i32x8{(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
+    return wsbase[ST * S::kWSBytes + boff(i) * 64];
+  };
+  // the MFMA of fragment f with weight block B (the byte select must be a
+  // constant, hence one instantiation per block)
+  auto mf = [&](auto bt, int f, const glm_i32x8 &xv, int xs) {
+    constexpr int B = decltype(bt)::value;
+    const int ct = f % NB;
+    if (f < NB)
+      acc[B][ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+          wa[B], xv, acc[B][ct], 4, S::kMfmaFmt, B & 3, wsp[B >> 2], 0, xs);
+    else
+      acc[B][ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+          wa[B], xv, acc[B][ct], 4, S::kMfmaFmtLo, B & 3, wsp[B >> 2], 0, xs);
+  };
+  auto mf8 = [&](int f, const glm_i32x8 &xv, int xs) {
+    mf(W8Stage<0>{}, f, xv, xs);
+    mf(W8Stage<1>{}, f, xv, xs);
+    mf(W8Stage<2>{}, f, xv, xs);
+    mf(W8Stage<3>{}, f, xv, xs);
+    mf(W8Stage<4>{}, f, xv, xs);
+    mf(W8Stage<5>{}, f, xv, xs);
+    mf(W8Stage<6>{}, f, xv, xs);
+    mf(W8Stage<7>{}, f, xv, xs);
+  };
+  // a chunk's weight blocks, scales and first fragment (parity P)
+  auto read_head = [&](auto st, auto par) {
+    constexpr int P = decltype(par)::value;
+    xfrag(st, 0, xb[P], xsc[P]);
 #pragma unroll
-      for (int hb = 0; hb < 2; ++hb) {
-        uint32_t sb[4];
+    for (int hb = 0; hb < 2; ++hb) {
+      uint32_t sb[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int blk = wblk(4 * hb + i);
-          const glm_u32x4 v =
-              *reinterpret_cast<const glm_u32x4 *>(smem + wl + ST * S::kWBytes + blk * 1024);
-          wa[4 * hb + i] = glm_i32x8{(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
-          sb[i] = smem[wsl + ST * S::kWSBytes + blk * 64];
-        }
-        wsp[hb] = (int)(sb[0] | (sb[1] << 8) | (sb[2] << 16) | (sb[3] << 24));
+      for (int i = 0; i < 4; ++i) sb[i] = wread(st, 4 * hb + i, wa[4 * hb + i]);
+      wsp[hb] = (int)(sb[0] | (sb[1] << 8) | (sb[2] << 16) | (sb[3] << 24));
+    }
+  };
+
+  // The MFMAs of the chunk in stage ST (parity P), its head already in
+  // registers: each fragment's 8 MFMAs run while the next fragment is read.
+  // Before the last fragment's MFMAs the wave waits for its own loads of the
+  // next chunk and for its reads of this stage, and meets the other waves at
+  // the barrier: after it every wave's loads of the next chunk have landed
+  // and no wave reads this stage again.  The next chunk's head is then read
+  // into the registers that the last fragment's MFMAs free, one weight block
+  // behind each MFMA, so the next chunk's first MFMAs need not wait for a
+  // burst of reads after the barrier.
+  auto run_chunk = [&](auto st, auto par, auto nx) {
+    constexpr int ST = decltype(st)::value, P = decltype(par)::value;
+    constexpr int kNx = decltype(nx)::value;  // 1: a next chunk follows
+    constexpr int L = kFrags - 1;
+    // fragments 0 .. L - 2, each with the next one read ahead; the read of
+    // fragment L is the chunk's last access to its stage
+#pragma unroll
+    for (int f = 0; f + 1 < L; ++f) {
+      xfrag(st, f + 1, xb[(f + 1 + P) & 1], xsc[(f + 1 + P) & 1]);
+      mf8(f, xb[(f + P) & 1], xsc[(f + P) & 1]);
+    }
+    if constexpr (L >= 1) xfrag(st, L, xb[(L + P) & 1], xsc[(L + P) & 1]);
+#pragma unroll
+    for (int f = 0; f + 1 < L; ++f) {
+      __builtin_amdgcn_sched_group_barrier(0x100, S::kParts + 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    }
+    if constexpr (L >= 1) __builtin_amdgcn_sched_group_barrier(0x100, S::kParts + 1, 0);
+    if constexpr (kNx > 0) {
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & ~(15 << 8));  // vmcnt(0) lgkmcnt(0)
+      ring_barrier();
+      if constexpr (L >= 1) mf8(L - 1, xb[(L - 1 + P) & 1], xsc[(L - 1 + P) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      constexpr W8Stage<1 - ST> ns{};
+      constexpr int NP = (P + kFrags) & 1;
+      const glm_i32x8 xv = xb[(L + P) & 1];
+      const int xs = xsc[(L + P) & 1];
+      uint32_t sb[8];
+      mf(W8Stage<0>{}, L, xv, xs);
+      sb[0] = wread(ns, 0, wa[0]);
+      mf(W8Stage<1>{}, L, xv, xs);
+      sb[1] = wread(ns, 1, wa[1]);
+      mf(W8Stage<2>{}, L, xv, xs);
+      sb[2] = wread(ns, 2, wa[2]);
+      mf(W8Stage<3>{}, L, xv, xs);
+      sb[3] = wread(ns, 3, wa[3]);
+      mf(W8Stage<4>{}, L, xv, xs);
+      sb[4] = wread(ns, 4, wa[4]);
+      mf(W8Stage<5>{}, L, xv, xs);
+      sb[5] = wread(ns, 5, wa[5]);
+      mf(W8Stage<6>{}, L, xv, xs);
+      sb[6] = wread(ns, 6, wa[6]);
+      mf(W8Stage<7>{}, L, xv, xs);
+      sb[7] = wread(ns, 7, wa[7]);
+      xfrag(ns, 0, xb[NP], xsc[NP]);
+      wsp[0] = (int)(sb[0] | (sb[1] << 8) | (sb[2] << 16) | (sb[3] << 24));
+      wsp[1] = (int)(sb[4] | (sb[5] << 8) | (sb[6] << 16) | (sb[7] << 24));
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       }
-#pragma unroll
-      for (int f = 0; f < kFrags; ++f) {
-        if (f + 1 < kFrags) xfrag(f + 1, xb[(f + 1) & 1], xsc[(f + 1) & 1]);
-        const int ct = f % NB;
-        const glm_i32x8 &xv = xb[f & 1];
-        const int xs = xsc[f & 1];
-        // weight block B (its scale byte B % 4 of wsp[B / 4]); the byte
-        // select must be a constant, hence one instantiation per block
-        auto mf = [&](auto bt) {
-          constexpr int B = decltype(bt)::value;
-          if (f < NB)
-            acc[B][ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                wa[B], xv, acc[B][ct], 4, S::kMfmaFmt, B & 3, wsp[B >> 2], 0, xs);
-          else
-            acc[B][ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                wa[B], xv, acc[B][ct], 4, S::kMfmaFmtLo, B & 3, wsp[B >> 2], 0, xs);
-        };
-        mf(W8Stage<0>{});
-        mf(W8Stage<1>{});
-        mf(W8Stage<2>{});
-        mf(W8Stage<3>{});
-        mf(W8Stage<4>{});
-        mf(W8Stage<5>{});
-        mf(W8Stage<6>{});
-        mf(W8Stage<7>{});
-      }
-      // the schedule: the chunk's first fragment, weights and scales, then per
-      // fragment the next fragment's three reads ahead of its 8 MFMAs
-      __builtin_amdgcn_sched_group_barrier(0x100, 3 + 16, 0);
-#pragma unroll
-      for (int f = 0; f < kFrags; ++f) {
-        if (f + 1 < kFrags) __builtin_amdgcn_sched_group_barrier(0x100, S::kParts + 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-      }
+      __builtin_amdgcn_sched_group_barrier(0x100, S::kParts + 1, 0);
+    } else {
+      if constexpr (L >= 1) mf8(L - 1, xb[(L - 1 + P) & 1], xsc[(L - 1 + P) & 1]);
+      mf8(L, xb[(L + P) & 1], xsc[(L + P) & 1]);
     }
   };
 
   // Double buffer, unrolled by two so that each stage's offsets are
-  // immediates: the loads of chunk c + 1 are issued after the barrier that
-  // follows every wave's chunk c - 1 (whose stage they overwrite) and land
-  // while chunk c is consumed.
-  auto step = [&](auto st, int c) {
-    constexpr int ST = decltype(st)::value;
+  // immediates: the loads of chunk c + 1 are issued at the top of chunk c,
+  // into the stage of chunk c - 1 (free since the barrier inside chunk
+  // c - 1), and land while chunk c is consumed.  A wave without token blocks
+  // issues its loads and meets the same barriers.
+  ring_barrier();  // the row table
+  {
+    uint32_t xrow[kXL];
+    table_rows(xrow);
+    issue_loads(W8Stage<0>{}, 0, xrow);
+  }
+  if constexpr (AF == ACT_FP8X2) {
+    // The exact FP8 split: the operands cross the barrier in registers (see
+    // run_chunk).  The chunk count is even (K a multiple of 256); the last
+    // chunk, which has no next one, is peeled.
+    constexpr int kP1 = kFrags & 1;  // parity of the chunks in stage 1
+    auto step = [&](auto st, int c, auto nx) {
+      constexpr int kNx = decltype(nx)::value;
+      constexpr int ST = decltype(st)::value;
+      if constexpr (kNx > 0) {
+        uint32_t xrow[kXL];
+        table_rows(xrow);
+        issue_loads(W8Stage<1 - ST>{}, c + 1, xrow);
+      }
+      if constexpr (NB > 0) {
+        run_chunk(st, W8Stage<ST == 0 ? 0 : kP1>{}, nx);
+      } else if constexpr (kNx > 0) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & ~(15 << 8));
+        ring_barrier();
+      }
+    };
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     ring_barrier();
-    if (c + 1 < nchunks) issue(W8Stage<1 - ST>{}, c + 1);
-    compute(st);
-  };
-  ring_barrier();  // the row table
-  issue(W8Stage<0>{}, 0);
-  for (int c = 0; c < nchunks; c += 2) {
-    step(W8Stage<0>{}, c);
-    if (c + 1 < nchunks) step(W8Stage<1>{}, c + 1);
+    if constexpr (NB > 0) read_head(W8Stage<0>{}, W8Stage<0>{});
+    for (int c = 0; c + 2 < nchunks; c += 2) {
+      step(W8Stage<0>{}, c, W8Stage<1>{});
+      step(W8Stage<1>{}, c + 1, W8Stage<1>{});
+    }
+    step(W8Stage<0>{}, nchunks - 2, W8Stage<1>{});
+    step(W8Stage<1>{}, nchunks - 1, W8Stage<0>{});
+  } else {
+    // The other formats (their kernels spill with the operands carried in
+    // registers): each chunk's head is read after the barrier that releases
+    // the chunk, then its fragments with the next one read ahead.
+    auto compute = [&](auto st) {
+      if constexpr (NB > 0) {
+        read_head(st, W8Stage<0>{});
+#pragma unroll
+        for (int f = 0; f < kFrags; ++f) {
+          if (f + 1 < kFrags) xfrag(st, f + 1, xb[(f + 1) & 1], xsc[(f + 1) & 1]);
+          mf8(f, xb[f & 1], xsc[f & 1]);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, S::kParts + 1 + 16, 0);
+#pragma unroll
+        for (int f = 0; f < kFrags; ++f) {
+          if (f + 1 < kFrags) __builtin_amdgcn_sched_group_barrier(0x100, S::kParts + 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+        }
+      }
+    };
+    auto step = [&](auto st, int c) {
+      constexpr int ST = decltype(st)::value;
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      ring_barrier();
+      if (c + 1 < nchunks) {
+        uint32_t xrow[kXL];
+        table_rows(xrow);
+        issue_loads(W8Stage<1 - ST>{}, c + 1, xrow);
+      }
+      compute(st);
+    };
+    for (int c = 0; c < nchunks; c += 2) {
+      step(W8Stage<0>{}, c);
+      if (c + 1 < nchunks) step(W8Stage<1>{}, c + 1);
+    }
   }
   // the down epilogue stages y in LDS that other waves may still read:
   // every wave (also one without token blocks) passes this barrier first
