@@ -115,6 +115,29 @@ def _grouped(gu, layer, shape, idx, fmt):
     return h, y, (counts, offsets, perm, inv, active)
 
 
+@pytest.mark.parametrize("d", [512, 2048])
+def test_gate_up_every_token_block_count(gu, d):
+    # expert sizes chosen so that the row tiles (at most 160 rows; an
+    # expert's 16-row blocks dealt over its tiles) hold 1 to 10 blocks, full
+    # and ragged, so the eight-wave gate/up's two token waves run every block
+    # count 0..5; d = 512 is four K chunks (the shortest K loop), d = 2048
+    # sixteen
+    counts = [3, 17, 33, 47, 64, 81, 100, 127, 144, 160, 161, 250, 320]
+    E, I = len(counts), 256
+    T = sum(counts)
+    shape = MoEShape("blocks", T, d, E, 1, I, 0)
+    layer = make_layer(shape, 4242 + d)
+    rng = np.random.default_rng(d)
+    idx = rng.permutation(np.repeat(np.arange(E, dtype=np.int64), counts)).reshape(T, 1)
+    h, _, (_, _, _, inv, _) = _grouped(gu, layer, shape, idx, A.FP8X2)
+    bank = O.Bank(*(layer[key] for key in BANK_KEYS))
+    xq = A.dequant(A.split(layer["x"], d, A.FP8X2), d, A.FP8X2).astype(np.float32)
+    _, inter = O.routed_experts(xq, idx, bank, shape.swiglu_limit, return_intermediates=True)
+    h_got = O.bf16_bits_to_f32(gu.bf16_bits(h))[inv].reshape(T, 1, I)
+    assert O.rel_l2(h_got, inter["h"]) < REL_L2
+    assert np.mean(h_got == inter["h"]) > 0.97
+
+
 @pytest.mark.parametrize("fmt", FORMATS, ids=[A.NAMES[f] for f in FORMATS])
 def test_grouped_gemms_equal_products_of_the_split(gu, fmt):
     # 400 tokens, d = 1024, 32 experts, top-4, I = 256: partial tiles and
